@@ -1,0 +1,229 @@
+"""Benchmark of the shifted-window attention hot path on one MI355X.
+
+Step = one SW-MSA attention half of a Swin block on config c3 (the
+high-resolution ocean stage: B=1, 512x1024 tokens, C=192, 6 heads, window 8,
+shift 4, ~30 % land folded into the mask), bf16, inputs resident in HBM:
+
+    norm1 -> [roll + partition] -> qkv GEMM -> [fused window attention]
+          -> proj GEMM -> [reverse + roll + residual]
+
+The bracketed stages are this library's HIP kernels; LayerNorm and the GEMMs
+are torch (hipBLASLt).  `value` is tokens/s of the whole step.  The
+`roofline` object is for the fused attention kernel (the path's dominant
+custom kernel), timed with HIP events on the launch stream over the timed
+steps; partition / reverse are reported under `kernels`.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2516.6  # dense bf16
+METRIC = "window-attn fwd TFLOP/s & tokens/sec on 1 MI355X; % of MFMA/HBM roofline"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(cfg, blk, land, budget_s: float):
+    """The oracle's restatement of the reference block (torch CPU, fp32) on a
+    bounded sample: a band of whole window rows of the same workload."""
+    import torch
+
+    from oracle import swin_oracle as so
+    from terra_amd import workloads
+
+    threads = torch.get_num_threads()
+    params = {k: v.detach().float().cpu() for k, v in blk.state_dict().items() if k != "attn_mask"}
+    # sample: the first `rows` token rows (whole window rows); the shift wraps within the band
+    rows = 64
+    x = workloads.activations((1, rows * cfg.width, cfg.channels), 1000, torch.float32)
+    land_s = land[:rows]
+    times = []
+    t_end = time.perf_counter() + budget_s
+    with torch.inference_mode():
+        so.swin_block_attention(x, rows, cfg.width, cfg.window, blk.shift_size, cfg.heads, params, land=land_s)
+        while time.perf_counter() < t_end or len(times) < 2:
+            t0 = time.perf_counter()
+            so.swin_block_attention(x, rows, cfg.width, cfg.window, blk.shift_size, cfg.heads, params, land=land_s)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 20:
+                break
+    t = statistics.median(times)
+    tokens = rows * cfg.width
+    return {
+        "value": tokens / t,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle restatement of the reference op sequence (torch CPU fp32, {threads} threads, "
+                   f"{cpu_model()}): {rows}x{cfg.width}-token band of {cfg.name} ({tokens} tokens, "
+                   f"{tokens // cfg.tokens} windows), median of {len(times)} runs, {t * 1e3:.1f} ms each"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding is designed, "
+              "not built", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from terra_amd import kernels, workloads
+    import terra_amd._lib as lib
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    lib.load()
+    dev = torch.device("cuda:0")
+    cfg = workloads.CONFIGS[args.config]
+    dtype = cfg.dtype
+    land = workloads.land_mask(cfg.height, cfg.width, seed=42) if cfg.land else None
+    blk = workloads.block_for(cfg, 1 if cfg.shift else 0, land=land).to(dev).to(dtype)
+    x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 1003, dtype).to(dev)
+
+    # Per-kernel events on the launch stream (torch's current stream, which the
+    # C ABI receives as its hipStream_t).
+    events = {"partition": [], "window_attention": [], "reverse": []}
+    orig = (kernels.swin_partition, kernels.window_attention, kernels.swin_reverse)
+    recording = {"on": False}
+
+    def timed(name, fn):
+        def wrapper(*a, **kw):
+            if not recording["on"]:
+                return fn(*a, **kw)
+            s = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            out = fn(*a, **kw)
+            e1.record(s)
+            events[name].append((e0, e1))
+            return out
+        return wrapper
+
+    import terra_amd.transformer as tr
+    import terra_amd.attention as at
+    tr.kernels.swin_partition = timed("partition", orig[0])
+    tr.kernels.swin_reverse = timed("reverse", orig[2])
+    at.kernels.window_attention = timed("window_attention", orig[1])
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            blk(x)
+        torch.cuda.synchronize()
+        recording["on"] = True
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            y = blk(x)
+        t1.record()
+        torch.cuda.synchronize()
+        recording["on"] = False
+    kernels.swin_partition, kernels.window_attention, kernels.swin_reverse = orig
+    ms = t0.elapsed_time(t1) / args.steps
+
+    B_, N, C = cfg.num_windows, cfg.tokens, cfg.channels
+    elt = torch.tensor([], dtype=dtype).element_size()
+    n_real = cfg.tokens  # square windows, no padded keys
+    core_flops = 4.0 * n_real * n_real * C * B_
+    core_bytes = 4.0 * B_ * N * C * elt
+    part_bytes = float(cfg.batch * cfg.height * cfg.width * C * elt + B_ * N * C * elt)
+    rev_bytes = float(B_ * N * C * elt + 2 * cfg.batch * cfg.height * cfg.width * C * elt)  # windows + residual in, y out
+
+    def avg_us(name):
+        return 1e3 * statistics.mean(a.elapsed_time(b) for a, b in events[name])
+
+    t_attn, t_part, t_rev = avg_us("window_attention"), avg_us("partition"), avg_us("reverse")
+    tokens = cfg.real_tokens
+    attn_gbs = core_bytes / (t_attn * 1e-6) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": tokens / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (seeded N(0,1) activations, trunc-normal(0.02) weights, seeded smoothed-noise land mask)",
+        "config": {
+            "workload": (f"{cfg.name}: SW-MSA attention half of a Swin block (LN, roll+partition, qkv GEMM, fused "
+                         f"window attention, proj GEMM, reverse+roll+residual), B={cfg.batch}, "
+                         f"{cfg.height}x{cfg.width} tokens, C={C}, {cfg.heads} heads, window {cfg.window}, "
+                         f"shift {cfg.shift}" + (", ~30% land mask" if cfg.land else "")),
+            "windows": B_,
+            "tokens": tokens,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "kernel": "window_attn_kernel (fused QK^T + bias + mask + softmax + PV)",
+            "bound": "hbm",
+            "achieved": attn_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": attn_gbs / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": core_bytes,
+            "avg_launch_us": t_attn,
+        },
+        "kernels": {
+            "window_attention": {
+                "us": t_attn,
+                "GB_s": attn_gbs,
+                "hbm_frac": attn_gbs / HBM_PEAK_GBS,
+                "TFLOP_s": core_flops / (t_attn * 1e-6) / 1e12,
+                "mfma_frac": core_flops / (t_attn * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                "windows_per_s": B_ / (t_attn * 1e-6),
+                "tokens_per_s": tokens / (t_attn * 1e-6),
+            },
+            "partition": {"us": t_part, "GB_s": part_bytes / (t_part * 1e-6) / 1e9,
+                          "hbm_frac": part_bytes / (t_part * 1e-6) / 1e9 / HBM_PEAK_GBS},
+            "reverse_residual": {"us": t_rev, "GB_s": rev_bytes / (t_rev * 1e-6) / 1e9,
+                                 "hbm_frac": rev_bytes / (t_rev * 1e-6) / 1e9 / HBM_PEAK_GBS},
+        },
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(cfg, blk, land if land is not None else
+                                           torch.zeros(cfg.height, cfg.width, dtype=torch.bool), args.cpu_seconds)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

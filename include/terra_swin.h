@@ -1,0 +1,173 @@
+/*
+ * terra_swin.h — C ABI of the MI355X (gfx950) shifted-window attention hot path.
+ *
+ * The reference (TERRA, pure Python on PyTorch) has no FFI for this path: every
+ * step is an ATen call made from Python.  Each entry point below replaces a
+ * specific group of those calls; the citation next to each declaration names
+ * the reference lines it stands in for (paths relative to the TERRA tree).
+ *
+ * Conventions
+ *   - All tensors are device pointers allocated by the caller (PyTorch).  The
+ *     library never allocates or frees device memory on these paths.
+ *   - Every entry point validates its arguments on the host before launching
+ *     anything and returns TERRA_OK (0) or a negative terra_status.  The text
+ *     of the last error of the calling thread is returned by terra_last_error().
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL is the
+ *     default stream).  Nothing synchronises the host.
+ *   - Entry points are stateless and reentrant.
+ */
+#ifndef TERRA_SWIN_H
+#define TERRA_SWIN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TERRA_SWIN_ABI_VERSION 1
+
+/* Element types of activations (q/k/v/o, token grids, windows). */
+enum terra_dtype {
+  TERRA_DTYPE_F32 = 0,
+  TERRA_DTYPE_F16 = 1,
+  TERRA_DTYPE_BF16 = 2,
+  TERRA_DTYPE_U8 = 3 /* partition / reverse only (e.g. per-token land flags) */
+};
+
+enum terra_status {
+  TERRA_OK = 0,
+  TERRA_ERR_NULL = -1,        /* a required pointer is NULL                  */
+  TERRA_ERR_DTYPE = -2,       /* dtype not supported by this entry point     */
+  TERRA_ERR_SHAPE = -3,       /* inconsistent or out-of-range sizes          */
+  TERRA_ERR_ALIGN = -4,       /* pointer / stride not aligned as required    */
+  TERRA_ERR_UNSUPPORTED = -5, /* valid request this build does not implement */
+  TERRA_ERR_LAUNCH = -6       /* the HIP runtime rejected a launch           */
+};
+
+/* Geometry of a token grid and of the window grid cut from it.
+ *
+ * The window frame is the token grid padded by (pad_top, pad_bottom,
+ * pad_left, pad_right) with `pad_value`, then cyclically shifted by
+ * (-shift_h, -shift_w) over the padded extents Hp = height+pad_top+pad_bottom,
+ * Wp = width+pad_left+pad_right, exactly as torch.roll(x, (-sh, -sw), (1, 2))
+ * on the padded tensor.  Hp and Wp must be multiples of `window`.
+ *
+ * Windows are numbered image-major then row-major over the emitted window rows
+ * [win_row_begin, win_row_begin + win_rows) of the Hp/ws x Wp/ws window grid
+ * (win_rows <= 0 means all rows).  Windows of an image whose flat index
+ * (row-major within the emitted rows) lies outside [valid_begin, valid_end)
+ * are pad windows: partition writes them as pad_value and reverse ignores
+ * them.  valid_end <= 0 means "all windows valid".
+ */
+typedef struct terra_swin_geom {
+  int32_t batch;    /* B                                   */
+  int32_t height;   /* H  (token rows of x / y)            */
+  int32_t width;    /* W  (token columns of x / y)         */
+  int32_t channels; /* C                                   */
+  int32_t window;   /* ws (square windows, N = ws*ws)      */
+  int32_t shift_h;  /* 0 <= shift_h < Hp                   */
+  int32_t shift_w;  /* 0 <= shift_w < Wp                   */
+  int32_t pad_top, pad_bottom, pad_left, pad_right;
+  int32_t win_row_begin;
+  int32_t win_rows;
+  int32_t valid_begin;
+  int32_t valid_end;
+} terra_swin_geom;
+
+/* Mask modes of terra_swin_attn_fwd. */
+enum terra_mask_mode {
+  TERRA_MASK_NONE = 0,     /* no additive mask                                  */
+  TERRA_MASK_SHIFT = 1,    /* analytic Swin shift mask, from the frame geometry */
+  TERRA_MASK_EXPLICIT = 2  /* caller's fp32 [mask_windows, N, N] additive mask  */
+};
+
+/* Description of one fused window-attention forward call.
+ *
+ * q, k, v, o hold `num_windows` windows of `tokens` rows each; row r of window
+ * w starts at element (w*tokens + r)*{q,k,v,o}_stride, and head h occupies
+ * columns [h*D, (h+1)*D) with D = channels/heads.  Per window w and head h:
+ *
+ *   S = (q_h k_h^T) * scale + bias_h + M[w]        (fp32)
+ *   S[:, j] = pad_key_value   for keys j >= n_real (masked_fill, after M)
+ *   o_h = softmax(S) v_h                           (P rounded to the
+ *                                                   activation dtype)
+ *
+ * bias_h[i, j] = bias_table[idx(i, j) * heads + h] with the Swin relative
+ * position index idx of a window_h x window_w window; bias_table == NULL
+ * disables the bias.  M[w] is the sum of
+ *   - the shift mask (mask_mode == TERRA_MASK_SHIFT): mask_value where the
+ *     region ids of query and key differ, region ids from the frame
+ *     (frame_h x frame_w tokens, shifts shift_h/shift_w, window w at window row
+ *     win_row_begin + (w % (win_rows*win_cols)) / win_cols of the frame), or
+ *     the caller's explicit_mask[w % mask_windows] (TERRA_MASK_EXPLICIT);
+ *   - the land term: mask_value for every key j whose bit j is set in
+ *     land_bits[w % mask_windows] (land_bits == NULL disables it).
+ */
+typedef struct terra_swin_attn_desc {
+  int32_t num_windows; /* B_                                       */
+  int32_t tokens;      /* N  (<= 64)                               */
+  int32_t channels;    /* C                                        */
+  int32_t heads;       /* nH (D = C / nH in {32, 64})              */
+  int32_t window_h, window_w; /* window_h * window_w == tokens     */
+  int32_t n_real;      /* keys >= n_real get pad_key_value         */
+  int32_t q_stride, k_stride, v_stride, o_stride; /* elements per token row */
+  float scale;
+  float mask_value;    /* -100.0 in the reference                  */
+  float pad_key_value; /* -10000.0 in the reference                */
+  int32_t mask_mode;   /* enum terra_mask_mode                     */
+  int32_t mask_windows;/* period of explicit_mask / land_bits      */
+  int32_t frame_h, frame_w;
+  int32_t shift_h, shift_w;
+  int32_t win_row_begin, win_rows, win_cols;
+} terra_swin_attn_desc;
+
+/* ABI version of the loaded library (TERRA_SWIN_ABI_VERSION at build time). */
+int terra_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* terra_last_error(void);
+
+/* Fused pad + cyclic shift + window partition.
+ * Replaces  torch.roll(x, (-s, -s), dims=(1, 2))      models/transformer.py:179
+ *           window_partition(shifted_x, ws)           models/utils.py:35-39
+ *           x_windows.view(-1, ws*ws, C)              models/transformer.py:225
+ * and the model-level zero padding before the blocks
+ *           (models/reference_model/sequential_hierarchical_swin.py:277-278).
+ * x: [B, H, W, C] contiguous; windows: [B * nW_emitted, ws*ws, C] contiguous.
+ */
+int terra_swin_partition(const void* x, void* windows, int dtype,
+                         const terra_swin_geom* geom, float pad_value,
+                         void* stream);
+
+/* Fused window reverse + inverse cyclic shift + crop (+ residual add).
+ * Replaces  window_reverse(attn_windows, ws, H, W)    models/utils.py:41-45
+ *           torch.roll(shifted_x, (s, s), dims=(1, 2))  models/transformer.py:246
+ *           x = shortcut + x.view(B, H*W, C)          models/transformer.py:296-298
+ * y[b, h, w] = residual[b, h, w] (if residual != NULL) + the window token that
+ * partition would have read from (b, h, w); tokens whose window is not emitted
+ * or is a pad window contribute 0.  y may alias residual.
+ */
+int terra_swin_reverse(const void* windows, void* y, const void* residual,
+                       int dtype, const terra_swin_geom* geom, void* stream);
+
+/* Fused per-window multi-head attention core (bf16 or fp32 activations).
+ * Replaces  q = q * self.scale                        models/attention.py:256
+ *           attn = q @ k.transpose(-2, -1)            models/attention.py:258
+ *           relative-position bias gather + add      models/attention.py:260-266
+ *           mask add (shift mask buffer)              models/attention.py:269-272
+ *           softmax                                   models/attention.py:273-275
+ *           (attn @ v).transpose(1, 2).reshape(B_,N,C) models/attention.py:278
+ *           padded-key masked_fill(-10000)            models/attention.py:905-907
+ * The q/k/v/proj Linear layers stay with the caller.
+ */
+int terra_swin_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                        int dtype, const terra_swin_attn_desc* desc,
+                        const float* bias_table, const float* explicit_mask,
+                        const uint64_t* land_bits, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TERRA_SWIN_H */

@@ -1,0 +1,145 @@
+"""Brute-force restatements used to pin the oracle — TEST INFRASTRUCTURE ONLY.
+
+Plain Python loops over coordinates, written from the definitions rather than
+from tensor reshapes, so that a transposed permute, an off-by-one roll or a
+wrong region slice in ``swin_oracle`` shows up as a mismatch.  Sizes must stay
+tiny (a few thousand tokens).
+"""
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Sequence, Tuple
+
+import numpy as np
+
+
+def frame_source(B: int, H: int, W: int, ws: int, shift_h: int = 0, shift_w: int = 0,
+                 pad: Sequence[int] = (0, 0, 0, 0), win_row_begin: int = 0, win_rows: Optional[int] = None,
+                 valid: Optional[Tuple[int, int]] = None) -> List[Optional[Tuple[int, int, int]]]:
+    """For every output (window, token) in order, the (b, h, w) source token of the
+    unpadded grid, or None where the output is padding / a pad window.
+
+    Definition: shifted[b, i, j] = padded[b, (i + sh) mod Hp, (j + sw) mod Wp]
+    (torch.roll by -s); window (wr, wc) holds shifted rows wr*ws..wr*ws+ws-1,
+    columns wc*ws..; token t = ti*ws + tj; windows image-major, row-major.
+    """
+    top, bottom, left, right = pad
+    Hp, Wp = H + top + bottom, W + left + right
+    nwh, nww = Hp // ws, Wp // ws
+    rows = nwh - win_row_begin if win_rows is None else win_rows
+    out = []
+    for b in range(B):
+        for r in range(rows):
+            for wc in range(nww):
+                flat = r * nww + wc
+                is_valid = valid is None or (valid[0] <= flat < valid[1])
+                wr = r + win_row_begin
+                for ti in range(ws):
+                    for tj in range(ws):
+                        i, j = wr * ws + ti, wc * ws + tj
+                        ph, pw = (i + shift_h) % Hp, (j + shift_w) % Wp
+                        sh, sw = ph - top, pw - left
+                        if is_valid and 0 <= sh < H and 0 <= sw < W:
+                            out.append((b, sh, sw))
+                        else:
+                            out.append(None)
+    return out
+
+
+def partition(x: np.ndarray, ws: int, **geom) -> np.ndarray:
+    """x [B, H, W, C] -> [B_, N, C] through frame_source (pad value 0)."""
+    B, H, W, C = x.shape
+    src = frame_source(B, H, W, ws, **geom)
+    out = np.zeros((len(src), C), dtype=x.dtype)
+    for n, s in enumerate(src):
+        if s is not None:
+            out[n] = x[s]
+    return out.reshape(-1, ws * ws, C)
+
+
+def reverse(windows: np.ndarray, B: int, H: int, W: int, ws: int, residual: Optional[np.ndarray] = None,
+            **geom) -> np.ndarray:
+    """Inverse map: every grid token takes the one window token whose source it is;
+    tokens no emitted window reads stay 0; then + residual."""
+    C = windows.shape[-1]
+    flat = windows.reshape(-1, C)
+    y = np.zeros((B, H, W, C), dtype=windows.dtype)
+    for n, s in enumerate(frame_source(B, H, W, ws, **geom)):
+        if s is not None:
+            y[s] = flat[n]
+    if residual is not None:
+        y = residual.reshape(B, H, W, C) + y
+    return y
+
+
+def relative_index(wh: int, ww: int) -> np.ndarray:
+    """idx[i, j] for i = (hi, wi), j = (hj, wj): the (dh, dw) offset pair mapped
+    row-major onto a (2wh-1) x (2ww-1) table with (0, 0) at the centre."""
+    n = wh * ww
+    idx = np.zeros((n, n), dtype=np.int64)
+    for i in range(n):
+        hi, wi = divmod(i, ww)
+        for j in range(n):
+            hj, wj = divmod(j, ww)
+            idx[i, j] = (hi - hj + wh - 1) * (2 * ww - 1) + (wi - wj + ww - 1)
+    return idx
+
+
+def _region(coord: int, extent: int, ws: int, shift: int) -> int:
+    if coord < extent - ws:
+        return 0
+    if coord < extent - shift:
+        return 1
+    return 2
+
+
+def shift_mask(H: int, W: int, ws: int, shift: int) -> np.ndarray:
+    """[nW, N, N]: -100 where the two tokens of a window come from different
+    regions of the rolled frame, else 0."""
+    nwh, nww = H // ws, W // ws
+    n = ws * ws
+    m = np.zeros((nwh * nww, n, n), dtype=np.float32)
+    for wr in range(nwh):
+        for wc in range(nww):
+            rid = []
+            for t in range(n):
+                ti, tj = divmod(t, ws)
+                rid.append((_region(wr * ws + ti, H, ws, shift), _region(wc * ws + tj, W, ws, shift)))
+            for i in range(n):
+                for j in range(n):
+                    if rid[i] != rid[j]:
+                        m[wr * nww + wc, i, j] = -100.0
+    return m
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, num_heads: int, scale: float,
+              bias: Optional[np.ndarray] = None, mask: Optional[np.ndarray] = None,
+              n_real: Optional[int] = None) -> np.ndarray:
+    """float64 loops: for each window, head and query row, logits over keys,
+    max-subtracted exponentials, normalised weights, weighted sum of values.
+    bias: [nH, N, N] or None; mask: [nW, N, N] (window w uses mask[w % nW])."""
+    B_, N, C = q.shape
+    d = C // num_heads
+    out = np.zeros((B_, N, C), dtype=np.float64)
+    for w in range(B_):
+        for h in range(num_heads):
+            cs = slice(h * d, (h + 1) * d)
+            for i in range(N):
+                logits = []
+                for j in range(N):
+                    s = float(np.dot(q[w, i, cs].astype(np.float64) * scale, k[w, j, cs].astype(np.float64)))
+                    if bias is not None:
+                        s += float(bias[h, i, j])
+                    if mask is not None:
+                        s += float(mask[w % mask.shape[0], i, j])
+                    if n_real is not None and j >= n_real:
+                        s = -10000.0
+                    logits.append(s)
+                mx = max(logits)
+                e = [math.exp(s - mx) for s in logits]
+                tot = sum(e)
+                acc = np.zeros(d, dtype=np.float64)
+                for j in range(N):
+                    acc += (e[j] / tot) * v[w, j, cs].astype(np.float64)
+                out[w, i, cs] = acc
+    return out

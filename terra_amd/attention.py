@@ -1,0 +1,109 @@
+"""Drop-in ``WindowAttention`` (models/attention.py:175-283) on the HIP core.
+
+Constructor arguments, parameter / buffer names and initialisation order are
+the reference's, so its state dicts load unchanged:
+``relative_position_bias_table``, ``relative_position_index``, ``q_linear``,
+``k_linear``, ``v_linear``, ``proj``.  The forward runs the three q/k/v
+projections as one GEMM over the concatenated weights (x is read once), the
+fused HIP attention core on the projection output in place (no permute
+copies), then ``proj``.
+"""
+from __future__ import annotations
+
+from typing import Callable, Optional, Sequence, Union
+
+import torch
+import torch.nn.functional as F
+
+from . import kernels
+from .kernels import ShiftMask, WindowMask
+
+
+def run_with_seed(init_seed: Optional[int], fn: Callable):
+    """Run ``fn`` under ``torch.manual_seed(init_seed)`` and restore the global
+    RNG state afterwards (models/model_utils/init_weight.py:31-41)."""
+    if init_seed is None:
+        return fn()
+    devices = list(range(torch.cuda.device_count())) if torch.cuda.is_available() else []
+    with torch.random.fork_rng(devices=devices):
+        torch.manual_seed(int(init_seed))
+        return fn()
+
+
+def make_linear_with_seed(in_dim: int, out_dim: int, bias: bool = True,
+                          init_seed: Optional[int] = None) -> torch.nn.Linear:
+    """``nn.Linear`` created under a fixed seed (models/model_utils/init_weight.py:18-28)."""
+    return run_with_seed(init_seed, lambda: torch.nn.Linear(in_dim, out_dim, bias=bias))
+
+
+def relative_position_index(window_size: Sequence[int]) -> torch.Tensor:
+    """Swin relative-position index [Wh*Ww, Wh*Ww] (models/attention.py:205-214):
+    idx[i, j] = (hi - hj + Wh - 1) * (2*Ww - 1) + (wi - wj + Ww - 1)."""
+    wh, ww = int(window_size[0]), int(window_size[1])
+    hi = torch.arange(wh).repeat_interleave(ww)
+    wi = torch.arange(ww).repeat(wh)
+    return (hi[:, None] - hi[None, :] + wh - 1) * (2 * ww - 1) + (wi[:, None] - wi[None, :] + ww - 1)
+
+
+class WindowAttention(torch.nn.Module):
+    """Window multi-head self-attention with relative-position bias.
+
+    ``forward(x[B_, N, C], mask)``; ``mask`` may be None, a dense additive
+    ``[nW, N, N]`` tensor (as in the reference), a :class:`kernels.ShiftMask`
+    (the same mask in closed form), or a :class:`kernels.WindowMask` adding
+    per-window land bits.  ``use_flash_attention`` is accepted for signature
+    compatibility; the fused HIP core serves every case.
+    """
+
+    def __init__(self, embedding_dim, window_size, num_heads, qkv_bias=True, qk_scale=None,
+                 use_attn_mask=True, use_relative_position_bias=True, use_flash_attention=False,
+                 init_seed_base=None):
+        super().__init__()
+        self.use_attn_mask = use_attn_mask
+        self.use_relative_position_bias = use_relative_position_bias
+        self.use_flash_attention = use_flash_attention
+        self.dim = embedding_dim
+        self.window_size = tuple(window_size)
+        self.num_heads = num_heads
+        if self.dim % num_heads != 0:
+            raise AssertionError(f"dim {self.dim} must be divisible by num_heads {num_heads}")
+        head_dim = self.dim // num_heads
+        self.scale = qk_scale or head_dim ** -0.5
+
+        if self.use_relative_position_bias:
+            wh, ww = self.window_size
+            self.relative_position_bias_table = torch.nn.Parameter(
+                torch.zeros((2 * wh - 1) * (2 * ww - 1), num_heads))
+            self.register_buffer("relative_position_index", relative_position_index(self.window_size))
+            run_with_seed(init_seed_base,
+                          lambda: torch.nn.init.trunc_normal_(self.relative_position_bias_table, std=.02))
+
+        seed = (lambda k: None if init_seed_base is None else init_seed_base + k)
+        self.q_linear = make_linear_with_seed(self.dim, self.dim, bias=qkv_bias, init_seed=seed(1))
+        self.k_linear = make_linear_with_seed(self.dim, self.dim, bias=qkv_bias, init_seed=seed(2))
+        self.v_linear = make_linear_with_seed(self.dim, self.dim, bias=qkv_bias, init_seed=seed(3))
+        self.proj = make_linear_with_seed(self.dim, self.dim, bias=True, init_seed=seed(4))
+        self.softmax = torch.nn.Softmax(dim=-1)
+
+    def qkv(self, x: torch.Tensor) -> torch.Tensor:
+        """The three projections as one GEMM: [B_, N, C] -> [B_, N, 3C]."""
+        w = torch.cat([self.q_linear.weight, self.k_linear.weight, self.v_linear.weight], 0)
+        b = None
+        if self.q_linear.bias is not None:
+            b = torch.cat([self.q_linear.bias, self.k_linear.bias, self.v_linear.bias], 0)
+        return F.linear(x, w, b)
+
+    def core(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+             mask: Union[None, torch.Tensor, ShiftMask, WindowMask] = None,
+             n_real: Optional[int] = None) -> torch.Tensor:
+        """Fused core on projected q/k/v [B_, N, C] (row strides may exceed C)."""
+        table = self.relative_position_bias_table if self.use_relative_position_bias else None
+        return kernels.window_attention(q, k, v, self.num_heads, self.window_size, self.scale,
+                                        bias_table=table, mask=mask, n_real=n_real)
+
+    def forward(self, x: torch.Tensor, mask=None) -> torch.Tensor:
+        B_, N, C = x.shape
+        qkv = self.qkv(x)
+        q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
+        o = self.core(q, k, v, mask=mask)
+        return self.proj(o)

@@ -1,0 +1,64 @@
+"""Builds ``terra_amd/libterra_swin.so`` from ``terra_amd/csrc`` with hipcc for gfx950.
+
+    python -m terra_amd.build
+
+The library is written in-tree (it travels with the source tree to the GPU
+host; nothing is JIT-compiled at run time).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+SOURCES = ("abi.hip", "window_copy.hip", "window_attention.hip")
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # Packed-fp32 VALU ops are kept out of the device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm toolchain required to build libterra_swin.so)")
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile every HIP source into the shared library; returns its path."""
+    from ._lib import LIB_PATH  # noqa: WPS433 (path only; does not open the library)
+
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    fd, tmp = tempfile.mkstemp(prefix="libterra_swin.", suffix=".so.tmp", dir=HERE)
+    os.close(fd)
+    cmd = [hipcc(), *HIPCC_FLAGS, *srcs, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(line for line in proc.stdout.splitlines() if "packed-fp32-ops" not in line)
+    if proc.returncode != 0:
+        os.unlink(tmp)
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{out}")
+    if verbose and out.strip():
+        print(out, flush=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build_library(verbose=True)
+    print(path)
+    sys.exit(0)

@@ -1,0 +1,67 @@
+// Shared helpers of the gfx950 kernels: error reporting for the C ABI,
+// fast division by launch-time constants, bf16 conversions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <hip/hip_fp16.h>
+
+#include "../../include/terra_swin.h"
+
+namespace terra {
+
+// Records the message returned by terra_last_error() for this thread and
+// returns `status`, so validation code can `return fail(...)`.
+int fail(int status, const char* fmt, ...);
+void clear_error();
+
+// Element size in bytes of a terra_dtype, or 0 if unknown.
+inline int dtype_size(int dtype) {
+  switch (dtype) {
+    case TERRA_DTYPE_F32: return 4;
+    case TERRA_DTYPE_F16: return 2;
+    case TERRA_DTYPE_BF16: return 2;
+    case TERRA_DTYPE_U8: return 1;
+    default: return 0;
+  }
+}
+
+// Unsigned division by a divisor fixed at launch time (Granlund–Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994):
+//   n / d == (umulhi(n, m) + n) >> s   for all 32-bit n,
+// with s = ceil(log2 d) and m = floor(2^32 * (2^s - d) / d) + 1.
+struct FastDiv {
+  uint32_t d, m, s;
+  FastDiv() : d(1), m(0), s(0) {}
+  explicit FastDiv(uint32_t div) : d(div) {
+    s = 0;
+    while ((1ull << s) < div) ++s;
+    m = (uint32_t)(((1ull << 32) * ((1ull << s) - div)) / div + 1);
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    uint32_t hi = __umulhi(n, m);
+    return (uint32_t)(((uint64_t)hi + n) >> s);
+  }
+  __device__ __forceinline__ void divmod(uint32_t n, uint32_t& q, uint32_t& r) const {
+    q = div(n);
+    r = n - q * d;
+  }
+};
+
+// float -> bf16 bits, round to nearest even (what torch does on a cast).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+}  // namespace terra

@@ -1,0 +1,345 @@
+// Fused pad + cyclic shift + window partition, and its inverse
+// (window reverse + inverse shift + crop + optional residual add).
+//
+// Both kernels are pure permutations at token granularity: a token is a
+// contiguous C-vector in the [B, H, W, C] grid and in the [B_, N, C] window
+// tensor alike, so every 16-byte chunk a lane moves is read from and written
+// to contiguous memory, and consecutive lanes touch consecutive chunks of the
+// same token row.  Each kernel iterates over its *destination* (gather form),
+// so writes are perfectly sequential and each destination byte is written
+// exactly once; reads are contiguous runs of C*elt bytes.  Nothing is staged
+// through LDS: with >= 192-byte contiguous runs on both sides there is no
+// uncoalesced access for LDS to fix.
+#include "common.h"
+
+namespace terra {
+namespace {
+
+template <int VB> struct Chunk;
+template <> struct Chunk<16> { using T = uint4; };
+template <> struct Chunk<8> { using T = uint2; };
+template <> struct Chunk<4> { using T = uint32_t; };
+template <> struct Chunk<2> { using T = uint16_t; };
+template <> struct Chunk<1> { using T = uint8_t; };
+
+template <int VB>
+__device__ __forceinline__ typename Chunk<VB>::T fill_chunk(uint32_t pat) {
+  using T = typename Chunk<VB>::T;
+  T v;
+  if constexpr (VB == 16) { v.x = v.y = v.z = v.w = pat; }
+  else if constexpr (VB == 8) { v.x = v.y = pat; }
+  else { v = (T)pat; }
+  return v;
+}
+
+struct CopyGeom {
+  int32_t H, W, ws, Hp, Wp;
+  int32_t shift_h, shift_w, pad_top, pad_left;
+  int32_t win_row_begin, win_rows, nWw;
+  int32_t valid_begin, valid_end;  // valid_end <= 0: all valid
+  int32_t N;
+  int64_t row_bytes;               // C * elt
+  FastDiv fd_cv, fd_N, fd_nWe, fd_nWw, fd_ws, fd_W, fd_H;
+  uint32_t total;                  // chunks in the destination
+  uint32_t pad_pattern;
+};
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+template <int VB>
+__global__ __launch_bounds__(kThreads) void partition_kernel(const uint8_t* __restrict__ x,
+                                                             uint8_t* __restrict__ win,
+                                                             const CopyGeom g) {
+  using T = typename Chunk<VB>::T;
+  const uint32_t base = blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+  T vals[kUnroll];
+  uint32_t dst[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t c = base + u * kThreads;
+    dst[u] = c;
+    vals[u] = fill_chunk<VB>(g.pad_pattern);
+    if (c < g.total) {
+      uint32_t rest, cv, rest2, t, b, wl, wr, wc, ti, tj;
+      g.fd_cv.divmod(c, rest, cv);
+      g.fd_N.divmod(rest, rest2, t);
+      g.fd_nWe.divmod(rest2, b, wl);
+      g.fd_nWw.divmod(wl, wr, wc);
+      g.fd_ws.divmod(t, ti, tj);
+      const bool valid = g.valid_end <= 0 || ((int)wl >= g.valid_begin && (int)wl < g.valid_end);
+      int ph = (int)((wr + g.win_row_begin) * g.ws + ti) + g.shift_h;
+      int pw = (int)(wc * g.ws + tj) + g.shift_w;
+      if (ph >= g.Hp) ph -= g.Hp;
+      if (pw >= g.Wp) pw -= g.Wp;
+      const int sh = ph - g.pad_top;
+      const int sw = pw - g.pad_left;
+      if (valid && (unsigned)sh < (unsigned)g.H && (unsigned)sw < (unsigned)g.W) {
+        const int64_t src = (((int64_t)b * g.H + sh) * g.W + sw) * g.row_bytes + (int64_t)cv * VB;
+        vals[u] = *reinterpret_cast<const T*>(x + src);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    if (dst[u] < g.total) reinterpret_cast<T*>(win)[dst[u]] = vals[u];
+  }
+}
+
+// Element-wise residual add of one chunk, rounding like the torch op
+// (fp32 add; bf16 / fp16: add in fp32, round to nearest even).
+template <int VB, int DT>
+__device__ __forceinline__ typename Chunk<VB>::T add_chunk(typename Chunk<VB>::T a,
+                                                           typename Chunk<VB>::T b) {
+  using T = typename Chunk<VB>::T;
+  T r;
+  if constexpr (DT == TERRA_DTYPE_F32) {
+    static_assert(VB % 4 == 0, "fp32 chunks hold whole elements");
+    const float* pa = reinterpret_cast<const float*>(&a);
+    const float* pb = reinterpret_cast<const float*>(&b);
+    float* pr = reinterpret_cast<float*>(&r);
+#pragma unroll
+    for (int i = 0; i < VB / 4; ++i) pr[i] = pa[i] + pb[i];
+  } else {
+    static_assert(VB % 2 == 0, "16-bit chunks hold whole elements");
+    const uint16_t* pa = reinterpret_cast<const uint16_t*>(&a);
+    const uint16_t* pb = reinterpret_cast<const uint16_t*>(&b);
+    uint16_t* pr = reinterpret_cast<uint16_t*>(&r);
+#pragma unroll
+    for (int i = 0; i < VB / 2; ++i) {
+      if constexpr (DT == TERRA_DTYPE_BF16) {
+        pr[i] = f32_to_bf16_bits(bf16_bits_to_f32(pa[i]) + bf16_bits_to_f32(pb[i]));
+      } else {
+        const __half ha = __ushort_as_half(pa[i]);
+        const __half hb = __ushort_as_half(pb[i]);
+        pr[i] = __half_as_ushort(__float2half_rn(__half2float(ha) + __half2float(hb)));
+      }
+    }
+  }
+  return r;
+}
+
+template <int VB, int DT>
+__global__ __launch_bounds__(kThreads) void reverse_kernel(const uint8_t* __restrict__ win,
+                                                           uint8_t* y,
+                                                           const uint8_t* residual,
+                                                           const CopyGeom g) {
+  using T = typename Chunk<VB>::T;
+  const uint32_t base = blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+  T vals[kUnroll];
+  uint32_t dst[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t c = base + u * kThreads;
+    dst[u] = c;
+    vals[u] = fill_chunk<VB>(0u);
+    if (c < g.total) {
+      uint32_t rest, cv, rest2, sw, b, sh;
+      g.fd_cv.divmod(c, rest, cv);
+      g.fd_W.divmod(rest, rest2, sw);
+      g.fd_H.divmod(rest2, b, sh);
+      int fi = (int)sh + g.pad_top - g.shift_h;
+      int fj = (int)sw + g.pad_left - g.shift_w;
+      if (fi < 0) fi += g.Hp;
+      if (fj < 0) fj += g.Wp;
+      uint32_t wr, ti, wc, tj;
+      g.fd_ws.divmod((uint32_t)fi, wr, ti);
+      g.fd_ws.divmod((uint32_t)fj, wc, tj);
+      const int wr_l = (int)wr - g.win_row_begin;
+      if ((unsigned)wr_l < (unsigned)g.win_rows) {
+        const int wl = wr_l * g.nWw + (int)wc;
+        const bool valid = g.valid_end <= 0 || (wl >= g.valid_begin && wl < g.valid_end);
+        if (valid) {
+          const int64_t w = (int64_t)b * g.win_rows * g.nWw + wl;
+          const int64_t src = (w * g.N + (int64_t)(ti * g.ws + tj)) * g.row_bytes + (int64_t)cv * VB;
+          vals[u] = *reinterpret_cast<const T*>(win + src);
+        }
+      }
+    }
+  }
+  if constexpr (DT != TERRA_DTYPE_U8 && (DT != TERRA_DTYPE_F32 || VB >= 4)) {
+    if (residual != nullptr) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (dst[u] < g.total) {
+          const T r = reinterpret_cast<const T*>(residual)[dst[u]];
+          vals[u] = add_chunk<VB, DT>(r, vals[u]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    if (dst[u] < g.total) reinterpret_cast<T*>(y)[dst[u]] = vals[u];
+  }
+}
+
+uint32_t pad_pattern(int dtype, float v) {
+  switch (dtype) {
+    case TERRA_DTYPE_F32: {
+      uint32_t u;
+      memcpy(&u, &v, 4);
+      return u;
+    }
+    case TERRA_DTYPE_BF16: {
+      uint32_t u;
+      memcpy(&u, &v, 4);
+      uint32_t b;
+      if ((u & 0x7fffffffu) > 0x7f800000u) b = (u >> 16) | 0x40;
+      else b = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+      return (b & 0xffff) | (b << 16);
+    }
+    case TERRA_DTYPE_F16: {
+      const __half h = __float2half(v);
+      uint16_t b;
+      memcpy(&b, &h, 2);
+      return (uint32_t)b | ((uint32_t)b << 16);
+    }
+    default: {
+      const uint32_t b = (uint32_t)((int)v) & 0xff;
+      return b | (b << 8) | (b << 16) | (b << 24);
+    }
+  }
+}
+
+// Validates `geom` and fills the kernel-side geometry.  `total_dst_tokens`
+// selects which side is the destination (window tokens or grid tokens).
+int prepare(const terra_swin_geom* geom, int dtype, bool dest_is_windows, CopyGeom* g, int* vb,
+            const void* p0, const void* p1, const void* p2) {
+  if (geom == nullptr) return fail(TERRA_ERR_NULL, "geom is NULL");
+  const int elt = dtype_size(dtype);
+  if (elt == 0) return fail(TERRA_ERR_DTYPE, "unknown dtype %d", dtype);
+  const terra_swin_geom& q = *geom;
+  if (q.batch <= 0 || q.height <= 0 || q.width <= 0 || q.channels <= 0 || q.window <= 0)
+    return fail(TERRA_ERR_SHAPE, "batch/height/width/channels/window must be positive (got %d/%d/%d/%d/%d)",
+                q.batch, q.height, q.width, q.channels, q.window);
+  if (q.pad_top < 0 || q.pad_bottom < 0 || q.pad_left < 0 || q.pad_right < 0)
+    return fail(TERRA_ERR_SHAPE, "padding must be non-negative");
+  const int64_t Hp = (int64_t)q.height + q.pad_top + q.pad_bottom;
+  const int64_t Wp = (int64_t)q.width + q.pad_left + q.pad_right;
+  if (Hp % q.window != 0 || Wp % q.window != 0)
+    return fail(TERRA_ERR_SHAPE, "padded grid %lldx%lld is not a multiple of window %d",
+                (long long)Hp, (long long)Wp, q.window);
+  if (q.shift_h < 0 || q.shift_h >= Hp || q.shift_w < 0 || q.shift_w >= Wp)
+    return fail(TERRA_ERR_SHAPE, "shift (%d, %d) outside [0, padded extent)", q.shift_h, q.shift_w);
+  const int64_t nWh = Hp / q.window, nWw = Wp / q.window;
+  const int64_t rows = q.win_rows <= 0 ? nWh - q.win_row_begin : q.win_rows;
+  if (q.win_row_begin < 0 || rows <= 0 || q.win_row_begin + rows > nWh)
+    return fail(TERRA_ERR_SHAPE, "window rows [%d, %lld) outside the %lld-row window grid",
+                q.win_row_begin, (long long)(q.win_row_begin + rows), (long long)nWh);
+  const int64_t nWe = rows * nWw;
+  if (q.valid_end > 0 && (q.valid_begin < 0 || q.valid_begin >= q.valid_end || q.valid_end > nWe))
+    return fail(TERRA_ERR_SHAPE, "valid window range [%d, %d) outside [0, %lld)", q.valid_begin,
+                q.valid_end, (long long)nWe);
+  const int64_t row_bytes = (int64_t)q.channels * elt;
+  int v = 16;
+  while (v > 1 && (row_bytes % v) != 0) v >>= 1;
+  for (const void* p : {p0, p1, p2}) {
+    while (v > 1 && p != nullptr && ((uintptr_t)p % v) != 0) v >>= 1;
+  }
+  if (v < elt) return fail(TERRA_ERR_ALIGN, "pointer not aligned to its element size");
+  const int64_t N = (int64_t)q.window * q.window;
+  const int64_t tokens = dest_is_windows ? (int64_t)q.batch * nWe * N
+                                         : (int64_t)q.batch * q.height * q.width;
+  const int64_t chunks = tokens * (row_bytes / v);
+  if (chunks >= (1ll << 31))
+    return fail(TERRA_ERR_SHAPE, "%lld chunks exceed one launch (2^31); split the batch", (long long)chunks);
+  g->H = q.height; g->W = q.width; g->ws = q.window; g->Hp = (int32_t)Hp; g->Wp = (int32_t)Wp;
+  g->shift_h = q.shift_h; g->shift_w = q.shift_w; g->pad_top = q.pad_top; g->pad_left = q.pad_left;
+  g->win_row_begin = q.win_row_begin; g->win_rows = (int32_t)rows; g->nWw = (int32_t)nWw;
+  g->valid_begin = q.valid_end > 0 ? q.valid_begin : 0;
+  g->valid_end = q.valid_end > 0 ? q.valid_end : 0;
+  g->N = (int32_t)N;
+  g->row_bytes = row_bytes;
+  g->fd_cv = FastDiv((uint32_t)(row_bytes / v));
+  g->fd_N = FastDiv((uint32_t)N);
+  g->fd_nWe = FastDiv((uint32_t)nWe);
+  g->fd_nWw = FastDiv((uint32_t)nWw);
+  g->fd_ws = FastDiv((uint32_t)q.window);
+  g->fd_W = FastDiv((uint32_t)q.width);
+  g->fd_H = FastDiv((uint32_t)q.height);
+  g->total = (uint32_t)chunks;
+  *vb = v;
+  return TERRA_OK;
+}
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return TERRA_OK;
+}
+
+template <int VB>
+void launch_partition(const void* x, void* win, const CopyGeom& g, hipStream_t s) {
+  const uint32_t blocks = (g.total + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  partition_kernel<VB><<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g);
+}
+
+template <int VB, int DT>
+void launch_reverse(const void* win, void* y, const void* res, const CopyGeom& g, hipStream_t s) {
+  const uint32_t blocks = (g.total + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  reverse_kernel<VB, DT><<<blocks, kThreads, 0, s>>>((const uint8_t*)win, (uint8_t*)y,
+                                                      (const uint8_t*)res, g);
+}
+
+template <int VB>
+void dispatch_reverse(int dtype, const void* win, void* y, const void* res, const CopyGeom& g,
+                      hipStream_t s) {
+  switch (dtype) {
+    case TERRA_DTYPE_F32: launch_reverse<VB, TERRA_DTYPE_F32>(win, y, res, g, s); break;
+    case TERRA_DTYPE_F16: launch_reverse<VB, TERRA_DTYPE_F16>(win, y, res, g, s); break;
+    case TERRA_DTYPE_BF16: launch_reverse<VB, TERRA_DTYPE_BF16>(win, y, res, g, s); break;
+    default: launch_reverse<VB, TERRA_DTYPE_U8>(win, y, res, g, s); break;
+  }
+}
+
+}  // namespace
+}  // namespace terra
+
+using namespace terra;
+
+extern "C" int terra_swin_partition(const void* x, void* windows, int dtype,
+                                    const terra_swin_geom* geom, float pad_value, void* stream) {
+  clear_error();
+  if (x == nullptr || windows == nullptr) return fail(TERRA_ERR_NULL, "x or windows is NULL");
+  CopyGeom g;
+  int vb = 0;
+  const int st = prepare(geom, dtype, true, &g, &vb, x, windows, nullptr);
+  if (st != TERRA_OK) return st;
+  g.pad_pattern = pad_pattern(dtype, pad_value);
+  hipStream_t s = (hipStream_t)stream;
+  switch (vb) {
+    case 16: launch_partition<16>(x, windows, g, s); break;
+    case 8: launch_partition<8>(x, windows, g, s); break;
+    case 4: launch_partition<4>(x, windows, g, s); break;
+    case 2: launch_partition<2>(x, windows, g, s); break;
+    default: launch_partition<1>(x, windows, g, s); break;
+  }
+  return launch_status("terra_swin_partition");
+}
+
+extern "C" int terra_swin_reverse(const void* windows, void* y, const void* residual, int dtype,
+                                  const terra_swin_geom* geom, void* stream) {
+  clear_error();
+  if (windows == nullptr || y == nullptr) return fail(TERRA_ERR_NULL, "windows or y is NULL");
+  if (residual != nullptr && dtype == TERRA_DTYPE_U8)
+    return fail(TERRA_ERR_DTYPE, "residual add is not defined for u8");
+  CopyGeom g;
+  int vb = 0;
+  const int st = prepare(geom, dtype, false, &g, &vb, windows, y, residual);
+  if (st != TERRA_OK) return st;
+  g.pad_pattern = 0;
+  hipStream_t s = (hipStream_t)stream;
+  switch (vb) {
+    case 16: dispatch_reverse<16>(dtype, windows, y, residual, g, s); break;
+    case 8: dispatch_reverse<8>(dtype, windows, y, residual, g, s); break;
+    case 4: dispatch_reverse<4>(dtype, windows, y, residual, g, s); break;
+    case 2:
+      if (dtype == TERRA_DTYPE_F16) launch_reverse<2, TERRA_DTYPE_F16>(windows, y, residual, g, s);
+      else if (dtype == TERRA_DTYPE_BF16) launch_reverse<2, TERRA_DTYPE_BF16>(windows, y, residual, g, s);
+      else launch_reverse<2, TERRA_DTYPE_U8>(windows, y, nullptr, g, s);
+      break;
+    default: launch_reverse<1, TERRA_DTYPE_U8>(windows, y, nullptr, g, s); break;
+  }
+  return launch_status("terra_swin_reverse");
+}

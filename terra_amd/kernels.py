@@ -1,0 +1,297 @@
+"""Tensor-level entry points of the HIP hot path.
+
+Each function validates its torch arguments, fills the C descriptor and calls
+the C ABI on the current HIP stream of the tensor's device.  There is no CPU
+or eager-PyTorch fallback: a tensor that is not on a ROCm device, or a build
+without ``libterra_swin.so``, raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Sequence, Tuple, Union
+
+import torch
+
+from . import _lib
+
+_DTYPES = {
+    torch.float32: _lib.DTYPE_F32,
+    torch.float16: _lib.DTYPE_F16,
+    torch.bfloat16: _lib.DTYPE_BF16,
+    torch.uint8: _lib.DTYPE_U8,
+}
+
+# Additive constants of the reference: the shift mask uses -100.0
+# (models/utils.py:84) and padded keys are filled with -10000.0
+# (models/attention.py:907).
+MASK_VALUE = -100.0
+PAD_KEY_VALUE = -10000.0
+
+
+@dataclass(frozen=True)
+class WindowGeometry:
+    """Token grid -> window grid geometry (mirror of ``terra_swin_geom``).
+
+    The window frame is the grid zero-padded by ``pad`` = (top, bottom, left,
+    right) and rolled by ``(-shift_h, -shift_w)``; windows of the frame rows
+    ``[win_row_begin, win_row_begin + win_rows)`` are emitted, and windows of an
+    image outside ``valid`` (flat index range) are pad windows.
+    """
+
+    batch: int
+    height: int
+    width: int
+    channels: int
+    window: int
+    shift_h: int = 0
+    shift_w: int = 0
+    pad: Tuple[int, int, int, int] = (0, 0, 0, 0)
+    win_row_begin: int = 0
+    win_rows: Optional[int] = None
+    valid: Optional[Tuple[int, int]] = None
+
+    @property
+    def frame_h(self) -> int:
+        return self.height + self.pad[0] + self.pad[1]
+
+    @property
+    def frame_w(self) -> int:
+        return self.width + self.pad[2] + self.pad[3]
+
+    @property
+    def rows(self) -> int:
+        return self.win_rows if self.win_rows is not None else self.frame_h // self.window - self.win_row_begin
+
+    @property
+    def cols(self) -> int:
+        return self.frame_w // self.window
+
+    @property
+    def windows_per_image(self) -> int:
+        return self.rows * self.cols
+
+    @property
+    def num_windows(self) -> int:
+        return self.batch * self.windows_per_image
+
+    def to_c(self) -> _lib.SwinGeom:
+        g = _lib.SwinGeom()
+        g.batch, g.height, g.width, g.channels, g.window = (
+            self.batch, self.height, self.width, self.channels, self.window)
+        g.shift_h, g.shift_w = self.shift_h, self.shift_w
+        g.pad_top, g.pad_bottom, g.pad_left, g.pad_right = self.pad
+        g.win_row_begin = self.win_row_begin
+        g.win_rows = self.win_rows if self.win_rows is not None else 0
+        if self.valid is not None:
+            g.valid_begin, g.valid_end = self.valid
+        else:
+            g.valid_begin, g.valid_end = 0, 0
+        return g
+
+
+@dataclass(frozen=True)
+class ShiftMask:
+    """Analytic Swin shift mask of a window frame (no [nW, N, N] tensor).
+
+    Equal, element for element, to ``get_swin_attention_mask`` of the frame
+    (models/utils.py:56-94) for the emitted window rows.
+    """
+
+    frame_h: int
+    frame_w: int
+    shift_h: int
+    shift_w: int
+    win_row_begin: int
+    win_rows: int
+    win_cols: int
+
+    @staticmethod
+    def from_geometry(geom: WindowGeometry) -> "ShiftMask":
+        return ShiftMask(geom.frame_h, geom.frame_w, geom.shift_h, geom.shift_w,
+                         geom.win_row_begin, geom.rows, geom.cols)
+
+
+@dataclass(frozen=True)
+class WindowMask:
+    """Mask terms of one attention call: a shift mask (analytic or explicit
+    ``[nW, N, N]`` fp32 tensor) plus optional per-window land bits (uint64 bit
+    j set: key j is land and receives ``mask_value``)."""
+
+    shift: Union[None, ShiftMask, torch.Tensor] = None
+    land_bits: Optional[torch.Tensor] = None
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"expected a tensor, got {type(t).__name__}")
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "terra_amd kernels run on ROCm devices only (got a tensor on "
+                f"'{t.device}'); there is no CPU fallback")
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _dtype_code(t: torch.Tensor, allowed: Sequence[torch.dtype]) -> int:
+    if t.dtype not in allowed:
+        raise TypeError(f"dtype {t.dtype} not supported here (supported: {', '.join(map(str, allowed))})")
+    return _DTYPES[t.dtype]
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def swin_partition(x: torch.Tensor, geom: WindowGeometry, pad_value: float = 0.0,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused pad + roll(-shift) + window_partition of ``x`` [B, H, W, C].
+
+    Returns windows ``[B * nW, ws*ws, C]`` (the layout of
+    ``window_partition(...).view(-1, ws*ws, C)``, models/transformer.py:225).
+    """
+    dev = _require_device(x)
+    code = _dtype_code(x, tuple(_DTYPES))
+    if x.dim() != 4 or tuple(x.shape) != (geom.batch, geom.height, geom.width, geom.channels):
+        raise ValueError(f"x shape {tuple(x.shape)} does not match geometry "
+                         f"{(geom.batch, geom.height, geom.width, geom.channels)}")
+    if not x.is_contiguous():
+        raise ValueError("x must be contiguous [B, H, W, C]")
+    shape = (geom.num_windows, geom.window * geom.window, geom.channels)
+    if out is None:
+        out = torch.empty(shape, dtype=x.dtype, device=dev)
+    elif tuple(out.shape) != shape or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
+        raise ValueError(f"out must be a contiguous {x.dtype} tensor of shape {shape} on {dev}")
+    c_geom = geom.to_c()
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_partition(_ptr(x), _ptr(out), code, ctypes.byref(c_geom),
+                                              float(pad_value), _stream(dev))
+    _lib.check(st, "terra_swin_partition")
+    return out
+
+
+def swin_reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional[torch.Tensor] = None,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused window_reverse + roll(+shift) + crop (+ residual) to [B, H, W, C]."""
+    dev = _require_device(windows) if residual is None else _require_device(windows, residual)
+    code = _dtype_code(windows, tuple(_DTYPES))
+    n = geom.window * geom.window
+    if windows.numel() != geom.num_windows * n * geom.channels:
+        raise ValueError(f"windows has {windows.numel()} elements, geometry needs "
+                         f"{geom.num_windows} x {n} x {geom.channels}")
+    if not windows.is_contiguous():
+        raise ValueError("windows must be contiguous")
+    shape = (geom.batch, geom.height, geom.width, geom.channels)
+    if residual is not None:
+        if residual.dtype != windows.dtype or residual.numel() != geom.batch * geom.height * geom.width * geom.channels:
+            raise ValueError("residual must match the output grid in dtype and size")
+        if not residual.is_contiguous():
+            raise ValueError("residual must be contiguous")
+    if out is None:
+        out = torch.empty(shape, dtype=windows.dtype, device=dev)
+    elif out.numel() != geom.batch * geom.height * geom.width * geom.channels or out.dtype != windows.dtype \
+            or not out.is_contiguous() or out.device != dev:
+        raise ValueError(f"out must be a contiguous {windows.dtype} tensor with {shape} elements on {dev}")
+    c_geom = geom.to_c()
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_reverse(_ptr(windows), _ptr(out), _ptr(residual), code,
+                                            ctypes.byref(c_geom), _stream(dev))
+    _lib.check(st, "terra_swin_reverse")
+    return out.view(shape)
+
+
+def _row_stride(t: torch.Tensor, name: str, num_windows: int, tokens: int, channels: int) -> int:
+    if t.dim() != 3 or tuple(t.shape) != (num_windows, tokens, channels):
+        raise ValueError(f"{name} must be [{num_windows}, {tokens}, {channels}], got {tuple(t.shape)}")
+    s0, s1, s2 = t.stride()
+    if s2 != 1 or s0 != tokens * s1:
+        raise ValueError(f"{name} must have unit channel stride and packed windows (strides {t.stride()})")
+    return s1
+
+
+def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
+                     window_size: Tuple[int, int], scale: float,
+                     bias_table: Optional[torch.Tensor] = None,
+                     mask: Union[None, torch.Tensor, ShiftMask, WindowMask] = None,
+                     n_real: Optional[int] = None,
+                     mask_value: float = MASK_VALUE, pad_key_value: float = PAD_KEY_VALUE,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused window-attention core: softmax(q k^T * scale + bias + mask) v.
+
+    q, k, v: [B_, N, C] (row stride may exceed C, e.g. slices of a fused qkv
+    projection); heads are contiguous D = C / num_heads column blocks.
+    Returns o [B_, N, C] contiguous, i.e. ``(attn @ v).transpose(1, 2)
+    .reshape(B_, N, C)`` of models/attention.py:278.
+    """
+    dev = _require_device(q, k, v)
+    code = _dtype_code(q, (torch.bfloat16, torch.float32))
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k and v must share a dtype")
+    num_windows, tokens, channels = q.shape
+    qs = _row_stride(q, "q", num_windows, tokens, channels)
+    ks = _row_stride(k, "k", num_windows, tokens, channels)
+    vs = _row_stride(v, "v", num_windows, tokens, channels)
+    if out is None:
+        out = torch.empty((num_windows, tokens, channels), dtype=q.dtype, device=dev)
+    os_ = _row_stride(out, "out", num_windows, tokens, channels)
+
+    d = _lib.SwinAttnDesc()
+    d.num_windows, d.tokens, d.channels, d.heads = num_windows, tokens, channels, num_heads
+    d.window_h, d.window_w = int(window_size[0]), int(window_size[1])
+    d.n_real = tokens if n_real is None else int(n_real)
+    d.q_stride, d.k_stride, d.v_stride, d.o_stride = qs, ks, vs, os_
+    d.scale, d.mask_value, d.pad_key_value = float(scale), float(mask_value), float(pad_key_value)
+
+    table = None
+    if bias_table is not None:
+        _require_device(bias_table)
+        n_rel = (2 * d.window_h - 1) * (2 * d.window_w - 1)
+        if tuple(bias_table.shape) != (n_rel, num_heads):
+            raise ValueError(f"bias table must be [{n_rel}, {num_heads}], got {tuple(bias_table.shape)}")
+        table = bias_table.detach().to(torch.float32).contiguous()
+
+    shift = mask.shift if isinstance(mask, WindowMask) else mask
+    land = mask.land_bits if isinstance(mask, WindowMask) else None
+    emask = None
+    d.mask_mode = _lib.MASK_NONE
+    d.mask_windows = 0
+    if isinstance(shift, ShiftMask):
+        d.mask_mode = _lib.MASK_SHIFT
+        d.frame_h, d.frame_w = shift.frame_h, shift.frame_w
+        d.shift_h, d.shift_w = shift.shift_h, shift.shift_w
+        d.win_row_begin, d.win_rows, d.win_cols = shift.win_row_begin, shift.win_rows, shift.win_cols
+    elif isinstance(shift, torch.Tensor):
+        _require_device(shift)
+        n_geo = d.window_h * d.window_w
+        if shift.dim() != 3 or tuple(shift.shape[1:]) != (n_geo, n_geo):
+            raise ValueError(f"mask must be [nW, {n_geo}, {n_geo}], got {tuple(shift.shape)}")
+        if num_windows % shift.shape[0] != 0:
+            raise ValueError(f"attention batch {num_windows} must be divisible by mask windows {shift.shape[0]}")
+        emask = shift.detach().to(torch.float32).contiguous()
+        d.mask_mode = _lib.MASK_EXPLICIT
+        d.mask_windows = shift.shape[0]
+    elif shift is not None:
+        raise TypeError(f"unsupported mask type {type(shift).__name__}")
+    if land is not None:
+        _require_device(land)
+        if land.dtype != torch.int64 or land.dim() != 1:
+            raise ValueError("land_bits must be a 1-D int64 tensor (one 64-bit key mask per window)")
+        if emask is not None and land.shape[0] != emask.shape[0]:
+            raise ValueError("land_bits and the explicit mask must cover the same number of windows")
+        if num_windows % land.shape[0] != 0:
+            raise ValueError(f"attention batch {num_windows} must be divisible by land windows {land.shape[0]}")
+        land = land.contiguous()
+        d.mask_windows = land.shape[0]
+
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out), code, ctypes.byref(d),
+                                             _ptr(table), _ptr(emask), _ptr(land), _stream(dev))
+    _lib.check(st, "terra_swin_attn_fwd")
+    return out

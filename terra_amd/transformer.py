@@ -1,0 +1,113 @@
+"""Drop-in ``SequentialSwinTransformer`` (models/transformer.py:71-356).
+
+The attention half of a Swin block on one GPU:
+
+    x -> norm1 -> [roll(-s) + window partition]      one HIP gather
+      -> q/k/v projection (one GEMM)                 hipBLASLt via torch
+      -> fused window-attention core                 one HIP kernel
+      -> proj                                        hipBLASLt via torch
+      -> [window reverse + roll(+s) + residual add]  one HIP scatter
+
+Module construction, parameter and buffer names (``norm1``, ``attn.*``,
+``attn_mask``) follow the reference so its checkpoints load.  The shift mask
+is evaluated in closed form inside the attention kernel; the dense
+``attn_mask`` buffer is kept only for state-dict compatibility and equals that
+closed form element for element.
+
+Additions that the reference does not have (both optional, build-defined):
+``land_mask`` — a [H, W] boolean grid whose land keys receive the mask value
+-100 in every window (folded into the attention mask); ``geometry`` overrides
+(padding, window-row range, valid-window range) for slabs such as one rank's
+share of a window-parallel grid.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import config, kernels
+from .attention import WindowAttention
+from .kernels import ShiftMask, WindowGeometry, WindowMask
+from .utils import get_swin_attention_mask, land_window_bits
+
+
+class SequentialSwinTransformer(torch.nn.Module):
+    def __init__(self, layer_idx=-1, height=720 // 6, width=1440 // 6, embedding_dim=4320,
+                 norm_layer=torch.nn.LayerNorm, window_size=6, num_heads=4320 // 72,
+                 use_attn_mask=True, use_relative_position_bias=True, use_flash_attention=False,
+                 init_seed_base=None, land_mask: Optional[torch.Tensor] = None,
+                 pad: Tuple[int, int, int, int] = (0, 0, 0, 0), win_row_begin: int = 0,
+                 win_rows: Optional[int] = None, valid_windows: Optional[Tuple[int, int]] = None):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.init_seed_base = None if init_seed_base is None else int(init_seed_base) + int(layer_idx) * 100
+        # W-MSA on even layers, SW-MSA (shift ws//2) on odd ones (models/transformer.py:88-91).
+        shift_size = 0 if (self.layer_idx % 2 == 0) else window_size // 2
+        if config.use_shift_size_0:
+            shift_size = 0
+        self.shift_size = shift_size
+        self.window_size = window_size
+        self.use_attn_mask = use_attn_mask
+        if config.use_layernorm:
+            self.norm1 = norm_layer(embedding_dim)
+        self.input_resolution = (height, width)
+        self.embedding_dim = embedding_dim
+        self.attn = WindowAttention(embedding_dim, window_size=(window_size, window_size), num_heads=num_heads,
+                                    qkv_bias=True, qk_scale=None, use_attn_mask=use_attn_mask,
+                                    use_relative_position_bias=use_relative_position_bias,
+                                    use_flash_attention=use_flash_attention, init_seed_base=self.init_seed_base)
+        self.pad = tuple(int(p) for p in pad)
+        self.win_row_begin = int(win_row_begin)
+        self.win_rows = win_rows
+        self.valid_windows = valid_windows
+        frame = (height + self.pad[0] + self.pad[1], width + self.pad[2] + self.pad[3])
+        attn_mask = None
+        if self.shift_size > 0 and self.use_attn_mask:
+            attn_mask = get_swin_attention_mask("sequential", frame, self.window_size, self.shift_size)
+        self.register_buffer("attn_mask", attn_mask)
+        if land_mask is not None:
+            land_mask = torch.as_tensor(land_mask).to(torch.bool)
+            if tuple(land_mask.shape) != (height, width):
+                raise ValueError(f"land_mask must be [{height}, {width}], got {tuple(land_mask.shape)}")
+            self.register_buffer("land_mask", land_mask, persistent=False)
+        else:
+            self.land_mask = None
+        self._land_bits_cache = {}
+
+    def geometry(self, batch: int) -> WindowGeometry:
+        H, W = self.input_resolution
+        return WindowGeometry(batch, H, W, self.embedding_dim, self.window_size, self.shift_size,
+                              self.shift_size, self.pad, self.win_row_begin, self.win_rows, self.valid_windows)
+
+    def window_mask(self, geom: WindowGeometry):
+        """Mask argument of the attention core for this block, or None."""
+        shift = ShiftMask.from_geometry(geom) if (self.shift_size > 0 and self.use_attn_mask) else None
+        land = None
+        if self.land_mask is not None:
+            key = (self.land_mask.device, self.land_mask.data_ptr())
+            land = self._land_bits_cache.get(key)
+            if land is None:
+                land = land_window_bits(self.land_mask, WindowGeometry(
+                    1, geom.height, geom.width, 1, geom.window, geom.shift_h, geom.shift_w, geom.pad,
+                    geom.win_row_begin, geom.win_rows, geom.valid))
+                self._land_bits_cache = {key: land}
+        if shift is None and land is None:
+            return None
+        return WindowMask(shift=shift, land_bits=land)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        H, W = self.input_resolution
+        B, L, C = x.shape
+        if L != H * W:
+            raise AssertionError("input feature has wrong size")
+        shortcut = x
+        if config.use_layernorm:
+            x = self.norm1(x)
+        geom = self.geometry(B)
+        x_windows = kernels.swin_partition(x.contiguous().view(B, H, W, C), geom)
+        attn_windows = self.attn(x_windows, mask=self.window_mask(geom))
+        out_dtype = torch.promote_types(attn_windows.dtype, shortcut.dtype)
+        y = kernels.swin_reverse(attn_windows.to(out_dtype), geom,
+                                 residual=shortcut.to(out_dtype).contiguous())
+        return y.view(B, H * W, C)

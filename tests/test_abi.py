@@ -1,0 +1,146 @@
+"""The C-ABI library: loads, exports what include/terra_swin.h declares, and
+rejects bad arguments before any launch (all on the CPU, no kernel runs)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import terra_amd._lib as L
+from terra_amd import kernels
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "terra_swin.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(terra_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_and_binding_agree():
+    assert _declared_functions() == sorted(L.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_struct_sizes():
+    lib = L.load()
+    assert lib.terra_abi_version() == L.ABI_VERSION
+    text = open(HEADER).read()
+    assert f"#define TERRA_SWIN_ABI_VERSION {L.ABI_VERSION}" in text
+    # every field of the C structs is 4 bytes wide
+    assert ctypes.sizeof(L.SwinGeom) == 4 * len(L.SwinGeom._fields_) == 60
+    assert ctypes.sizeof(L.SwinAttnDesc) == 4 * len(L.SwinAttnDesc._fields_) == 92
+
+
+def _geom(**kw):
+    g = L.SwinGeom()
+    vals = dict(batch=1, height=16, width=16, channels=8, window=8)
+    vals.update(kw)
+    for k, v in vals.items():
+        setattr(g, k, v)
+    return g
+
+
+FAKE = ctypes.c_void_p(1 << 20)  # never dereferenced: every case below fails validation
+
+
+@pytest.mark.parametrize("kw,code,text", [
+    (dict(height=15), -3, "not a multiple of window"),
+    (dict(window=0), -3, "must be positive"),
+    (dict(shift_h=16), -3, "shift"),
+    (dict(pad_top=-1), -3, "non-negative"),
+    (dict(win_row_begin=1, win_rows=2), -3, "window rows"),
+    (dict(valid_begin=3, valid_end=2), -3, "valid window range"),
+    (dict(valid_begin=0, valid_end=5), -3, "valid window range"),
+])
+def test_partition_rejects_bad_geometry(kw, code, text):
+    lib = L.load()
+    g = _geom(**kw)
+    st = lib.terra_swin_partition(FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(g), 0.0, None)
+    assert st == code
+    assert text in L.last_error()
+
+
+def test_partition_rejects_null_and_dtype():
+    lib = L.load()
+    g = _geom()
+    assert lib.terra_swin_partition(None, FAKE, L.DTYPE_BF16, ctypes.byref(g), 0.0, None) == -1
+    assert lib.terra_swin_partition(FAKE, FAKE, 9, ctypes.byref(g), 0.0, None) == -2
+    assert lib.terra_swin_partition(FAKE, FAKE, L.DTYPE_BF16, None, 0.0, None) == -1
+    assert lib.terra_swin_reverse(FAKE, FAKE, FAKE, L.DTYPE_U8, ctypes.byref(g), None) == -2
+
+
+def test_partition_rejects_misaligned_elements():
+    lib = L.load()
+    g = _geom()
+    assert lib.terra_swin_partition(ctypes.c_void_p((1 << 20) + 1), FAKE, L.DTYPE_F32, ctypes.byref(g), 0.0,
+                                    None) == -4
+
+
+def _desc(**kw):
+    d = L.SwinAttnDesc()
+    vals = dict(num_windows=4, tokens=64, channels=64, heads=2, window_h=8, window_w=8, n_real=64,
+                q_stride=64, k_stride=64, v_stride=64, o_stride=64, scale=0.17, mask_value=-100.0,
+                pad_key_value=-10000.0, mask_mode=0)
+    vals.update(kw)
+    for k, v in vals.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("kw,code,text", [
+    (dict(tokens=81, window_h=9, window_w=9, n_real=81), -5, "tokens per window"),
+    (dict(heads=3), -3, "not divisible"),
+    (dict(channels=48, heads=3, q_stride=48, k_stride=48, v_stride=48, o_stride=48), -5, "head dim"),
+    (dict(window_h=9), -5, "outside 1..8"),
+    (dict(n_real=0), -3, "n_real"),
+    (dict(q_stride=60), -3, ">= channels"),
+    (dict(q_stride=68), -4, "multiples"),
+    (dict(mask_mode=7), -3, "mask_mode"),
+    (dict(mask_mode=2, mask_windows=4), -1, "explicit"),
+    (dict(mask_mode=1, frame_h=16, frame_w=16, shift_h=4, shift_w=4, win_rows=2, win_cols=3), -3, "win_cols"),
+    (dict(mask_mode=1, frame_h=16, frame_w=16, shift_h=8, shift_w=4, win_rows=2, win_cols=2), -3, "0 < shift"),
+    (dict(mask_mode=1, frame_h=16, frame_w=24, shift_h=4, shift_w=4, win_rows=2, win_cols=3), -3, "multiple"),
+])
+def test_attention_rejects_bad_descriptors(kw, code, text):
+    lib = L.load()
+    d = _desc(**kw)
+    st = lib.terra_swin_attn_fwd(FAKE, FAKE, FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(d), None, None, None, None)
+    assert st == code, L.last_error()
+    assert text in L.last_error()
+
+
+def test_attention_rejects_dtype_null_alignment():
+    lib = L.load()
+    d = _desc()
+    assert lib.terra_swin_attn_fwd(FAKE, FAKE, FAKE, FAKE, L.DTYPE_F16, ctypes.byref(d), None, None, None,
+                                   None) == -2
+    assert lib.terra_swin_attn_fwd(None, FAKE, FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(d), None, None, None,
+                                   None) == -1
+    bad = ctypes.c_void_p((1 << 20) + 8)
+    assert lib.terra_swin_attn_fwd(bad, FAKE, FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(d), None, None, None,
+                                   None) == -4
+
+
+def test_python_wrapper_raises_instead_of_falling_back():
+    x = torch.zeros(1, 16, 16, 8)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        kernels.swin_partition(x, kernels.WindowGeometry(1, 16, 16, 8, 8))
+    q = torch.zeros(2, 64, 64)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        kernels.window_attention(q, q, q, 2, (8, 8), 0.1)
+
+
+def test_check_maps_status_to_exceptions():
+    with pytest.raises(ValueError, match="TERRA_ERR_SHAPE"):
+        L.check(-3, "x")
+    with pytest.raises(L.TerraError):
+        L.check(-6, "x")
+    L.check(0, "x")

@@ -1,0 +1,178 @@
+"""GPU parity of the fused window-attention core against the CPU oracle.
+
+Tolerances (written per the path's contract):
+  fp32 activations: max |out - ref| <= 1e-5 and <= 1e-5 * max |ref| (+1e-6),
+                    ref = oracle in float64 on the same fp32 inputs;
+  bf16 activations: max |out - ref| <= 2e-2 * max |ref|, ref = oracle in fp32
+                    on the same bf16-rounded inputs (the kernel rounds the
+                    probabilities to bf16 before P@V, as autocast does).
+Mask terms are exact small integers, so the analytic shift mask must agree
+bit for bit with the same mask given as a dense tensor.
+"""
+import pytest
+import torch
+
+from oracle import swin_oracle as so
+from terra_amd import kernels, utils, workloads
+from terra_amd.kernels import ShiftMask, WindowGeometry, WindowMask
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B_, N, C, heads, ws, dtype, seed, qkv_scale=1.0):
+    q = workloads.activations((B_, N, C), seed, torch.float32) * qkv_scale
+    k = workloads.activations((B_, N, C), seed + 1, torch.float32) * qkv_scale
+    v = workloads.activations((B_, N, C), seed + 2, torch.float32)
+    g = workloads.generator(seed + 3)
+    table = torch.empty((2 * ws - 1) ** 2, heads)
+    torch.nn.init.trunc_normal_(table, std=0.02, generator=g)
+    return q.to(dtype), k.to(dtype), v.to(dtype), table
+
+
+def _check(out, ref, dtype):
+    out = out.double().cpu()
+    ref = ref.double()
+    err = (out - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    if dtype == torch.float32:
+        assert err <= 1e-5 and err <= 1e-5 * scale + 1e-6, (err, scale)
+    else:
+        assert err <= 2e-2 * scale, (err, scale)
+    return err / max(scale, 1e-30)
+
+
+def _run(dev, q, k, v, heads, ws, table, mask=None, n_real=None, **kw):
+    return kernels.window_attention(q.to(dev), k.to(dev), v.to(dev), heads, (ws, ws), (q.shape[-1] // heads) ** -0.5,
+                                    bias_table=None if table is None else table.to(dev), mask=mask, n_real=n_real,
+                                    **kw)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ws,C,heads", [(7, 96, 3), (8, 192, 6), (8, 768, 12), (7, 128, 4), (6, 64, 2)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_core_no_mask(dev, dtype, ws, C, heads, with_bias):
+    B_, N = 24, ws * ws
+    q, k, v, table = _inputs(B_, N, C, heads, ws, dtype, 200)
+    tab = table if with_bias else None
+    out = _run(dev, q, k, v, heads, ws, tab)
+    cd = torch.float64 if dtype == torch.float32 else torch.float32
+    ref = so.window_attention_core(q, k, v, heads, (C // heads) ** -0.5, tab, (ws, ws), compute_dtype=cd)
+    _check(out, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("H,W,ws,s,C,heads", [(56, 56, 7, 3, 96, 3), (32, 48, 8, 4, 192, 6), (16, 24, 8, 4, 128, 2)])
+def test_core_shift_mask_analytic_and_dense(dev, dtype, H, W, ws, s, C, heads):
+    nW = (H // ws) * (W // ws)
+    B = 2
+    q, k, v, table = _inputs(B * nW, ws * ws, C, heads, ws, dtype, 210, qkv_scale=2.0)
+    dense = so.shift_mask(H, W, ws, s)
+    analytic = ShiftMask(H, W, s, s, 0, H // ws, W // ws)
+    out_a = _run(dev, q, k, v, heads, ws, table, mask=analytic)
+    out_d = _run(dev, q, k, v, heads, ws, table, mask=dense.to(dev))
+    assert torch.equal(out_a, out_d)
+    cd = torch.float64 if dtype == torch.float32 else torch.float32
+    ref = so.window_attention_core(q, k, v, heads, (C // heads) ** -0.5, table, (ws, ws), dense, compute_dtype=cd)
+    _check(out_a, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_core_land_bits(dev, dtype):
+    H, W, ws, s, C, heads = 32, 64, 8, 4, 192, 6
+    land = workloads.land_mask(H, W, seed=9)
+    g = WindowGeometry(1, H, W, 1, ws, s, s)
+    bits = utils.land_window_bits(land.to(dev), g)
+    nW = g.num_windows
+    q, k, v, table = _inputs(nW, ws * ws, C, heads, ws, dtype, 220, qkv_scale=2.0)
+    mask = WindowMask(shift=ShiftMask.from_geometry(g), land_bits=bits)
+    out = _run(dev, q, k, v, heads, ws, table, mask=mask)
+    total = so.fold_land(so.shift_mask(H, W, ws, s), so.land_key_flags(land, ws, s, s))
+    out_dense = _run(dev, q, k, v, heads, ws, table, mask=total.to(dev))
+    assert torch.equal(out, out_dense)
+    cd = torch.float64 if dtype == torch.float32 else torch.float32
+    ref = so.window_attention_core(q, k, v, heads, (C // heads) ** -0.5, table, (ws, ws), total, compute_dtype=cd)
+    _check(out, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_core_padded_tokens_and_keys(dev, dtype):
+    # a10: 49 real tokens of a 7x7 window carried in 64-token rows; bias and
+    # mask cover the real 49 x 49 block; keys >= 49 get -10000.
+    B_, N, C, heads, ws = 16, 64, 128, 4, 7
+    q, k, v, table = _inputs(B_, N, C, heads, ws, dtype, 230)
+    mask = so.shift_mask(14, 14, 7, 3)
+    out = _run(dev, q, k, v, heads, ws, table, mask=mask.to(dev), n_real=49)
+    cd = torch.float64 if dtype == torch.float32 else torch.float32
+    ref = so.window_attention_core(q, k, v, heads, (C // heads) ** -0.5, table, (ws, ws), mask, n_real=49,
+                                   compute_dtype=cd)
+    _check(out, ref, dtype)
+
+
+def test_core_strided_qkv_equals_contiguous(dev):
+    B_, N, C, heads, ws = 32, 64, 192, 6, 8
+    qkv = workloads.activations((B_, N, 3 * C), 240, torch.bfloat16).to(dev)
+    table = (workloads.activations((225, heads), 241) * 0.02).to(dev)
+    q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
+    a = kernels.window_attention(q, k, v, heads, (ws, ws), 32 ** -0.5, bias_table=table)
+    b = kernels.window_attention(q.contiguous(), k.contiguous(), v.contiguous(), heads, (ws, ws), 32 ** -0.5,
+                                 bias_table=table)
+    assert torch.equal(a, b)
+
+
+def test_core_deterministic(dev):
+    B_, N, C, heads, ws = 64, 64, 192, 6, 8
+    q, k, v, table = _inputs(B_, N, C, heads, ws, torch.bfloat16, 250)
+    a = _run(dev, q, k, v, heads, ws, table)
+    b = _run(dev, q, k, v, heads, ws, table)
+    assert torch.equal(a, b)
+
+
+def test_core_reference_autocast_distance(dev):
+    """The kernel sits at least as close to the fp32 restatement as the
+    reference's own bf16 autocast op sequence does (reported, bounded)."""
+    B_, N, C, heads, ws = 64, 64, 192, 6, 8
+    q, k, v, table = _inputs(B_, N, C, heads, ws, torch.bfloat16, 260, qkv_scale=2.0)
+    out = _run(dev, q, k, v, heads, ws, table).double().cpu()
+    ref = so.window_attention_core(q, k, v, heads, 32 ** -0.5, table, (ws, ws)).double()
+    ac = so.window_attention_autocast_bf16(q, k, v, heads, 32 ** -0.5, table, (ws, ws)).double()
+    e_kernel = (out - ref).abs().max().item()
+    e_ref = (ac - ref).abs().max().item()
+    assert e_kernel <= e_ref * 1.5 + 1e-6, (e_kernel, e_ref)
+
+
+@pytest.mark.parametrize("name", ["c3", "c5"])
+def test_core_full_size_sampled_windows(dev, name):
+    """Full-size launch (every window computed); a seeded sample of windows is
+    checked against the oracle, and the whole output must be finite."""
+    cfg = workloads.CONFIGS[name]
+    B_, N, C, heads, ws = cfg.num_windows, cfg.tokens, cfg.channels, cfg.heads, cfg.window
+    q = workloads.activations((B_, N, C), 270, torch.bfloat16)
+    k = workloads.activations((B_, N, C), 271, torch.bfloat16)
+    v = workloads.activations((B_, N, C), 272, torch.bfloat16)
+    table = workloads.activations(((2 * ws - 1) ** 2, heads), 273) * 0.02
+    g = WindowGeometry(cfg.batch, cfg.height, cfg.width, 1, ws, cfg.shift, cfg.shift, cfg.pad,
+                       cfg.win_row_begin, cfg.win_rows, cfg.valid)
+    land = workloads.land_mask(cfg.height, cfg.width, seed=274)
+    bits = utils.land_window_bits(land.to(dev), WindowGeometry(1, cfg.height, cfg.width, 1, ws, cfg.shift,
+                                                                cfg.shift, cfg.pad, cfg.win_row_begin,
+                                                                cfg.win_rows, cfg.valid))
+    mask = WindowMask(shift=ShiftMask.from_geometry(g), land_bits=bits)
+    out = _run(dev, q, k, v, heads, ws, table, mask=mask)
+    assert torch.isfinite(out.float()).all()
+    # dense mask of the emitted windows, for the sampled ones
+    fh, fw = g.frame_h, g.frame_w
+    full = so.shift_mask(fh, fw, ws, cfg.shift).view(fh // ws, fw // ws, N, N)
+    rows = g.rows
+    shift_m = full[g.win_row_begin:g.win_row_begin + rows].reshape(rows * (fw // ws), N, N)
+    flags = so.land_key_flags(land, ws, cfg.shift, cfg.shift, cfg.pad, cfg.win_row_begin, cfg.win_rows, cfg.valid)
+    total = so.fold_land(shift_m, flags)
+    per_img = g.windows_per_image
+    gen = workloads.generator(275)
+    sample = torch.randperm(B_, generator=gen)[:384]
+    # always include the boundary windows of the last row / column
+    sample = torch.unique(torch.cat([sample, torch.arange(per_img - fw // ws, per_img),
+                                     torch.arange(fw // ws - 1, per_img, fw // ws)]))
+    # window w uses total[w % per_img]; one mask per sampled window
+    ref = so.window_attention_core(q[sample], k[sample], v[sample], heads, (C // heads) ** -0.5, table, (ws, ws),
+                                   total[sample % per_img])
+    _check(out.cpu()[sample], ref, torch.bfloat16)

@@ -1,0 +1,194 @@
+"""Pins the CPU oracle (oracle/swin_oracle.py) before anything is checked against it.
+
+Each oracle function is compared with something it cannot share a mistake
+with: brute-force coordinate loops (oracle/brute.py), closed forms and known
+answers, library special cases, and the reference's own unit-test vector.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import brute
+from oracle import swin_oracle as so
+
+
+def _rand(shape, seed, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float64).to(dtype)
+
+
+GRIDS = [  # (B, H, W, C, ws, shift)
+    (2, 14, 21, 3, 7, 3),
+    (1, 16, 24, 5, 8, 4),
+    (2, 14, 14, 2, 7, 0),
+    (1, 12, 18, 4, 6, 3),
+]
+
+
+@pytest.mark.parametrize("B,H,W,C,ws,s", GRIDS)
+def test_roll_partition_matches_brute(B, H, W, C, ws, s):
+    x = _rand((B, H, W, C), 1)
+    got = so.roll_partition(x, ws, s).numpy()
+    want = brute.partition(x.numpy(), ws, shift_h=s, shift_w=s)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("B,H,W,C,ws,s", GRIDS)
+def test_reverse_unroll_matches_brute_and_inverts(B, H, W, C, ws, s):
+    x = _rand((B, H, W, C), 2)
+    win = so.roll_partition(x, ws, s)
+    y = so.reverse_unroll(win, ws, H, W, s)
+    assert torch.equal(y, x)  # reverse o partition == id, roll(+s) o roll(-s) == id
+    want = brute.reverse(win.numpy(), B, H, W, ws, shift_h=s, shift_w=s)
+    assert np.array_equal(y.numpy(), want)
+
+
+def test_roll_matches_distributed_shift_formula():
+    # core/parallel/layout_transform.py:341-348 states the same map as
+    # shifted_i = (gi - s) mod H for the position a global row gi lands on.
+    H, W, s = 16, 24, 4
+    x = torch.arange(H * W, dtype=torch.float64).view(1, H, W, 1)
+    shifted = torch.roll(x, (-s, -s), (1, 2))
+    for gi in range(H):
+        for gj in range(W):
+            assert shifted[0, (gi - s) % H, (gj - s) % W, 0] == x[0, gi, gj, 0]
+
+
+FRAMES = [  # (B, H, W, ws, shift_h, shift_w, pad, win_row_begin, win_rows, valid)
+    (1, 13, 21, 7, 3, 3, (0, 1, 0, 0), 0, None, None),
+    (2, 10, 17, 4, 2, 1, (1, 1, 2, 1), 1, 2, None),
+    (2, 20, 16, 8, 4, 4, (0, 4, 0, 0), 0, 2, (3, 4)),
+    (1, 16, 16, 8, 4, 4, (0, 8, 0, 0), 0, 2, (1, 3)),
+]
+
+
+@pytest.mark.parametrize("B,H,W,ws,sh,sw,pad,r0,rows,valid", FRAMES)
+def test_partition_frame_matches_brute(B, H, W, ws, sh, sw, pad, r0, rows, valid):
+    x = _rand((B, H, W, 3), 3)
+    got = so.partition_frame(x, ws, sh, sw, pad, r0, rows, valid).numpy()
+    want = brute.partition(x.numpy(), ws, shift_h=sh, shift_w=sw, pad=pad, win_row_begin=r0,
+                           win_rows=rows, valid=valid)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("B,H,W,ws,sh,sw,pad,r0,rows,valid", FRAMES)
+def test_reverse_frame_matches_brute(B, H, W, ws, sh, sw, pad, r0, rows, valid):
+    x = _rand((B, H, W, 3), 4)
+    res = _rand((B, H, W, 3), 5)
+    win = so.partition_frame(x, ws, sh, sw, pad, r0, rows, valid)
+    win = win + _rand(win.shape, 6)  # arbitrary window contents
+    got = so.reverse_frame(win, B, H, W, ws, sh, sw, pad, r0, rows, valid, residual=res).numpy()
+    want = brute.reverse(win.numpy(), B, H, W, ws, residual=res.numpy(), shift_h=sh, shift_w=sw, pad=pad,
+                         win_row_begin=r0, win_rows=rows, valid=valid)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("wh,ww", [(7, 7), (8, 8), (6, 6), (3, 5)])
+def test_relative_position_index(wh, ww):
+    idx = so.relative_position_index((wh, ww))
+    assert np.array_equal(idx.numpy(), brute.relative_index(wh, ww))
+    centre = (wh - 1) * (2 * ww - 1) + (ww - 1)
+    assert torch.all(idx + idx.T == 2 * centre)
+    assert torch.all(idx.diagonal() == centre)
+    # decoding idx gives back the coordinate difference of the two tokens
+    n = wh * ww
+    hi = torch.arange(n) // ww
+    wi = torch.arange(n) % ww
+    dh, dw = torch.div(idx, 2 * ww - 1, rounding_mode="floor") - (wh - 1), idx % (2 * ww - 1) - (ww - 1)
+    assert torch.equal(dh, hi[:, None] - hi[None, :])
+    assert torch.equal(dw, wi[:, None] - wi[None, :])
+
+
+def test_relative_position_index_known_values():
+    i7 = so.relative_position_index((7, 7))
+    assert i7[0, 0] == 84 and i7.max() == 168 and i7[48, 0] == 168 and i7.min() == 0 and i7[0, 48] == 0
+    i8 = so.relative_position_index((8, 8))
+    assert i8[0, 0] == 112 and i8.max() == 224 and i8[63, 0] == 224 and i8[0, 63] == 0
+
+
+def test_bias_gather_matches_loops():
+    table = _rand((169, 3), 7)
+    bias = so.relative_position_bias(table, (7, 7))
+    idx = brute.relative_index(7, 7)
+    for h in range(3):
+        for i in range(0, 49, 5):
+            for j in range(0, 49, 3):
+                assert bias[h, i, j] == table[idx[i, j], h]
+
+
+@pytest.mark.parametrize("H,W,ws,s", [(14, 21, 7, 3), (16, 24, 8, 4), (56, 56, 7, 3), (24, 16, 8, 2)])
+def test_shift_mask_matches_brute(H, W, ws, s):
+    m = so.shift_mask(H, W, ws, s)
+    assert np.array_equal(m.numpy(), brute.shift_mask(H, W, ws, s))
+    assert torch.equal(m, m.transpose(1, 2))
+    assert torch.all(m.diagonal(dim1=1, dim2=2) == 0)
+    nww = W // ws
+    interior = [w for w in range(m.shape[0]) if w // nww < H // ws - 1 and w % nww < nww - 1]
+    assert torch.all(m[interior] == 0)
+
+
+def test_shift_mask_known_counts():
+    m7 = so.shift_mask(56, 56, 7, 3)  # 8 x 8 windows
+    assert int((m7[7 * 8 + 0] == -100).sum()) == 1176      # last row, not last column
+    assert int((m7[7 * 8 + 7] == -100).sum()) == 1776      # bottom-right
+    assert int((m7[0 * 8 + 7] == -100).sum()) == 1176      # last column, not last row
+    m8 = so.shift_mask(32, 32, 8, 4)
+    assert int((m8[3 * 4 + 0] == -100).sum()) == 2048
+    assert int((m8[3 * 4 + 3] == -100).sum()) == 3072
+    assert set(torch.unique(m8).tolist()) == {-100.0, 0.0}
+
+
+def test_land_flags_and_fold():
+    g = torch.Generator().manual_seed(11)
+    land = torch.rand(16, 24, generator=g) < 0.3
+    flags = so.land_key_flags(land, 8, 4, 4)
+    src = brute.frame_source(1, 16, 24, 8, shift_h=4, shift_w=4)
+    want = np.array([bool(land[s[1], s[2]]) if s is not None else False for s in src]).reshape(-1, 64)
+    assert np.array_equal(flags.numpy(), want)
+    m = so.shift_mask(16, 24, 8, 4)
+    tot = so.fold_land(m, flags)
+    for w in range(tot.shape[0]):
+        for j in range(64):
+            assert torch.equal(tot[w, :, j], m[w, :, j] + (-100.0 if want[w, j] else 0.0))
+
+
+@pytest.mark.parametrize("with_bias,with_mask,n_real", [(False, False, None), (True, False, None),
+                                                       (True, True, None), (True, True, 40)])
+def test_attention_core_matches_float64_brute(with_bias, with_mask, n_real):
+    B_, N, C, nH = 4, 49, 16, 2
+    q, k, v = _rand((B_, N, C), 20), _rand((B_, N, C), 21), _rand((B_, N, C), 22)
+    table = _rand((169, nH), 23) if with_bias else None
+    mask = so.shift_mask(14, 14, 7, 3).double() if with_mask else None
+    scale = (C // nH) ** -0.5
+    got = so.window_attention_core(q, k, v, nH, scale, table, (7, 7), mask, n_real, compute_dtype=torch.float64)
+    bias = so.relative_position_bias(table, (7, 7)).numpy() if with_bias else None
+    want = brute.attention(q.numpy(), k.numpy(), v.numpy(), nH, scale, bias,
+                           None if mask is None else mask.numpy(), n_real)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_core_equals_sdpa_without_bias_and_mask():
+    B_, N, C, nH = 6, 64, 64, 2
+    q, k, v = _rand((B_, N, C), 30), _rand((B_, N, C), 31), _rand((B_, N, C), 32)
+    got = so.window_attention_core(q, k, v, nH, (C // nH) ** -0.5, compute_dtype=torch.float64)
+    split = lambda t: t.view(B_, N, nH, C // nH).transpose(1, 2)
+    want = F.scaled_dot_product_attention(split(q), split(k), split(v)).transpose(1, 2).reshape(B_, N, C)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_padded_keys_reduce_to_real_window():
+    # keys >= n_real get -10000, so their weight underflows to exactly 0: the
+    # result on the real rows equals attention over the first n_real tokens.
+    B_, N, C, nH, nr = 3, 64, 32, 1, 49
+    q, k, v = _rand((B_, N, C), 40), _rand((B_, N, C), 41), _rand((B_, N, C), 42)
+    got = so.window_attention_core(q, k, v, nH, 0.2, n_real=nr, compute_dtype=torch.float64)
+    ref = so.window_attention_core(q[:, :nr], k[:, :nr], v[:, :nr], nH, 0.2, compute_dtype=torch.float64)
+    torch.testing.assert_close(got[:, :nr], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_ragged_row_major_reference_vector():
+    # tests/unit/test_window_assignment.py:10-23 of the reference
+    per_rank = so.ragged_row_major(2, 5, 4)
+    ids = [[r * 5 + c for r, c in chunk] for chunk in per_rank]
+    assert ids == [[0, 1], [2, 3, 4], [5, 6], [7, 8, 9]]
