@@ -26,6 +26,9 @@ HIPCC_FLAGS = [
     "-shared",
     # Packed-fp32 VALU ops are kept out of the device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in arch VGPRs (no AGPR round trip): keeps the attention
+    # kernel at <= 128 VGPRs, i.e. 4 waves per SIMD.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
 ]
 
