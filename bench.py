@@ -4,11 +4,11 @@ Step = one SW-MSA attention half of a Swin block on config c3 (the
 high-resolution ocean stage: B=1, 512x1024 tokens, C=192, 6 heads, window 8,
 shift 4, ~30 % land folded into the mask), bf16, inputs resident in HBM:
 
-    norm1 -> [roll + partition] -> qkv GEMM -> [fused window attention]
+    [norm1 + roll + partition] -> qkv GEMM -> [fused window attention]
           -> proj GEMM -> [reverse + roll + residual]
 
-The bracketed stages are this library's HIP kernels; LayerNorm and the GEMMs
-are torch (hipBLASLt).  `value` is tokens/s of the whole step.  The
+The bracketed stages are this library's HIP kernels; the two GEMMs are torch
+(hipBLASLt).  `value` is tokens/s of the whole step.  The
 `roofline` object is for the fused attention kernel (the path's dominant
 custom kernel), timed with HIP events on the launch stream over the timed
 steps; partition / reverse are reported under `kernels`.
@@ -118,7 +118,7 @@ def main():
     # Per-kernel events on the launch stream (torch's current stream, which the
     # C ABI receives as its hipStream_t).
     events = {"partition": [], "window_attention": [], "reverse": []}
-    orig = (kernels.swin_partition, kernels.window_attention, kernels.swin_reverse)
+    orig = (kernels.swin_partition_ln, kernels.window_attention, kernels.swin_reverse)
     recording = {"on": False}
 
     def timed(name, fn):
@@ -134,11 +134,9 @@ def main():
             return out
         return wrapper
 
-    import terra_amd.transformer as tr
-    import terra_amd.attention as at
-    tr.kernels.swin_partition = timed("partition", orig[0])
-    tr.kernels.swin_reverse = timed("reverse", orig[2])
-    at.kernels.window_attention = timed("window_attention", orig[1])
+    kernels.swin_partition_ln = timed("partition", orig[0])
+    kernels.window_attention = timed("window_attention", orig[1])
+    kernels.swin_reverse = timed("reverse", orig[2])
 
     with torch.no_grad():
         for _ in range(args.warmup):
@@ -153,7 +151,7 @@ def main():
         t1.record()
         torch.cuda.synchronize()
         recording["on"] = False
-    kernels.swin_partition, kernels.window_attention, kernels.swin_reverse = orig
+    kernels.swin_partition_ln, kernels.window_attention, kernels.swin_reverse = orig
     ms = t0.elapsed_time(t1) / args.steps
 
     B_, N, C = cfg.num_windows, cfg.tokens, cfg.channels
@@ -184,7 +182,7 @@ def main():
         "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
         "data": "synthetic (seeded N(0,1) activations, trunc-normal(0.02) weights, seeded smoothed-noise land mask)",
         "config": {
-            "workload": (f"{cfg.name}: SW-MSA attention half of a Swin block (LN, roll+partition, qkv GEMM, fused "
+            "workload": (f"{cfg.name}: SW-MSA attention half of a Swin block (LN+roll+partition, qkv GEMM, fused "
                          f"window attention, proj GEMM, reverse+roll+residual), B={cfg.batch}, "
                          f"{cfg.height}x{cfg.width} tokens, C={C}, {cfg.heads} heads, window {cfg.window}, "
                          f"shift {cfg.shift}" + (", ~30% land mask" if cfg.land else "")),
@@ -213,8 +211,8 @@ def main():
                 "windows_per_s": B_ / (t_attn * 1e-6),
                 "tokens_per_s": tokens / (t_attn * 1e-6),
             },
-            "partition": {"us": t_part, "GB_s": part_bytes / (t_part * 1e-6) / 1e9,
-                          "hbm_frac": part_bytes / (t_part * 1e-6) / 1e9 / HBM_PEAK_GBS},
+            "layernorm_partition": {"us": t_part, "GB_s": part_bytes / (t_part * 1e-6) / 1e9,
+                                    "hbm_frac": part_bytes / (t_part * 1e-6) / 1e9 / HBM_PEAK_GBS},
             "reverse_residual": {"us": t_rev, "GB_s": rev_bytes / (t_rev * 1e-6) / 1e9,
                                  "hbm_frac": rev_bytes / (t_rev * 1e-6) / 1e9 / HBM_PEAK_GBS},
         },

@@ -140,6 +140,20 @@ int terra_swin_partition(const void* x, void* windows, int dtype,
                          const terra_swin_geom* geom, float pad_value,
                          void* stream);
 
+/* Fused LayerNorm + pad + cyclic shift + window partition.
+ * Replaces  x = self.norm1(x)      (nn.LayerNorm over C)  models/transformer.py:98, 150
+ * followed by the sequence terra_swin_partition replaces.  Statistics are
+ * fp32 over the C channels of each token, y = (x - mean) * rsqrt(var + eps)
+ * * gamma + beta, rounded once to the activation dtype (f32 / f16 / bf16).
+ * gamma, beta: C floats each, or NULL for 1 / 0.  Padding applies to the
+ * normalised grid: frame padding and pad windows are written as pad_value.
+ * Needs C * element size to be a multiple of 16 bytes and at most 1536.
+ */
+int terra_swin_partition_ln(const void* x, void* windows, int dtype,
+                            const terra_swin_geom* geom, const float* gamma,
+                            const float* beta, float eps, float pad_value,
+                            void* stream);
+
 /* Fused window reverse + inverse cyclic shift + crop (+ residual add).
  * Replaces  window_reverse(attn_windows, ws, H, W)    models/utils.py:41-45
  *           torch.roll(shifted_x, (s, s), dims=(1, 2))  models/transformer.py:246

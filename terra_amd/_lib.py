@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "terra_abi_version",
     "terra_last_error",
     "terra_swin_partition",
+    "terra_swin_partition_ln",
     "terra_swin_reverse",
     "terra_swin_attn_fwd",
 )
@@ -134,6 +135,9 @@ def load() -> ctypes.CDLL:
         lib.terra_last_error.argtypes = []
         lib.terra_swin_partition.restype = ctypes.c_int
         lib.terra_swin_partition.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(SwinGeom), ctypes.c_float, vp]
+        lib.terra_swin_partition_ln.restype = ctypes.c_int
+        lib.terra_swin_partition_ln.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(SwinGeom), vp, vp,
+                                                ctypes.c_float, ctypes.c_float, vp]
         lib.terra_swin_reverse.restype = ctypes.c_int
         lib.terra_swin_reverse.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinGeom), vp]
         lib.terra_swin_attn_fwd.restype = ctypes.c_int

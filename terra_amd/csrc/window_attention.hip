@@ -1,32 +1,37 @@
 // Fused per-window multi-head attention forward for gfx950.
 //
-// One wavefront computes one (window, head) item.  With the window padded to
-// 64 tokens (4 tiles of 16) and head dim D:
+// Math per (window, head), window padded to 64 tokens (4 tiles of 16), head
+// dim D:
 //
-//   S^T = K Q^T      v_mfma_f32_16x16x32_bf16 (bf16) / 16x16x4_f32 (fp32).
-//                    Both operands come straight from global memory: lane
-//                    (c, g) of a 16-row tile loads row 16t + c, channels
-//                    [8g, 8g + 8) of a 32-channel step as one 16-byte load.
-//   softmax          fp32, in the log2 domain: y = s*scale*log2e + bias*log2e
-//                    (+ mask*log2e), p = exp2(y - max).  A query row lives in
-//                    4 lanes x 16 registers: in-lane reduction + 2 shuffles.
+//   S^T = K Q^T      v_mfma_f32_16x16x32_bf16 (bf16) / 16x16x4_f32 (fp32)
+//   softmax          fp32 in the log2 domain: y = s*scale*log2e + bias*log2e
+//                    (+ mask*log2e), p = exp2(y - max); a query row lives in
+//                    4 lanes x 16 registers (in-lane reduction + 2 shuffles)
 //   O^T = V^T P^T    P^T comes out of the S^T accumulators already in MFMA
-//                    operand order; V is staged in LDS (row-major, padded
-//                    pitch) and read as the transposed operand.  1/sum is
-//                    applied to O, not to P.
+//                    operand order; V is read from LDS as the transposed
+//                    operand; 1/sum is applied to O, not to P.
 //
 // Accumulator layout of a 16x16 tile (lane l, g = l/16, c = l%16): element
 // (row 4g + r, col c), r = 0..3.  In S^T rows are keys and columns queries,
-// so lane l holds queries i = 16*it + c and keys j = 16*jt + 4g + r.
+// so lane l holds queries i = 16*it + c and keys j = 16*jt + 4g + r.  Query
+// tiles are processed in two halves (it = 0,1 then 2,3): at most 32 score
+// registers are live and a wave fits in 128 VGPRs.
 //
-// The query tiles are processed in two halves (it = 0,1 then 2,3) so that at
-// most 32 score registers are live; the wave stays within 128 VGPRs (4 waves
-// per SIMD).
+// Two kernels share that core:
 //
-// kWs8 specialises 8x8 windows (N = 64): the relative-position index of lane
-// element (it, jt, r) is lane_base + 30*(it - jt) - r, so the bias comes from
-// LDS with compile-time offsets and no index arithmetic.  Other windows
-// (N <= 64, any Wh x Ww <= 8 x 8, padded tokens) take the generic path.
+//   window_attn_tile_kernel   bf16, 8x8 windows, no padded tokens, analytic
+//       masks.  One workgroup per (window, group of G heads), one wave per
+//       head.  The group's q, k, v rows (G*D <= 192 channels, a contiguous
+//       384-byte slice of each token row) are streamed into LDS as whole
+//       cache lines with nontemporal loads; O is staged in LDS over Q and
+//       streamed out as whole lines.  The relative-position index of lane
+//       element (it, jt, r) is lane_base + 30*(it - jt) - r, so the bias comes
+//       from LDS with compile-time offsets.
+//
+//   window_attn_wave_kernel   everything else (fp32, any window up to 8x8,
+//       padded tokens and keys, explicit dense masks): one wavefront per
+//       (window, head), K and Q fragments loaded straight from global memory,
+//       V staged in the wave's LDS.
 #include "common.h"
 
 #include <math.h>
@@ -37,9 +42,8 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
 constexpr int kNPad = 64;       // window tokens padded to 4 tiles of 16
 constexpr int kTableMax = 228;  // >= (2*8-1)^2 = 225, multiple of 4
 constexpr float kLog2e = 1.4426950408889634f;
@@ -66,32 +70,14 @@ struct AttnParams {
   int32_t mask_mode, mask_windows;
   int32_t frame_h, frame_w, shift_h, shift_w;
   int32_t win_row_begin, win_rows, win_cols;
+  // window-tile kernel
+  int32_t group;      // heads per workgroup
+  int32_t groups;     // head groups per window
 };
 
 __device__ __forceinline__ int region(int coord, int extent, int ws, int shift) {
   // Swin shift-mask slices (0:-ws), (-ws:-shift), (-shift:) of one axis.
   return coord < extent - ws ? 0 : (coord < extent - shift ? 1 : 2);
-}
-
-template <bool kBf16> struct EltTraits;
-template <> struct EltTraits<true> { using T = uint16_t; };
-template <> struct EltTraits<false> { using T = float; };
-
-template <bool kBf16, int D>
-struct alignas(16) LdsLayout {
-  using T = typename EltTraits<kBf16>::T;
-  // Row pitch of the per-wave V tile: 16 extra bytes put the 4 row groups
-  // read by one instruction into disjoint LDS bank ranges.
-  static constexpr int kPitch = D + 16 / (int)sizeof(T);
-  T v[kWaves][kNPad * kPitch];
-  float table[kWaves][kTableMax];
-};
-
-// Orders this wave's LDS writes before its later LDS reads.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ __forceinline__ float xor_max(float v) {
@@ -111,13 +97,477 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-template <bool kBf16, int D, bool kWs8, bool kExplicit>
-__global__ __launch_bounds__(kThreads) void window_attn_kernel(const AttnParams p) {
+// Mask state of one window (uniform across the wave).
+struct WindowMaskState {
+  bool use_shift;     // window touches the last window row / column of the frame
+  bool use_mask;      // shift boundary or any land key
+  int wr, wc;         // window row / column in the frame
+  uint64_t land;      // land bit per key
+};
+
+__device__ __forceinline__ WindowMaskState window_mask_state(const AttnParams& p, int w, bool analytic) {
+  WindowMaskState m;
+  m.use_shift = false;
+  m.wr = m.wc = 0;
+  if (analytic && p.mask_mode == TERRA_MASK_SHIFT) {
+    const int per_img = p.win_rows * p.win_cols;
+    const int wl = w % per_img;
+    const int rr = wl / p.win_cols;
+    m.wr = rr + p.win_row_begin;
+    m.wc = wl - rr * p.win_cols;
+    m.use_shift = (m.wr + 2) * p.window_h > p.frame_h || (m.wc + 2) * p.window_w > p.frame_w;
+  }
+  m.land = p.land_bits != nullptr ? p.land_bits[w % p.mask_windows] : 0ull;
+  m.use_mask = m.use_shift || m.land != 0ull;
+  return m;
+}
+
+// Per-lane index terms of the window geometry.
+//   kWs8: closed form for 8x8 windows.
+//   generic: lane t computes token t's terms, other lanes fetch them with
+//   shuffles; bias index idx(i, j) = base(i) - off(j).
+template <bool kWs8>
+struct LaneGeom {
+  const float* tab8;      // kWs8: bias pointer so that offsets 30*(it-jt) - r + 93 >= 0
+  const float* tab;       // generic: this head's bias column (x log2e)
+  int g_base, g_rid;      // generic: this lane's token terms (shuffle sources)
+  int off_j[kWs8 ? 1 : 4][4];
+  uint64_t rid_pack;      // 4-bit region id of key (jt, r) at bit 4*(4*jt + r)
+  uint64_t land_lane;     // land bit of key (jt, r) at bit 16*jt + r
+};
+
+template <bool kWs8>
+__device__ __forceinline__ void lane_geom_init(LaneGeom<kWs8>& lg, const AttnParams& p, const WindowMaskState& m,
+                                               const float* tab, int lane) {
+  const int g = lane >> 4, c16 = lane & 15;
+  lg.tab = tab;
+  lg.g_base = lg.g_rid = 0;
+  int g_off = 0;
+  if constexpr (kWs8) {
+    const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;  // in [93, 134]
+    lg.tab8 = tab + (lane_base - 93);
+  } else {
+    lg.tab8 = tab;
+    const int t = lane < p.n_geo ? lane : p.n_geo - 1;
+    const int ti = t / p.window_w;
+    const int tj = t - ti * p.window_w;
+    const int rel_w = 2 * p.window_w - 1;
+    lg.g_base = (ti + p.window_h - 1) * rel_w + tj + p.window_w - 1;
+    g_off = ti * rel_w + tj;
+    if (m.use_shift)
+      lg.g_rid = 3 * region(m.wr * p.window_h + ti, p.frame_h, p.window_h, p.shift_h) +
+                 region(m.wc * p.window_w + tj, p.frame_w, p.window_w, p.shift_w);
+  }
+  lg.rid_pack = 0;
+  lg.land_lane = m.land >> (4 * g);
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * jt + 4 * g + r;
+      int rid;
+      if constexpr (kWs8) {
+        rid = m.use_shift ? 3 * region(m.wr * 8 + 2 * jt + (g >> 1), p.frame_h, 8, p.shift_h) +
+                                region(m.wc * 8 + 4 * (g & 1) + r, p.frame_w, 8, p.shift_w)
+                          : 0;
+      } else {
+        const int jg = j < p.n_geo ? j : p.n_geo - 1;
+        lg.off_j[jt][r] = __shfl(g_off, jg);
+        rid = __shfl(lg.g_rid, jg);
+      }
+      lg.rid_pack |= (uint64_t)rid << (4 * (4 * jt + r));
+    }
+  }
+}
+
+// Turns the raw scores of query tiles it = 2*half + {0, 1} into unnormalised
+// probabilities in place and returns 1/rowsum per tile.
+template <bool kWs8, bool kExplicit>
+__device__ __forceinline__ void softmax_half(f32x4 (&s)[2][4], float (&inv)[2], int half, const AttnParams& p,
+                                             const WindowMaskState& m, const LaneGeom<kWs8>& lg,
+                                             const float* emask, int lane) {
+  const int g = lane >> 4, c16 = lane & 15;
+  int base_i[2] = {0, 0}, rid_i[2] = {0, 0};
+  bool i_geo[2] = {true, true};
+#pragma unroll
+  for (int il = 0; il < 2; ++il) {
+    const int it = 2 * half + il;
+    const int i = 16 * it + c16;
+    if constexpr (kWs8) {
+      if (m.use_shift)
+        rid_i[il] = 3 * region(m.wr * 8 + 2 * it + (c16 >> 3), p.frame_h, 8, p.shift_h) +
+                    region(m.wc * 8 + (c16 & 7), p.frame_w, 8, p.shift_w);
+    } else {
+      const int ig = i < p.n_geo ? i : p.n_geo - 1;
+      i_geo[il] = i < p.n_geo;
+      base_i[il] = __shfl(lg.g_base, ig);
+      rid_i[il] = __shfl(lg.g_rid, ig);
+    }
+  }
+  // Pass 1, branch-free: y = s * scale * log2e + bias * log2e.
+#pragma unroll
+  for (int il = 0; il < 2; ++il) {
+    const int it = 2 * half + il;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float b;
+        if constexpr (kWs8) {
+          b = lg.tab8[30 * (it - jt) - r + 93];
+        } else {
+          const int j = 16 * jt + 4 * g + r;
+          b = lg.tab[base_i[il] - lg.off_j[jt][r]];  // clamped indices: always in range
+          b = (i_geo[il] && j < p.n_geo) ? b : 0.f;
+        }
+        s[il][jt][r] = __builtin_fmaf(s[il][jt][r], p.scale_l2e, b);
+      }
+    }
+  }
+  // Pass 2 (only windows with a shift boundary or land keys): + mask.
+  if constexpr (kExplicit) {
+#pragma unroll
+    for (int il = 0; il < 2; ++il) {
+      const int i = 16 * (2 * half + il) + c16;
+      const int ig = i < p.n_geo ? i : p.n_geo - 1;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * jt + 4 * g + r;
+          const int jg = j < p.n_geo ? j : p.n_geo - 1;
+          const float me = emask[ig * p.n_geo + jg] * kLog2e;
+          const bool land_j = (lg.land_lane >> (16 * jt + r)) & 1ull;
+          const bool jin = kWs8 || j < p.n_geo;
+          s[il][jt][r] += ((i_geo[il] && jin) ? me : 0.f) + ((land_j && jin) ? p.mask_l2e : 0.f);
+        }
+      }
+    }
+  } else if (m.use_mask) {
+#pragma unroll
+    for (int il = 0; il < 2; ++il) {
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * jt + 4 * g + r;
+          const int rid_j = (int)((lg.rid_pack >> (4 * (4 * jt + r))) & 15ull);
+          const bool land_j = ((lg.land_lane >> (16 * jt + r)) & 1ull) && (kWs8 || j < p.n_geo);
+          const float ms = (i_geo[il] && rid_i[il] != rid_j) ? p.mask_l2e : 0.f;
+          s[il][jt][r] += ms + (land_j ? p.mask_l2e : 0.f);
+        }
+      }
+    }
+  }
+  // Padded keys (generic path): keys >= n_real take the pad value, keys
+  // beyond the window's rows are excluded.
+  if constexpr (!kWs8) {
+#pragma unroll
+    for (int il = 0; il < 2; ++il)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * jt + 4 * g + r;
+          float y = s[il][jt][r];
+          y = j >= p.n_real ? p.pad_key_l2e : y;
+          s[il][jt][r] = j >= p.N ? -INFINITY : y;
+        }
+  }
+  // Row softmax: max, exp2, sum.
+#pragma unroll
+  for (int il = 0; il < 2; ++il) {
+    float mx = s[il][0][0];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[il][jt][r]);
+    mx = xor_max(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = __builtin_amdgcn_exp2f(s[il][jt][r] - mx);
+        s[il][jt][r] = e;
+        sum += e;
+      }
+    }
+    inv[il] = __builtin_amdgcn_rcpf(xor_sum(sum));
+  }
+}
+
+// S^T tiles of two query tiles from K fragments (4 key tiles) and the Q
+// fragments of those two query tiles (bf16: one 16-byte fragment per
+// 32-channel step; fp32: D/16 fragments, lane group g holding channels
+// [g*D/4, (g+1)*D/4) in both operands).
+template <bool kBf16, int D>
+__device__ __forceinline__ void scores_pair(f32x4 (&s)[2][4], const uint4 (&kf)[4][kBf16 ? D / 32 : D / 16],
+                                            const uint4 (&qp)[2][kBf16 ? D / 32 : D / 16]) {
+  constexpr int kKF = kBf16 ? D / 32 : D / 16;
+#pragma unroll
+  for (int il = 0; il < 2; ++il) {
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (kBf16) {
+#pragma unroll
+        for (int ks = 0; ks < kKF; ++ks)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt][ks]),
+                                                        __builtin_bit_cast(bf16x8, qp[il][ks]), acc, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < kKF; ++ks) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = __uint_as_float(reinterpret_cast<const uint32_t*>(&kf[jt][ks])[e]);
+            const float b = __uint_as_float(reinterpret_cast<const uint32_t*>(&qp[il][ks])[e]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+          }
+        }
+      }
+      s[il][jt] = acc;
+    }
+  }
+}
+
+// O^T tiles (ct, il) = V^T P^T for one half.  vread(j, c) returns V[j][c]
+// (channel c of the head) from LDS.
+template <bool kBf16, int D, class VRead>
+__device__ __forceinline__ void pv_half(f32x4 (&o)[D / 16][2], const f32x4 (&s)[2][4], int lane, VRead vread) {
+  const int g = lane >> 4, c16 = lane & 15;
+  constexpr int kCT = D / 16;
+#pragma unroll
+  for (int ct = 0; ct < kCT; ++ct)
+#pragma unroll
+    for (int il = 0; il < 2; ++il) o[ct][il] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (kBf16) {
+#pragma unroll
+    for (int js = 0; js < 2; ++js) {
+      // k-slot e of lane group g is key 32*js + 16*(e/4) + 4g + e%4 in both
+      // the P^T fragment (from the accumulators) and the V^T fragment.
+      bf16x8 pf[2];
+#pragma unroll
+      for (int il = 0; il < 2; ++il) {
+        uint32_t wds[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+          wds[e / 2] = pack_bf16x2(s[il][2 * js + (e >> 2)][e & 3], s[il][2 * js + (e >> 2)][(e & 3) + 1]);
+        pf[il] = __builtin_bit_cast(bf16x8, wds);
+      }
+#pragma unroll
+      for (int ct = 0; ct < kCT; ++ct) {
+        uint16_t bits[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bits[e] = vread(32 * js + 16 * (e >> 2) + 4 * g + (e & 3), 16 * ct + c16);
+        const bf16x8 vfrag = __builtin_bit_cast(bf16x8, bits);
+#pragma unroll
+        for (int il = 0; il < 2; ++il)
+          o[ct][il] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag, pf[il], o[ct][il], 0, 0, 0);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * jt + 4 * g + r;
+#pragma unroll
+        for (int ct = 0; ct < kCT; ++ct) {
+          const float a = vread(j, 16 * ct + c16);
+#pragma unroll
+          for (int il = 0; il < 2; ++il)
+            o[ct][il] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s[il][jt][r], o[ct][il], 0, 0, 0);
+        }
+      }
+    }
+  }
+}
+
+// ============================================================================
+// window-tile kernel: bf16, 8x8 windows, one workgroup per (window, head group)
+// ============================================================================
+
+constexpr int kTileMaxRowBytes = 384;  // G*D*2 <= 384 (<= 192 bf16 channels)
+
+// 16-byte chunk slot of (row, chunk) in a [64][cpr] tile: the chunk index is
+// XOR-swizzled within its aligned group of 8 so that the 16 rows read by one
+// fragment load (and the 4 row groups of a V^T read) hit distinct banks.
+__device__ __forceinline__ int tile_slot(int row, int chunk, int cpr) {
+  return row * cpr + (chunk ^ ((row >> 1) & 7));
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int nthreads = G * 128;              // two waves per head
+  constexpr int cpr = G * D / 8;                 // chunks per row (multiple of 8)
+  constexpr int tile_bytes = kNPad * cpr * 16;
+  static_assert(cpr % 8 == 0 && G * D * 2 <= kTileMaxRowBytes, "head group must be whole 128-byte lines");
+  uint8_t* qs = smem;                            // Q, later O
+  uint8_t* ks = smem + tile_bytes;
+  uint8_t* vs = smem + 2 * tile_bytes;
+  float* tables = reinterpret_cast<float*>(smem + 3 * tile_bytes);
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int head = wave >> 1;                    // head of the group
+  const int half = wave & 1;                     // query tiles 2*half, 2*half + 1
+  const int lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int units = (p.items / p.heads) * p.groups;  // (window, head group) pairs
+
+  // A workgroup streams whole rows: each thread keeps one 16-byte chunk column
+  // of the group's row slice and steps down rows row0 + kRowStep*u.
+  constexpr int kPer = kNPad * cpr / nthreads;   // chunks per thread per tensor (D/16)
+  constexpr int kRowStep = nthreads / cpr;
+  static_assert(kRowStep * cpr == nthreads && kRowStep * kPer == kNPad, "row tiling");
+  const int row0 = tid / cpr, chunk0 = tid % cpr;
+
+  // q, k, v of one unit -> registers (nontemporal: every byte is read once).
+  uint4 buf[3][kPer];
+  auto fetch = [&](int unit) {
+    const int w = unit / p.groups, hg = unit - w * p.groups;
+    const int64_t row_base = (int64_t)w * kNPad + row0;
+    const int col = hg * G * D + chunk0 * 8;
+    const uint16_t* src[3] = {reinterpret_cast<const uint16_t*>(p.q) + row_base * p.q_stride + col,
+                              reinterpret_cast<const uint16_t*>(p.k) + row_base * p.k_stride + col,
+                              reinterpret_cast<const uint16_t*>(p.v) + row_base * p.v_stride + col};
+    const int64_t step[3] = {kRowStep * p.q_stride, kRowStep * p.k_stride, kRowStep * p.v_stride};
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+#pragma unroll
+      for (int u = 0; u < kPer; ++u)
+        buf[t][u] = __builtin_bit_cast(
+            uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[t] + u * step[t])));
+  };
+
+  int unit = blockIdx.x;
+  if (unit >= units) return;  // uniform across the workgroup
+  fetch(unit);
+  int table_group = -1;
+  float* tab = tables + head * kTableMax;
+
+  // Persistent loop, software-pipelined: while unit n is computed from LDS,
+  // the loads of unit n + gridDim.x are in flight into `buf`.
+  for (;;) {
+    const int w = unit / p.groups, hg = unit - w * p.groups;
+    __syncthreads();  // the previous unit's O has been read out of LDS
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int off = tile_slot(row0 + kRowStep * u, chunk0, cpr) * 16;
+      *reinterpret_cast<uint4*>(qs + off) = buf[0][u];
+      *reinterpret_cast<uint4*>(ks + off) = buf[1][u];
+      *reinterpret_cast<uint4*>(vs + off) = buf[2][u];
+    }
+    if (hg != table_group) {  // bias column of this head (x log2e); the two waves split it
+      table_group = hg;
+      const int h = hg * G + head;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int e = lane + 64 * (2 * u + half);
+        if (e < kTableMax)
+          tab[e] = (p.bias_table != nullptr && e < p.table_size) ? p.bias_table[(int64_t)e * p.heads + h] * kLog2e
+                                                                : 0.f;
+      }
+    }
+    __syncthreads();
+    const int next = unit + (int)gridDim.x;
+    if (next < units) fetch(next);
+
+    // ---- this wave: one head, query tiles 2*half, 2*half + 1 ---------------
+    const WindowMaskState m = window_mask_state(p, w, true);
+    LaneGeom<true> lg;
+    lane_geom_init<true>(lg, p, m, tab, lane);
+    constexpr int kKF = D / 32;
+    uint4 kf[4][kKF], qp[2][kKF];
+    const int hc = head * (D / 8);               // first chunk of this head
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int s = 0; s < kKF; ++s)
+        kf[t][s] = *reinterpret_cast<const uint4*>(ks + tile_slot(16 * t + c16, hc + 4 * s + g, cpr) * 16);
+#pragma unroll
+    for (int il = 0; il < 2; ++il)
+#pragma unroll
+      for (int s = 0; s < kKF; ++s)
+        qp[il][s] = *reinterpret_cast<const uint4*>(
+            qs + tile_slot(16 * (2 * half + il) + c16, hc + 4 * s + g, cpr) * 16);
+    auto vread = [&](int j, int c) -> uint16_t {
+      const int cc = head * D + c;
+      return *reinterpret_cast<const uint16_t*>(vs + tile_slot(j, cc >> 3, cpr) * 16 + (cc & 7) * 2);
+    };
+    // This wave's Q rows are in registers; its O overwrites exactly those
+    // rows of its head's columns.  Order the reads before the writes.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    {
+      f32x4 s[2][4];
+      scores_pair<true, D>(s, kf, qp);
+      float inv[2];
+      softmax_half<true, false>(s, inv, half, p, m, lg, nullptr, lane);
+      f32x4 o[D / 16][2];
+      pv_half<true, D>(o, s, lane, vread);
+#pragma unroll
+      for (int il = 0; il < 2; ++il) {
+        const int i = 16 * (2 * half + il) + c16;
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) {
+          const f32x4 v = o[ct][il] * inv[il];
+          const int cc = head * D + 16 * ct + 4 * g;  // 4 channels, 8 bytes
+          uint2 pk;
+          pk.x = pack_bf16x2(v[0], v[1]);
+          pk.y = pack_bf16x2(v[2], v[3]);
+          *reinterpret_cast<uint2*>(qs + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- stream O out (whole lines) ------------------------------------------
+    {
+      const int64_t row_base = (int64_t)w * kNPad + row0;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(p.o) + row_base * p.o_stride + hg * G * D + chunk0 * 8;
+      const int64_t ostep = kRowStep * p.o_stride;
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int off = tile_slot(row0 + kRowStep * u, chunk0, cpr) * 16;
+        const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(qs + off));
+        __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst + u * ostep));
+      }
+    }
+    if (next >= units) break;
+    unit = next;
+  }
+}
+
+// ============================================================================
+// per-wave kernel (generic path)
+// ============================================================================
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+template <bool kBf16> struct EltTraits;
+template <> struct EltTraits<true> { using T = uint16_t; };
+template <> struct EltTraits<false> { using T = float; };
+
+template <bool kBf16, int D>
+struct alignas(16) WaveLds {
   using T = typename EltTraits<kBf16>::T;
-  using L = LdsLayout<kBf16, D>;
+  // Row pitch of the per-wave V tile: 16 extra bytes put the 4 row groups
+  // read by one instruction into disjoint LDS bank ranges.
+  static constexpr int kPitch = D + 16 / (int)sizeof(T);
+  T v[kWaves][kNPad * kPitch];
+  float table[kWaves][kTableMax];
+};
+
+template <bool kBf16, int D, bool kExplicit>
+__global__ __launch_bounds__(kThreads) void window_attn_wave_kernel(const AttnParams p) {
+  using T = typename EltTraits<kBf16>::T;
+  using L = WaveLds<kBf16, D>;
   __shared__ L lds;
   constexpr int kPitch = L::kPitch;
-  static_assert(!kWs8 || kBf16, "the 8x8 specialisation is the bf16 path");
 
   // The wave index is uniform across the wave; saying so keeps the item,
   // window, head and base pointers in scalar registers.
@@ -131,13 +581,12 @@ __global__ __launch_bounds__(kThreads) void window_attn_kernel(const AttnParams 
   const int item = live ? item_raw : p.items - 1;
   const int w = item / p.heads;
   const int h = item - w * p.heads;
-  const int N = kWs8 ? 64 : p.N;
+  const int N = p.N;
 
   const T* qw = reinterpret_cast<const T*>(p.q) + (int64_t)w * N * p.q_stride + (int64_t)h * D;
   const T* kw = reinterpret_cast<const T*>(p.k) + (int64_t)w * N * p.k_stride + (int64_t)h * D;
   const T* vw = reinterpret_cast<const T*>(p.v) + (int64_t)w * N * p.v_stride + (int64_t)h * D;
 
-  // ---- global loads --------------------------------------------------------
   // Bias-table column of head h (L2-resident; 4 loads per lane cover 256 >= 225).
   float tabv[4];
 #pragma unroll
@@ -145,33 +594,29 @@ __global__ __launch_bounds__(kThreads) void window_attn_kernel(const AttnParams 
     const int e = lane + 64 * u;
     tabv[u] = (p.bias_table != nullptr && e < p.table_size) ? p.bias_table[(int64_t)e * p.heads + h] : 0.f;
   }
-  // K and Q fragments.  bf16: one 16-byte load per 32-channel step.  fp32:
-  // lane holds channels [g*D/4, (g+1)*D/4), the k order being permuted the
-  // same way in both operands (the dot products are unchanged).
+  // K and Q fragments straight from global memory.
   constexpr int kKF = kBf16 ? D / 32 : D / 16;
   uint4 kf[4][kKF];
   uint4 qf[4][kKF];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int row = 16 * t + c16;
-    const bool ok = kWs8 || row < N;
 #pragma unroll
     for (int s = 0; s < kKF; ++s) {
       const int col = kBf16 ? 32 * s + 8 * g : g * (D / 4) + 4 * s;
-      kf[t][s] = ok ? *reinterpret_cast<const uint4*>(kw + (int64_t)row * p.k_stride + col) : make_uint4(0, 0, 0, 0);
+      kf[t][s] = row < N ? *reinterpret_cast<const uint4*>(kw + (int64_t)row * p.k_stride + col) : make_uint4(0, 0, 0, 0);
     }
   }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int row = 16 * t + c16;
-    const bool ok = kWs8 || row < N;
 #pragma unroll
     for (int s = 0; s < kKF; ++s) {
       const int col = kBf16 ? 32 * s + 8 * g : g * (D / 4) + 4 * s;
-      qf[t][s] = ok ? *reinterpret_cast<const uint4*>(qw + (int64_t)row * p.q_stride + col) : make_uint4(0, 0, 0, 0);
+      qf[t][s] = row < N ? *reinterpret_cast<const uint4*>(qw + (int64_t)row * p.q_stride + col) : make_uint4(0, 0, 0, 0);
     }
   }
-  // V tile as 16-byte chunks.
+  // V tile as 16-byte chunks (rows beyond N are zero).
   constexpr int kChunksPerRow = D * (int)sizeof(T) / 16;
   constexpr int kVLoads = kNPad * kChunksPerRow / 64;
   uint4 vr[kVLoads];
@@ -180,65 +625,12 @@ __global__ __launch_bounds__(kThreads) void window_attn_kernel(const AttnParams 
     const int chunk = lane + 64 * u;
     const int row = chunk / kChunksPerRow;
     const int col = (chunk % kChunksPerRow) * (16 / (int)sizeof(T));
-    vr[u] = (kWs8 || row < N) ? *reinterpret_cast<const uint4*>(vw + (int64_t)row * p.v_stride + col)
-                              : make_uint4(0, 0, 0, 0);
+    vr[u] = row < N ? *reinterpret_cast<const uint4*>(vw + (int64_t)row * p.v_stride + col) : make_uint4(0, 0, 0, 0);
   }
 
-  // ---- per-window mask state (wave-uniform) ---------------------------------
-  bool use_shift = false;
-  int wr = 0, wc = 0;
-  if (!kExplicit && p.mask_mode == TERRA_MASK_SHIFT) {
-    const int per_img = p.win_rows * p.win_cols;
-    const int wl = w % per_img;
-    const int rr = wl / p.win_cols;
-    wr = rr + p.win_row_begin;
-    wc = wl - rr * p.win_cols;
-    use_shift = (wr + 2) * p.window_h > p.frame_h || (wc + 2) * p.window_w > p.frame_w;
-  }
-  const uint64_t land = p.land_bits != nullptr ? p.land_bits[w % p.mask_windows] : 0ull;
-  const bool use_mask = use_shift || land != 0ull;
+  const WindowMaskState m = window_mask_state(p, w, !kExplicit);
 
-  // ---- per-lane token geometry ----------------------------------------------
-  // Generic path: lane t computes token t's bias-index terms and region id;
-  // other lanes fetch them with shuffles.  idx(i, j) = base(i) - off(j).
-  int g_base = 0, g_off = 0, g_rid = 0;
-  if constexpr (!kWs8) {
-    const int t = lane < p.n_geo ? lane : p.n_geo - 1;
-    const int ti = t / p.window_w;
-    const int tj = t - ti * p.window_w;
-    const int rel_w = 2 * p.window_w - 1;
-    g_base = (ti + p.window_h - 1) * rel_w + tj + p.window_w - 1;
-    g_off = ti * rel_w + tj;
-    if (use_shift)
-      g_rid = 3 * region(wr * p.window_h + ti, p.frame_h, p.window_h, p.shift_h) +
-              region(wc * p.window_w + tj, p.frame_w, p.window_w, p.shift_w);
-  }
-  // Key-side terms, lane (c, g) holding keys j = 16*jt + 4g + r:
-  //   rid_pack  4-bit region id of key (jt, r) at bit 4*(4*jt + r)
-  //   land_lane land bit of key (jt, r) at bit 16*jt + r
-  int off_j[kWs8 ? 1 : 4][4];  // generic path: bias offset of key (jt, r)
-  uint64_t rid_pack = 0;
-  const uint64_t land_lane = land >> (4 * g);
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int j = 16 * jt + 4 * g + r;
-      int rid;
-      if constexpr (kWs8) {
-        rid = use_shift ? 3 * region(wr * 8 + 2 * jt + (g >> 1), p.frame_h, 8, p.shift_h) +
-                              region(wc * 8 + 4 * (g & 1) + r, p.frame_w, 8, p.shift_w)
-                        : 0;
-      } else {
-        const int jg = j < p.n_geo ? j : p.n_geo - 1;
-        off_j[jt][r] = __shfl(g_off, jg);
-        rid = __shfl(g_rid, jg);
-      }
-      rid_pack |= (uint64_t)rid << (4 * (4 * jt + r));
-    }
-  }
-
-  // ---- stage bias column (x log2e) and V in this wave's LDS -----------------
+  // Stage the bias column (x log2e) and V in this wave's LDS.
   float* tab = lds.table[wave];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -253,219 +645,35 @@ __global__ __launch_bounds__(kThreads) void window_attn_kernel(const AttnParams 
     const int col = (chunk % kChunksPerRow) * (16 / (int)sizeof(T));
     *reinterpret_cast<uint4*>(vt + row * kPitch + col) = vr[u];
   }
-  wave_lds_sync();
+  // Order this wave's LDS writes before its later LDS reads.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  constexpr int kCT = D / 16;
-
-  // ws = 8: lane part of the relative-position index (see header comment).
-  const int lane_base8 = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;
-  const float* tab8 = tab + (lane_base8 - 93);  // offsets 30*(it-jt) - r + 93 lie in [0, 183]
-
-  T* ow = reinterpret_cast<T*>(p.o) + (int64_t)w * N * p.o_stride + (int64_t)h * D;
+  LaneGeom<false> lg;
+  lane_geom_init<false>(lg, p, m, tab, lane);
   const float* emask = nullptr;
   if constexpr (kExplicit) emask = p.explicit_mask + (int64_t)(w % p.mask_windows) * p.n_geo * p.n_geo;
+  auto vread = [&](int j, int c) -> T { return vt[j * kPitch + c]; };
 
+  T* ow = reinterpret_cast<T*>(p.o) + (int64_t)w * N * p.o_stride + (int64_t)h * D;
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
-    // ---- S^T tiles of queries it = 2*half, 2*half + 1 -----------------------
     f32x4 s[2][4];
-#pragma unroll
-    for (int il = 0; il < 2; ++il) {
-      const int it = 2 * half + il;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (kBf16) {
-#pragma unroll
-          for (int ks = 0; ks < kKF; ++ks)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt][ks]),
-                                                          __builtin_bit_cast(bf16x8, qf[it][ks]), acc, 0, 0, 0);
-        } else {
-#pragma unroll
-          for (int ks = 0; ks < kKF; ++ks) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float a = __uint_as_float(reinterpret_cast<const uint32_t*>(&kf[jt][ks])[e]);
-              const float b = __uint_as_float(reinterpret_cast<const uint32_t*>(&qf[it][ks])[e]);
-              acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
-            }
-          }
-        }
-        s[il][jt] = acc;
-      }
-    }
-
-    // ---- logits (log2 domain) ----------------------------------------------
-    // Pass 1, branch-free: y = s * scale * log2e + bias * log2e.
-    int base_i[2] = {0, 0}, rid_i[2] = {0, 0};
-    bool i_geo[2] = {true, true};
-#pragma unroll
-    for (int il = 0; il < 2; ++il) {
-      const int it = 2 * half + il;
-      const int i = 16 * it + c16;
-      if constexpr (kWs8) {
-        if (use_shift)
-          rid_i[il] = 3 * region(wr * 8 + 2 * it + (c16 >> 3), p.frame_h, 8, p.shift_h) +
-                      region(wc * 8 + (c16 & 7), p.frame_w, 8, p.shift_w);
-      } else {
-        const int ig = i < p.n_geo ? i : p.n_geo - 1;
-        i_geo[il] = i < p.n_geo;
-        base_i[il] = __shfl(g_base, ig);
-        rid_i[il] = __shfl(g_rid, ig);
-      }
-    }
-#pragma unroll
-    for (int il = 0; il < 2; ++il) {
-      const int it = 2 * half + il;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float b;
-          if constexpr (kWs8) {
-            b = tab8[30 * (it - jt) - r + 93];
-          } else {
-            const int j = 16 * jt + 4 * g + r;
-            b = tab[base_i[il] - off_j[jt][r]];  // clamped indices: always in range
-            b = (i_geo[il] && j < p.n_geo) ? b : 0.f;
-          }
-          s[il][jt][r] = __builtin_fmaf(s[il][jt][r], p.scale_l2e, b);
-        }
-      }
-    }
-    // Pass 2 (windows with a shift boundary or land keys only): + mask.
-    if constexpr (kExplicit) {
-#pragma unroll
-      for (int il = 0; il < 2; ++il) {
-        const int i = 16 * (2 * half + il) + c16;
-        const int ig = i < p.n_geo ? i : p.n_geo - 1;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int j = 16 * jt + 4 * g + r;
-            const int jg = j < p.n_geo ? j : p.n_geo - 1;
-            const float m = emask[ig * p.n_geo + jg] * kLog2e;
-            const bool land_j = (land_lane >> (16 * jt + r)) & 1ull;
-            const bool jin = kWs8 || j < p.n_geo;
-            s[il][jt][r] += ((i_geo[il] && jin) ? m : 0.f) + ((land_j && jin) ? p.mask_l2e : 0.f);
-          }
-        }
-      }
-    } else if (use_mask) {
-#pragma unroll
-      for (int il = 0; il < 2; ++il) {
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int j = 16 * jt + 4 * g + r;
-            const int rid_j = (int)((rid_pack >> (4 * (4 * jt + r))) & 15ull);
-            const bool land_j = ((land_lane >> (16 * jt + r)) & 1ull) && (kWs8 || j < p.n_geo);
-            const float ms = (i_geo[il] && rid_i[il] != rid_j) ? p.mask_l2e : 0.f;
-            s[il][jt][r] += ms + (land_j ? p.mask_l2e : 0.f);
-          }
-        }
-      }
-    }
-    // Padded keys (generic path): keys >= n_real take the pad value, keys
-    // beyond the window's rows are excluded.
-    if constexpr (!kWs8) {
-#pragma unroll
-      for (int il = 0; il < 2; ++il)
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int j = 16 * jt + 4 * g + r;
-            float y = s[il][jt][r];
-            y = j >= p.n_real ? p.pad_key_l2e : y;
-            s[il][jt][r] = j >= N ? -INFINITY : y;
-          }
-    }
-
-    // ---- row softmax: max, exp2, sum ------------------------------------------
+    const uint4 (&qp)[2][kKF] = *reinterpret_cast<const uint4(*)[2][kKF]>(&qf[2 * half]);
+    scores_pair<kBf16, D>(s, kf, qp);
     float inv[2];
-#pragma unroll
-    for (int il = 0; il < 2; ++il) {
-      float mx = s[il][0][0];
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[il][jt][r]);
-      mx = xor_max(mx);
-      float sum = 0.f;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float e = __builtin_amdgcn_exp2f(s[il][jt][r] - mx);
-          s[il][jt][r] = e;
-          sum += e;
-        }
-      }
-      inv[il] = __builtin_amdgcn_rcpf(xor_sum(sum));
-    }
-
-    // ---- O^T = V^T P^T for this half ----------------------------------------
-    f32x4 o[kCT][2];
-#pragma unroll
-    for (int ct = 0; ct < kCT; ++ct)
-#pragma unroll
-      for (int il = 0; il < 2; ++il) o[ct][il] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (kBf16) {
-#pragma unroll
-      for (int js = 0; js < 2; ++js) {
-        bf16x8 pf[2];
-#pragma unroll
-        for (int il = 0; il < 2; ++il) {
-          uint32_t wds[4];
-#pragma unroll
-          for (int e = 0; e < 8; e += 2)
-            wds[e / 2] = pack_bf16x2(s[il][2 * js + (e >> 2)][e & 3], s[il][2 * js + (e >> 2)][(e & 3) + 1]);
-          pf[il] = __builtin_bit_cast(bf16x8, wds);
-        }
-#pragma unroll
-        for (int ct = 0; ct < kCT; ++ct) {
-          // V^T operand fragment from LDS: k-slot e of lane group g is key
-          // 32*js + 16*(e/4) + 4g + e%4, the order of the P^T fragment.
-          uint16_t bits[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int j = 32 * js + 16 * (e >> 2) + 4 * g + (e & 3);
-            bits[e] = vt[j * kPitch + 16 * ct + c16];
-          }
-          const bf16x8 vfrag = __builtin_bit_cast(bf16x8, bits);
-#pragma unroll
-          for (int il = 0; il < 2; ++il)
-            o[ct][il] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag, pf[il], o[ct][il], 0, 0, 0);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * jt + 4 * g + r;
-#pragma unroll
-          for (int ct = 0; ct < kCT; ++ct) {
-            const float a = vt[j * kPitch + 16 * ct + c16];
-#pragma unroll
-            for (int il = 0; il < 2; ++il)
-              o[ct][il] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s[il][jt][r], o[ct][il], 0, 0, 0);
-          }
-        }
-      }
-    }
-
-    // ---- store: lane holds O[i = 16*it + c16][16*ct + 4g .. +4] -------------
+    softmax_half<false, kExplicit>(s, inv, half, p, m, lg, emask, lane);
+    f32x4 o[D / 16][2];
+    pv_half<kBf16, D>(o, s, lane, vread);
+    // Store: lane holds O[i = 16*it + c16][16*ct + 4g .. +4].
     if (live) {
 #pragma unroll
       for (int il = 0; il < 2; ++il) {
         const int i = 16 * (2 * half + il) + c16;
-        if (kWs8 || i < N) {
+        if (i < N) {
 #pragma unroll
-          for (int ct = 0; ct < kCT; ++ct) {
+          for (int ct = 0; ct < D / 16; ++ct) {
             T* dst = ow + (int64_t)i * p.o_stride + 16 * ct + 4 * g;
             const f32x4 v = o[ct][il] * inv[il];
             if constexpr (kBf16) {
@@ -483,20 +691,71 @@ __global__ __launch_bounds__(kThreads) void window_attn_kernel(const AttnParams 
   }
 }
 
-template <bool kBf16, int D, bool kWs8, bool kExplicit>
-void launch(const AttnParams& p, hipStream_t s) {
+template <bool kBf16, int D, bool kExplicit>
+void launch_wave(const AttnParams& p, hipStream_t s) {
   const int blocks = (p.items + kWaves - 1) / kWaves;
-  window_attn_kernel<kBf16, D, kWs8, kExplicit><<<blocks, kThreads, 0, s>>>(p);
+  window_attn_wave_kernel<kBf16, D, kExplicit><<<blocks, kThreads, 0, s>>>(p);
 }
 
-template <bool kBf16, int D>
-void dispatch(const AttnParams& p, bool ws8, bool expl, hipStream_t s) {
-  if constexpr (kBf16) {
-    if (ws8 && !expl) return launch<true, D, true, false>(p, s);
-    if (ws8 && expl) return launch<true, D, true, true>(p, s);
+// Resident workgroups of the persistent tile kernel: as many as the device's
+// CUs hold at once (LDS and VGPR limited), queried per device once.
+template <int D, int G>
+int tile_grid(int lds) {
+  constexpr int kMaxDevices = 64;
+  static int cache[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, window_attn_tile_kernel<D, G>, G * 128, lds) !=
+        hipSuccess)
+      return 0;
+    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
   }
-  if (expl) launch<kBf16, D, false, true>(p, s);
-  else launch<kBf16, D, false, false>(p, s);
+  return cache[dev];
+}
+
+template <int D, int G>
+int launch_tile(const AttnParams& p, hipStream_t s) {
+  constexpr int lds = 3 * kNPad * G * D * 2 + G * kTableMax * (int)sizeof(float);
+  // The >64 KiB dynamic-LDS opt-in is a per-kernel attribute: set it once.
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&window_attn_tile_kernel<D, G>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  const int resident = tile_grid<D, G>(lds);
+  if (resident <= 0) return fail(TERRA_ERR_LAUNCH, "cannot size the tile kernel grid for this device");
+  const int units = (p.items / p.heads) * p.groups;
+  const int blocks = units < resident ? units : resident;
+  window_attn_tile_kernel<D, G><<<blocks, G * 128, lds, s>>>(p);
+  return TERRA_OK;
+}
+
+// Heads per workgroup of the tile kernel: the largest divisor G of `heads`
+// among the instantiated group widths (row slices of 128, 256 or 384 bytes,
+// i.e. whole 128-byte lines, at most 192 channels); 0 if there is none.
+int tile_group(int heads, int D) {
+  static const int kG32[] = {6, 4, 2};  // head dim 32
+  static const int kG64[] = {3, 2, 1};  // head dim 64
+  const int* cand = D == 32 ? kG32 : kG64;
+  for (int i = 0; i < 3; ++i)
+    if (heads % cand[i] == 0) return cand[i];
+  return 0;
+}
+
+int dispatch_tile(const AttnParams& p, int D, hipStream_t s) {
+  if (D == 32) {
+    switch (p.group) {
+      case 6: return launch_tile<32, 6>(p, s);
+      case 4: return launch_tile<32, 4>(p, s);
+      default: return launch_tile<32, 2>(p, s);
+    }
+  }
+  switch (p.group) {
+    case 3: return launch_tile<64, 3>(p, s);
+    case 2: return launch_tile<64, 2>(p, s);
+    default: return launch_tile<64, 1>(p, s);
+  }
 }
 
 }  // namespace
@@ -586,17 +845,26 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
   p.frame_h = d.frame_h; p.frame_w = d.frame_w; p.shift_h = d.shift_h; p.shift_w = d.shift_w;
   p.win_row_begin = d.win_row_begin; p.win_rows = d.win_rows; p.win_cols = d.win_cols;
 
-  // 8x8 windows without padded tokens take the closed-form bias path.
-  const bool ws8 = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
-                   d.n_real == 64;
-  const bool expl = d.mask_mode == TERRA_MASK_EXPLICIT;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == TERRA_DTYPE_BF16) {
-    if (D == 32) dispatch<true, 32>(p, ws8, expl, s);
-    else dispatch<true, 64>(p, ws8, expl, s);
+  // bf16 8x8 windows without padded tokens or a dense mask: window-tile kernel.
+  const int G = tile_group(d.heads, D);
+  const bool tile = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
+                    d.n_real == 64 && d.mask_mode != TERRA_MASK_EXPLICIT && G > 0;
+  if (tile) {
+    p.group = G;
+    p.groups = d.heads / G;
+    const int st = dispatch_tile(p, D, s);
+    if (st != TERRA_OK) return st;
   } else {
-    if (D == 32) dispatch<false, 32>(p, false, expl, s);
-    else dispatch<false, 64>(p, false, expl, s);
+    p.group = p.groups = 0;
+    const bool expl = d.mask_mode == TERRA_MASK_EXPLICIT;
+    if (dtype == TERRA_DTYPE_BF16) {
+      if (D == 32) expl ? launch_wave<true, 32, true>(p, s) : launch_wave<true, 32, false>(p, s);
+      else expl ? launch_wave<true, 64, true>(p, s) : launch_wave<true, 64, false>(p, s);
+    } else {
+      if (D == 32) expl ? launch_wave<false, 32, true>(p, s) : launch_wave<false, 32, false>(p, s);
+      else expl ? launch_wave<false, 64, true>(p, s) : launch_wave<false, 64, false>(p, s);
+    }
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "terra_swin_attn_fwd launch failed: %s", hipGetErrorString(e));

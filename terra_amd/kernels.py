@@ -177,6 +177,44 @@ def swin_partition(x: torch.Tensor, geom: WindowGeometry, pad_value: float = 0.0
     return out
 
 
+def swin_partition_ln(x: torch.Tensor, geom: WindowGeometry, weight: Optional[torch.Tensor],
+                      bias: Optional[torch.Tensor], eps: float, pad_value: float = 0.0,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused LayerNorm over C (nn.LayerNorm semantics, fp32 statistics) +
+    pad + roll(-shift) + window_partition of ``x`` [B, H, W, C].
+
+    Replaces ``norm1`` followed by the roll and partition of
+    models/transformer.py:150-182.  Returns windows ``[B * nW, ws*ws, C]``.
+    """
+    dev = _require_device(x)
+    code = _dtype_code(x, (torch.float32, torch.float16, torch.bfloat16))
+    if x.dim() != 4 or tuple(x.shape) != (geom.batch, geom.height, geom.width, geom.channels):
+        raise ValueError(f"x shape {tuple(x.shape)} does not match geometry "
+                         f"{(geom.batch, geom.height, geom.width, geom.channels)}")
+    if not x.is_contiguous():
+        raise ValueError("x must be contiguous [B, H, W, C]")
+    params = []
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t is None:
+            params.append(None)
+            continue
+        _require_device(x, t)
+        if t.dim() != 1 or t.shape[0] != geom.channels:
+            raise ValueError(f"LayerNorm {name} must be [{geom.channels}]")
+        params.append(t.detach().to(torch.float32).contiguous())
+    shape = (geom.num_windows, geom.window * geom.window, geom.channels)
+    if out is None:
+        out = torch.empty(shape, dtype=x.dtype, device=dev)
+    elif tuple(out.shape) != shape or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
+        raise ValueError(f"out must be a contiguous {x.dtype} tensor of shape {shape} on {dev}")
+    c_geom = geom.to_c()
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_partition_ln(_ptr(x), _ptr(out), code, ctypes.byref(c_geom), _ptr(params[0]),
+                                                 _ptr(params[1]), float(eps), float(pad_value), _stream(dev))
+    _lib.check(st, "terra_swin_partition_ln")
+    return out
+
+
 def swin_reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional[torch.Tensor] = None,
                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused window_reverse + roll(+shift) + crop (+ residual) to [B, H, W, C]."""

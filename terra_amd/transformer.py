@@ -2,7 +2,7 @@
 
 The attention half of a Swin block on one GPU:
 
-    x -> norm1 -> [roll(-s) + window partition]      one HIP gather
+    x -> [norm1 + roll(-s) + window partition]      one HIP gather
       -> q/k/v projection (one GEMM)                 hipBLASLt via torch
       -> fused window-attention core                 one HIP kernel
       -> proj                                        hipBLASLt via torch
@@ -96,16 +96,29 @@ class SequentialSwinTransformer(torch.nn.Module):
             return None
         return WindowMask(shift=shift, land_bits=land)
 
+    def _fusable_norm(self, dtype: torch.dtype) -> bool:
+        """norm1 is a plain LayerNorm over C that the gather kernel computes
+        for activations of `dtype` (rows of whole 16-byte chunks, <= 1536 B)."""
+        n = self.norm1
+        row_bytes = self.embedding_dim * torch.empty((), dtype=dtype).element_size()
+        return (type(n) is torch.nn.LayerNorm and tuple(n.normalized_shape) == (self.embedding_dim,)
+                and dtype in (torch.float32, torch.float16, torch.bfloat16)
+                and row_bytes % 16 == 0 and row_bytes <= 1536)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         H, W = self.input_resolution
         B, L, C = x.shape
         if L != H * W:
             raise AssertionError("input feature has wrong size")
         shortcut = x
-        if config.use_layernorm:
-            x = self.norm1(x)
         geom = self.geometry(B)
-        x_windows = kernels.swin_partition(x.contiguous().view(B, H, W, C), geom)
+        grid = x.contiguous().view(B, H, W, C)
+        if config.use_layernorm and self._fusable_norm(grid.dtype):
+            x_windows = kernels.swin_partition_ln(grid, geom, self.norm1.weight, self.norm1.bias, self.norm1.eps)
+        else:
+            if config.use_layernorm:  # a norm layer the gather cannot fuse runs on its own
+                grid = self.norm1(grid.view(B, L, C)).contiguous().view(B, H, W, C)
+            x_windows = kernels.swin_partition(grid, geom)
         attn_windows = self.attn(x_windows, mask=self.window_mask(geom))
         out_dtype = torch.promote_types(attn_windows.dtype, shortcut.dtype)
         y = kernels.swin_reverse(attn_windows.to(out_dtype), geom,

@@ -99,3 +99,52 @@ def test_full_size_partition_and_round_trip(dev, name):
         want_back = so.reverse_frame(want, cfg.batch, cfg.height, cfg.width, cfg.window, cfg.shift, cfg.shift,
                                      cfg.pad, cfg.win_row_begin, cfg.win_rows, cfg.valid)
         assert torch.equal(back.cpu(), want_back)
+
+
+LN_CASES = [  # (B, H, W, C, ws, shift, pad, win_row_begin, win_rows, valid)
+    (2, 14, 21, 96, 7, 3, (0, 0, 0, 0), 0, None, None),
+    (1, 16, 24, 192, 8, 4, (0, 0, 0, 0), 0, None, None),
+    (2, 20, 16, 384, 8, 4, (0, 4, 0, 0), 0, 2, (3, 4)),
+    (1, 16, 16, 768, 8, 4, (0, 8, 0, 0), 0, 2, (1, 3)),
+    (1, 6, 6, 64, 4, 2, (1, 1, 1, 1), 0, None, None),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", LN_CASES)
+@pytest.mark.parametrize("affine", [True, False])
+def test_partition_ln_matches_layer_norm_then_partition(dev, dtype, case, affine):
+    """Fused LayerNorm + partition == F.layer_norm (fp32) then the partition map.
+    Tolerance: one rounding of the output dtype (fp32: 2e-6 relative + 1e-6);
+    padding and pad windows are bit-exact."""
+    B, H, W, C, ws, s, pad, r0, rows, valid = case
+    if dtype == torch.float32 and C * 4 > 1536:
+        pytest.skip("row larger than the fused kernel's 1536-byte limit")
+    x = workloads.activations((B, H, W, C), 110, torch.float32) * 3 + 0.5
+    x = x.to(dtype)
+    w = (workloads.activations((C,), 111) * 0.1 + 1.0) if affine else None
+    b = (workloads.activations((C,), 112) * 0.1) if affine else None
+    g = _geom(*case)
+    got = kernels.swin_partition_ln(x.to(dev), g, None if w is None else w.to(dev), None if b is None else b.to(dev),
+                                    1e-5).cpu()
+    ln = torch.nn.functional.layer_norm(x.float(), (C,), w, b, 1e-5)
+    want = so.partition_frame(ln, ws, s, s, pad, r0, rows, valid)
+    pad_mask = so.partition_frame(torch.ones(B, H, W, 1), ws, s, s, pad, r0, rows, valid) == 0
+    pad_mask = pad_mask.expand_as(want)
+    assert torch.all(got[pad_mask] == 0)
+    err = (got.float() - want).abs()
+    if dtype == torch.float32:
+        tol = 2e-6 * want.abs() + 1e-6
+    else:
+        ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+        tol = ulp * want.abs() + 1e-4
+    assert torch.all(err <= tol), float((err - tol).max())
+
+
+def test_block_uses_fused_layer_norm(dev):
+    """The drop-in block routes LayerNorm through the fused gather."""
+    from terra_amd.transformer import SequentialSwinTransformer
+
+    blk = SequentialSwinTransformer(layer_idx=1, height=16, width=16, embedding_dim=64, window_size=8,
+                                    num_heads=2).to(dev).to(torch.bfloat16)
+    assert blk._fusable_norm(torch.bfloat16)
