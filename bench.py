@@ -14,6 +14,9 @@ custom kernel), timed with HIP events on the launch stream over the timed
 steps; partition / reverse are reported under `kernels`.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py --mode kernels --steps 3     # the step's HIP kernels only,
+                                                 # plus a 192 MiB device copy
+                                                 # (rocprofv3 counter calibration)
 """
 from __future__ import annotations
 
@@ -42,7 +45,53 @@ def parse():
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--mode", choices=("step", "kernels"), default="step",
+                    help="step: the timed benchmark; kernels: run the step's HIP kernels --steps times "
+                         "(for rocprofv3 counter passes) and a 192 MiB copy of known size")
     return ap.parse_args()
+
+
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "window_attention_c3_pmc.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the attention kernel from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known
+    size), or None when that summary is absent."""
+    try:
+        with open(PROFILE_TRAFFIC) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def run_kernels(cfg, blk, x, steps):
+    """The three HIP kernels of one c3 step on the step's own tensors, `steps`
+    times, then a device copy of 192 MiB (the counter calibration)."""
+    import torch
+
+    from terra_amd import kernels
+
+    B, L, C = x.shape
+    geom = blk.geometry(B)
+    grid = x.view(B, cfg.height, cfg.width, C)
+    with torch.no_grad():
+        win = kernels.swin_partition_ln(grid, geom, blk.norm1.weight, blk.norm1.bias, blk.norm1.eps)
+        qkv = blk.attn.qkv(win)
+        mask = blk.window_mask(geom)
+        for _ in range(steps):
+            win = kernels.swin_partition_ln(grid, geom, blk.norm1.weight, blk.norm1.bias, blk.norm1.eps)
+            o = blk.attn.core(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], mask=mask)
+            kernels.swin_reverse(o, geom, residual=grid)
+        src = torch.ones(192 << 20, dtype=torch.uint8, device=x.device)
+        dst = torch.zeros_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "kernels", "steps": steps, "calibration_copy_bytes": src.numel()}), flush=True)
 
 
 def cpu_model() -> str:
@@ -114,6 +163,9 @@ def main():
     land = workloads.land_mask(cfg.height, cfg.width, seed=42) if cfg.land else None
     blk = workloads.block_for(cfg, 1 if cfg.shift else 0, land=land).to(dev).to(dtype)
     x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 1003, dtype).to(dev)
+    if args.mode == "kernels":
+        run_kernels(cfg, blk, x, args.steps)
+        return
 
     # Per-kernel events on the launch stream (torch's current stream, which the
     # C ABI receives as its hipStream_t).
@@ -197,7 +249,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": attn_gbs / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(),
             "algorithmic_bytes_per_launch": core_bytes,
             "avg_launch_us": t_attn,
         },

@@ -176,3 +176,25 @@ def test_core_full_size_sampled_windows(dev, name):
     ref = so.window_attention_core(q[sample], k[sample], v[sample], heads, (C // heads) ** -0.5, table, (ws, ws),
                                    total[sample % per_img])
     _check(out.cpu()[sample], ref, torch.bfloat16)
+
+
+def test_kernels_against_committed_golden_fixture(dev):
+    """The committed tiny SW-MSA fixture (tests/golden/swin_tiny.npz): partition
+    bit-exact, fp32 attention within 1e-5 of the stored float64 target."""
+    import os
+
+    import numpy as np
+
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "swin_tiny.npz"))
+    B, H, W, C, nH, ws, s = (int(v) for v in z["meta"])
+    x = torch.from_numpy(z["x"]).to(dev)
+    g = WindowGeometry(B, H, W, C, ws, s, s)
+    win = kernels.swin_partition(x, g)
+    assert np.array_equal(win.cpu().numpy(), z["windows"])
+    bits = utils.land_window_bits(torch.from_numpy(z["land"]).to(dev), WindowGeometry(1, H, W, 1, ws, s, s))
+    qkv = torch.from_numpy(z["qkv"]).to(dev)
+    out = kernels.window_attention(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], nH, (ws, ws),
+                                   (C // nH) ** -0.5, bias_table=torch.from_numpy(z["table"]).to(dev),
+                                   mask=WindowMask(shift=ShiftMask.from_geometry(g), land_bits=bits))
+    err = np.abs(out.cpu().double().numpy() - z["o"].astype(np.float64)).max()
+    assert err <= 1e-5, err

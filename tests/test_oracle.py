@@ -192,3 +192,44 @@ def test_ragged_row_major_reference_vector():
     per_rank = so.ragged_row_major(2, 5, 4)
     ids = [[r * 5 + c for r, c in chunk] for chunk in per_rank]
     assert ids == [[0, 1], [2, 3, 4], [5, 6], [7, 8, 9]]
+
+
+# ---- committed golden fixtures (tests/golden, written by make_golden.py) ----
+
+import json as _json
+import os as _os
+
+_GOLDEN = _os.path.join(_os.path.dirname(_os.path.abspath(__file__)), "golden")
+
+
+def test_known_answers_fixture():
+    ka = _json.load(open(_os.path.join(_GOLDEN, "known_answers.json")))
+    ids = [[r * 5 + c for r, c in chunk] for chunk in so.ragged_row_major(2, 5, 4)]
+    assert ids == ka["ragged_row_major_2x5_m4"]
+    i7, i8 = so.relative_position_index((7, 7)), so.relative_position_index((8, 8))
+    assert ka["rel_index_7x7"] == {"i00": 84, "max": 168, "i_48_0": 168, "i_0_48": 0}
+    assert ka["rel_index_8x8"] == {"i00": 112, "max": 224, "i_63_0": 224, "i_0_63": 0}
+    assert int(i7[48, 0]) == 168 and int(i8[0, 0]) == 112
+    assert ka["shift_mask_ws7_s3_counts"] == {"last_row": 1176, "corner": 1776}
+    assert ka["shift_mask_ws8_s4_counts"] == {"last_row": 2048, "corner": 3072}
+
+
+def test_tiny_fixture_oracle_has_not_drifted():
+    z = np.load(_os.path.join(_GOLDEN, "swin_tiny.npz"))
+    B, H, W, C, nH, ws, s = (int(v) for v in z["meta"])
+    x = torch.from_numpy(z["x"]).double()
+    win = so.roll_partition(x, ws, s)
+    assert np.array_equal(win.float().numpy(), z["windows"])
+    land = torch.from_numpy(z["land"])
+    mask = so.fold_land(so.shift_mask(H, W, ws, s).double(), so.land_key_flags(land, ws, s, s))
+    assert np.array_equal(mask.float().numpy(), z["mask"])
+    qkv = torch.from_numpy(z["qkv"]).double()
+    o = so.window_attention_core(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], nH, (C // nH) ** -0.5,
+                                 torch.from_numpy(z["table"]).double(), (ws, ws), mask,
+                                 compute_dtype=torch.float64)
+    np.testing.assert_allclose(o.numpy(), z["o"], rtol=1e-6, atol=1e-7)
+    # and the float64 brute force agrees with the stored target
+    bias = so.relative_position_bias(torch.from_numpy(z["table"]).double(), (ws, ws)).numpy()
+    want = brute.attention(qkv[..., :C].numpy(), qkv[..., C:2 * C].numpy(), qkv[..., 2 * C:].numpy(), nH,
+                           (C // nH) ** -0.5, bias, mask.numpy())
+    np.testing.assert_allclose(want, z["o"], rtol=1e-6, atol=1e-7)
