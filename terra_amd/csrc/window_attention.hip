@@ -20,13 +20,14 @@
 // Two kernels share that core:
 //
 //   window_attn_tile_kernel   bf16, 8x8 windows, no padded tokens, analytic
-//       masks.  One workgroup per (window, group of G heads), one wave per
-//       head.  The group's q, k, v rows (G*D <= 192 channels, a contiguous
-//       384-byte slice of each token row) are streamed into LDS as whole
-//       cache lines with nontemporal loads; O is staged in LDS over Q and
-//       streamed out as whole lines.  The relative-position index of lane
-//       element (it, jt, r) is lane_base + 30*(it - jt) - r, so the bias comes
-//       from LDS with compile-time offsets.
+//       masks.  A persistent workgroup loops over (window, group of G heads)
+//       units, two waves per head (one per query half).  The group's q, k, v
+//       rows (a contiguous slice of G*D channels, whole 128-byte lines) are
+//       streamed into LDS with nontemporal loads while the previous unit is
+//       computed; O is staged in LDS over Q and streamed out as whole lines.
+//       The relative-position index of lane element (it, jt, r) is
+//       lane_base + 30*(it - jt) - r, so the bias comes from LDS with
+//       compile-time offsets.
 //
 //   window_attn_wave_kernel   everything else (fp32, any window up to 8x8,
 //       padded tokens and keys, explicit dense masks): one wavefront per
@@ -80,14 +81,26 @@ __device__ __forceinline__ int region(int coord, int extent, int ws, int shift) 
   return coord < extent - ws ? 0 : (coord < extent - shift ? 1 : 2);
 }
 
+// Reductions over the 4 lanes l, l^16, l^32, l^48 that share a query row.
+// v_permlane16_swap / v_permlane32_swap with both operands = v return the
+// value of the own 16-lane (32-lane) half and of the partner half, so one
+// VALU op per step replaces an LDS-crossbar shuffle.
 __device__ __forceinline__ float xor_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return fmaxf(v, __shfl_xor(v, 32));
+  const uint32_t b = __float_as_uint(v);
+  const auto p16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  v = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+  const uint32_t c = __float_as_uint(v);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
 }
 
 __device__ __forceinline__ float xor_sum(float v) {
-  v += __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
+  const uint32_t b = __float_as_uint(v);
+  const auto p16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+  const uint32_t c = __float_as_uint(v);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
@@ -243,7 +256,7 @@ __device__ __forceinline__ void softmax_half(f32x4 (&s)[2][4], float (&inv)[2], 
         }
       }
     }
-  } else if (m.use_mask) {
+  } else if (m.use_shift) {  // boundary windows: region test per element, plus land keys
 #pragma unroll
     for (int il = 0; il < 2; ++il) {
 #pragma unroll
@@ -256,6 +269,18 @@ __device__ __forceinline__ void softmax_half(f32x4 (&s)[2][4], float (&inv)[2], 
           const float ms = (i_geo[il] && rid_i[il] != rid_j) ? p.mask_l2e : 0.f;
           s[il][jt][r] += ms + (land_j ? p.mask_l2e : 0.f);
         }
+      }
+    }
+  } else if (m.land != 0ull) {  // land keys only: one additive term per key column
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * jt + 4 * g + r;
+        const bool land_j = ((lg.land_lane >> (16 * jt + r)) & 1ull) && (kWs8 || j < p.n_geo);
+        const float ml = land_j ? p.mask_l2e : 0.f;
+#pragma unroll
+        for (int il = 0; il < 2; ++il) s[il][jt][r] += ml;
       }
     }
   }
@@ -331,10 +356,12 @@ __device__ __forceinline__ void scores_pair(f32x4 (&s)[2][4], const uint4 (&kf)[
   }
 }
 
-// O^T tiles (ct, il) = V^T P^T for one half.  vread(j, c) returns V[j][c]
-// (channel c of the head) from LDS.
-template <bool kBf16, int D, class VRead>
-__device__ __forceinline__ void pv_half(f32x4 (&o)[D / 16][2], const f32x4 (&s)[2][4], int lane, VRead vread) {
+// O^T tiles (ct, il) = V^T P^T for one half.  bf16: vfrag(ct, js) returns the
+// V^T operand fragment whose k-slot e (lane group g) is key
+// 32*js + 16*(e/4) + 4g + e%4 and whose row is channel 16*ct + c; fp32:
+// vread(j, c) returns V[j][c].
+template <bool kBf16, int D, class VFrag>
+__device__ __forceinline__ void pv_half(f32x4 (&o)[D / 16][2], const f32x4 (&s)[2][4], int lane, VFrag vsrc) {
   const int g = lane >> 4, c16 = lane & 15;
   constexpr int kCT = D / 16;
 #pragma unroll
@@ -344,8 +371,7 @@ __device__ __forceinline__ void pv_half(f32x4 (&o)[D / 16][2], const f32x4 (&s)[
   if constexpr (kBf16) {
 #pragma unroll
     for (int js = 0; js < 2; ++js) {
-      // k-slot e of lane group g is key 32*js + 16*(e/4) + 4g + e%4 in both
-      // the P^T fragment (from the accumulators) and the V^T fragment.
+      // P^T fragment from the accumulators, same k-slot order as vfrag.
       bf16x8 pf[2];
 #pragma unroll
       for (int il = 0; il < 2; ++il) {
@@ -357,13 +383,10 @@ __device__ __forceinline__ void pv_half(f32x4 (&o)[D / 16][2], const f32x4 (&s)[
       }
 #pragma unroll
       for (int ct = 0; ct < kCT; ++ct) {
-        uint16_t bits[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bits[e] = vread(32 * js + 16 * (e >> 2) + 4 * g + (e & 3), 16 * ct + c16);
-        const bf16x8 vfrag = __builtin_bit_cast(bf16x8, bits);
+        const bf16x8 vf = vsrc(ct, js);
 #pragma unroll
         for (int il = 0; il < 2; ++il)
-          o[ct][il] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag, pf[il], o[ct][il], 0, 0, 0);
+          o[ct][il] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[il], o[ct][il], 0, 0, 0);
       }
     }
   } else {
@@ -374,7 +397,7 @@ __device__ __forceinline__ void pv_half(f32x4 (&o)[D / 16][2], const f32x4 (&s)[
         const int j = 16 * jt + 4 * g + r;
 #pragma unroll
         for (int ct = 0; ct < kCT; ++ct) {
-          const float a = vread(j, 16 * ct + c16);
+          const float a = vsrc(j, 16 * ct + c16);
 #pragma unroll
           for (int il = 0; il < 2; ++il)
             o[ct][il] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s[il][jt][r], o[ct][il], 0, 0, 0);
@@ -382,6 +405,19 @@ __device__ __forceinline__ void pv_half(f32x4 (&o)[D / 16][2], const f32x4 (&s)[
       }
     }
   }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16: within each 16-lane group, output lane l receives
+// element (l & 3) of the 8-byte words addressed by lanes (l >> 2) + 4m,
+// m = 0..3.  When lane s addresses V[row(s >> 2)][c0 + 4*(s & 3) ..], lane l
+// receives V[row(m)][c0 + l] for m = 0..3: four keys of one channel.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* addr) {
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4*)(__attribute__((address_space(3))) uint8_t*)(const_cast<uint8_t*>(addr)));
+  return __builtin_bit_cast(uint2, r);
 }
 
 // ============================================================================
@@ -493,9 +529,17 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
       for (int s = 0; s < kKF; ++s)
         qp[il][s] = *reinterpret_cast<const uint4*>(
             qs + tile_slot(16 * (2 * half + il) + c16, hc + 4 * s + g, cpr) * 16);
-    auto vread = [&](int j, int c) -> uint16_t {
-      const int cc = head * D + c;
-      return *reinterpret_cast<const uint16_t*>(vs + tile_slot(j, cc >> 3, cpr) * 16 + (cc & 7) * 2);
+    // V^T fragment (ct, js): two transposed reads, keys 32*js + 16*half2 + 4g + m.
+    auto vfrag = [&](int ct, int js) -> bf16x8 {
+      const int cc = head * D + 16 * ct + 4 * (c16 & 3);  // channel of this source lane
+      uint2 part[2];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int row = 32 * js + 16 * h2 + 4 * g + (c16 >> 2);
+        part[h2] = lds_read_tr16(vs + tile_slot(row, cc >> 3, cpr) * 16 + (cc & 7) * 2);
+      }
+      const uint32_t w[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
+      return __builtin_bit_cast(bf16x8, w);
     };
     // This wave's Q rows are in registers; its O overwrites exactly those
     // rows of its head's columns.  Order the reads before the writes.
@@ -507,7 +551,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
       float inv[2];
       softmax_half<true, false>(s, inv, half, p, m, lg, nullptr, lane);
       f32x4 o[D / 16][2];
-      pv_half<true, D>(o, s, lane, vread);
+      pv_half<true, D>(o, s, lane, vfrag);
 #pragma unroll
       for (int il = 0; il < 2; ++il) {
         const int i = 16 * (2 * half + il) + c16;
@@ -654,7 +698,18 @@ __global__ __launch_bounds__(kThreads) void window_attn_wave_kernel(const AttnPa
   lane_geom_init<false>(lg, p, m, tab, lane);
   const float* emask = nullptr;
   if constexpr (kExplicit) emask = p.explicit_mask + (int64_t)(w % p.mask_windows) * p.n_geo * p.n_geo;
-  auto vread = [&](int j, int c) -> T { return vt[j * kPitch + c]; };
+  // V^T source: bf16 fragments gathered element by element from the padded
+  // row-major tile; fp32 element reads.
+  auto vsrc = [&](int a, int b) {
+    if constexpr (kBf16) {
+      uint16_t bits[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bits[e] = vt[(32 * b + 16 * (e >> 2) + 4 * g + (e & 3)) * kPitch + 16 * a + c16];
+      return __builtin_bit_cast(bf16x8, bits);
+    } else {
+      return vt[a * kPitch + b];
+    }
+  };
 
   T* ow = reinterpret_cast<T*>(p.o) + (int64_t)w * N * p.o_stride + (int64_t)h * D;
 #pragma unroll
@@ -665,7 +720,7 @@ __global__ __launch_bounds__(kThreads) void window_attn_wave_kernel(const AttnPa
     float inv[2];
     softmax_half<false, kExplicit>(s, inv, half, p, m, lg, emask, lane);
     f32x4 o[D / 16][2];
-    pv_half<kBf16, D>(o, s, lane, vread);
+    pv_half<kBf16, D>(o, s, lane, vsrc);
     // Store: lane holds O[i = 16*it + c16][16*ct + 4g .. +4].
     if (live) {
 #pragma unroll
@@ -731,12 +786,15 @@ int launch_tile(const AttnParams& p, hipStream_t s) {
   return TERRA_OK;
 }
 
-// Heads per workgroup of the tile kernel: the largest divisor G of `heads`
-// among the instantiated group widths (row slices of 128, 256 or 384 bytes,
-// i.e. whole 128-byte lines, at most 192 channels); 0 if there is none.
+// Heads per workgroup of the tile kernel: the smallest divisor G of `heads`
+// among the instantiated group widths whose row slice is a whole number of
+// 128-byte lines (128, 256 or 384 bytes); 0 if there is none.  Small groups
+// mean small workgroups (2*G waves, ~26 KB of LDS for G*D = 64), so three
+// independent pipelines share a CU and their load and compute phases
+// interleave (c3: 145 us with G = 2 against 166 us with G = 6).
 int tile_group(int heads, int D) {
-  static const int kG32[] = {6, 4, 2};  // head dim 32
-  static const int kG64[] = {3, 2, 1};  // head dim 64
+  static const int kG32[] = {2, 4, 6};  // head dim 32
+  static const int kG64[] = {1, 2, 3};  // head dim 64
   const int* cand = D == 32 ? kG32 : kG64;
   for (int i = 0; i < 3; ++i)
     if (heads % cand[i] == 0) return cand[i];
