@@ -1,20 +1,22 @@
 """Benchmark of the shifted-window attention hot path on one MI355X.
 
-Step = one SW-MSA attention half of a Swin block on config c3 (the
-high-resolution ocean stage: B=1, 512x1024 tokens, C=192, 6 heads, window 8,
-shift 4, ~30 % land folded into the mask), bf16, inputs resident in HBM:
+Step = one SW-MSA attention half of a Swin block (SequentialSwinTransformer
+.forward) on config c3 (the high-resolution ocean stage: B=1, 512x1024 tokens,
+C=192, 6 heads, window 8, shift 4, ~30 % land folded into the mask), bf16,
+inputs resident in HBM.  For this shape the drop-in runs the whole half-block
+as one HIP kernel:
 
-    [norm1 + roll + partition] -> qkv GEMM -> [fused window attention]
-          -> proj GEMM -> [reverse + roll + residual]
+    [gather + LayerNorm + q/k/v + window attention + proj + residual + scatter]
 
-The bracketed stages are this library's HIP kernels; the two GEMMs are torch
-(hipBLASLt).  `value` is tokens/s of the whole step.  The
-`roofline` object is for the fused attention kernel (the path's dominant
-custom kernel), timed with HIP events on the launch stream over the timed
-steps; partition / reverse are reported under `kernels`.
+`value` is tokens/s of the step.  The `roofline` object is for that kernel,
+timed with HIP events on its launch stream over the timed steps: it is
+MFMA-bound (1.80e11 flop against 403 MB of HBM traffic per launch), so
+`achieved` is TFLOP/s against the dense bf16 peak.  `five_stage` reports the
+same step through the unfused path (LN+partition gather, q/k/v GEMM, attention
+kernel, proj GEMM, reverse+residual scatter) for comparison.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
-    python bench.py --mode kernels --steps 3     # the step's HIP kernels only,
+    python bench.py --mode kernels --steps 3     # the step's kernels only,
                                                  # plus a 192 MiB device copy
                                                  # (rocprofv3 counter calibration)
 """
@@ -51,13 +53,13 @@ def parse():
     return ap.parse_args()
 
 
-PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "window_attention_c3_pmc.md")
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "swin_block_c3_pmc.md")
 
 
 def measured_traffic():
-    """HBM bytes per launch of the attention kernel from the committed rocprofv3
-    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known
-    size), or None when that summary is absent."""
+    """HBM bytes per launch of the fused block kernel from the committed
+    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of
+    known size), or None when that summary is absent."""
     try:
         with open(PROFILE_TRAFFIC) as f:
             for line in f:
@@ -69,8 +71,9 @@ def measured_traffic():
 
 
 def run_kernels(cfg, blk, x, steps):
-    """The three HIP kernels of one c3 step on the step's own tensors, `steps`
-    times, then a device copy of 192 MiB (the counter calibration)."""
+    """The step's kernels on the step's own tensors, `steps` times: the fused
+    block kernel, then the five-stage path's three HIP kernels; then a device
+    copy of 192 MiB (the counter calibration)."""
     import torch
 
     from terra_amd import kernels
@@ -79,6 +82,8 @@ def run_kernels(cfg, blk, x, steps):
     geom = blk.geometry(B)
     grid = x.view(B, cfg.height, cfg.width, C)
     with torch.no_grad():
+        for _ in range(steps):
+            blk(x)
         win = kernels.swin_partition_ln(grid, geom, blk.norm1.weight, blk.norm1.bias, blk.norm1.eps)
         qkv = blk.attn.qkv(win)
         mask = blk.window_mask(geom)
@@ -167,13 +172,15 @@ def main():
         run_kernels(cfg, blk, x, args.steps)
         return
 
-    # Per-kernel events on the launch stream (torch's current stream, which the
-    # C ABI receives as its hipStream_t).
-    events = {"partition": [], "window_attention": [], "reverse": []}
-    orig = (kernels.swin_partition_ln, kernels.window_attention, kernels.swin_reverse)
+    # Events around the fused kernel on its launch stream (torch's current
+    # stream, which the C ABI receives as its hipStream_t).
+    events = {"swin_block": [], "partition": [], "window_attention": [], "reverse": []}
+    names = ("swin_block", "swin_partition_ln", "window_attention", "swin_reverse")
+    keys = ("swin_block", "partition", "window_attention", "reverse")
+    orig = {n: getattr(kernels, n) for n in names}
     recording = {"on": False}
 
-    def timed(name, fn):
+    def timed(key, fn):
         def wrapper(*a, **kw):
             if not recording["on"]:
                 return fn(*a, **kw)
@@ -182,44 +189,59 @@ def main():
             e0.record(s)
             out = fn(*a, **kw)
             e1.record(s)
-            events[name].append((e0, e1))
+            events[key].append((e0, e1))
             return out
         return wrapper
 
-    kernels.swin_partition_ln = timed("partition", orig[0])
-    kernels.window_attention = timed("window_attention", orig[1])
-    kernels.swin_reverse = timed("reverse", orig[2])
+    for n, k in zip(names, keys):
+        setattr(kernels, n, timed(k, orig[n]))
 
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            blk(x)
-        torch.cuda.synchronize()
-        recording["on"] = True
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for _ in range(args.steps):
-            y = blk(x)
-        t1.record()
-        torch.cuda.synchronize()
-        recording["on"] = False
-    kernels.swin_partition_ln, kernels.window_attention, kernels.swin_reverse = orig
-    ms = t0.elapsed_time(t1) / args.steps
+    def run(steps, warmup):
+        with torch.no_grad():
+            for _ in range(warmup):
+                blk(x)
+            torch.cuda.synchronize()
+            recording["on"] = True
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(steps):
+                blk(x)
+            t1.record()
+            torch.cuda.synchronize()
+            recording["on"] = False
+        return t0.elapsed_time(t1) / steps
+
+    try:
+        ms = run(args.steps, args.warmup)
+        if not events["swin_block"]:
+            raise RuntimeError("the fused block kernel did not serve the benchmark step")
+        blk.use_fused_block = False  # the five-stage path, for comparison
+        ms_five = run(max(5, args.steps // 2), 3)
+        blk.use_fused_block = True
+    finally:
+        for n in names:
+            setattr(kernels, n, orig[n])
 
     B_, N, C = cfg.num_windows, cfg.tokens, cfg.channels
     elt = torch.tensor([], dtype=dtype).element_size()
     n_real = cfg.tokens  # square windows, no padded keys
+    grid_bytes = float(cfg.batch * cfg.height * cfg.width * C * elt)
+    block_bytes = 2.0 * grid_bytes                       # x read once, y written once
+    flops_win = 2.0 * N * C * 3 * C + 4.0 * n_real * n_real * C + 2.0 * N * C * C
+    block_flops = flops_win * B_
     core_flops = 4.0 * n_real * n_real * C * B_
     core_bytes = 4.0 * B_ * N * C * elt
-    part_bytes = float(cfg.batch * cfg.height * cfg.width * C * elt + B_ * N * C * elt)
-    rev_bytes = float(B_ * N * C * elt + 2 * cfg.batch * cfg.height * cfg.width * C * elt)  # windows + residual in, y out
+    part_bytes = grid_bytes + B_ * N * C * elt
+    rev_bytes = B_ * N * C * elt + 2 * grid_bytes
 
     def avg_us(name):
         return 1e3 * statistics.mean(a.elapsed_time(b) for a, b in events[name])
 
+    t_blk = avg_us("swin_block")
     t_attn, t_part, t_rev = avg_us("window_attention"), avg_us("partition"), avg_us("reverse")
     tokens = cfg.real_tokens
-    attn_gbs = core_bytes / (t_attn * 1e-6) / 1e9
+    blk_tflops = block_flops / (t_blk * 1e-6) / 1e12
     res = {
         "metric": METRIC,
         "value": tokens / (ms * 1e-3),
@@ -234,34 +256,37 @@ def main():
         "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
         "data": "synthetic (seeded N(0,1) activations, trunc-normal(0.02) weights, seeded smoothed-noise land mask)",
         "config": {
-            "workload": (f"{cfg.name}: SW-MSA attention half of a Swin block (LN+roll+partition, qkv GEMM, fused "
-                         f"window attention, proj GEMM, reverse+roll+residual), B={cfg.batch}, "
-                         f"{cfg.height}x{cfg.width} tokens, C={C}, {cfg.heads} heads, window {cfg.window}, "
-                         f"shift {cfg.shift}" + (", ~30% land mask" if cfg.land else "")),
+            "workload": (f"{cfg.name}: SW-MSA attention half of a Swin block (LayerNorm, roll+partition, q/k/v, "
+                         f"window attention with relative-position bias + shift/land mask, proj, reverse+roll, "
+                         f"residual) as one fused kernel, B={cfg.batch}, {cfg.height}x{cfg.width} tokens, C={C}, "
+                         f"{cfg.heads} heads, window {cfg.window}, shift {cfg.shift}"
+                         + (", ~30% land mask" if cfg.land else "")),
             "windows": B_,
             "tokens": tokens,
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "window_attn_kernel (fused QK^T + bias + mask + softmax + PV)",
-            "bound": "hbm",
-            "achieved": attn_gbs,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": attn_gbs / HBM_PEAK_GBS,
+            "kernel": "swin_block_kernel<6> (fused LN + qkv + window attention + proj + residual, gather/scatter)",
+            "bound": "mfma",
+            "achieved": blk_tflops,
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": blk_tflops / MFMA_BF16_PEAK_TFLOPS,
             "traffic": measured_traffic(),
-            "algorithmic_bytes_per_launch": core_bytes,
-            "avg_launch_us": t_attn,
+            "algorithmic_flops_per_launch": block_flops,
+            "algorithmic_bytes_per_launch": block_bytes,
+            "avg_launch_us": t_blk,
+            "hbm_GB_s": block_bytes / (t_blk * 1e-6) / 1e9,
+            "hbm_frac": block_bytes / (t_blk * 1e-6) / 1e9 / HBM_PEAK_GBS,
         },
-        "kernels": {
+        "five_stage": {
+            "ms_per_step": ms_five,
+            "tokens_per_s": tokens / (ms_five * 1e-3),
             "window_attention": {
                 "us": t_attn,
-                "GB_s": attn_gbs,
-                "hbm_frac": attn_gbs / HBM_PEAK_GBS,
+                "GB_s": core_bytes / (t_attn * 1e-6) / 1e9,
+                "hbm_frac": core_bytes / (t_attn * 1e-6) / 1e9 / HBM_PEAK_GBS,
                 "TFLOP_s": core_flops / (t_attn * 1e-6) / 1e12,
-                "mfma_frac": core_flops / (t_attn * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-                "windows_per_s": B_ / (t_attn * 1e-6),
-                "tokens_per_s": tokens / (t_attn * 1e-6),
             },
             "layernorm_partition": {"us": t_part, "GB_s": part_bytes / (t_part * 1e-6) / 1e9,
                                     "hbm_frac": part_bytes / (t_part * 1e-6) / 1e9 / HBM_PEAK_GBS},

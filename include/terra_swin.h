@@ -122,6 +122,24 @@ typedef struct terra_swin_attn_desc {
   int32_t win_row_begin, win_rows, win_cols;
 } terra_swin_attn_desc;
 
+/* Description of one fused Swin attention half-block call.
+ *
+ * geom: the token grid [B, H, W, C] (channels = C), window (must be 8),
+ * shift, frame padding and the emitted window rows / valid-window range,
+ * exactly as for terra_swin_partition.  Per emitted window the call computes
+ * norm1 -> qkv -> window attention -> proj and adds the result to the window's
+ * tokens of x; tokens of windows that are not emitted keep x. */
+typedef struct terra_swin_block_desc {
+  terra_swin_geom geom;
+  int32_t heads;        /* C / heads == 32; 6 or 12 heads               */
+  float scale;          /* q k^T scale (head_dim^-0.5 in the reference) */
+  float ln_eps;         /* LayerNorm eps                                */
+  float mask_value;     /* -100.0 in the reference                      */
+  int32_t layernorm;    /* 1: norm1 = LayerNorm(gamma, beta); 0: none   */
+  int32_t shift_mask;   /* 1: analytic Swin shift mask over the frame   */
+  int32_t land_windows; /* period of land_bits (emitted windows / image) */
+} terra_swin_block_desc;
+
 /* ABI version of the loaded library (TERRA_SWIN_ABI_VERSION at build time). */
 int terra_abi_version(void);
 
@@ -179,6 +197,32 @@ int terra_swin_attn_fwd(const void* q, const void* k, const void* v, void* o,
                         int dtype, const terra_swin_attn_desc* desc,
                         const float* bias_table, const float* explicit_mask,
                         const uint64_t* land_bits, void* stream);
+
+/* Fused Swin attention half-block (bf16, 8x8 windows, head dim 32).
+ * Replaces SequentialSwinTransformer.forward   models/transformer.py:142-300:
+ *           x = self.norm1(x)                   models/transformer.py:98, 150
+ *           roll(-s) + window_partition         models/transformer.py:179-225
+ *           qkv = self.qkv(x)                   models/attention.py:244-246
+ *           window attention core               models/attention.py:256-278
+ *           x = self.proj(x)                    models/attention.py:281
+ *           window_reverse + roll(+s)           models/transformer.py:241-246
+ *           x = shortcut + x                    models/transformer.py:296-298
+ * with the land term of terra_swin_attn_fwd (land_bits[w % land_windows],
+ * w = b * emitted windows per image + emitted window index).
+ * x, y: [B, H, W, C] bf16 contiguous; y may equal x (in place) but must not
+ * overlap it otherwise.  qkv_weight [3C, C] and proj_weight [C, C] bf16
+ * (nn.Linear layout); qkv_bias [3C], proj_bias [C], ln_gamma / ln_beta [C]
+ * fp32 or NULL; bias_table fp32 [225, heads] or NULL.  Rounding follows the
+ * bf16 module: LayerNorm output, q/k/v, P, O and the proj output are rounded
+ * to bf16, and the residual add is fp32 rounded once.
+ */
+int terra_swin_block_fwd(const void* x, void* y, int dtype,
+                         const terra_swin_block_desc* desc,
+                         const float* ln_gamma, const float* ln_beta,
+                         const void* qkv_weight, const float* qkv_bias,
+                         const void* proj_weight, const float* proj_bias,
+                         const float* bias_table, const uint64_t* land_bits,
+                         void* stream);
 
 #ifdef __cplusplus
 }

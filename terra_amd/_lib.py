@@ -47,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "terra_swin_partition_ln",
     "terra_swin_reverse",
     "terra_swin_attn_fwd",
+    "terra_swin_block_fwd",
 )
 
 
@@ -102,6 +103,21 @@ class SwinAttnDesc(ctypes.Structure):
     ]
 
 
+class SwinBlockDesc(ctypes.Structure):
+    """Mirror of ``terra_swin_block_desc``."""
+
+    _fields_ = [
+        ("geom", SwinGeom),
+        ("heads", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("ln_eps", ctypes.c_float),
+        ("mask_value", ctypes.c_float),
+        ("layernorm", ctypes.c_int32),
+        ("shift_mask", ctypes.c_int32),
+        ("land_windows", ctypes.c_int32),
+    ]
+
+
 class TerraError(RuntimeError):
     """A C-ABI call returned a launch-time failure."""
 
@@ -142,6 +158,9 @@ def load() -> ctypes.CDLL:
         lib.terra_swin_reverse.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinGeom), vp]
         lib.terra_swin_attn_fwd.restype = ctypes.c_int
         lib.terra_swin_attn_fwd.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinAttnDesc), vp, vp, vp, vp]
+        lib.terra_swin_block_fwd.restype = ctypes.c_int
+        lib.terra_swin_block_fwd.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(SwinBlockDesc), vp, vp, vp, vp, vp,
+                                             vp, vp, vp, vp]
         version = lib.terra_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"terra_amd: {LIB_PATH} has ABI version {version}, expected {ABI_VERSION}; rebuild it")

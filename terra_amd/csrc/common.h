@@ -64,4 +64,23 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
 
+// Sum over the 8 aligned lanes l^1, l^2, l^4 (one LayerNorm token group).
+__device__ __forceinline__ float group8_sum(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  return v + __shfl_xor(v, 4);
+}
+
+// Derived sizes of a validated terra_swin_geom.
+struct GeomDims {
+  int64_t Hp, Wp;      // padded frame
+  int64_t nWh, nWw;    // frame windows per column / row
+  int64_t rows;        // emitted window rows (win_rows resolved)
+  int64_t nWe;         // emitted windows per image
+};
+
+// Checks the shape fields of `geom` (positive sizes, whole windows, shift
+// and window-row / valid-window ranges inside the frame) and fills `dims`.
+int validate_geom(const terra_swin_geom* geom, GeomDims* dims);
+
 }  // namespace terra

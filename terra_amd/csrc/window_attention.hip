@@ -34,404 +34,16 @@
 //       (window, head), K and Q fragments loaded straight from global memory,
 //       V staged in the wave's LDS.
 #include "common.h"
-
-#include <math.h>
+#include "attn_core.h"
 
 namespace terra {
 namespace {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kNPad = 64;       // window tokens padded to 4 tiles of 16
-constexpr int kTableMax = 228;  // >= (2*8-1)^2 = 225, multiple of 4
-constexpr float kLog2e = 1.4426950408889634f;
-
-struct AttnParams {
-  const void* q;
-  const void* k;
-  const void* v;
-  void* o;
-  int64_t q_stride, k_stride, v_stride, o_stride;
-  const float* bias_table;
-  const float* explicit_mask;
-  const uint64_t* land_bits;
-  int32_t items;      // num_windows * heads
-  int32_t heads;
-  int32_t N;          // token rows per window
-  int32_t n_geo;      // window_h * window_w (bias / mask extent)
-  int32_t window_h, window_w;
-  int32_t table_size; // (2Wh-1)(2Ww-1)
-  int32_t n_real;
-  float scale_l2e;    // scale * log2(e)
-  float mask_l2e;     // mask_value * log2(e)
-  float pad_key_l2e;  // pad_key_value * log2(e)
-  int32_t mask_mode, mask_windows;
-  int32_t frame_h, frame_w, shift_h, shift_w;
-  int32_t win_row_begin, win_rows, win_cols;
-  // window-tile kernel
-  int32_t group;      // heads per workgroup
-  int32_t groups;     // head groups per window
-};
-
-__device__ __forceinline__ int region(int coord, int extent, int ws, int shift) {
-  // Swin shift-mask slices (0:-ws), (-ws:-shift), (-shift:) of one axis.
-  return coord < extent - ws ? 0 : (coord < extent - shift ? 1 : 2);
-}
-
-// Reductions over the 4 lanes l, l^16, l^32, l^48 that share a query row.
-// v_permlane16_swap / v_permlane32_swap with both operands = v return the
-// value of the own 16-lane (32-lane) half and of the partner half, so one
-// VALU op per step replaces an LDS-crossbar shuffle.
-__device__ __forceinline__ float xor_max(float v) {
-  const uint32_t b = __float_as_uint(v);
-  const auto p16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
-  v = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
-  const uint32_t c = __float_as_uint(v);
-  const auto p32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
-  return fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
-}
-
-__device__ __forceinline__ float xor_sum(float v) {
-  const uint32_t b = __float_as_uint(v);
-  const auto p16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
-  v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
-  const uint32_t c = __float_as_uint(v);
-  const auto p32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
-  return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
-}
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  bf16x2 r;
-  r[0] = (__bf16)a;
-  r[1] = (__bf16)b;
-  return __builtin_bit_cast(uint32_t, r);
-}
-
-// Mask state of one window (uniform across the wave).
-struct WindowMaskState {
-  bool use_shift;     // window touches the last window row / column of the frame
-  bool use_mask;      // shift boundary or any land key
-  int wr, wc;         // window row / column in the frame
-  uint64_t land;      // land bit per key
-};
-
-__device__ __forceinline__ WindowMaskState window_mask_state(const AttnParams& p, int w, bool analytic) {
-  WindowMaskState m;
-  m.use_shift = false;
-  m.wr = m.wc = 0;
-  if (analytic && p.mask_mode == TERRA_MASK_SHIFT) {
-    const int per_img = p.win_rows * p.win_cols;
-    const int wl = w % per_img;
-    const int rr = wl / p.win_cols;
-    m.wr = rr + p.win_row_begin;
-    m.wc = wl - rr * p.win_cols;
-    m.use_shift = (m.wr + 2) * p.window_h > p.frame_h || (m.wc + 2) * p.window_w > p.frame_w;
-  }
-  m.land = p.land_bits != nullptr ? p.land_bits[w % p.mask_windows] : 0ull;
-  m.use_mask = m.use_shift || m.land != 0ull;
-  return m;
-}
-
-// Per-lane index terms of the window geometry.
-//   kWs8: closed form for 8x8 windows.
-//   generic: lane t computes token t's terms, other lanes fetch them with
-//   shuffles; bias index idx(i, j) = base(i) - off(j).
-template <bool kWs8>
-struct LaneGeom {
-  const float* tab8;      // kWs8: bias pointer so that offsets 30*(it-jt) - r + 93 >= 0
-  const float* tab;       // generic: this head's bias column (x log2e)
-  int g_base, g_rid;      // generic: this lane's token terms (shuffle sources)
-  int off_j[kWs8 ? 1 : 4][4];
-  uint64_t rid_pack;      // 4-bit region id of key (jt, r) at bit 4*(4*jt + r)
-  uint64_t land_lane;     // land bit of key (jt, r) at bit 16*jt + r
-};
-
-template <bool kWs8>
-__device__ __forceinline__ void lane_geom_init(LaneGeom<kWs8>& lg, const AttnParams& p, const WindowMaskState& m,
-                                               const float* tab, int lane) {
-  const int g = lane >> 4, c16 = lane & 15;
-  lg.tab = tab;
-  lg.g_base = lg.g_rid = 0;
-  int g_off = 0;
-  if constexpr (kWs8) {
-    const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;  // in [93, 134]
-    lg.tab8 = tab + (lane_base - 93);
-  } else {
-    lg.tab8 = tab;
-    const int t = lane < p.n_geo ? lane : p.n_geo - 1;
-    const int ti = t / p.window_w;
-    const int tj = t - ti * p.window_w;
-    const int rel_w = 2 * p.window_w - 1;
-    lg.g_base = (ti + p.window_h - 1) * rel_w + tj + p.window_w - 1;
-    g_off = ti * rel_w + tj;
-    if (m.use_shift)
-      lg.g_rid = 3 * region(m.wr * p.window_h + ti, p.frame_h, p.window_h, p.shift_h) +
-                 region(m.wc * p.window_w + tj, p.frame_w, p.window_w, p.shift_w);
-  }
-  lg.rid_pack = 0;
-  lg.land_lane = m.land >> (4 * g);
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int j = 16 * jt + 4 * g + r;
-      int rid;
-      if constexpr (kWs8) {
-        rid = m.use_shift ? 3 * region(m.wr * 8 + 2 * jt + (g >> 1), p.frame_h, 8, p.shift_h) +
-                                region(m.wc * 8 + 4 * (g & 1) + r, p.frame_w, 8, p.shift_w)
-                          : 0;
-      } else {
-        const int jg = j < p.n_geo ? j : p.n_geo - 1;
-        lg.off_j[jt][r] = __shfl(g_off, jg);
-        rid = __shfl(lg.g_rid, jg);
-      }
-      lg.rid_pack |= (uint64_t)rid << (4 * (4 * jt + r));
-    }
-  }
-}
-
-// Turns the raw scores of query tiles it = 2*half + {0, 1} into unnormalised
-// probabilities in place and returns 1/rowsum per tile.
-template <bool kWs8, bool kExplicit>
-__device__ __forceinline__ void softmax_half(f32x4 (&s)[2][4], float (&inv)[2], int half, const AttnParams& p,
-                                             const WindowMaskState& m, const LaneGeom<kWs8>& lg,
-                                             const float* emask, int lane) {
-  const int g = lane >> 4, c16 = lane & 15;
-  int base_i[2] = {0, 0}, rid_i[2] = {0, 0};
-  bool i_geo[2] = {true, true};
-#pragma unroll
-  for (int il = 0; il < 2; ++il) {
-    const int it = 2 * half + il;
-    const int i = 16 * it + c16;
-    if constexpr (kWs8) {
-      if (m.use_shift)
-        rid_i[il] = 3 * region(m.wr * 8 + 2 * it + (c16 >> 3), p.frame_h, 8, p.shift_h) +
-                    region(m.wc * 8 + (c16 & 7), p.frame_w, 8, p.shift_w);
-    } else {
-      const int ig = i < p.n_geo ? i : p.n_geo - 1;
-      i_geo[il] = i < p.n_geo;
-      base_i[il] = __shfl(lg.g_base, ig);
-      rid_i[il] = __shfl(lg.g_rid, ig);
-    }
-  }
-  // Pass 1, branch-free: y = s * scale * log2e + bias * log2e.
-#pragma unroll
-  for (int il = 0; il < 2; ++il) {
-    const int it = 2 * half + il;
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float b;
-        if constexpr (kWs8) {
-          b = lg.tab8[30 * (it - jt) - r + 93];
-        } else {
-          const int j = 16 * jt + 4 * g + r;
-          b = lg.tab[base_i[il] - lg.off_j[jt][r]];  // clamped indices: always in range
-          b = (i_geo[il] && j < p.n_geo) ? b : 0.f;
-        }
-        s[il][jt][r] = __builtin_fmaf(s[il][jt][r], p.scale_l2e, b);
-      }
-    }
-  }
-  // Pass 2 (only windows with a shift boundary or land keys): + mask.
-  if constexpr (kExplicit) {
-#pragma unroll
-    for (int il = 0; il < 2; ++il) {
-      const int i = 16 * (2 * half + il) + c16;
-      const int ig = i < p.n_geo ? i : p.n_geo - 1;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * jt + 4 * g + r;
-          const int jg = j < p.n_geo ? j : p.n_geo - 1;
-          const float me = emask[ig * p.n_geo + jg] * kLog2e;
-          const bool land_j = (lg.land_lane >> (16 * jt + r)) & 1ull;
-          const bool jin = kWs8 || j < p.n_geo;
-          s[il][jt][r] += ((i_geo[il] && jin) ? me : 0.f) + ((land_j && jin) ? p.mask_l2e : 0.f);
-        }
-      }
-    }
-  } else if (m.use_shift) {  // boundary windows: region test per element, plus land keys
-#pragma unroll
-    for (int il = 0; il < 2; ++il) {
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * jt + 4 * g + r;
-          const int rid_j = (int)((lg.rid_pack >> (4 * (4 * jt + r))) & 15ull);
-          const bool land_j = ((lg.land_lane >> (16 * jt + r)) & 1ull) && (kWs8 || j < p.n_geo);
-          const float ms = (i_geo[il] && rid_i[il] != rid_j) ? p.mask_l2e : 0.f;
-          s[il][jt][r] += ms + (land_j ? p.mask_l2e : 0.f);
-        }
-      }
-    }
-  } else if (m.land != 0ull) {  // land keys only: one additive term per key column
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * jt + 4 * g + r;
-        const bool land_j = ((lg.land_lane >> (16 * jt + r)) & 1ull) && (kWs8 || j < p.n_geo);
-        const float ml = land_j ? p.mask_l2e : 0.f;
-#pragma unroll
-        for (int il = 0; il < 2; ++il) s[il][jt][r] += ml;
-      }
-    }
-  }
-  // Padded keys (generic path): keys >= n_real take the pad value, keys
-  // beyond the window's rows are excluded.
-  if constexpr (!kWs8) {
-#pragma unroll
-    for (int il = 0; il < 2; ++il)
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * jt + 4 * g + r;
-          float y = s[il][jt][r];
-          y = j >= p.n_real ? p.pad_key_l2e : y;
-          s[il][jt][r] = j >= p.N ? -INFINITY : y;
-        }
-  }
-  // Row softmax: max, exp2, sum.
-#pragma unroll
-  for (int il = 0; il < 2; ++il) {
-    float mx = s[il][0][0];
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[il][jt][r]);
-    mx = xor_max(mx);
-    float sum = 0.f;
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e = __builtin_amdgcn_exp2f(s[il][jt][r] - mx);
-        s[il][jt][r] = e;
-        sum += e;
-      }
-    }
-    inv[il] = __builtin_amdgcn_rcpf(xor_sum(sum));
-  }
-}
-
-// S^T tiles of two query tiles from K fragments (4 key tiles) and the Q
-// fragments of those two query tiles (bf16: one 16-byte fragment per
-// 32-channel step; fp32: D/16 fragments, lane group g holding channels
-// [g*D/4, (g+1)*D/4) in both operands).
-template <bool kBf16, int D>
-__device__ __forceinline__ void scores_pair(f32x4 (&s)[2][4], const uint4 (&kf)[4][kBf16 ? D / 32 : D / 16],
-                                            const uint4 (&qp)[2][kBf16 ? D / 32 : D / 16]) {
-  constexpr int kKF = kBf16 ? D / 32 : D / 16;
-#pragma unroll
-  for (int il = 0; il < 2; ++il) {
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (kBf16) {
-#pragma unroll
-        for (int ks = 0; ks < kKF; ++ks)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt][ks]),
-                                                        __builtin_bit_cast(bf16x8, qp[il][ks]), acc, 0, 0, 0);
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < kKF; ++ks) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float a = __uint_as_float(reinterpret_cast<const uint32_t*>(&kf[jt][ks])[e]);
-            const float b = __uint_as_float(reinterpret_cast<const uint32_t*>(&qp[il][ks])[e]);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
-          }
-        }
-      }
-      s[il][jt] = acc;
-    }
-  }
-}
-
-// O^T tiles (ct, il) = V^T P^T for one half.  bf16: vfrag(ct, js) returns the
-// V^T operand fragment whose k-slot e (lane group g) is key
-// 32*js + 16*(e/4) + 4g + e%4 and whose row is channel 16*ct + c; fp32:
-// vread(j, c) returns V[j][c].
-template <bool kBf16, int D, class VFrag>
-__device__ __forceinline__ void pv_half(f32x4 (&o)[D / 16][2], const f32x4 (&s)[2][4], int lane, VFrag vsrc) {
-  const int g = lane >> 4, c16 = lane & 15;
-  constexpr int kCT = D / 16;
-#pragma unroll
-  for (int ct = 0; ct < kCT; ++ct)
-#pragma unroll
-    for (int il = 0; il < 2; ++il) o[ct][il] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if constexpr (kBf16) {
-#pragma unroll
-    for (int js = 0; js < 2; ++js) {
-      // P^T fragment from the accumulators, same k-slot order as vfrag.
-      bf16x8 pf[2];
-#pragma unroll
-      for (int il = 0; il < 2; ++il) {
-        uint32_t wds[4];
-#pragma unroll
-        for (int e = 0; e < 8; e += 2)
-          wds[e / 2] = pack_bf16x2(s[il][2 * js + (e >> 2)][e & 3], s[il][2 * js + (e >> 2)][(e & 3) + 1]);
-        pf[il] = __builtin_bit_cast(bf16x8, wds);
-      }
-#pragma unroll
-      for (int ct = 0; ct < kCT; ++ct) {
-        const bf16x8 vf = vsrc(ct, js);
-#pragma unroll
-        for (int il = 0; il < 2; ++il)
-          o[ct][il] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[il], o[ct][il], 0, 0, 0);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * jt + 4 * g + r;
-#pragma unroll
-        for (int ct = 0; ct < kCT; ++ct) {
-          const float a = vsrc(j, 16 * ct + c16);
-#pragma unroll
-          for (int il = 0; il < 2; ++il)
-            o[ct][il] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s[il][jt][r], o[ct][il], 0, 0, 0);
-        }
-      }
-    }
-  }
-}
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// ds_read_b64_tr_b16: within each 16-lane group, output lane l receives
-// element (l & 3) of the 8-byte words addressed by lanes (l >> 2) + 4m,
-// m = 0..3.  When lane s addresses V[row(s >> 2)][c0 + 4*(s & 3) ..], lane l
-// receives V[row(m)][c0 + l] for m = 0..3: four keys of one channel.
-__device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* addr) {
-  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_s16x4*)(__attribute__((address_space(3))) uint8_t*)(const_cast<uint8_t*>(addr)));
-  return __builtin_bit_cast(uint2, r);
-}
 
 // ============================================================================
 // window-tile kernel: bf16, 8x8 windows, one workgroup per (window, head group)
 // ============================================================================
 
 constexpr int kTileMaxRowBytes = 384;  // G*D*2 <= 384 (<= 192 bf16 channels)
-
-// 16-byte chunk slot of (row, chunk) in a [64][cpr] tile: the chunk index is
-// XOR-swizzled within its aligned group of 8 so that the 16 rows read by one
-// fragment load (and the 4 row groups of a V^T read) hit distinct banks.
-__device__ __forceinline__ int tile_slot(int row, int chunk, int cpr) {
-  return row * cpr + (chunk ^ ((row >> 1) & 7));
-}
 
 template <int D, int G>
 __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnParams p) {
@@ -450,7 +62,6 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
   const int head = wave >> 1;                    // head of the group
   const int half = wave & 1;                     // query tiles 2*half, 2*half + 1
   const int lane = tid & 63;
-  const int g = lane >> 4, c16 = lane & 15;
   const int units = (p.items / p.heads) * p.groups;  // (window, head group) pairs
 
   // A workgroup streams whole rows: each thread keeps one 16-byte chunk column
@@ -513,59 +124,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
 
     // ---- this wave: one head, query tiles 2*half, 2*half + 1 ---------------
     const WindowMaskState m = window_mask_state(p, w, true);
-    LaneGeom<true> lg;
-    lane_geom_init<true>(lg, p, m, tab, lane);
-    constexpr int kKF = D / 32;
-    uint4 kf[4][kKF], qp[2][kKF];
-    const int hc = head * (D / 8);               // first chunk of this head
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int s = 0; s < kKF; ++s)
-        kf[t][s] = *reinterpret_cast<const uint4*>(ks + tile_slot(16 * t + c16, hc + 4 * s + g, cpr) * 16);
-#pragma unroll
-    for (int il = 0; il < 2; ++il)
-#pragma unroll
-      for (int s = 0; s < kKF; ++s)
-        qp[il][s] = *reinterpret_cast<const uint4*>(
-            qs + tile_slot(16 * (2 * half + il) + c16, hc + 4 * s + g, cpr) * 16);
-    // V^T fragment (ct, js): two transposed reads, keys 32*js + 16*half2 + 4g + m.
-    auto vfrag = [&](int ct, int js) -> bf16x8 {
-      const int cc = head * D + 16 * ct + 4 * (c16 & 3);  // channel of this source lane
-      uint2 part[2];
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const int row = 32 * js + 16 * h2 + 4 * g + (c16 >> 2);
-        part[h2] = lds_read_tr16(vs + tile_slot(row, cc >> 3, cpr) * 16 + (cc & 7) * 2);
-      }
-      const uint32_t w[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
-      return __builtin_bit_cast(bf16x8, w);
-    };
-    // This wave's Q rows are in registers; its O overwrites exactly those
-    // rows of its head's columns.  Order the reads before the writes.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    {
-      f32x4 s[2][4];
-      scores_pair<true, D>(s, kf, qp);
-      float inv[2];
-      softmax_half<true, false>(s, inv, half, p, m, lg, nullptr, lane);
-      f32x4 o[D / 16][2];
-      pv_half<true, D>(o, s, lane, vfrag);
-#pragma unroll
-      for (int il = 0; il < 2; ++il) {
-        const int i = 16 * (2 * half + il) + c16;
-#pragma unroll
-        for (int ct = 0; ct < D / 16; ++ct) {
-          const f32x4 v = o[ct][il] * inv[il];
-          const int cc = head * D + 16 * ct + 4 * g;  // 4 channels, 8 bytes
-          uint2 pk;
-          pk.x = pack_bf16x2(v[0], v[1]);
-          pk.y = pack_bf16x2(v[2], v[3]);
-          *reinterpret_cast<uint2*>(qs + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
-        }
-      }
-    }
+    tile_attention_wave<D, cpr>(qs, ks, vs, head, half, p, m, tab, lane);
     __syncthreads();
 
     // ---- stream O out (whole lines) ------------------------------------------

@@ -13,6 +13,35 @@
 #include "common.h"
 
 namespace terra {
+
+int validate_geom(const terra_swin_geom* geom, GeomDims* dims) {
+  if (geom == nullptr) return fail(TERRA_ERR_NULL, "geom is NULL");
+  const terra_swin_geom& q = *geom;
+  if (q.batch <= 0 || q.height <= 0 || q.width <= 0 || q.channels <= 0 || q.window <= 0)
+    return fail(TERRA_ERR_SHAPE, "batch/height/width/channels/window must be positive (got %d/%d/%d/%d/%d)",
+                q.batch, q.height, q.width, q.channels, q.window);
+  if (q.pad_top < 0 || q.pad_bottom < 0 || q.pad_left < 0 || q.pad_right < 0)
+    return fail(TERRA_ERR_SHAPE, "padding must be non-negative");
+  const int64_t Hp = (int64_t)q.height + q.pad_top + q.pad_bottom;
+  const int64_t Wp = (int64_t)q.width + q.pad_left + q.pad_right;
+  if (Hp % q.window != 0 || Wp % q.window != 0)
+    return fail(TERRA_ERR_SHAPE, "padded grid %lldx%lld is not a multiple of window %d",
+                (long long)Hp, (long long)Wp, q.window);
+  if (q.shift_h < 0 || q.shift_h >= Hp || q.shift_w < 0 || q.shift_w >= Wp)
+    return fail(TERRA_ERR_SHAPE, "shift (%d, %d) outside [0, padded extent)", q.shift_h, q.shift_w);
+  const int64_t nWh = Hp / q.window, nWw = Wp / q.window;
+  const int64_t rows = q.win_rows <= 0 ? nWh - q.win_row_begin : q.win_rows;
+  if (q.win_row_begin < 0 || rows <= 0 || q.win_row_begin + rows > nWh)
+    return fail(TERRA_ERR_SHAPE, "window rows [%d, %lld) outside the %lld-row window grid",
+                q.win_row_begin, (long long)(q.win_row_begin + rows), (long long)nWh);
+  const int64_t nWe = rows * nWw;
+  if (q.valid_end > 0 && (q.valid_begin < 0 || q.valid_begin >= q.valid_end || q.valid_end > nWe))
+    return fail(TERRA_ERR_SHAPE, "valid window range [%d, %d) outside [0, %lld)", q.valid_begin,
+                q.valid_end, (long long)nWe);
+  dims->Hp = Hp; dims->Wp = Wp; dims->nWh = nWh; dims->nWw = nWw; dims->rows = rows; dims->nWe = nWe;
+  return TERRA_OK;
+}
+
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -151,12 +180,6 @@ __device__ __forceinline__ u32x4 pack_chunk(const float* f) {
     }
   }
   return c;
-}
-
-__device__ __forceinline__ float group8_sum(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  return v + __shfl_xor(v, 4);
 }
 
 struct LnParams {
@@ -378,28 +401,11 @@ int prepare(const terra_swin_geom* geom, int dtype, bool dest_is_windows, CopyGe
   if (geom == nullptr) return fail(TERRA_ERR_NULL, "geom is NULL");
   const int elt = dtype_size(dtype);
   if (elt == 0) return fail(TERRA_ERR_DTYPE, "unknown dtype %d", dtype);
+  GeomDims dims;
+  const int st = validate_geom(geom, &dims);
+  if (st != TERRA_OK) return st;
   const terra_swin_geom& q = *geom;
-  if (q.batch <= 0 || q.height <= 0 || q.width <= 0 || q.channels <= 0 || q.window <= 0)
-    return fail(TERRA_ERR_SHAPE, "batch/height/width/channels/window must be positive (got %d/%d/%d/%d/%d)",
-                q.batch, q.height, q.width, q.channels, q.window);
-  if (q.pad_top < 0 || q.pad_bottom < 0 || q.pad_left < 0 || q.pad_right < 0)
-    return fail(TERRA_ERR_SHAPE, "padding must be non-negative");
-  const int64_t Hp = (int64_t)q.height + q.pad_top + q.pad_bottom;
-  const int64_t Wp = (int64_t)q.width + q.pad_left + q.pad_right;
-  if (Hp % q.window != 0 || Wp % q.window != 0)
-    return fail(TERRA_ERR_SHAPE, "padded grid %lldx%lld is not a multiple of window %d",
-                (long long)Hp, (long long)Wp, q.window);
-  if (q.shift_h < 0 || q.shift_h >= Hp || q.shift_w < 0 || q.shift_w >= Wp)
-    return fail(TERRA_ERR_SHAPE, "shift (%d, %d) outside [0, padded extent)", q.shift_h, q.shift_w);
-  const int64_t nWh = Hp / q.window, nWw = Wp / q.window;
-  const int64_t rows = q.win_rows <= 0 ? nWh - q.win_row_begin : q.win_rows;
-  if (q.win_row_begin < 0 || rows <= 0 || q.win_row_begin + rows > nWh)
-    return fail(TERRA_ERR_SHAPE, "window rows [%d, %lld) outside the %lld-row window grid",
-                q.win_row_begin, (long long)(q.win_row_begin + rows), (long long)nWh);
-  const int64_t nWe = rows * nWw;
-  if (q.valid_end > 0 && (q.valid_begin < 0 || q.valid_begin >= q.valid_end || q.valid_end > nWe))
-    return fail(TERRA_ERR_SHAPE, "valid window range [%d, %d) outside [0, %lld)", q.valid_begin,
-                q.valid_end, (long long)nWe);
+  const int64_t Hp = dims.Hp, Wp = dims.Wp, nWw = dims.nWw, rows = dims.rows, nWe = dims.nWe;
   const int64_t row_bytes = (int64_t)q.channels * elt;
   int v = 16;
   while (v > 1 && (row_bytes % v) != 0) v >>= 1;

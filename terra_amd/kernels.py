@@ -333,3 +333,83 @@ def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_head
                                              _ptr(table), _ptr(emask), _ptr(land), _stream(dev))
     _lib.check(st, "terra_swin_attn_fwd")
     return out
+
+
+# Shapes the fused block kernel is built for: 8x8 windows, head dim 32.
+BLOCK_HEADS = (6, 12)
+
+
+def swin_block_supported(x: torch.Tensor, geom: WindowGeometry, num_heads: int) -> bool:
+    """Whether :func:`swin_block` serves this call (bf16 device tensor, 8x8
+    windows, head dim 32 with 6 or 12 heads)."""
+    return (x.device.type == "cuda" and x.dtype == torch.bfloat16 and geom.window == 8
+            and num_heads in BLOCK_HEADS and geom.channels == 32 * num_heads)
+
+
+def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: float,
+               qkv_weight: torch.Tensor, qkv_bias: Optional[torch.Tensor],
+               proj_weight: torch.Tensor, proj_bias: Optional[torch.Tensor],
+               ln_weight: Optional[torch.Tensor] = None, ln_bias: Optional[torch.Tensor] = None,
+               ln_eps: float = 1e-5, layernorm: bool = True,
+               bias_table: Optional[torch.Tensor] = None, shift_mask: bool = False,
+               land_bits: Optional[torch.Tensor] = None, mask_value: float = MASK_VALUE,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused Swin attention half-block on ``x`` [B, H, W, C] (bf16):
+
+        y = x + reverse(proj(attention(qkv(partition(LayerNorm(x))))))
+
+    i.e. SequentialSwinTransformer.forward (models/transformer.py:142-300) with
+    the attention of models/attention.py:236-283, in one kernel.  Float
+    parameters (LayerNorm affine, biases, bias table) are passed as fp32;
+    weights in the activation dtype.  ``shift_mask`` enables the analytic
+    shift mask of the padded frame; ``land_bits`` ([emitted windows per
+    image] int64) adds ``mask_value`` on land keys.  ``out`` may be ``x``.
+    """
+    dev = _require_device(x, qkv_weight, proj_weight)
+    code = _dtype_code(x, (torch.bfloat16,))
+    C = geom.channels
+    if tuple(x.shape) != (geom.batch, geom.height, geom.width, C) or not x.is_contiguous():
+        raise ValueError(f"x must be a contiguous [{geom.batch}, {geom.height}, {geom.width}, {C}] tensor")
+    for name, t, shape in (("qkv_weight", qkv_weight, (3 * C, C)), ("proj_weight", proj_weight, (C, C))):
+        if tuple(t.shape) != shape or t.dtype != x.dtype or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {x.dtype} tensor of shape {shape}")
+
+    def f32(t, n, name):
+        if t is None:
+            return None
+        _require_device(x, t)
+        if t.numel() != n:
+            raise ValueError(f"{name} must have {n} elements")
+        return t.detach().reshape(-1).to(torch.float32).contiguous()
+
+    params = (f32(ln_weight, C, "ln_weight") if layernorm else None,
+              f32(ln_bias, C, "ln_bias") if layernorm else None,
+              f32(qkv_bias, 3 * C, "qkv_bias"), f32(proj_bias, C, "proj_bias"))
+    table = None
+    if bias_table is not None:
+        _require_device(x, bias_table)
+        if tuple(bias_table.shape) != (225, num_heads):
+            raise ValueError(f"bias table must be [225, {num_heads}], got {tuple(bias_table.shape)}")
+        table = bias_table.detach().to(torch.float32).contiguous()
+    d = _lib.SwinBlockDesc()
+    d.geom = geom.to_c()
+    d.heads, d.scale, d.ln_eps, d.mask_value = num_heads, float(scale), float(ln_eps), float(mask_value)
+    d.layernorm, d.shift_mask = int(bool(layernorm)), int(bool(shift_mask))
+    d.land_windows = 0
+    if land_bits is not None:
+        _require_device(x, land_bits)
+        if land_bits.dtype != torch.int64 or land_bits.dim() != 1:
+            raise ValueError("land_bits must be a 1-D int64 tensor (one 64-bit key mask per window)")
+        land_bits = land_bits.contiguous()
+        d.land_windows = land_bits.shape[0]
+    if out is None:
+        out = torch.empty_like(x)
+    elif tuple(out.shape) != tuple(x.shape) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
+        raise ValueError("out must be a contiguous tensor like x")
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_block_fwd(_ptr(x), _ptr(out), code, ctypes.byref(d), _ptr(params[0]),
+                                              _ptr(params[1]), _ptr(qkv_weight), _ptr(params[2]),
+                                              _ptr(proj_weight), _ptr(params[3]), _ptr(table), _ptr(land_bits),
+                                              _stream(dev))
+    _lib.check(st, "terra_swin_block_fwd")
+    return out

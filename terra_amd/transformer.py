@@ -1,6 +1,9 @@
 """Drop-in ``SequentialSwinTransformer`` (models/transformer.py:71-356).
 
-The attention half of a Swin block on one GPU:
+The attention half of a Swin block on one GPU.  For bf16 activations, 8x8
+windows and head dim 32 (6 or 12 heads) the whole half-block is one HIP
+kernel (``kernels.swin_block``: gather + LayerNorm + q/k/v + attention + proj
++ residual + scatter).  Otherwise:
 
     x -> [norm1 + roll(-s) + window partition]      one HIP gather
       -> q/k/v projection (one GEMM)                 hipBLASLt via torch
@@ -74,6 +77,9 @@ class SequentialSwinTransformer(torch.nn.Module):
         else:
             self.land_mask = None
         self._land_bits_cache = {}
+        # Run the whole half-block as one kernel where the shapes allow it
+        # (see _fusable_block); False forces the five-stage path.
+        self.use_fused_block = True
 
     def geometry(self, batch: int) -> WindowGeometry:
         H, W = self.input_resolution
@@ -105,6 +111,51 @@ class SequentialSwinTransformer(torch.nn.Module):
                 and dtype in (torch.float32, torch.float16, torch.bfloat16)
                 and row_bytes % 16 == 0 and row_bytes <= 1536)
 
+    def _fusable_block(self, x: torch.Tensor, geom: WindowGeometry) -> bool:
+        """The whole half-block runs as one kernel: bf16, 8x8 windows, head
+        dim 32 (6 or 12 heads), a plain LayerNorm (or none), biased q/k/v, and
+        no gradient needed (the fused kernel is forward-only)."""
+        attn = self.attn
+        if not self.use_fused_block or not kernels.swin_block_supported(x, geom, attn.num_heads):
+            return False
+        if config.use_layernorm and not self._fusable_norm(x.dtype):
+            return False
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        lins = (attn.q_linear, attn.k_linear, attn.v_linear, attn.proj)
+        return all(l.weight.dtype == x.dtype for l in lins) and attn.q_linear.bias is not None
+
+    def _fused_args(self) -> dict:
+        """Concatenated q/k/v weight and fp32 copies of the small parameters,
+        cached until any of them changes (data pointer or in-place version)."""
+        attn = self.attn
+        tensors = [attn.q_linear.weight, attn.k_linear.weight, attn.v_linear.weight, attn.q_linear.bias,
+                   attn.k_linear.bias, attn.v_linear.bias, attn.proj.weight, attn.proj.bias]
+        if config.use_layernorm:
+            tensors += [self.norm1.weight, self.norm1.bias]
+        if attn.use_relative_position_bias:
+            tensors.append(attn.relative_position_bias_table)
+        key = tuple((t.data_ptr(), t._version, t.device) if t is not None else None for t in tensors)
+        cached = getattr(self, "_fused_cache", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        with torch.no_grad():
+            f32 = lambda t: None if t is None else t.detach().to(torch.float32).contiguous()  # noqa: E731
+            args = dict(
+                qkv_weight=torch.cat([attn.q_linear.weight, attn.k_linear.weight, attn.v_linear.weight], 0)
+                .detach().contiguous(),
+                qkv_bias=f32(torch.cat([attn.q_linear.bias, attn.k_linear.bias, attn.v_linear.bias], 0)),
+                proj_weight=attn.proj.weight.detach().contiguous(),
+                proj_bias=f32(attn.proj.bias),
+                ln_weight=f32(self.norm1.weight) if config.use_layernorm else None,
+                ln_bias=f32(self.norm1.bias) if config.use_layernorm else None,
+                ln_eps=float(self.norm1.eps) if config.use_layernorm else 0.0,
+                layernorm=bool(config.use_layernorm),
+                bias_table=f32(attn.relative_position_bias_table) if attn.use_relative_position_bias else None,
+            )
+        self._fused_cache = (key, args)
+        return args
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         H, W = self.input_resolution
         B, L, C = x.shape
@@ -113,6 +164,12 @@ class SequentialSwinTransformer(torch.nn.Module):
         shortcut = x
         geom = self.geometry(B)
         grid = x.contiguous().view(B, H, W, C)
+        if self._fusable_block(grid, geom):
+            mask = self.window_mask(geom)
+            y = kernels.swin_block(grid, geom, self.attn.num_heads, self.attn.scale,
+                                   shift_mask=mask is not None and mask.shift is not None,
+                                   land_bits=None if mask is None else mask.land_bits, **self._fused_args())
+            return y.view(B, H * W, C)
         if config.use_layernorm and self._fusable_norm(grid.dtype):
             x_windows = kernels.swin_partition_ln(grid, geom, self.norm1.weight, self.norm1.bias, self.norm1.eps)
         else:

@@ -37,6 +37,7 @@ def test_abi_version_and_struct_sizes():
     # every field of the C structs is 4 bytes wide
     assert ctypes.sizeof(L.SwinGeom) == 4 * len(L.SwinGeom._fields_) == 60
     assert ctypes.sizeof(L.SwinAttnDesc) == 4 * len(L.SwinAttnDesc._fields_) == 92
+    assert ctypes.sizeof(L.SwinBlockDesc) == 60 + 4 * (len(L.SwinBlockDesc._fields_) - 1) == 88
 
 
 def _geom(**kw):
@@ -157,3 +158,58 @@ def test_partition_ln_rejects_bad_arguments():
     assert lib.terra_swin_partition_ln(FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(big), None, None, 1e-5, 0.0, None) == -5
     assert "1536" in L.last_error()
     assert lib.terra_swin_partition_ln(FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(g), None, None, -1.0, 0.0, None) == -3
+
+
+def _block_desc(geom_kw=None, **kw):
+    d = L.SwinBlockDesc()
+    gk = dict(channels=192, window=8)
+    gk.update(geom_kw or {})
+    d.geom = _geom(**gk)
+    vals = dict(heads=6, scale=32 ** -0.5, ln_eps=1e-5, mask_value=-100.0, layernorm=1, shift_mask=0,
+                land_windows=0)
+    vals.update(kw)
+    for k, v in vals.items():
+        setattr(d, k, v)
+    return d
+
+
+def _block_call(d, dtype=L.DTYPE_BF16, x=FAKE, land=None):
+    return L.load().terra_swin_block_fwd(x, FAKE, dtype, ctypes.byref(d) if d is not None else None, None, None,
+                                         FAKE, None, FAKE, None, None, land, None)
+
+
+@pytest.mark.parametrize("geom_kw,kw,dtype,code,text", [
+    ({}, {}, L.DTYPE_F32, -5, "bf16 only"),
+    ({}, {}, 9, -2, "unknown dtype"),
+    ({"window": 4}, {}, L.DTYPE_BF16, -5, "8x8 windows"),
+    ({"channels": 128}, {"heads": 4}, L.DTYPE_BF16, -5, "6 or 12 heads"),
+    ({"channels": 384}, {"heads": 6}, L.DTYPE_BF16, -5, "head dim 32"),
+    ({"height": 12}, {}, L.DTYPE_BF16, -3, "not a multiple of window"),
+    ({"valid_begin": 0, "valid_end": 9}, {}, L.DTYPE_BF16, -3, "valid window range"),
+    ({}, {"ln_eps": -1.0}, L.DTYPE_BF16, -3, "ln_eps"),
+])
+def test_block_rejects_bad_descriptors(geom_kw, kw, dtype, code, text):
+    st = _block_call(_block_desc(geom_kw, **kw), dtype)
+    assert st == code, L.last_error()
+    assert text in L.last_error()
+
+
+def test_block_rejects_null_alignment_overlap_land():
+    d = _block_desc()
+    assert _block_call(None) == -1
+    assert _block_call(d, x=None) == -1
+    assert _block_call(d, x=ctypes.c_void_p((1 << 20) + 8)) == -4
+    assert _block_call(d, land=FAKE) == -3  # land bits without a period
+    assert "land_windows" in L.last_error()
+    lib = L.load()
+    y = ctypes.c_void_p((1 << 20) + 4096)  # overlaps x without being x
+    assert lib.terra_swin_block_fwd(FAKE, y, L.DTYPE_BF16, ctypes.byref(d), None, None, FAKE, None, FAKE, None,
+                                    None, None, None) == -3
+    assert "overlaps" in L.last_error()
+
+
+def test_block_wrapper_raises_on_cpu_tensors():
+    x = torch.zeros(1, 16, 16, 192, dtype=torch.bfloat16)
+    w = torch.zeros(576, 192, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        kernels.swin_block(x, kernels.WindowGeometry(1, 16, 16, 192, 8), 6, 0.17, w, None, w[:192], None)

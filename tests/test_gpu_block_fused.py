@@ -1,0 +1,187 @@
+"""The fused half-block kernel (gather + LayerNorm + q/k/v + window attention
++ proj + residual + scatter in one launch) against the five-stage path of the
+same module and against the oracle's fp32 restatement of the reference block.
+
+Tolerances: both GPU paths round the same intermediates to bf16 (LayerNorm
+output, q/k/v, P, O, proj output) and differ only in GEMM summation order, so
+elementwise |y_fused - y_five_stage| <= one bf16 ulp of y (2^-7 |y|) + 2e-2 of
+the max-abs attention delta (y - x).  Against the fp32 oracle: the 2e-2
+max-abs relative bound of the other bf16 block tests on y, and 3e-2 normwise
+on the delta.  The weights are scaled up (gain) so that the delta is O(1) and
+these checks see the attention, not the residual (q/k/v gain 4: logits of
+standard deviation ~1; proj gain 16).  Pass-through tokens
+(windows the frame does not emit) are bit-exact copies of x.
+"""
+import pytest
+import torch
+
+from oracle import swin_oracle as so
+from terra_amd import config, kernels, workloads
+from terra_amd.kernels import WindowGeometry
+from terra_amd.transformer import SequentialSwinTransformer
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(block):
+    return {k: v.detach().float().cpu() for k, v in block.state_dict().items() if k != "attn_mask"}
+
+
+def _rel(out, ref):
+    out, ref = out.double().cpu(), ref.double().cpu()
+    return ((out - ref).abs().max() / ref.abs().max()).item()
+
+
+def _block(dev, H, W, C, heads, layer, land=None, pad=(0, 0, 0, 0), win_row_begin=0, win_rows=None, valid=None,
+           bias=True, gain_qkv=4.0, gain_proj=16.0):
+    blk = SequentialSwinTransformer(layer_idx=layer, height=H, width=W, embedding_dim=C, window_size=8,
+                                    num_heads=heads, init_seed_base=workloads.SEED_BASE, land_mask=land, pad=pad,
+                                    win_row_begin=win_row_begin, win_rows=win_rows, valid_windows=valid,
+                                    use_relative_position_bias=bias)
+    workloads.init_block_params(blk, layer)
+    with torch.no_grad():
+        for lin in (blk.attn.q_linear, blk.attn.k_linear, blk.attn.v_linear, blk.attn.proj):
+            lin.weight.mul_(gain_proj if lin is blk.attn.proj else gain_qkv)
+            lin.bias.copy_(workloads.activations(lin.bias.shape, 409, torch.float32) * 0.1)
+        if bias:
+            blk.attn.relative_position_bias_table.mul_(50.0)
+        blk.norm1.weight.copy_(1.0 + 0.1 * workloads.activations((C,), 410, torch.float32))
+        blk.norm1.bias.copy_(0.1 * workloads.activations((C,), 411, torch.float32))
+    return blk.to(dev).to(torch.bfloat16)
+
+
+def _assert_paths_agree(y_f, y_u, x):
+    d_u = y_u.float() - x.float()
+    scale = d_u.abs().max().item()
+    assert scale > 0.5, "attention delta too small to test"
+    tol = 2.0 ** -7 * y_u.float().abs() + 2e-2 * scale
+    err = (y_f.float() - y_u.float()).abs()
+    assert bool((err <= tol).all()), float((err - tol).max())
+
+
+def _assert_matches_oracle(y_f, ref, x):
+    assert _rel(y_f, ref) <= 2e-2
+    d_f = y_f.double().cpu() - x.double()
+    d_r = ref.double() - x.double()
+    assert (torch.linalg.vector_norm(d_f - d_r) / torch.linalg.vector_norm(d_r)).item() <= 3e-2
+
+
+def _both_paths(blk, x):
+    calls = {"n": 0}
+    orig = kernels.swin_block
+
+    def counting(*a, **kw):
+        calls["n"] += 1
+        return orig(*a, **kw)
+
+    kernels.swin_block = counting
+    try:
+        with torch.no_grad():
+            blk.use_fused_block = True
+            y_f = blk(x)
+            assert calls["n"] == 1, "the fused kernel did not serve this block"
+            blk.use_fused_block = False
+            y_u = blk(x)
+            assert calls["n"] == 1
+    finally:
+        kernels.swin_block = orig
+        blk.use_fused_block = True
+    return y_f, y_u
+
+
+CASES = [  # (H, W, C, heads, layer, land, pad, win_row_begin, win_rows, valid, bias)
+    (32, 64, 192, 6, 1, True, (0, 0, 0, 0), 0, None, None, True),     # c3 semantics, SW-MSA + land
+    (32, 64, 192, 6, 0, False, (0, 0, 0, 0), 0, None, None, True),    # W-MSA, no mask
+    (24, 40, 192, 6, 1, False, (0, 0, 0, 0), 0, None, None, False),   # no bias table
+    (40, 64, 384, 12, 1, True, (0, 8, 0, 0), 0, 5, (3, 37), True),    # c5 semantics: slab, pad windows
+    (16, 48, 384, 12, 0, True, (0, 0, 0, 0), 0, None, None, True),    # 12 heads, W-MSA + land
+    (20, 24, 192, 6, 1, True, (2, 2, 0, 8), 1, 1, None, True),        # pad on all sides, window-row band
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_fused_matches_five_stage_and_oracle(dev, case):
+    H, W, C, heads, layer, land_on, pad, r0, rows, valid, bias = case
+    land = workloads.land_mask(H, W, seed=400) if land_on else None
+    blk = _block(dev, H, W, C, heads, layer, land, pad, r0, rows, valid, bias)
+    x = workloads.activations((2, H * W, C), 401, torch.bfloat16)
+    xd = x.to(dev)
+    y_f, y_u = _both_paths(blk, xd)
+    _assert_paths_agree(y_f, y_u, xd)
+    ref = so.swin_block_attention(x, H, W, 8, blk.shift_size, heads, _params(blk), land=land, pad=pad,
+                                  win_row_begin=r0, win_rows=rows, valid=valid)
+    _assert_matches_oracle(y_f, ref, x)
+
+
+def _emitted_tokens(B, H, W, pad, r0, rows, valid, shift):
+    ones = torch.ones(B, H, W, 1)
+    win = so.partition_frame(ones, 8, shift, shift, pad, r0, rows, valid)
+    back = so.reverse_frame(win, B, H, W, 8, shift, shift, pad, r0, rows, valid)
+    return back.view(B, H * W) > 0
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c[8] is not None or c[9] is not None])
+def test_fused_pass_through_tokens_are_exact(dev, case):
+    H, W, C, heads, layer, land_on, pad, r0, rows, valid, bias = case
+    blk = _block(dev, H, W, C, heads, layer, None, pad, r0, rows, valid, bias)
+    x = workloads.activations((2, H * W, C), 402, torch.bfloat16).to(dev)
+    with torch.no_grad():
+        y = blk(x)
+    emitted = _emitted_tokens(2, H, W, pad, r0, rows, valid, blk.shift_size).to(dev)
+    assert (~emitted).any() and emitted.any()
+    assert torch.equal(y[~emitted], x[~emitted])
+    assert not torch.equal(y[emitted], x[emitted])
+
+
+def test_fused_in_place_equals_out_of_place(dev):
+    H, W, C, heads = 32, 48, 192, 6
+    land = workloads.land_mask(H, W, seed=403)
+    blk = _block(dev, H, W, C, heads, 1, land)
+    x = workloads.activations((1, H, W, C), 404, torch.bfloat16).to(dev)
+    geom = blk.geometry(1)
+    mask = blk.window_mask(geom)
+    args = dict(shift_mask=True, land_bits=mask.land_bits, **blk._fused_args())
+    with torch.no_grad():
+        y = kernels.swin_block(x, geom, heads, blk.attn.scale, **args)
+        xi = x.clone()
+        kernels.swin_block(xi, geom, heads, blk.attn.scale, out=xi, **args)
+    assert torch.equal(xi, y)
+
+
+def test_fused_without_layernorm(dev, monkeypatch):
+    monkeypatch.setattr(config, "use_layernorm", False)
+    H, W, C, heads = 16, 32, 192, 6
+    blk = SequentialSwinTransformer(layer_idx=1, height=H, width=W, embedding_dim=C, window_size=8,
+                                    num_heads=heads, init_seed_base=workloads.SEED_BASE)
+    workloads.init_block_params(blk, 1)
+    with torch.no_grad():
+        for lin in (blk.attn.q_linear, blk.attn.k_linear, blk.attn.v_linear, blk.attn.proj):
+            lin.weight.mul_(16.0 if lin is blk.attn.proj else 4.0)
+    blk = blk.to(dev).to(torch.bfloat16)
+    x = workloads.activations((1, H * W, C), 405, torch.bfloat16)
+    y_f, y_u = _both_paths(blk, x.to(dev))
+    _assert_paths_agree(y_f, y_u, x.to(dev))
+    ref = so.swin_block_attention(x, H, W, 8, 4, heads, _params(blk), use_layernorm=False)
+    _assert_matches_oracle(y_f, ref, x)
+
+
+def test_fused_deterministic(dev):
+    blk = _block(dev, 32, 64, 192, 6, 1, workloads.land_mask(32, 64, seed=406))
+    x = workloads.activations((1, 32 * 64, 192), 407, torch.bfloat16).to(dev)
+    with torch.no_grad():
+        a = blk(x)
+        b = blk(x)
+    assert torch.equal(a, b)
+
+
+def test_fused_full_size_c3(dev):
+    """The benchmark configuration end to end: fused kernel vs the oracle."""
+    cfg = workloads.CONFIGS["c3"]
+    land = workloads.land_mask(cfg.height, cfg.width, seed=42)
+    blk = workloads.block_for(cfg, 1, land=land).to(dev).to(torch.bfloat16)
+    x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 1003, torch.bfloat16)
+    y_f, y_u = _both_paths(blk, x.to(dev))
+    d = (y_f.float() - y_u.float()).abs()
+    assert bool((d <= 2.0 ** -7 * y_u.float().abs() + 1e-2).all())
+    ref = so.swin_block_attention(x, cfg.height, cfg.width, cfg.window, 4, cfg.heads, _params(blk), land=land)
+    assert _rel(y_f, ref) <= 2e-2
