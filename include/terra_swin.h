@@ -138,6 +138,8 @@ typedef struct terra_swin_block_desc {
   int32_t layernorm;    /* 1: norm1 = LayerNorm(gamma, beta); 0: none   */
   int32_t shift_mask;   /* 1: analytic Swin shift mask over the frame   */
   int32_t land_windows; /* period of land_bits (emitted windows / image) */
+  int32_t packed_weights; /* 0: qkv/proj weights in nn.Linear layout;
+                             1: in the layout of terra_swin_pack_linear */
 } terra_swin_block_desc;
 
 /* ABI version of the loaded library (TERRA_SWIN_ABI_VERSION at build time). */
@@ -223,6 +225,17 @@ int terra_swin_block_fwd(const void* x, void* y, int dtype,
                          const void* proj_weight, const float* proj_bias,
                          const float* bias_table, const uint64_t* land_bits,
                          void* stream);
+
+/* MFMA fragment order of a bf16 [out_features, in_features] weight (out
+ * multiple of 16, in multiple of 32) for terra_swin_block_fwd with
+ * packed_weights = 1: packed[((rt * in/32 + ks) * 64 + l) * 8 + e] =
+ * weight[16 rt + l % 16][32 ks + 8 (l / 16) + e].  A wave then reads each
+ * 16 x 32 operand tile as one contiguous 1 KB block.  No reference
+ * counterpart: a one-time re-layout of nn.Linear.weight (models/attention.py:
+ * 223-228, 281) that the caller keeps with the module.
+ */
+int terra_swin_pack_linear(const void* weight, void* packed, int dtype,
+                           int out_features, int in_features, void* stream);
 
 #ifdef __cplusplus
 }

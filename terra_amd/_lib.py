@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "terra_swin_reverse",
     "terra_swin_attn_fwd",
     "terra_swin_block_fwd",
+    "terra_swin_pack_linear",
 )
 
 
@@ -115,6 +116,7 @@ class SwinBlockDesc(ctypes.Structure):
         ("layernorm", ctypes.c_int32),
         ("shift_mask", ctypes.c_int32),
         ("land_windows", ctypes.c_int32),
+        ("packed_weights", ctypes.c_int32),
     ]
 
 
@@ -161,6 +163,8 @@ def load() -> ctypes.CDLL:
         lib.terra_swin_block_fwd.restype = ctypes.c_int
         lib.terra_swin_block_fwd.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(SwinBlockDesc), vp, vp, vp, vp, vp,
                                              vp, vp, vp, vp]
+        lib.terra_swin_pack_linear.restype = ctypes.c_int
+        lib.terra_swin_pack_linear.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
         version = lib.terra_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"terra_amd: {LIB_PATH} has ABI version {version}, expected {ABI_VERSION}; rebuild it")

@@ -62,6 +62,7 @@ struct BlockParams {
   const float* bias_table;   // [(2*8-1)^2, heads] or NULL
   const uint64_t* land_bits; // [land_windows] or NULL
   int32_t land_windows;
+  int32_t packed;            // weights in MFMA fragment order (terra_swin_pack_linear)
   int32_t layernorm;         // 0: xn = x
   int32_t shift_mask;        // analytic shift mask on/off
   float eps, inv_c;
@@ -120,6 +121,18 @@ __device__ __forceinline__ uint4 pack_frag(const f32x4& lo, const f32x4& hi) {
 __device__ __forceinline__ f32x4 load_f32x4(const float* p) {
   const float4 v = *reinterpret_cast<const float4*>(p);
   return f32x4{v.x, v.y, v.z, v.w};
+}
+
+// The 16-byte A/B-operand fragment of weight rows [16*rt, 16*rt + 16),
+// input channels [32*ks, 32*ks + 32) for this lane (row rt*16 + lane%16,
+// channels 32ks + 8*(lane/16) ..): strided rows of the nn.Linear layout, or
+// one contiguous 1 KB block per (rt, ks) in the packed layout.
+template <int kC>
+__device__ __forceinline__ uint4 weight_frag(const uint16_t* w, int packed, int rt, int ks, int lane) {
+  const uint4* src = packed ? reinterpret_cast<const uint4*>(w) + ((rt * (kC / 32) + ks) * 64 + lane)
+                            : reinterpret_cast<const uint4*>(w + (int64_t)(16 * rt + (lane & 15)) * kC + 32 * ks +
+                                                             8 * (lane >> 4));
+  return *src;
 }
 
 // Cache-policy bits of the global -> LDS loads: nontemporal (every x byte is
@@ -349,14 +362,11 @@ __global__ __launch_bounds__(128 * kH) void swin_block_tile_kernel(const BlockPa
       // ---- this wave's q|k|v weight rows [f0, f0 + kFeat), all k-steps ------
       const int f0 = kFeat * wave;
       uint4 wf[kKS][kQkvTiles];
-      {
-        const uint16_t* wrow = p.w_qkv + (int64_t)(f0 + c16) * C + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < kKS; ++ks)
+      for (int ks = 0; ks < kKS; ++ks)
 #pragma unroll
-          for (int ft = 0; ft < kQkvTiles; ++ft)
-            wf[ks][ft] = *reinterpret_cast<const uint4*>(wrow + 16 * ft * C + 32 * ks);
-      }
+        for (int ft = 0; ft < kQkvTiles; ++ft)
+          wf[ks][ft] = weight_frag<C>(p.w_qkv, p.packed, f0 / 16 + ft, ks, lane_i);
 
       layernorm_window<cpr, nthreads>(p, cur, xr, xn, s_gamma, s_beta, tid_i);
       __syncthreads();
@@ -405,11 +415,8 @@ __global__ __launch_bounds__(128 * kH) void swin_block_tile_kernel(const BlockPa
       // (issued before the next window's loads, so waiting for them never
       // waits for those)
       uint4 wp[kKS];
-      {
-        const uint16_t* prow = p.w_proj + (int64_t)(16 * wave + c16) * C + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < kKS; ++ks) wp[ks] = *reinterpret_cast<const uint4*>(prow + 32 * ks);
-      }
+      for (int ks = 0; ks < kKS; ++ks) wp[ks] = weight_frag<C>(p.w_proj, p.packed, wave, ks, lane_i);
       __syncthreads();  // q, k, v complete; xn is dead
       if (next < p.units) fetch_window<cpr, kWaves>(p, nxt, xn, wave, lane_i);
 
@@ -531,18 +538,15 @@ void swin_block_kernel(const BlockParams p) {
         }
       }
       {
-        const uint16_t* wq = p.w_qkv + (int64_t)(32 * h + c16) * C + 8 * g;
-        const uint16_t* wk = wq + (int64_t)C * C;
-        const uint16_t* wv = wq + (int64_t)2 * C * C;
         const int sw = (c16 >> 1) & 7;
 #pragma unroll 1
         for (int ks = 0; ks < kKS; ++ks) {
           uint4 fq[2], fk[2], fv[2], xf[4];
 #pragma unroll
           for (int dt = 0; dt < 2; ++dt) {
-            fq[dt] = *reinterpret_cast<const uint4*>(wq + 16 * dt * C + 32 * ks);
-            fk[dt] = *reinterpret_cast<const uint4*>(wk + 16 * dt * C + 32 * ks);
-            fv[dt] = *reinterpret_cast<const uint4*>(wv + 16 * dt * C + 32 * ks);
+            fq[dt] = weight_frag<C>(p.w_qkv, p.packed, 2 * h + dt, ks, lane_i);
+            fk[dt] = weight_frag<C>(p.w_qkv, p.packed, C / 16 + 2 * h + dt, ks, lane_i);
+            fv[dt] = weight_frag<C>(p.w_qkv, p.packed, C / 8 + 2 * h + dt, ks, lane_i);
           }
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
@@ -633,13 +637,12 @@ void swin_block_kernel(const BlockParams p) {
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt) ya[ft][tt] = bp;
         }
-        const uint16_t* wp = p.w_proj + (int64_t)(f0 + c16) * C + 8 * g;
         const int sw = (c16 >> 1) & 7;
 #pragma unroll 2
         for (int ks = 0; ks < kKS; ++ks) {
           uint4 fp[2], of[4];
 #pragma unroll
-          for (int ft = 0; ft < 2; ++ft) fp[ft] = *reinterpret_cast<const uint4*>(wp + 16 * ft * C + 32 * ks);
+          for (int ft = 0; ft < 2; ++ft) fp[ft] = weight_frag<C>(p.w_proj, p.packed, f0 / 16 + ft, ks, lane_i);
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
             of[tt] = *reinterpret_cast<const uint4*>(
@@ -712,6 +715,19 @@ int launch_block(const BlockParams& p, hipStream_t s) {
   }
 }
 
+// packed[(rt * K/32 + ks) * 64 + lane] (16 bytes) = w[16 rt + lane%16][32 ks
+// + 8 (lane/16) .. + 8]: one thread per 16-byte fragment chunk.
+__global__ __launch_bounds__(256) void pack_linear_kernel(const uint4* __restrict__ w, uint4* __restrict__ packed,
+                                                          uint32_t chunks, int k_chunks) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= chunks) return;
+  const uint32_t lane = i & 63u, blk = i >> 6;
+  const uint32_t ksteps = (uint32_t)k_chunks / 4u;
+  const uint32_t rt = blk / ksteps, ks = blk - rt * ksteps;
+  const uint32_t row = 16u * rt + (lane & 15u), col_chunk = 4u * ks + (lane >> 4);
+  packed[i] = w[(uint64_t)row * (uint32_t)k_chunks + col_chunk];
+}
+
 bool ranges_overlap(const void* a, const void* b, int64_t bytes) {
   const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
   return x < y + (uintptr_t)bytes && y < x + (uintptr_t)bytes;
@@ -782,6 +798,7 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   p.bias_table = bias_table;
   p.land_bits = land_bits;
   p.land_windows = land_bits != nullptr ? d.land_windows : 1;
+  p.packed = d.packed_weights != 0;
   p.layernorm = d.layernorm != 0;
   p.shift_mask = d.shift_mask != 0;
   p.eps = d.ln_eps;
@@ -809,5 +826,26 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   if (ls != TERRA_OK) return ls;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "block kernel launch failed: %s", hipGetErrorString(e));
+  return TERRA_OK;
+}
+
+extern "C" int terra_swin_pack_linear(const void* weight, void* packed, int dtype, int out_features,
+                                      int in_features, void* stream) {
+  clear_error();
+  if (weight == nullptr || packed == nullptr) return fail(TERRA_ERR_NULL, "weight and packed must be non-NULL");
+  if (dtype_size(dtype) == 0) return fail(TERRA_ERR_DTYPE, "unknown dtype %d", dtype);
+  if (dtype != TERRA_DTYPE_BF16) return fail(TERRA_ERR_UNSUPPORTED, "fragment packing is bf16 only");
+  if (out_features <= 0 || in_features <= 0 || out_features % 16 != 0 || in_features % 32 != 0)
+    return fail(TERRA_ERR_SHAPE, "weight [%d, %d] must be a multiple of [16, 32]", out_features, in_features);
+  if ((((uintptr_t)weight) & 15u) != 0 || (((uintptr_t)packed) & 15u) != 0)
+    return fail(TERRA_ERR_ALIGN, "weight and packed must be 16-byte aligned");
+  const int64_t bytes = (int64_t)out_features * in_features * 2;
+  if (bytes / 16 >= (1ll << 31)) return fail(TERRA_ERR_SHAPE, "weight too large");
+  if (ranges_overlap(weight, packed, bytes)) return fail(TERRA_ERR_SHAPE, "packed overlaps weight");
+  const uint32_t chunks = (uint32_t)(bytes / 16);
+  pack_linear_kernel<<<(chunks + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint4*>(weight), static_cast<uint4*>(packed), chunks, in_features / 8);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "pack launch failed: %s", hipGetErrorString(e));
   return TERRA_OK;
 }

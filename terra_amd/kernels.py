@@ -346,6 +346,22 @@ def swin_block_supported(x: torch.Tensor, geom: WindowGeometry, num_heads: int) 
             and num_heads in BLOCK_HEADS and geom.channels == 32 * num_heads)
 
 
+def pack_linear(weight: torch.Tensor) -> torch.Tensor:
+    """MFMA fragment order of a bf16 nn.Linear weight [out, in] (out % 16 == 0,
+    in % 32 == 0) for :func:`swin_block` with ``packed_weights=True``; returns
+    a flat tensor of the same number of elements."""
+    dev = _require_device(weight)
+    code = _dtype_code(weight, (torch.bfloat16,))
+    if weight.dim() != 2 or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous 2-D tensor")
+    n, k = weight.shape
+    out = torch.empty(n * k, dtype=weight.dtype, device=dev)
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_pack_linear(_ptr(weight), _ptr(out), code, int(n), int(k), _stream(dev))
+    _lib.check(st, "terra_swin_pack_linear")
+    return out
+
+
 def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: float,
                qkv_weight: torch.Tensor, qkv_bias: Optional[torch.Tensor],
                proj_weight: torch.Tensor, proj_bias: Optional[torch.Tensor],
@@ -353,7 +369,7 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
                ln_eps: float = 1e-5, layernorm: bool = True,
                bias_table: Optional[torch.Tensor] = None, shift_mask: bool = False,
                land_bits: Optional[torch.Tensor] = None, mask_value: float = MASK_VALUE,
-               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+               packed_weights: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused Swin attention half-block on ``x`` [B, H, W, C] (bf16):
 
         y = x + reverse(proj(attention(qkv(partition(LayerNorm(x))))))
@@ -363,7 +379,8 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
     parameters (LayerNorm affine, biases, bias table) are passed as fp32;
     weights in the activation dtype.  ``shift_mask`` enables the analytic
     shift mask of the padded frame; ``land_bits`` ([emitted windows per
-    image] int64) adds ``mask_value`` on land keys.  ``out`` may be ``x``.
+    image] int64) adds ``mask_value`` on land keys.  ``packed_weights``: the
+    two weights come from :func:`pack_linear` (flat).  ``out`` may be ``x``.
     """
     dev = _require_device(x, qkv_weight, proj_weight)
     code = _dtype_code(x, (torch.bfloat16,))
@@ -371,8 +388,10 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
     if tuple(x.shape) != (geom.batch, geom.height, geom.width, C) or not x.is_contiguous():
         raise ValueError(f"x must be a contiguous [{geom.batch}, {geom.height}, {geom.width}, {C}] tensor")
     for name, t, shape in (("qkv_weight", qkv_weight, (3 * C, C)), ("proj_weight", proj_weight, (C, C))):
-        if tuple(t.shape) != shape or t.dtype != x.dtype or not t.is_contiguous():
-            raise ValueError(f"{name} must be a contiguous {x.dtype} tensor of shape {shape}")
+        ok_shape = t.numel() == shape[0] * shape[1] if packed_weights else tuple(t.shape) == shape
+        if not ok_shape or t.dtype != x.dtype or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {x.dtype} tensor of shape {shape}"
+                             + (" (packed)" if packed_weights else ""))
 
     def f32(t, n, name):
         if t is None:
@@ -396,6 +415,7 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
     d.heads, d.scale, d.ln_eps, d.mask_value = num_heads, float(scale), float(ln_eps), float(mask_value)
     d.layernorm, d.shift_mask = int(bool(layernorm)), int(bool(shift_mask))
     d.land_windows = 0
+    d.packed_weights = int(bool(packed_weights))
     if land_bits is not None:
         _require_device(x, land_bits)
         if land_bits.dtype != torch.int64 or land_bits.dim() != 1:

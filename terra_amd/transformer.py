@@ -126,8 +126,9 @@ class SequentialSwinTransformer(torch.nn.Module):
         return all(l.weight.dtype == x.dtype for l in lins) and attn.q_linear.bias is not None
 
     def _fused_args(self) -> dict:
-        """Concatenated q/k/v weight and fp32 copies of the small parameters,
-        cached until any of them changes (data pointer or in-place version)."""
+        """Fragment-packed q|k|v and proj weights and fp32 copies of the small
+        parameters, cached until any of them changes (data pointer or in-place
+        version)."""
         attn = self.attn
         tensors = [attn.q_linear.weight, attn.k_linear.weight, attn.v_linear.weight, attn.q_linear.bias,
                    attn.k_linear.bias, attn.v_linear.bias, attn.proj.weight, attn.proj.bias]
@@ -141,11 +142,12 @@ class SequentialSwinTransformer(torch.nn.Module):
             return cached[1]
         with torch.no_grad():
             f32 = lambda t: None if t is None else t.detach().to(torch.float32).contiguous()  # noqa: E731
+            w_qkv = torch.cat([attn.q_linear.weight, attn.k_linear.weight, attn.v_linear.weight], 0).detach()
             args = dict(
-                qkv_weight=torch.cat([attn.q_linear.weight, attn.k_linear.weight, attn.v_linear.weight], 0)
-                .detach().contiguous(),
+                qkv_weight=kernels.pack_linear(w_qkv.contiguous()),
                 qkv_bias=f32(torch.cat([attn.q_linear.bias, attn.k_linear.bias, attn.v_linear.bias], 0)),
-                proj_weight=attn.proj.weight.detach().contiguous(),
+                proj_weight=kernels.pack_linear(attn.proj.weight.detach().contiguous()),
+                packed_weights=True,
                 proj_bias=f32(attn.proj.bias),
                 ln_weight=f32(self.norm1.weight) if config.use_layernorm else None,
                 ln_bias=f32(self.norm1.bias) if config.use_layernorm else None,

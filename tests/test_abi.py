@@ -37,7 +37,7 @@ def test_abi_version_and_struct_sizes():
     # every field of the C structs is 4 bytes wide
     assert ctypes.sizeof(L.SwinGeom) == 4 * len(L.SwinGeom._fields_) == 60
     assert ctypes.sizeof(L.SwinAttnDesc) == 4 * len(L.SwinAttnDesc._fields_) == 92
-    assert ctypes.sizeof(L.SwinBlockDesc) == 60 + 4 * (len(L.SwinBlockDesc._fields_) - 1) == 88
+    assert ctypes.sizeof(L.SwinBlockDesc) == 60 + 4 * (len(L.SwinBlockDesc._fields_) - 1) == 92
 
 
 def _geom(**kw):
@@ -213,3 +213,14 @@ def test_block_wrapper_raises_on_cpu_tensors():
     w = torch.zeros(576, 192, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         kernels.swin_block(x, kernels.WindowGeometry(1, 16, 16, 192, 8), 6, 0.17, w, None, w[:192], None)
+
+
+def test_pack_linear_rejects_bad_arguments():
+    lib = L.load()
+    assert lib.terra_swin_pack_linear(None, FAKE, L.DTYPE_BF16, 16, 32, None) == -1
+    assert lib.terra_swin_pack_linear(FAKE, FAKE, L.DTYPE_F32, 16, 32, None) == -5
+    assert lib.terra_swin_pack_linear(FAKE, FAKE, L.DTYPE_BF16, 24, 32, None) == -3
+    assert lib.terra_swin_pack_linear(FAKE, FAKE, L.DTYPE_BF16, 16, 48, None) == -3
+    assert lib.terra_swin_pack_linear(ctypes.c_void_p((1 << 20) + 2), ctypes.c_void_p(1 << 24), L.DTYPE_BF16,
+                                      16, 32, None) == -4
+    assert lib.terra_swin_pack_linear(FAKE, FAKE, L.DTYPE_BF16, 16, 32, None) == -3  # overlap

@@ -185,3 +185,31 @@ def test_fused_full_size_c3(dev):
     assert bool((d <= 2.0 ** -7 * y_u.float().abs() + 1e-2).all())
     ref = so.swin_block_attention(x, cfg.height, cfg.width, cfg.window, 4, cfg.heads, _params(blk), land=land)
     assert _rel(y_f, ref) <= 2e-2
+
+
+def test_pack_linear_layout(dev):
+    """packed[((rt*K/32 + ks)*64 + l)*8 + e] == w[16 rt + l%16][32 ks + 8 (l/16) + e], bit for bit."""
+    w = workloads.activations((96, 64), 420, torch.bfloat16)
+    got = kernels.pack_linear(w.to(dev)).cpu()
+    want = w.view(6, 16, 2, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
+    assert torch.equal(got, want)
+
+
+def test_fused_packed_equals_unpacked(dev):
+    """The weight layout changes only addresses: identical output bits."""
+    H, W, C, heads = 16, 32, 192, 6
+    blk = _block(dev, H, W, C, heads, 1, workloads.land_mask(H, W, seed=421))
+    x = workloads.activations((1, H, W, C), 422, torch.bfloat16).to(dev)
+    geom = blk.geometry(1)
+    mask = blk.window_mask(geom)
+    args = dict(blk._fused_args())
+    assert args.pop("packed_weights")
+    attn = blk.attn
+    plain = dict(args, qkv_weight=torch.cat([attn.q_linear.weight, attn.k_linear.weight,
+                                              attn.v_linear.weight], 0).contiguous(),
+                 proj_weight=attn.proj.weight.contiguous())
+    with torch.no_grad():
+        a = kernels.swin_block(x, geom, heads, attn.scale, shift_mask=True, land_bits=mask.land_bits,
+                               packed_weights=True, **args)
+        b = kernels.swin_block(x, geom, heads, attn.scale, shift_mask=True, land_bits=mask.land_bits, **plain)
+    assert torch.equal(a, b)
