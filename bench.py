@@ -266,7 +266,7 @@ def main():
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "swin_block_tile_kernel<6> (fused LN + qkv + window attention + proj + residual, gather/scatter)",
+            "kernel": "swin_block_pp_kernel<6> (fused LN + qkv + window attention + proj + residual, gather/scatter)",
             "bound": "mfma",
             "achieved": blk_tflops,
             "peak": MFMA_BF16_PEAK_TFLOPS,

@@ -468,5 +468,71 @@ __device__ __forceinline__ void tile_attention_wave(uint8_t* qs, const uint8_t* 
   }
 }
 
+// Scores, softmax and O^T = V^T P^T of one 16-query tile `it` of an 8x8
+// window against its 64 keys, for a Q operand that already carries
+// scale * log2(e).  The additive terms (relative-position bias at
+// tab8[30*(it - jt) - r + 93], land keys, shift regions, all x log2e) are the
+// accumulator init of the S^T MFMA, so the logits leave the MFMA ready for
+// the softmax.  kf[jt]: K operand of key tile jt; vfrag(ct, js): V^T operand
+// (keys 32js + 16(e/4) + 4g + e%4).  Returns the unnormalised O^T tiles and
+// 1/rowsum.
+template <class VFrag>
+__device__ __forceinline__ void attend_qtile(f32x4 (&o)[2], float& inv, int it, const uint4 (&kf)[4],
+                                             const uint4& qf, const float* tab8, const WindowMaskState& m,
+                                             uint64_t land_lane, uint64_t rid_pack, int rid_q, float mask_l2e,
+                                             VFrag vfrag) {
+  f32x4 s[4];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[jt][r] = tab8[30 * (it - jt) - r + 93];
+  if (m.use_shift) {
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rid_j = (int)((rid_pack >> (4 * (4 * jt + r))) & 15ull);
+        const bool land_j = (land_lane >> (16 * jt + r)) & 1ull;
+        s[jt][r] += (rid_j != rid_q ? mask_l2e : 0.f) + (land_j ? mask_l2e : 0.f);
+      }
+  } else if (m.land != 0ull) {
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[jt][r] += ((land_lane >> (16 * jt + r)) & 1ull) ? mask_l2e : 0.f;
+  }
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+    s[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt]), __builtin_bit_cast(bf16x8, qf),
+                                                    s[jt], 0, 0, 0);
+  float mx = s[0][0];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[jt][r]);
+  mx = xor_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e = __builtin_amdgcn_exp2f(s[jt][r] - mx);
+      s[jt][r] = e;
+      sum += e;
+    }
+  inv = __builtin_amdgcn_rcpf(xor_sum(sum));
+  o[0] = o[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int js = 0; js < 2; ++js) {
+    uint32_t wds[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2)
+      wds[e / 2] = pack_bf16x2(s[2 * js + (e >> 2)][e & 3], s[2 * js + (e >> 2)][(e & 3) + 1]);
+    const bf16x8 pf = __builtin_bit_cast(bf16x8, wds);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag(ct, js), pf, o[ct], 0, 0, 0);
+  }
+}
+
 }  // namespace
 }  // namespace terra

@@ -19,15 +19,7 @@
 // window is computed; they stay in LDS for the residual add and are
 // overwritten by the output rows, which are streamed back to the grid.
 //
-// swin_block_tile_kernel (6 heads, C = 192): one 12-wave workgroup per CU.
-//   Each wave loads its whole weight slice (48 q|k|v features, 16 proj
-//   features) into registers ahead of use, so the GEMM phases never wait on
-//   L2.  q|k|v go to LDS tiles; attention runs two waves per head (query
-//   halves) on those tiles; O overwrites Q and feeds the projection.  LDS:
-//   2 row tiles (raw / LayerNorm, roles alternating per window) + Q, K, V.
-//
-// swin_block_kernel (12 heads, C = 384; the tiles of the variant above do not
-// fit): one wave per head.  Wave h computes, for all 64 tokens,
+// One wave owns one head h of a window.  It computes, for all 64 tokens,
 //
 //   Q^T = W_q,h xn^T, K^T = W_k,h xn^T   (A = weight rows, B = xn rows)
 //   V   = xn W_v,h^T                     (A = xn rows,     B = weight rows)
@@ -38,8 +30,17 @@
 // S^T = K Q^T under the k-slot permutation (g, e) -> 16(e/4) + 4g + e%4 on
 // both sides; V's accumulators give the V^T operand of O^T = V^T P^T under
 // the key permutation that P^T inherits from the S^T accumulators.  So q, k
-// and v never leave registers.  Wave h then computes output features
-// [32h, 32h + 32) of the projection as Y^T = W_p O^T.
+// and v never leave registers.  O goes through LDS (all heads of a token are
+// the proj input), and wave h computes output features [32h, 32h + 32) of
+// the projection as Y^T = W_p O^T.
+//
+// swin_block_pp_kernel (6 heads, C = 192, the benchmark shape): two groups of
+// six such waves in one 12-wave workgroup per CU, each group on its own
+// window, one phase apart, so that MFMA phases of one group overlap VALU
+// phases of the other.
+//
+// swin_block_kernel (12 heads, C = 384): one group, one window at a time
+// (two groups' buffers do not fit LDS at this width).
 //
 // Windows that the frame does not emit (outside the slab's window rows, or
 // outside the valid-window range) pass x through unchanged, which is what
@@ -127,12 +128,12 @@ __device__ __forceinline__ f32x4 load_f32x4(const float* p) {
 // input channels [32*ks, 32*ks + 32) for this lane (row rt*16 + lane%16,
 // channels 32ks + 8*(lane/16) ..): strided rows of the nn.Linear layout, or
 // one contiguous 1 KB block per (rt, ks) in the packed layout.
-template <int kC>
-__device__ __forceinline__ uint4 weight_frag(const uint16_t* w, int packed, int rt, int ks, int lane) {
-  const uint4* src = packed ? reinterpret_cast<const uint4*>(w) + ((rt * (kC / 32) + ks) * 64 + lane)
-                            : reinterpret_cast<const uint4*>(w + (int64_t)(16 * rt + (lane & 15)) * kC + 32 * ks +
-                                                             8 * (lane >> 4));
-  return *src;
+template <int kC, bool kPacked>
+__device__ __forceinline__ uint4 weight_frag(const uint16_t* w, int rt, int ks, int lane) {
+  if constexpr (kPacked)
+    return reinterpret_cast<const uint4*>(w)[(rt * (kC / 32) + ks) * 64 + lane];
+  else
+    return *reinterpret_cast<const uint4*>(w + (int64_t)(16 * rt + (lane & 15)) * kC + 32 * ks + 8 * (lane >> 4));
 }
 
 // Cache-policy bits of the global -> LDS loads: nontemporal (every x byte is
@@ -177,71 +178,77 @@ __device__ __forceinline__ void fetch_window(const BlockParams& p, const UnitLoc
 
 // LayerNorm of the window rows xr -> xn (bf16).  Eight lanes own a token;
 // lane `sub` holds chunks sub + 8k, k < cpr/8.  Statistics are two-pass fp32
-// over the values in registers (reduced over the 8 lanes), y = (x - mean) *
-// rsqrt(var + eps) * gamma + beta rounded once: the arithmetic of
-// terra_swin_partition_ln.  Frame-padding tokens get zeros.  With
-// p.layernorm == 0 the rows are copied.
+// (reduced over the 8 lanes), y = (x - mean) * rsqrt(var + eps) * gamma + beta
+// rounded once, with the per-lane summation order of terra_swin_partition_ln.
+// The chunks are re-read from LDS for each pass instead of being held in
+// registers.  Frame-padding tokens get zeros.  With p.layernorm == 0 the rows
+// are copied.
 template <int kCpr, int kThreads>
 __device__ __forceinline__ void layernorm_window(const BlockParams& p, const UnitLoc u, const uint8_t* xr,
                                                  uint8_t* xn, const float* s_gamma, const float* s_beta, int tid) {
   constexpr int kTokPass = kThreads / 8;
   constexpr int kCPL = kCpr / 8;
   const int sub = tid & 7;
+  auto chunk = [&](int t, int k, float (&v)[8]) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
+    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
+      v[2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
+    }
+  };
   for (int t = tid >> 3; t < 64; t += kTokPass) {  // uniform per wave
     const bool in = grid_token(p, u, t >> 3, t & 7) >= 0;
-    float v[kCPL][8];
-#pragma unroll
-    for (int k = 0; k < kCPL; ++k) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
-      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[k][2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
-        v[k][2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
-      }
-    }
-    uint4 outc[kCPL];
-    if (p.layernorm) {
-      float sum = 0.f;
-#pragma unroll
-      for (int k = 0; k < kCPL; ++k)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sum += v[k][e];
-      const float mean = group8_sum(sum) * p.inv_c;
-      float sq = 0.f;
-#pragma unroll
-      for (int k = 0; k < kCPL; ++k)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float d = v[k][e] - mean;
-          sq += d * d;
-        }
-      const float rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+    if (!p.layernorm) {
 #pragma unroll
       for (int k = 0; k < kCPL; ++k) {
-        const int c0 = (sub + 8 * k) * 8;
-        float yv[8];
-#pragma unroll
-        for (int q = 0; q < 8; q += 4) {
-          const float4 gm = *reinterpret_cast<const float4*>(s_gamma + c0 + q);
-          const float4 bt = *reinterpret_cast<const float4*>(s_beta + c0 + q);
-          yv[q + 0] = (v[k][q + 0] - mean) * rstd * gm.x + bt.x;
-          yv[q + 1] = (v[k][q + 1] - mean) * rstd * gm.y + bt.y;
-          yv[q + 2] = (v[k][q + 2] - mean) * rstd * gm.z + bt.z;
-          yv[q + 3] = (v[k][q + 3] - mean) * rstd * gm.w + bt.w;
-        }
-        outc[k] = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]),
-                             pack_bf16x2(yv[4], yv[5]), pack_bf16x2(yv[6], yv[7]));
+        const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
+        *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) =
+            in ? raw : make_uint4(0u, 0u, 0u, 0u);
       }
-    } else {
-#pragma unroll
-      for (int k = 0; k < kCPL; ++k)
-        outc[k] = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
+      continue;
     }
+    float sum = 0.f;
 #pragma unroll
-    for (int k = 0; k < kCPL; ++k)
-      *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) =
-          in ? outc[k] : make_uint4(0u, 0u, 0u, 0u);
+    for (int k = 0; k < kCPL; ++k) {
+      float v[8];
+      chunk(t, k, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += v[e];
+    }
+    const float mean = group8_sum(sum) * p.inv_c;
+    float sq = 0.f;
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      float v[8];
+      chunk(t, k, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[e] - mean;
+        sq += d * d;
+      }
+    }
+    const float rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      float v[8];
+      chunk(t, k, v);
+      const int c0 = (sub + 8 * k) * 8;
+      float yv[8];
+#pragma unroll
+      for (int q = 0; q < 8; q += 4) {
+        const float4 gm = *reinterpret_cast<const float4*>(s_gamma + c0 + q);
+        const float4 bt = *reinterpret_cast<const float4*>(s_beta + c0 + q);
+        yv[q + 0] = (v[q + 0] - mean) * rstd * gm.x + bt.x;
+        yv[q + 1] = (v[q + 1] - mean) * rstd * gm.y + bt.y;
+        yv[q + 2] = (v[q + 2] - mean) * rstd * gm.z + bt.z;
+        yv[q + 3] = (v[q + 3] - mean) * rstd * gm.w + bt.w;
+      }
+      const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
+                                 pack_bf16x2(yv[6], yv[7]));
+      *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) = in ? o : make_uint4(0u, 0u, 0u, 0u);
+    }
   }
 }
 
@@ -295,176 +302,231 @@ __device__ __forceinline__ void stage_tables(const BlockParams& p, float* tabs, 
 }
 
 // ============================================================================
-// swin_block_tile_kernel: 6 heads (C = 192), 12 waves, one workgroup per CU
+// Per-head phases: one wave owns head h (features [32h, 32h + 32)) of a window
+// whose LayerNorm output is in `xn`.
 // ============================================================================
 
-template <int kH>
-constexpr int block_tile_lds_bytes() {
-  return 5 * 64 * 32 * kH * 2 + kH * kTableMax * 4 + 2 * 32 * kH * 4;
+// q, k, v of head h for the 64 tokens, straight into MFMA operand fragments:
+// kf4[jt] (K rows of key tile jt), vf[ct][js] (V^T operand), qf[it] (Q^T
+// operand, carrying scale * log2e).  The three projections run one after the
+// other (32 accumulators live) as one stream of 3 * C/32 k-steps whose weight
+// fragments flow through a ring kDepth steps deep, so each load has kDepth - 1
+// steps of MFMA work to arrive; the compiler barrier at each step keeps the
+// scheduler from hoisting further loads (register pressure).
+template <int C, bool kPacked>
+__device__ __forceinline__ void head_qkv(const BlockParams& p, const uint8_t* xn, int h, int lane, uint4 (&kf4)[4],
+                                         uint4 (&vf)[2][2], uint4 (&qf)[4]) {
+  constexpr int cpr = C / 8, kKS = C / 32;
+  constexpr int kSteps = 3 * kKS;
+  constexpr int kDepth = 3;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int sw = (c16 >> 1) & 7;
+  // Pass 0: K^T (rows = features), pass 1: V (rows = tokens), pass 2: Q^T.
+  auto row_tile0 = [&](int pass) { return pass == 0 ? C / 16 + 2 * h : (pass == 1 ? C / 8 + 2 * h : 2 * h); };
+  auto bias0 = [&](int pass) { return pass == 0 ? C + 32 * h : (pass == 1 ? 2 * C + 32 * h : 32 * h); };
+  // xn row address of token tile tt, k-step ks (tile_slot swizzle): the XOR
+  // only touches the low 3 bits, so even / odd k-steps share a base.
+  int xoff[2][4];
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) xoff[e][tt] = ((16 * tt + c16) * cpr + ((4 * e + g) ^ sw)) * 16;
+  auto xn_frag = [&](int tt, int ks) -> uint4 {
+    return *reinterpret_cast<const uint4*>(xn + xoff[ks & 1][tt] + (ks >> 1) * 128);
+  };
+  uint4 ring[kDepth][2];
+#pragma unroll
+  for (int st = 0; st < kDepth - 1; ++st)
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+      ring[st][dt] = weight_frag<C, kPacked>(p.w_qkv, row_tile0(st / kKS) + dt, st % kKS, lane);
+  uint4 xf[2][4];  // xn fragments of this and the next k-step
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) xf[0][tt] = xn_frag(tt, 0);
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const int pass = st / kKS, ks = st % kKS;
+    // Loads of later steps first (weights kDepth - 1 ahead, xn one ahead),
+    // then this step's MFMAs; the compiler barrier keeps further loads from
+    // being hoisted above this step (register pressure).
+    if (st + kDepth - 1 < kSteps) {
+      const int nst = st + kDepth - 1;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+        ring[nst % kDepth][dt] = weight_frag<C, kPacked>(p.w_qkv, row_tile0(nst / kKS) + dt, nst % kKS, lane);
+    }
+    if (st + 1 < kSteps) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) xf[(st + 1) & 1][tt] = xn_frag(tt, (st + 1) % kKS);
+    }
+    asm volatile("" ::: "memory");
+    if (ks == 0) {  // accumulators start at the bias
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        f32x4 b = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (p.b_qkv != nullptr) {
+          if (pass != 1) {
+            b = load_f32x4(p.b_qkv + bias0(pass) + 16 * dt + 4 * g);
+          } else {
+            const float bv = p.b_qkv[bias0(pass) + 16 * dt + c16];
+            b = f32x4{bv, bv, bv, bv};
+          }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc[dt][tt] = b;
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const bf16x8 x8 = __builtin_bit_cast(bf16x8, xf[st & 1][tt]);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const bf16x8 w8 = __builtin_bit_cast(bf16x8, ring[st % kDepth][dt]);
+        acc[dt][tt] = pass != 1 ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(w8, x8, acc[dt][tt], 0, 0, 0)
+                                : __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, w8, acc[dt][tt], 0, 0, 0);
+      }
+    }
+    if (ks == kKS - 1) {  // pass done: pack into operand fragments
+      if (pass == 0) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) kf4[tt] = pack_frag(acc[0][tt], acc[1][tt]);
+      } else if (pass == 1) {  // acc[ct][token tile]
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int js = 0; js < 2; ++js) vf[ct][js] = pack_frag(acc[ct][2 * js], acc[ct][2 * js + 1]);
+      } else {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) qf[tt] = pack_frag(acc[0][tt] * p.a.scale_l2e, acc[1][tt] * p.a.scale_l2e);
+      }
+    }
+  }
+  // Materialise the packed fragments here so that the fp32 accumulators die.
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    asm volatile("" : "+v"(kf4[tt].x), "+v"(kf4[tt].y), "+v"(kf4[tt].z), "+v"(kf4[tt].w));
+    asm volatile("" : "+v"(qf[tt].x), "+v"(qf[tt].y), "+v"(qf[tt].z), "+v"(qf[tt].w));
+  }
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int js = 0; js < 2; ++js)
+      asm volatile("" : "+v"(vf[ct][js].x), "+v"(vf[ct][js].y), "+v"(vf[ct][js].z), "+v"(vf[ct][js].w));
 }
 
-template <int kH>
-__global__ __launch_bounds__(128 * kH) void swin_block_tile_kernel(const BlockParams p) {
-  constexpr int C = 32 * kH;
+// Attention of head h from the register fragments, one query tile at a time;
+// O (bf16) goes to columns [32h, 32h + 32) of `o_tile`.
+template <int C>
+__device__ __forceinline__ void head_attention(const BlockParams& p, const UnitLoc cur, const float* tab, int h,
+                                               int lane, const uint4 (&kf4)[4], const uint4 (&vf)[2][2],
+                                               const uint4 (&qf)[4], uint8_t* o_tile) {
   constexpr int cpr = C / 8;
-  constexpr int kWaves = 2 * kH;
-  constexpr int nthreads = 64 * kWaves;
-  constexpr int tile = 64 * C * 2;
-  constexpr int kKS = C / 32;                      // 32-channel MFMA k-steps
-  constexpr int kQkvTiles = 3 * C / 16 / kWaves;   // 16-feature q|k|v tiles per wave
-  constexpr int kFeat = 16 * kQkvTiles;            // q|k|v features per wave
-  constexpr int kWavesPerTensor = C / kFeat;
-  static_assert(kQkvTiles * 16 * kWaves == 3 * C && kWavesPerTensor * kFeat == C, "q|k|v split");
-  static_assert(C / 16 == kWaves, "one 16-feature projection tile per wave");
-  static_assert(cpr % 8 == 0, "rows must be whole groups of 8 chunks (swizzle)");
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* xbuf = smem;                            // 2 row tiles: raw / LayerNorm, roles alternate
-  uint8_t* qs = smem + 2 * tile;                   // Q, later O
-  uint8_t* ks = smem + 3 * tile;
-  uint8_t* vs = smem + 4 * tile;
-  float* tabs = reinterpret_cast<float*>(smem + 5 * tile);
-  float* s_gamma = tabs + kH * kTableMax;
-  float* s_beta = s_gamma + C;
-
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-
-  int unit = blockIdx.x;
-  if (unit >= p.units) return;  // uniform across the workgroup
-  stage_tables<kH, nthreads>(p, tabs, s_gamma, s_beta, tid);
-
-  UnitLoc cur = locate(p, unit);
-  int par = 0;
-  fetch_window<cpr, kWaves>(p, cur, xbuf, wave, lane);
-
-  for (;;) {
-    // This window's rows have landed (nothing else is in flight); the
-    // barrier also orders the previous window's output reads before anything
-    // overwrites that tile.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    uint8_t* xr = xbuf + par * tile;        // raw rows, later the output rows
-    uint8_t* xn = xbuf + (par ^ 1) * tile;  // LayerNorm output, then the next window's rows
-    const int next = unit + (int)gridDim.x;
-    UnitLoc nxt = cur;
-    if (next < p.units) nxt = locate(p, next);
-
-    if (cur.computed) {  // uniform across the workgroup
-      // Lane-derived addresses are recomputed per window rather than held in
-      // registers across the persistent loop.
-      int lane_i = lane;
-      asm volatile("" : "+v"(lane_i));
-      const int g = lane_i >> 4, c16 = lane_i & 15;
-      const int tid_i = wave * 64 + lane_i;
-      const int sw = (c16 >> 1) & 7;  // tile_slot swizzle of rows 16t + c16
-
-      // ---- this wave's q|k|v weight rows [f0, f0 + kFeat), all k-steps ------
-      const int f0 = kFeat * wave;
-      uint4 wf[kKS][kQkvTiles];
+  const int g = lane >> 4, c16 = lane & 15;
+  const WindowMaskState m = block_mask_state(p, cur);
+  const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;  // in [93, 134]
+  const float* tab8 = tab + (lane_base - 93);
+  const uint64_t land_lane = m.land >> (4 * g);
+  uint64_t rid_pack = 0;
+  if (m.use_shift) {
 #pragma unroll
-      for (int ks = 0; ks < kKS; ++ks)
+    for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int ft = 0; ft < kQkvTiles; ++ft)
-          wf[ks][ft] = weight_frag<C>(p.w_qkv, p.packed, f0 / 16 + ft, ks, lane_i);
-
-      layernorm_window<cpr, nthreads>(p, cur, xr, xn, s_gamma, s_beta, tid_i);
-      __syncthreads();
-
-      // ---- q|k|v features [f0, f0 + kFeat) of the 64 tokens: Y^T = W xn^T --
-      {
-        f32x4 acc[kQkvTiles][4];
+      for (int r = 0; r < 4; ++r)
+        rid_pack |= (uint64_t)(3 * region(cur.wr * 8 + 2 * jt + (g >> 1), p.Hp, 8, p.shift_h) +
+                               region(cur.wc * 8 + 4 * (g & 1) + r, p.Wp, 8, p.shift_w))
+                    << (4 * (4 * jt + r));
+  }
+  auto vsrc = [&](int ct, int js) -> bf16x8 { return __builtin_bit_cast(bf16x8, vf[ct][js]); };
 #pragma unroll
-        for (int ft = 0; ft < kQkvTiles; ++ft) {
-          const f32x4 b = p.b_qkv != nullptr ? load_f32x4(p.b_qkv + f0 + 16 * ft + 4 * g)
-                                             : f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < 4; ++it) {
+    __builtin_amdgcn_sched_barrier(0);  // one query tile at a time (register pressure)
+    const int rid_q = m.use_shift ? 3 * region(cur.wr * 8 + 2 * it + (c16 >> 3), p.Hp, 8, p.shift_h) +
+                                        region(cur.wc * 8 + (c16 & 7), p.Wp, 8, p.shift_w)
+                                  : 0;
+    f32x4 o[2];
+    float inv;
+    attend_qtile(o, inv, it, kf4, qf[it], tab8, m, land_lane, rid_pack, rid_q, p.a.mask_l2e, vsrc);
+    const int i = 16 * it + c16;
 #pragma unroll
-          for (int tt = 0; tt < 4; ++tt) acc[ft][tt] = b;
-        }
-#pragma unroll
-        for (int ks = 0; ks < kKS; ++ks) {
-          uint4 xf[4];
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
-            xf[tt] = *reinterpret_cast<const uint4*>(xn + ((16 * tt + c16) * cpr + ((4 * ks + g) ^ sw)) * 16);
-#pragma unroll
-          for (int ft = 0; ft < kQkvTiles; ++ft)
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt)
-              acc[ft][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[ks][ft]),
-                                                                    __builtin_bit_cast(bf16x8, xf[tt]),
-                                                                    acc[ft][tt], 0, 0, 0);
-        }
-        // lane (c, g) element r: feature f0 + 16ft + 4g + r of token 16tt + c
-        const int tensor = wave / kWavesPerTensor;  // 0 q, 1 k, 2 v (wave-uniform)
-        uint8_t* dst = tensor == 0 ? qs : (tensor == 1 ? ks : vs);
-#pragma unroll
-        for (int ft = 0; ft < kQkvTiles; ++ft) {
-          const int fl = kFeat * (wave - tensor * kWavesPerTensor) + 16 * ft + 4 * g;
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt) {
-            uint2 pk;
-            pk.x = pack_bf16x2(acc[ft][tt][0], acc[ft][tt][1]);
-            pk.y = pack_bf16x2(acc[ft][tt][2], acc[ft][tt][3]);
-            *reinterpret_cast<uint2*>(dst + tile_slot(16 * tt + c16, fl >> 3, cpr) * 16 + (fl & 7) * 2) = pk;
-          }
-        }
-      }
-
-      // ---- this wave's proj weight rows [16w, 16w + 16), all k-steps ---------
-      // (issued before the next window's loads, so waiting for them never
-      // waits for those)
-      uint4 wp[kKS];
-#pragma unroll
-      for (int ks = 0; ks < kKS; ++ks) wp[ks] = weight_frag<C>(p.w_proj, p.packed, wave, ks, lane_i);
-      __syncthreads();  // q, k, v complete; xn is dead
-      if (next < p.units) fetch_window<cpr, kWaves>(p, nxt, xn, wave, lane_i);
-
-      // ---- attention: head wave/2, query half wave%2; O over Q ---------------
-      {
-        const int head = wave >> 1;
-        const WindowMaskState m = block_mask_state(p, cur);
-        tile_attention_wave<32, cpr>(qs, ks, vs, head, wave & 1, p.a, m, tabs + head * kTableMax, lane_i);
-      }
-      __syncthreads();  // O complete
-
-      // ---- proj features [16w, 16w + 16) + residual, in place over xr ----------
-      {
-        f32x4 acc[4];
-        const f32x4 b = p.b_proj != nullptr ? load_f32x4(p.b_proj + 16 * wave + 4 * g)
-                                            : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) acc[tt] = b;
-#pragma unroll
-        for (int ks = 0; ks < kKS; ++ks) {
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt) {
-            const uint4 of =
-                *reinterpret_cast<const uint4*>(qs + ((16 * tt + c16) * cpr + ((4 * ks + g) ^ sw)) * 16);
-            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wp[ks]),
-                                                              __builtin_bit_cast(bf16x8, of), acc[tt], 0, 0, 0);
-          }
-        }
-        const int fb = 16 * wave + 4 * g;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          residual_add4(xr + tile_slot(16 * tt + c16, fb >> 3, cpr) * 16 + (fb & 7) * 2, acc[tt]);
-      }
-      __syncthreads();  // output rows complete in xr
-    } else if (next < p.units) {
-      fetch_window<cpr, kWaves>(p, nxt, xn, wave, lane);
+    for (int ct = 0; ct < 2; ++ct) {
+      const f32x4 v = o[ct] * inv;
+      const int cc = 32 * h + 16 * ct + 4 * g;
+      uint2 pk;
+      pk.x = pack_bf16x2(v[0], v[1]);
+      pk.y = pack_bf16x2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(o_tile + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
     }
+  }
+}
 
-    store_window<cpr, nthreads>(p, cur, xr, tid);
-    if (next >= p.units) break;
-    unit = next;
-    cur = nxt;
-    par ^= 1;
+// Output features [32h, 32h + 32) = O W_p^T + b_p for the 64 tokens
+// (Y^T = W_p O^T), rounded to bf16 and added to the raw rows in `xr`.
+template <int C, bool kPacked>
+__device__ __forceinline__ void head_proj(const BlockParams& p, const uint8_t* o_tile, uint8_t* xr, int h,
+                                          int lane) {
+  constexpr int cpr = C / 8, kKS = C / 32;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int sw = (c16 >> 1) & 7;
+  const int f0 = 32 * h;
+  f32x4 ya[2][4];
+#pragma unroll
+  for (int ft = 0; ft < 2; ++ft) {
+    const f32x4 bp = p.b_proj != nullptr ? load_f32x4(p.b_proj + f0 + 16 * ft + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) ya[ft][tt] = bp;
+  }
+  constexpr int kDepth = 4;
+  int ooff[2][4];
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) ooff[e][tt] = ((16 * tt + c16) * cpr + ((4 * e + g) ^ sw)) * 16;
+  auto o_frag = [&](int tt, int ks) -> uint4 {
+    return *reinterpret_cast<const uint4*>(o_tile + ooff[ks & 1][tt] + (ks >> 1) * 128);
+  };
+  uint4 fp[kDepth][2];  // [ring slot][ft]
+#pragma unroll
+  for (int st = 0; st < kDepth - 1 && st < kKS; ++st)
+#pragma unroll
+    for (int ft = 0; ft < 2; ++ft) fp[st][ft] = weight_frag<C, kPacked>(p.w_proj, f0 / 16 + ft, st, lane);
+  uint4 of[2][4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) of[0][tt] = o_frag(tt, 0);
+#pragma unroll
+  for (int ks = 0; ks < kKS; ++ks) {
+    if (ks + kDepth - 1 < kKS) {
+#pragma unroll
+      for (int ft = 0; ft < 2; ++ft)
+        fp[(ks + kDepth - 1) % kDepth][ft] = weight_frag<C, kPacked>(p.w_proj, f0 / 16 + ft, ks + kDepth - 1, lane);
+    }
+    if (ks + 1 < kKS) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) of[(ks + 1) & 1][tt] = o_frag(tt, ks + 1);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+      for (int ft = 0; ft < 2; ++ft)
+        ya[ft][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fp[ks % kDepth][ft]),
+                                                             __builtin_bit_cast(bf16x8, of[ks & 1][tt]), ya[ft][tt],
+                                                             0, 0, 0);
+    }
+  }
+  // Y^T lane (c, g) element r: feature f0 + 16ft + 4g + r of token 16tt + c.
+#pragma unroll
+  for (int ft = 0; ft < 2; ++ft) {
+    const int fb = f0 + 16 * ft + 4 * g;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+      residual_add4(xr + tile_slot(16 * tt + c16, fb >> 3, cpr) * 16 + (fb & 7) * 2, ya[ft][tt]);
   }
 }
 
 // ============================================================================
-// swin_block_kernel: one wave per head (12 heads, C = 384)
+// swin_block_kernel: one wave per head, one window at a time (12 heads,
+// C = 384, whose doubled buffers of the variant below do not fit LDS)
 // ============================================================================
 
 template <int kH>
@@ -472,14 +534,13 @@ constexpr int block_lds_bytes() {
   return 3 * 64 * 32 * kH * 2 + kH * kTableMax * 4 + 2 * 32 * kH * 4;
 }
 
-template <int kH>
+template <int kH, bool kPacked>
 __global__ __launch_bounds__(64 * kH) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void swin_block_kernel(const BlockParams p) {
   constexpr int C = 32 * kH;
   constexpr int cpr = C / 8;                 // 16-byte chunks per token row
   constexpr int nthreads = 64 * kH;
   constexpr int tile = 64 * C * 2;
-  constexpr int kKS = C / 32;                // 32-channel MFMA k-steps
   static_assert(cpr % 8 == 0, "rows must be whole groups of 8 chunks (swizzle)");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* xbuf = smem;                      // 2 x [64][C]: raw rows of this and the next window
@@ -511,171 +572,135 @@ void swin_block_kernel(const BlockParams p) {
     const int next = unit + (int)gridDim.x;
     UnitLoc nxt = cur;
     if (next < p.units) nxt = locate(p, next);
+    // Lane-derived addresses are recomputed per window rather than held in
+    // registers across the persistent loop.
+    int lane_i = lane;
+    asm volatile("" : "+v"(lane_i));
+    const int tid_i = wave * 64 + lane_i;
 
     if (cur.computed) {  // uniform across the workgroup
-      // Lane-derived addresses are recomputed per window rather than held in
-      // registers across the persistent loop.
-      int lane_i = lane;
-      asm volatile("" : "+v"(lane_i));
-      const int g = lane_i >> 4, c16 = lane_i & 15;
-      const int tid_i = wave * 64 + lane_i;
       layernorm_window<cpr, nthreads>(p, cur, xr, xn, s_gamma, s_beta, tid_i);
       __syncthreads();
-      // ---- q, k, v of head `wave` for the 64 tokens ------------------------
-      const int h = wave;
-      f32x4 qa[2][4], ka[2][4], va[4][2];
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        const int fq = 32 * h + 16 * dt + 4 * g;
-        const f32x4 bq = p.b_qkv != nullptr ? load_f32x4(p.b_qkv + fq) : f32x4{0.f, 0.f, 0.f, 0.f};
-        const f32x4 bk = p.b_qkv != nullptr ? load_f32x4(p.b_qkv + C + fq) : f32x4{0.f, 0.f, 0.f, 0.f};
-        const float bv = p.b_qkv != nullptr ? p.b_qkv[2 * C + 32 * h + 16 * dt + c16] : 0.f;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          qa[dt][tt] = bq;
-          ka[dt][tt] = bk;
-          va[tt][dt] = f32x4{bv, bv, bv, bv};
-        }
-      }
-      {
-        const int sw = (c16 >> 1) & 7;
-#pragma unroll 1
-        for (int ks = 0; ks < kKS; ++ks) {
-          uint4 fq[2], fk[2], fv[2], xf[4];
-#pragma unroll
-          for (int dt = 0; dt < 2; ++dt) {
-            fq[dt] = weight_frag<C>(p.w_qkv, p.packed, 2 * h + dt, ks, lane_i);
-            fk[dt] = weight_frag<C>(p.w_qkv, p.packed, C / 16 + 2 * h + dt, ks, lane_i);
-            fv[dt] = weight_frag<C>(p.w_qkv, p.packed, C / 8 + 2 * h + dt, ks, lane_i);
-          }
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
-            xf[tt] = *reinterpret_cast<const uint4*>(
-                xn + ((16 * tt + c16) * cpr + ((4 * ks + g) ^ sw)) * 16);
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt) {
-            const bf16x8 x8 = __builtin_bit_cast(bf16x8, xf[tt]);
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt) {
-              qa[dt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fq[dt]), x8,
-                                                                   qa[dt][tt], 0, 0, 0);
-              ka[dt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fk[dt]), x8,
-                                                                   ka[dt][tt], 0, 0, 0);
-              va[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, __builtin_bit_cast(bf16x8, fv[dt]),
-                                                                   va[tt][dt], 0, 0, 0);
-            }
-          }
-        }
-      }
+      uint4 kf4[4], vf[2][2], qf[4];
+      head_qkv<C, kPacked>(p, xn, wave, lane_i, kf4, vf, qf);
       // Next window's rows stream in behind the q/k/v loads (the attention
       // phase issues no vector-memory loads of its own).
       if (next < p.units) fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane_i);
-      uint4 kf[4][1], qf[4];
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        kf[tt][0] = pack_frag(ka[0][tt], ka[1][tt]);
-        qf[tt] = pack_frag(qa[0][tt], qa[1][tt]);
-      }
-      uint4 vf[2][2];  // [ct][js]
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int js = 0; js < 2; ++js) vf[ct][js] = pack_frag(va[2 * js][ct], va[2 * js + 1][ct]);
-      // Materialise the packed fragments here so that the fp32 accumulators die.
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        asm volatile("" : "+v"(kf[tt][0].x), "+v"(kf[tt][0].y), "+v"(kf[tt][0].z), "+v"(kf[tt][0].w));
-        asm volatile("" : "+v"(qf[tt].x), "+v"(qf[tt].y), "+v"(qf[tt].z), "+v"(qf[tt].w));
-      }
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int js = 0; js < 2; ++js)
-          asm volatile("" : "+v"(vf[ct][js].x), "+v"(vf[ct][js].y), "+v"(vf[ct][js].z), "+v"(vf[ct][js].w));
       __syncthreads();  // every wave has read xn; O overwrites it
-
-      // ---- attention of head h ----------------------------------------------
-      {
-        const WindowMaskState m = block_mask_state(p, cur);
-        LaneGeom<true> lg;
-        lane_geom_init<true>(lg, p.a, m, tabs + h * kTableMax, lane);
-        auto vsrc = [&](int ct, int js) -> bf16x8 { return __builtin_bit_cast(bf16x8, vf[ct][js]); };
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const uint4 qp[2][1] = {{qf[2 * half]}, {qf[2 * half + 1]}};
-          f32x4 s[2][4];
-          scores_pair<true, 32>(s, kf, qp);
-          float inv[2];
-          softmax_half<true, false>(s, inv, half, p.a, m, lg, nullptr, lane);
-          f32x4 o[2][2];
-          pv_half<true, 32>(o, s, lane, vsrc);
-#pragma unroll
-          for (int il = 0; il < 2; ++il) {
-            const int i = 16 * (2 * half + il) + c16;
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-              const f32x4 v = o[ct][il] * inv[il];
-              const int cc = 32 * h + 16 * ct + 4 * g;
-              uint2 pk;
-              pk.x = pack_bf16x2(v[0], v[1]);
-              pk.y = pack_bf16x2(v[2], v[3]);
-              *reinterpret_cast<uint2*>(xn + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
-            }
-          }
-        }
-      }
+      head_attention<C>(p, cur, tabs + wave * kTableMax, wave, lane_i, kf4, vf, qf, xn);
       __syncthreads();  // O complete
-
-      // ---- projection features [32h, 32h+32) + residual ----------------------
-      {
-        const int f0 = 32 * h;
-        f32x4 ya[2][4];
-#pragma unroll
-        for (int ft = 0; ft < 2; ++ft) {
-          const f32x4 bp = p.b_proj != nullptr ? load_f32x4(p.b_proj + f0 + 16 * ft + 4 * g)
-                                               : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt) ya[ft][tt] = bp;
-        }
-        const int sw = (c16 >> 1) & 7;
-#pragma unroll 2
-        for (int ks = 0; ks < kKS; ++ks) {
-          uint4 fp[2], of[4];
-#pragma unroll
-          for (int ft = 0; ft < 2; ++ft) fp[ft] = weight_frag<C>(p.w_proj, p.packed, f0 / 16 + ft, ks, lane_i);
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
-            of[tt] = *reinterpret_cast<const uint4*>(
-                xn + ((16 * tt + c16) * cpr + ((4 * ks + g) ^ sw)) * 16);
-#pragma unroll
-          for (int ft = 0; ft < 2; ++ft)
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt)
-              ya[ft][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fp[ft]),
-                                                                   __builtin_bit_cast(bf16x8, of[tt]),
-                                                                   ya[ft][tt], 0, 0, 0);
-        }
-        // Y^T lane (c, g) element r: feature f0 + 16ft + 4g + r of token 16tt + c.
-#pragma unroll
-        for (int ft = 0; ft < 2; ++ft) {
-          const int fb = f0 + 16 * ft + 4 * g;
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt) {
-            residual_add4(xr + tile_slot(16 * tt + c16, fb >> 3, cpr) * 16 + (fb & 7) * 2, ya[ft][tt]);
-          }
-        }
-      }
+      head_proj<C, kPacked>(p, xn, xr, wave, lane_i);
       __syncthreads();  // output rows complete in xr
     } else if (next < p.units) {
-      fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane);
+      fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane_i);
     }
 
-
-    store_window<cpr, nthreads>(p, cur, xr, tid);
+    store_window<cpr, nthreads>(p, cur, xr, tid_i);
     if (next >= p.units) break;
     unit = next;
     cur = nxt;
     par ^= 1;
+  }
+}
+
+// ============================================================================
+// swin_block_pp_kernel: two groups of one-wave-per-head, two windows in
+// flight (6 heads, C = 192; 12 waves, one workgroup per CU)
+// ============================================================================
+//
+// Group g (waves [6g, 6g + 6)) takes the workgroup's windows 2k + g.  A
+// window passes through four phases separated by workgroup barriers:
+//
+//   A  store the previous window's output rows; LayerNorm      (VALU, LDS)
+//   B  q, k, v into registers; issue the next window's rows    (MFMA)
+//   C  attention, O -> LDS                                     (VALU, exp)
+//   D  proj + residual into the raw rows                       (MFMA)
+//
+// Group 1 runs one phase behind group 0, so every barrier interval pairs an
+// MFMA phase of one group with a VALU phase of the other, and each SIMD
+// (which holds waves of both groups) overlaps them.  Per group LDS: two row
+// buffers (window k's raw rows, later its output; the other receives window
+// k + 1 during phase B) and one LayerNorm / O tile.
+
+template <int kH>
+constexpr int block_pp_lds_bytes() {
+  return 6 * 64 * 32 * kH * 2 + kH * kTableMax * 4 + 2 * 32 * kH * 4;
+}
+
+template <int kH, bool kPacked>
+__global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockParams p) {
+  constexpr int C = 32 * kH;
+  constexpr int cpr = C / 8;
+  constexpr int tile = 64 * C * 2;
+  constexpr int kGroupThreads = 64 * kH;
+  static_assert(cpr % 8 == 0, "rows must be whole groups of 8 chunks (swizzle)");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  float* tabs = reinterpret_cast<float*>(smem + 6 * tile);
+  float* s_gamma = tabs + kH * kTableMax;
+  float* s_beta = s_gamma + C;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int grp = wave >= kH ? 1 : 0;
+  const int h = wave - grp * kH;  // this wave's head
+  uint8_t* gbuf = smem + grp * 3 * tile;
+  uint8_t* xn = gbuf + 2 * tile;
+
+  if ((int)blockIdx.x >= p.units) return;  // uniform across the workgroup
+  stage_tables<kH, 2 * kGroupThreads>(p, tabs, s_gamma, s_beta, tid);
+
+  // Windows of group g: unit blockIdx.x + (2k + g) * gridDim.x, k < count[g].
+  const int stride = 2 * (int)gridDim.x;
+  const int first0 = blockIdx.x, first1 = blockIdx.x + gridDim.x;
+  const int n0 = first0 < p.units ? (p.units - 1 - first0) / stride + 1 : 0;
+  const int n1 = first1 < p.units ? (p.units - 1 - first1) / stride + 1 : 0;
+  const int n_mine = grp ? n1 : n0;
+  const int first_mine = grp ? first1 : first0;
+  // Group g ends with the store of its last window, in phase A of cycle n_g
+  // (slot g + 4 n_g).
+  const int slots = (4 * n0 + 1) > (4 * n1 + 2) ? (4 * n0 + 1) : (4 * n1 + 2);
+
+  if (n_mine > 0) fetch_window<cpr, kH>(p, locate(p, first_mine), gbuf, h, lane);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  uint4 kf4[4], vf[2][2], qf[4];  // phase B -> phase C
+  for (int t = 0; t < slots; ++t) {
+    const int q = t - grp;  // group-local slot
+    // Lane-derived addresses are recomputed per slot rather than held in
+    // registers across the loop.
+    int lane_i = lane;
+    asm volatile("" : "+v"(lane_i));
+    if (q >= 0) {
+      const int k = q >> 2, ph = q & 3;
+      const bool have = k < n_mine;
+      const UnitLoc cur = locate(p, first_mine + k * stride);
+      uint8_t* xr = gbuf + (k & 1) * tile;
+      if (ph == 0) {
+        if (k >= 1) store_window<cpr, kGroupThreads>(p, locate(p, first_mine + (k - 1) * stride),
+                                                     gbuf + ((k - 1) & 1) * tile, h * 64 + lane_i);
+        if (have && cur.computed)
+          layernorm_window<cpr, kGroupThreads>(p, cur, xr, xn, s_gamma, s_beta, h * 64 + lane_i);
+      } else if (ph == 1) {
+        if (have) {
+          if (cur.computed) head_qkv<C, kPacked>(p, xn, h, lane_i, kf4, vf, qf);
+          // The next window's rows, behind the q/k/v loads; the buffer's last
+          // reader was phase A's store.
+          if (k + 1 < n_mine)
+            fetch_window<cpr, kH>(p, locate(p, first_mine + (k + 1) * stride), gbuf + ((k + 1) & 1) * tile, h,
+                                  lane_i);
+        }
+      } else if (ph == 2) {
+        if (have && cur.computed)
+          head_attention<C>(p, cur, tabs + h * kTableMax, h, lane_i, kf4, vf, qf, xn);
+      } else {
+        if (have && cur.computed) head_proj<C, kPacked>(p, xn, xr, h, lane_i);
+        // The next window's rows have landed before phase A reads them.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -697,22 +722,28 @@ int launch_persistent(K kernel, int threads, int lds, int units, const BlockPara
 }
 
 // The >64 KiB dynamic-LDS opt-in is a per-kernel attribute: set once each.
-template <int kH>
-int launch_block(const BlockParams& p, hipStream_t s) {
+template <int kH, bool kPacked>
+int launch_block_layout(const BlockParams& p, hipStream_t s) {
   static int resident[64] = {0};
   if constexpr (kH == 6) {
-    constexpr int lds = block_tile_lds_bytes<kH>();
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&swin_block_tile_kernel<kH>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    constexpr int lds = block_pp_lds_bytes<kH>();
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&swin_block_pp_kernel<kH, kPacked>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
-    return launch_persistent(swin_block_tile_kernel<kH>, 128 * kH, lds, p.units, p, s, resident);
+    return launch_persistent(swin_block_pp_kernel<kH, kPacked>, 128 * kH, lds, p.units, p, s, resident);
   } else {
     constexpr int lds = block_lds_bytes<kH>();
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&swin_block_kernel<kH>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&swin_block_kernel<kH, kPacked>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
-    return launch_persistent(swin_block_kernel<kH>, 64 * kH, lds, p.units, p, s, resident);
+    return launch_persistent(swin_block_kernel<kH, kPacked>, 64 * kH, lds, p.units, p, s, resident);
   }
+}
+
+template <int kH>
+int launch_block(const BlockParams& p, hipStream_t s) {
+  return p.packed ? launch_block_layout<kH, true>(p, s) : launch_block_layout<kH, false>(p, s);
 }
 
 // packed[(rt * K/32 + ks) * 64 + lane] (16 bytes) = w[16 rt + lane%16][32 ks
