@@ -473,14 +473,14 @@ __device__ __forceinline__ void tile_attention_wave(uint8_t* qs, const uint8_t* 
 // scale * log2(e).  The additive terms (relative-position bias at
 // tab8[30*(it - jt) - r + 93], land keys, shift regions, all x log2e) are the
 // accumulator init of the S^T MFMA, so the logits leave the MFMA ready for
-// the softmax.  kf[jt]: K operand of key tile jt; vfrag(ct, js): V^T operand
-// (keys 32js + 16(e/4) + 4g + e%4).  Returns the unnormalised O^T tiles and
-// 1/rowsum.
+// the softmax.  land_term[jt][r]: mask_l2e for land key 16jt + 4g + r, else 0.
+// kf[jt]: K operand of key tile jt; vfrag(ct, js): V^T operand (keys 32js +
+// 16(e/4) + 4g + e%4).  Returns the unnormalised O^T tiles and 1/rowsum.
 template <class VFrag>
 __device__ __forceinline__ void attend_qtile(f32x4 (&o)[2], float& inv, int it, const uint4 (&kf)[4],
                                              const uint4& qf, const float* tab8, const WindowMaskState& m,
-                                             uint64_t land_lane, uint64_t rid_pack, int rid_q, float mask_l2e,
-                                             VFrag vfrag) {
+                                             const f32x4 (&land_term)[4], uint64_t rid_pack, int rid_q,
+                                             float mask_l2e, VFrag vfrag) {
   f32x4 s[4];
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
@@ -492,14 +492,11 @@ __device__ __forceinline__ void attend_qtile(f32x4 (&o)[2], float& inv, int it, 
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int rid_j = (int)((rid_pack >> (4 * (4 * jt + r))) & 15ull);
-        const bool land_j = (land_lane >> (16 * jt + r)) & 1ull;
-        s[jt][r] += (rid_j != rid_q ? mask_l2e : 0.f) + (land_j ? mask_l2e : 0.f);
+        s[jt][r] += (rid_j != rid_q ? mask_l2e : 0.f) + land_term[jt][r];
       }
   } else if (m.land != 0ull) {
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[jt][r] += ((land_lane >> (16 * jt + r)) & 1ull) ? mask_l2e : 0.f;
+    for (int jt = 0; jt < 4; ++jt) s[jt] += land_term[jt];
   }
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)

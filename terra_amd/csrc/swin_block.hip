@@ -180,8 +180,7 @@ __device__ __forceinline__ void fetch_window(const BlockParams& p, const UnitLoc
 // lane `sub` holds chunks sub + 8k, k < cpr/8.  Statistics are two-pass fp32
 // (reduced over the 8 lanes), y = (x - mean) * rsqrt(var + eps) * gamma + beta
 // rounded once, with the per-lane summation order of terra_swin_partition_ln.
-// The chunks are re-read from LDS for each pass instead of being held in
-// registers.  Frame-padding tokens get zeros.  With p.layernorm == 0 the rows
+// Frame-padding tokens get zeros.  With p.layernorm == 0 the rows
 // are copied.
 template <int kCpr, int kThreads>
 __device__ __forceinline__ void layernorm_window(const BlockParams& p, const UnitLoc u, const uint8_t* xr,
@@ -209,11 +208,27 @@ __device__ __forceinline__ void layernorm_window(const BlockParams& p, const Uni
       }
       continue;
     }
+    // Narrow rows (<= 3 chunks per lane) keep their values in registers;
+    // wider rows re-read LDS for each pass.  Same arithmetic either way.
+    constexpr bool kHold = kCPL <= 3;
+    float vh[kHold ? kCPL : 1][8];
+    if constexpr (kHold) {
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k) chunk(t, k, vh[k]);
+    }
+    auto values = [&](int k, float (&v)[8]) {
+      if constexpr (kHold) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = vh[k][e];
+      } else {
+        chunk(t, k, v);
+      }
+    };
     float sum = 0.f;
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
       float v[8];
-      chunk(t, k, v);
+      values(k, v);
 #pragma unroll
       for (int e = 0; e < 8; ++e) sum += v[e];
     }
@@ -222,7 +237,7 @@ __device__ __forceinline__ void layernorm_window(const BlockParams& p, const Uni
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
       float v[8];
-      chunk(t, k, v);
+      values(k, v);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float d = v[e] - mean;
@@ -233,7 +248,7 @@ __device__ __forceinline__ void layernorm_window(const BlockParams& p, const Uni
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
       float v[8];
-      chunk(t, k, v);
+      values(k, v);
       const int c0 = (sub + 8 * k) * 8;
       float yv[8];
 #pragma unroll
@@ -318,7 +333,7 @@ __device__ __forceinline__ void head_qkv(const BlockParams& p, const uint8_t* xn
                                          uint4 (&vf)[2][2], uint4 (&qf)[4]) {
   constexpr int cpr = C / 8, kKS = C / 32;
   constexpr int kSteps = 3 * kKS;
-  constexpr int kDepth = 3;
+  constexpr int kDepth = C <= 192 ? 3 : 2;  // weight ring depth (registers)
   const int g = lane >> 4, c16 = lane & 15;
   const int sw = (c16 >> 1) & 7;
   // Pass 0: K^T (rows = features), pass 1: V (rows = tokens), pass 2: Q^T.
@@ -427,6 +442,11 @@ __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitL
   const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;  // in [93, 134]
   const float* tab8 = tab + (lane_base - 93);
   const uint64_t land_lane = m.land >> (4 * g);
+  f32x4 land_term[4];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) land_term[jt][r] = ((land_lane >> (16 * jt + r)) & 1ull) ? p.a.mask_l2e : 0.f;
   uint64_t rid_pack = 0;
   if (m.use_shift) {
 #pragma unroll
@@ -446,7 +466,7 @@ __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitL
                                   : 0;
     f32x4 o[2];
     float inv;
-    attend_qtile(o, inv, it, kf4, qf[it], tab8, m, land_lane, rid_pack, rid_q, p.a.mask_l2e, vsrc);
+    attend_qtile(o, inv, it, kf4, qf[it], tab8, m, land_term, rid_pack, rid_q, p.a.mask_l2e, vsrc);
     const int i = 16 * it + c16;
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
@@ -476,7 +496,7 @@ __device__ __forceinline__ void head_proj(const BlockParams& p, const uint8_t* o
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) ya[ft][tt] = bp;
   }
-  constexpr int kDepth = 4;
+  constexpr int kDepth = C <= 192 ? 4 : 2;  // weight ring depth (registers)
   int ooff[2][4];
 #pragma unroll
   for (int e = 0; e < 2; ++e)
