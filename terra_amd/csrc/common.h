@@ -71,6 +71,52 @@ __device__ __forceinline__ float group8_sum(float v) {
   return v + __shfl_xor(v, 4);
 }
 
+// ---- streaming stores ------------------------------------------------------
+// Output streams are written through buffer stores carrying the sc1 cache-
+// policy bit.  Measured on MI355X (201 MB arrays, 16-byte accesses):
+// nontemporal loads + sc1 stores copy at 7.2 TB/s, against 6.0-6.4 TB/s with
+// nontemporal stores and 5.6-5.8 TB/s with plain ones; a 3-read/1-write
+// stream goes from 6.5 to 7.2 TB/s.  The buffer descriptor also bounds every
+// store to [base, base + bytes): out-of-range lanes are dropped by the
+// hardware.
+constexpr int kCacheNt = 2;    // nt: streaming (loads)
+constexpr int kCacheSc1 = 16;  // sc1 (stores)
+constexpr int kBufferWord3 = 0x00020000;  // raw 32-bit records, gfx950
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferWord3);
+}
+
+typedef uint32_t stream_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t stream_u32x2 __attribute__((ext_vector_type(2)));
+
+// Stores `v` at byte offset `off` of the descriptor's range.
+template <typename T>
+__device__ __forceinline__ void stream_store_sc1(T v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(T) == 16) {
+    stream_u32x4 w;
+    __builtin_memcpy(&w, &v, 16);
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, kCacheSc1);
+  } else if constexpr (sizeof(T) == 8) {
+    stream_u32x2 w;
+    __builtin_memcpy(&w, &v, 8);
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, off, 0, kCacheSc1);
+  } else if constexpr (sizeof(T) == 4) {
+    uint32_t w;
+    __builtin_memcpy(&w, &v, 4);
+    __builtin_amdgcn_raw_buffer_store_b32(w, r, off, 0, kCacheSc1);
+  } else if constexpr (sizeof(T) == 2) {
+    uint16_t w;
+    __builtin_memcpy(&w, &v, 2);
+    __builtin_amdgcn_raw_buffer_store_b16(w, r, off, 0, kCacheSc1);
+  } else {
+    static_assert(sizeof(T) == 1, "1, 2, 4, 8 or 16-byte stores");
+    uint8_t w;
+    __builtin_memcpy(&w, &v, 1);
+    __builtin_amdgcn_raw_buffer_store_b8(w, r, off, 0, kCacheSc1);
+  }
+}
+
 // Derived sizes of a validated terra_swin_geom.
 struct GeomDims {
   int64_t Hp, Wp;      // padded frame

@@ -274,6 +274,9 @@ __device__ __forceinline__ void store_window(const BlockParams& p, const UnitLoc
   constexpr int kRowStep = kThreads / kCpr;
   static_assert(kRowStep * kCpr == kThreads && 64 % kRowStep == 0, "whole rows per pass");
   const int row0 = tid / kCpr, ch0 = tid - row0 * kCpr;
+  // Token offsets are image-relative (grid_token), and an image is < 4 GiB.
+  const __amdgpu_buffer_rsrc_t out =
+      buffer_rsrc(p.y + (int64_t)u.b * p.H * p.W * (kCpr * 16), (uint32_t)((int64_t)p.H * p.W * (kCpr * 16)));
 #pragma unroll
   for (int r = 0; r < 64 / kRowStep; ++r) {
     const int row = row0 + kRowStep * r;
@@ -281,7 +284,7 @@ __device__ __forceinline__ void store_window(const BlockParams& p, const UnitLoc
     if (t >= 0) {
       const u32x4 val =
           __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(xr + tile_slot(row, ch0, kCpr) * 16));
-      __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(p.y + (int64_t)t * (kCpr * 16) + ch0 * 16));
+      stream_store_sc1(val, out, (uint32_t)(t - u.b * p.H * p.W) * (kCpr * 16) + ch0 * 16);
     }
   }
 }
@@ -827,6 +830,8 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   const int64_t units = (int64_t)q.batch * frame_windows;
   if (units >= (1ll << 31) || tokens >= (1ll << 31) || (int64_t)q.batch * dims.nWe >= (1ll << 31))
     return fail(TERRA_ERR_SHAPE, "grid too large for one launch; split the batch");
+  if ((int64_t)q.height * q.width * q.channels * 2 >= (1ll << 32))
+    return fail(TERRA_ERR_SHAPE, "one image of the grid must be under 4 GiB");
 
   BlockParams p;
   memset(&p, 0, sizeof(p));

@@ -129,14 +129,16 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
 
     // ---- stream O out (whole lines) ------------------------------------------
     {
-      const int64_t row_base = (int64_t)w * kNPad + row0;
-      uint16_t* dst = reinterpret_cast<uint16_t*>(p.o) + row_base * p.o_stride + hg * G * D + chunk0 * 8;
-      const int64_t ostep = kRowStep * p.o_stride;
+      // The unit's slice of o: kNPad rows of G*D elements at row stride o_stride.
+      const uint16_t* slice = reinterpret_cast<const uint16_t*>(p.o) + (int64_t)w * kNPad * p.o_stride + hg * G * D;
+      const __amdgpu_buffer_rsrc_t out =
+          buffer_rsrc(slice, (uint32_t)(((int64_t)(kNPad - 1) * p.o_stride + G * D) * 2));
 #pragma unroll
       for (int u = 0; u < kPer; ++u) {
-        const int off = tile_slot(row0 + kRowStep * u, chunk0, cpr) * 16;
+        const int row = row0 + kRowStep * u;
+        const int off = tile_slot(row, chunk0, cpr) * 16;
         const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(qs + off));
-        __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst + u * ostep));
+        stream_store_sc1(val, out, (uint32_t)(row * p.o_stride + chunk0 * 8) * 2);
       }
     }
     if (next >= units) break;
@@ -441,6 +443,8 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
     return fail(TERRA_ERR_ALIGN, "bias_table must be 4-byte aligned");
   const int64_t items = (int64_t)d.num_windows * d.heads;
   if (items >= (1ll << 31)) return fail(TERRA_ERR_SHAPE, "too many window-heads for one launch");
+  if ((int64_t)d.o_stride * d.tokens * elt >= (1ll << 32))
+    return fail(TERRA_ERR_SHAPE, "one window of o must span under 4 GiB");
 
   AttnParams p;
   p.q = q; p.k = k; p.v = v; p.o = o;

@@ -61,13 +61,10 @@ __device__ __forceinline__ typename Chunk<VB>::T fill_chunk(uint32_t pat) {
   else return (T)pat;
 }
 
-// Every byte is touched once per launch, so loads and stores carry the
-// nontemporal (streaming) hint: on MI355X this lifts a copy from ~5.6 to
-// ~6.3 TB/s.
+// Every byte is touched once per launch: loads carry the nontemporal hint and
+// stores go out as sc1 buffer stores (stream_store_sc1).
 template <typename T>
 __device__ __forceinline__ T stream_load(const T* p) { return __builtin_nontemporal_load(p); }
-template <typename T>
-__device__ __forceinline__ void stream_store(T v, T* p) { __builtin_nontemporal_store(v, p); }
 
 struct CopyGeom {
   int32_t H, W, ws, Hp, Wp;
@@ -89,37 +86,41 @@ __global__ __launch_bounds__(kThreads) void partition_kernel(const uint8_t* __re
                                                              uint8_t* __restrict__ win,
                                                              const CopyGeom g) {
   using T = typename Chunk<VB>::T;
-  const uint32_t base = blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
-  T vals[kUnroll];
-  uint32_t dst[kUnroll];
+  const uint32_t first = blockIdx.x * (kThreads * kUnroll);
+  const uint32_t base = first + threadIdx.x;
+  const __amdgpu_buffer_rsrc_t out =
+      buffer_rsrc(win + (int64_t)first * VB, min(g.total - first, (uint32_t)(kThreads * kUnroll)) * VB);
+  // Loads are unconditional (lanes without a source read chunk 0 and take the
+  // pad value afterwards): a load under a branch gets its own wait at the
+  // branch join, which would leave one load in flight per lane.
+  int64_t src[kUnroll];
+  bool have[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const uint32_t c = base + u * kThreads;
-    dst[u] = c;
-    vals[u] = fill_chunk<VB>(g.pad_pattern);
-    if (c < g.total) {
-      uint32_t rest, cv, rest2, t, b, wl, wr, wc, ti, tj;
-      g.fd_cv.divmod(c, rest, cv);
-      g.fd_N.divmod(rest, rest2, t);
-      g.fd_nWe.divmod(rest2, b, wl);
-      g.fd_nWw.divmod(wl, wr, wc);
-      g.fd_ws.divmod(t, ti, tj);
-      const bool valid = g.valid_end <= 0 || ((int)wl >= g.valid_begin && (int)wl < g.valid_end);
-      int ph = (int)((wr + g.win_row_begin) * g.ws + ti) + g.shift_h;
-      int pw = (int)(wc * g.ws + tj) + g.shift_w;
-      if (ph >= g.Hp) ph -= g.Hp;
-      if (pw >= g.Wp) pw -= g.Wp;
-      const int sh = ph - g.pad_top;
-      const int sw = pw - g.pad_left;
-      if (valid && (unsigned)sh < (unsigned)g.H && (unsigned)sw < (unsigned)g.W) {
-        const int64_t src = (((int64_t)b * g.H + sh) * g.W + sw) * g.row_bytes + (int64_t)cv * VB;
-        vals[u] = stream_load(reinterpret_cast<const T*>(x + src));
-      }
-    }
+    uint32_t rest, cv, rest2, t, b, wl, wr, wc, ti, tj;
+    g.fd_cv.divmod(c, rest, cv);
+    g.fd_N.divmod(rest, rest2, t);
+    g.fd_nWe.divmod(rest2, b, wl);
+    g.fd_nWw.divmod(wl, wr, wc);
+    g.fd_ws.divmod(t, ti, tj);
+    const bool valid = g.valid_end <= 0 || ((int)wl >= g.valid_begin && (int)wl < g.valid_end);
+    int ph = (int)((wr + g.win_row_begin) * g.ws + ti) + g.shift_h;
+    int pw = (int)(wc * g.ws + tj) + g.shift_w;
+    if (ph >= g.Hp) ph -= g.Hp;
+    if (pw >= g.Wp) pw -= g.Wp;
+    const int sh = ph - g.pad_top;
+    const int sw = pw - g.pad_left;
+    have[u] = c < g.total && valid && (unsigned)sh < (unsigned)g.H && (unsigned)sw < (unsigned)g.W;
+    src[u] = have[u] ? (((int64_t)b * g.H + sh) * g.W + sw) * g.row_bytes + (int64_t)cv * VB : 0;
   }
+  T vals[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) vals[u] = stream_load(reinterpret_cast<const T*>(x + src[u]));
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    if (dst[u] < g.total) stream_store(vals[u], reinterpret_cast<T*>(win) + dst[u]);
+    if (!have[u]) vals[u] = fill_chunk<VB>(g.pad_pattern);
+    if (base + u * kThreads < g.total) stream_store_sc1(vals[u], out, (threadIdx.x + u * kThreads) * VB);
   }
 }
 
@@ -227,12 +228,18 @@ __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* _
 
   const u32x4* src = reinterpret_cast<const u32x4*>(x + (((int64_t)b * g.H + sh) * g.W + sw) * g.row_bytes);
   float v[CPL][E];
+  // Unconditional loads (absent chunks read chunk 0 of x, then count as
+  // zeros): a load under a branch gets its own wait at the branch join.
+  u32x4 raw[CPL];
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
     const int c = sub + kLnLanes * k;
-    u32x4 raw = u32x4(0u);
-    if (in && c < ln.chunks) raw = __builtin_nontemporal_load(src + c);
-    unpack_chunk<DT>(raw, v[k]);
+    raw[k] = __builtin_nontemporal_load((in && c < ln.chunks) ? src + c : reinterpret_cast<const u32x4*>(x));
+  }
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int c = sub + kLnLanes * k;
+    unpack_chunk<DT>((in && c < ln.chunks) ? raw[k] : u32x4(0u), v[k]);
   }
   float sum = 0.f;
 #pragma unroll
@@ -252,12 +259,16 @@ __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* _
   }
   const float rstd = rsqrtf(group8_sum(sq) * ln.inv_c + ln.eps);
 
-  u32x4* dst = reinterpret_cast<u32x4*>(win + (int64_t)tok * g.row_bytes);
+  const uint32_t first = blockIdx.x * kLnTokensPerBlock;
+  const __amdgpu_buffer_rsrc_t out =
+      buffer_rsrc(win + (int64_t)first * g.row_bytes,
+                  (uint32_t)(min(ln.tokens - first, (uint32_t)kLnTokensPerBlock) * g.row_bytes));
+  const uint32_t row_off = (tok - first) * (uint32_t)g.row_bytes;
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
     const int c = sub + kLnLanes * k;
     if (c < ln.chunks) {
-      u32x4 out;
+      u32x4 val;
       if (in) {
         float y[E];
 #pragma unroll
@@ -269,11 +280,11 @@ __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* _
           y[q + 2] = (v[k][q + 2] - mean) * rstd * gm.z + bt.z;
           y[q + 3] = (v[k][q + 3] - mean) * rstd * gm.w + bt.w;
         }
-        out = pack_chunk<DT>(y);
+        val = pack_chunk<DT>(y);
       } else {
-        out = u32x4(g.pad_pattern);
+        val = u32x4(g.pad_pattern);
       }
-      __builtin_nontemporal_store(out, dst + c);
+      stream_store_sc1(val, out, row_off + c * 16);
     }
   }
 }
@@ -311,59 +322,60 @@ __device__ __forceinline__ typename Chunk<VB>::T add_chunk(typename Chunk<VB>::T
   return r;
 }
 
-template <int VB, int DT>
+template <int VB, int DT, bool kResidual>
 __global__ __launch_bounds__(kThreads) void reverse_kernel(const uint8_t* __restrict__ win,
                                                            uint8_t* y,
                                                            const uint8_t* residual,
                                                            const CopyGeom g) {
   using T = typename Chunk<VB>::T;
-  const uint32_t base = blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
-  T vals[kUnroll];
-  uint32_t dst[kUnroll];
+  const uint32_t first = blockIdx.x * (kThreads * kUnroll);
+  const uint32_t base = first + threadIdx.x;
+  const __amdgpu_buffer_rsrc_t out =
+      buffer_rsrc(y + (int64_t)first * VB, min(g.total - first, (uint32_t)(kThreads * kUnroll)) * VB);
+  // Unconditional loads, as in partition_kernel: lanes without a source
+  // window token read chunk 0 and take zero afterwards.
+  int64_t src[kUnroll];
+  bool have[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const uint32_t c = base + u * kThreads;
-    dst[u] = c;
-    vals[u] = fill_chunk<VB>(0u);
-    if (c < g.total) {
-      uint32_t rest, cv, rest2, sw, b, sh;
-      g.fd_cv.divmod(c, rest, cv);
-      g.fd_W.divmod(rest, rest2, sw);
-      g.fd_H.divmod(rest2, b, sh);
-      int fi = (int)sh + g.pad_top - g.shift_h;
-      int fj = (int)sw + g.pad_left - g.shift_w;
-      if (fi < 0) fi += g.Hp;
-      if (fj < 0) fj += g.Wp;
-      uint32_t wr, ti, wc, tj;
-      g.fd_ws.divmod((uint32_t)fi, wr, ti);
-      g.fd_ws.divmod((uint32_t)fj, wc, tj);
-      const int wr_l = (int)wr - g.win_row_begin;
-      if ((unsigned)wr_l < (unsigned)g.win_rows) {
-        const int wl = wr_l * g.nWw + (int)wc;
-        const bool valid = g.valid_end <= 0 || (wl >= g.valid_begin && wl < g.valid_end);
-        if (valid) {
-          const int64_t w = (int64_t)b * g.win_rows * g.nWw + wl;
-          const int64_t src = (w * g.N + (int64_t)(ti * g.ws + tj)) * g.row_bytes + (int64_t)cv * VB;
-          vals[u] = stream_load(reinterpret_cast<const T*>(win + src));
-        }
-      }
-    }
+    uint32_t rest, cv, rest2, sw, b, sh;
+    g.fd_cv.divmod(c, rest, cv);
+    g.fd_W.divmod(rest, rest2, sw);
+    g.fd_H.divmod(rest2, b, sh);
+    int fi = (int)sh + g.pad_top - g.shift_h;
+    int fj = (int)sw + g.pad_left - g.shift_w;
+    if (fi < 0) fi += g.Hp;
+    if (fj < 0) fj += g.Wp;
+    uint32_t wr, ti, wc, tj;
+    g.fd_ws.divmod((uint32_t)fi, wr, ti);
+    g.fd_ws.divmod((uint32_t)fj, wc, tj);
+    const int wr_l = (int)wr - g.win_row_begin;
+    const int wl = wr_l * g.nWw + (int)wc;
+    const bool valid = g.valid_end <= 0 || (wl >= g.valid_begin && wl < g.valid_end);
+    have[u] = c < g.total && (unsigned)wr_l < (unsigned)g.win_rows && valid;
+    const int64_t w = (int64_t)b * g.win_rows * g.nWw + wl;
+    src[u] = have[u] ? (w * g.N + (int64_t)(ti * g.ws + tj)) * g.row_bytes + (int64_t)cv * VB : 0;
   }
-  if constexpr (DT != TERRA_DTYPE_U8 && (DT != TERRA_DTYPE_F32 || VB >= 4)) {
-    if (residual != nullptr) {
+  T vals[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (dst[u] < g.total) {
-          const T r = stream_load(reinterpret_cast<const T*>(residual) + dst[u]);
-          vals[u] = add_chunk<VB, DT>(r, vals[u]);
-        }
-      }
+  for (int u = 0; u < kUnroll; ++u) vals[u] = stream_load(reinterpret_cast<const T*>(win + src[u]));
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u)
+    if (!have[u]) vals[u] = fill_chunk<VB>(0u);
+  if constexpr (kResidual) {
+    T r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t c = base + u * kThreads;
+      r[u] = stream_load(reinterpret_cast<const T*>(residual) + (c < g.total ? c : 0u));
     }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) vals[u] = add_chunk<VB, DT>(r[u], vals[u]);
   }
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    if (dst[u] < g.total) stream_store(vals[u], reinterpret_cast<T*>(y) + dst[u]);
-  }
+  for (int u = 0; u < kUnroll; ++u)
+    if (base + u * kThreads < g.total) stream_store_sc1(vals[u], out, (threadIdx.x + u * kThreads) * VB);
 }
 
 uint32_t pad_pattern(int dtype, float v) {
@@ -471,8 +483,14 @@ void dispatch_partition_ln(int cpl, const void* x, void* win, const CopyGeom& g,
 template <int VB, int DT>
 void launch_reverse(const void* win, void* y, const void* res, const CopyGeom& g, hipStream_t s) {
   const uint32_t blocks = (g.total + kThreads * kUnroll - 1) / (kThreads * kUnroll);
-  reverse_kernel<VB, DT><<<blocks, kThreads, 0, s>>>((const uint8_t*)win, (uint8_t*)y,
-                                                      (const uint8_t*)res, g);
+  if constexpr (DT != TERRA_DTYPE_U8 && (DT != TERRA_DTYPE_F32 || VB >= 4)) {
+    if (res != nullptr) {
+      reverse_kernel<VB, DT, true><<<blocks, kThreads, 0, s>>>((const uint8_t*)win, (uint8_t*)y,
+                                                              (const uint8_t*)res, g);
+      return;
+    }
+  }
+  reverse_kernel<VB, DT, false><<<blocks, kThreads, 0, s>>>((const uint8_t*)win, (uint8_t*)y, nullptr, g);
 }
 
 template <int VB>
