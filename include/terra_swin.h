@@ -122,6 +122,15 @@ typedef struct terra_swin_attn_desc {
   int32_t win_row_begin, win_rows, win_cols;
 } terra_swin_attn_desc;
 
+/* Description of one window-attention backward call: the forward call's
+ * descriptor (q/k/v strides, masks, scale; its o_stride is unused) plus the
+ * row strides of the output gradient and of the three input gradients. */
+typedef struct terra_swin_attn_bwd_desc {
+  terra_swin_attn_desc fwd;
+  int32_t dout_stride;  /* elements per token row of dout       */
+  int32_t dq_stride, dk_stride, dv_stride;
+} terra_swin_attn_bwd_desc;
+
 /* Description of one fused Swin attention half-block call.
  *
  * geom: the token grid [B, H, W, C] (channels = C), window (must be 8),
@@ -198,6 +207,26 @@ int terra_swin_reverse(const void* windows, void* y, const void* residual,
 int terra_swin_attn_fwd(const void* q, const void* k, const void* v, void* o,
                         int dtype, const terra_swin_attn_desc* desc,
                         const float* bias_table, const float* explicit_mask,
+                        const uint64_t* land_bits, void* stream);
+
+/* Backward of terra_swin_attn_fwd (bf16, 8x8 windows, head dim 32 or 64,
+ * no padded keys; any mask mode, land bits).
+ * Replaces the autograd backward of the same ATen sequence
+ *           models/attention.py:256-278 (matmul, bias gather + add, mask add,
+ *           softmax, matmul), as run by the training step
+ *           core/runtime/run_model.py:362-617.
+ * P is recomputed from q, k and the masks.  Writes
+ *   dq = scale * dz k,  dk = scale * dz^T q,  dv = P^T dout     (bf16)
+ * with dz = P * (dout v^T - rowsum(P * (dout v^T))) per window and head, and,
+ * when dbias_table != NULL, ADDS sum over windows of dz[i, j] into
+ * dbias_table[idx(i, j) * heads + h] (fp32, same layout as bias_table; the
+ * caller zeroes it first; float atomics, so the summation order varies).
+ * dq, dk, dv may be column blocks of one [B_, N, 3C] buffer.
+ */
+int terra_swin_attn_bwd(const void* q, const void* k, const void* v, const void* dout,
+                        void* dq, void* dk, void* dv, int dtype,
+                        const terra_swin_attn_bwd_desc* desc, const float* bias_table,
+                        float* dbias_table, const float* explicit_mask,
                         const uint64_t* land_bits, void* stream);
 
 /* Fused Swin attention half-block (bf16, 8x8 windows, head dim 32).

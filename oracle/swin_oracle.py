@@ -264,7 +264,8 @@ def swin_block_attention(x: torch.Tensor, H: int, W: int, window_size: int, shif
     square-grid case (pad, window-row range, pad windows) as in partition_frame.
     """
     B, L, C = x.shape
-    p = {k_: v_.detach().to(compute_dtype).cpu() for k_, v_ in params.items()}
+    # Parameters that require a gradient stay in the graph (backward parity).
+    p = {k_: (v_ if v_.requires_grad else v_.detach()).to(compute_dtype).cpu() for k_, v_ in params.items()}
     x = x.to(compute_dtype)
     shortcut = x
     if use_layernorm:

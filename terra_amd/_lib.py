@@ -47,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "terra_swin_partition_ln",
     "terra_swin_reverse",
     "terra_swin_attn_fwd",
+    "terra_swin_attn_bwd",
     "terra_swin_block_fwd",
     "terra_swin_pack_linear",
 )
@@ -101,6 +102,18 @@ class SwinAttnDesc(ctypes.Structure):
         ("win_row_begin", ctypes.c_int32),
         ("win_rows", ctypes.c_int32),
         ("win_cols", ctypes.c_int32),
+    ]
+
+
+class SwinAttnBwdDesc(ctypes.Structure):
+    """Mirror of ``terra_swin_attn_bwd_desc``."""
+
+    _fields_ = [
+        ("fwd", SwinAttnDesc),
+        ("dout_stride", ctypes.c_int32),
+        ("dq_stride", ctypes.c_int32),
+        ("dk_stride", ctypes.c_int32),
+        ("dv_stride", ctypes.c_int32),
     ]
 
 
@@ -160,6 +173,9 @@ def load() -> ctypes.CDLL:
         lib.terra_swin_reverse.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinGeom), vp]
         lib.terra_swin_attn_fwd.restype = ctypes.c_int
         lib.terra_swin_attn_fwd.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinAttnDesc), vp, vp, vp, vp]
+        lib.terra_swin_attn_bwd.restype = ctypes.c_int
+        lib.terra_swin_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinAttnBwdDesc),
+                                            vp, vp, vp, vp, vp]
         lib.terra_swin_block_fwd.restype = ctypes.c_int
         lib.terra_swin_block_fwd.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(SwinBlockDesc), vp, vp, vp, vp, vp,
                                              vp, vp, vp, vp]

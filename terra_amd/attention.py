@@ -6,7 +6,8 @@ the reference's, so its state dicts load unchanged:
 ``k_linear``, ``v_linear``, ``proj``.  The forward runs the three q/k/v
 projections as one GEMM over the concatenated weights (x is read once), the
 fused HIP attention core on the projection output in place (no permute
-copies), then ``proj``.
+copies), then ``proj``.  With gradients enabled the core's backward is the
+HIP backward kernel (terra_amd.autograd).
 """
 from __future__ import annotations
 
@@ -15,7 +16,7 @@ from typing import Callable, Optional, Sequence, Union
 import torch
 import torch.nn.functional as F
 
-from . import kernels
+from . import autograd, kernels
 from .kernels import ShiftMask, WindowMask
 
 
@@ -98,12 +99,11 @@ class WindowAttention(torch.nn.Module):
              n_real: Optional[int] = None) -> torch.Tensor:
         """Fused core on projected q/k/v [B_, N, C] (row strides may exceed C)."""
         table = self.relative_position_bias_table if self.use_relative_position_bias else None
-        return kernels.window_attention(q, k, v, self.num_heads, self.window_size, self.scale,
-                                        bias_table=table, mask=mask, n_real=n_real)
+        return autograd.window_attention(q, k, v, self.num_heads, self.window_size, self.scale,
+                                         bias_table=table, mask=mask, n_real=n_real)
 
     def forward(self, x: torch.Tensor, mask=None) -> torch.Tensor:
-        B_, N, C = x.shape
-        qkv = self.qkv(x)
-        q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
-        o = self.core(q, k, v, mask=mask)
+        table = self.relative_position_bias_table if self.use_relative_position_bias else None
+        o = autograd.window_attention_qkv(self.qkv(x), self.num_heads, self.window_size, self.scale,
+                                          bias_table=table, mask=mask)
         return self.proj(o)

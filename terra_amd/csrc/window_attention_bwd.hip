@@ -1,0 +1,434 @@
+// Backward of the window-attention core (bf16, 8x8 windows, head dim 32/64).
+//
+// Per window w and head h, with z = (q k^T) * scale + bias + M the natural
+// logits and P = softmax(z) (recomputed here from q, k and the masks, the
+// same way the forward computes it):
+//
+//   dP  = dO V^T
+//   dz  = P * (dP - rowsum(P * dP))        (rowsum(P * dP) = rowsum(dO * O))
+//   dV  = P^T dO,   dQ = scale * dz K,   dK = scale * dz^T Q
+//   dbias[idx(i, j), h] += sum over windows of dz[i, j]
+//
+// One workgroup per (window, head group), persistent, with a fixed head group
+// per workgroup (the grid is a multiple of the number of head groups), so
+// each lane keeps its share of the bias gradient in registers across all its
+// windows and flushes it once.  Two waves per head:
+//   phase 1 (wave = query tiles 2*half, 2*half + 1): S^T and dP^T on MFMA in
+//     the forward's layout (lane = one query, 16 keys), softmax, dz; P and dz
+//     go to LDS as [query][key] bf16 tiles; dQ^T = K^T dz^T straight from the
+//     dz accumulators (the forward's P^T-operand trick) and out to memory.
+//   phase 2 (wave = keys [32*half, 32*half + 32)): dV^T = dO^T P and
+//     dK^T = Q^T dz with both operands read across rows of the LDS tiles
+//     (transposing LDS reads), contraction over all 64 queries.
+#include "common.h"
+#include "attn_core.h"
+
+namespace terra {
+namespace {
+
+struct BwdParams {
+  AttnParams a;         // forward call; a.o / a.o_stride carry dout
+  void* dq;
+  void* dk;
+  void* dv;
+  int64_t dq_stride, dk_stride, dv_stride;
+  float* dbias;         // fp32 [table_size, heads], accumulated; NULL: not wanted
+  float scale;          // natural q k^T scale
+};
+
+constexpr int kBwdTile = kNPad * 8 * 16;  // one [64][64] bf16 P or dz tile: 8 KB
+
+// 16x16x32 bf16 operand fragment read across the rows of a [64][cpr]-chunk
+// tile: lane (c, g) receives column col0 + c at rows 32*js + 16*(e/4) + 4g +
+// e%4 for k slot e (col0 a multiple of 16).  As an A operand the column is
+// the output row; as a B operand it is the output column.
+__device__ __forceinline__ bf16x8 rows_frag(const uint8_t* tile, int cpr, int col0, int js, int lane) {
+  const int g = lane >> 4, c16 = lane & 15;
+  const int cc = col0 + 4 * (c16 & 3);  // column addressed by this source lane
+  uint2 part[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    const int row = 32 * js + 16 * h2 + 4 * g + (c16 >> 2);
+    part[h2] = lds_read_tr16(tile + tile_slot(row, cc >> 3, cpr) * 16 + (cc & 7) * 2);
+  }
+  const uint32_t w[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+__device__ __forceinline__ uint2 pack4_bf16(const f32x4& v) {
+  uint2 r;
+  r.x = pack_bf16x2(v[0], v[1]);
+  r.y = pack_bf16x2(v[2], v[3]);
+  return r;
+}
+
+template <int D, int G, bool kExplicit>
+__global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParams bp) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const AttnParams& p = bp.a;
+  constexpr int nthreads = G * 128;
+  constexpr int cpr = G * D / 8;                 // chunks per row of the head group
+  constexpr int tile_bytes = kNPad * cpr * 16;
+  constexpr int kKF = D / 32;
+  uint8_t* qs = smem;
+  uint8_t* ks = smem + tile_bytes;
+  uint8_t* vs = smem + 2 * tile_bytes;
+  uint8_t* dos = smem + 3 * tile_bytes;
+  uint8_t* pz = smem + 4 * tile_bytes;           // per head: P tile, then dz tile
+  float* tables = reinterpret_cast<float*>(pz + 2 * G * kBwdTile);  // G bias columns (x log2e)
+  float* dtab = tables + G * kTableMax;          // G bias-gradient columns
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int head = wave >> 1;
+  const int half = wave & 1;
+  const int lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int units = (p.items / p.heads) * p.groups;
+  const int hg = blockIdx.x % p.groups;          // fixed: gridDim.x is a multiple of groups
+  const int h = hg * G + head;
+  uint8_t* ptile = pz + head * 2 * kBwdTile;
+  uint8_t* ztile = ptile + kBwdTile;
+
+  // Bias column of this head (x log2e, for the softmax) and a zeroed
+  // gradient column.
+  float* tab = tables + head * kTableMax;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int e = lane + 64 * (2 * u + half);
+    if (e < kTableMax) {
+      tab[e] = (p.bias_table != nullptr && e < p.table_size) ? p.bias_table[(int64_t)e * p.heads + h] * kLog2e : 0.f;
+      dtab[head * kTableMax + e] = 0.f;
+    }
+  }
+
+  constexpr int kPer = kNPad * cpr / nthreads;   // chunks per thread per tensor
+  constexpr int kRowStep = nthreads / cpr;
+  static_assert(kRowStep * cpr == nthreads && kRowStep * kPer == kNPad, "row tiling");
+  const int row0 = tid / cpr, chunk0 = tid % cpr;
+
+  f32x4 gz[2][4];  // this lane's bias-gradient share: dz summed over the windows
+#pragma unroll
+  for (int il = 0; il < 2; ++il)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) gz[il][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int unit = blockIdx.x; unit < units; unit += gridDim.x) {
+    const int w = unit / p.groups;
+    // ---- q, k, v, dout rows of the head group -> LDS --------------------------
+    {
+      const int64_t row_base = (int64_t)w * kNPad + row0;
+      const int col = hg * G * D + chunk0 * 8;
+      const uint16_t* src[4] = {reinterpret_cast<const uint16_t*>(p.q) + row_base * p.q_stride + col,
+                                reinterpret_cast<const uint16_t*>(p.k) + row_base * p.k_stride + col,
+                                reinterpret_cast<const uint16_t*>(p.v) + row_base * p.v_stride + col,
+                                reinterpret_cast<const uint16_t*>(p.o) + row_base * p.o_stride + col};
+      const int64_t step[4] = {kRowStep * p.q_stride, kRowStep * p.k_stride, kRowStep * p.v_stride,
+                               kRowStep * p.o_stride};
+      uint4 buf[4][kPer];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < kPer; ++u)
+          buf[t][u] = __builtin_bit_cast(
+              uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[t] + u * step[t])));
+      __syncthreads();  // the previous unit is done with every tile
+      uint8_t* dst[4] = {qs, ks, vs, dos};
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < kPer; ++u)
+          *reinterpret_cast<uint4*>(dst[t] + tile_slot(row0 + kRowStep * u, chunk0, cpr) * 16) = buf[t][u];
+      __syncthreads();
+    }
+
+    // ---- phase 1: query tiles 2*half, 2*half + 1 of head `head` ---------------
+    const WindowMaskState m = window_mask_state(p, w, true);
+    const float* emask = nullptr;
+    if constexpr (kExplicit) emask = p.explicit_mask + (int64_t)(w % p.mask_windows) * p.n_geo * p.n_geo;
+    LaneGeom<true> lg;
+    lane_geom_init<true>(lg, p, m, tab, lane);
+    const int hc = head * (D / 8);  // first chunk of this head in the tiles
+    f32x4 s[2][4];
+    float inv[2];
+    {
+      uint4 kf[4][kKF], qp[2][kKF];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < kKF; ++c)
+          kf[t][c] = *reinterpret_cast<const uint4*>(ks + tile_slot(16 * t + c16, hc + 4 * c + g, cpr) * 16);
+#pragma unroll
+      for (int il = 0; il < 2; ++il)
+#pragma unroll
+        for (int c = 0; c < kKF; ++c)
+          qp[il][c] = *reinterpret_cast<const uint4*>(
+              qs + tile_slot(16 * (2 * half + il) + c16, hc + 4 * c + g, cpr) * 16);
+      scores_pair<true, D>(s, kf, qp);
+    }
+    softmax_half<true, kExplicit>(s, inv, half, p, m, lg, emask, lane);
+    f32x4 dp[2][4];
+    {
+      uint4 vf[4][kKF], df[2][kKF];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < kKF; ++c)
+          vf[t][c] = *reinterpret_cast<const uint4*>(vs + tile_slot(16 * t + c16, hc + 4 * c + g, cpr) * 16);
+#pragma unroll
+      for (int il = 0; il < 2; ++il)
+#pragma unroll
+        for (int c = 0; c < kKF; ++c)
+          df[il][c] = *reinterpret_cast<const uint4*>(
+              dos + tile_slot(16 * (2 * half + il) + c16, hc + 4 * c + g, cpr) * 16);
+      scores_pair<true, D>(dp, vf, df);  // dP^T: keys 16jt + 4g + r, query c16
+    }
+    // P = e * (1 / rowsum); dz = P * (dP - sum_j P dP).  P is rounded to bf16
+    // for the tile the dV product reads, as the forward rounds it for P V.
+#pragma unroll
+    for (int il = 0; il < 2; ++il) {
+      float dsum = 0.f;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        s[il][jt] *= inv[il];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dsum += s[il][jt][r] * dp[il][jt][r];
+      }
+      dsum = xor_sum(dsum);
+      const int i = 16 * (2 * half + il) + c16;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const f32x4 z = s[il][jt] * (dp[il][jt] - dsum);
+        gz[il][jt] += z;
+        // [query][key] tiles: this lane's keys 16jt + 4g .. + 3 are 8 bytes.
+        const int off = tile_slot(i, 2 * jt + (g >> 1), 8) * 16 + (g & 1) * 8;
+        *reinterpret_cast<uint2*>(ptile + off) = pack4_bf16(s[il][jt]);
+        *reinterpret_cast<uint2*>(ztile + off) = pack4_bf16(z);
+        dp[il][jt] = z;
+      }
+    }
+    // dQ^T = K^T dz^T (dz accumulators as the P^T operand), times scale.
+    {
+      f32x4 o[D / 16][2];
+      auto kfrag = [&](int ct, int js) -> bf16x8 { return rows_frag(ks, cpr, head * D + 16 * ct, js, lane); };
+      pv_half<true, D>(o, dp, lane, kfrag);
+      const uint16_t* base = reinterpret_cast<const uint16_t*>(bp.dq) + (int64_t)w * kNPad * bp.dq_stride;
+      const __amdgpu_buffer_rsrc_t out =
+          buffer_rsrc(base, (uint32_t)(((int64_t)(kNPad - 1) * bp.dq_stride + p.heads * D) * 2));
+#pragma unroll
+      for (int il = 0; il < 2; ++il) {
+        const int i = 16 * (2 * half + il) + c16;
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct)
+          stream_store_sc1(pack4_bf16(o[ct][il] * bp.scale), out,
+                           (uint32_t)(i * bp.dq_stride + h * D + 16 * ct + 4 * g) * 2);
+      }
+    }
+    __syncthreads();  // P and dz tiles of both halves are in LDS
+
+    // ---- phase 2: keys [32*half, 32*half + 32) of head `head` -----------------
+    {
+      f32x4 av[D / 16][2], ak[D / 16][2];
+#pragma unroll
+      for (int ct = 0; ct < D / 16; ++ct)
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) av[ct][jt] = ak[ct][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int js = 0; js < 2; ++js) {  // 32 queries per MFMA step
+        bf16x8 pf[2], zf[2];
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) {
+          pf[jt] = rows_frag(ptile, 8, 32 * half + 16 * jt, js, lane);
+          zf[jt] = rows_frag(ztile, 8, 32 * half + 16 * jt, js, lane);
+        }
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) {
+          const bf16x8 dof = rows_frag(dos, cpr, head * D + 16 * ct, js, lane);
+          const bf16x8 qf = rows_frag(qs, cpr, head * D + 16 * ct, js, lane);
+#pragma unroll
+          for (int jt = 0; jt < 2; ++jt) {
+            av[ct][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dof, pf[jt], av[ct][jt], 0, 0, 0);
+            ak[ct][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf, zf[jt], ak[ct][jt], 0, 0, 0);
+          }
+        }
+      }
+      // lane (c16, g) of tile (ct, jt): channels 16ct + 4g .. + 3 of key 32half + 16jt + c16
+      const int64_t wrow = (int64_t)w * kNPad;
+      const __amdgpu_buffer_rsrc_t ov = buffer_rsrc(
+          reinterpret_cast<const uint16_t*>(bp.dv) + wrow * bp.dv_stride,
+          (uint32_t)(((int64_t)(kNPad - 1) * bp.dv_stride + p.heads * D) * 2));
+      const __amdgpu_buffer_rsrc_t ok = buffer_rsrc(
+          reinterpret_cast<const uint16_t*>(bp.dk) + wrow * bp.dk_stride,
+          (uint32_t)(((int64_t)(kNPad - 1) * bp.dk_stride + p.heads * D) * 2));
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) {
+        const int j = 32 * half + 16 * jt + c16;
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) {
+          const int col = h * D + 16 * ct + 4 * g;
+          stream_store_sc1(pack4_bf16(av[ct][jt]), ov, (uint32_t)(j * bp.dv_stride + col) * 2);
+          stream_store_sc1(pack4_bf16(ak[ct][jt] * bp.scale), ok, (uint32_t)(j * bp.dk_stride + col) * 2);
+        }
+      }
+    }
+  }
+
+  // ---- bias gradient: registers -> LDS column -> global table ----------------
+  if (bp.dbias == nullptr) return;  // uniform
+  // Lane element (il, jt, r) is the pair (query 16(2half+il) + c16, key 16jt + 4g + r):
+  // relative index lane_base + 30*(it - jt) - r.
+  const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;
+  float* dcol = dtab + head * kTableMax;
+#pragma unroll
+  for (int il = 0; il < 2; ++il)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        atomicAdd(dcol + lane_base + 30 * (2 * half + il - jt) - r, gz[il][jt][r]);
+  __syncthreads();
+  for (int e = tid; e < G * p.table_size; e += nthreads) {
+    const int hh = e / p.table_size, idx = e - hh * p.table_size;
+    unsafeAtomicAdd(bp.dbias + (int64_t)idx * p.heads + hg * G + hh, dtab[hh * kTableMax + idx]);
+  }
+}
+
+template <int D, int G>
+constexpr int bwd_lds_bytes() {
+  return 4 * kNPad * (G * D / 8) * 16 + 2 * G * kBwdTile + 2 * G * kTableMax * (int)sizeof(float);
+}
+
+template <int D, int G, bool kExplicit>
+int launch_bwd(const BwdParams& bp, hipStream_t s) {
+  constexpr int lds = bwd_lds_bytes<D, G>();
+  auto kern = window_attn_bwd_kernel<D, G, kExplicit>;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  constexpr int kMaxDevices = 64;
+  static int resident_cache[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(TERRA_ERR_LAUNCH, "cannot query the current device");
+  if (resident_cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, G * 128, lds) != hipSuccess)
+      return fail(TERRA_ERR_LAUNCH, "cannot size the backward grid for this device");
+    resident_cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  const int groups = bp.a.groups;
+  const int units = (bp.a.items / bp.a.heads) * groups;
+  int blocks = units < resident_cache[dev] ? units : resident_cache[dev];
+  blocks -= blocks % groups;  // every workgroup keeps one head group
+  if (blocks < groups) blocks = groups;
+  kern<<<blocks, G * 128, lds, s>>>(bp);
+  return TERRA_OK;
+}
+
+}  // namespace
+}  // namespace terra
+
+using namespace terra;
+
+extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, const void* dout, void* dq,
+                                   void* dk, void* dv, int dtype, const terra_swin_attn_bwd_desc* desc,
+                                   const float* bias_table, float* dbias_table, const float* explicit_mask,
+                                   const uint64_t* land_bits, void* stream) {
+  clear_error();
+  if (desc == nullptr) return fail(TERRA_ERR_NULL, "desc is NULL");
+  if (q == nullptr || k == nullptr || v == nullptr || dout == nullptr || dq == nullptr || dk == nullptr ||
+      dv == nullptr)
+    return fail(TERRA_ERR_NULL, "q, k, v, dout, dq, dk and dv must be non-NULL");
+  if (dtype != TERRA_DTYPE_BF16) return fail(TERRA_ERR_UNSUPPORTED, "attention backward is built for bf16");
+  const terra_swin_attn_desc& d = desc->fwd;
+  if (d.num_windows <= 0 || d.heads <= 0 || d.channels <= 0)
+    return fail(TERRA_ERR_SHAPE, "num_windows/channels/heads must be positive");
+  if (d.window_h != 8 || d.window_w != 8 || d.tokens != 64 || d.n_real != 64)
+    return fail(TERRA_ERR_UNSUPPORTED, "attention backward is built for 8x8 windows without padded keys");
+  if (d.channels % d.heads != 0)
+    return fail(TERRA_ERR_SHAPE, "channels %d not divisible by heads %d", d.channels, d.heads);
+  const int D = d.channels / d.heads;
+  if (D != 32 && D != 64) return fail(TERRA_ERR_UNSUPPORTED, "head dim %d not in {32, 64}", D);
+  const int32_t strides[8] = {d.q_stride, d.k_stride, d.v_stride, desc->dout_stride,
+                              desc->dq_stride, desc->dk_stride, desc->dv_stride, d.channels};
+  for (int i = 0; i < 7; ++i) {
+    if (strides[i] < d.channels) return fail(TERRA_ERR_SHAPE, "row strides must be >= channels");
+    if (strides[i] % 8 != 0) return fail(TERRA_ERR_ALIGN, "row strides must be multiples of 8 elements");
+    if ((int64_t)strides[i] * d.tokens * 2 >= (1ll << 32))
+      return fail(TERRA_ERR_SHAPE, "one window must span under 4 GiB");
+  }
+  for (const void* ptr : {q, k, v, dout, (const void*)dq, (const void*)dk, (const void*)dv})
+    if ((uintptr_t)ptr % 16 != 0) return fail(TERRA_ERR_ALIGN, "q/k/v/dout/dq/dk/dv must be 16-byte aligned");
+  if ((bias_table != nullptr && (uintptr_t)bias_table % 4 != 0) ||
+      (dbias_table != nullptr && (uintptr_t)dbias_table % 4 != 0))
+    return fail(TERRA_ERR_ALIGN, "bias tables must be 4-byte aligned");
+  if (dbias_table != nullptr && bias_table == nullptr)
+    return fail(TERRA_ERR_SHAPE, "dbias_table without bias_table");
+  if (d.mask_mode != TERRA_MASK_NONE && d.mask_mode != TERRA_MASK_SHIFT && d.mask_mode != TERRA_MASK_EXPLICIT)
+    return fail(TERRA_ERR_SHAPE, "unknown mask_mode %d", d.mask_mode);
+  if ((d.mask_mode == TERRA_MASK_EXPLICIT || land_bits != nullptr) && d.mask_windows <= 0)
+    return fail(TERRA_ERR_SHAPE, "mask_windows must be positive with an explicit mask or land bits");
+  if (d.mask_mode == TERRA_MASK_EXPLICIT && explicit_mask == nullptr)
+    return fail(TERRA_ERR_NULL, "explicit mask mode without a mask");
+  if (d.mask_mode == TERRA_MASK_EXPLICIT && d.num_windows % d.mask_windows != 0)
+    return fail(TERRA_ERR_SHAPE, "num_windows %d not divisible by mask windows %d", d.num_windows, d.mask_windows);
+  if (d.mask_mode == TERRA_MASK_SHIFT) {
+    if (d.win_rows <= 0 || d.win_cols <= 0 || d.frame_h <= 0 || d.frame_w <= 0)
+      return fail(TERRA_ERR_SHAPE, "shift mask needs a positive frame and window grid");
+    if (d.frame_h % 8 || d.frame_w % 8) return fail(TERRA_ERR_SHAPE, "frame not a multiple of the window");
+    if (d.win_cols != d.frame_w / 8) return fail(TERRA_ERR_SHAPE, "win_cols %d != frame_w / 8", d.win_cols);
+    if (d.win_row_begin < 0 || (d.win_row_begin + d.win_rows) * 8 > d.frame_h)
+      return fail(TERRA_ERR_SHAPE, "window rows outside the frame");
+    if (d.shift_h <= 0 || d.shift_h >= 8 || d.shift_w <= 0 || d.shift_w >= 8)
+      return fail(TERRA_ERR_SHAPE, "shift mask needs 0 < shift < window (got %d, %d)", d.shift_h, d.shift_w);
+    if (d.num_windows % (d.win_rows * d.win_cols) != 0)
+      return fail(TERRA_ERR_SHAPE, "num_windows %d not a multiple of the %d windows per image", d.num_windows,
+                  d.win_rows * d.win_cols);
+  }
+  const int64_t items = (int64_t)d.num_windows * d.heads;
+  if (items >= (1ll << 31)) return fail(TERRA_ERR_SHAPE, "too many window-heads for one launch");
+
+  BwdParams bp;
+  memset(&bp, 0, sizeof(bp));
+  AttnParams& p = bp.a;
+  p.q = q; p.k = k; p.v = v; p.o = const_cast<void*>(dout);
+  p.q_stride = d.q_stride; p.k_stride = d.k_stride; p.v_stride = d.v_stride; p.o_stride = desc->dout_stride;
+  p.bias_table = bias_table;
+  p.explicit_mask = explicit_mask;
+  p.land_bits = land_bits;
+  p.items = (int32_t)items;
+  p.heads = d.heads;
+  p.N = d.tokens;
+  p.n_geo = 64;
+  p.window_h = p.window_w = 8;
+  p.table_size = 225;
+  p.n_real = 64;
+  p.scale_l2e = d.scale * kLog2e;
+  p.mask_l2e = d.mask_value * kLog2e;
+  p.pad_key_l2e = d.pad_key_value * kLog2e;
+  p.mask_mode = d.mask_mode; p.mask_windows = d.mask_windows > 0 ? d.mask_windows : 1;
+  p.frame_h = d.frame_h; p.frame_w = d.frame_w; p.shift_h = d.shift_h; p.shift_w = d.shift_w;
+  p.win_row_begin = d.win_row_begin; p.win_rows = d.win_rows; p.win_cols = d.win_cols;
+  bp.dq = dq; bp.dk = dk; bp.dv = dv;
+  bp.dq_stride = desc->dq_stride; bp.dk_stride = desc->dk_stride; bp.dv_stride = desc->dv_stride;
+  bp.dbias = dbias_table;
+  bp.scale = d.scale;
+
+  // Two heads per workgroup for head dim 32 (128-byte row slices), else one.
+  const int G = (D == 32 && d.heads % 2 == 0) ? 2 : 1;
+  p.group = G;
+  p.groups = d.heads / G;
+  const bool expl = d.mask_mode == TERRA_MASK_EXPLICIT;
+  hipStream_t s = (hipStream_t)stream;
+  int st;
+  if (D == 32)
+    st = G == 2 ? (expl ? launch_bwd<32, 2, true>(bp, s) : launch_bwd<32, 2, false>(bp, s))
+                : (expl ? launch_bwd<32, 1, true>(bp, s) : launch_bwd<32, 1, false>(bp, s));
+  else
+    st = expl ? launch_bwd<64, 1, true>(bp, s) : launch_bwd<64, 1, false>(bp, s);
+  if (st != TERRA_OK) return st;
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "terra_swin_attn_bwd launch failed: %s", hipGetErrorString(e));
+  return TERRA_OK;
+}

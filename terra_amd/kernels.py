@@ -280,21 +280,33 @@ def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_head
         out = torch.empty((num_windows, tokens, channels), dtype=q.dtype, device=dev)
     os_ = _row_stride(out, "out", num_windows, tokens, channels)
 
+    d = _attn_desc(q, num_heads, window_size, scale, n_real, mask_value, pad_key_value, (qs, ks, vs, os_))
+    table = _bias_table(bias_table, d)
+    emask, land = _attn_masks(d, num_windows, mask)
+
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out), code, ctypes.byref(d),
+                                             _ptr(table), _ptr(emask), _ptr(land), _stream(dev))
+    _lib.check(st, "terra_swin_attn_fwd")
+    return out
+
+
+def _attn_desc(q: torch.Tensor, num_heads: int, window_size: Tuple[int, int], scale: float,
+               n_real: Optional[int], mask_value: float, pad_key_value: float,
+               strides: Tuple[int, int, int, int]) -> _lib.SwinAttnDesc:
+    num_windows, tokens, channels = q.shape
     d = _lib.SwinAttnDesc()
     d.num_windows, d.tokens, d.channels, d.heads = num_windows, tokens, channels, num_heads
     d.window_h, d.window_w = int(window_size[0]), int(window_size[1])
     d.n_real = tokens if n_real is None else int(n_real)
-    d.q_stride, d.k_stride, d.v_stride, d.o_stride = qs, ks, vs, os_
+    d.q_stride, d.k_stride, d.v_stride, d.o_stride = strides
     d.scale, d.mask_value, d.pad_key_value = float(scale), float(mask_value), float(pad_key_value)
+    return d
 
-    table = None
-    if bias_table is not None:
-        _require_device(bias_table)
-        n_rel = (2 * d.window_h - 1) * (2 * d.window_w - 1)
-        if tuple(bias_table.shape) != (n_rel, num_heads):
-            raise ValueError(f"bias table must be [{n_rel}, {num_heads}], got {tuple(bias_table.shape)}")
-        table = bias_table.detach().to(torch.float32).contiguous()
 
+def _attn_masks(d: _lib.SwinAttnDesc, num_windows: int,
+                mask: Union[None, torch.Tensor, ShiftMask, WindowMask]):
+    """Fills the mask fields of ``d``; returns (explicit fp32 mask, land bits)."""
     shift = mask.shift if isinstance(mask, WindowMask) else mask
     land = mask.land_bits if isinstance(mask, WindowMask) else None
     emask = None
@@ -327,12 +339,79 @@ def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_head
             raise ValueError(f"attention batch {num_windows} must be divisible by land windows {land.shape[0]}")
         land = land.contiguous()
         d.mask_windows = land.shape[0]
+    return emask, land
 
+
+def _bias_table(bias_table: Optional[torch.Tensor], d: _lib.SwinAttnDesc) -> Optional[torch.Tensor]:
+    if bias_table is None:
+        return None
+    _require_device(bias_table)
+    n_rel = (2 * d.window_h - 1) * (2 * d.window_w - 1)
+    if tuple(bias_table.shape) != (n_rel, d.heads):
+        raise ValueError(f"bias table must be [{n_rel}, {d.heads}], got {tuple(bias_table.shape)}")
+    return bias_table.detach().to(torch.float32).contiguous()
+
+
+def attention_backward_supported(q: torch.Tensor, num_heads: int, window_size: Tuple[int, int],
+                                 n_real: Optional[int] = None) -> bool:
+    """Whether :func:`window_attention_backward` serves this shape (bf16, 8x8
+    windows of 64 tokens without padded keys, head dim 32 or 64)."""
+    tokens, channels = q.shape[-2], q.shape[-1]
+    return (q.dtype == torch.bfloat16 and tuple(int(w) for w in window_size) == (8, 8) and tokens == 64
+            and (n_real is None or int(n_real) == 64) and channels % num_heads == 0
+            and channels // num_heads in (32, 64))
+
+
+def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dout: torch.Tensor,
+                              num_heads: int, window_size: Tuple[int, int], scale: float,
+                              bias_table: Optional[torch.Tensor] = None,
+                              mask: Union[None, torch.Tensor, ShiftMask, WindowMask] = None,
+                              n_real: Optional[int] = None, mask_value: float = MASK_VALUE,
+                              pad_key_value: float = PAD_KEY_VALUE,
+                              dq: Optional[torch.Tensor] = None, dk: Optional[torch.Tensor] = None,
+                              dv: Optional[torch.Tensor] = None, dbias: Optional[torch.Tensor] = None):
+    """Gradients of :func:`window_attention` (terra_swin_attn_bwd).
+
+    Returns (dq, dk, dv); each may be given as an output view (e.g. a column
+    block of one [B_, N, 3C] buffer).  ``dbias``: an fp32 tensor shaped like
+    the bias table that the kernel ADDS the bias gradient into, or None.
+    """
+    dev = _require_device(q, k, v, dout)
+    for t in (k, v, dout):
+        if t.dtype != q.dtype:
+            raise TypeError("q, k, v and dout must share a dtype")
+    if q.dtype != torch.bfloat16:
+        raise ValueError("attention backward is built for bf16 activations")
+    num_windows, tokens, channels = q.shape
+    strides = tuple(_row_stride(t, n, num_windows, tokens, channels)
+                    for t, n in ((q, "q"), (k, "k"), (v, "v"), (dout, "dout")))
+    outs = []
+    for t, n in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        if t is None:
+            t = torch.empty((num_windows, tokens, channels), dtype=q.dtype, device=dev)
+        elif t.dtype != q.dtype or t.device != dev:
+            raise ValueError(f"{n} must be a {q.dtype} tensor on {dev}")
+        outs.append(t)
+    out_strides = tuple(_row_stride(t, n, num_windows, tokens, channels) for t, n in zip(outs, ("dq", "dk", "dv")))
+    bd = _lib.SwinAttnBwdDesc()
+    bd.fwd = _attn_desc(q, num_heads, window_size, scale, n_real, mask_value, pad_key_value,
+                        (strides[0], strides[1], strides[2], strides[3]))
+    bd.dout_stride = strides[3]
+    bd.dq_stride, bd.dk_stride, bd.dv_stride = out_strides
+    table = _bias_table(bias_table, bd.fwd)
+    if dbias is not None:
+        if table is None:
+            raise ValueError("dbias needs the bias table")
+        if dbias.dtype != torch.float32 or tuple(dbias.shape) != tuple(table.shape) or not dbias.is_contiguous() \
+                or dbias.device != dev:
+            raise ValueError(f"dbias must be a contiguous fp32 tensor of shape {tuple(table.shape)} on {dev}")
+    emask, land = _attn_masks(bd.fwd, num_windows, mask)
     with torch.cuda.device(dev):
-        st = _lib.load().terra_swin_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out), code, ctypes.byref(d),
-                                             _ptr(table), _ptr(emask), _ptr(land), _stream(dev))
-    _lib.check(st, "terra_swin_attn_fwd")
-    return out
+        st = _lib.load().terra_swin_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(outs[0]), _ptr(outs[1]),
+                                             _ptr(outs[2]), _dtype_code(q, (torch.bfloat16,)), ctypes.byref(bd),
+                                             _ptr(table), _ptr(dbias), _ptr(emask), _ptr(land), _stream(dev))
+    _lib.check(st, "terra_swin_attn_bwd")
+    return tuple(outs)
 
 
 # Shapes the fused block kernel is built for: 8x8 windows, head dim 32.

@@ -29,7 +29,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from . import config, kernels
+from . import autograd, config, kernels
 from .attention import WindowAttention
 from .kernels import ShiftMask, WindowGeometry, WindowMask
 from .utils import get_swin_attention_mask, land_window_bits
@@ -172,14 +172,17 @@ class SequentialSwinTransformer(torch.nn.Module):
                                    shift_mask=mask is not None and mask.shift is not None,
                                    land_bits=None if mask is None else mask.land_bits, **self._fused_args())
             return y.view(B, H * W, C)
-        if config.use_layernorm and self._fusable_norm(grid.dtype):
+        # Training: norm1 is torch's LayerNorm (its own backward), then the
+        # partition / reverse permutations with their adjoint as gradient.
+        training = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+        if config.use_layernorm and not training and self._fusable_norm(grid.dtype):
             x_windows = kernels.swin_partition_ln(grid, geom, self.norm1.weight, self.norm1.bias, self.norm1.eps)
         else:
-            if config.use_layernorm:  # a norm layer the gather cannot fuse runs on its own
+            if config.use_layernorm:  # a norm layer the gather does not fuse here runs on its own
                 grid = self.norm1(grid.view(B, L, C)).contiguous().view(B, H, W, C)
-            x_windows = kernels.swin_partition(grid, geom)
+            x_windows = autograd.partition(grid, geom)
         attn_windows = self.attn(x_windows, mask=self.window_mask(geom))
         out_dtype = torch.promote_types(attn_windows.dtype, shortcut.dtype)
-        y = kernels.swin_reverse(attn_windows.to(out_dtype), geom,
-                                 residual=shortcut.to(out_dtype).contiguous())
+        y = autograd.reverse(attn_windows.to(out_dtype).contiguous(), geom,
+                             residual=shortcut.to(out_dtype).contiguous().view(B, H, W, C))
         return y.view(B, H * W, C)

@@ -38,6 +38,7 @@ def test_abi_version_and_struct_sizes():
     assert ctypes.sizeof(L.SwinGeom) == 4 * len(L.SwinGeom._fields_) == 60
     assert ctypes.sizeof(L.SwinAttnDesc) == 4 * len(L.SwinAttnDesc._fields_) == 92
     assert ctypes.sizeof(L.SwinBlockDesc) == 60 + 4 * (len(L.SwinBlockDesc._fields_) - 1) == 92
+    assert ctypes.sizeof(L.SwinAttnBwdDesc) == 92 + 4 * 4 == 108
 
 
 def _geom(**kw):
@@ -130,6 +131,48 @@ def test_attention_rejects_dtype_null_alignment():
                                    None) == -4
 
 
+def _bwd_desc(dout_stride=64, dq_stride=64, dk_stride=64, dv_stride=64, **kw):
+    bd = L.SwinAttnBwdDesc()
+    bd.fwd = _desc(**kw)
+    bd.dout_stride, bd.dq_stride, bd.dk_stride, bd.dv_stride = dout_stride, dq_stride, dk_stride, dv_stride
+    return bd
+
+
+@pytest.mark.parametrize("kw,code,text", [
+    (dict(window_h=7, window_w=7, tokens=49, n_real=49), -5, "8x8 windows"),
+    (dict(n_real=40), -5, "padded keys"),
+    (dict(heads=3), -3, "not divisible"),
+    (dict(channels=48, heads=3, q_stride=48, k_stride=48, v_stride=48, o_stride=48, dout_stride=48,
+          dq_stride=48, dk_stride=48, dv_stride=48), -5, "head dim"),
+    (dict(dq_stride=60), -3, ">= channels"),
+    (dict(dv_stride=68), -4, "multiples"),
+    (dict(mask_mode=7), -3, "mask_mode"),
+    (dict(mask_mode=2, mask_windows=4), -1, "explicit"),
+    (dict(mask_mode=1, frame_h=16, frame_w=16, shift_h=4, shift_w=4, win_rows=2, win_cols=3), -3, "win_cols"),
+])
+def test_attention_backward_rejects_bad_descriptors(kw, code, text):
+    lib = L.load()
+    bd = _bwd_desc(**kw)
+    st = lib.terra_swin_attn_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(bd), None, None,
+                                 None, None, None)
+    assert st == code, L.last_error()
+    assert text in L.last_error()
+
+
+def test_attention_backward_rejects_dtype_null_alignment_table():
+    lib = L.load()
+    bd = _bwd_desc()
+    call = lambda *a: lib.terra_swin_attn_bwd(*a, ctypes.byref(bd), None, None, None, None, None)  # noqa: E731
+    assert call(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, L.DTYPE_F32) == -5
+    assert call(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, L.DTYPE_BF16) == -1
+    bad = ctypes.c_void_p((1 << 20) + 8)
+    assert call(FAKE, FAKE, FAKE, FAKE, FAKE, bad, FAKE, L.DTYPE_BF16) == -4
+    # a bias-table gradient needs the bias table
+    st = lib.terra_swin_attn_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(bd), None,
+                                 FAKE, None, None, None)
+    assert st == -3 and "dbias_table" in L.last_error()
+
+
 def test_python_wrapper_raises_instead_of_falling_back():
     x = torch.zeros(1, 16, 16, 8)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
@@ -137,6 +180,9 @@ def test_python_wrapper_raises_instead_of_falling_back():
     q = torch.zeros(2, 64, 64)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         kernels.window_attention(q, q, q, 2, (8, 8), 0.1)
+    qb = q.to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        kernels.window_attention_backward(qb, qb, qb, qb, 2, (8, 8), 0.1)
 
 
 def test_check_maps_status_to_exceptions():

@@ -1,0 +1,222 @@
+"""GPU parity of the training-path backward (row f3) against the CPU oracle.
+
+The reference path is the oracle's forward restatement differentiated by
+torch autograd in fp32 on the same bf16-rounded inputs (the oracle forward is
+pinned by tests/test_oracle.py; tests/test_oracle.py also gradchecks it).
+
+Tolerances (bf16 activations; the kernel rounds P and dz to bf16 as MFMA
+operands, as the forward rounds P):
+  dq, dk, dv:  max |got - ref| <= 2e-2 * max |ref| per tensor;
+  dbias:       max |got - ref| <= 2e-2 * max |ref| (fp32, summed over windows);
+  module (LayerNorm + Linears + attention + residual, all bf16 in torch's
+  and the kernel's rounding): normwise |got - ref| / |ref| <= 3e-2 per tensor.
+Partition / reverse gradients are permutations: bit-exact.
+"""
+import pytest
+import torch
+
+from oracle import swin_oracle as so
+from terra_amd import autograd, kernels, utils, workloads
+from terra_amd.kernels import ShiftMask, WindowGeometry, WindowMask
+from terra_amd.transformer import SequentialSwinTransformer
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B_, C, heads, seed, qkv_scale=2.0):
+    q = workloads.activations((B_, 64, C), seed) * qkv_scale
+    k = workloads.activations((B_, 64, C), seed + 1) * qkv_scale
+    v = workloads.activations((B_, 64, C), seed + 2)
+    dout = workloads.activations((B_, 64, C), seed + 3)
+    table = torch.empty(225, heads)
+    torch.nn.init.trunc_normal_(table, std=0.5, generator=workloads.generator(seed + 4))
+    bf = lambda t: t.to(torch.bfloat16)  # noqa: E731
+    return bf(q), bf(k), bf(v), bf(dout), table
+
+
+def _oracle_grads(q, k, v, dout, heads, table, dense_mask):
+    leaves = [t.float().clone().requires_grad_(True) for t in (q, k, v)]
+    tab = None if table is None else table.clone().requires_grad_(True)
+    C = q.shape[-1]
+    out = so.window_attention_core(*leaves, heads, (C // heads) ** -0.5, tab, (8, 8), dense_mask,
+                                   compute_dtype=torch.float32)
+    (out * dout.float()).sum().backward()
+    return [t.grad for t in leaves], (None if tab is None else tab.grad)
+
+
+def _close(got, ref, rel=2e-2):
+    got = got.double().cpu()
+    ref = ref.double()
+    err = (got - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    assert err <= rel * scale, (err, scale)
+
+
+def _mask_case(kind, B, H, W, seed):
+    """(kernel mask argument, dense oracle mask) of one test case."""
+    g = WindowGeometry(B, H, W, 1, 8, 4, 4)
+    if kind == "none":
+        return None, None
+    dense = so.shift_mask(H, W, 8, 4)
+    if kind == "shift":
+        return ShiftMask.from_geometry(g), dense
+    if kind == "explicit":
+        return dense, dense
+    land = workloads.land_mask(H, W, seed=seed)
+    bits = utils.land_window_bits(land.cuda(), g)
+    total = so.fold_land(dense, so.land_key_flags(land, 8, 4, 4))
+    return WindowMask(shift=ShiftMask.from_geometry(g), land_bits=bits), total
+
+
+@pytest.mark.parametrize("C,heads", [(192, 6), (128, 2)])
+@pytest.mark.parametrize("kind", ["none", "shift", "explicit", "land"])
+def test_attention_backward_matches_oracle(dev, C, heads, kind):
+    B, H, W = 2, 32, 48
+    B_ = B * (H // 8) * (W // 8)
+    q, k, v, dout, table = _inputs(B_, C, heads, 300)
+    mask, dense = _mask_case(kind, B, H, W, 31)
+    if isinstance(mask, torch.Tensor):
+        mask = mask.to(dev)
+    dbias = torch.zeros(225, heads, device=dev)
+    dq, dk, dv = kernels.window_attention_backward(q.to(dev), k.to(dev), v.to(dev), dout.to(dev), heads, (8, 8),
+                                                   (C // heads) ** -0.5, bias_table=table.to(dev), mask=mask,
+                                                   dbias=dbias)
+    (rq, rk, rv), rtab = _oracle_grads(q, k, v, dout, heads, table, dense)
+    for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
+        _close(got, ref)
+    _close(dbias, rtab)
+
+
+def test_attention_backward_no_bias_table(dev):
+    B_, C, heads = 24, 192, 6
+    q, k, v, dout, _ = _inputs(B_, C, heads, 310)
+    dq, dk, dv = kernels.window_attention_backward(q.to(dev), k.to(dev), v.to(dev), dout.to(dev), heads, (8, 8),
+                                                   32 ** -0.5)
+    (rq, rk, rv), _ = _oracle_grads(q, k, v, dout, heads, None, None)
+    for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
+        _close(got, ref)
+
+
+def test_attention_backward_into_qkv_buffer(dev):
+    """dq | dk | dv written as column blocks of one [B_, N, 3C] buffer from
+    q | k | v column blocks equal the separate-tensor results bit for bit;
+    dq, dk, dv are deterministic."""
+    B_, C, heads = 48, 192, 6
+    q, k, v, dout, table = _inputs(B_, C, heads, 320)
+    qkv = torch.cat([q, k, v], -1).to(dev)
+    dqkv = torch.full_like(qkv, float("nan"))
+    args = (heads, (8, 8), 32 ** -0.5)
+    kernels.window_attention_backward(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], dout.to(dev), *args,
+                                      bias_table=table.to(dev), dq=dqkv[..., :C], dk=dqkv[..., C:2 * C],
+                                      dv=dqkv[..., 2 * C:])
+    sep = kernels.window_attention_backward(q.to(dev), k.to(dev), v.to(dev), dout.to(dev), *args,
+                                            bias_table=table.to(dev))
+    assert torch.equal(dqkv, torch.cat(sep, -1))
+    again = kernels.window_attention_backward(q.to(dev), k.to(dev), v.to(dev), dout.to(dev), *args,
+                                              bias_table=table.to(dev))
+    for a, b in zip(sep, again):
+        assert torch.equal(a, b)
+
+
+def test_attention_autograd_function(dev):
+    """autograd.window_attention_qkv: gradients of the qkv input and of the
+    bias table through torch's backward() equal the kernel called directly."""
+    B_, C, heads = 24, 192, 6
+    q, k, v, dout, table = _inputs(B_, C, heads, 330)
+    qkv = torch.cat([q, k, v], -1).to(dev).requires_grad_(True)
+    tab = table.to(dev).requires_grad_(True)
+    o = autograd.window_attention_qkv(qkv, heads, (8, 8), 32 ** -0.5, bias_table=tab)
+    o.backward(dout.to(dev))
+    dbias = torch.zeros_like(tab)
+    want = kernels.window_attention_backward(qkv.detach()[..., :C], qkv.detach()[..., C:2 * C],
+                                             qkv.detach()[..., 2 * C:], dout.to(dev), heads, (8, 8), 32 ** -0.5,
+                                             bias_table=tab.detach(), dbias=dbias)
+    assert torch.equal(qkv.grad, torch.cat(want, -1))
+    assert torch.allclose(tab.grad, dbias, rtol=1e-5, atol=1e-6)  # float-atomic summation order
+
+
+def test_backward_rejects_unsupported_shapes(dev):
+    q = torch.zeros(4, 49, 96, dtype=torch.bfloat16, device=dev, requires_grad=True)
+    o = autograd.window_attention(q, q, q, 3, (7, 7), 32 ** -0.5)
+    with pytest.raises(NotImplementedError):
+        o.sum().backward()
+    x = torch.zeros(4, 64, 96, device=dev)
+    with pytest.raises(ValueError):
+        kernels.window_attention_backward(x, x, x, x, 3, (8, 8), 1.0)
+
+
+@pytest.mark.parametrize("slab", [False, True])
+def test_partition_reverse_gradients(dev, slab):
+    """Gradients through the partition and reverse kernels equal the oracle's
+    autograd through its pad / roll / partition restatement, bit for bit."""
+    if slab:
+        B, H, W, C, geo = 2, 20, 32, 64, dict(pad=(0, 4, 0, 0), win_row_begin=1, win_rows=2, valid=(1, 7))
+    else:
+        B, H, W, C, geo = 2, 16, 24, 64, {}
+    g = WindowGeometry(B, H, W, C, 8, 4, 4, geo.get("pad", (0, 0, 0, 0)), geo.get("win_row_begin", 0),
+                       geo.get("win_rows"), geo.get("valid"))
+    x = workloads.activations((B, H, W, C), 340).to(torch.bfloat16)
+    gw = workloads.activations((g.num_windows, 64, C), 341).to(torch.bfloat16)
+    xd = x.to(dev).requires_grad_(True)
+    autograd.partition(xd, g).backward(gw.to(dev))
+    xr = x.float().requires_grad_(True)
+    so.partition_frame(xr, 8, 4, 4, **geo).backward(gw.float())
+    assert torch.equal(xd.grad.float().cpu(), xr.grad)
+
+    win = gw.to(dev).requires_grad_(True)
+    res = x.to(dev).requires_grad_(True)
+    gy = workloads.activations((B, H, W, C), 342).to(torch.bfloat16)
+    autograd.reverse(win, g, residual=res).backward(gy.to(dev))
+    wr = gw.float().requires_grad_(True)
+    rr = x.float().requires_grad_(True)
+    so.reverse_frame(wr, B, H, W, 8, 4, 4, residual=rr, **geo).backward(gy.float())
+    assert torch.equal(win.grad.float().cpu(), wr.grad)
+    assert torch.equal(res.grad.float().cpu(), rr.grad)
+
+
+def _normwise(got, ref):
+    got = got.double().cpu()
+    ref = ref.double().cpu()
+    return ((got - ref).norm() / ref.norm()).item()
+
+
+@pytest.mark.parametrize("layer_idx,use_land", [(0, False), (1, True)])
+def test_block_backward_matches_oracle(dev, layer_idx, use_land):
+    """SequentialSwinTransformer.backward (bf16; torch LayerNorm and Linears,
+    HIP partition / attention / reverse) against the fp32 oracle block under
+    autograd: input gradient and every parameter gradient."""
+    H, W, C, heads = 32, 48, 192, 6
+    land = workloads.land_mask(H, W, seed=7) if use_land else None
+    blk = SequentialSwinTransformer(layer_idx=layer_idx, height=H, width=W, embedding_dim=C, window_size=8,
+                                    num_heads=heads, land_mask=land)
+    workloads.init_block_params(blk, layer_idx)
+    with torch.no_grad():  # O(1) attention logits so the softmax is not near-uniform
+        for lin in (blk.attn.q_linear, blk.attn.k_linear):
+            lin.weight.mul_(4.0)
+        blk.attn.proj.weight.mul_(8.0)  # the attention term is O(1) next to the residual
+        blk.attn.relative_position_bias_table.mul_(25.0)
+    params = {n: p.detach().to(torch.bfloat16).float().clone().requires_grad_(True)
+              for n, p in blk.named_parameters()}
+    blk = blk.to(dev).to(torch.bfloat16)
+    x = workloads.activations((2, H * W, C), 350).to(torch.bfloat16)
+    gy = workloads.activations((2, H * W, C), 351).to(torch.bfloat16)
+    xd = x.to(dev).requires_grad_(True)
+    y = blk(xd)
+    y.backward(gy.to(dev))
+    xr = x.float().requires_grad_(True)
+    yr = so.swin_block_attention(xr, H, W, 8, blk.shift_size, heads, params, land=land)
+    yr.backward(gy.float())
+    assert _normwise(y.detach(), yr.detach()) <= 2e-2
+    assert _normwise(xd.grad, xr.grad) <= 3e-2
+    for name, p in blk.named_parameters():
+        assert p.grad is not None, name
+        if name == "attn.k_linear.bias":
+            # Softmax is invariant to q.b_k, constant over a query's keys: the
+            # exact gradient is 0 and what remains is the rounding of
+            # sum_j dz_ij (zero in exact arithmetic).  Bound it by the scale
+            # of the query-bias gradient, which has no such cancellation.
+            ref_scale = params["attn.q_linear.bias"].grad.norm().item()
+            got = p.grad.double().norm().item()
+            assert got <= 3e-2 * ref_scale, (got, ref_scale)
+            continue
+        assert _normwise(p.grad, params[name].grad) <= 3e-2, name

@@ -177,6 +177,33 @@ def test_attention_core_equals_sdpa_without_bias_and_mask():
     torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
 
 
+def test_attention_core_gradient_is_the_derivative():
+    # Backward parity (row f3) takes torch autograd of this restatement as the
+    # reference gradient: finite differences pin it for q, k, v and the bias
+    # table, with the shift mask on.
+    B_, N, C, nH = 4, 16, 8, 2
+    q, k, v = (_rand((B_, N, C), s).requires_grad_(True) for s in (50, 51, 52))
+    table = _rand((49, nH), 53).requires_grad_(True)
+    mask = so.shift_mask(8, 8, 4, 2).double()
+    fn = lambda q_, k_, v_, t_: so.window_attention_core(q_, k_, v_, nH, 0.35, t_, (4, 4), mask,  # noqa: E731
+                                                         compute_dtype=torch.float64)
+    assert torch.autograd.gradcheck(fn, (q, k, v, table), eps=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("H,pad,r0,rows,valid", [(16, (0, 0, 0, 0), 0, None, None),
+                                                  (20, (0, 4, 0, 0), 1, 2, (1, 7))])
+def test_partition_and_reverse_are_adjoint(H, pad, r0, rows, valid):
+    # <partition(x), w> == <x, reverse(w)>: the gradient of partition is
+    # reverse and vice versa (what the autograd wrappers of the kernels use).
+    B, W, C = 2, 32, 3
+    x = _rand((B, H, W, C), 60)
+    win = so.partition_frame(x, 8, 4, 4, pad, r0, rows, valid)
+    w = _rand(tuple(win.shape), 61)
+    lhs = (win * w).sum().item()
+    rhs = (x * so.reverse_frame(w, B, H, W, 8, 4, 4, pad, r0, rows, valid)).sum().item()
+    assert abs(lhs - rhs) <= 1e-9 * max(1.0, abs(lhs))
+
+
 def test_padded_keys_reduce_to_real_window():
     # keys >= n_real get -10000, so their weight underflows to exactly 0: the
     # result on the real rows equals attention over the first n_real tokens.
