@@ -16,10 +16,13 @@
 //   phase 1 (wave = query tiles 2*half, 2*half + 1): S^T and dP^T on MFMA in
 //     the forward's layout (lane = one query, 16 keys), softmax, dz; P and dz
 //     go to LDS as [query][key] bf16 tiles; dQ^T = K^T dz^T straight from the
-//     dz accumulators (the forward's P^T-operand trick) and out to memory.
+//     dz accumulators (the forward's P^T-operand trick).
 //   phase 2 (wave = keys [32*half, 32*half + 32)): dV^T = dO^T P and
 //     dK^T = Q^T dz with both operands read across rows of the LDS tiles
 //     (transposing LDS reads), contraction over all 64 queries.
+// dQ, dK and dV are staged in the V, K and dout tiles once those are dead and
+// leave as whole 128-byte row slices (8-byte accumulator stores straight to
+// memory made the kernel twice as slow).
 #include "common.h"
 #include "attn_core.h"
 
@@ -113,25 +116,33 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) gz[il][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int unit = blockIdx.x; unit < units; unit += gridDim.x) {
+  // q, k, v, dout rows of one unit's head group -> registers (nontemporal).
+  uint4 buf[4][kPer];
+  auto fetch = [&](int unit) {
+    const int64_t row_base = (int64_t)(unit / p.groups) * kNPad + row0;
+    const int col = hg * G * D + chunk0 * 8;
+    const uint16_t* src[4] = {reinterpret_cast<const uint16_t*>(p.q) + row_base * p.q_stride + col,
+                              reinterpret_cast<const uint16_t*>(p.k) + row_base * p.k_stride + col,
+                              reinterpret_cast<const uint16_t*>(p.v) + row_base * p.v_stride + col,
+                              reinterpret_cast<const uint16_t*>(p.o) + row_base * p.o_stride + col};
+    const int64_t step[4] = {kRowStep * p.q_stride, kRowStep * p.k_stride, kRowStep * p.v_stride,
+                             kRowStep * p.o_stride};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int u = 0; u < kPer; ++u)
+        buf[t][u] = __builtin_bit_cast(
+            uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[t] + u * step[t])));
+  };
+
+  // Persistent loop, software-pipelined: the loads of unit n + gridDim.x are
+  // issued once unit n's phase 1 is done and land during its phase 2.
+  int unit = blockIdx.x;  // < units: the grid is never larger than the work
+  fetch(unit);
+  for (;;) {
     const int w = unit / p.groups;
     // ---- q, k, v, dout rows of the head group -> LDS --------------------------
     {
-      const int64_t row_base = (int64_t)w * kNPad + row0;
-      const int col = hg * G * D + chunk0 * 8;
-      const uint16_t* src[4] = {reinterpret_cast<const uint16_t*>(p.q) + row_base * p.q_stride + col,
-                                reinterpret_cast<const uint16_t*>(p.k) + row_base * p.k_stride + col,
-                                reinterpret_cast<const uint16_t*>(p.v) + row_base * p.v_stride + col,
-                                reinterpret_cast<const uint16_t*>(p.o) + row_base * p.o_stride + col};
-      const int64_t step[4] = {kRowStep * p.q_stride, kRowStep * p.k_stride, kRowStep * p.v_stride,
-                               kRowStep * p.o_stride};
-      uint4 buf[4][kPer];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int u = 0; u < kPer; ++u)
-          buf[t][u] = __builtin_bit_cast(
-              uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[t] + u * step[t])));
       __syncthreads();  // the previous unit is done with every tile
       uint8_t* dst[4] = {qs, ks, vs, dos};
 #pragma unroll
@@ -208,23 +219,25 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       }
     }
     // dQ^T = K^T dz^T (dz accumulators as the P^T operand), times scale.
+    f32x4 dqa[D / 16][2];
     {
-      f32x4 o[D / 16][2];
       auto kfrag = [&](int ct, int js) -> bf16x8 { return rows_frag(ks, cpr, head * D + 16 * ct, js, lane); };
-      pv_half<true, D>(o, dp, lane, kfrag);
-      const uint16_t* base = reinterpret_cast<const uint16_t*>(bp.dq) + (int64_t)w * kNPad * bp.dq_stride;
-      const __amdgpu_buffer_rsrc_t out =
-          buffer_rsrc(base, (uint32_t)(((int64_t)(kNPad - 1) * bp.dq_stride + p.heads * D) * 2));
+      pv_half<true, D>(dqa, dp, lane, kfrag);
+    }
+    __syncthreads();  // P and dz tiles of both halves are in LDS; K and V are no longer read
+    // dQ rows of this wave -> the V tile (lane: 4 channels of query row i).
 #pragma unroll
-      for (int il = 0; il < 2; ++il) {
-        const int i = 16 * (2 * half + il) + c16;
+    for (int il = 0; il < 2; ++il) {
+      const int i = 16 * (2 * half + il) + c16;
 #pragma unroll
-        for (int ct = 0; ct < D / 16; ++ct)
-          stream_store_sc1(pack4_bf16(o[ct][il] * bp.scale), out,
-                           (uint32_t)(i * bp.dq_stride + h * D + 16 * ct + 4 * g) * 2);
+      for (int ct = 0; ct < D / 16; ++ct) {
+        const int cc = head * D + 16 * ct + 4 * g;
+        *reinterpret_cast<uint2*>(vs + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) =
+            pack4_bf16(dqa[ct][il] * bp.scale);
       }
     }
-    __syncthreads();  // P and dz tiles of both halves are in LDS
+    const int next = unit + (int)gridDim.x;
+    if (next < units) fetch(next);
 
     // ---- phase 2: keys [32*half, 32*half + 32) of head `head` -----------------
     {
@@ -252,25 +265,52 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
           }
         }
       }
-      // lane (c16, g) of tile (ct, jt): channels 16ct + 4g .. + 3 of key 32half + 16jt + c16
-      const int64_t wrow = (int64_t)w * kNPad;
-      const __amdgpu_buffer_rsrc_t ov = buffer_rsrc(
-          reinterpret_cast<const uint16_t*>(bp.dv) + wrow * bp.dv_stride,
-          (uint32_t)(((int64_t)(kNPad - 1) * bp.dv_stride + p.heads * D) * 2));
-      const __amdgpu_buffer_rsrc_t ok = buffer_rsrc(
-          reinterpret_cast<const uint16_t*>(bp.dk) + wrow * bp.dk_stride,
-          (uint32_t)(((int64_t)(kNPad - 1) * bp.dk_stride + p.heads * D) * 2));
+      // lane (c16, g) of tile (ct, jt): channels 16ct + 4g .. + 3 of key 32half + 16jt + c16.
+      // dK -> the K tile (not read since phase 1); dV -> the dout tile once
+      // every wave is done reading it.
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt) {
         const int j = 32 * half + 16 * jt + c16;
 #pragma unroll
         for (int ct = 0; ct < D / 16; ++ct) {
-          const int col = h * D + 16 * ct + 4 * g;
-          stream_store_sc1(pack4_bf16(av[ct][jt]), ov, (uint32_t)(j * bp.dv_stride + col) * 2);
-          stream_store_sc1(pack4_bf16(ak[ct][jt] * bp.scale), ok, (uint32_t)(j * bp.dk_stride + col) * 2);
+          const int cc = head * D + 16 * ct + 4 * g;
+          *reinterpret_cast<uint2*>(ks + tile_slot(j, cc >> 3, cpr) * 16 + (cc & 7) * 2) =
+              pack4_bf16(ak[ct][jt] * bp.scale);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) {
+        const int j = 32 * half + 16 * jt + c16;
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) {
+          const int cc = head * D + 16 * ct + 4 * g;
+          *reinterpret_cast<uint2*>(dos + tile_slot(j, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pack4_bf16(av[ct][jt]);
         }
       }
     }
+    __syncthreads();
+    // ---- dq (V tile), dk (K tile), dv (dout tile) -> memory, whole rows -------
+    {
+      const int col = hg * G * D + chunk0 * 8;
+      const uint8_t* src[3] = {vs, ks, dos};
+      void* const dst[3] = {bp.dq, bp.dk, bp.dv};
+      const int64_t stride[3] = {bp.dq_stride, bp.dk_stride, bp.dv_stride};
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const uint16_t* base = reinterpret_cast<const uint16_t*>(dst[t]) + (int64_t)w * kNPad * stride[t];
+        const __amdgpu_buffer_rsrc_t out =
+            buffer_rsrc(base, (uint32_t)(((int64_t)(kNPad - 1) * stride[t] + p.heads * D) * 2));
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+          const int row = row0 + kRowStep * u;
+          const uint4 val = *reinterpret_cast<const uint4*>(src[t] + tile_slot(row, chunk0, cpr) * 16);
+          stream_store_sc1(val, out, (uint32_t)(row * stride[t] + col) * 2);
+        }
+      }
+    }
+    if (next >= units) break;
+    unit = next;
   }
 
   // ---- bias gradient: registers -> LDS column -> global table ----------------
