@@ -73,8 +73,9 @@ def measured_traffic():
 
 def run_kernels(cfg, blk, x, steps):
     """The step's kernels on the step's own tensors, `steps` times: the fused
-    block kernel, then the five-stage path's three HIP kernels; then a device
-    copy of 192 MiB (the counter calibration)."""
+    block kernel, then the five-stage path's three HIP kernels, then the
+    attention backward on the same q / k / v; then a device copy of 192 MiB
+    (the counter calibration)."""
     import torch
 
     from terra_amd import kernels
@@ -92,6 +93,14 @@ def run_kernels(cfg, blk, x, steps):
             win = kernels.swin_partition_ln(grid, geom, blk.norm1.weight, blk.norm1.bias, blk.norm1.eps)
             o = blk.attn.core(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], mask=mask)
             kernels.swin_reverse(o, geom, residual=grid)
+        dqkv = torch.empty_like(qkv)
+        dbias = torch.zeros_like(blk.attn.relative_position_bias_table, dtype=torch.float32)
+        for _ in range(steps):
+            kernels.window_attention_backward(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], o, blk.attn.num_heads,
+                                              blk.attn.window_size, blk.attn.scale,
+                                              bias_table=blk.attn.relative_position_bias_table, mask=mask,
+                                              dq=dqkv[..., :C], dk=dqkv[..., C:2 * C], dv=dqkv[..., 2 * C:],
+                                              dbias=dbias)
         src = torch.ones(192 << 20, dtype=torch.uint8, device=x.device)
         dst = torch.zeros_like(src)
         for _ in range(3):
@@ -241,6 +250,20 @@ def main():
         ms_five = run(max(5, args.steps // 2), 10)
         blk.use_fused_block = True
         iso = {k: isolated_us(k) for k in ("partition", "window_attention", "reverse")}
+        # The training-path backward of the same attention call (row f3): the
+        # step's q / k / v, a synthetic output gradient, dq | dk | dv into one
+        # [B_, N, 3C] buffer and the bias-table gradient.
+        fn, a, kw = last_call["window_attention"]
+        q_, k_, v_ = a[0], a[1], a[2]
+        dout = torch.randn(q_.shape, generator=torch.Generator(device=q_.device).manual_seed(7), device=q_.device,
+                           dtype=q_.dtype)
+        dqkv = torch.empty(q_.shape[:-1] + (3 * q_.shape[-1],), device=q_.device, dtype=q_.dtype)
+        C_ = q_.shape[-1]
+        dbias = None if kw.get("bias_table") is None else torch.zeros_like(kw["bias_table"], dtype=torch.float32)
+        last_call["attention_backward"] = (kernels.window_attention_backward, (q_, k_, v_, dout) + tuple(a[3:]), dict(
+            bias_table=kw.get("bias_table"), mask=kw.get("mask"), dq=dqkv[..., :C_], dk=dqkv[..., C_:2 * C_],
+            dv=dqkv[..., 2 * C_:], dbias=dbias))
+        iso["attention_backward"] = isolated_us("attention_backward")
     finally:
         for n in names:
             setattr(kernels, n, orig[n])
@@ -255,6 +278,8 @@ def main():
     core_flops = 4.0 * n_real * n_real * C * B_
     core_bytes = 4.0 * B_ * N * C * elt
     part_bytes = grid_bytes + B_ * N * C * elt
+    bwd_bytes = 7.0 * B_ * N * C * elt
+    bwd_flops = 10.0 * n_real * n_real * C * B_
     rev_bytes = B_ * N * C * elt + 2 * grid_bytes
 
     def avg_us(name):
@@ -319,6 +344,19 @@ def main():
             "reverse_residual": {"us": iso["reverse"],
                                  "GB_s": rev_bytes / (iso["reverse"] * 1e-6) / 1e9,
                                  "hbm_frac": rev_bytes / (iso["reverse"] * 1e-6) / 1e9 / HBM_PEAK_GBS},
+        },
+        # Training path (row f3): backward of the attention core on the same
+        # call, timed alone.  Algorithmic bytes: read q, k, v, dout and write
+        # dq, dk, dv (7 N C elt per window); FLOPs: S recomputed, dP, dV, dQ,
+        # dK (10 N^2 C per window).
+        "attention_backward": {
+            "kernel": "window_attn_bwd_kernel<32, 2>",
+            "us": iso["attention_backward"],
+            "GB_s": bwd_bytes / (iso["attention_backward"] * 1e-6) / 1e9,
+            "hbm_frac": bwd_bytes / (iso["attention_backward"] * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "TFLOP_s": bwd_flops / (iso["attention_backward"] * 1e-6) / 1e12,
+            "algorithmic_bytes_per_launch": bwd_bytes,
+            "algorithmic_flops_per_launch": bwd_flops,
         },
     }
     if not args.no_cpu_baseline:
