@@ -95,7 +95,8 @@ struct WindowMaskState {
   uint64_t land;      // land bit per key
 };
 
-__device__ __forceinline__ WindowMaskState window_mask_state(const AttnParams& p, int w, bool analytic) {
+__device__ __forceinline__ WindowMaskState window_mask_state(const AttnParams& p, int w, bool analytic,
+                                                             bool read_land = true) {
   WindowMaskState m;
   m.use_shift = false;
   m.wr = m.wc = 0;
@@ -107,7 +108,7 @@ __device__ __forceinline__ WindowMaskState window_mask_state(const AttnParams& p
     m.wc = wl - rr * p.win_cols;
     m.use_shift = (m.wr + 2) * p.window_h > p.frame_h || (m.wc + 2) * p.window_w > p.frame_w;
   }
-  m.land = p.land_bits != nullptr ? p.land_bits[w % p.mask_windows] : 0ull;
+  m.land = (read_land && p.land_bits != nullptr) ? p.land_bits[w % p.mask_windows] : 0ull;
   m.use_mask = m.use_shift || m.land != 0ull;
   return m;
 }
@@ -397,6 +398,30 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* addr) {
   return __builtin_bit_cast(uint2, r);
 }
 
+// Workgroup barrier for LDS hand-offs only.  __syncthreads() also waits for
+// every outstanding global load and store of the wave (s_waitcnt vmcnt(0)),
+// which would drain prefetches and output stores at each barrier; this waits
+// for the wave's LDS operations only.  Data loaded into LDS by global->LDS
+// DMA needs its own s_waitcnt vmcnt before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One 16-byte global -> LDS load per lane (nontemporal): lane l of the wave
+// writes LDS bytes [lds_base + 16 l, +16).  Issued from inline assembly so
+// that the compiler does not place an s_waitcnt vmcnt(0) before every later
+// LDS read (it cannot tell which LDS bytes the load writes); the caller waits
+// for it with an explicit vmcnt.  lds_base is wave-uniform (it goes to M0).
+__device__ __forceinline__ void dma_to_lds16(const void* src, uint32_t lds_base) {
+  // M0 is bound by the operand constraint (the compiler writes it); the
+  // s_nop is the wait state between an M0 write and an LDS DMA.
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" : : "v"(src), "{m0}"(lds_base) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // 16-byte chunk slot of (row, chunk) in a [64][cpr] tile: the chunk index is
 // XOR-swizzled within its aligned group of 8 so that the 16 rows read by one
 // fragment load (and the 4 row groups of a V^T read) hit distinct banks.
@@ -469,18 +494,21 @@ __device__ __forceinline__ void tile_attention_wave(uint8_t* qs, const uint8_t* 
 }
 
 // Scores, softmax and O^T = V^T P^T of one 16-query tile `it` of an 8x8
-// window against its 64 keys, for a Q operand that already carries
-// scale * log2(e).  The additive terms (relative-position bias at
-// tab8[30*(it - jt) - r + 93], land keys, shift regions, all x log2e) are the
-// accumulator init of the S^T MFMA, so the logits leave the MFMA ready for
-// the softmax.  land_term[jt][r]: mask_l2e for land key 16jt + 4g + r, else 0.
-// kf[jt]: K operand of key tile jt; vfrag(ct, js): V^T operand (keys 32js +
-// 16(e/4) + 4g + e%4).  Returns the unnormalised O^T tiles and 1/rowsum.
+// window against its 64 keys.  The additive terms (relative-position bias at
+// tab8[30*(it - jt) - r + 93], land keys, shift regions) are the accumulator
+// init of the S^T MFMA, in the units of the accumulator: the base-2 logit is
+// acc * logit_scale.  With a Q operand that already carries scale * log2(e),
+// logit_scale = 1 and the terms are x log2e; with raw q, logit_scale =
+// scale * log2(e) (> 0) and the terms are divided by scale.
+// land_term[jt][r]: mask term of land key 16jt + 4g + r, else 0; mask_term:
+// the shift-region term.  kf[jt]: K operand of key tile jt; vfrag(ct, js):
+// V^T operand (keys 32js + 16(e/4) + 4g + e%4).  Returns the unnormalised O^T
+// tiles and 1/rowsum.
 template <class VFrag>
 __device__ __forceinline__ void attend_qtile(f32x4 (&o)[2], float& inv, int it, const uint4 (&kf)[4],
                                              const uint4& qf, const float* tab8, const WindowMaskState& m,
                                              const f32x4 (&land_term)[4], uint64_t rid_pack, int rid_q,
-                                             float mask_l2e, VFrag vfrag) {
+                                             float mask_term, float logit_scale, VFrag vfrag) {
   f32x4 s[4];
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
@@ -492,7 +520,7 @@ __device__ __forceinline__ void attend_qtile(f32x4 (&o)[2], float& inv, int it, 
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int rid_j = (int)((rid_pack >> (4 * (4 * jt + r))) & 15ull);
-        s[jt][r] += (rid_j != rid_q ? mask_l2e : 0.f) + land_term[jt][r];
+        s[jt][r] += (rid_j != rid_q ? mask_term : 0.f) + land_term[jt][r];
       }
   } else if (m.land != 0ull) {
 #pragma unroll
@@ -508,12 +536,13 @@ __device__ __forceinline__ void attend_qtile(f32x4 (&o)[2], float& inv, int it, 
 #pragma unroll
     for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[jt][r]);
   mx = xor_max(mx);
+  const float neg_mx = -mx * logit_scale;  // logit_scale > 0: the max commutes with the scaling
   float sum = 0.f;
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float e = __builtin_amdgcn_exp2f(s[jt][r] - mx);
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt][r], logit_scale, neg_mx));
       s[jt][r] = e;
       sum += e;
     }

@@ -136,10 +136,6 @@ __device__ __forceinline__ uint4 weight_frag(const uint16_t* w, int rt, int ks, 
     return *reinterpret_cast<const uint4*>(w + (int64_t)(16 * rt + (lane & 15)) * kC + 32 * ks + 8 * (lane >> 4));
 }
 
-// Cache-policy bits of the global -> LDS loads: nontemporal (every x byte is
-// read once; the weights should keep L2).
-constexpr int kNtAux = 2;
-
 // Mask terms of an emitted window (shift regions over the padded frame, land
 // keys of the slab window).
 __device__ __forceinline__ WindowMaskState block_mask_state(const BlockParams& p, const UnitLoc u) {
@@ -147,7 +143,12 @@ __device__ __forceinline__ WindowMaskState block_mask_state(const BlockParams& p
   m.wr = u.wr;
   m.wc = u.wc;
   m.use_shift = p.shift_mask && ((u.wr + 2) * 8 > p.Hp || (u.wc + 2) * 8 > p.Wp);
-  m.land = p.land_bits != nullptr ? p.land_bits[u.w_slab % p.land_windows] : 0ull;
+  // The land word through the scalar (constant) path: a vector load would be
+  // waited for together with the next window's rows in flight.
+  m.land = p.land_bits != nullptr
+               ? ((const __attribute__((address_space(4))) uint64_t*)
+                      p.land_bits)[__builtin_amdgcn_readfirstlane(u.w_slab % p.land_windows)]
+               : 0ull;
   m.use_mask = m.use_shift || m.land != 0ull;
   return m;
 }
@@ -171,8 +172,7 @@ __device__ __forceinline__ void fetch_window(const BlockParams& p, const UnitLoc
     const int ch = (sl - row * kCpr) ^ ((row >> 1) & 7);
     const int t = grid_token(p, u, row >> 3, row & 7);
     const uint8_t* src = p.x + (int64_t)(t >= 0 ? t : 0) * (kCpr * 16) + ch * 16;
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)(dst + blk * 1024), 16, 0, kNtAux);
+    dma_to_lds16(src, __builtin_amdgcn_readfirstlane(lds_address(dst + blk * 1024)));
   }
 }
 
@@ -469,7 +469,7 @@ __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitL
                                   : 0;
     f32x4 o[2];
     float inv;
-    attend_qtile(o, inv, it, kf4, qf[it], tab8, m, land_term, rid_pack, rid_q, p.a.mask_l2e, vsrc);
+    attend_qtile(o, inv, it, kf4, qf[it], tab8, m, land_term, rid_pack, rid_q, p.a.mask_l2e, 1.0f, vsrc);
     const int i = 16 * it + c16;
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
@@ -723,7 +723,9 @@ __global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockPara
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
     }
-    __syncthreads();
+    // LDS hand-off only: the next window's rows stay in flight across the
+    // slots between phase B and phase D, and the output stores are not waited.
+    lds_barrier();
   }
 }
 

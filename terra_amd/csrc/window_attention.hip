@@ -147,6 +147,196 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
 }
 
 // ============================================================================
+// ring kernel: head dim 32, one query tile per wave, loads two windows ahead
+// ============================================================================
+//
+// One workgroup per (window, head group of G heads), persistent, and a fixed
+// head group per workgroup (the grid is a multiple of the number of groups).
+// Four waves per head, one 16-query tile each.  q, k, v of a unit go straight
+// from memory into one of three LDS buffers by direct global->LDS loads,
+// issued two units ahead, so a workgroup never holds loads in registers and
+// always has two units in flight.  The additive terms are in raw-score units
+// (bias / scale), added as the accumulator init of S^T (attend_qtile).
+
+constexpr int kRingBufs = 3;
+
+template <int G>
+constexpr int ring_lds_bytes() {
+  return kRingBufs * 3 * kNPad * (G * 4) * 16 + G * kTableMax * (int)sizeof(float);
+}
+
+template <int G>
+__global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int D = 32;
+  constexpr int nthreads = G * 256;
+  constexpr int cpr = G * D / 8;                  // chunks per row (multiple of 8)
+  constexpr int tile_bytes = kNPad * cpr * 16;
+  constexpr int unit_bytes = 3 * tile_bytes;
+  constexpr int kRounds = unit_bytes / (nthreads * 16);  // 16-byte loads per thread per unit
+  constexpr int kBlocksPerTile = tile_bytes / 1024;
+  static_assert(cpr % 8 == 0 && kRounds * nthreads * 16 == unit_bytes, "whole 1 KB blocks per wave");
+  static_assert(kRounds == 3, "the vmcnt wait below counts 3 loads per thread per unit");
+  float* tables = reinterpret_cast<float*>(smem + kRingBufs * unit_bytes);
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int head = wave >> 2;                     // head of the group
+  const int it = wave & 3;                        // query tile
+  const int lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int windows = p.items / p.heads;
+  // Units are (window, head group) pairs, unit = window * groups + hg; the
+  // grid is a multiple of groups, so this workgroup keeps head group hg and
+  // steps through windows w0, w0 + wstride, ...
+  const int hg = blockIdx.x % p.groups;
+  const int w0 = blockIdx.x / p.groups;
+  const int wstride = gridDim.x / p.groups;
+  const int h = hg * G + head;
+
+  // Bias column of this head in raw-score units; the head's four waves split it.
+  float* tab = tables + head * kTableMax;
+  const float tab_mul = kLog2e / p.scale_l2e;     // = 1 / scale
+  for (int e = lane + 64 * it; e < kTableMax; e += 256)
+    tab[e] = (p.bias_table != nullptr && e < p.table_size) ? p.bias_table[(int64_t)e * p.heads + h] * tab_mul : 0.f;
+  const float mask_term = p.mask_l2e / p.scale_l2e;  // mask_value / scale
+
+  // This thread's part of a unit's loads: one 1 KB block of one tensor per
+  // wave and round, LDS slot s of the block holding (row, chunk) with
+  // tile_slot(row, chunk) = block * 64 + s.  Per round: the tensor, its row
+  // stride, the element offset inside the window's rows and the LDS block.
+  const uint16_t* src_base[kRounds];
+  int64_t src_stride[kRounds];
+  int32_t src_off[kRounds];
+  int32_t lds_blk[kRounds];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int blk = r * (nthreads / 64) + wave;   // 0 .. 3 * kBlocksPerTile - 1
+    const int t = blk / kBlocksPerTile;           // 0 q, 1 k, 2 v
+    const int sl = (blk - t * kBlocksPerTile) * 64 + lane;
+    const int row = sl / cpr;
+    const int ch = (sl - row * cpr) ^ ((row >> 1) & 7);
+    src_base[r] = t == 0 ? reinterpret_cast<const uint16_t*>(p.q)
+                         : t == 1 ? reinterpret_cast<const uint16_t*>(p.k) : reinterpret_cast<const uint16_t*>(p.v);
+    src_stride[r] = t == 0 ? p.q_stride : t == 1 ? p.k_stride : p.v_stride;
+    src_off[r] = (int32_t)(row * src_stride[r]) + hg * G * D + ch * 8;
+    lds_blk[r] = blk * 1024;
+  }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  auto issue = [&](int w, int buf) {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r)
+      dma_to_lds16(src_base[r] + (int64_t)w * kNPad * src_stride[r] + src_off[r],
+                   lds0 + buf * unit_bytes + lds_blk[r]);
+  };
+
+  int w = w0;                                     // < windows: the grid is never larger than the work
+  issue(w, 0);
+  if (w + wstride < windows) issue(w + wstride, 1);
+  // Per lane: the bias of element (it, jt, r) sits at tab8[30*(it - jt) - r + 93].
+  const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;  // in [93, 134]
+  const float* tab8 = tab + (lane_base - 93);
+  const int hc = head * 4;                        // first chunk of this head
+  const int orow = tid / cpr, ochunk = tid - (tid / cpr) * cpr;  // this thread's O chunk
+  for (int n = 0;; ++n) {
+    const int buf = n % kRingBufs;
+    const bool more = w + wstride < windows;
+    // This unit's loads are complete once at most the next unit's kRounds
+    // loads are outstanding.  Loads complete in order among themselves, but
+    // not in order with stores, so the count covers later loads only: with
+    // the previous unit's O store still pending, vmcnt(3) waits for more.
+    if (more) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();                                // every wave's part of the unit is in LDS
+    // Unit n + 2 goes into the buffer of unit n - 1, whose O every thread has
+    // read out before the barrier above.
+    if (w + 2 * wstride < windows) issue(w + 2 * wstride, (n + 2) % kRingBufs);
+    uint8_t* qs = smem + buf * unit_bytes;
+    const uint8_t* ks = qs + tile_bytes;
+    const uint8_t* vs = qs + 2 * tile_bytes;
+    // Mask state of the window.  The land word is read through the scalar
+    // (constant) path: a vector load here would be waited for together with
+    // the loads in flight for the next units.
+    WindowMaskState m = window_mask_state(p, w, true, /*land=*/false);
+    if (p.land_bits != nullptr) {
+      const int li = __builtin_amdgcn_readfirstlane(w % p.mask_windows);
+      m.land = ((const __attribute__((address_space(4))) uint64_t*)p.land_bits)[li];
+      m.use_mask = m.use_shift || m.land != 0ull;
+    }
+    {
+      uint4 kf[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        kf[t] = *reinterpret_cast<const uint4*>(ks + tile_slot(16 * t + c16, hc + g, cpr) * 16);
+      const uint4 qf = *reinterpret_cast<const uint4*>(qs + tile_slot(16 * it + c16, hc + g, cpr) * 16);
+      auto vfrag = [&](int ct, int js) -> bf16x8 {
+        const int cc = head * D + 16 * ct + 4 * (c16 & 3);  // channel of this source lane
+        uint2 part[2];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int row = 32 * js + 16 * h2 + 4 * g + (c16 >> 2);
+          part[h2] = lds_read_tr16(vs + tile_slot(row, cc >> 3, cpr) * 16 + (cc & 7) * 2);
+        }
+        const uint32_t wd[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
+        return __builtin_bit_cast(bf16x8, wd);
+      };
+      f32x4 land_term[4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) land_term[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (m.land != 0ull) {                        // uniform: only windows with land keys
+        const uint64_t land_lane = m.land >> (4 * g);
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) land_term[jt][r] = ((land_lane >> (16 * jt + r)) & 1ull) ? mask_term : 0.f;
+      }
+      uint64_t rid_pack = 0;
+      int rid_q = 0;
+      if (m.use_shift) {
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            rid_pack |= (uint64_t)(3 * region(m.wr * 8 + 2 * jt + (g >> 1), p.frame_h, 8, p.shift_h) +
+                                   region(m.wc * 8 + 4 * (g & 1) + r, p.frame_w, 8, p.shift_w))
+                        << (4 * (4 * jt + r));
+        rid_q = 3 * region(m.wr * 8 + 2 * it + (c16 >> 3), p.frame_h, 8, p.shift_h) +
+                region(m.wc * 8 + (c16 & 7), p.frame_w, 8, p.shift_w);
+      }
+      f32x4 o[2];
+      float inv;
+      attend_qtile(o, inv, it, kf, qf, tab8, m, land_term, rid_pack, rid_q, mask_term, p.scale_l2e, vfrag);
+      // O over this wave's own Q rows (read above, before any write).
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      const int i = 16 * it + c16;
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const f32x4 v = o[ct] * inv;
+        const int cc = head * D + 16 * ct + 4 * g;  // 4 channels, 8 bytes
+        uint2 pk;
+        pk.x = pack_bf16x2(v[0], v[1]);
+        pk.y = pack_bf16x2(v[2], v[3]);
+        *reinterpret_cast<uint2*>(qs + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
+      }
+    }
+    lds_barrier();                                // O complete
+    {
+      // One whole-line store per thread (kNPad * cpr chunks == nthreads).
+      static_assert(kNPad * cpr == nthreads, "one O chunk per thread");
+      const uint16_t* slice = reinterpret_cast<const uint16_t*>(p.o) + (int64_t)w * kNPad * p.o_stride + hg * G * D;
+      const __amdgpu_buffer_rsrc_t out =
+          buffer_rsrc(slice, (uint32_t)(((int64_t)(kNPad - 1) * p.o_stride + G * D) * 2));
+      const u32x4 val =
+          __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(qs + tile_slot(orow, ochunk, cpr) * 16));
+      stream_store_sc1(val, out, (uint32_t)(orow * p.o_stride + ochunk * 8) * 2);
+    }
+    if (!more) break;
+    w += wstride;
+  }
+}
+
+// ============================================================================
 // per-wave kernel (generic path)
 // ============================================================================
 
@@ -347,6 +537,36 @@ int launch_tile(const AttnParams& p, hipStream_t s) {
   return TERRA_OK;
 }
 
+// Persistent grid of the ring kernel: as many workgroups as the device holds
+// at once, rounded down to a multiple of the head groups (each workgroup keeps
+// one head group), never more than the work.
+template <int G>
+int launch_ring(const AttnParams& p, hipStream_t s) {
+  constexpr int lds = ring_lds_bytes<G>();
+  auto kern = window_attn_ring_kernel<G>;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  constexpr int kMaxDevices = 64;
+  static int cache[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(TERRA_ERR_LAUNCH, "cannot query the current device");
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, G * 256, lds) != hipSuccess)
+      return fail(TERRA_ERR_LAUNCH, "cannot size the ring kernel grid for this device");
+    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  const int units = (p.items / p.heads) * p.groups;
+  int blocks = units < cache[dev] ? units : cache[dev];
+  blocks -= blocks % p.groups;
+  if (blocks < p.groups) blocks = p.groups;
+  kern<<<blocks, G * 256, lds, s>>>(p);
+  return TERRA_OK;
+}
+
 // Heads per workgroup of the tile kernel: the smallest divisor G of `heads`
 // among the instantiated group widths whose row slice is a whole number of
 // 128-byte lines (128, 256 or 384 bytes); 0 if there is none.  Small groups
@@ -471,7 +691,16 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
   const int G = tile_group(d.heads, D);
   const bool tile = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
                     d.n_real == 64 && d.mask_mode != TERRA_MASK_EXPLICIT && G > 0;
-  if (tile) {
+  // Head dim 32 with an even head count: the ring kernel (two heads per
+  // workgroup).  It adds bias and masks in raw-score units (bias / scale), so
+  // it needs a positive, not tiny scale.
+  const bool ring = tile && D == 32 && d.heads % 2 == 0 && d.scale >= 0x1p-20f;
+  if (ring) {
+    p.group = 2;
+    p.groups = d.heads / 2;
+    const int st = launch_ring<2>(p, s);
+    if (st != TERRA_OK) return st;
+  } else if (tile) {
     p.group = G;
     p.groups = d.heads / G;
     const int st = dispatch_tile(p, D, s);
