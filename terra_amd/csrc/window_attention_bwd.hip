@@ -143,14 +143,14 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
     const int w = unit / p.groups;
     // ---- q, k, v, dout rows of the head group -> LDS --------------------------
     {
-      __syncthreads();  // the previous unit is done with every tile
+      lds_barrier();  // the previous unit is done with every tile
       uint8_t* dst[4] = {qs, ks, vs, dos};
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int u = 0; u < kPer; ++u)
           *reinterpret_cast<uint4*>(dst[t] + tile_slot(row0 + kRowStep * u, chunk0, cpr) * 16) = buf[t][u];
-      __syncthreads();
+      lds_barrier();
     }
 
     // ---- phase 1: query tiles 2*half, 2*half + 1 of head `head` ---------------
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       auto kfrag = [&](int ct, int js) -> bf16x8 { return rows_frag(ks, cpr, head * D + 16 * ct, js, lane); };
       pv_half<true, D>(dqa, dp, lane, kfrag);
     }
-    __syncthreads();  // P and dz tiles of both halves are in LDS; K and V are no longer read
+    lds_barrier();  // P and dz tiles of both halves are in LDS; K and V are no longer read
     // dQ rows of this wave -> the V tile (lane: 4 channels of query row i).
 #pragma unroll
     for (int il = 0; il < 2; ++il) {
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
               pack4_bf16(ak[ct][jt] * bp.scale);
         }
       }
-      __syncthreads();
+      lds_barrier();
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt) {
         const int j = 32 * half + 16 * jt + c16;
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     // ---- dq (V tile), dk (K tile), dv (dout tile) -> memory, whole rows -------
     {
       const int col = hg * G * D + chunk0 * 8;
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         atomicAdd(dcol + lane_base + 30 * (2 * half + il - jt) - r, gz[il][jt][r]);
-  __syncthreads();
+  lds_barrier();
   for (int e = tid; e < G * p.table_size; e += nthreads) {
     const int hh = e / p.table_size, idx = e - hh * p.table_size;
     unsafeAtomicAdd(bp.dbias + (int64_t)idx * p.heads + hg * G + hh, dtab[hh * kTableMax + idx]);
