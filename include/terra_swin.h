@@ -209,15 +209,18 @@ int terra_swin_attn_fwd(const void* q, const void* k, const void* v, void* o,
                         const float* bias_table, const float* explicit_mask,
                         const uint64_t* land_bits, void* stream);
 
-/* Backward of terra_swin_attn_fwd (bf16, 8x8 windows, head dim 32 or 64,
- * no padded keys; any mask mode, land bits).
+/* Backward of terra_swin_attn_fwd, for the shapes the forward takes (bf16 or
+ * f32, windows up to 8x8 in at most 64 token rows, padded keys, head dim 32
+ * or 64; any mask mode, land bits).  bf16 8x8 windows without padded keys run
+ * on an MFMA kernel, the rest on a plain fp32 one.
  * Replaces the autograd backward of the same ATen sequence
  *           models/attention.py:256-278 (matmul, bias gather + add, mask add,
  *           softmax, matmul), as run by the training step
  *           core/runtime/run_model.py:362-617.
  * P is recomputed from q, k and the masks.  Writes
- *   dq = scale * dz k,  dk = scale * dz^T q,  dv = P^T dout     (bf16)
- * with dz = P * (dout v^T - rowsum(P * (dout v^T))) per window and head, and,
+ *   dq = scale * dz k,  dk = scale * dz^T q,  dv = P^T dout     (activation dtype)
+ * with dz = P * (dout v^T - rowsum(P * (dout v^T))) per window and head (zero
+ * for padded keys, which the forward overwrites with pad_key_value), and,
  * when dbias_table != NULL, ADDS sum over windows of dz[i, j] into
  * dbias_table[idx(i, j) * heads + h] (fp32, same layout as bias_table; the
  * caller zeroes it first; float atomics, so the summation order varies).

@@ -10,7 +10,9 @@ models/transformer.py:142-300).
   partition (pad window tokens get zero), both on the same geometry.
 - The attention core's backward is ``terra_swin_attn_bwd`` (P recomputed
   from q and k; dq, dk, dv, and the bias-table gradient summed over
-  windows).  For shapes that kernel is not built for, the forward still runs
+  windows): an MFMA tile kernel for bf16 8x8 windows without padded keys,
+  a plain fp32 kernel for every other shape the forward serves (fp32, 7x7
+  windows, padded keys).  For a shape neither serves the forward still runs
   and backward() raises NotImplementedError (there is no non-HIP backward).
 
 Each function runs the plain kernel when no input needs a gradient.
@@ -76,8 +78,8 @@ def reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional[torc
 def _check_backward(q: torch.Tensor, num_heads: int, window_size: Tuple[int, int], n_real: Optional[int]) -> None:
     if not kernels.attention_backward_supported(q, num_heads, window_size, n_real):
         raise NotImplementedError(
-            "terra_amd: the attention backward kernel is built for bf16 activations, 8x8 windows of 64 tokens "
-            f"without padded keys and head dim 32 or 64 (got {q.dtype}, window {tuple(window_size)}, "
+            "terra_amd: the attention backward kernels are built for bf16 / fp32 activations, windows up to 8x8 "
+            f"in at most 64 token rows and head dim 32 or 64 (got {q.dtype}, window {tuple(window_size)}, "
             f"{q.shape[-2]} tokens, n_real {n_real}, head dim {q.shape[-1] // num_heads})")
 
 
@@ -100,8 +102,8 @@ class _Attention(torch.autograd.Function):
         if table is not None and ctx.needs_input_grad[3]:
             dbias = torch.zeros(table.shape, dtype=torch.float32, device=table.device)
         dq, dk, dv = kernels.window_attention_backward(q, k, v, grad.contiguous(), num_heads, window_size, scale,
-                                                       bias_table=table, mask=mask, mask_value=mask_value,
-                                                       dbias=dbias)
+                                                       bias_table=table, mask=mask, n_real=n_real,
+                                                       mask_value=mask_value, dbias=dbias)
         dtable = None if dbias is None else dbias.to(table.dtype)
         return dq, dk, dv, dtable, None, None, None, None, None, None
 
@@ -130,7 +132,7 @@ class _AttentionQKV(torch.autograd.Function):
         if table is not None and ctx.needs_input_grad[1]:
             dbias = torch.zeros(table.shape, dtype=torch.float32, device=table.device)
         kernels.window_attention_backward(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], grad.contiguous(),
-                                          num_heads, window_size, scale, bias_table=table, mask=mask,
+                                          num_heads, window_size, scale, bias_table=table, mask=mask, n_real=n_real,
                                           mask_value=mask_value, dq=dqkv[..., :C], dk=dqkv[..., C:2 * C],
                                           dv=dqkv[..., 2 * C:], dbias=dbias)
         dtable = None if dbias is None else dbias.to(table.dtype)

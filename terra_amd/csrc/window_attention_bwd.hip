@@ -37,6 +37,8 @@ struct BwdParams {
   int64_t dq_stride, dk_stride, dv_stride;
   float* dbias;         // fp32 [table_size, heads], accumulated; NULL: not wanted
   float scale;          // natural q k^T scale
+  float mask_value;     // natural-unit mask and padded-key values (generic kernel)
+  float pad_key_value;
 };
 
 constexpr int kBwdTile = kNPad * 8 * 16;  // one [64][64] bf16 P or dz tile: 8 KB
@@ -366,6 +368,179 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
   return TERRA_OK;
 }
 
+// ============================================================================
+// generic backward: fp32 or bf16, any window up to 8x8, padded tokens / keys
+// ============================================================================
+//
+// One workgroup per (window, head), plain fp32 arithmetic on LDS copies of
+// q, k, v and dout (no MFMA): the shapes it serves (fp32 activations, 7x7
+// windows) are small configurations.  The logits follow the forward:
+// z = q k^T * scale + bias + mask for tokens of the window geometry, keys
+// >= n_real replaced by pad_key_value (their gradient is zero: masked_fill),
+// keys >= tokens excluded.
+
+template <bool kBf16> struct BwdElt;
+template <> struct BwdElt<true> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(const T* p) { return bf16_bits_to_f32(*p); }
+  static __device__ __forceinline__ void store(T* p, float v) { *p = f32_to_bf16_bits(v); }
+};
+template <> struct BwdElt<false> {
+  using T = float;
+  static __device__ __forceinline__ float load(const T* p) { return *p; }
+  static __device__ __forceinline__ void store(T* p, float v) { *p = v; }
+};
+
+template <int D>
+constexpr int generic_bwd_lds_bytes() {
+  return (4 * kNPad * (D + 1) + 2 * kNPad * (kNPad + 1) + kTableMax) * (int)sizeof(float);
+}
+
+template <bool kBf16, int D, bool kExplicit>
+__global__ __launch_bounds__(256) void window_attn_bwd_generic_kernel(const BwdParams bp) {
+  using E = BwdElt<kBf16>;
+  using T = typename E::T;
+  extern __shared__ __attribute__((aligned(16))) float smf[];
+  const AttnParams& p = bp.a;
+  constexpr int PD = D + 1;                     // odd row pitches: conflict-free column walks
+  constexpr int PP = kNPad + 1;
+  float* qs = smf;
+  float* ks = qs + kNPad * PD;
+  float* vs = ks + kNPad * PD;
+  float* ds = vs + kNPad * PD;                  // dout
+  float* ps = ds + kNPad * PD;                  // P
+  float* zs = ps + kNPad * PP;                  // dz
+  float* dtab = zs + kNPad * PP;                // this window-head's bias gradient
+  const int tid = threadIdx.x;
+  const int w = blockIdx.x / p.heads, h = blockIdx.x - (blockIdx.x / p.heads) * p.heads;
+  const int N = p.N, ng = p.n_geo, ww = p.window_w, wh = p.window_h;
+
+  auto load_rows = [&](const void* base, int64_t stride, float* dst) {
+    for (int e = tid; e < N * D; e += 256) {
+      const int r = e / D, c = e - r * D;
+      dst[r * PD + c] = E::load(reinterpret_cast<const T*>(base) + ((int64_t)w * N + r) * stride + h * D + c);
+    }
+  };
+  load_rows(p.q, p.q_stride, qs);
+  load_rows(p.k, p.k_stride, ks);
+  load_rows(p.v, p.v_stride, vs);
+  load_rows(p.o, p.o_stride, ds);
+  for (int e = tid; e < kTableMax; e += 256) dtab[e] = 0.f;
+  __syncthreads();
+
+  const WindowMaskState m = window_mask_state(p, w, true);
+  const float* emask = nullptr;
+  if constexpr (kExplicit) emask = p.explicit_mask + (int64_t)(w % p.mask_windows) * ng * ng;
+  auto rid = [&](int t) {                       // shift-mask region id of window token t < ng
+    const int ti = t / ww, tj = t - (t / ww) * ww;
+    return 3 * region(m.wr * wh + ti, p.frame_h, wh, p.shift_h) + region(m.wc * ww + tj, p.frame_w, ww, p.shift_w);
+  };
+
+  // Phase 1: four threads per query row i, keys j = jq + 4k.
+  const int i = tid >> 2, jq = tid & 3;
+  const bool row = i < N;
+  const int rid_i = (row && i < ng && m.use_shift) ? rid(i) : 0;
+  float z[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int j = jq + 4 * k;
+    float val = -INFINITY;
+    if (row && j < N) {
+      float dot = 0.f;
+#pragma unroll 8
+      for (int c = 0; c < D; ++c) dot = __builtin_fmaf(qs[i * PD + c], ks[j * PD + c], dot);
+      val = dot * bp.scale;
+      if (i < ng && j < ng) {
+        if (p.bias_table != nullptr) {
+          const int hi = i / ww, wi = i - hi * ww, hj = j / ww, wj = j - hj * ww;
+          val += p.bias_table[(int64_t)((hi - hj + wh - 1) * (2 * ww - 1) + (wi - wj + ww - 1)) * p.heads + h];
+        }
+        if constexpr (kExplicit) val += emask[i * ng + j];
+        else if (m.use_shift && rid(j) != rid_i) val += bp.mask_value;
+      }
+      if (j < ng && ((m.land >> j) & 1ull)) val += bp.mask_value;  // land keys, every query row
+      if (j >= p.n_real) val = bp.pad_key_value;
+    }
+    z[k] = val;
+  }
+  float mx = z[0];
+#pragma unroll
+  for (int k = 1; k < 16; ++k) mx = fmaxf(mx, z[k]);
+  mx = fmaxf(mx, __shfl_xor(mx, 1));
+  mx = fmaxf(mx, __shfl_xor(mx, 2));
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    z[k] = z[k] == -INFINITY ? 0.f : expf(z[k] - mx);
+    sum += z[k];
+  }
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  const float inv = row ? 1.f / sum : 0.f;
+  float dp[16], dsum = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int j = jq + 4 * k;
+    z[k] *= inv;                                // P
+    float acc = 0.f;
+    if (row && j < N) {
+#pragma unroll 8
+      for (int c = 0; c < D; ++c) acc = __builtin_fmaf(ds[i * PD + c], vs[j * PD + c], acc);
+    }
+    dp[k] = acc;
+    dsum = __builtin_fmaf(z[k], acc, dsum);
+  }
+  dsum += __shfl_xor(dsum, 1);
+  dsum += __shfl_xor(dsum, 2);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int j = jq + 4 * k;
+    if (row && j < N) {
+      const float dz = j < p.n_real ? z[k] * (dp[k] - dsum) : 0.f;
+      ps[i * PP + j] = z[k];
+      zs[i * PP + j] = dz;
+      if (bp.dbias != nullptr && i < ng && j < ng) {
+        const int hi = i / ww, wi = i - hi * ww, hj = j / ww, wj = j - hj * ww;
+        atomicAdd(dtab + (hi - hj + wh - 1) * (2 * ww - 1) + (wi - wj + ww - 1), dz);
+      }
+    }
+  }
+  __syncthreads();
+
+  // Phase 2: dq[r] = scale * sum_j dz[r][j] k[j],  dk[r] = scale * sum_i dz[i][r] q[i],
+  //          dv[r] = sum_i P[i][r] dout[i].
+  for (int e = tid; e < N * D; e += 256) {
+    const int r = e / D, c = e - r * D;
+    float aq = 0.f, ak = 0.f, av = 0.f;
+    for (int t = 0; t < N; ++t) {
+      aq = __builtin_fmaf(zs[r * PP + t], ks[t * PD + c], aq);
+      ak = __builtin_fmaf(zs[t * PP + r], qs[t * PD + c], ak);
+      av = __builtin_fmaf(ps[t * PP + r], ds[t * PD + c], av);
+    }
+    const int64_t row_g = (int64_t)w * N + r;
+    E::store(reinterpret_cast<T*>(bp.dq) + row_g * bp.dq_stride + h * D + c, aq * bp.scale);
+    E::store(reinterpret_cast<T*>(bp.dk) + row_g * bp.dk_stride + h * D + c, ak * bp.scale);
+    E::store(reinterpret_cast<T*>(bp.dv) + row_g * bp.dv_stride + h * D + c, av);
+  }
+  if (bp.dbias == nullptr) return;  // uniform
+  __syncthreads();
+  for (int e = tid; e < p.table_size; e += 256) {
+    const float v = dtab[e];
+    if (v != 0.f) unsafeAtomicAdd(bp.dbias + (int64_t)e * p.heads + h, v);
+  }
+}
+
+template <bool kBf16, int D, bool kExplicit>
+int launch_bwd_generic(const BwdParams& bp, hipStream_t s) {
+  constexpr int lds = generic_bwd_lds_bytes<D>();
+  auto kern = window_attn_bwd_generic_kernel<kBf16, D, kExplicit>;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  kern<<<bp.a.items, 256, lds, s>>>(bp);
+  return TERRA_OK;
+}
+
 }  // namespace
 }  // namespace terra
 
@@ -380,22 +555,29 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   if (q == nullptr || k == nullptr || v == nullptr || dout == nullptr || dq == nullptr || dk == nullptr ||
       dv == nullptr)
     return fail(TERRA_ERR_NULL, "q, k, v, dout, dq, dk and dv must be non-NULL");
-  if (dtype != TERRA_DTYPE_BF16) return fail(TERRA_ERR_UNSUPPORTED, "attention backward is built for bf16");
+  if (dtype != TERRA_DTYPE_BF16 && dtype != TERRA_DTYPE_F32)
+    return fail(TERRA_ERR_DTYPE, "attention backward supports bf16 and f32 activations (got dtype %d)", dtype);
   const terra_swin_attn_desc& d = desc->fwd;
-  if (d.num_windows <= 0 || d.heads <= 0 || d.channels <= 0)
-    return fail(TERRA_ERR_SHAPE, "num_windows/channels/heads must be positive");
-  if (d.window_h != 8 || d.window_w != 8 || d.tokens != 64 || d.n_real != 64)
-    return fail(TERRA_ERR_UNSUPPORTED, "attention backward is built for 8x8 windows without padded keys");
+  if (d.num_windows <= 0 || d.tokens <= 0 || d.heads <= 0 || d.channels <= 0)
+    return fail(TERRA_ERR_SHAPE, "num_windows/tokens/channels/heads must be positive");
+  if (d.tokens > kNPad) return fail(TERRA_ERR_UNSUPPORTED, "tokens per window %d > %d", d.tokens, kNPad);
+  if (d.window_h <= 0 || d.window_w <= 0 || d.window_h > 8 || d.window_w > 8)
+    return fail(TERRA_ERR_UNSUPPORTED, "window %dx%d outside 1..8", d.window_h, d.window_w);
+  if (d.window_h * d.window_w > d.tokens)
+    return fail(TERRA_ERR_SHAPE, "window %dx%d has more than %d tokens", d.window_h, d.window_w, d.tokens);
+  if (d.n_real <= 0 || d.n_real > d.tokens) return fail(TERRA_ERR_SHAPE, "n_real %d outside [1, %d]", d.n_real, d.tokens);
   if (d.channels % d.heads != 0)
     return fail(TERRA_ERR_SHAPE, "channels %d not divisible by heads %d", d.channels, d.heads);
   const int D = d.channels / d.heads;
   if (D != 32 && D != 64) return fail(TERRA_ERR_UNSUPPORTED, "head dim %d not in {32, 64}", D);
-  const int32_t strides[8] = {d.q_stride, d.k_stride, d.v_stride, desc->dout_stride,
-                              desc->dq_stride, desc->dk_stride, desc->dv_stride, d.channels};
+  const int elt = dtype == TERRA_DTYPE_BF16 ? 2 : 4;
+  const int32_t strides[7] = {d.q_stride, d.k_stride, d.v_stride, desc->dout_stride,
+                              desc->dq_stride, desc->dk_stride, desc->dv_stride};
   for (int i = 0; i < 7; ++i) {
     if (strides[i] < d.channels) return fail(TERRA_ERR_SHAPE, "row strides must be >= channels");
-    if (strides[i] % 8 != 0) return fail(TERRA_ERR_ALIGN, "row strides must be multiples of 8 elements");
-    if ((int64_t)strides[i] * d.tokens * 2 >= (1ll << 32))
+    if (strides[i] % (16 / elt) != 0)
+      return fail(TERRA_ERR_ALIGN, "row strides must be multiples of %d elements", 16 / elt);
+    if ((int64_t)strides[i] * d.tokens * elt >= (1ll << 32))
       return fail(TERRA_ERR_SHAPE, "one window must span under 4 GiB");
   }
   for (const void* ptr : {q, k, v, dout, (const void*)dq, (const void*)dk, (const void*)dv})
@@ -416,11 +598,13 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   if (d.mask_mode == TERRA_MASK_SHIFT) {
     if (d.win_rows <= 0 || d.win_cols <= 0 || d.frame_h <= 0 || d.frame_w <= 0)
       return fail(TERRA_ERR_SHAPE, "shift mask needs a positive frame and window grid");
-    if (d.frame_h % 8 || d.frame_w % 8) return fail(TERRA_ERR_SHAPE, "frame not a multiple of the window");
-    if (d.win_cols != d.frame_w / 8) return fail(TERRA_ERR_SHAPE, "win_cols %d != frame_w / 8", d.win_cols);
-    if (d.win_row_begin < 0 || (d.win_row_begin + d.win_rows) * 8 > d.frame_h)
+    if (d.frame_h % d.window_h || d.frame_w % d.window_w)
+      return fail(TERRA_ERR_SHAPE, "frame %dx%d not a multiple of the window", d.frame_h, d.frame_w);
+    if (d.win_cols != d.frame_w / d.window_w)
+      return fail(TERRA_ERR_SHAPE, "win_cols %d != frame_w / window_w", d.win_cols);
+    if (d.win_row_begin < 0 || (d.win_row_begin + d.win_rows) * d.window_h > d.frame_h)
       return fail(TERRA_ERR_SHAPE, "window rows outside the frame");
-    if (d.shift_h <= 0 || d.shift_h >= 8 || d.shift_w <= 0 || d.shift_w >= 8)
+    if (d.shift_h <= 0 || d.shift_h >= d.window_h || d.shift_w <= 0 || d.shift_w >= d.window_w)
       return fail(TERRA_ERR_SHAPE, "shift mask needs 0 < shift < window (got %d, %d)", d.shift_h, d.shift_w);
     if (d.num_windows % (d.win_rows * d.win_cols) != 0)
       return fail(TERRA_ERR_SHAPE, "num_windows %d not a multiple of the %d windows per image", d.num_windows,
@@ -440,10 +624,11 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   p.items = (int32_t)items;
   p.heads = d.heads;
   p.N = d.tokens;
-  p.n_geo = 64;
-  p.window_h = p.window_w = 8;
-  p.table_size = 225;
-  p.n_real = 64;
+  p.n_geo = d.window_h * d.window_w;
+  p.window_h = d.window_h;
+  p.window_w = d.window_w;
+  p.table_size = (2 * d.window_h - 1) * (2 * d.window_w - 1);
+  p.n_real = d.n_real;
   p.scale_l2e = d.scale * kLog2e;
   p.mask_l2e = d.mask_value * kLog2e;
   p.pad_key_l2e = d.pad_key_value * kLog2e;
@@ -454,19 +639,33 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   bp.dq_stride = desc->dq_stride; bp.dk_stride = desc->dk_stride; bp.dv_stride = desc->dv_stride;
   bp.dbias = dbias_table;
   bp.scale = d.scale;
+  bp.mask_value = d.mask_value;
+  bp.pad_key_value = d.pad_key_value;
 
-  // Two heads per workgroup for head dim 32 (128-byte row slices), else one.
-  const int G = (D == 32 && d.heads % 2 == 0) ? 2 : 1;
-  p.group = G;
-  p.groups = d.heads / G;
   const bool expl = d.mask_mode == TERRA_MASK_EXPLICIT;
   hipStream_t s = (hipStream_t)stream;
   int st;
-  if (D == 32)
-    st = G == 2 ? (expl ? launch_bwd<32, 2, true>(bp, s) : launch_bwd<32, 2, false>(bp, s))
-                : (expl ? launch_bwd<32, 1, true>(bp, s) : launch_bwd<32, 1, false>(bp, s));
-  else
-    st = expl ? launch_bwd<64, 1, true>(bp, s) : launch_bwd<64, 1, false>(bp, s);
+  const bool tile = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
+                    d.n_real == 64;
+  if (tile) {
+    // Two heads per workgroup for head dim 32 (128-byte row slices), else one.
+    const int G = (D == 32 && d.heads % 2 == 0) ? 2 : 1;
+    p.group = G;
+    p.groups = d.heads / G;
+    if (D == 32)
+      st = G == 2 ? (expl ? launch_bwd<32, 2, true>(bp, s) : launch_bwd<32, 2, false>(bp, s))
+                  : (expl ? launch_bwd<32, 1, true>(bp, s) : launch_bwd<32, 1, false>(bp, s));
+    else
+      st = expl ? launch_bwd<64, 1, true>(bp, s) : launch_bwd<64, 1, false>(bp, s);
+  } else {
+    p.group = p.groups = 0;
+    if (dtype == TERRA_DTYPE_BF16)
+      st = D == 32 ? (expl ? launch_bwd_generic<true, 32, true>(bp, s) : launch_bwd_generic<true, 32, false>(bp, s))
+                   : (expl ? launch_bwd_generic<true, 64, true>(bp, s) : launch_bwd_generic<true, 64, false>(bp, s));
+    else
+      st = D == 32 ? (expl ? launch_bwd_generic<false, 32, true>(bp, s) : launch_bwd_generic<false, 32, false>(bp, s))
+                   : (expl ? launch_bwd_generic<false, 64, true>(bp, s) : launch_bwd_generic<false, 64, false>(bp, s));
+  }
   if (st != TERRA_OK) return st;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "terra_swin_attn_bwd launch failed: %s", hipGetErrorString(e));

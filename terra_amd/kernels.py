@@ -354,12 +354,14 @@ def _bias_table(bias_table: Optional[torch.Tensor], d: _lib.SwinAttnDesc) -> Opt
 
 def attention_backward_supported(q: torch.Tensor, num_heads: int, window_size: Tuple[int, int],
                                  n_real: Optional[int] = None) -> bool:
-    """Whether :func:`window_attention_backward` serves this shape (bf16, 8x8
-    windows of 64 tokens without padded keys, head dim 32 or 64)."""
+    """Whether :func:`window_attention_backward` serves this shape: the
+    forward's (bf16 or fp32, windows up to 8x8 in at most 64 token rows,
+    head dim 32 or 64)."""
     tokens, channels = q.shape[-2], q.shape[-1]
-    return (q.dtype == torch.bfloat16 and tuple(int(w) for w in window_size) == (8, 8) and tokens == 64
-            and (n_real is None or int(n_real) == 64) and channels % num_heads == 0
-            and channels // num_heads in (32, 64))
+    wh, ww = (int(w) for w in window_size)
+    return (q.dtype in (torch.bfloat16, torch.float32) and 1 <= wh <= 8 and 1 <= ww <= 8
+            and wh * ww <= tokens <= 64 and (n_real is None or 1 <= int(n_real) <= tokens)
+            and channels % num_heads == 0 and channels // num_heads in (32, 64))
 
 
 def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dout: torch.Tensor,
@@ -380,8 +382,7 @@ def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     for t in (k, v, dout):
         if t.dtype != q.dtype:
             raise TypeError("q, k, v and dout must share a dtype")
-    if q.dtype != torch.bfloat16:
-        raise ValueError("attention backward is built for bf16 activations")
+    code = _dtype_code(q, (torch.bfloat16, torch.float32))
     num_windows, tokens, channels = q.shape
     strides = tuple(_row_stride(t, n, num_windows, tokens, channels)
                     for t, n in ((q, "q"), (k, "k"), (v, "v"), (dout, "dout")))
@@ -408,7 +409,7 @@ def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     emask, land = _attn_masks(bd.fwd, num_windows, mask)
     with torch.cuda.device(dev):
         st = _lib.load().terra_swin_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(outs[0]), _ptr(outs[1]),
-                                             _ptr(outs[2]), _dtype_code(q, (torch.bfloat16,)), ctypes.byref(bd),
+                                             _ptr(outs[2]), code, ctypes.byref(bd),
                                              _ptr(table), _ptr(dbias), _ptr(emask), _ptr(land), _stream(dev))
     _lib.check(st, "terra_swin_attn_bwd")
     return tuple(outs)

@@ -139,8 +139,9 @@ def _bwd_desc(dout_stride=64, dq_stride=64, dk_stride=64, dv_stride=64, **kw):
 
 
 @pytest.mark.parametrize("kw,code,text", [
-    (dict(window_h=7, window_w=7, tokens=49, n_real=49), -5, "8x8 windows"),
-    (dict(n_real=40), -5, "padded keys"),
+    (dict(tokens=81, window_h=9, window_w=9, n_real=81), -5, "tokens per window"),
+    (dict(window_h=9), -5, "outside 1..8"),
+    (dict(n_real=0), -3, "n_real"),
     (dict(heads=3), -3, "not divisible"),
     (dict(channels=48, heads=3, q_stride=48, k_stride=48, v_stride=48, o_stride=48, dout_stride=48,
           dq_stride=48, dk_stride=48, dv_stride=48), -5, "head dim"),
@@ -163,7 +164,7 @@ def test_attention_backward_rejects_dtype_null_alignment_table():
     lib = L.load()
     bd = _bwd_desc()
     call = lambda *a: lib.terra_swin_attn_bwd(*a, ctypes.byref(bd), None, None, None, None, None)  # noqa: E731
-    assert call(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, L.DTYPE_F32) == -5
+    assert call(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, L.DTYPE_F16) == -2
     assert call(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, L.DTYPE_BF16) == -1
     bad = ctypes.c_void_p((1 << 20) + 8)
     assert call(FAKE, FAKE, FAKE, FAKE, FAKE, bad, FAKE, L.DTYPE_BF16) == -4

@@ -8,6 +8,8 @@ Tolerances (bf16 activations; the kernel rounds P and dz to bf16 as MFMA
 operands, as the forward rounds P):
   dq, dk, dv:  max |got - ref| <= 2e-2 * max |ref| per tensor;
   dbias:       max |got - ref| <= 2e-2 * max |ref| (fp32, summed over windows);
+fp32 activations (the generic kernel, all fp32; reference in float64):
+  every gradient: max |got - ref| <= 2e-5 * max |ref| + 1e-6;
   module (LayerNorm + Linears + attention + residual, all bf16 in torch's
   and the kernel's rounding): normwise |got - ref| / |ref| <= 3e-2 per tensor.
 Partition / reverse gradients are permutations: bit-exact.
@@ -135,14 +137,92 @@ def test_attention_autograd_function(dev):
     assert torch.allclose(tab.grad, dbias, rtol=1e-5, atol=1e-6)  # float-atomic summation order
 
 
-def test_backward_rejects_unsupported_shapes(dev):
-    q = torch.zeros(4, 49, 96, dtype=torch.bfloat16, device=dev, requires_grad=True)
-    o = autograd.window_attention(q, q, q, 3, (7, 7), 32 ** -0.5)
-    with pytest.raises(NotImplementedError):
-        o.sum().backward()
-    x = torch.zeros(4, 64, 96, device=dev)
-    with pytest.raises(ValueError):
+def test_backward_rejects_unsupported_dtypes(dev):
+    x = torch.zeros(4, 64, 96, dtype=torch.float16, device=dev)
+    with pytest.raises(TypeError):
         kernels.window_attention_backward(x, x, x, x, 3, (8, 8), 1.0)
+    assert not kernels.attention_backward_supported(x, 3, (8, 8))
+
+
+def _oracle_grads_generic(q, k, v, dout, heads, table, ws, dense_mask, n_real, cd):
+    leaves = [t.to(cd).clone().requires_grad_(True) for t in (q, k, v)]
+    tab = None if table is None else table.to(cd).clone().requires_grad_(True)
+    C = q.shape[-1]
+    out = so.window_attention_core(*leaves, heads, (C // heads) ** -0.5, tab, (ws, ws),
+                                   None if dense_mask is None else dense_mask.to(cd), n_real, compute_dtype=cd)
+    (out * dout.to(cd)).sum().backward()
+    return [t.grad for t in leaves], (None if tab is None else tab.grad)
+
+
+def _close_dtype(got, ref, dtype):
+    got = got.double().cpu()
+    ref = ref.double()
+    err = (got - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    if dtype == torch.float32:
+        assert err <= 2e-5 * scale + 1e-6, (err, scale)
+    else:
+        assert err <= 2e-2 * scale, (err, scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind", ["none", "shift", "explicit", "land"])
+def test_generic_backward_7x7_matches_oracle(dev, dtype, kind):
+    """7x7 windows (c1, c2): the generic kernel, every mask form."""
+    B, H, W, C, heads, ws, s = 2, 14, 21, 96, 3, 7, 3
+    g = WindowGeometry(B, H, W, 1, ws, s, s)
+    B_ = g.num_windows
+    q, k, v, dout, _ = _inputs(B_, C, heads, 360)
+    q, k, v, dout = (t[:, :49].contiguous() for t in (q, k, v, dout))
+    table = torch.empty(169, heads)
+    torch.nn.init.trunc_normal_(table, std=0.5, generator=workloads.generator(361))
+    if dtype == torch.float32:
+        q, k, v, dout = (workloads.activations(tuple(t.shape), 362 + i) * (2.0 if i < 2 else 1.0)
+                         for i, t in enumerate((q, k, v, dout)))
+    q, k, v, dout = (t.to(dtype) for t in (q, k, v, dout))
+    dense = so.shift_mask(H, W, ws, s)
+    mask, ref_mask = None, None
+    if kind == "shift":
+        mask, ref_mask = ShiftMask.from_geometry(g), dense
+    elif kind == "explicit":
+        mask, ref_mask = dense.to(dev), dense
+    elif kind == "land":
+        land = workloads.land_mask(H, W, seed=33)
+        bits = utils.land_window_bits(land.to(dev), g)
+        mask = WindowMask(shift=ShiftMask.from_geometry(g), land_bits=bits)
+        ref_mask = so.fold_land(dense, so.land_key_flags(land, ws, s, s))
+    dbias = torch.zeros(169, heads, device=dev)
+    got = kernels.window_attention_backward(q.to(dev), k.to(dev), v.to(dev), dout.to(dev), heads, (ws, ws),
+                                            (C // heads) ** -0.5, bias_table=table.to(dev), mask=mask, dbias=dbias)
+    cd = torch.float64 if dtype == torch.float32 else torch.float32
+    ref, rtab = _oracle_grads_generic(q, k, v, dout, heads, table, ws, ref_mask, None, cd)
+    for a, b in zip(got, ref):
+        _close_dtype(a, b, dtype)
+    _close_dtype(dbias, rtab, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_generic_backward_padded_tokens_and_keys(dev, dtype):
+    """a10: 49 real tokens of 7x7 windows in 64-token rows, keys >= 49 filled
+    with -10000 (no gradient through them)."""
+    B_, N, C, heads, ws = 8, 64, 128, 4, 7
+    q = workloads.activations((B_, N, C), 370).to(dtype)
+    k = workloads.activations((B_, N, C), 371).to(dtype)
+    v = workloads.activations((B_, N, C), 372).to(dtype)
+    dout = workloads.activations((B_, N, C), 373).to(dtype)
+    table = torch.empty(169, heads)
+    torch.nn.init.trunc_normal_(table, std=0.5, generator=workloads.generator(374))
+    mask = so.shift_mask(14, 14, 7, 3)
+    dbias = torch.zeros(169, heads, device=dev)
+    got = kernels.window_attention_backward(q.to(dev), k.to(dev), v.to(dev), dout.to(dev), heads, (ws, ws),
+                                            (C // heads) ** -0.5, bias_table=table.to(dev), mask=mask.to(dev),
+                                            n_real=49, dbias=dbias)
+    cd = torch.float64 if dtype == torch.float32 else torch.float32
+    ref, rtab = _oracle_grads_generic(q, k, v, dout, heads, table, ws, mask, 49, cd)
+    for a, b in zip(got, ref):
+        _close_dtype(a, b, dtype)
+    _close_dtype(dbias, rtab, dtype)
+    assert torch.count_nonzero(got[1][:, 49:].float()) == 0  # padded keys get no gradient
 
 
 @pytest.mark.parametrize("slab", [False, True])
@@ -178,6 +258,33 @@ def _normwise(got, ref):
     got = got.double().cpu()
     ref = ref.double().cpu()
     return ((got - ref).norm() / ref.norm()).item()
+
+
+def test_block_backward_fp32_c1_matches_oracle(dev):
+    """c1 (fp32, 56x56, C=96, 3 heads, window 7), layer 1 (shift 3): the
+    generic backward inside the module, against the float64 oracle block."""
+    cfg = workloads.CONFIGS["c1"]
+    blk = workloads.block_for(cfg, 1)
+    with torch.no_grad():
+        for lin in (blk.attn.q_linear, blk.attn.k_linear):
+            lin.weight.mul_(4.0)
+        blk.attn.proj.weight.mul_(8.0)
+        blk.attn.relative_position_bias_table.mul_(25.0)
+    params = {n: p.detach().double().clone().requires_grad_(True) for n, p in blk.named_parameters()}
+    blk = blk.to(dev)
+    x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 380)
+    gy = workloads.activations(tuple(x.shape), 381)
+    xd = x.to(dev).requires_grad_(True)
+    blk(xd).backward(gy.to(dev))
+    xr = x.double().requires_grad_(True)
+    so.swin_block_attention(xr, cfg.height, cfg.width, cfg.window, blk.shift_size, cfg.heads, params,
+                            compute_dtype=torch.float64).backward(gy.double())
+    assert _normwise(xd.grad, xr.grad) <= 1e-5
+    for name, p in blk.named_parameters():
+        if name == "attn.k_linear.bias":  # exactly 0 in exact arithmetic (see below)
+            assert p.grad.double().norm().item() <= 1e-5 * params["attn.q_linear.bias"].grad.norm().item()
+            continue
+        assert _normwise(p.grad, params[name].grad) <= 1e-5, name
 
 
 @pytest.mark.parametrize("layer_idx,use_land", [(0, False), (1, True)])
