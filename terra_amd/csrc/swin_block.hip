@@ -581,15 +581,20 @@ void swin_block_kernel(const BlockParams p) {
   stage_tables<kH, nthreads>(p, tabs, s_gamma, s_beta, tid);
 
   UnitLoc cur = locate(p, unit);
+  UnitLoc prev = cur;
+  bool have_prev = false;
   int par = 0;
   fetch_window<cpr, kH>(p, cur, xbuf, wave, lane);
 
+  // Barriers are LDS-only (lds_barrier): the next window's rows stay in
+  // flight from the q/k/v phase to the top of the next iteration, and a
+  // window's output rows are stored at the start of the next iteration, so
+  // the wait for the rows does not also wait for those stores.
   for (;;) {
-    // This window's rows have landed (nothing else is in flight); the
-    // barrier also orders the previous window's output reads of the other
-    // buffer before the next fetch overwrites it.
+    // This window's rows have landed; the barrier also orders the previous
+    // window's proj writes before its store below.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    lds_barrier();
     uint8_t* xr = xbuf + par * tile;
     uint8_t* xr_next = xbuf + (par ^ 1) * tile;
     const int next = unit + (int)gridDim.x;
@@ -600,30 +605,35 @@ void swin_block_kernel(const BlockParams p) {
     int lane_i = lane;
     asm volatile("" : "+v"(lane_i));
     const int tid_i = wave * 64 + lane_i;
+    if (have_prev) store_window<cpr, nthreads>(p, prev, xr_next, tid_i);  // the previous window's rows
 
     if (cur.computed) {  // uniform across the workgroup
       layernorm_window<cpr, nthreads>(p, cur, xr, xn, s_gamma, s_beta, tid_i);
-      __syncthreads();
+      lds_barrier();     // also: the previous window's rows are read out of xr_next
       uint4 kf4[4], vf[2][2], qf[4];
       head_qkv<C, kPacked>(p, xn, wave, lane_i, kf4, vf, qf);
       // Next window's rows stream in behind the q/k/v loads (the attention
       // phase issues no vector-memory loads of its own).
       if (next < p.units) fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane_i);
-      __syncthreads();  // every wave has read xn; O overwrites it
+      lds_barrier();     // every wave has read xn; O overwrites it
       head_attention<C>(p, cur, tabs + wave * kTableMax, wave, lane_i, kf4, vf, qf, xn);
-      __syncthreads();  // O complete
+      lds_barrier();     // O complete
       head_proj<C, kPacked>(p, xn, xr, wave, lane_i);
-      __syncthreads();  // output rows complete in xr
     } else if (next < p.units) {
+      lds_barrier();     // the previous window's rows are read out of xr_next
       fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane_i);
     }
-
-    store_window<cpr, nthreads>(p, cur, xr, tid_i);
+    prev = cur;
+    have_prev = true;
     if (next >= p.units) break;
     unit = next;
     cur = nxt;
     par ^= 1;
   }
+  lds_barrier();         // output rows complete in the last window's buffer
+  int lane_f = lane;
+  asm volatile("" : "+v"(lane_f));
+  store_window<cpr, nthreads>(p, prev, xbuf + par * tile, wave * 64 + lane_f);
 }
 
 // ============================================================================
