@@ -151,6 +151,15 @@ typedef struct terra_swin_block_desc {
                              1: in the layout of terra_swin_pack_linear */
 } terra_swin_block_desc;
 
+/* Description of one fused MLP half-block call (terra_swin_mlp_fwd). */
+typedef struct terra_swin_mlp_desc {
+  int32_t tokens;     /* rows of x (any count; B*H*W for a [B, H, W, C] grid) */
+  int32_t channels;   /* C: 192 or 384                                     */
+  int32_t hidden;     /* fc1 out features: 4 * C (mlp_ratio 4)             */
+  int32_t layernorm;  /* 1: norm2 = LayerNorm(gamma, beta); 0: none        */
+  float ln_eps;       /* LayerNorm eps                                     */
+} terra_swin_mlp_desc;
+
 /* ABI version of the loaded library (TERRA_SWIN_ABI_VERSION at build time). */
 int terra_abi_version(void);
 
@@ -268,6 +277,28 @@ int terra_swin_block_fwd(const void* x, void* y, int dtype,
  */
 int terra_swin_pack_linear(const void* weight, void* packed, int dtype,
                            int out_features, int in_features, void* stream);
+
+/* Fused MLP half-block (bf16 activations).
+ * Replaces SequentialMlp.forward              models/mlp.py:152-172:
+ *           x = self.norm2(x)                  models/mlp.py:159 (nn.LayerNorm)
+ *           x = self.fc1(x)                    models/mlp.py:162 (C -> 4C)
+ *           x = self.act(x)                    models/mlp.py:165 (nn.GELU, erf form)
+ *           x = self.fc2(x)                    models/mlp.py:168 (4C -> C)
+ *           x = shortcut + x                   models/mlp.py:171
+ * per token row of x [tokens, C] (bf16, contiguous).  y may equal x (in
+ * place) but must not overlap it otherwise.  fc1_weight / fc2_weight are the
+ * bf16 nn.Linear weights [4C, C] / [C, 4C] in the layout of
+ * terra_swin_pack_linear; fc1_bias [4C], fc2_bias [C], ln_gamma / ln_beta
+ * [C] fp32 or NULL.  Rounding follows the bf16 module: LayerNorm output,
+ * fc1 output (bias added in fp32), GELU output and fc2 output are rounded to
+ * bf16, and the residual add is fp32 rounded once.
+ */
+int terra_swin_mlp_fwd(const void* x, void* y, int dtype,
+                       const terra_swin_mlp_desc* desc,
+                       const float* ln_gamma, const float* ln_beta,
+                       const void* fc1_weight, const float* fc1_bias,
+                       const void* fc2_weight, const float* fc2_bias,
+                       void* stream);
 
 #ifdef __cplusplus
 }

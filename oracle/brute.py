@@ -143,3 +143,48 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, num_heads: int, scale
                     acc += (e[j] / tot) * v[w, j, cs].astype(np.float64)
                 out[w, i, cs] = acc
     return out
+
+
+def bf16_round(v: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bfloat16 (ties to even), as float32, by bit arithmetic
+    on the float32 encoding (NaN kept quiet)."""
+    f = np.asarray(v, dtype=np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(f)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    r = np.where(nan, (u.astype(np.uint32) & 0xFFFF0000) | 0x00400000, r).astype(np.uint32)
+    return r.view(np.float32)
+
+
+def gelu(v: float) -> float:
+    """nn.GELU() (exact form): x * Phi(x) = 0.5 x (1 + erf(x / sqrt 2))."""
+    return 0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0)))
+
+
+def mlp(x: np.ndarray, p: dict, use_layernorm: bool = True, eps: float = 1e-5,
+        round_bf16: bool = False) -> np.ndarray:
+    """SequentialMlp.forward (models/mlp.py:152-172) token by token with loops:
+    LayerNorm over C, fc1 (weight [hid, C]), GELU, fc2 (weight [C, hid]),
+    + x.  With ``round_bf16`` the float64 results are rounded to float32 and
+    then to bf16 where a bf16 module rounds: LayerNorm output, fc1 output,
+    GELU output, fc2 output and the residual sum."""
+    rnd = (lambda a: bf16_round(np.float32(a)).astype(np.float64)) if round_bf16 else (lambda a: a)  # noqa: E731
+    w1, b1 = np.asarray(p["fc1.weight"], np.float64), np.asarray(p["fc1.bias"], np.float64)
+    w2, b2 = np.asarray(p["fc2.weight"], np.float64), np.asarray(p["fc2.bias"], np.float64)
+    hid, C = w1.shape
+    xs = np.asarray(x, np.float64).reshape(-1, C)
+    out = np.empty_like(xs)
+    for t in range(xs.shape[0]):
+        row = xs[t]
+        if use_layernorm:
+            mean = sum(row) / C
+            var = sum((c - mean) ** 2 for c in row) / C
+            g, b = np.asarray(p["norm2.weight"], np.float64), np.asarray(p["norm2.bias"], np.float64)
+            xn = [rnd((row[c] - mean) / math.sqrt(var + eps) * g[c] + b[c]) for c in range(C)]
+        else:
+            xn = list(row)
+        h = [rnd(gelu(rnd(sum(w1[j, c] * xn[c] for c in range(C)) + b1[j]))) for j in range(hid)]
+        for c in range(C):
+            y = rnd(sum(w2[c, j] * h[j] for j in range(hid)) + b2[c])
+            out[t, c] = rnd(row[c] + y)
+    return out.reshape(np.asarray(x).shape)

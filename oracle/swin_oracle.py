@@ -20,9 +20,11 @@ brute-force loops, closed forms, library special cases, known answers):
   land_key_flags / fold_land           brute loops
   ragged_row_major                     the reference's own unit-test vector
                                        (tests/unit/test_window_assignment.py:10-23)
-  swin_block_attention / mlp           composition of the pinned parts above;
-                                       LayerNorm / Linear / GELU are torch's own
-                                       ops (parity unpinned beyond torch itself)
+  swin_block_attention                 composition of the pinned parts above;
+                                       LayerNorm / Linear are torch's own ops
+  mlp / mlp_bf16                       brute.mlp (token loops, math.erf GELU,
+                                       bit-level bf16 rounding); GELU known
+                                       values; LayerNorm against its definition
 """
 from __future__ import annotations
 
@@ -296,12 +298,34 @@ def swin_block_attention(x: torch.Tensor, H: int, W: int, window_size: int, shif
 
 
 def mlp(x: torch.Tensor, params: dict, use_layernorm: bool = True) -> torch.Tensor:
-    """SequentialMlp.forward (models/mlp.py:152-174): LN -> fc1 -> GELU -> fc2 -> +x."""
+    """SequentialMlp.forward (models/mlp.py:152-172): LN -> fc1 -> GELU -> fc2 -> +x."""
     p = {k_: v_.detach().float().cpu() for k_, v_ in params.items()}
     x = x.float()
     h = F.layer_norm(x, (x.shape[-1],), p["norm2.weight"], p["norm2.bias"]) if use_layernorm else x
     h = F.gelu(F.linear(h, p["fc1.weight"], p["fc1.bias"]))
     return F.linear(h, p["fc2.weight"], p["fc2.bias"]) + x
+
+
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+    """Round to bfloat16 through float32 (the GPU's fp32 epilogues), as float64."""
+    return t.float().bfloat16().double()
+
+
+def mlp_bf16(x: torch.Tensor, params: dict, use_layernorm: bool = True, eps: float = 1e-5) -> torch.Tensor:
+    """SequentialMlp.forward (models/mlp.py:152-172) of a bf16 module: float64
+    arithmetic on the bf16 input and bf16-rounded weights, rounded to bf16 where
+    the bf16 module rounds (LayerNorm output, fc1 output with its fp32 bias,
+    GELU output, fc2 output, the residual sum).  Returns float64 [.., C]."""
+    p = {k_: v_.detach().cpu() for k_, v_ in params.items()}
+    C = x.shape[-1]
+    xb = _bf16(x.detach().cpu())
+    h = xb
+    if use_layernorm:
+        h = _bf16(F.layer_norm(xb, (C,), p["norm2.weight"].double(), p["norm2.bias"].double(), eps))
+    h = _bf16(F.linear(h, _bf16(p["fc1.weight"]), p["fc1.bias"].float().double()))
+    h = _bf16(0.5 * h * (1.0 + torch.special.erf(h / 2.0 ** 0.5)))
+    y = _bf16(F.linear(h, _bf16(p["fc2.weight"]), p["fc2.bias"].float().double()))
+    return _bf16(xb + y)
 
 
 # ----------------------------------------------------------------------------

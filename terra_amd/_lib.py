@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "terra_swin_attn_bwd",
     "terra_swin_block_fwd",
     "terra_swin_pack_linear",
+    "terra_swin_mlp_fwd",
 )
 
 
@@ -133,6 +134,18 @@ class SwinBlockDesc(ctypes.Structure):
     ]
 
 
+class SwinMlpDesc(ctypes.Structure):
+    """Mirror of ``terra_swin_mlp_desc``."""
+
+    _fields_ = [
+        ("tokens", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("layernorm", ctypes.c_int32),
+        ("ln_eps", ctypes.c_float),
+    ]
+
+
 class TerraError(RuntimeError):
     """A C-ABI call returned a launch-time failure."""
 
@@ -181,6 +194,9 @@ def load() -> ctypes.CDLL:
                                              vp, vp, vp, vp]
         lib.terra_swin_pack_linear.restype = ctypes.c_int
         lib.terra_swin_pack_linear.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
+        lib.terra_swin_mlp_fwd.restype = ctypes.c_int
+        lib.terra_swin_mlp_fwd.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(SwinMlpDesc), vp, vp, vp, vp, vp, vp,
+                                           vp]
         version = lib.terra_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"terra_amd: {LIB_PATH} has ABI version {version}, expected {ABI_VERSION}; rebuild it")

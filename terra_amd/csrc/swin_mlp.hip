@@ -1,0 +1,482 @@
+// Fused MLP half of a Swin block (SequentialMlp.forward, models/mlp.py:152-172):
+//
+//   y = x + fc2(GELU(fc1(LayerNorm(x))))        per token, bf16 activations
+//
+// One persistent workgroup per CU (12 waves) walks 64-token tiles.  A tile's
+// rows arrive by direct global->LDS loads (double-buffered for C = 192: the
+// next tile streams in while this one computes), LayerNorm writes the bf16
+// operand tile, and the hidden layer never leaves the CU: it is produced in
+// chunks of 384 features (fc1 on MFMA, bias as the accumulator init, then
+// bf16 -> exact GELU -> bf16 into LDS) and consumed by fc2 right away, whose
+// accumulators persist across the chunks.  The output is added to the raw
+// rows in LDS (bf16(x + bf16(y))) and the rows are stored as whole lines at
+// the start of the next tile.  Weights are in the fragment-packed layout of
+// terra_swin_pack_linear and stream from L2 once per tile.
+//
+// Rounding follows the bf16 module: LayerNorm output, fc1 output, GELU output
+// and fc2 output are rounded to bf16 (fp32 accumulation and epilogues), and
+// the residual add is fp32 rounded once.
+#include "common.h"
+#include "attn_core.h"
+
+namespace terra {
+namespace {
+
+struct MlpParams {
+  const uint8_t* x;
+  uint8_t* y;
+  const float* gamma;  // C floats or NULL (1)
+  const float* beta;   // C floats or NULL (0)
+  const uint16_t* w1;  // fc1.weight [H, C], fragment-packed
+  const float* b1;     // H floats or NULL
+  const uint16_t* w2;  // fc2.weight [C, H], fragment-packed
+  const float* b2;     // C floats or NULL
+  float eps;
+  float inv_c;
+  int32_t tokens;
+  int32_t tiles;       // ceil(tokens / 64)
+  int32_t layernorm;
+};
+
+constexpr int kMlpWaves = 12;
+constexpr int kMlpThreads = 64 * kMlpWaves;
+constexpr int kHC = 32 * kMlpWaves;  // hidden features per chunk: 32 per wave
+
+// GELU of a bf16 input by table.  The fc1 output is rounded to bf16 before
+// the activation, so GELU sees one of 2^16 inputs; for 2^-12 <= |x| < 8 the
+// bf16 result is read from a table that each workgroup fills at start with
+// the module's formula, 0.5 x (1 + erf(x / sqrt 2)) in fp32 rounded to bf16
+// (the value PyTorch's GPU kernel computes for a bf16 input).  Outside that
+// range the bf16 result has a closed form: 0.5 x for |x| < 2^-12 (the fp32
+// value is 0.5 x (1 + d) with |d| < 2^-12, and 0.5 x is a bf16 value, so it
+// rounds to 0.5 x); x for x >= 8 (erf = 1 in fp32); -0 for x <= -8 (erf = -1
+// in fp32); -inf gives NaN (-inf * 0) and NaN stays NaN.
+constexpr uint32_t kGeluLo = 0x3980;   // bf16 bits of 2^-12
+constexpr uint32_t kGeluHi = 0x4100;   // bf16 bits of 8
+constexpr int kGeluSpan = (int)(kGeluHi - kGeluLo);  // 1920 entries per sign
+constexpr int kGeluBytes = 2 * kGeluSpan * 2;
+
+// LDS: GELU table, gamma, beta, b2, raw rows (two tiles when double-
+// buffered), LayerNorm tile, hidden chunk (reused for the fc2 k-split
+// reduction).  b1 is read from global memory as the fc1 accumulator init.
+template <int C>
+constexpr int mlp_rows_offset() {
+  return kGeluBytes + 3 * C * 4;
+}
+template <int C, bool kDB>
+constexpr int mlp_lds_bytes() {
+  return mlp_rows_offset<C>() + (kDB ? 3 : 2) * 64 * C * 2 + 64 * kHC * 2;
+}
+
+__device__ __forceinline__ f32x4 load_f32x4_lds(const float* p) {
+  return *reinterpret_cast<const f32x4*>(p);
+}
+
+// Packed weight fragment (row tile rt, k-step ks) of a [rows, kIn] weight.
+template <int kIn>
+__device__ __forceinline__ uint4 packed_frag(const uint16_t* w, int rt, int ks, int lane) {
+  return reinterpret_cast<const uint4*>(w)[(rt * (kIn / 32) + ks) * 64 + lane];
+}
+
+// Fills the GELU table (see kGeluLo): entry sign * kGeluSpan + (mag - kGeluLo).
+__device__ __forceinline__ void gelu_table_fill(uint16_t* table, int tid) {
+  for (int e = tid; e < 2 * kGeluSpan; e += kMlpThreads) {
+    const uint32_t sign = e >= kGeluSpan ? 0x8000u : 0u;
+    const uint32_t bits = sign | (kGeluLo + (uint32_t)(e - (sign ? kGeluSpan : 0)));
+    const float x = bf16_bits_to_f32((uint16_t)bits);
+    table[e] = f32_to_bf16_bits(x * 0.5f * (1.f + erff(x * 0.70710678118654752f)));
+  }
+}
+
+// bf16 bits of GELU(x) for the bf16 bits of x.
+__device__ __forceinline__ uint32_t gelu_bf16(uint32_t b, const uint16_t* table) {
+  const uint32_t mag = b & 0x7fffu;
+  const uint32_t sign = b >> 15;
+  int idx = (int)mag - (int)kGeluLo;
+  idx = idx < 0 ? 0 : (idx >= kGeluSpan ? kGeluSpan - 1 : idx);
+  const uint32_t tab = table[idx + (sign ? kGeluSpan : 0)];
+  const uint32_t half = (uint32_t)f32_to_bf16_bits(0.5f * bf16_bits_to_f32((uint16_t)b));
+  const uint32_t big = b == 0xff80u ? 0x7fc0u : ((sign && mag <= 0x7f80u) ? 0x8000u : b);
+  return mag < kGeluLo ? half : (mag < kGeluHi ? tab : big);
+}
+
+// Rows [64 t, 64 t + 64) of x -> LDS (tile_slot layout), direct global->LDS.
+// Rows past the end load row 0 (never stored).
+template <int kCpr>
+__device__ __forceinline__ void mlp_fetch(const MlpParams& p, int t, uint8_t* dst, int wave, int lane) {
+  constexpr int kRounds = kCpr / kMlpWaves;
+  static_assert(kRounds * kMlpWaves == kCpr, "whole wave-rounds of 64 slots");
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int blk = r * kMlpWaves + wave;
+    const int sl = blk * 64 + lane;
+    const int row = sl / kCpr;
+    const int ch = (sl - row * kCpr) ^ ((row >> 1) & 7);
+    const int tok = t * 64 + row;
+    const uint8_t* src = p.x + ((int64_t)(tok < p.tokens ? tok : 0) * kCpr + ch) * 16;
+    dma_to_lds16(src, __builtin_amdgcn_readfirstlane(lds_address(dst + blk * 1024)));
+  }
+}
+
+// The tile's rows -> y, whole lines; rows past the end are skipped.
+template <int kCpr>
+__device__ __forceinline__ void mlp_store(const MlpParams& p, int t, const uint8_t* xr, int tid) {
+  constexpr int kRowStep = kMlpThreads / kCpr;
+  static_assert(kRowStep * kCpr == kMlpThreads && 64 % kRowStep == 0, "whole rows per pass");
+  const int row0 = tid / kCpr, ch = tid - row0 * kCpr;
+  const int64_t first = (int64_t)t * 64;
+  const int rows = p.tokens - (int)first < 64 ? p.tokens - (int)first : 64;
+  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(p.y + first * kCpr * 16, (uint32_t)(rows * kCpr * 16));
+#pragma unroll
+  for (int r = 0; r < 64 / kRowStep; ++r) {
+    const int row = row0 + kRowStep * r;
+    const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(xr + tile_slot(row, ch, kCpr) * 16));
+    stream_store_sc1(val, out, (uint32_t)(row * kCpr + ch) * 16);  // rows past the end fall outside the range
+  }
+}
+
+// LayerNorm of the 64 raw rows -> xn (bf16).  Eight lanes per token, two-pass
+// fp32 statistics over values held in registers; with layernorm == 0 the
+// identity (mean 0, rstd 1, gamma 1, beta 0).
+template <int C>
+__device__ __forceinline__ void mlp_layernorm(const MlpParams& p, const uint8_t* xr, uint8_t* xn, const float* s_gamma,
+                                              const float* s_beta, int tid) {
+  constexpr int kCpr = C / 8, kCPL = kCpr / 8;
+  const int sub = tid & 7;
+  for (int t = tid >> 3; t < 64; t += kMlpThreads / 8) {  // uniform per wave
+    float v[kCPL][8];
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
+      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[k][2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
+        v[k][2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
+      }
+    }
+    float mean = 0.f, rstd = 1.f;
+    if (p.layernorm) {
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += v[k][e];
+      mean = group8_sum(sum) * p.inv_c;
+      float sq = 0.f;
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[k][e] - mean;
+          sq += d * d;
+        }
+      rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      const int c0 = (sub + 8 * k) * 8;
+      float yv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        yv[e] = (v[k][e] - mean) * rstd * s_gamma[c0 + e] + s_beta[c0 + e];
+      const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
+                                 pack_bf16x2(yv[6], yv[7]));
+      *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) = o;
+    }
+  }
+}
+
+template <int C, bool kDB>
+__global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p) {
+  constexpr int H = 4 * C;
+  constexpr int kCpr = C / 8;
+  constexpr int kHcpr = kHC / 8;               // 48 chunks per hidden-chunk row
+  constexpr int kTile = 64 * C * 2;
+  constexpr int kChunks = H / kHC;
+  constexpr int kNF = C / 32;                  // fc2 feature groups of 32
+  constexpr int kKS = kMlpWaves / kNF;         // fc2 k-split (2 for C = 192, 1 for C = 384)
+  constexpr int kKR = kHC / kKS;               // fc2 k range per wave and chunk
+  constexpr int kSteps1 = C / 32;              // fc1 k-steps
+  constexpr int kSteps2 = kKR / 32;            // fc2 k-steps per chunk
+  static_assert(kNF * kKS == kMlpWaves && kCpr % 8 == 0 && kKR % 64 == 0, "shapes");
+  static_assert(kKS <= 2 && (kKS == 1 || 64 * C * 4 <= 64 * kHC * 2), "the fc2 reduction reuses the hidden chunk");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint16_t* s_gelu = reinterpret_cast<uint16_t*>(smem);
+  float* s_gamma = reinterpret_cast<float*>(smem + kGeluBytes);
+  float* s_beta = s_gamma + C;
+  float* s_b2 = s_beta + C;
+  uint8_t* xbuf = smem + mlp_rows_offset<C>();            // raw rows: 1 or 2 tiles
+  uint8_t* xn = xbuf + (kDB ? 2 : 1) * kTile;
+  uint8_t* hb = xn + kTile;                               // hidden chunk [64][kHC] bf16
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  if ((int)blockIdx.x >= p.tiles) return;  // uniform
+  for (int i = tid; i < C; i += kMlpThreads) {
+    // Without LayerNorm the normalisation below is the identity (mean 0, rstd 1, gamma 1, beta 0).
+    s_gamma[i] = p.layernorm && p.gamma != nullptr ? p.gamma[i] : 1.f;
+    s_beta[i] = p.layernorm && p.beta != nullptr ? p.beta[i] : 0.f;
+    s_b2[i] = p.b2 != nullptr ? p.b2[i] : 0.f;
+  }
+  gelu_table_fill(s_gelu, tid);
+
+  const int fr = wave % kNF, kh = wave / kNF;  // fc2: features [32 fr, +32), k part kh
+  // Per-lane LDS byte offsets.  Rows 16 tt + c16 share the swizzle sw, and
+  // chunk 8 a + b (b < 8) of such a row sits in slot row * cpr + 8 a + (b ^ sw),
+  // so every fragment address below is one of two bases plus a constant.
+  const int sw = (c16 >> 1) & 7;
+  uint32_t xa[2], ha[2], hw[2], rw[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    xa[q] = (c16 * kCpr + ((4 * q + g) ^ sw)) * 16;   // fc1 B: chunk 4 ks + g, ks & 1 == q
+    ha[q] = (c16 * kHcpr + ((4 * q + g) ^ sw)) * 16;  // fc2 B: chunk 4 s + g, s & 1 == q
+    // GELU output: hidden columns 32 wave + 16 q + 4 g .. +3
+    hw[q] = (c16 * kHcpr + 8 * (wave >> 1) + ((4 * (wave & 1) + 2 * q + (g >> 1)) ^ sw)) * 16 + (g & 1) * 8;
+    // residual: features 32 fr + 16 q + 4 g .. +3
+    rw[q] = (c16 * kCpr + 8 * (fr >> 1) + ((4 * (fr & 1) + 2 * q + (g >> 1)) ^ sw)) * 16 + (g & 1) * 8;
+  }
+
+  int t = blockIdx.x, prev = -1, par = 0;
+  mlp_fetch<kCpr>(p, t, xbuf, wave, lane);
+  for (;;) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile's rows have landed
+    lds_barrier();
+    uint8_t* xr = xbuf + (kDB ? par * kTile : 0);
+    const int next = t + (int)gridDim.x;
+    if constexpr (kDB) {
+      if (prev >= 0) mlp_store<kCpr>(p, prev, xbuf + (par ^ 1) * kTile, tid);  // the previous tile's rows
+    }
+    mlp_layernorm<C>(p, xr, xn, s_gamma, s_beta, tid);
+    lds_barrier();  // xn complete; the previous tile's rows are read out of the other buffer
+
+    f32x4 acc2[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const f32x4 b = kh == 0 ? load_f32x4_lds(s_b2 + 32 * fr + 16 * i + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) acc2[i][tt] = b;
+    }
+    for (int chk = 0; chk < kChunks; ++chk) {
+      // ---- fc1 + bias: hidden [chk*kHC + 32 wave, +32) x 64 tokens ----------
+      const int rt1 = chk * (kHC / 16) + 2 * wave;
+      f32x4 acc1[2][4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const f32x4 b = p.b1 != nullptr ? *reinterpret_cast<const f32x4*>(p.b1 + 16 * (rt1 + i) + 4 * g)
+                                         : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc1[i][tt] = b;
+      }
+      {
+        uint4 wf[3][2];  // weight ring: step ks in slot ks % 3, loaded two steps ahead
+#pragma unroll
+        for (int s0 = 0; s0 < 2; ++s0)
+#pragma unroll
+          for (int i = 0; i < 2; ++i) wf[s0][i] = packed_frag<C>(p.w1, rt1 + i, s0, lane);
+#pragma unroll
+        for (int ks = 0; ks < kSteps1; ++ks) {
+          if (ks + 2 < kSteps1) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) wf[(ks + 2) % 3][i] = packed_frag<C>(p.w1, rt1 + i, ks + 2, lane);
+          }
+          uint4 xf[4];
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            xf[tt] = *reinterpret_cast<const uint4*>(xn + xa[ks & 1] + (ks >> 1) * 128 + tt * (16 * kCpr * 16));
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+              acc1[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[ks % 3][i]),
+                                                                    __builtin_bit_cast(bf16x8, xf[tt]), acc1[i][tt],
+                                                                    0, 0, 0);
+        }
+      }
+      if constexpr (kDB) {
+        // The next tile's rows stream in under the GELU epilogue (the first
+        // later wait on a global load also waits for them).
+        if (chk == 0 && next < p.tiles) mlp_fetch<kCpr>(p, next, xbuf + (par ^ 1) * kTile, wave, lane);
+      }
+      // ---- bf16 -> GELU -> bf16 into the hidden chunk -------------------------
+      // lane (c16, g) of (i, tt): hidden 16 i + 4 g + r of token 16 tt + c16.
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const uint32_t h01 = pack_bf16x2(acc1[i][tt][0], acc1[i][tt][1]);
+          const uint32_t h23 = pack_bf16x2(acc1[i][tt][2], acc1[i][tt][3]);
+          uint2 pk;
+          pk.x = gelu_bf16(h01 & 0xffffu, s_gelu) | (gelu_bf16(h01 >> 16, s_gelu) << 16);
+          pk.y = gelu_bf16(h23 & 0xffffu, s_gelu) | (gelu_bf16(h23 >> 16, s_gelu) << 16);
+          *reinterpret_cast<uint2*>(hb + hw[i] + tt * (16 * kHcpr * 16)) = pk;
+        }
+      lds_barrier();  // hidden chunk complete
+      // ---- fc2 partial: features [32 fr, +32), hidden [kh*kKR, +kKR) of the chunk ----
+      {
+        const int ks0 = (chk * kHC + kh * kKR) / 32;  // k-step of this wave's first hidden column
+        uint4 wf[3][2];
+#pragma unroll
+        for (int s0 = 0; s0 < 2; ++s0)
+#pragma unroll
+          for (int i = 0; i < 2; ++i) wf[s0][i] = packed_frag<H>(p.w2, 2 * fr + i, ks0 + s0, lane);
+#pragma unroll
+        for (int s = 0; s < kSteps2; ++s) {
+          if (s + 2 < kSteps2) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) wf[(s + 2) % 3][i] = packed_frag<H>(p.w2, 2 * fr + i, ks0 + s + 2, lane);
+          }
+          uint4 hf[4];
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            hf[tt] = *reinterpret_cast<const uint4*>(hb + ha[s & 1] + (kh * (kKR / 64) + (s >> 1)) * 128 +
+                                                     tt * (16 * kHcpr * 16));
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+              acc2[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[s % 3][i]),
+                                                                    __builtin_bit_cast(bf16x8, hf[tt]), acc2[i][tt],
+                                                                    0, 0, 0);
+        }
+      }
+      lds_barrier();  // the chunk is consumed before the next one overwrites it
+    }
+
+    // ---- fc2 k-split reduction, + bias, residual ---------------------------
+    // lane (c16, g) of (i, tt): features 32 fr + 16 i + 4 g + r of token 16 tt + c16.
+    // With the k-split, part kh finishes token tiles tt in [2 kh, 2 kh + 2)
+    // and hands the other two to its partner through the idle hidden chunk
+    // (fp32, 16-byte chunks XOR-swizzled by c16 & 7 against bank conflicts).
+    if constexpr (kKS == 2) {
+      float* red = reinterpret_cast<float*>(hb);  // [64][C] fp32
+      const int rc = ((8 * fr + g) ^ (c16 & 7));  // 16-byte chunk of 32 fr + 4 g (+ 16 i: chunk + 4 i)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          if ((tt >> 1) != kh) *reinterpret_cast<f32x4*>(red + (16 * tt + c16) * C + 4 * (rc ^ (4 * i))) = acc2[i][tt];
+      lds_barrier();
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          if ((tt >> 1) == kh) acc2[i][tt] += *reinterpret_cast<const f32x4*>(red + (16 * tt + c16) * C + 4 * (rc ^ (4 * i)));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        if (kKS == 2 && (tt >> 1) != kh) continue;
+        uint8_t* addr = xr + rw[i] + tt * (16 * kCpr * 16);
+        const uint2 xv = *reinterpret_cast<const uint2*>(addr);
+        uint2 out;
+        out.x = pack_bf16x2(bf16_bits_to_f32((uint16_t)(xv.x & 0xffffu)) + (float)(__bf16)acc2[i][tt][0],
+                            bf16_bits_to_f32((uint16_t)(xv.x >> 16)) + (float)(__bf16)acc2[i][tt][1]);
+        out.y = pack_bf16x2(bf16_bits_to_f32((uint16_t)(xv.y & 0xffffu)) + (float)(__bf16)acc2[i][tt][2],
+                            bf16_bits_to_f32((uint16_t)(xv.y >> 16)) + (float)(__bf16)acc2[i][tt][3]);
+        *reinterpret_cast<uint2*>(addr) = out;
+      }
+    if constexpr (!kDB) {
+      lds_barrier();                                 // output rows complete
+      mlp_store<kCpr>(p, t, xr, tid);
+      if (next >= p.tiles) break;
+      lds_barrier();                                 // the rows are read out before the next load
+      mlp_fetch<kCpr>(p, next, xbuf, wave, lane);
+      t = next;
+    } else {
+      prev = t;
+      if (next >= p.tiles) {
+        lds_barrier();                               // output rows complete
+        mlp_store<kCpr>(p, t, xr, tid);
+        break;
+      }
+      t = next;
+      par ^= 1;
+    }
+  }
+}
+
+template <int C, bool kDB>
+int launch_mlp(const MlpParams& p, hipStream_t s) {
+  constexpr int lds = mlp_lds_bytes<C, kDB>();
+  static_assert(lds <= 160 * 1024, "LDS");
+  auto kern = swin_mlp_kernel<C, kDB>;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  constexpr int kMaxDevices = 64;
+  static int cache[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(TERRA_ERR_LAUNCH, "cannot query the current device");
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kMlpThreads, lds) != hipSuccess)
+      return fail(TERRA_ERR_LAUNCH, "cannot size the MLP grid for this device");
+    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  const int blocks = p.tiles < cache[dev] ? p.tiles : cache[dev];
+  kern<<<blocks, kMlpThreads, lds, s>>>(p);
+  return TERRA_OK;
+}
+
+bool mlp_ranges_overlap(const void* a, const void* b, int64_t bytes) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + (uintptr_t)bytes && y < x + (uintptr_t)bytes;
+}
+
+}  // namespace
+}  // namespace terra
+
+using namespace terra;
+
+extern "C" int terra_swin_mlp_fwd(const void* x, void* y, int dtype, const terra_swin_mlp_desc* desc,
+                                  const float* ln_gamma, const float* ln_beta, const void* fc1_weight,
+                                  const float* fc1_bias, const void* fc2_weight, const float* fc2_bias,
+                                  void* stream) {
+  clear_error();
+  if (desc == nullptr) return fail(TERRA_ERR_NULL, "desc is NULL");
+  if (x == nullptr || y == nullptr || fc1_weight == nullptr || fc2_weight == nullptr)
+    return fail(TERRA_ERR_NULL, "x, y and the packed fc1 / fc2 weights must be non-NULL");
+  if (dtype_size(dtype) == 0) return fail(TERRA_ERR_DTYPE, "unknown dtype %d", dtype);
+  if (dtype != TERRA_DTYPE_BF16) return fail(TERRA_ERR_UNSUPPORTED, "the fused MLP is built for bf16 activations");
+  const terra_swin_mlp_desc& d = *desc;
+  if (d.tokens <= 0) return fail(TERRA_ERR_SHAPE, "tokens must be positive");
+  if (d.channels != 192 && d.channels != 384)
+    return fail(TERRA_ERR_UNSUPPORTED, "channels %d not in {192, 384}", d.channels);
+  if (d.hidden != 4 * d.channels)
+    return fail(TERRA_ERR_UNSUPPORTED, "hidden %d != 4 * channels (%d)", d.hidden, 4 * d.channels);
+  if (!(d.ln_eps >= 0.f)) return fail(TERRA_ERR_SHAPE, "ln_eps must be >= 0");
+  for (const void* ptr : {x, (const void*)y, fc1_weight, fc2_weight, (const void*)ln_gamma, (const void*)ln_beta,
+                          (const void*)fc1_bias, (const void*)fc2_bias})
+    if (((uintptr_t)ptr & 15u) != 0) return fail(TERRA_ERR_ALIGN, "tensors must be 16-byte aligned");
+  const int64_t bytes = (int64_t)d.tokens * d.channels * 2;
+  if (bytes >= (1ll << 32)) return fail(TERRA_ERR_SHAPE, "x must be under 4 GiB; split the tokens");
+  if (x != y && mlp_ranges_overlap(x, y, bytes)) return fail(TERRA_ERR_SHAPE, "y overlaps x without being x");
+
+  MlpParams p;
+  memset(&p, 0, sizeof(p));
+  p.x = static_cast<const uint8_t*>(x);
+  p.y = static_cast<uint8_t*>(y);
+  p.gamma = ln_gamma;
+  p.beta = ln_beta;
+  p.w1 = static_cast<const uint16_t*>(fc1_weight);
+  p.b1 = fc1_bias;
+  p.w2 = static_cast<const uint16_t*>(fc2_weight);
+  p.b2 = fc2_bias;
+  p.eps = d.ln_eps;
+  p.inv_c = 1.f / (float)d.channels;
+  p.tokens = d.tokens;
+  p.tiles = (d.tokens + 63) / 64;
+  p.layernorm = d.layernorm != 0;
+  hipStream_t s = (hipStream_t)stream;
+  const int st = d.channels == 192 ? launch_mlp<192, true>(p, s) : launch_mlp<384, false>(p, s);
+  if (st != TERRA_OK) return st;
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "terra_swin_mlp_fwd launch failed: %s", hipGetErrorString(e));
+  return TERRA_OK;
+}

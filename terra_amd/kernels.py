@@ -513,3 +513,68 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
                                               _stream(dev))
     _lib.check(st, "terra_swin_block_fwd")
     return out
+
+
+MLP_CHANNELS = (192, 384)
+
+
+def swin_mlp_supported(x: torch.Tensor, channels: int, hidden: int) -> bool:
+    """Whether :func:`swin_mlp` serves this call (bf16 device tensor,
+    C in {192, 384}, hidden = 4 C)."""
+    return (x.device.type == "cuda" and x.dtype == torch.bfloat16 and channels in MLP_CHANNELS
+            and hidden == 4 * channels)
+
+
+def swin_mlp(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_bias: Optional[torch.Tensor],
+             fc2_weight: torch.Tensor, fc2_bias: Optional[torch.Tensor],
+             ln_weight: Optional[torch.Tensor] = None, ln_bias: Optional[torch.Tensor] = None,
+             ln_eps: float = 1e-5, layernorm: bool = True, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused MLP half-block over the token rows of ``x`` [..., C] (bf16):
+
+        y = x + fc2(GELU(fc1(LayerNorm(x))))
+
+    i.e. SequentialMlp.forward (models/mlp.py:152-172) in one kernel.
+    ``fc1_weight`` / ``fc2_weight`` come from :func:`pack_linear` (flat, bf16)
+    of the nn.Linear weights [4C, C] / [C, 4C]; biases and the LayerNorm
+    affine are passed as fp32 (or None).  ``out`` may be ``x``.
+    """
+    dev = _require_device(x, fc1_weight, fc2_weight)
+    code = _dtype_code(x, (torch.bfloat16,))
+    if not x.is_contiguous() or x.dim() < 1:
+        raise ValueError("x must be a contiguous [..., C] tensor")
+    C = x.shape[-1]
+    H = fc1_weight.numel() // C if C else 0
+    if not swin_mlp_supported(x, C, H):
+        raise ValueError(f"the fused MLP serves bf16 rows of C in {MLP_CHANNELS} with hidden 4C "
+                         f"(got {x.dtype}, C {C}, hidden {H})")
+    tokens = x.numel() // C
+    if tokens == 0:
+        return x.clone() if out is None else out
+    for name, t, n in (("fc1_weight", fc1_weight, H * C), ("fc2_weight", fc2_weight, C * H)):
+        if t.numel() != n or t.dtype != x.dtype or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous packed {x.dtype} tensor of {n} elements")
+
+    def f32(t, n, name):
+        if t is None:
+            return None
+        _require_device(x, t)
+        if t.numel() != n:
+            raise ValueError(f"{name} must have {n} elements")
+        return t.detach().reshape(-1).to(torch.float32).contiguous()
+
+    params = (f32(ln_weight, C, "ln_weight") if layernorm else None,
+              f32(ln_bias, C, "ln_bias") if layernorm else None,
+              f32(fc1_bias, H, "fc1_bias"), f32(fc2_bias, C, "fc2_bias"))
+    d = _lib.SwinMlpDesc()
+    d.tokens, d.channels, d.hidden = int(tokens), int(C), int(H)
+    d.layernorm, d.ln_eps = int(bool(layernorm)), float(ln_eps)
+    if out is None:
+        out = torch.empty_like(x)
+    elif tuple(out.shape) != tuple(x.shape) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
+        raise ValueError("out must be a contiguous tensor like x")
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_mlp_fwd(_ptr(x), _ptr(out), code, ctypes.byref(d), _ptr(params[0]),
+                                            _ptr(params[1]), _ptr(fc1_weight), _ptr(params[2]), _ptr(fc2_weight),
+                                            _ptr(params[3]), _stream(dev))
+    _lib.check(st, "terra_swin_mlp_fwd")
+    return out

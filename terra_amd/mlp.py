@@ -1,0 +1,102 @@
+"""Drop-in ``SequentialMlp`` (models/mlp.py:138-172), the MLP half of a Swin
+block: ``x + fc2(GELU(fc1(norm2(x))))`` per token.
+
+For bf16 activations with C in {192, 384} and hidden = 4C, the forward is one
+HIP kernel (``kernels.swin_mlp``): LayerNorm, fc1 on MFMA, exact GELU, fc2 on
+MFMA and the residual add, with the hidden layer kept on chip.  The module
+packs ``fc1.weight`` / ``fc2.weight`` with ``kernels.pack_linear`` and caches
+the packed weights and fp32 copies of the small parameters until a
+parameter's data pointer or in-place version changes.
+
+Other shapes and dtypes, and any call that needs a gradient, run the
+reference's own sequence of torch modules on the device (norm2, fc1, act,
+fc2, residual).  Parameter names (``norm2``, ``fc1``, ``fc2``) and the seeded
+initialisation follow the reference so its checkpoints load.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import config, kernels
+from .attention import make_linear_with_seed
+
+
+def _disable_parameters_if_mlp_off(module: torch.nn.Module) -> None:
+    """models/mlp.py:18-21."""
+    if not config.use_MLP:
+        for param in module.parameters():
+            param.requires_grad_(False)
+
+
+class SequentialMlp(torch.nn.Module):
+    def __init__(self, in_features, hidden_features=None, out_features=None, act_layer=torch.nn.GELU, drop=0.,
+                 init_seed_base=None):
+        super().__init__()
+        out_features = out_features or in_features
+        hidden_features = hidden_features or in_features
+        if config.use_layernorm:
+            self.norm2 = torch.nn.LayerNorm(in_features)
+        seed = (lambda k: None if init_seed_base is None else init_seed_base + k)  # noqa: E731
+        self.fc1 = make_linear_with_seed(in_features, hidden_features, init_seed=seed(1))
+        self.act = act_layer()
+        self.fc2 = make_linear_with_seed(hidden_features, out_features, init_seed=seed(2))
+        _disable_parameters_if_mlp_off(self)
+        self.use_fused_mlp = True
+
+    def _fusable(self, x: torch.Tensor) -> bool:
+        """One kernel serves the call: bf16 rows of C in {192, 384}, hidden
+        4C, out C, the exact GELU, a plain LayerNorm over C (or none), biased
+        linears of the activation dtype, and no gradient needed."""
+        if not self.use_fused_mlp or x.dim() < 1:
+            return False
+        C = x.shape[-1]
+        fc1, fc2 = self.fc1, self.fc2
+        if not kernels.swin_mlp_supported(x, C, fc1.out_features) or fc1.in_features != C or fc2.out_features != C:
+            return False
+        if type(self.act) is not torch.nn.GELU or self.act.approximate != "none":
+            return False
+        if config.use_layernorm:
+            n = self.norm2
+            if type(n) is not torch.nn.LayerNorm or tuple(n.normalized_shape) != (C,) or n.weight is None:
+                return False
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        return all(l.weight.dtype == x.dtype and l.bias is not None for l in (fc1, fc2))
+
+    def _fused_args(self) -> dict:
+        tensors = [self.fc1.weight, self.fc1.bias, self.fc2.weight, self.fc2.bias]
+        if config.use_layernorm:
+            tensors += [self.norm2.weight, self.norm2.bias]
+        key = tuple((t.data_ptr(), t._version, t.device) if t is not None else None for t in tensors)
+        cached = getattr(self, "_fused_cache", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        with torch.no_grad():
+            f32 = lambda t: None if t is None else t.detach().to(torch.float32).contiguous()  # noqa: E731
+            args = dict(
+                fc1_weight=kernels.pack_linear(self.fc1.weight.detach().contiguous()),
+                fc1_bias=f32(self.fc1.bias),
+                fc2_weight=kernels.pack_linear(self.fc2.weight.detach().contiguous()),
+                fc2_bias=f32(self.fc2.bias),
+                ln_weight=f32(self.norm2.weight) if config.use_layernorm else None,
+                ln_bias=f32(self.norm2.bias) if config.use_layernorm else None,
+                ln_eps=float(self.norm2.eps) if config.use_layernorm else 0.0,
+                layernorm=bool(config.use_layernorm),
+            )
+        self._fused_cache = (key, args)
+        return args
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if not config.use_MLP:
+            return x
+        if x.device.type != "cuda":
+            raise RuntimeError("terra_amd: SequentialMlp runs on device tensors only (got a CPU tensor)")
+        if self._fusable(x):
+            return kernels.swin_mlp(x.contiguous(), out=out, **self._fused_args())
+        shortcut = x
+        if config.use_layernorm:
+            x = self.norm2(x)
+        x = self.fc2(self.act(self.fc1(x)))
+        return x + shortcut

@@ -39,6 +39,7 @@ def test_abi_version_and_struct_sizes():
     assert ctypes.sizeof(L.SwinAttnDesc) == 4 * len(L.SwinAttnDesc._fields_) == 92
     assert ctypes.sizeof(L.SwinBlockDesc) == 60 + 4 * (len(L.SwinBlockDesc._fields_) - 1) == 92
     assert ctypes.sizeof(L.SwinAttnBwdDesc) == 92 + 4 * 4 == 108
+    assert ctypes.sizeof(L.SwinMlpDesc) == 4 * len(L.SwinMlpDesc._fields_) == 20
 
 
 def _geom(**kw):
@@ -271,3 +272,53 @@ def test_pack_linear_rejects_bad_arguments():
     assert lib.terra_swin_pack_linear(ctypes.c_void_p((1 << 20) + 2), ctypes.c_void_p(1 << 24), L.DTYPE_BF16,
                                       16, 32, None) == -4
     assert lib.terra_swin_pack_linear(FAKE, FAKE, L.DTYPE_BF16, 16, 32, None) == -3  # overlap
+
+
+def _mlp_desc(**kw):
+    d = L.SwinMlpDesc()
+    vals = dict(tokens=100, channels=192, hidden=768, layernorm=1, ln_eps=1e-5)
+    vals.update(kw)
+    for k, v in vals.items():
+        setattr(d, k, v)
+    return d
+
+
+def _mlp_call(d, dtype=L.DTYPE_BF16, x=FAKE, y=ctypes.c_void_p(1 << 24), w1=FAKE, b1=None):
+    return L.load().terra_swin_mlp_fwd(x, y, dtype, ctypes.byref(d) if d is not None else None, None, None,
+                                       w1, b1, FAKE, None, None)
+
+
+@pytest.mark.parametrize("kw,dtype,code,text", [
+    ({}, L.DTYPE_F32, -5, "bf16 activations"),
+    ({}, 9, -2, "unknown dtype"),
+    ({"channels": 256, "hidden": 1024}, L.DTYPE_BF16, -5, "not in {192, 384}"),
+    ({"hidden": 576}, L.DTYPE_BF16, -5, "4 * channels"),
+    ({"tokens": 0}, L.DTYPE_BF16, -3, "tokens must be positive"),
+    ({"ln_eps": -1.0}, L.DTYPE_BF16, -3, "ln_eps"),
+    ({"tokens": 1 << 30}, L.DTYPE_BF16, -3, "under 4 GiB"),
+])
+def test_mlp_rejects_bad_descriptors(kw, dtype, code, text):
+    st = _mlp_call(_mlp_desc(**kw), dtype)
+    assert st == code, L.last_error()
+    assert text in L.last_error()
+
+
+def test_mlp_rejects_null_alignment_overlap():
+    d = _mlp_desc()
+    assert _mlp_call(None) == -1
+    assert _mlp_call(d, x=None) == -1
+    assert _mlp_call(d, w1=None) == -1
+    assert _mlp_call(d, x=ctypes.c_void_p((1 << 20) + 8)) == -4
+    assert _mlp_call(d, b1=ctypes.c_void_p((1 << 20) + 4)) == -4
+    assert _mlp_call(d, y=ctypes.c_void_p((1 << 20) + 4096)) == -3  # overlaps x without being x
+    assert "overlaps" in L.last_error()
+
+
+def test_mlp_wrapper_raises_on_cpu_tensors():
+    x = torch.zeros(64, 192, dtype=torch.bfloat16)
+    w = torch.zeros(768 * 192, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        kernels.swin_mlp(x, w, None, w, None)
+    from terra_amd.mlp import SequentialMlp
+    with pytest.raises(RuntimeError, match="device tensors only"):
+        SequentialMlp(192, 768)(x.float())

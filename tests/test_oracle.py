@@ -260,3 +260,69 @@ def test_tiny_fixture_oracle_has_not_drifted():
     want = brute.attention(qkv[..., :C].numpy(), qkv[..., C:2 * C].numpy(), qkv[..., 2 * C:].numpy(), nH,
                            (C // nH) ** -0.5, bias, mask.numpy())
     np.testing.assert_allclose(want, z["o"], rtol=1e-6, atol=1e-7)
+
+
+# ----------------------------------------------------------------------------
+# MLP half (models/mlp.py:152-172)
+# ----------------------------------------------------------------------------
+
+def test_gelu_known_values_and_torch():
+    # Phi(1) = 0.8413447460685429, Phi(-1) = 0.15865525393145707 (normal table)
+    assert abs(brute.gelu(1.0) - 0.8413447460685429) < 1e-15
+    assert abs(brute.gelu(-1.0) + 0.15865525393145707) < 1e-15
+    assert brute.gelu(0.0) == 0.0 and brute.gelu(40.0) == 40.0 and brute.gelu(-40.0) == 0.0
+    xs = torch.linspace(-9, 9, 1001, dtype=torch.float64)
+    ref = torch.tensor([brute.gelu(float(v)) for v in xs], dtype=torch.float64)
+    assert torch.allclose(F.gelu(xs), ref, rtol=1e-14, atol=1e-15)
+
+
+def test_bf16_round_matches_torch_cast():
+    bits = np.arange(0, 1 << 32, 65537, dtype=np.uint64).astype(np.uint32)
+    f = bits.view(np.float32)
+    ours = brute.bf16_round(f)
+    theirs = torch.from_numpy(f.copy()).bfloat16().float().numpy()
+    fin = np.isfinite(f)
+    assert np.array_equal(ours[fin].view(np.uint32), theirs[fin].view(np.uint32))
+    assert np.array_equal(np.isnan(ours), np.isnan(theirs))
+    # ties to even: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 and rounds to 1
+    assert brute.bf16_round(np.float32(1 + 2 ** -8)) == 1.0
+    assert brute.bf16_round(np.float32(1 + 3 * 2 ** -8)) == np.float32(1 + 2 ** -6)
+
+
+def _mlp_params(C, hid, seed, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    return {
+        "norm2.weight": 1 + 0.1 * torch.randn(C, generator=g, dtype=dtype),
+        "norm2.bias": 0.1 * torch.randn(C, generator=g, dtype=dtype),
+        "fc1.weight": torch.randn(hid, C, generator=g, dtype=dtype) / C ** 0.5,
+        "fc1.bias": 0.1 * torch.randn(hid, generator=g, dtype=dtype),
+        "fc2.weight": torch.randn(C, hid, generator=g, dtype=dtype) / hid ** 0.5,
+        "fc2.bias": 0.1 * torch.randn(C, generator=g, dtype=dtype),
+    }
+
+
+@pytest.mark.parametrize("use_ln", [True, False])
+def test_mlp_matches_token_loops(use_ln):
+    C, hid = 6, 10  # hid != C: a transposed weight cannot go unnoticed
+    p = _mlp_params(C, hid, 3)
+    x = _rand((2, 3, C), 4)
+    ref = brute.mlp(x.numpy(), {k: v.numpy() for k, v in p.items()}, use_layernorm=use_ln)
+    got = so.mlp(x, p, use_layernorm=use_ln).double()
+    assert np.allclose(got.numpy(), ref, rtol=1e-5, atol=1e-6)  # so.mlp computes in float32
+
+
+@pytest.mark.parametrize("use_ln", [True, False])
+def test_mlp_bf16_matches_token_loops(use_ln):
+    C, hid = 8, 12
+    p = {k: v.bfloat16().double() if "weight" in k and "norm" not in k else v for k, v in _mlp_params(C, hid, 5).items()}
+    x = _rand((5, C), 6).bfloat16().double()
+    ref = brute.mlp(x.numpy(), {k: v.numpy() for k, v in p.items()}, use_layernorm=use_ln, round_bf16=True)
+    got = so.mlp_bf16(x, p, use_layernorm=use_ln).numpy()
+    # identical rounding points: equal except where float64 summation-order
+    # noise crosses a bf16 rounding boundary (then one bf16 ulp)
+    ulp = np.abs(ref) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(got - ref) <= ulp)
+    assert np.mean(got == ref) > 0.95
+    # and within bf16 tolerance of the unrounded float64 module
+    exact = brute.mlp(x.numpy(), {k: v.numpy() for k, v in p.items()}, use_layernorm=use_ln)
+    assert np.max(np.abs(got - exact)) <= 3e-2 * np.max(np.abs(exact))
