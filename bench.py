@@ -14,7 +14,10 @@ MFMA-bound (1.80e11 flop against 403 MB of HBM traffic per launch), so
 `achieved` is TFLOP/s against the dense bf16 peak.  `five_stage` reports the
 same step through the unfused path (LN+partition gather, q/k/v GEMM, attention
 kernel, proj GEMM, reverse+residual scatter) for comparison, with each of its
-HIP kernels timed alone on the step's own arguments.
+HIP kernels timed alone on the step's own arguments.  `attention_backward` is
+the training path's attention-core backward on the step's q / k / v;
+`mlp_half` the block's MLP half (SequentialMlp) as one kernel against the same
+module through torch's ops, and `full_block` both halves together.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
     python bench.py --mode kernels --steps 3     # the step's kernels only,
@@ -74,11 +77,11 @@ def measured_traffic():
 def run_kernels(cfg, blk, x, steps):
     """The step's kernels on the step's own tensors, `steps` times: the fused
     block kernel, then the five-stage path's three HIP kernels, then the
-    attention backward on the same q / k / v; then a device copy of 192 MiB
-    (the counter calibration)."""
+    attention backward on the same q / k / v, then the fused MLP half on the
+    block's output; then a device copy of 192 MiB (the counter calibration)."""
     import torch
 
-    from terra_amd import kernels
+    from terra_amd import kernels, workloads
 
     B, L, C = x.shape
     geom = blk.geometry(B)
@@ -101,6 +104,10 @@ def run_kernels(cfg, blk, x, steps):
                                               bias_table=blk.attn.relative_position_bias_table, mask=mask,
                                               dq=dqkv[..., :C], dk=dqkv[..., C:2 * C], dv=dqkv[..., 2 * C:],
                                               dbias=dbias)
+        y = blk(x)
+        mlp = workloads.mlp_for(cfg, 1).to(x.device).to(x.dtype)
+        for _ in range(steps):
+            mlp(y)
         src = torch.ones(192 << 20, dtype=torch.uint8, device=x.device)
         dst = torch.zeros_like(src)
         for _ in range(3):
@@ -264,6 +271,22 @@ def main():
             bias_table=kw.get("bias_table"), mask=kw.get("mask"), dq=dqkv[..., :C_], dk=dqkv[..., C_:2 * C_],
             dv=dqkv[..., 2 * C_:], dbias=dbias))
         iso["attention_backward"] = isolated_us("attention_backward")
+        # The block's MLP half (row f4's buildable part): the SequentialMlp that
+        # follows the attention half, on the step's output, as one kernel; and
+        # the same module through torch's ops (the reference's norm2 / fc1 /
+        # GELU / fc2 / add sequence) for comparison.
+        mlp = workloads.mlp_for(cfg, 1).to(dev).to(dtype)
+        with torch.no_grad():
+            y_blk = blk(x)
+            if not mlp._fusable(y_blk):
+                raise RuntimeError("the fused MLP kernel does not serve this configuration")
+            mlp_args = mlp._fused_args()
+        last_call["mlp"] = (kernels.swin_mlp, (y_blk,), dict(out=torch.empty_like(y_blk), **mlp_args))
+        iso["mlp"] = isolated_us("mlp")
+        mlp.use_fused_mlp = False
+        last_call["mlp_torch"] = (mlp, (y_blk,), {})
+        iso["mlp_torch"] = isolated_us("mlp_torch")
+        mlp.use_fused_mlp = True
     finally:
         for n in names:
             setattr(kernels, n, orig[n])
@@ -281,6 +304,9 @@ def main():
     bwd_bytes = 7.0 * B_ * N * C * elt
     bwd_flops = 10.0 * n_real * n_real * C * B_
     rev_bytes = B_ * N * C * elt + 2 * grid_bytes
+    grid_tokens = cfg.batch * cfg.height * cfg.width
+    mlp_flops = 2.0 * 2.0 * grid_tokens * C * (4 * C)    # fc1 + fc2
+    mlp_bytes = 2.0 * grid_bytes                         # x read once, y written once
 
     def avg_us(name):
         return 1e3 * statistics.mean(a.elapsed_time(b) for a, b in events[name])
@@ -359,6 +385,19 @@ def main():
             "algorithmic_flops_per_launch": bwd_flops,
         },
     }
+    res["mlp_half"] = {
+        "kernel": "swin_mlp_kernel<192, true> (LayerNorm + fc1 + exact GELU + fc2 + residual, hidden layer on chip)",
+        "us": iso["mlp"],
+        "TFLOP_s": mlp_flops / (iso["mlp"] * 1e-6) / 1e12,
+        "mfma_frac": mlp_flops / (iso["mlp"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "GB_s": mlp_bytes / (iso["mlp"] * 1e-6) / 1e9,
+        "torch_us": iso["mlp_torch"],
+        "speedup_vs_torch": iso["mlp_torch"] / iso["mlp"],
+        "algorithmic_flops_per_launch": mlp_flops,
+        "algorithmic_bytes_per_launch": mlp_bytes,
+    }
+    # The whole Swin block (attention half + MLP half), both fused.
+    res["full_block"] = {"us": t_blk + iso["mlp"], "tokens_per_s": tokens / ((t_blk + iso["mlp"]) * 1e-6)}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg, blk, land if land is not None else
                                            torch.zeros(cfg.height, cfg.width, dtype=torch.bool), args.cpu_seconds)

@@ -43,17 +43,17 @@ constexpr int kMlpThreads = 64 * kMlpWaves;
 constexpr int kHC = 32 * kMlpWaves;  // hidden features per chunk: 32 per wave
 
 // GELU of a bf16 input by table.  The fc1 output is rounded to bf16 before
-// the activation, so GELU sees one of 2^16 inputs; for 2^-12 <= |x| < 8 the
+// the activation, so GELU sees one of 2^16 inputs; for 2^-16 <= |x| < 32 the
 // bf16 result is read from a table that each workgroup fills at start with
 // the module's formula, 0.5 x (1 + erf(x / sqrt 2)) in fp32 rounded to bf16
 // (the value PyTorch's GPU kernel computes for a bf16 input).  Outside that
-// range the bf16 result has a closed form: 0.5 x for |x| < 2^-12 (the fp32
-// value is 0.5 x (1 + d) with |d| < 2^-12, and 0.5 x is a bf16 value, so it
-// rounds to 0.5 x); x for x >= 8 (erf = 1 in fp32); -0 for x <= -8 (erf = -1
-// in fp32); -inf gives NaN (-inf * 0) and NaN stays NaN.
-constexpr uint32_t kGeluLo = 0x3980;   // bf16 bits of 2^-12
-constexpr uint32_t kGeluHi = 0x4100;   // bf16 bits of 8
-constexpr int kGeluSpan = (int)(kGeluHi - kGeluLo);  // 1920 entries per sign
+// range the bf16 result has a closed form: 0.5 x for |x| < 2^-16 (the fp32
+// value is 0.5 x (1 + d) with |d| < 2^-16, and 0.5 x is a bf16 value, so it
+// rounds to 0.5 x); x for x >= 32 (erf = 1 in fp32); -0 for x <= -32 (erf =
+// -1 in fp32); -inf gives NaN (-inf * 0) and NaN stays NaN.
+constexpr uint32_t kGeluLo = 0x3780;   // bf16 bits of 2^-16
+constexpr uint32_t kGeluHi = 0x4200;   // bf16 bits of 32
+constexpr int kGeluSpan = (int)(kGeluHi - kGeluLo);  // 2688 entries per sign
 constexpr int kGeluBytes = 2 * kGeluSpan * 2;
 
 // LDS: GELU table, gamma, beta, b2, raw rows (two tiles when double-
@@ -78,6 +78,28 @@ __device__ __forceinline__ uint4 packed_frag(const uint16_t* w, int rt, int ks, 
   return reinterpret_cast<const uint4*>(w)[(rt * (kIn / 32) + ks) * 64 + lane];
 }
 
+// Tiles in LDS: 64 rows of 16-byte chunks, stored as column blocks of kBlk =
+// 24 chunks (384-byte rows): one block for a C = 192 tile, two for C = 384
+// and for a hidden chunk.  Within a block, chunk b of row r sits in slot
+// r * 24 + (b ^ ((r >> 1) & 7)): the 384-byte pitch puts odd rows half a
+// bank period after even ones and the XOR spreads the row pairs over the 8
+// 16-byte columns, so the 16 rows of a fragment read (and the 32 lanes of an
+// 8-byte write) hit distinct banks.
+constexpr int kBlk = 24;
+constexpr int kBlkBytes = 64 * kBlk * 16;
+
+__device__ __forceinline__ int mlp_slot(int row, int chunk) {
+  const int b = chunk >= kBlk ? 1 : 0;  // chunk < 2 kBlk
+  return b * (64 * kBlk) + row * kBlk + ((chunk - b * kBlk) ^ ((row >> 1) & 7));
+}
+
+// Byte offset of chunk c0 + g of row 16 tt + c16 (c0 a multiple of 4, g < 4)
+// relative to the lane's base for parity (c0 >> 2) & 1, which is
+// (c16 * kBlk + ((4 * parity + g) ^ sw)) * 16 with sw = (c16 >> 1) & 7.
+constexpr int frag_off(int c0, int tt) {
+  return (c0 / kBlk) * kBlkBytes + ((c0 % kBlk) >> 3) * 128 + tt * (16 * kBlk * 16);
+}
+
 // Fills the GELU table (see kGeluLo): entry sign * kGeluSpan + (mag - kGeluLo).
 __device__ __forceinline__ void gelu_table_fill(uint16_t* table, int tid) {
   for (int e = tid; e < 2 * kGeluSpan; e += kMlpThreads) {
@@ -88,19 +110,36 @@ __device__ __forceinline__ void gelu_table_fill(uint16_t* table, int tid) {
   }
 }
 
-// bf16 bits of GELU(x) for the bf16 bits of x.
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// Table lookups for the two bf16 values of `p` (two GELU results, packed the
+// same way), with packed 16-bit index arithmetic.  `dmax` collects mag - kGeluLo
+// per half (wrapping below kGeluLo): a value >= kGeluSpan marks an input
+// outside the table, whose lookup here is clamped and wrong.
+__device__ __forceinline__ uint32_t gelu_pair_table(uint32_t p, const uint16_t* table, u16x2& dmax) {
+  const u16x2 v = __builtin_bit_cast(u16x2, p);
+  const u16x2 d = (v & (u16x2)0x7fff) - (u16x2)(uint16_t)kGeluLo;
+  dmax = __builtin_elementwise_max(dmax, d);
+  const u16x2 idx = __builtin_elementwise_min(d, (u16x2)(uint16_t)(kGeluSpan - 1)) + (v >> 15) * (u16x2)(uint16_t)kGeluSpan;
+  const u16x2 off = idx << 1;  // byte offsets (< 2^15)
+  const uint8_t* t = reinterpret_cast<const uint8_t*>(table);
+  return (uint32_t)*reinterpret_cast<const uint16_t*>(t + off.x) |
+         ((uint32_t)*reinterpret_cast<const uint16_t*>(t + off.y) << 16);
+}
+
+// bf16 bits of GELU(x) for the bf16 bits of any x (the table or the closed forms).
 __device__ __forceinline__ uint32_t gelu_bf16(uint32_t b, const uint16_t* table) {
   const uint32_t mag = b & 0x7fffu;
   const uint32_t sign = b >> 15;
-  int idx = (int)mag - (int)kGeluLo;
-  idx = idx < 0 ? 0 : (idx >= kGeluSpan ? kGeluSpan - 1 : idx);
-  const uint32_t tab = table[idx + (sign ? kGeluSpan : 0)];
-  const uint32_t half = (uint32_t)f32_to_bf16_bits(0.5f * bf16_bits_to_f32((uint16_t)b));
+  const uint32_t d = mag - kGeluLo;  // wraps below kGeluLo
+  const uint32_t idx = (d < (uint32_t)kGeluSpan ? d : 0u) + (sign ? kGeluSpan : 0);
+  const uint32_t tab = table[idx];
+  const uint32_t half = __builtin_bit_cast(uint16_t, (__bf16)(0.5f * bf16_bits_to_f32((uint16_t)b)));
   const uint32_t big = b == 0xff80u ? 0x7fc0u : ((sign && mag <= 0x7f80u) ? 0x8000u : b);
   return mag < kGeluLo ? half : (mag < kGeluHi ? tab : big);
 }
 
-// Rows [64 t, 64 t + 64) of x -> LDS (tile_slot layout), direct global->LDS.
+// Rows [64 t, 64 t + 64) of x -> LDS (mlp_slot layout), direct global->LDS.
 // Rows past the end load row 0 (never stored).
 template <int kCpr>
 __device__ __forceinline__ void mlp_fetch(const MlpParams& p, int t, uint8_t* dst, int wave, int lane) {
@@ -110,8 +149,10 @@ __device__ __forceinline__ void mlp_fetch(const MlpParams& p, int t, uint8_t* ds
   for (int r = 0; r < kRounds; ++r) {
     const int blk = r * kMlpWaves + wave;
     const int sl = blk * 64 + lane;
-    const int row = sl / kCpr;
-    const int ch = (sl - row * kCpr) ^ ((row >> 1) & 7);
+    const int cb = sl >= 64 * kBlk ? 1 : 0;  // column block
+    const int rem = sl - cb * (64 * kBlk);
+    const int row = rem / kBlk;
+    const int ch = cb * kBlk + ((rem - row * kBlk) ^ ((row >> 1) & 7));
     const int tok = t * 64 + row;
     const uint8_t* src = p.x + ((int64_t)(tok < p.tokens ? tok : 0) * kCpr + ch) * 16;
     dma_to_lds16(src, __builtin_amdgcn_readfirstlane(lds_address(dst + blk * 1024)));
@@ -130,7 +171,7 @@ __device__ __forceinline__ void mlp_store(const MlpParams& p, int t, const uint8
 #pragma unroll
   for (int r = 0; r < 64 / kRowStep; ++r) {
     const int row = row0 + kRowStep * r;
-    const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(xr + tile_slot(row, ch, kCpr) * 16));
+    const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(xr + mlp_slot(row, ch) * 16));
     stream_store_sc1(val, out, (uint32_t)(row * kCpr + ch) * 16);  // rows past the end fall outside the range
   }
 }
@@ -147,7 +188,7 @@ __device__ __forceinline__ void mlp_layernorm(const MlpParams& p, const uint8_t*
     float v[kCPL][8];
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
+      const uint4 raw = *reinterpret_cast<const uint4*>(xr + mlp_slot(t, sub + 8 * k) * 16);
       const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -182,7 +223,7 @@ __device__ __forceinline__ void mlp_layernorm(const MlpParams& p, const uint8_t*
         yv[e] = (v[k][e] - mean) * rstd * s_gamma[c0 + e] + s_beta[c0 + e];
       const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
                                  pack_bf16x2(yv[6], yv[7]));
-      *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) = o;
+      *reinterpret_cast<uint4*>(xn + mlp_slot(t, sub + 8 * k) * 16) = o;
     }
   }
 }
@@ -191,7 +232,6 @@ template <int C, bool kDB>
 __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p) {
   constexpr int H = 4 * C;
   constexpr int kCpr = C / 8;
-  constexpr int kHcpr = kHC / 8;               // 48 chunks per hidden-chunk row
   constexpr int kTile = 64 * C * 2;
   constexpr int kChunks = H / kHC;
   constexpr int kNF = C / 32;                  // fc2 feature groups of 32
@@ -199,7 +239,7 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
   constexpr int kKR = kHC / kKS;               // fc2 k range per wave and chunk
   constexpr int kSteps1 = C / 32;              // fc1 k-steps
   constexpr int kSteps2 = kKR / 32;            // fc2 k-steps per chunk
-  static_assert(kNF * kKS == kMlpWaves && kCpr % 8 == 0 && kKR % 64 == 0, "shapes");
+  static_assert(kNF * kKS == kMlpWaves && kCpr % kBlk == 0 && kCpr <= 2 * kBlk && (kKR / 8) % kBlk == 0, "shapes");
   static_assert(kKS <= 2 && (kKS == 1 || 64 * C * 4 <= 64 * kHC * 2), "the fc2 reduction reuses the hidden chunk");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t* s_gelu = reinterpret_cast<uint16_t*>(smem);
@@ -224,19 +264,20 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
   gelu_table_fill(s_gelu, tid);
 
   const int fr = wave % kNF, kh = wave / kNF;  // fc2: features [32 fr, +32), k part kh
-  // Per-lane LDS byte offsets.  Rows 16 tt + c16 share the swizzle sw, and
-  // chunk 8 a + b (b < 8) of such a row sits in slot row * cpr + 8 a + (b ^ sw),
-  // so every fragment address below is one of two bases plus a constant.
+  // Per-lane LDS byte offsets (see frag_off): every fragment address below
+  // is one of two bases plus a constant.
   const int sw = (c16 >> 1) & 7;
-  uint32_t xa[2], ha[2], hw[2], rw[2];
+  uint32_t fa[2], hw[2], rw[2];
+  const int wl = wave % 6, fl = fr % 6;  // 4-chunk column groups within a block
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    xa[q] = (c16 * kCpr + ((4 * q + g) ^ sw)) * 16;   // fc1 B: chunk 4 ks + g, ks & 1 == q
-    ha[q] = (c16 * kHcpr + ((4 * q + g) ^ sw)) * 16;  // fc2 B: chunk 4 s + g, s & 1 == q
-    // GELU output: hidden columns 32 wave + 16 q + 4 g .. +3
-    hw[q] = (c16 * kHcpr + 8 * (wave >> 1) + ((4 * (wave & 1) + 2 * q + (g >> 1)) ^ sw)) * 16 + (g & 1) * 8;
+    fa[q] = (c16 * kBlk + ((4 * q + g) ^ sw)) * 16;  // MFMA B operand reads
+    // GELU output: hidden columns 32 wave + 16 q + 4 g .. +3 (chunk 4 wave + 2 q + g / 2)
+    hw[q] = (wave / 6) * kBlkBytes + (c16 * kBlk + 8 * (wl >> 1) + ((4 * (wl & 1) + 2 * q + (g >> 1)) ^ sw)) * 16 +
+            (g & 1) * 8;
     // residual: features 32 fr + 16 q + 4 g .. +3
-    rw[q] = (c16 * kCpr + 8 * (fr >> 1) + ((4 * (fr & 1) + 2 * q + (g >> 1)) ^ sw)) * 16 + (g & 1) * 8;
+    rw[q] = (fr / 6) * kBlkBytes + (c16 * kBlk + 8 * (fl >> 1) + ((4 * (fl & 1) + 2 * q + (g >> 1)) ^ sw)) * 16 +
+            (g & 1) * 8;
   }
 
   int t = blockIdx.x, prev = -1, par = 0;
@@ -285,7 +326,7 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
           uint4 xf[4];
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
-            xf[tt] = *reinterpret_cast<const uint4*>(xn + xa[ks & 1] + (ks >> 1) * 128 + tt * (16 * kCpr * 16));
+            xf[tt] = *reinterpret_cast<const uint4*>(xn + fa[ks & 1] + frag_off(4 * ks, tt));
 #pragma unroll
           for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -302,17 +343,38 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
       }
       // ---- bf16 -> GELU -> bf16 into the hidden chunk -------------------------
       // lane (c16, g) of (i, tt): hidden 16 i + 4 g + r of token 16 tt + c16.
+      // Table lookups for all values; if any lane holds a value outside the
+      // table (|x| < 2^-16 or >= 32: rare), the wave redoes the chunk exactly.
+      {
+        uint32_t hp[2][4][2], gp[2][4][2];
+        u16x2 dmax = {0, 0};
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          const uint32_t h01 = pack_bf16x2(acc1[i][tt][0], acc1[i][tt][1]);
-          const uint32_t h23 = pack_bf16x2(acc1[i][tt][2], acc1[i][tt][3]);
-          uint2 pk;
-          pk.x = gelu_bf16(h01 & 0xffffu, s_gelu) | (gelu_bf16(h01 >> 16, s_gelu) << 16);
-          pk.y = gelu_bf16(h23 & 0xffffu, s_gelu) | (gelu_bf16(h23 >> 16, s_gelu) << 16);
-          *reinterpret_cast<uint2*>(hb + hw[i] + tt * (16 * kHcpr * 16)) = pk;
+          for (int tt = 0; tt < 4; ++tt) {
+            hp[i][tt][0] = pack_bf16x2(acc1[i][tt][0], acc1[i][tt][1]);
+            hp[i][tt][1] = pack_bf16x2(acc1[i][tt][2], acc1[i][tt][3]);
+            // the packed pairs are the operands from here on (no per-half re-conversion)
+            asm volatile("" : "+v"(hp[i][tt][0]), "+v"(hp[i][tt][1]));
+            gp[i][tt][0] = gelu_pair_table(hp[i][tt][0], s_gelu, dmax);
+            gp[i][tt][1] = gelu_pair_table(hp[i][tt][1], s_gelu, dmax);
+          }
+        const uint32_t dm = dmax.x > dmax.y ? dmax.x : dmax.y;
+        if (__builtin_amdgcn_ballot_w64(dm >= (uint32_t)kGeluSpan) != 0) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+              for (int q = 0; q < 2; ++q)
+                gp[i][tt][q] = gelu_bf16(hp[i][tt][q] & 0xffffu, s_gelu) | (gelu_bf16(hp[i][tt][q] >> 16, s_gelu) << 16);
         }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            *reinterpret_cast<uint2*>(hb + hw[i] + tt * (16 * kBlk * 16)) = make_uint2(gp[i][tt][0], gp[i][tt][1]);
+      }
       lds_barrier();  // hidden chunk complete
       // ---- fc2 partial: features [32 fr, +32), hidden [kh*kKR, +kKR) of the chunk ----
       {
@@ -331,8 +393,8 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
           uint4 hf[4];
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
-            hf[tt] = *reinterpret_cast<const uint4*>(hb + ha[s & 1] + (kh * (kKR / 64) + (s >> 1)) * 128 +
-                                                     tt * (16 * kHcpr * 16));
+            hf[tt] = *reinterpret_cast<const uint4*>(hb + fa[s & 1] + kh * (kKR / 8 / kBlk) * kBlkBytes +
+                                                     frag_off(4 * s, tt));
 #pragma unroll
           for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -349,10 +411,10 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
     // lane (c16, g) of (i, tt): features 32 fr + 16 i + 4 g + r of token 16 tt + c16.
     // With the k-split, part kh finishes token tiles tt in [2 kh, 2 kh + 2)
     // and hands the other two to its partner through the idle hidden chunk
-    // (fp32, 16-byte chunks XOR-swizzled by c16 & 7 against bank conflicts).
+    // (fp32, 16-byte chunks XOR-swizzled by c16 against bank conflicts).
     if constexpr (kKS == 2) {
       float* red = reinterpret_cast<float*>(hb);  // [64][C] fp32
-      const int rc = ((8 * fr + g) ^ (c16 & 7));  // 16-byte chunk of 32 fr + 4 g (+ 16 i: chunk + 4 i)
+      const int rc = ((8 * fr + g) ^ c16);  // 16-byte chunk of 32 fr + 4 g (+ 16 i: chunk ^ 4 i)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -370,7 +432,7 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         if (kKS == 2 && (tt >> 1) != kh) continue;
-        uint8_t* addr = xr + rw[i] + tt * (16 * kCpr * 16);
+        uint8_t* addr = xr + rw[i] + tt * (16 * kBlk * 16);
         const uint2 xv = *reinterpret_cast<const uint2*>(addr);
         uint2 out;
         out.x = pack_bf16x2(bf16_bits_to_f32((uint16_t)(xv.x & 0xffffu)) + (float)(__bf16)acc2[i][tt][0],

@@ -146,6 +146,25 @@ def init_block_params(block: torch.nn.Module, layer_idx: int) -> None:
                 lin.bias.zero_()
 
 
+def mlp_for(cfg: SwinConfig, layer_idx: int):
+    """The SequentialMlp that follows block `layer_idx` of `cfg` (hidden
+    mlp_ratio * C, 4 when the config names none, as BasicLayer builds it in
+    models/reference_model/parallel_layers.py:46-70), weights trunc-normal(std=
+    0.02) from fixed seeds, biases zero, LayerNorm defaults, on the CPU."""
+    from .mlp import SequentialMlp
+
+    C = cfg.channels
+    mlp = SequentialMlp(C, (cfg.mlp_ratio or 4) * C)
+    base = SEED_BASE + 100 * layer_idx + 50
+    with torch.no_grad():
+        for k, lin in enumerate((mlp.fc1, mlp.fc2), start=1):
+            w = torch.empty_like(lin.weight, device="cpu")
+            torch.nn.init.trunc_normal_(w, std=0.02, generator=generator(base + k))
+            lin.weight.copy_(w)
+            lin.bias.zero_()
+    return mlp
+
+
 def block_for(cfg: SwinConfig, layer_idx: int, land: Optional[torch.Tensor] = None):
     """A SequentialSwinTransformer of `cfg` for layer `layer_idx` (shift on odd
     layers, as in the reference), with seeded weights, on the CPU."""

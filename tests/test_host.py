@@ -117,3 +117,14 @@ def test_window_mask_descriptor_of_block():
     blk0 = SequentialSwinTransformer(layer_idx=0, height=16, width=24, embedding_dim=64, window_size=8,
                                      num_heads=2)
     assert blk0.window_mask(blk0.geometry(1)) is None
+
+
+def test_mlp_workload_is_seeded_and_named_like_the_reference():
+    from terra_amd import workloads
+    cfg = workloads.CONFIGS["c3"]
+    a, b = workloads.mlp_for(cfg, 1), workloads.mlp_for(cfg, 1)
+    assert sorted(a.state_dict()) == ["fc1.bias", "fc1.weight", "fc2.bias", "fc2.weight", "norm2.bias",
+                                      "norm2.weight"]
+    assert a.fc1.weight.shape == (4 * cfg.channels, cfg.channels)
+    assert all(torch.equal(a.state_dict()[k], b.state_dict()[k]) for k in a.state_dict())
+    assert not torch.equal(a.fc1.weight, workloads.mlp_for(cfg, 0).fc1.weight)
