@@ -43,25 +43,30 @@ constexpr int kMlpThreads = 64 * kMlpWaves;
 constexpr int kHC = 32 * kMlpWaves;  // hidden features per chunk: 32 per wave
 
 // GELU of a bf16 input by table.  The fc1 output is rounded to bf16 before
-// the activation, so GELU sees one of 2^16 inputs; for 2^-16 <= |x| < 32 the
+// the activation, so GELU sees one of 2^16 inputs; for 2^-22 <= |x| < 32 the
 // bf16 result is read from a table that each workgroup fills at start with
 // the module's formula, 0.5 x (1 + erf(x / sqrt 2)) in fp32 rounded to bf16
 // (the value PyTorch's GPU kernel computes for a bf16 input).  Outside that
-// range the bf16 result has a closed form: 0.5 x for |x| < 2^-16 (the fp32
-// value is 0.5 x (1 + d) with |d| < 2^-16, and 0.5 x is a bf16 value, so it
+// range the bf16 result has a closed form: 0.5 x for |x| < 2^-22 (the fp32
+// value is 0.5 x (1 + d) with |d| < 2^-22, and 0.5 x is a bf16 value, so it
 // rounds to 0.5 x); x for x >= 32 (erf = 1 in fp32); -0 for x <= -32 (erf =
 // -1 in fp32); -inf gives NaN (-inf * 0) and NaN stays NaN.
-constexpr uint32_t kGeluLo = 0x3780;   // bf16 bits of 2^-16
+constexpr uint32_t kGeluLo = 0x3480;   // bf16 bits of 2^-22
 constexpr uint32_t kGeluHi = 0x4200;   // bf16 bits of 32
-constexpr int kGeluSpan = (int)(kGeluHi - kGeluLo);  // 2688 entries per sign
+constexpr int kGeluSpan = (int)(kGeluHi - kGeluLo);  // 3456 entries per sign
 constexpr int kGeluBytes = 2 * kGeluSpan * 2;
 
-// LDS: GELU table, gamma, beta, b2, raw rows (two tiles when double-
+// LDS: GELU table, b2, LayerNorm gamma and beta (C = 192; for C = 384 the
+// LayerNorm reads them from global memory), raw rows (two tiles when double-
 // buffered), LayerNorm tile, hidden chunk (reused for the fc2 k-split
 // reduction).  b1 is read from global memory as the fc1 accumulator init.
 template <int C>
+constexpr bool mlp_affine_in_lds() {
+  return C <= 192;
+}
+template <int C>
 constexpr int mlp_rows_offset() {
-  return kGeluBytes + 3 * C * 4;
+  return kGeluBytes + (mlp_affine_in_lds<C>() ? 3 : 1) * C * 4;
 }
 template <int C, bool kDB>
 constexpr int mlp_lds_bytes() {
@@ -72,10 +77,16 @@ __device__ __forceinline__ f32x4 load_f32x4_lds(const float* p) {
   return *reinterpret_cast<const f32x4*>(p);
 }
 
-// Packed weight fragment (row tile rt, k-step ks) of a [rows, kIn] weight.
+// Packed weight fragment (row tile rt, k-step ks) of a [rows, kIn] weight,
+// by buffer load: the wave-uniform 1 KB block offset in an SGPR, the lane's
+// 16-byte offset in a VGPR (no per-lane 64-bit address per fragment).
+// The low two bits of the k-step go to the instruction's immediate offset
+// (k-steps 4 apart share one SGPR offset).
 template <int kIn>
-__device__ __forceinline__ uint4 packed_frag(const uint16_t* w, int rt, int ks, int lane) {
-  return reinterpret_cast<const uint4*>(w)[(rt * (kIn / 32) + ks) * 64 + lane];
+__device__ __forceinline__ uint4 packed_frag(__amdgpu_buffer_rsrc_t w, int rt, int ks, int lane) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(w, (uint32_t)lane * 16u + (uint32_t)(ks & 3) * 1024u,
+                                                        (rt * (kIn / 32) + (ks & ~3)) * 1024, 0);
+  return __builtin_bit_cast(uint4, v);
 }
 
 // Tiles in LDS: 64 rows of 16-byte chunks, stored as column blocks of kBlk =
@@ -179,9 +190,17 @@ __device__ __forceinline__ void mlp_store(const MlpParams& p, int t, const uint8
 // LayerNorm of the 64 raw rows -> xn (bf16).  Eight lanes per token, two-pass
 // fp32 statistics over values held in registers; with layernorm == 0 the
 // identity (mean 0, rstd 1, gamma 1, beta 0).
-template <int C>
+template <int C, bool kAffineLds>
 __device__ __forceinline__ void mlp_layernorm(const MlpParams& p, const uint8_t* xr, uint8_t* xn, const float* s_gamma,
                                               const float* s_beta, int tid) {
+  // gamma and beta from LDS, or from global memory (then NULL means 1 / 0,
+  // and without LayerNorm both are the identity)
+  const float* gptr = kAffineLds ? s_gamma : (p.layernorm ? p.gamma : nullptr);
+  const float* bptr = kAffineLds ? s_beta : (p.layernorm ? p.beta : nullptr);
+  if constexpr (!kAffineLds) {
+    // read per tile (not hoisted into registers for the whole kernel)
+    asm volatile("" : "+s"(gptr), "+s"(bptr));
+  }
   constexpr int kCpr = C / 8, kCPL = kCpr / 8;
   const int sub = tid & 7;
   for (int t = tid >> 3; t < 64; t += kMlpThreads / 8) {  // uniform per wave
@@ -217,10 +236,20 @@ __device__ __forceinline__ void mlp_layernorm(const MlpParams& p, const uint8_t*
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
       const int c0 = (sub + 8 * k) * 8;
+      float gv[8], bv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 gq = gptr != nullptr ? *reinterpret_cast<const f32x4*>(gptr + c0 + 4 * h) : f32x4{1.f, 1.f, 1.f, 1.f};
+        const f32x4 bq = bptr != nullptr ? *reinterpret_cast<const f32x4*>(bptr + c0 + 4 * h) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          gv[4 * h + e] = gq[e];
+          bv[4 * h + e] = bq[e];
+        }
+      }
       float yv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        yv[e] = (v[k][e] - mean) * rstd * s_gamma[c0 + e] + s_beta[c0 + e];
+      for (int e = 0; e < 8; ++e) yv[e] = (v[k][e] - mean) * rstd * gv[e] + bv[e];
       const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
                                  pack_bf16x2(yv[6], yv[7]));
       *reinterpret_cast<uint4*>(xn + mlp_slot(t, sub + 8 * k) * 16) = o;
@@ -243,9 +272,9 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
   static_assert(kKS <= 2 && (kKS == 1 || 64 * C * 4 <= 64 * kHC * 2), "the fc2 reduction reuses the hidden chunk");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t* s_gelu = reinterpret_cast<uint16_t*>(smem);
-  float* s_gamma = reinterpret_cast<float*>(smem + kGeluBytes);
+  float* s_b2 = reinterpret_cast<float*>(smem + kGeluBytes);
+  float* s_gamma = s_b2 + C;  // C = 192 only
   float* s_beta = s_gamma + C;
-  float* s_b2 = s_beta + C;
   uint8_t* xbuf = smem + mlp_rows_offset<C>();            // raw rows: 1 or 2 tiles
   uint8_t* xn = xbuf + (kDB ? 2 : 1) * kTile;
   uint8_t* hb = xn + kTile;                               // hidden chunk [64][kHC] bf16
@@ -257,13 +286,17 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
   if ((int)blockIdx.x >= p.tiles) return;  // uniform
   for (int i = tid; i < C; i += kMlpThreads) {
     // Without LayerNorm the normalisation below is the identity (mean 0, rstd 1, gamma 1, beta 0).
-    s_gamma[i] = p.layernorm && p.gamma != nullptr ? p.gamma[i] : 1.f;
-    s_beta[i] = p.layernorm && p.beta != nullptr ? p.beta[i] : 0.f;
+    if constexpr (mlp_affine_in_lds<C>()) {
+      s_gamma[i] = p.layernorm && p.gamma != nullptr ? p.gamma[i] : 1.f;
+      s_beta[i] = p.layernorm && p.beta != nullptr ? p.beta[i] : 0.f;
+    }
     s_b2[i] = p.b2 != nullptr ? p.b2[i] : 0.f;
   }
   gelu_table_fill(s_gelu, tid);
 
-  const int fr = wave % kNF, kh = wave / kNF;  // fc2: features [32 fr, +32), k part kh
+  const int fr = wave % kNF, kh = wave / kNF;
+  const __amdgpu_buffer_rsrc_t w1r = buffer_rsrc(p.w1, (uint32_t)(H * C * 2));
+  const __amdgpu_buffer_rsrc_t w2r = buffer_rsrc(p.w2, (uint32_t)(H * C * 2));  // fc2: features [32 fr, +32), k part kh
   // Per-lane LDS byte offsets (see frag_off): every fragment address below
   // is one of two bases plus a constant.
   const int sw = (c16 >> 1) & 7;
@@ -290,7 +323,7 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
     if constexpr (kDB) {
       if (prev >= 0) mlp_store<kCpr>(p, prev, xbuf + (par ^ 1) * kTile, tid);  // the previous tile's rows
     }
-    mlp_layernorm<C>(p, xr, xn, s_gamma, s_beta, tid);
+    mlp_layernorm<C, mlp_affine_in_lds<C>()>(p, xr, xn, s_gamma, s_beta, tid);
     lds_barrier();  // xn complete; the previous tile's rows are read out of the other buffer
 
     f32x4 acc2[2][4];
@@ -316,12 +349,12 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
 #pragma unroll
         for (int s0 = 0; s0 < 2; ++s0)
 #pragma unroll
-          for (int i = 0; i < 2; ++i) wf[s0][i] = packed_frag<C>(p.w1, rt1 + i, s0, lane);
+          for (int i = 0; i < 2; ++i) wf[s0][i] = packed_frag<C>(w1r, rt1 + i, s0, lane);
 #pragma unroll
         for (int ks = 0; ks < kSteps1; ++ks) {
           if (ks + 2 < kSteps1) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) wf[(ks + 2) % 3][i] = packed_frag<C>(p.w1, rt1 + i, ks + 2, lane);
+            for (int i = 0; i < 2; ++i) wf[(ks + 2) % 3][i] = packed_frag<C>(w1r, rt1 + i, ks + 2, lane);
           }
           uint4 xf[4];
 #pragma unroll
@@ -344,7 +377,7 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
       // ---- bf16 -> GELU -> bf16 into the hidden chunk -------------------------
       // lane (c16, g) of (i, tt): hidden 16 i + 4 g + r of token 16 tt + c16.
       // Table lookups for all values; if any lane holds a value outside the
-      // table (|x| < 2^-16 or >= 32: rare), the wave redoes the chunk exactly.
+      // table (|x| < 2^-22 or >= 32: rare), the wave redoes the chunk exactly.
       {
         uint32_t hp[2][4][2], gp[2][4][2];
         u16x2 dmax = {0, 0};
@@ -383,12 +416,12 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
 #pragma unroll
         for (int s0 = 0; s0 < 2; ++s0)
 #pragma unroll
-          for (int i = 0; i < 2; ++i) wf[s0][i] = packed_frag<H>(p.w2, 2 * fr + i, ks0 + s0, lane);
+          for (int i = 0; i < 2; ++i) wf[s0][i] = packed_frag<H>(w2r, 2 * fr + i, ks0 + s0, lane);
 #pragma unroll
         for (int s = 0; s < kSteps2; ++s) {
           if (s + 2 < kSteps2) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) wf[(s + 2) % 3][i] = packed_frag<H>(p.w2, 2 * fr + i, ks0 + s + 2, lane);
+            for (int i = 0; i < 2; ++i) wf[(s + 2) % 3][i] = packed_frag<H>(w2r, 2 * fr + i, ks0 + s + 2, lane);
           }
           uint4 hf[4];
 #pragma unroll
