@@ -351,13 +351,23 @@ __device__ __forceinline__ void head_qkv(const BlockParams& p, const uint8_t* xn
   auto bias0 = [&](int pass) { return pass == 0 ? C + 32 * h : (pass == 1 ? 2 * C + 32 * h : 32 * h); };
   // xn row address of token tile tt, k-step ks (tile_slot swizzle): the XOR
   // only touches the low 3 bits, so even / odd k-steps share a base.
-  int xoff[2][4];
+  // For C > 192 the offsets are 32-bit LDS addresses, so that the k-step part
+  // folds into the instruction's immediate offset: at 12 k-steps per pass the
+  // per-k-step addresses were otherwise kept in (spilled) registers (c5
+  // 547 -> 456 us).  At C = 192 the generic form is faster (274 against 354 us).
+  constexpr bool kLds32 = C > 192;
+  uint32_t xoff[2][4];
 #pragma unroll
   for (int e = 0; e < 2; ++e)
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) xoff[e][tt] = ((16 * tt + c16) * cpr + ((4 * e + g) ^ sw)) * 16;
+    for (int tt = 0; tt < 4; ++tt)
+      xoff[e][tt] = (kLds32 ? lds_address(xn) : 0u) + ((16 * tt + c16) * cpr + ((4 * e + g) ^ sw)) * 16;
   auto xn_frag = [&](int tt, int ks) -> uint4 {
-    return *reinterpret_cast<const uint4*>(xn + xoff[ks & 1][tt] + (ks >> 1) * 128);
+    if constexpr (kLds32)
+      return __builtin_bit_cast(uint4, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+                                           (uintptr_t)(xoff[ks & 1][tt] + (ks >> 1) * 128)));
+    else
+      return *reinterpret_cast<const uint4*>(xn + xoff[ks & 1][tt] + (ks >> 1) * 128);
   };
   uint4 ring[kDepth][2];
 #pragma unroll
@@ -507,13 +517,19 @@ __device__ __forceinline__ void head_proj(const BlockParams& p, const uint8_t* o
     for (int tt = 0; tt < 4; ++tt) ya[ft][tt] = bp;
   }
   constexpr int kDepth = C <= 192 ? 4 : 2;  // weight ring depth (registers)
-  int ooff[2][4];
+  constexpr bool kLds32 = C > 192;  // as in head_qkv
+  uint32_t ooff[2][4];
 #pragma unroll
   for (int e = 0; e < 2; ++e)
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) ooff[e][tt] = ((16 * tt + c16) * cpr + ((4 * e + g) ^ sw)) * 16;
+    for (int tt = 0; tt < 4; ++tt)
+      ooff[e][tt] = (kLds32 ? lds_address(o_tile) : 0u) + ((16 * tt + c16) * cpr + ((4 * e + g) ^ sw)) * 16;
   auto o_frag = [&](int tt, int ks) -> uint4 {
-    return *reinterpret_cast<const uint4*>(o_tile + ooff[ks & 1][tt] + (ks >> 1) * 128);
+    if constexpr (kLds32)
+      return __builtin_bit_cast(uint4, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+                                           (uintptr_t)(ooff[ks & 1][tt] + (ks >> 1) * 128)));
+    else
+      return *reinterpret_cast<const uint4*>(o_tile + ooff[ks & 1][tt] + (ks >> 1) * 128);
   };
   uint4 fp[kDepth][2];  // [ring slot][ft]
 #pragma unroll
