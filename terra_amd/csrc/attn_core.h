@@ -493,71 +493,153 @@ __device__ __forceinline__ void tile_attention_wave(uint8_t* qs, const uint8_t* 
   }
 }
 
-// Scores, softmax and O^T = V^T P^T of one 16-query tile `it` of an 8x8
-// window against its 64 keys.  The additive terms (relative-position bias at
-// tab8[30*(it - jt) - r + 93], land keys, shift regions) are the accumulator
-// init of the S^T MFMA, in the units of the accumulator: the base-2 logit is
-// acc * logit_scale.  With a Q operand that already carries scale * log2(e),
-// logit_scale = 1 and the terms are x log2e; with raw q, logit_scale =
-// scale * log2(e) (> 0) and the terms are divided by scale.
-// land_term[jt][r]: mask term of land key 16jt + 4g + r, else 0; mask_term:
-// the shift-region term.  kf[jt]: K operand of key tile jt; vfrag(ct, js):
-// V^T operand (keys 32js + 16(e/4) + 4g + e%4).  Returns the unnormalised O^T
-// tiles and 1/rowsum.
-template <class VFrag>
-__device__ __forceinline__ void attend_qtile(f32x4 (&o)[2], float& inv, int it, const uint4 (&kf)[4],
-                                             const uint4& qf, const float* tab8, const WindowMaskState& m,
-                                             const f32x4 (&land_term)[4], uint64_t rid_pack, int rid_q,
-                                             float mask_term, float logit_scale, VFrag vfrag) {
-  f32x4 s[4];
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) s[jt][r] = tab8[30 * (it - jt) - r + 93];
-  if (m.use_shift) {
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rid_j = (int)((rid_pack >> (4 * (4 * jt + r))) & 15ull);
-        s[jt][r] += (rid_j != rid_q ? mask_term : 0.f) + land_term[jt][r];
-      }
-  } else if (m.land != 0ull) {
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) s[jt] += land_term[jt];
-  }
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-    s[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt]), __builtin_bit_cast(bf16x8, qf),
-                                                    s[jt], 0, 0, 0);
-  float mx = s[0][0];
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[jt][r]);
-  mx = xor_max(mx);
-  const float neg_mx = -mx * logit_scale;  // logit_scale > 0: the max commutes with the scaling
-  float sum = 0.f;
+// bf16 operand fragment of ones: 1^T P^T puts each query's sum over the keys
+// in every row of the tile, so the row sum runs on the matrix cores (two
+// MFMAs per query tile) instead of 16 adds and a cross-lane reduction.
+__device__ __forceinline__ bf16x8 ones_frag() {
+  const uint32_t w[4] = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// Land terms of an 8x8 window for lane group g: land_term[jt][r] = mask_term
+// if key 16jt + 4g + r is land, else 0 (a sign-extended bit ANDed with the
+// term's bits).
+__device__ __forceinline__ void land_terms(f32x4 (&land_term)[4], uint64_t land, int g, float mask_term) {
+  const uint64_t ll = land >> (4 * g);
+  const uint32_t half[2] = {(uint32_t)ll, (uint32_t)(ll >> 32)};
+  const uint32_t mb = __float_as_uint(mask_term);
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt][r], logit_scale, neg_mx));
-      s[jt][r] = e;
-      sum += e;
+      const int bit = 16 * (jt & 1) + r;
+      const uint32_t sel = (uint32_t)((int32_t)(half[jt >> 1] << (31 - bit)) >> 31);
+      land_term[jt][r] = __uint_as_float(sel & mb);
     }
-  inv = __builtin_amdgcn_rcpf(xor_sum(sum));
-  o[0] = o[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// Bias columns read by attend_qtiles are staged reversed: slot kTableRev - i
+// holds relative index i, so the four keys r = 0..3 of an accumulator lane
+// (index lane_base + 30 (it - jt) - r) sit at increasing addresses and load
+// straight into the accumulator registers in order.
+constexpr int kTableRev = kTableMax - 1;
+
+// This lane's pointer into a reversed column: element (it, jt, r) of an 8x8
+// window is at [30 (3 - it + jt) + r].
+__device__ __forceinline__ const float* lane_bias_rev(const float* tab_rev, int lane) {
+  const int g = lane >> 4, c16 = lane & 15;
+  const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;  // in [93, 134]
+  return tab_rev + (kTableRev - 90 - lane_base);  // offset in [3, 44]; largest slot 227
+}
+
+// Mask modes of attend_qtiles, chosen at compile time so that the query-tile
+// loop of a window holds no branch whose two sides the register allocator
+// would merge with copies: kMaskNone, kMaskLand (land keys only), kMaskShift
+// (shift regions, plus land keys when the window has any).
+constexpr int kMaskNone = 0, kMaskLand = 1, kMaskShift = 2;
+
+template <int V>
+struct MaskMode {
+  static constexpr int value = V;
+};
+
+// Scores, softmax and O^T = V^T P^T of NQ 16-query tiles it0, it0 + 1, ... of
+// an 8x8 window against its 64 keys.  The relative-position bias (tabr from
+// lane_bias_rev) is the accumulator init of the S^T MFMA; land keys and shift
+// regions are added to its result.  All terms are in the units of the
+// accumulator: the base-2 logit is acc * logit_scale.  With a Q operand that
+// already carries scale * log2(e), logit_scale = 1 and the terms are x log2e;
+// with raw q, logit_scale = scale * log2(e) (> 0) and the terms are divided by
+// scale.
+// land_term[jt][r]: mask term of land key 16jt + 4g + r, else 0 (read only
+// when the window has land keys); mask_term: the shift-region term.  kf[jt]:
+// K operand of key tile jt; vfrag(ct, js): V^T operand (keys 32js +
+// 16(e/4) + 4g + e%4); qf[q], rid_q[q]: Q operand and query region id of tile
+// it0 + q.  Returns per tile the unnormalised O^T tiles and 1 / (sum over keys
+// of the bf16 probabilities that enter P V), so that the normalised weights
+// sum to 1.
+template <int kMask, int NQ, class VFrag>
+__device__ __forceinline__ void attend_qtiles(f32x4 (&o)[NQ][2], float (&inv)[NQ], int it0, const uint4 (&kf)[4],
+                                              const uint4 (&qf)[NQ], const float* tabr, const WindowMaskState& m,
+                                              const f32x4 (&land_term)[4], uint64_t rid_pack, const int (&rid_q)[NQ],
+                                              float mask_term, float logit_scale, VFrag vfrag) {
+  // The NQ query tiles advance through each stage together, which gives the
+  // scheduler independent MFMA / VALU chains to interleave.
+  f32x4 s[NQ][4];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[q][jt][r] = tabr[30 * (3 - it0 - q + jt) + r];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+      s[q][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt]),
+                                                         __builtin_bit_cast(bf16x8, qf[q]), s[q][jt], 0, 0, 0);
+  // Mask terms after the MFMA, on its result.
+  if constexpr (kMask == kMaskShift) {  // boundary windows: region test per element, plus land keys
+    const bool land = m.land != 0ull;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rid_j = (int)((rid_pack >> (4 * (4 * jt + r))) & 15ull);
+          s[q][jt][r] += (rid_j != rid_q[q] ? mask_term : 0.f) + (land ? land_term[jt][r] : 0.f);
+        }
+  } else if constexpr (kMask == kMaskLand) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) s[q][jt] += land_term[jt];
+  }
+  float mx[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    mx[q] = s[q][0][0];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx[q] = fmaxf(mx[q], s[q][jt][r]);
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) mx[q] = xor_max(mx[q]);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const float neg_mx = -mx[q] * logit_scale;  // logit_scale > 0: the max commutes with the scaling
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        s[q][jt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[q][jt][r], logit_scale, neg_mx));
+  }
+  const bf16x8 ones = ones_frag();
+  f32x4 rs[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    o[q][0] = o[q][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    rs[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 #pragma unroll
   for (int js = 0; js < 2; ++js) {
-    uint32_t wds[4];
 #pragma unroll
-    for (int e = 0; e < 8; e += 2)
-      wds[e / 2] = pack_bf16x2(s[2 * js + (e >> 2)][e & 3], s[2 * js + (e >> 2)][(e & 3) + 1]);
-    const bf16x8 pf = __builtin_bit_cast(bf16x8, wds);
+    for (int q = 0; q < NQ; ++q) {
+      uint32_t wds[4];
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag(ct, js), pf, o[ct], 0, 0, 0);
+      for (int e = 0; e < 8; e += 2)
+        wds[e / 2] = pack_bf16x2(s[q][2 * js + (e >> 2)][e & 3], s[q][2 * js + (e >> 2)][(e & 3) + 1]);
+      const bf16x8 pf = __builtin_bit_cast(bf16x8, wds);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        o[q][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag(ct, js), pf, o[q][ct], 0, 0, 0);
+      rs[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, rs[q], 0, 0, 0);
+    }
   }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) inv[q] = __builtin_amdgcn_rcpf(rs[q][0]);
 }
 
 }  // namespace

@@ -314,11 +314,16 @@ __device__ __forceinline__ void residual_add4(uint8_t* addr, const f32x4& yv) {
 // Bias columns (x log2e) of all heads and the LayerNorm affine -> LDS.
 template <int kH, int kThreads>
 __device__ __forceinline__ void stage_tables(const BlockParams& p, float* tabs, float* s_gamma, float* s_beta,
-                                             int tid) {
+                                             int tid, float* s_bqkv = nullptr, float* s_bproj = nullptr) {
   constexpr int C = 32 * kH;
+  if (s_bqkv != nullptr) {  // linear biases (zeros when absent)
+    for (int c = tid; c < 3 * C; c += kThreads) s_bqkv[c] = p.b_qkv != nullptr ? p.b_qkv[c] : 0.f;
+    for (int c = tid; c < C; c += kThreads) s_bproj[c] = p.b_proj != nullptr ? p.b_proj[c] : 0.f;
+  }
   for (int e = tid; e < kH * kTableMax; e += kThreads) {
     const int h = e / kTableMax, i = e - h * kTableMax;
-    tabs[e] = (p.bias_table != nullptr && i < 225) ? p.bias_table[i * kH + h] * kLog2e : 0.f;
+    const int ri = kTableRev - i;  // reversed column (lane_bias_rev)
+    tabs[e] = (p.bias_table != nullptr && ri < 225) ? p.bias_table[ri * kH + h] * kLog2e : 0.f;
   }
   for (int c = tid; c < C; c += kThreads) {
     s_gamma[c] = p.gamma != nullptr ? p.gamma[c] : 1.f;
@@ -337,10 +342,13 @@ __device__ __forceinline__ void stage_tables(const BlockParams& p, float* tabs, 
 // other (32 accumulators live) as one stream of 3 * C/32 k-steps whose weight
 // fragments flow through a ring kDepth steps deep, so each load has kDepth - 1
 // steps of MFMA work to arrive; the compiler barrier at each step keeps the
-// scheduler from hoisting further loads (register pressure).
+// scheduler from hoisting further loads (register pressure).  `bqkv` is the
+// bias (NULL: none).  From LDS it costs no wait on the weight loads in flight;
+// from global memory the first MFMA of each pass waits for it, and with it
+// for every weight fragment already requested (vmcnt counts in order).
 template <int C, bool kPacked>
 __device__ __forceinline__ void head_qkv(const BlockParams& p, const uint8_t* xn, int h, int lane, uint4 (&kf4)[4],
-                                         uint4 (&vf)[2][2], uint4 (&qf)[4]) {
+                                         uint4 (&vf)[2][2], uint4 (&qf)[4], const float* bqkv) {
   constexpr int cpr = C / 8, kKS = C / 32;
   constexpr int kSteps = 3 * kKS;
   constexpr int kDepth = C <= 192 ? 3 : 2;  // weight ring depth (registers)
@@ -400,11 +408,11 @@ __device__ __forceinline__ void head_qkv(const BlockParams& p, const uint8_t* xn
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
         f32x4 b = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (p.b_qkv != nullptr) {
+        if (bqkv != nullptr) {
           if (pass != 1) {
-            b = load_f32x4(p.b_qkv + bias0(pass) + 16 * dt + 4 * g);
+            b = load_f32x4(bqkv + bias0(pass) + 16 * dt + 4 * g);
           } else {
-            const float bv = p.b_qkv[bias0(pass) + 16 * dt + c16];
+            const float bv = bqkv[bias0(pass) + 16 * dt + c16];
             b = f32x4{bv, bv, bv, bv};
           }
         }
@@ -459,16 +467,44 @@ __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitL
   constexpr int cpr = C / 8;
   const int g = lane >> 4, c16 = lane & 15;
   const WindowMaskState m = block_mask_state(p, cur);
-  const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;  // in [93, 134]
-  const float* tab8 = tab + (lane_base - 93);
-  const uint64_t land_lane = m.land >> (4 * g);
-  f32x4 land_term[4];
+  const float* tabr = lane_bias_rev(tab, lane);
+  auto vsrc = [&](int ct, int js) -> bf16x8 { return __builtin_bit_cast(bf16x8, vf[ct][js]); };
+  // The four query tiles under one mask mode (a wave-uniform choice per
+  // window, outside the loop).
+  auto run = [&](auto mode, const f32x4 (&land_term)[4], uint64_t rid_pack) {
+    constexpr int kMask = decltype(mode)::value;
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
+    for (int it0 = 0; it0 < 4; it0 += 2) {
+      __builtin_amdgcn_sched_barrier(0);  // two query tiles at a time (register pressure)
+      int rid_q[2] = {0, 0};
+      if constexpr (kMask == kMaskShift) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) land_term[jt][r] = ((land_lane >> (16 * jt + r)) & 1ull) ? p.a.mask_l2e : 0.f;
-  uint64_t rid_pack = 0;
+        for (int q = 0; q < 2; ++q)
+          rid_q[q] = 3 * region(cur.wr * 8 + 2 * (it0 + q) + (c16 >> 3), p.Hp, 8, p.shift_h) +
+                     region(cur.wc * 8 + (c16 & 7), p.Wp, 8, p.shift_w);
+      }
+      const uint4 qp[2] = {qf[it0], qf[it0 + 1]};
+      f32x4 o[2][2];
+      float inv[2];
+      attend_qtiles<kMask, 2>(o, inv, it0, kf4, qp, tabr, m, land_term, rid_pack, rid_q, p.a.mask_l2e, 1.0f, vsrc);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int i = 16 * (it0 + q) + c16;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const f32x4 v = o[q][ct] * inv[q];
+          const int cc = 32 * h + 16 * ct + 4 * g;
+          uint2 pk;
+          pk.x = pack_bf16x2(v[0], v[1]);
+          pk.y = pack_bf16x2(v[2], v[3]);
+          *reinterpret_cast<uint2*>(o_tile + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
+        }
+      }
+    }
+  };
+  f32x4 land_term[4];  // read by attend_qtiles only when the window has land keys
   if (m.use_shift) {
+    uint64_t rid_pack = 0;
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
@@ -476,27 +512,13 @@ __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitL
         rid_pack |= (uint64_t)(3 * region(cur.wr * 8 + 2 * jt + (g >> 1), p.Hp, 8, p.shift_h) +
                                region(cur.wc * 8 + 4 * (g & 1) + r, p.Wp, 8, p.shift_w))
                     << (4 * (4 * jt + r));
-  }
-  auto vsrc = [&](int ct, int js) -> bf16x8 { return __builtin_bit_cast(bf16x8, vf[ct][js]); };
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    __builtin_amdgcn_sched_barrier(0);  // one query tile at a time (register pressure)
-    const int rid_q = m.use_shift ? 3 * region(cur.wr * 8 + 2 * it + (c16 >> 3), p.Hp, 8, p.shift_h) +
-                                        region(cur.wc * 8 + (c16 & 7), p.Wp, 8, p.shift_w)
-                                  : 0;
-    f32x4 o[2];
-    float inv;
-    attend_qtile(o, inv, it, kf4, qf[it], tab8, m, land_term, rid_pack, rid_q, p.a.mask_l2e, 1.0f, vsrc);
-    const int i = 16 * it + c16;
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const f32x4 v = o[ct] * inv;
-      const int cc = 32 * h + 16 * ct + 4 * g;
-      uint2 pk;
-      pk.x = pack_bf16x2(v[0], v[1]);
-      pk.y = pack_bf16x2(v[2], v[3]);
-      *reinterpret_cast<uint2*>(o_tile + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
-    }
+    if (m.land != 0ull) land_terms(land_term, m.land, g, p.a.mask_l2e);
+    run(MaskMode<kMaskShift>{}, land_term, rid_pack);
+  } else if (m.land != 0ull) {
+    land_terms(land_term, m.land, g, p.a.mask_l2e);
+    run(MaskMode<kMaskLand>{}, land_term, 0ull);
+  } else {
+    run(MaskMode<kMaskNone>{}, land_term, 0ull);
   }
 }
 
@@ -504,7 +526,7 @@ __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitL
 // (Y^T = W_p O^T), rounded to bf16 and added to the raw rows in `xr`.
 template <int C, bool kPacked>
 __device__ __forceinline__ void head_proj(const BlockParams& p, const uint8_t* o_tile, uint8_t* xr, int h,
-                                          int lane) {
+                                          int lane, const float* bproj) {
   constexpr int cpr = C / 8, kKS = C / 32;
   const int g = lane >> 4, c16 = lane & 15;
   const int sw = (c16 >> 1) & 7;
@@ -512,7 +534,7 @@ __device__ __forceinline__ void head_proj(const BlockParams& p, const uint8_t* o
   f32x4 ya[2][4];
 #pragma unroll
   for (int ft = 0; ft < 2; ++ft) {
-    const f32x4 bp = p.b_proj != nullptr ? load_f32x4(p.b_proj + f0 + 16 * ft + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 bp = bproj != nullptr ? load_f32x4(bproj + f0 + 16 * ft + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) ya[ft][tt] = bp;
   }
@@ -634,14 +656,14 @@ void swin_block_kernel(const BlockParams p) {
       layernorm_window<cpr, nthreads>(p, cur, xr, xn, s_gamma, s_beta, tid_i);
       lds_barrier();     // also: the previous window's rows are read out of xr_next
       uint4 kf4[4], vf[2][2], qf[4];
-      head_qkv<C, kPacked>(p, xn, wave, lane_i, kf4, vf, qf);
+      head_qkv<C, kPacked>(p, xn, wave, lane_i, kf4, vf, qf, p.b_qkv);
       // Next window's rows stream in behind the q/k/v loads (the attention
       // phase issues no vector-memory loads of its own).
       if (next < p.units) fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane_i);
       lds_barrier();     // every wave has read xn; O overwrites it
       head_attention<C>(p, cur, tabs + wave * kTableMax, wave, lane_i, kf4, vf, qf, xn);
       lds_barrier();     // O complete
-      head_proj<C, kPacked>(p, xn, xr, wave, lane_i);
+      head_proj<C, kPacked>(p, xn, xr, wave, lane_i, p.b_proj);
     } else if (next < p.units) {
       lds_barrier();     // the previous window's rows are read out of xr_next
       fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane_i);
@@ -680,7 +702,7 @@ void swin_block_kernel(const BlockParams p) {
 
 template <int kH>
 constexpr int block_pp_lds_bytes() {
-  return 6 * 64 * 32 * kH * 2 + kH * kTableMax * 4 + 2 * 32 * kH * 4;
+  return 6 * 64 * 32 * kH * 2 + kH * kTableMax * 4 + 2 * 32 * kH * 4 + 4 * 32 * kH * 4;
 }
 
 template <int kH, bool kPacked>
@@ -694,6 +716,8 @@ __global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockPara
   float* tabs = reinterpret_cast<float*>(smem + 6 * tile);
   float* s_gamma = tabs + kH * kTableMax;
   float* s_beta = s_gamma + C;
+  float* s_bqkv = s_beta + C;    // [3C]
+  float* s_bproj = s_bqkv + 3 * C;  // [C]
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -704,7 +728,7 @@ __global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockPara
   uint8_t* xn = gbuf + 2 * tile;
 
   if ((int)blockIdx.x >= p.units) return;  // uniform across the workgroup
-  stage_tables<kH, 2 * kGroupThreads>(p, tabs, s_gamma, s_beta, tid);
+  stage_tables<kH, 2 * kGroupThreads>(p, tabs, s_gamma, s_beta, tid, s_bqkv, s_bproj);
 
   // Windows of group g: unit blockIdx.x + (2k + g) * gridDim.x, k < count[g].
   const int stride = 2 * (int)gridDim.x;
@@ -740,7 +764,7 @@ __global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockPara
           layernorm_window<cpr, kGroupThreads>(p, cur, xr, xn, s_gamma, s_beta, h * 64 + lane_i);
       } else if (ph == 1) {
         if (have) {
-          if (cur.computed) head_qkv<C, kPacked>(p, xn, h, lane_i, kf4, vf, qf);
+          if (cur.computed) head_qkv<C, kPacked>(p, xn, h, lane_i, kf4, vf, qf, s_bqkv);
           // The next window's rows, behind the q/k/v loads; the buffer's last
           // reader was phase A's store.
           if (k + 1 < n_mine)
@@ -751,7 +775,7 @@ __global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockPara
         if (have && cur.computed)
           head_attention<C>(p, cur, tabs + h * kTableMax, h, lane_i, kf4, vf, qf, xn);
       } else {
-        if (have && cur.computed) head_proj<C, kPacked>(p, xn, xr, h, lane_i);
+        if (have && cur.computed) head_proj<C, kPacked>(p, xn, xr, h, lane_i, s_bproj);
         // The next window's rows have landed before phase A reads them.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }

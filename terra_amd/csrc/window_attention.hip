@@ -156,7 +156,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
 // from memory into one of three LDS buffers by direct global->LDS loads,
 // issued two units ahead, so a workgroup never holds loads in registers and
 // always has two units in flight.  The additive terms are in raw-score units
-// (bias / scale), added as the accumulator init of S^T (attend_qtile).
+// (bias / scale), added as the accumulator init of S^T (attend_qtiles).
 
 constexpr int kRingBufs = 3;
 
@@ -197,8 +197,10 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
   // Bias column of this head in raw-score units; the head's four waves split it.
   float* tab = tables + head * kTableMax;
   const float tab_mul = kLog2e / p.scale_l2e;     // = 1 / scale
-  for (int e = lane + 64 * it; e < kTableMax; e += 256)
-    tab[e] = (p.bias_table != nullptr && e < p.table_size) ? p.bias_table[(int64_t)e * p.heads + h] * tab_mul : 0.f;
+  for (int e = lane + 64 * it; e < kTableMax; e += 256) {
+    const int ri = kTableRev - e;  // reversed column (lane_bias_rev)
+    tab[e] = (p.bias_table != nullptr && ri < p.table_size) ? p.bias_table[(int64_t)ri * p.heads + h] * tab_mul : 0.f;
+  }
   const float mask_term = p.mask_l2e / p.scale_l2e;  // mask_value / scale
 
   // This thread's part of a unit's loads: one 1 KB block of one tensor per
@@ -233,9 +235,7 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
   int w = w0;                                     // < windows: the grid is never larger than the work
   issue(w, 0);
   if (w + wstride < windows) issue(w + wstride, 1);
-  // Per lane: the bias of element (it, jt, r) sits at tab8[30*(it - jt) - r + 93].
-  const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;  // in [93, 134]
-  const float* tab8 = tab + (lane_base - 93);
+  const float* tabr = lane_bias_rev(tab, lane);  // bias of element (it, jt, r) at tabr[30 (3 - it + jt) + r]
   const int hc = head * 4;                        // first chunk of this head
   const int orow = tid / cpr, ochunk = tid - (tid / cpr) * cpr;  // this thread's O chunk
   for (int n = 0;; ++n) {
@@ -280,19 +280,12 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
         const uint32_t wd[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
         return __builtin_bit_cast(bf16x8, wd);
       };
-      f32x4 land_term[4];
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) land_term[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (m.land != 0ull) {                        // uniform: only windows with land keys
-        const uint64_t land_lane = m.land >> (4 * g);
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) land_term[jt][r] = ((land_lane >> (16 * jt + r)) & 1ull) ? mask_term : 0.f;
-      }
-      uint64_t rid_pack = 0;
-      int rid_q = 0;
-      if (m.use_shift) {
+      f32x4 o[1][2];
+      float inv[1];
+      const uint4 qp[1] = {qf};
+      f32x4 land_term[4];                          // read by attend_qtiles only for windows with land keys
+      if (m.use_shift) {                           // wave-uniform mask mode of the window
+        uint64_t rid_pack = 0;
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
@@ -300,19 +293,29 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
             rid_pack |= (uint64_t)(3 * region(m.wr * 8 + 2 * jt + (g >> 1), p.frame_h, 8, p.shift_h) +
                                    region(m.wc * 8 + 4 * (g & 1) + r, p.frame_w, 8, p.shift_w))
                         << (4 * (4 * jt + r));
-        rid_q = 3 * region(m.wr * 8 + 2 * it + (c16 >> 3), p.frame_h, 8, p.shift_h) +
-                region(m.wc * 8 + (c16 & 7), p.frame_w, 8, p.shift_w);
+        const int rid_q[1] = {3 * region(m.wr * 8 + 2 * it + (c16 >> 3), p.frame_h, 8, p.shift_h) +
+                              region(m.wc * 8 + (c16 & 7), p.frame_w, 8, p.shift_w)};
+        if (m.land != 0ull) land_terms(land_term, m.land, g, mask_term);
+        attend_qtiles<kMaskShift, 1>(o, inv, it, kf, qp, tabr, m, land_term, rid_pack, rid_q, mask_term,
+                                     p.scale_l2e, vfrag);
+      } else {
+        const int rid_q[1] = {0};
+        if (m.land != 0ull) {
+          land_terms(land_term, m.land, g, mask_term);
+          attend_qtiles<kMaskLand, 1>(o, inv, it, kf, qp, tabr, m, land_term, 0ull, rid_q, mask_term, p.scale_l2e,
+                                      vfrag);
+        } else {
+          attend_qtiles<kMaskNone, 1>(o, inv, it, kf, qp, tabr, m, land_term, 0ull, rid_q, mask_term, p.scale_l2e,
+                                      vfrag);
+        }
       }
-      f32x4 o[2];
-      float inv;
-      attend_qtile(o, inv, it, kf, qf, tab8, m, land_term, rid_pack, rid_q, mask_term, p.scale_l2e, vfrag);
       // O over this wave's own Q rows (read above, before any write).
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       const int i = 16 * it + c16;
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
-        const f32x4 v = o[ct] * inv;
+        const f32x4 v = o[0][ct] * inv[0];
         const int cc = head * D + 16 * ct + 4 * g;  // 4 channels, 8 bytes
         uint2 pk;
         pk.x = pack_bf16x2(v[0], v[1]);
