@@ -76,7 +76,8 @@ def measured_traffic():
 
 def run_kernels(cfg, blk, x, steps):
     """The step's kernels on the step's own tensors, `steps` times: the fused
-    block kernel, then the five-stage path's three HIP kernels, then the
+    block kernel, then the five-stage path's three HIP kernels, the plain
+    partition kernel, then the
     attention backward on the same q / k / v, then the fused MLP half on the
     block's output; then a device copy of 192 MiB (the counter calibration)."""
     import torch
@@ -96,6 +97,8 @@ def run_kernels(cfg, blk, x, steps):
             win = kernels.swin_partition_ln(grid, geom, blk.norm1.weight, blk.norm1.bias, blk.norm1.eps)
             o = blk.attn.core(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], mask=mask)
             kernels.swin_reverse(o, geom, residual=grid)
+        for _ in range(steps):
+            kernels.swin_partition(grid, geom)
         dqkv = torch.empty_like(qkv)
         dbias = torch.zeros_like(blk.attn.relative_position_bias_table, dtype=torch.float32)
         for _ in range(steps):
@@ -233,7 +236,9 @@ def main():
 
     def isolated_us(key, reps=5, per=20):
         """Median over `reps` loops of `per` back-to-back launches of one
-        five-stage kernel on the arguments of its last call in the step."""
+        kernel on the arguments of its last call in the step, between two
+        events (steady state of the kernel run repeatedly; any gap the host
+        leaves between launches counts, so this errs on the slow side)."""
         fn, a, kw = last_call[key]
         with torch.no_grad():
             for _ in range(per):
@@ -257,6 +262,11 @@ def main():
         ms_five = run(max(5, args.steps // 2), 10)
         blk.use_fused_block = True
         iso = {k: isolated_us(k) for k in ("partition", "window_attention", "reverse")}
+        # The plain gather (pad + roll + partition, no LayerNorm) on the same
+        # frame: the partition kernel of a block whose LayerNorm is not fused.
+        x_grid, geom_ = last_call["partition"][1][0], last_call["partition"][1][1]
+        last_call["partition_plain"] = (kernels.swin_partition, (x_grid, geom_), {})
+        iso["partition_plain"] = isolated_us("partition_plain")
         # The training-path backward of the same attention call (row f3): the
         # step's q / k / v, a synthetic output gradient, dq | dk | dv into one
         # [B_, N, 3C] buffer and the bias-table gradient.
@@ -352,9 +362,7 @@ def main():
             "hbm_frac": block_bytes / (t_blk * 1e-6) / 1e9 / HBM_PEAK_GBS,
         },
         # The unfused path, for comparison.  Its kernels are timed alone, back to
-        # back on the step's own arguments (median of 5 x 20 launches): inside
-        # the step the host's launch cadence, not the GPU, sets the gaps that
-        # event pairs around a single launch would include.
+        # back on the step's own arguments (median of 5 x 20 launches).
         "five_stage": {
             "ms_per_step": ms_five,
             "tokens_per_s": tokens / (ms_five * 1e-3),
@@ -364,6 +372,9 @@ def main():
                 "hbm_frac": core_bytes / (iso["window_attention"] * 1e-6) / 1e9 / HBM_PEAK_GBS,
                 "TFLOP_s": core_flops / (iso["window_attention"] * 1e-6) / 1e12,
             },
+            "partition": {"us": iso["partition_plain"],
+                          "GB_s": part_bytes / (iso["partition_plain"] * 1e-6) / 1e9,
+                          "hbm_frac": part_bytes / (iso["partition_plain"] * 1e-6) / 1e9 / HBM_PEAK_GBS},
             "layernorm_partition": {"us": iso["partition"],
                                     "GB_s": part_bytes / (iso["partition"] * 1e-6) / 1e9,
                                     "hbm_frac": part_bytes / (iso["partition"] * 1e-6) / 1e9 / HBM_PEAK_GBS},

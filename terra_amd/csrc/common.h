@@ -64,11 +64,22 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
 
-// Sum over the 8 aligned lanes l^1, l^2, l^4 (one LayerNorm token group).
+// DPP move of a float between lanes of a row (kCtrl: the DPP control word).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+
+// Sum over the 8 aligned lanes of one LayerNorm token group, in registers
+// (DPP) rather than through the LDS crossbar: partners l^1 and l^2 (quad
+// permutes [1,0,3,2] and [2,3,0,1]), then the other quad of the group (half-row
+// mirror, lane i <-> 7 - i).  Each step adds the same two values on both
+// partners, so all 8 lanes end with the same, order-independent result.  The
+// whole group must be active.
 __device__ __forceinline__ float group8_sum(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  return v + __shfl_xor(v, 4);
+  v += dpp_move<0xb1>(v);
+  v += dpp_move<0x4e>(v);
+  return v + dpp_move<0x141>(v);
 }
 
 // ---- streaming stores ------------------------------------------------------

@@ -471,24 +471,31 @@ __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitL
   auto vsrc = [&](int ct, int js) -> bf16x8 { return __builtin_bit_cast(bf16x8, vf[ct][js]); };
   // The four query tiles under one mask mode (a wave-uniform choice per
   // window, outside the loop).
+  // All four query tiles advance together: the most independent work to
+  // overlap the MFMA, exp and cross-lane latencies of a tile (measured faster
+  // than two at a time, although the register budget then spills one 16-byte
+  // value per window).
   auto run = [&](auto mode, const f32x4 (&land_term)[4], uint64_t rid_pack) {
     constexpr int kMask = decltype(mode)::value;
+    constexpr int kNQ = 4;
 #pragma unroll
-    for (int it0 = 0; it0 < 4; it0 += 2) {
-      __builtin_amdgcn_sched_barrier(0);  // two query tiles at a time (register pressure)
-      int rid_q[2] = {0, 0};
-      if constexpr (kMask == kMaskShift) {
+    for (int it0 = 0; it0 < 4; it0 += kNQ) {
+      __builtin_amdgcn_sched_barrier(0);  // kNQ query tiles at a time (register pressure)
+      int rid_q[kNQ];
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
-          rid_q[q] = 3 * region(cur.wr * 8 + 2 * (it0 + q) + (c16 >> 3), p.Hp, 8, p.shift_h) +
-                     region(cur.wc * 8 + (c16 & 7), p.Wp, 8, p.shift_w);
-      }
-      const uint4 qp[2] = {qf[it0], qf[it0 + 1]};
-      f32x4 o[2][2];
-      float inv[2];
-      attend_qtiles<kMask, 2>(o, inv, it0, kf4, qp, tabr, m, land_term, rid_pack, rid_q, p.a.mask_l2e, 1.0f, vsrc);
+      for (int q = 0; q < kNQ; ++q)
+        rid_q[q] = kMask == kMaskShift ? 3 * region(cur.wr * 8 + 2 * (it0 + q) + (c16 >> 3), p.Hp, 8, p.shift_h) +
+                                             region(cur.wc * 8 + (c16 & 7), p.Wp, 8, p.shift_w)
+                                       : 0;
+      uint4 qp[kNQ];
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
+      for (int q = 0; q < kNQ; ++q) qp[q] = qf[it0 + q];
+      f32x4 o[kNQ][2];
+      float inv[kNQ];
+      attend_qtiles<kMask, kNQ>(o, inv, it0, kf4, qp, tabr, m, land_term, rid_pack, rid_q, p.a.mask_l2e, 1.0f,
+                                vsrc);
+#pragma unroll
+      for (int q = 0; q < kNQ; ++q) {
         const int i = 16 * (it0 + q) + c16;
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
