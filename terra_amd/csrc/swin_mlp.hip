@@ -356,6 +356,10 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
 #pragma unroll
             for (int i = 0; i < 2; ++i) wf[(ks + 2) % 3][i] = packed_frag<C>(w1r, rt1 + i, ks + 2, lane);
           }
+          // Compiler barrier: without it the scheduler sinks each weight load
+          // to just before its MFMA (least register pressure), which exposes
+          // the whole L2 latency of every fragment.
+          asm volatile("" ::: "memory");
           uint4 xf[4];
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
@@ -423,6 +427,7 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
 #pragma unroll
             for (int i = 0; i < 2; ++i) wf[(s + 2) % 3][i] = packed_frag<H>(w2r, 2 * fr + i, ks0 + s + 2, lane);
           }
+          asm volatile("" ::: "memory");  // keeps the weight loads two steps ahead (see fc1)
           uint4 hf[4];
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
