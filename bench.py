@@ -19,7 +19,13 @@ the training path's attention-core backward on the step's q / k / v;
 `mlp_half` the block's MLP half (SequentialMlp) as one kernel against the same
 module through torch's ops, and `full_block` both halves together.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--config c1..c5]
+
+The other configurations (default c3) run the same measurement: c5 through
+the 12-head fused kernel; c1, c2 and c4 (fp32, 7x7 windows, head dim 64)
+through the five-stage path, whose roofline is then the attention core's
+(HBM-bound), with the MLP half through torch's ops where no fused MLP kernel
+serves the shape.
     python bench.py --mode kernels --steps 3     # the step's kernels only,
                                                  # plus a 192 MiB device copy
                                                  # (rocprofv3 counter calibration)
@@ -48,7 +54,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="c3")
+    ap.add_argument("--config", default="c3", choices=("c1", "c2", "c3", "c4", "c5"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--mode", choices=("step", "kernels"), default="step",
@@ -141,7 +147,7 @@ def cpu_baseline(cfg, blk, land, budget_s: float):
     threads = torch.get_num_threads()
     params = {k: v.detach().float().cpu() for k, v in blk.state_dict().items() if k != "attn_mask"}
     # sample: the first `rows` token rows (whole window rows); the shift wraps within the band
-    rows = 64
+    rows = min(cfg.height, max(cfg.window, (64 // cfg.window) * cfg.window))
     x = workloads.activations((1, rows * cfg.width, cfg.channels), 1000, torch.float32)
     land_s = land[:rows]
     times = []
@@ -256,11 +262,17 @@ def main():
 
     try:
         ms = run(args.steps, args.warmup)
-        if not events["swin_block"]:
+        # The fused kernel serves bf16, 8x8 windows, head dim 32 (c3, c5); the
+        # other configurations run the five-stage path as the step itself.
+        fused = bool(events["swin_block"])
+        if args.config == "c3" and not fused:
             raise RuntimeError("the fused block kernel did not serve the benchmark step")
-        blk.use_fused_block = False  # the five-stage path, for comparison
-        ms_five = run(max(5, args.steps // 2), 10)
-        blk.use_fused_block = True
+        if fused:
+            blk.use_fused_block = False  # the five-stage path, for comparison
+            ms_five = run(max(5, args.steps // 2), 10)
+            blk.use_fused_block = True
+        else:
+            ms_five = ms
         iso = {k: isolated_us(k) for k in ("partition", "window_attention", "reverse")}
         # The plain gather (pad + roll + partition, no LayerNorm) on the same
         # frame: the partition kernel of a block whose LayerNorm is not fused.
@@ -288,11 +300,12 @@ def main():
         mlp = workloads.mlp_for(cfg, 1).to(dev).to(dtype)
         with torch.no_grad():
             y_blk = blk(x)
-            if not mlp._fusable(y_blk):
+            mlp_fused = mlp._fusable(y_blk)
+            if args.config == "c3" and not mlp_fused:
                 raise RuntimeError("the fused MLP kernel does not serve this configuration")
-            mlp_args = mlp._fused_args()
-        last_call["mlp"] = (kernels.swin_mlp, (y_blk,), dict(out=torch.empty_like(y_blk), **mlp_args))
-        iso["mlp"] = isolated_us("mlp")
+        if mlp_fused:  # bf16 with C = 192 or 384; other shapes run torch's sequence only
+            last_call["mlp"] = (kernels.swin_mlp, (y_blk,), dict(out=torch.empty_like(y_blk), **mlp._fused_args()))
+            iso["mlp"] = isolated_us("mlp")
         mlp.use_fused_mlp = False
         last_call["mlp_torch"] = (mlp, (y_blk,), {})
         iso["mlp_torch"] = isolated_us("mlp_torch")
@@ -321,9 +334,42 @@ def main():
     def avg_us(name):
         return 1e3 * statistics.mean(a.elapsed_time(b) for a, b in events[name])
 
-    t_blk = avg_us("swin_block")
     tokens = cfg.real_tokens
-    blk_tflops = block_flops / (t_blk * 1e-6) / 1e12
+    if fused:
+        t_blk = avg_us("swin_block")
+        blk_tflops = block_flops / (t_blk * 1e-6) / 1e12
+        roofline = {
+            "kernel": (f"swin_block_{'pp_' if cfg.heads == 6 else ''}kernel<{cfg.heads}> (fused LN + qkv + window "
+                       "attention + proj + residual, gather/scatter)"),
+            "bound": "mfma",
+            "achieved": blk_tflops,
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": blk_tflops / MFMA_BF16_PEAK_TFLOPS,
+            "traffic": measured_traffic() if args.config == "c3" else None,
+            "algorithmic_flops_per_launch": block_flops,
+            "algorithmic_bytes_per_launch": block_bytes,
+            "avg_launch_us": t_blk,
+            "hbm_GB_s": block_bytes / (t_blk * 1e-6) / 1e9,
+            "hbm_frac": block_bytes / (t_blk * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        }
+    else:
+        # The step is the five-stage path; its dominant HIP kernel is the
+        # window attention core, HBM-bound (N / elt flop per byte).
+        t_att = iso["window_attention"]
+        roofline = {
+            "kernel": "window attention core (five-stage path)",
+            "bound": "hbm",
+            "achieved": core_bytes / (t_att * 1e-6) / 1e9,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": core_bytes / (t_att * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": core_bytes,
+            "algorithmic_flops_per_launch": core_flops,
+            "avg_launch_us": t_att,
+            "TFLOP_s": core_flops / (t_att * 1e-6) / 1e12,
+        }
     res = {
         "metric": METRIC,
         "value": tokens / (ms * 1e-3),
@@ -338,29 +384,18 @@ def main():
         "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
         "data": "synthetic (seeded N(0,1) activations, trunc-normal(0.02) weights, seeded smoothed-noise land mask)",
         "config": {
-            "workload": (f"{cfg.name}: SW-MSA attention half of a Swin block (LayerNorm, roll+partition, q/k/v, "
-                         f"window attention with relative-position bias + shift/land mask, proj, reverse+roll, "
-                         f"residual) as one fused kernel, B={cfg.batch}, {cfg.height}x{cfg.width} tokens, C={C}, "
+            "workload": (f"{cfg.name}: {'SW' if cfg.shift else 'W'}-MSA attention half of a Swin block (LayerNorm, "
+                         f"roll+partition, q/k/v, window attention with relative-position bias"
+                         f"{' + shift' if cfg.shift else ''}{'/land' if cfg.land else ''} mask, proj, reverse+roll, "
+                         f"residual) {'as one fused kernel' if fused else 'through the five-stage path'}, "
+                         f"B={cfg.batch}, {cfg.height}x{cfg.width} tokens, C={C}, "
                          f"{cfg.heads} heads, window {cfg.window}, shift {cfg.shift}"
                          + (", ~30% land mask" if cfg.land else "")),
             "windows": B_,
             "tokens": tokens,
             "parallelism": "single GPU",
         },
-        "roofline": {
-            "kernel": "swin_block_pp_kernel<6> (fused LN + qkv + window attention + proj + residual, gather/scatter)",
-            "bound": "mfma",
-            "achieved": blk_tflops,
-            "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": blk_tflops / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": measured_traffic(),
-            "algorithmic_flops_per_launch": block_flops,
-            "algorithmic_bytes_per_launch": block_bytes,
-            "avg_launch_us": t_blk,
-            "hbm_GB_s": block_bytes / (t_blk * 1e-6) / 1e9,
-            "hbm_frac": block_bytes / (t_blk * 1e-6) / 1e9 / HBM_PEAK_GBS,
-        },
+        "roofline": roofline,
         # The unfused path, for comparison.  Its kernels are timed alone, back to
         # back on the step's own arguments (median of 5 x 20 launches).
         "five_stage": {
@@ -396,19 +431,38 @@ def main():
             "algorithmic_flops_per_launch": bwd_flops,
         },
     }
-    res["mlp_half"] = {
-        "kernel": "swin_mlp_kernel<192, true> (LayerNorm + fc1 + exact GELU + fc2 + residual, hidden layer on chip)",
-        "us": iso["mlp"],
-        "TFLOP_s": mlp_flops / (iso["mlp"] * 1e-6) / 1e12,
-        "mfma_frac": mlp_flops / (iso["mlp"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-        "GB_s": mlp_bytes / (iso["mlp"] * 1e-6) / 1e9,
-        "torch_us": iso["mlp_torch"],
-        "speedup_vs_torch": iso["mlp_torch"] / iso["mlp"],
-        "algorithmic_flops_per_launch": mlp_flops,
-        "algorithmic_bytes_per_launch": mlp_bytes,
+    # The targets the hot path is held to, with this run's figures: the
+    # attention core (HBM-bound) >= 70 % of HBM, partition and reverse >= 80 %,
+    # and the fused kernel's fraction of the dense bf16 MFMA peak.
+    fs = res["five_stage"]
+    res["targets"] = {
+        "attention_core_hbm_frac": {"value": fs["window_attention"]["hbm_frac"], "target": 0.70},
+        "partition_hbm_frac": {"value": fs["partition"]["hbm_frac"], "target": 0.80},
+        "reverse_hbm_frac": {"value": fs["reverse_residual"]["hbm_frac"], "target": 0.80},
     }
-    # The whole Swin block (attention half + MLP half), both fused.
-    res["full_block"] = {"us": t_blk + iso["mlp"], "tokens_per_s": tokens / ((t_blk + iso["mlp"]) * 1e-6)}
+    if fused:
+        res["targets"]["fused_block_mfma_frac"] = {"value": res["roofline"]["frac"], "target": 0.50}
+    t_attn_half = t_blk if fused else ms * 1e3
+    if mlp_fused:
+        res["mlp_half"] = {
+            "kernel": (f"swin_mlp_kernel<{C}, {'true' if C <= 192 else 'false'}> (LayerNorm + fc1 + exact GELU + fc2 "
+                       "+ residual, hidden layer on chip)"),
+            "us": iso["mlp"],
+            "TFLOP_s": mlp_flops / (iso["mlp"] * 1e-6) / 1e12,
+            "mfma_frac": mlp_flops / (iso["mlp"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "GB_s": mlp_bytes / (iso["mlp"] * 1e-6) / 1e9,
+            "torch_us": iso["mlp_torch"],
+            "speedup_vs_torch": iso["mlp_torch"] / iso["mlp"],
+            "algorithmic_flops_per_launch": mlp_flops,
+            "algorithmic_bytes_per_launch": mlp_bytes,
+        }
+        t_mlp = iso["mlp"]
+    else:
+        res["mlp_half"] = {"kernel": None, "torch_us": iso["mlp_torch"],
+                           "note": "no fused MLP kernel for this shape: torch's op sequence timed"}
+        t_mlp = iso["mlp_torch"]
+    # The whole Swin block (attention half + MLP half).
+    res["full_block"] = {"us": t_attn_half + t_mlp, "tokens_per_s": tokens / ((t_attn_half + t_mlp) * 1e-6)}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg, blk, land if land is not None else
                                            torch.zeros(cfg.height, cfg.width, dtype=torch.bool), args.cpu_seconds)
