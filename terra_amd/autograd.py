@@ -10,9 +10,8 @@ models/transformer.py:142-300).
   partition (pad window tokens get zero), both on the same geometry.
 - The attention core's backward is ``terra_swin_attn_bwd`` (P recomputed
   from q and k; dq, dk, dv, and the bias-table gradient summed over
-  windows): an MFMA tile kernel for bf16 8x8 windows without padded keys,
-  a plain fp32 kernel for every other shape the forward serves (fp32, 7x7
-  windows, padded keys).  For a shape neither serves the forward still runs
+  windows): an MFMA tile kernel for every bf16 window (8x8, 7x7, padded
+  keys), a plain fp32 kernel for fp32 activations.  For a shape neither serves the forward still runs
   and backward() raises NotImplementedError (there is no non-HIP backward).
 
 Each function runs the plain kernel when no input needs a gradient.

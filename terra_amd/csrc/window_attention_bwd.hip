@@ -1,4 +1,5 @@
-// Backward of the window-attention core (bf16, 8x8 windows, head dim 32/64).
+// Backward of the window-attention core (bf16, windows up to 8x8 in rows of
+// up to 64 tokens, head dim 32/64).
 //
 // Per window w and head h, with z = (q k^T) * scale + bias + M the natural
 // logits and P = softmax(z) (recomputed here from q, k and the masks, the
@@ -23,6 +24,12 @@
 // dQ, dK and dV are staged in the V, K and dout tiles once those are dead and
 // leave as whole 128-byte row slices (8-byte accumulator stores straight to
 // memory made the kernel twice as slow).
+//
+// Windows other than 8x8 in 64-token rows (7x7: 49 tokens) run the same
+// tiles with rows N..63 zero-filled: their keys take -inf (P = 0, dz = 0),
+// their dout rows are zero (dz = 0 for those query rows), and they are never
+// stored.  Keys >= n_real take the pad value in the softmax and get no
+// gradient (the forward's masked_fill).
 #include "common.h"
 #include "attn_core.h"
 
@@ -67,13 +74,19 @@ __device__ __forceinline__ uint2 pack4_bf16(const f32x4& v) {
   return r;
 }
 
-template <int D, int G, bool kExplicit>
+// LDS row pitch of the q / k / v / dout tiles in 16-byte chunks: the
+// tile_slot swizzle permutes chunks within aligned groups of 8, so rows
+// narrower than 8 chunks (one head of dim 32) are padded to 8.
+constexpr int bwd_tile_cpr(int G, int D) { return G * D / 8 < 8 ? 8 : G * D / 8; }
+
+template <int D, int G, bool kExplicit, bool kWs8>
 __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParams bp) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const AttnParams& p = bp.a;
   constexpr int nthreads = G * 128;
   constexpr int cpr = G * D / 8;                 // chunks per row of the head group
-  constexpr int tile_bytes = kNPad * cpr * 16;
+  constexpr int lcpr = bwd_tile_cpr(G, D);       // LDS row pitch in chunks
+  constexpr int tile_bytes = kNPad * lcpr * 16;
   constexpr int kKF = D / 32;
   uint8_t* qs = smem;
   uint8_t* ks = smem + tile_bytes;
@@ -111,6 +124,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
   constexpr int kRowStep = nthreads / cpr;
   static_assert(kRowStep * cpr == nthreads && kRowStep * kPer == kNPad, "row tiling");
   const int row0 = tid / cpr, chunk0 = tid % cpr;
+  const int n_rows = kWs8 ? kNPad : p.N;         // token rows per window in memory
 
   f32x4 gz[2][4];  // this lane's bias-gradient share: dz summed over the windows
 #pragma unroll
@@ -118,10 +132,11 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) gz[il][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // q, k, v, dout rows of one unit's head group -> registers (nontemporal).
+  // q, k, v, dout rows of one unit's head group -> registers (nontemporal);
+  // rows >= n_rows are zeros.
   uint4 buf[4][kPer];
   auto fetch = [&](int unit) {
-    const int64_t row_base = (int64_t)(unit / p.groups) * kNPad + row0;
+    const int64_t row_base = (int64_t)(unit / p.groups) * n_rows + row0;
     const int col = hg * G * D + chunk0 * 8;
     const uint16_t* src[4] = {reinterpret_cast<const uint16_t*>(p.q) + row_base * p.q_stride + col,
                               reinterpret_cast<const uint16_t*>(p.k) + row_base * p.k_stride + col,
@@ -133,8 +148,10 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int u = 0; u < kPer; ++u)
-        buf[t][u] = __builtin_bit_cast(
-            uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[t] + u * step[t])));
+        buf[t][u] = (kWs8 || row0 + kRowStep * u < n_rows)
+                        ? __builtin_bit_cast(uint4, __builtin_nontemporal_load(
+                                                        reinterpret_cast<const u32x4*>(src[t] + u * step[t])))
+                        : uint4{0u, 0u, 0u, 0u};
   };
 
   // Persistent loop, software-pipelined: the loads of unit n + gridDim.x are
@@ -151,7 +168,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int u = 0; u < kPer; ++u)
-          *reinterpret_cast<uint4*>(dst[t] + tile_slot(row0 + kRowStep * u, chunk0, cpr) * 16) = buf[t][u];
+          *reinterpret_cast<uint4*>(dst[t] + tile_slot(row0 + kRowStep * u, chunk0, lcpr) * 16) = buf[t][u];
       lds_barrier();
     }
 
@@ -159,8 +176,8 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
     const WindowMaskState m = window_mask_state(p, w, true);
     const float* emask = nullptr;
     if constexpr (kExplicit) emask = p.explicit_mask + (int64_t)(w % p.mask_windows) * p.n_geo * p.n_geo;
-    LaneGeom<true> lg;
-    lane_geom_init<true>(lg, p, m, tab, lane);
+    LaneGeom<kWs8> lg;
+    lane_geom_init<kWs8>(lg, p, m, tab, lane);
     const int hc = head * (D / 8);  // first chunk of this head in the tiles
     f32x4 s[2][4];
     float inv[2];
@@ -170,16 +187,16 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int c = 0; c < kKF; ++c)
-          kf[t][c] = *reinterpret_cast<const uint4*>(ks + tile_slot(16 * t + c16, hc + 4 * c + g, cpr) * 16);
+          kf[t][c] = *reinterpret_cast<const uint4*>(ks + tile_slot(16 * t + c16, hc + 4 * c + g, lcpr) * 16);
 #pragma unroll
       for (int il = 0; il < 2; ++il)
 #pragma unroll
         for (int c = 0; c < kKF; ++c)
           qp[il][c] = *reinterpret_cast<const uint4*>(
-              qs + tile_slot(16 * (2 * half + il) + c16, hc + 4 * c + g, cpr) * 16);
+              qs + tile_slot(16 * (2 * half + il) + c16, hc + 4 * c + g, lcpr) * 16);
       scores_pair<true, D>(s, kf, qp);
     }
-    softmax_half<true, kExplicit>(s, inv, half, p, m, lg, emask, lane);
+    softmax_half<kWs8, kExplicit>(s, inv, half, p, m, lg, emask, lane);
     f32x4 dp[2][4];
     {
       uint4 vf[4][kKF], df[2][kKF];
@@ -187,13 +204,13 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int c = 0; c < kKF; ++c)
-          vf[t][c] = *reinterpret_cast<const uint4*>(vs + tile_slot(16 * t + c16, hc + 4 * c + g, cpr) * 16);
+          vf[t][c] = *reinterpret_cast<const uint4*>(vs + tile_slot(16 * t + c16, hc + 4 * c + g, lcpr) * 16);
 #pragma unroll
       for (int il = 0; il < 2; ++il)
 #pragma unroll
         for (int c = 0; c < kKF; ++c)
           df[il][c] = *reinterpret_cast<const uint4*>(
-              dos + tile_slot(16 * (2 * half + il) + c16, hc + 4 * c + g, cpr) * 16);
+              dos + tile_slot(16 * (2 * half + il) + c16, hc + 4 * c + g, lcpr) * 16);
       scores_pair<true, D>(dp, vf, df);  // dP^T: keys 16jt + 4g + r, query c16
     }
     // P = e * (1 / rowsum); dz = P * (dP - sum_j P dP).  P is rounded to bf16
@@ -211,7 +228,11 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       const int i = 16 * (2 * half + il) + c16;
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
-        const f32x4 z = s[il][jt] * (dp[il][jt] - dsum);
+        f32x4 z = s[il][jt] * (dp[il][jt] - dsum);
+        if constexpr (!kWs8) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) z[r] = 16 * jt + 4 * g + r < p.n_real ? z[r] : 0.f;
+        }
         gz[il][jt] += z;
         // [query][key] tiles: this lane's keys 16jt + 4g .. + 3 are 8 bytes.
         const int off = tile_slot(i, 2 * jt + (g >> 1), 8) * 16 + (g & 1) * 8;
@@ -223,7 +244,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
     // dQ^T = K^T dz^T (dz accumulators as the P^T operand), times scale.
     f32x4 dqa[D / 16][2];
     {
-      auto kfrag = [&](int ct, int js) -> bf16x8 { return rows_frag(ks, cpr, head * D + 16 * ct, js, lane); };
+      auto kfrag = [&](int ct, int js) -> bf16x8 { return rows_frag(ks, lcpr, head * D + 16 * ct, js, lane); };
       pv_half<true, D>(dqa, dp, lane, kfrag);
     }
     lds_barrier();  // P and dz tiles of both halves are in LDS; K and V are no longer read
@@ -234,7 +255,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
 #pragma unroll
       for (int ct = 0; ct < D / 16; ++ct) {
         const int cc = head * D + 16 * ct + 4 * g;
-        *reinterpret_cast<uint2*>(vs + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) =
+        *reinterpret_cast<uint2*>(vs + tile_slot(i, cc >> 3, lcpr) * 16 + (cc & 7) * 2) =
             pack4_bf16(dqa[ct][il] * bp.scale);
       }
     }
@@ -258,8 +279,8 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
         }
 #pragma unroll
         for (int ct = 0; ct < D / 16; ++ct) {
-          const bf16x8 dof = rows_frag(dos, cpr, head * D + 16 * ct, js, lane);
-          const bf16x8 qf = rows_frag(qs, cpr, head * D + 16 * ct, js, lane);
+          const bf16x8 dof = rows_frag(dos, lcpr, head * D + 16 * ct, js, lane);
+          const bf16x8 qf = rows_frag(qs, lcpr, head * D + 16 * ct, js, lane);
 #pragma unroll
           for (int jt = 0; jt < 2; ++jt) {
             av[ct][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dof, pf[jt], av[ct][jt], 0, 0, 0);
@@ -276,7 +297,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
 #pragma unroll
         for (int ct = 0; ct < D / 16; ++ct) {
           const int cc = head * D + 16 * ct + 4 * g;
-          *reinterpret_cast<uint2*>(ks + tile_slot(j, cc >> 3, cpr) * 16 + (cc & 7) * 2) =
+          *reinterpret_cast<uint2*>(ks + tile_slot(j, cc >> 3, lcpr) * 16 + (cc & 7) * 2) =
               pack4_bf16(ak[ct][jt] * bp.scale);
         }
       }
@@ -287,7 +308,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
 #pragma unroll
         for (int ct = 0; ct < D / 16; ++ct) {
           const int cc = head * D + 16 * ct + 4 * g;
-          *reinterpret_cast<uint2*>(dos + tile_slot(j, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pack4_bf16(av[ct][jt]);
+          *reinterpret_cast<uint2*>(dos + tile_slot(j, cc >> 3, lcpr) * 16 + (cc & 7) * 2) = pack4_bf16(av[ct][jt]);
         }
       }
     }
@@ -300,13 +321,14 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       const int64_t stride[3] = {bp.dq_stride, bp.dk_stride, bp.dv_stride};
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
-        const uint16_t* base = reinterpret_cast<const uint16_t*>(dst[t]) + (int64_t)w * kNPad * stride[t];
+        const uint16_t* base = reinterpret_cast<const uint16_t*>(dst[t]) + (int64_t)w * n_rows * stride[t];
         const __amdgpu_buffer_rsrc_t out =
-            buffer_rsrc(base, (uint32_t)(((int64_t)(kNPad - 1) * stride[t] + p.heads * D) * 2));
+            buffer_rsrc(base, (uint32_t)(((int64_t)(n_rows - 1) * stride[t] + p.heads * D) * 2));
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
           const int row = row0 + kRowStep * u;
-          const uint4 val = *reinterpret_cast<const uint4*>(src[t] + tile_slot(row, chunk0, cpr) * 16);
+          if (!kWs8 && row >= n_rows) continue;
+          const uint4 val = *reinterpret_cast<const uint4*>(src[t] + tile_slot(row, chunk0, lcpr) * 16);
           stream_store_sc1(val, out, (uint32_t)(row * stride[t] + col) * 2);
         }
       }
@@ -317,17 +339,35 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
 
   // ---- bias gradient: registers -> LDS column -> global table ----------------
   if (bp.dbias == nullptr) return;  // uniform
-  // Lane element (il, jt, r) is the pair (query 16(2half+il) + c16, key 16jt + 4g + r):
-  // relative index lane_base + 30*(it - jt) - r.
-  const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;
+  // Lane element (il, jt, r) is the pair (query 16(2half+il) + c16, key 16jt + 4g + r).
   float* dcol = dtab + head * kTableMax;
+  if constexpr (kWs8) {
+    // relative index lane_base + 30*(it - jt) - r
+    const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;
 #pragma unroll
-  for (int il = 0; il < 2; ++il)
+    for (int il = 0; il < 2; ++il)
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
+      for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        atomicAdd(dcol + lane_base + 30 * (2 * half + il - jt) - r, gz[il][jt][r]);
+        for (int r = 0; r < 4; ++r)
+          atomicAdd(dcol + lane_base + 30 * (2 * half + il - jt) - r, gz[il][jt][r]);
+  } else {
+    // pairs of window tokens only: idx = (hi - hj + wh - 1) (2 ww - 1) + wi - wj + ww - 1
+    const int ww = p.window_w, rel = 2 * p.window_w - 1;
+#pragma unroll
+    for (int il = 0; il < 2; ++il) {
+      const int i = 16 * (2 * half + il) + c16;
+      if (i >= p.n_geo) continue;
+      const int base_i = (i / ww + p.window_h - 1) * rel + i % ww + ww - 1;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * jt + 4 * g + r;
+          if (j < p.n_geo) atomicAdd(dcol + base_i - (j / ww) * rel - j % ww, gz[il][jt][r]);
+        }
+    }
+  }
   lds_barrier();
   for (int e = tid; e < G * p.table_size; e += nthreads) {
     const int hh = e / p.table_size, idx = e - hh * p.table_size;
@@ -337,13 +377,13 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
 
 template <int D, int G>
 constexpr int bwd_lds_bytes() {
-  return 4 * kNPad * (G * D / 8) * 16 + 2 * G * kBwdTile + 2 * G * kTableMax * (int)sizeof(float);
+  return 4 * kNPad * bwd_tile_cpr(G, D) * 16 + 2 * G * kBwdTile + 2 * G * kTableMax * (int)sizeof(float);
 }
 
-template <int D, int G, bool kExplicit>
+template <int D, int G, bool kExplicit, bool kWs8>
 int launch_bwd(const BwdParams& bp, hipStream_t s) {
   constexpr int lds = bwd_lds_bytes<D, G>();
-  auto kern = window_attn_bwd_kernel<D, G, kExplicit>;
+  auto kern = window_attn_bwd_kernel<D, G, kExplicit, kWs8>;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
@@ -368,38 +408,32 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
   return TERRA_OK;
 }
 
+template <bool kWs8>
+int launch_bwd_tiles(const BwdParams& bp, hipStream_t s, int D, int G, bool expl) {
+  if (D == 32)
+    return G == 2 ? (expl ? launch_bwd<32, 2, true, kWs8>(bp, s) : launch_bwd<32, 2, false, kWs8>(bp, s))
+                  : (expl ? launch_bwd<32, 1, true, kWs8>(bp, s) : launch_bwd<32, 1, false, kWs8>(bp, s));
+  return expl ? launch_bwd<64, 1, true, kWs8>(bp, s) : launch_bwd<64, 1, false, kWs8>(bp, s);
+}
+
 // ============================================================================
-// generic backward: fp32 or bf16, any window up to 8x8, padded tokens / keys
+// fp32 backward: any window up to 8x8, padded tokens / keys
 // ============================================================================
 //
 // One workgroup per (window, head), plain fp32 arithmetic on LDS copies of
-// q, k, v and dout (no MFMA): the shapes it serves (fp32 activations, 7x7
-// windows) are small configurations.  The logits follow the forward:
+// q, k, v and dout (no MFMA): the shapes it serves (fp32 activations) are
+// small configurations.  The logits follow the forward:
 // z = q k^T * scale + bias + mask for tokens of the window geometry, keys
 // >= n_real replaced by pad_key_value (their gradient is zero: masked_fill),
 // keys >= tokens excluded.
-
-template <bool kBf16> struct BwdElt;
-template <> struct BwdElt<true> {
-  using T = uint16_t;
-  static __device__ __forceinline__ float load(const T* p) { return bf16_bits_to_f32(*p); }
-  static __device__ __forceinline__ void store(T* p, float v) { *p = f32_to_bf16_bits(v); }
-};
-template <> struct BwdElt<false> {
-  using T = float;
-  static __device__ __forceinline__ float load(const T* p) { return *p; }
-  static __device__ __forceinline__ void store(T* p, float v) { *p = v; }
-};
 
 template <int D>
 constexpr int generic_bwd_lds_bytes() {
   return (4 * kNPad * (D + 1) + 2 * kNPad * (kNPad + 1) + kTableMax) * (int)sizeof(float);
 }
 
-template <bool kBf16, int D, bool kExplicit>
+template <int D, bool kExplicit>
 __global__ __launch_bounds__(256) void window_attn_bwd_generic_kernel(const BwdParams bp) {
-  using E = BwdElt<kBf16>;
-  using T = typename E::T;
   extern __shared__ __attribute__((aligned(16))) float smf[];
   const AttnParams& p = bp.a;
   constexpr int PD = D + 1;                     // odd row pitches: conflict-free column walks
@@ -418,7 +452,7 @@ __global__ __launch_bounds__(256) void window_attn_bwd_generic_kernel(const BwdP
   auto load_rows = [&](const void* base, int64_t stride, float* dst) {
     for (int e = tid; e < N * D; e += 256) {
       const int r = e / D, c = e - r * D;
-      dst[r * PD + c] = E::load(reinterpret_cast<const T*>(base) + ((int64_t)w * N + r) * stride + h * D + c);
+      dst[r * PD + c] = reinterpret_cast<const float*>(base)[((int64_t)w * N + r) * stride + h * D + c];
     }
   };
   load_rows(p.q, p.q_stride, qs);
@@ -518,9 +552,9 @@ __global__ __launch_bounds__(256) void window_attn_bwd_generic_kernel(const BwdP
       av = __builtin_fmaf(ps[t * PP + r], ds[t * PD + c], av);
     }
     const int64_t row_g = (int64_t)w * N + r;
-    E::store(reinterpret_cast<T*>(bp.dq) + row_g * bp.dq_stride + h * D + c, aq * bp.scale);
-    E::store(reinterpret_cast<T*>(bp.dk) + row_g * bp.dk_stride + h * D + c, ak * bp.scale);
-    E::store(reinterpret_cast<T*>(bp.dv) + row_g * bp.dv_stride + h * D + c, av);
+    reinterpret_cast<float*>(bp.dq)[row_g * bp.dq_stride + h * D + c] = aq * bp.scale;
+    reinterpret_cast<float*>(bp.dk)[row_g * bp.dk_stride + h * D + c] = ak * bp.scale;
+    reinterpret_cast<float*>(bp.dv)[row_g * bp.dv_stride + h * D + c] = av;
   }
   if (bp.dbias == nullptr) return;  // uniform
   __syncthreads();
@@ -530,10 +564,10 @@ __global__ __launch_bounds__(256) void window_attn_bwd_generic_kernel(const BwdP
   }
 }
 
-template <bool kBf16, int D, bool kExplicit>
+template <int D, bool kExplicit>
 int launch_bwd_generic(const BwdParams& bp, hipStream_t s) {
   constexpr int lds = generic_bwd_lds_bytes<D>();
-  auto kern = window_attn_bwd_generic_kernel<kBf16, D, kExplicit>;
+  auto kern = window_attn_bwd_generic_kernel<D, kExplicit>;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
@@ -645,26 +679,19 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   const bool expl = d.mask_mode == TERRA_MASK_EXPLICIT;
   hipStream_t s = (hipStream_t)stream;
   int st;
-  const bool tile = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
-                    d.n_real == 64;
-  if (tile) {
-    // Two heads per workgroup for head dim 32 (128-byte row slices), else one.
+  if (dtype == TERRA_DTYPE_BF16) {
+    // MFMA tiles for every bf16 window; the 8x8 closed-form geometry where it
+    // applies.  Two heads per workgroup for head dim 32 (128-byte row
+    // slices), else one.
+    const bool ws8 = d.window_h == 8 && d.window_w == 8 && d.tokens == 64 && d.n_real == 64;
     const int G = (D == 32 && d.heads % 2 == 0) ? 2 : 1;
     p.group = G;
     p.groups = d.heads / G;
-    if (D == 32)
-      st = G == 2 ? (expl ? launch_bwd<32, 2, true>(bp, s) : launch_bwd<32, 2, false>(bp, s))
-                  : (expl ? launch_bwd<32, 1, true>(bp, s) : launch_bwd<32, 1, false>(bp, s));
-    else
-      st = expl ? launch_bwd<64, 1, true>(bp, s) : launch_bwd<64, 1, false>(bp, s);
+    st = ws8 ? launch_bwd_tiles<true>(bp, s, D, G, expl) : launch_bwd_tiles<false>(bp, s, D, G, expl);
   } else {
     p.group = p.groups = 0;
-    if (dtype == TERRA_DTYPE_BF16)
-      st = D == 32 ? (expl ? launch_bwd_generic<true, 32, true>(bp, s) : launch_bwd_generic<true, 32, false>(bp, s))
-                   : (expl ? launch_bwd_generic<true, 64, true>(bp, s) : launch_bwd_generic<true, 64, false>(bp, s));
-    else
-      st = D == 32 ? (expl ? launch_bwd_generic<false, 32, true>(bp, s) : launch_bwd_generic<false, 32, false>(bp, s))
-                   : (expl ? launch_bwd_generic<false, 64, true>(bp, s) : launch_bwd_generic<false, 64, false>(bp, s));
+    st = D == 32 ? (expl ? launch_bwd_generic<32, true>(bp, s) : launch_bwd_generic<32, false>(bp, s))
+                 : (expl ? launch_bwd_generic<64, true>(bp, s) : launch_bwd_generic<64, false>(bp, s));
   }
   if (st != TERRA_OK) return st;
   const hipError_t e = hipGetLastError();

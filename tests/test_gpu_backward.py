@@ -70,9 +70,11 @@ def _mask_case(kind, B, H, W, seed):
     return WindowMask(shift=ShiftMask.from_geometry(g), land_bits=bits), total
 
 
-@pytest.mark.parametrize("C,heads", [(192, 6), (128, 2)])
+@pytest.mark.parametrize("C,heads", [(192, 6), (128, 2), (96, 3)])
 @pytest.mark.parametrize("kind", ["none", "shift", "explicit", "land"])
 def test_attention_backward_matches_oracle(dev, C, heads, kind):
+    """8x8 windows: two heads of dim 32 per workgroup (192, 6), one of dim 64
+    (128, 2) and one of dim 32 (96, 3: LDS rows padded to the 8-chunk swizzle)."""
     B, H, W = 2, 32, 48
     B_ = B * (H // 8) * (W // 8)
     q, k, v, dout, table = _inputs(B_, C, heads, 300)
@@ -167,11 +169,14 @@ def _close_dtype(got, ref, dtype):
         assert err <= 2e-2 * scale, (err, scale)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype,C,heads", [(torch.float32, 96, 3), (torch.bfloat16, 96, 3),
+                                           (torch.bfloat16, 128, 4)])
 @pytest.mark.parametrize("kind", ["none", "shift", "explicit", "land"])
-def test_generic_backward_7x7_matches_oracle(dev, dtype, kind):
-    """7x7 windows (c1, c2): the generic kernel, every mask form."""
-    B, H, W, C, heads, ws, s = 2, 14, 21, 96, 3, 7, 3
+def test_generic_backward_7x7_matches_oracle(dev, dtype, C, heads, kind):
+    """7x7 windows (c1, c2), every mask form: fp32 through the plain kernel,
+    bf16 through the MFMA tiles with rows 49..63 empty (one head of dim 32 per
+    workgroup, and two as in c2)."""
+    B, H, W, ws, s = 2, 14, 21, 7, 3
     g = WindowGeometry(B, H, W, 1, ws, s, s)
     B_ = g.num_windows
     q, k, v, dout, _ = _inputs(B_, C, heads, 360)
