@@ -87,6 +87,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
   constexpr int cpr = G * D / 8;                 // chunks per row of the head group
   constexpr int lcpr = bwd_tile_cpr(G, D);       // LDS row pitch in chunks
   constexpr int tile_bytes = kNPad * lcpr * 16;
+  static_assert(lcpr % 8 == 0, "LDS rows must be whole groups of 8 chunks (swizzle)");
   constexpr int kKF = D / 32;
   uint8_t* qs = smem;
   uint8_t* ks = smem + tile_bytes;
