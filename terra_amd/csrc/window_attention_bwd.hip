@@ -50,10 +50,18 @@ struct BwdParams {
 
 constexpr int kBwdTile = kNPad * 8 * 16;  // one [64][64] bf16 P or dz tile: 8 KB
 
+// Slot of chunk `chunk` of row `row` in a [64][8]-chunk P or dz tile: chunk
+// XOR (row & 7).  Those tiles are only written by 8-byte stores and read by
+// transposing reads of 4 consecutive rows per 16 lanes, which the pairwise
+// tile_slot swizzle ((row >> 1) & 7) maps onto the same banks two by two.
+__device__ __forceinline__ int pz_slot(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
 // 16x16x32 bf16 operand fragment read across the rows of a [64][cpr]-chunk
-// tile: lane (c, g) receives column col0 + c at rows 32*js + 16*(e/4) + 4g +
-// e%4 for k slot e (col0 a multiple of 16).  As an A operand the column is
-// the output row; as a B operand it is the output column.
+// tile (kPz: a P or dz tile in pz_slot layout, else tile_slot layout): lane
+// (c, g) receives column col0 + c at rows 32*js + 16*(e/4) + 4g + e%4 for k
+// slot e (col0 a multiple of 16).  As an A operand the column is the output
+// row; as a B operand it is the output column.
+template <bool kPz>
 __device__ __forceinline__ bf16x8 rows_frag(const uint8_t* tile, int cpr, int col0, int js, int lane) {
   const int g = lane >> 4, c16 = lane & 15;
   const int cc = col0 + 4 * (c16 & 3);  // column addressed by this source lane
@@ -61,7 +69,8 @@ __device__ __forceinline__ bf16x8 rows_frag(const uint8_t* tile, int cpr, int co
 #pragma unroll
   for (int h2 = 0; h2 < 2; ++h2) {
     const int row = 32 * js + 16 * h2 + 4 * g + (c16 >> 2);
-    part[h2] = lds_read_tr16(tile + tile_slot(row, cc >> 3, cpr) * 16 + (cc & 7) * 2);
+    const int slot = kPz ? pz_slot(row, cc >> 3) : tile_slot(row, cc >> 3, cpr);
+    part[h2] = lds_read_tr16(tile + slot * 16 + (cc & 7) * 2);
   }
   const uint32_t w[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
   return __builtin_bit_cast(bf16x8, w);
@@ -236,7 +245,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
         }
         gz[il][jt] += z;
         // [query][key] tiles: this lane's keys 16jt + 4g .. + 3 are 8 bytes.
-        const int off = tile_slot(i, 2 * jt + (g >> 1), 8) * 16 + (g & 1) * 8;
+        const int off = pz_slot(i, 2 * jt + (g >> 1)) * 16 + (g & 1) * 8;
         *reinterpret_cast<uint2*>(ptile + off) = pack4_bf16(s[il][jt]);
         *reinterpret_cast<uint2*>(ztile + off) = pack4_bf16(z);
         dp[il][jt] = z;
@@ -245,7 +254,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
     // dQ^T = K^T dz^T (dz accumulators as the P^T operand), times scale.
     f32x4 dqa[D / 16][2];
     {
-      auto kfrag = [&](int ct, int js) -> bf16x8 { return rows_frag(ks, lcpr, head * D + 16 * ct, js, lane); };
+      auto kfrag = [&](int ct, int js) -> bf16x8 { return rows_frag<false>(ks, lcpr, head * D + 16 * ct, js, lane); };
       pv_half<true, D>(dqa, dp, lane, kfrag);
     }
     lds_barrier();  // P and dz tiles of both halves are in LDS; K and V are no longer read
@@ -275,13 +284,13 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
         bf16x8 pf[2], zf[2];
 #pragma unroll
         for (int jt = 0; jt < 2; ++jt) {
-          pf[jt] = rows_frag(ptile, 8, 32 * half + 16 * jt, js, lane);
-          zf[jt] = rows_frag(ztile, 8, 32 * half + 16 * jt, js, lane);
+          pf[jt] = rows_frag<true>(ptile, 8, 32 * half + 16 * jt, js, lane);
+          zf[jt] = rows_frag<true>(ztile, 8, 32 * half + 16 * jt, js, lane);
         }
 #pragma unroll
         for (int ct = 0; ct < D / 16; ++ct) {
-          const bf16x8 dof = rows_frag(dos, lcpr, head * D + 16 * ct, js, lane);
-          const bf16x8 qf = rows_frag(qs, lcpr, head * D + 16 * ct, js, lane);
+          const bf16x8 dof = rows_frag<false>(dos, lcpr, head * D + 16 * ct, js, lane);
+          const bf16x8 qf = rows_frag<false>(qs, lcpr, head * D + 16 * ct, js, lane);
 #pragma unroll
           for (int jt = 0; jt < 2; ++jt) {
             av[ct][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dof, pf[jt], av[ct][jt], 0, 0, 0);
