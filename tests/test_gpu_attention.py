@@ -78,8 +78,11 @@ def test_core_no_mask(dev, dtype, ws, C, heads, with_bias):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("H,W,ws,s,C,heads", [(56, 56, 7, 3, 96, 3), (32, 48, 8, 4, 192, 6), (16, 24, 8, 4, 128, 2)])
+@pytest.mark.parametrize("H,W,ws,s,C,heads", [(56, 56, 7, 3, 96, 3), (32, 48, 8, 4, 192, 6), (16, 24, 8, 4, 128, 2),
+                                               (28, 42, 7, 3, 128, 4)])
 def test_core_shift_mask_analytic_and_dense(dev, dtype, H, W, ws, s, C, heads):
+    """The analytic mask (8x8 bf16 with an even head count: the tile kernels;
+    otherwise the per-wave kernel) against the dense mask and the oracle."""
     nW = (H // ws) * (W // ws)
     B = 2
     q, k, v, table = _inputs(B * nW, ws * ws, C, heads, ws, dtype, 210, qkv_scale=2.0)
@@ -94,8 +97,8 @@ def test_core_shift_mask_analytic_and_dense(dev, dtype, H, W, ws, s, C, heads):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_core_land_bits(dev, dtype):
-    H, W, ws, s, C, heads = 32, 64, 8, 4, 192, 6
+@pytest.mark.parametrize("H,W,ws,s,C,heads", [(32, 64, 8, 4, 192, 6), (28, 42, 7, 3, 128, 4)])
+def test_core_land_bits(dev, dtype, H, W, ws, s, C, heads):
     land = workloads.land_mask(H, W, seed=9)
     g = WindowGeometry(1, H, W, 1, ws, s, s)
     bits = utils.land_window_bits(land.to(dev), g)
@@ -123,6 +126,18 @@ def test_core_padded_tokens_and_keys(dev, dtype):
     ref = so.window_attention_core(q, k, v, heads, (C // heads) ** -0.5, table, (ws, ws), mask, n_real=49,
                                    compute_dtype=cd)
     _check(out, ref, dtype)
+
+
+@pytest.mark.parametrize("heads", [4, 2])
+def test_core_padded_keys_tile(dev, heads):
+    """Padded keys without a dense mask: 49 real tokens of 7x7 windows in
+    64-token rows, head dim 32 and 64, bf16."""
+    B_, N, C, ws = 16, 64, 128, 7
+    q, k, v, table = _inputs(B_, N, C, heads, ws, torch.bfloat16, 235)
+    out = _run(dev, q, k, v, heads, ws, table, n_real=49)
+    ref = so.window_attention_core(q, k, v, heads, (C // heads) ** -0.5, table, (ws, ws), None, n_real=49,
+                                   compute_dtype=torch.float32)
+    _check(out, ref, torch.bfloat16)
 
 
 def test_core_strided_qkv_equals_contiguous(dev):
