@@ -771,7 +771,12 @@ __global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockPara
           layernorm_window<cpr, kGroupThreads>(p, cur, xr, xn, s_gamma, s_beta, h * 64 + lane_i);
       } else if (ph == 1) {
         if (have) {
+          // MFMA phases run at raised wave priority: in each slot the
+          // arbiter then issues this group's matrix instructions ahead of the
+          // other group's VALU phase, which fills the MFMA shadow.
+          __builtin_amdgcn_s_setprio(1);
           if (cur.computed) head_qkv<C, kPacked>(p, xn, h, lane_i, kf4, vf, qf, s_bqkv);
+          __builtin_amdgcn_s_setprio(0);
           // The next window's rows, behind the q/k/v loads; the buffer's last
           // reader was phase A's store.
           if (k + 1 < n_mine)
@@ -782,7 +787,9 @@ __global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockPara
         if (have && cur.computed)
           head_attention<C>(p, cur, tabs + h * kTableMax, h, lane_i, kf4, vf, qf, xn);
       } else {
+        __builtin_amdgcn_s_setprio(1);
         if (have && cur.computed) head_proj<C, kPacked>(p, xn, xr, h, lane_i, s_bproj);
+        __builtin_amdgcn_s_setprio(0);
         // The next window's rows have landed before phase A reads them.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
