@@ -37,6 +37,7 @@ import json
 import os
 import platform
 import statistics
+import subprocess
 import sys
 import time
 
@@ -55,6 +56,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="c3", choices=("c1", "c2", "c3", "c4", "c5"))
+    ap.add_argument("--prewarm-s", type=float, default=3.0,
+                    help="seconds of untimed steps before the counted warm-up (clock settling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--mode", choices=("step", "kernels"), default="step",
@@ -126,6 +129,15 @@ def run_kernels(cfg, blk, x, steps):
 
 
 def cpu_model() -> str:
+    """The host CPU's model name as lscpu prints it (else /proc/cpuinfo)."""
+    try:
+        out = subprocess.run(["lscpu"], stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, text=True,
+                             timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -138,38 +150,60 @@ def cpu_model() -> str:
 
 def cpu_baseline(cfg, blk, land, budget_s: float):
     """The oracle's restatement of the reference block (torch CPU, fp32) on a
-    bounded sample: a band of whole window rows of the same workload."""
+    bounded sample: a band of whole window rows of the same workload, timed
+    with every thread torch uses and with one thread (two warm-up runs, then
+    the median of up to 5 runs within the budget of each)."""
     import torch
 
     from oracle import swin_oracle as so
     from terra_amd import workloads
 
-    threads = torch.get_num_threads()
     params = {k: v.detach().float().cpu() for k, v in blk.state_dict().items() if k != "attn_mask"}
     # sample: the first `rows` token rows (whole window rows); the shift wraps within the band
     rows = min(cfg.height, max(cfg.window, (64 // cfg.window) * cfg.window))
     x = workloads.activations((1, rows * cfg.width, cfg.channels), 1000, torch.float32)
     land_s = land[:rows]
-    times = []
-    t_end = time.perf_counter() + budget_s
-    with torch.inference_mode():
-        so.swin_block_attention(x, rows, cfg.width, cfg.window, blk.shift_size, cfg.heads, params, land=land_s)
-        while time.perf_counter() < t_end or len(times) < 2:
-            t0 = time.perf_counter()
-            so.swin_block_attention(x, rows, cfg.width, cfg.window, blk.shift_size, cfg.heads, params, land=land_s)
-            times.append(time.perf_counter() - t0)
-            if len(times) >= 20:
-                break
-    t = statistics.median(times)
     tokens = rows * cfg.width
+
+    def timed(threads: int, budget: float):
+        prev = torch.get_num_threads()
+        torch.set_num_threads(threads)
+        try:
+            times = []
+            with torch.inference_mode():
+                for _ in range(2):
+                    so.swin_block_attention(x, rows, cfg.width, cfg.window, blk.shift_size, cfg.heads, params,
+                                            land=land_s)
+                t_end = time.perf_counter() + budget
+                while len(times) < 5 and (time.perf_counter() < t_end or len(times) < 1):
+                    t0 = time.perf_counter()
+                    so.swin_block_attention(x, rows, cfg.width, cfg.window, blk.shift_size, cfg.heads, params,
+                                            land=land_s)
+                    times.append(time.perf_counter() - t0)
+        finally:
+            torch.set_num_threads(prev)
+        return statistics.median(times), len(times)
+
+    threads = torch.get_num_threads()
+    t_all, n_all = timed(threads, budget_s)
+    t_one, n_one = timed(1, budget_s)
     return {
-        "value": tokens / t,
+        "value": tokens / t_all,
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle restatement of the reference op sequence (torch CPU fp32, {threads} threads, "
-                   f"{cpu_model()}): {rows}x{cfg.width}-token band of {cfg.name} ({tokens} tokens, "
-                   f"{tokens // cfg.tokens} windows), median of {len(times)} runs, {t * 1e3:.1f} ms each"),
+        "sample": f"{rows}x{cfg.width} band of {cfg.name}, fp32 oracle",
+        "sample_tokens": tokens,
+        "sample_windows": tokens // cfg.tokens,
+        "ms_per_sample": t_all * 1e3,
+        "runs": n_all,
+        "value_1_thread": tokens / t_one,
+        "ms_per_sample_1_thread": t_one * 1e3,
+        "runs_1_thread": n_one,
+        "os_cpu_count": os.cpu_count(),
+        "torch_threads": threads,
+        "cpu_model": cpu_model(),
+        "what": "oracle restatement of the reference op sequence (torch CPU fp32, inference_mode)",
     }
 
 
@@ -224,8 +258,21 @@ def main():
     for n, k in zip(names, keys):
         setattr(kernels, n, timed(k, orig[n]))
 
-    def run(steps, warmup):
+    prewarm = {"s": 0.0, "steps": 0}
+
+    def run(steps, warmup, prewarm_s=0.0):
         with torch.no_grad():
+            # Time-based pre-warm: the step repeated for `prewarm_s` seconds,
+            # so that the GPU clock has settled under this load before the
+            # counted warm-up and the timed steps (a few launches from idle
+            # run at a lower clock).
+            t_end = time.perf_counter() + prewarm_s
+            while time.perf_counter() < t_end:
+                for _ in range(10):
+                    blk(x)
+                torch.cuda.synchronize()
+                prewarm["steps"] += 10
+            prewarm["s"] += prewarm_s
             for _ in range(warmup):
                 blk(x)
             torch.cuda.synchronize()
@@ -261,7 +308,7 @@ def main():
         return statistics.median(samples)
 
     try:
-        ms = run(args.steps, args.warmup)
+        ms = run(args.steps, args.warmup, args.prewarm_s)
         # The fused kernel serves bf16, 8x8 windows, head dim 32 (c3, c5); the
         # other configurations run the five-stage path as the step itself.
         fused = bool(events["swin_block"])
@@ -331,12 +378,15 @@ def main():
     mlp_flops = 2.0 * 2.0 * grid_tokens * C * (4 * C)    # fc1 + fc2
     mlp_bytes = 2.0 * grid_bytes                         # x read once, y written once
 
-    def avg_us(name):
-        return 1e3 * statistics.mean(a.elapsed_time(b) for a, b in events[name])
+    def launch_us(name):
+        """Per-launch durations (us) of a kernel over the timed steps: HIP
+        events on its launch stream around each launch."""
+        return [1e3 * a.elapsed_time(b) for a, b in events[name]]
 
     tokens = cfg.real_tokens
     if fused:
-        t_blk = avg_us("swin_block")
+        per_launch = launch_us("swin_block")
+        t_blk = statistics.mean(per_launch)
         blk_tflops = block_flops / (t_blk * 1e-6) / 1e12
         roofline = {
             "kernel": (f"swin_block_{'pp_' if cfg.heads == 6 else ''}kernel<{cfg.heads}> (fused LN + qkv + window "
@@ -350,6 +400,10 @@ def main():
             "algorithmic_flops_per_launch": block_flops,
             "algorithmic_bytes_per_launch": block_bytes,
             "avg_launch_us": t_blk,
+            "median_launch_us": statistics.median(per_launch),
+            "min_launch_us": min(per_launch),
+            "max_launch_us": max(per_launch),
+            "launches": len(per_launch),
             "hbm_GB_s": block_bytes / (t_blk * 1e-6) / 1e9,
             "hbm_frac": block_bytes / (t_blk * 1e-6) / 1e9 / HBM_PEAK_GBS,
         }
@@ -377,6 +431,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm": {"seconds": prewarm["s"], "steps": prewarm["steps"],
+                    "note": "untimed steps before the counted warm-up, so the clock has settled"},
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",

@@ -188,3 +188,131 @@ def mlp(x: np.ndarray, p: dict, use_layernorm: bool = True, eps: float = 1e-5,
             y = rnd(sum(w2[c, j] * h[j] for j in range(hid)) + b2[c])
             out[t, c] = rnd(row[c] + y)
     return out.reshape(np.asarray(x).shape)
+
+
+def _bf16_scalar(a: float) -> float:
+    """float64 -> float32 -> nearest bf16, as float64 (a GPU fp32 result cast to bf16)."""
+    return float(bf16_round(np.float32(a)))
+
+
+def attention_autocast_bf16(q: np.ndarray, k: np.ndarray, v: np.ndarray, num_heads: int, scale: float,
+                            bias: Optional[np.ndarray] = None, mask: Optional[np.ndarray] = None) -> np.ndarray:
+    """The attention core as a bf16 autocast region runs it, by loops: bf16
+    inputs; q * scale rounded to bf16; each logit q.k accumulated exactly and
+    rounded to bf16 (autocast's matmul output); bias and mask added in fp32;
+    softmax in float64 then rounded to bf16 (the probabilities are cast before
+    attn @ v); each output accumulated exactly and rounded to bf16.
+    bias: [nH, N, N] or None; mask: [nW, N, N] (window w uses mask[w % nW])."""
+    B_, N, C = q.shape
+    d = C // num_heads
+    qb = bf16_round(np.asarray(q, np.float32)).astype(np.float64)
+    kb = bf16_round(np.asarray(k, np.float32)).astype(np.float64)
+    vb = bf16_round(np.asarray(v, np.float32)).astype(np.float64)
+    out = np.zeros((B_, N, C), dtype=np.float64)
+    for w in range(B_):
+        for h in range(num_heads):
+            cs = slice(h * d, (h + 1) * d)
+            qs = [[_bf16_scalar(float(np.float32(a) * np.float32(scale))) for a in qb[w, i, cs]] for i in range(N)]
+            for i in range(N):
+                logits = []
+                for j in range(N):
+                    s = _bf16_scalar(sum(a * b for a, b in zip(qs[i], kb[w, j, cs])))
+                    if bias is not None:
+                        s = float(np.float32(s) + np.float32(bias[h, i, j]))
+                    if mask is not None:
+                        s = float(np.float32(s) + np.float32(mask[w % mask.shape[0], i, j]))
+                    logits.append(s)
+                mx = max(logits)
+                e = [math.exp(s - mx) for s in logits]
+                tot = sum(e)
+                p = [_bf16_scalar(x / tot) for x in e]
+                for c in range(d):
+                    out[w, i, h * d + c] = _bf16_scalar(sum(p[j] * vb[w, j, h * d + c] for j in range(N)))
+    return out
+
+
+def layer_norm_row(row: Sequence[float], gamma: Optional[Sequence[float]], beta: Optional[Sequence[float]],
+                   eps: float = 1e-5) -> List[float]:
+    """nn.LayerNorm over one token from its definition: biased variance."""
+    C = len(row)
+    mean = sum(row) / C
+    var = sum((c - mean) ** 2 for c in row) / C
+    inv = 1.0 / math.sqrt(var + eps)
+    return [(row[c] - mean) * inv * (1.0 if gamma is None else gamma[c]) + (0.0 if beta is None else beta[c])
+            for c in range(C)]
+
+
+def swin_block(x: np.ndarray, params: dict, ws: int, shift: int, num_heads: int,
+               land: Optional[np.ndarray] = None, use_attn_mask: bool = True, use_layernorm: bool = True,
+               pad: Sequence[int] = (0, 0, 0, 0), win_row_begin: int = 0, win_rows: Optional[int] = None,
+               valid: Optional[Tuple[int, int]] = None, eps: float = 1e-5) -> np.ndarray:
+    """The attention half of a Swin block, token by token in float64:
+    LayerNorm each token, cut the (padded, shifted) frame into windows through
+    frame_source (padding tokens and pad windows are zero vectors after the
+    LayerNorm), q/k/v = W xn + b per token, per window and head
+    softmax(q.k * d^-1/2 + table[relative index] + mask) v with the mask
+    -100 for keys of another shift region (regions of the padded frame) or on
+    land, proj, and every grid token takes back the output of the window token
+    it was read into, plus the input token (the residual).  Tokens that no
+    emitted window reads get the residual only.
+    x: [B, H, W, C]; params: state-dict names as numpy arrays (norm1.weight /
+    .bias, attn.{q,k,v}_linear.weight / .bias, attn.proj.weight / .bias,
+    attn.relative_position_bias_table); land: [H, W] bool or None.
+    Returns [B, H, W, C]."""
+    B, H, W, C = x.shape
+    top, bottom, left, right = pad
+    Hp, Wp = H + top + bottom, W + left + right
+    nww = Wp // ws
+    N = ws * ws
+    d = C // num_heads
+    scale = d ** -0.5
+    P = {k_: np.asarray(v_, np.float64) for k_, v_ in params.items()}
+    table = P.get("attn.relative_position_bias_table")
+    rel = relative_index(ws, ws)
+    src = frame_source(B, H, W, ws, shift, shift, pad, win_row_begin, win_rows, valid)
+    rows = (Hp // ws - win_row_begin) if win_rows is None else win_rows
+    xs = np.asarray(x, np.float64)
+    y = xs.copy()
+    for wi in range(len(src) // N):
+        toks = src[wi * N:(wi + 1) * N]
+        xn = []
+        for s in toks:
+            if s is None:
+                xn.append([0.0] * C)
+            elif use_layernorm:
+                xn.append(layer_norm_row(list(xs[s]), P["norm1.weight"], P["norm1.bias"], eps))
+            else:
+                xn.append(list(xs[s]))
+        lin = {}
+        for name in ("q", "k", "v"):
+            wgt, bia = P[f"attn.{name}_linear.weight"], P[f"attn.{name}_linear.bias"]
+            lin[name] = [[sum(wgt[o, c] * t[c] for c in range(C)) + bia[o] for o in range(C)] for t in xn]
+        # frame window of this emitted window and the region id of each token
+        r_local = (wi % (rows * nww)) // nww
+        wr, wc = r_local + win_row_begin, wi % nww
+        rid = [(_region(wr * ws + t // ws, Hp, ws, shift), _region(wc * ws + t % ws, Wp, ws, shift))
+               for t in range(N)]
+        is_land = [s is not None and land is not None and bool(land[s[1], s[2]]) for s in toks]
+        o = [[0.0] * C for _ in range(N)]
+        for h in range(num_heads):
+            for i in range(N):
+                logits = []
+                for j in range(N):
+                    s_ = scale * sum(lin["q"][i][h * d + c] * lin["k"][j][h * d + c] for c in range(d))
+                    if table is not None:
+                        s_ += table[rel[i, j], h]
+                    if shift > 0 and use_attn_mask and rid[i] != rid[j]:
+                        s_ += -100.0
+                    if is_land[j]:
+                        s_ += -100.0
+                    logits.append(s_)
+                mx = max(logits)
+                e = [math.exp(a - mx) for a in logits]
+                tot = sum(e)
+                for c in range(d):
+                    o[i][h * d + c] = sum(e[j] / tot * lin["v"][j][h * d + c] for j in range(N))
+        wp, bp = P["attn.proj.weight"], P["attn.proj.bias"]
+        for t, s in enumerate(toks):
+            if s is not None:
+                y[s] = xs[s] + np.array([sum(wp[f, c] * o[t][c] for c in range(C)) + bp[f] for f in range(C)])
+    return y

@@ -20,8 +20,13 @@ brute-force loops, closed forms, library special cases, known answers):
   land_key_flags / fold_land           brute loops
   ragged_row_major                     the reference's own unit-test vector
                                        (tests/unit/test_window_assignment.py:10-23)
-  swin_block_attention                 composition of the pinned parts above;
-                                       LayerNorm / Linear are torch's own ops
+  window_attention_autocast_bf16       brute.attention_autocast_bf16 (loops rounding
+                                       to bf16 at the same points); the fp32 core
+                                       must fail the same check
+  swin_block_attention                 brute.swin_block (float64 token loops: own
+                                       LayerNorm, frame walk, region ids, relative
+                                       index, softmax, reverse), with pad, slab,
+                                       pad-window, land and no-LayerNorm cases
   mlp / mlp_bf16                       brute.mlp (token loops, math.erf GELU,
                                        bit-level bf16 rounding); GELU known
                                        values; LayerNorm against its definition
@@ -230,7 +235,8 @@ def window_attention_autocast_bf16(q, k, v, num_heads, scale, bias_table=None, w
     """The reference's core under CUDA autocast(bf16) (core/runtime/run_model.py:424-448):
     q*scale and q@k^T rounded to bf16, bias/mask promote to fp32, fp32 softmax,
     probabilities re-cast to bf16 for attn@v, bf16 output.  Used to report how
-    far the reference itself sits from the fp32 restatement."""
+    far the reference itself sits from the fp32 restatement, and as the
+    yardstick of the drop-ins run under autocast."""
     B_, N, C = q.shape
     d = C // num_heads
     q = q.to(torch.bfloat16).reshape(B_, N, num_heads, d).permute(0, 2, 1, 3)

@@ -888,8 +888,13 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
                 q.channels, d.heads);
   if (d.layernorm != 0 && !(d.ln_eps >= 0.f))
     return fail(TERRA_ERR_SHAPE, "ln_eps must be a non-negative number");
-  if (land_bits != nullptr && d.land_windows <= 0)
-    return fail(TERRA_ERR_SHAPE, "land_windows must be positive when land_bits is given");
+  // land_bits[w % land_windows]: bits built for another frame would wrap onto
+  // the wrong windows, so the period must be whole images of emitted windows.
+  if (land_bits != nullptr &&
+      (d.land_windows <= 0 || ((int64_t)q.batch * dims.nWe) % d.land_windows != 0 || d.land_windows % dims.nWe != 0))
+    return fail(TERRA_ERR_SHAPE,
+                "land_windows (%d) must be a multiple of the emitted windows per image (%lld) dividing the batch's "
+                "(%lld)", d.land_windows, (long long)dims.nWe, (long long)((int64_t)q.batch * dims.nWe));
   for (const void* ptr : {x, (const void*)y, qkv_weight, proj_weight, (const void*)ln_gamma, (const void*)ln_beta,
                           (const void*)qkv_bias, (const void*)proj_bias}) {
     if (((uintptr_t)ptr & 15u) != 0) return fail(TERRA_ERR_ALIGN, "tensors must be 16-byte aligned");

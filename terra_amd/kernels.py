@@ -278,6 +278,8 @@ def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_head
     vs = _row_stride(v, "v", num_windows, tokens, channels)
     if out is None:
         out = torch.empty((num_windows, tokens, channels), dtype=q.dtype, device=dev)
+    elif out.dtype != q.dtype or out.device != dev:
+        raise ValueError(f"out must be a {q.dtype} tensor on {dev} (got {out.dtype} on {out.device})")
     os_ = _row_stride(out, "out", num_windows, tokens, channels)
 
     d = _attn_desc(q, num_heads, window_size, scale, n_real, mask_value, pad_key_value, (qs, ks, vs, os_))
@@ -500,8 +502,13 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
         _require_device(x, land_bits)
         if land_bits.dtype != torch.int64 or land_bits.dim() != 1:
             raise ValueError("land_bits must be a 1-D int64 tensor (one 64-bit key mask per window)")
+        n_land = land_bits.shape[0]
+        if n_land == 0 or geom.num_windows % n_land != 0 or n_land % geom.windows_per_image != 0:
+            raise ValueError(f"land_bits must hold the emitted windows of one image ({geom.windows_per_image}) "
+                             f"or of several whole images dividing the batch (got {n_land} for "
+                             f"{geom.num_windows} windows)")
         land_bits = land_bits.contiguous()
-        d.land_windows = land_bits.shape[0]
+        d.land_windows = n_land
     if out is None:
         out = torch.empty_like(x)
     elif tuple(out.shape) != tuple(x.shape) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:

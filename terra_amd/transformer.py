@@ -91,7 +91,7 @@ class SequentialSwinTransformer(torch.nn.Module):
         shift = ShiftMask.from_geometry(geom) if (self.shift_size > 0 and self.use_attn_mask) else None
         land = None
         if self.land_mask is not None:
-            key = (self.land_mask.device, self.land_mask.data_ptr())
+            key = (self.land_mask.device, self.land_mask.data_ptr(), self.land_mask._version)
             land = self._land_bits_cache.get(key)
             if land is None:
                 land = land_window_bits(self.land_mask, WindowGeometry(

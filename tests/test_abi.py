@@ -249,6 +249,11 @@ def test_block_rejects_null_alignment_overlap_land():
     assert _block_call(d, x=ctypes.c_void_p((1 << 20) + 8)) == -4
     assert _block_call(d, land=FAKE) == -3  # land bits without a period
     assert "land_windows" in L.last_error()
+    g = _geom(channels=192, window=8)
+    n_we = (g.height // 8) * (g.width // 8)
+    for bad in (n_we - 1, n_we + 1, 3 * n_we if g.batch % 3 else 5 * n_we):  # not whole images dividing the batch
+        assert _block_call(_block_desc(land_windows=bad), land=FAKE) == -3
+        assert "land_windows" in L.last_error()
     lib = L.load()
     y = ctypes.c_void_p((1 << 20) + 4096)  # overlaps x without being x
     assert lib.terra_swin_block_fwd(FAKE, y, L.DTYPE_BF16, ctypes.byref(d), None, None, FAKE, None, FAKE, None,

@@ -326,3 +326,69 @@ def test_mlp_bf16_matches_token_loops(use_ln):
     # and within bf16 tolerance of the unrounded float64 module
     exact = brute.mlp(x.numpy(), {k: v.numpy() for k, v in p.items()}, use_layernorm=use_ln)
     assert np.max(np.abs(got - exact)) <= 3e-2 * np.max(np.abs(exact))
+
+
+# ---- the bf16 autocast restatement and the block composition ----
+
+def _bf16_agree(a: np.ndarray, b: np.ndarray) -> bool:
+    """Within one bf16 rounding of each other (2^-7 of the value) plus 2^-9 of
+    the largest output: a logit or probability that lands on the other side of
+    a bf16 rounding boundary (fp32 vs float64 accumulation) moves an output by
+    about that much."""
+    return bool((np.abs(a - b) <= 2.0 ** -7 * np.abs(b) + 2.0 ** -9 * np.abs(b).max()).all())
+
+
+@pytest.mark.parametrize("with_bias,with_mask", [(False, False), (True, True)])
+def test_autocast_core_matches_bf16_loops(with_bias, with_mask):
+    """window_attention_autocast_bf16 against loops that round to bf16 at the
+    same points (q * scale, q.k, probabilities, output).  Logits of standard
+    deviation ~3 make the rounding of q.k visible: the fp32 core, which rounds
+    only its inputs, must fail the same check."""
+    B_, N, C, nH, ws = 4, 16, 16, 2, 4
+    q, k, v = (_rand((B_, N, C), s, torch.float32) * f for s, f in ((70, 2.5), (71, 2.5), (72, 1.0)))
+    table = _rand(((2 * ws - 1) ** 2, nH), 73, torch.float32) if with_bias else None
+    mask = so.shift_mask(8, 8, ws, 2) if with_mask else None
+    scale = (C // nH) ** -0.5
+    got = so.window_attention_autocast_bf16(q, k, v, nH, scale, table, (ws, ws), mask).double().numpy()
+    bias = so.relative_position_bias(table, (ws, ws)).numpy() if with_bias else None
+    want = brute.attention_autocast_bf16(q.numpy(), k.numpy(), v.numpy(), nH, scale, bias,
+                                         None if mask is None else mask.numpy())
+    assert _bf16_agree(got, want)
+    assert np.mean(got == want) >= 0.95  # most outputs bit-equal
+    fp32 = so.window_attention_core(q.bfloat16(), k.bfloat16(), v.bfloat16(), nH, scale, table, (ws, ws), mask)
+    assert not _bf16_agree(fp32.double().numpy(), want)
+
+
+BLOCK_CASES = [  # (B, H, W, C, heads, ws, shift, land, pad, r0, rows, valid, ln, bias)
+    (2, 8, 12, 8, 2, 4, 2, False, (0, 0, 0, 0), 0, None, None, True, True),
+    (1, 12, 8, 8, 2, 4, 0, True, (0, 0, 0, 0), 0, None, None, True, True),
+    (1, 10, 12, 6, 3, 4, 2, True, (1, 1, 0, 4), 0, None, None, True, False),
+    (2, 14, 8, 8, 2, 4, 2, True, (0, 2, 0, 0), 1, 2, (1, 3), True, True),
+    (1, 8, 8, 8, 1, 4, 2, False, (0, 0, 0, 0), 0, None, None, False, True),
+]
+
+
+@pytest.mark.parametrize("case", BLOCK_CASES)
+def test_block_oracle_matches_token_loops(case):
+    """swin_block_attention (LayerNorm, pad / roll / partition, q/k/v, core with
+    bias, shift and land masks, proj, reverse, residual) against the float64
+    token loops of brute.swin_block, which share none of its reshapes, mask
+    construction or index code; slab, pad-window and padded-frame cases
+    included."""
+    B, H, W, C, nH, ws, s, land_on, pad, r0, rows, valid, ln, bias = case
+    x = _rand((B, H, W, C), 80)
+    p = {"norm1.weight": 1.0 + 0.2 * _rand((C,), 81), "norm1.bias": 0.2 * _rand((C,), 82),
+         "attn.proj.weight": _rand((C, C), 83) * 0.4, "attn.proj.bias": _rand((C,), 84) * 0.1}
+    for i, n in enumerate("qkv"):
+        p[f"attn.{n}_linear.weight"] = _rand((C, C), 85 + i) * 0.6
+        p[f"attn.{n}_linear.bias"] = _rand((C,), 88 + i) * 0.1
+    if bias:
+        p["attn.relative_position_bias_table"] = _rand(((2 * ws - 1) ** 2, nH), 91)
+    land = (_rand((H, W), 92) > 0.4) if land_on else None
+    got = so.swin_block_attention(x.view(B, H * W, C), H, W, ws, s, nH, p, land=land, pad=pad, win_row_begin=r0,
+                                  win_rows=rows, valid=valid, use_layernorm=ln, compute_dtype=torch.float64)
+    want = brute.swin_block(x.numpy(), {k_: v_.numpy() for k_, v_ in p.items()}, ws, s, nH,
+                            land=None if land is None else land.numpy(), use_layernorm=ln, pad=pad,
+                            win_row_begin=r0, win_rows=rows, valid=valid)
+    np.testing.assert_allclose(got.view(B, H, W, C).numpy(), want, rtol=1e-10, atol=1e-10)
+    assert not np.allclose(want, x.numpy())  # the attention half changed the tokens it owns

@@ -1,27 +1,41 @@
-"""Window ownership (host-side), pinned by the reference's own unit test
-(tests/unit/test_window_assignment.py of TERRA) plus invariants."""
+"""Window ownership (host-side): the reference's own split vector and error
+text (kept as data), the oracle's restatement of the ragged row-major rule,
+and ownership invariants."""
 import pytest
 
 from oracle import swin_oracle as so
 from terra_amd.window_assignment import get_window_indices, slab_geometry
 
 
-def _flat_ids(indices, width):
-    return [row * width + col for row, col in indices]
+# Data from the reference's unit test of this split (TERRA
+# tests/unit/test_window_assignment.py): a 2 x 5 window grid over 4 ranks gives
+# these flat window ids per rank, and a 2 x 2 topology is refused with this text.
+REFERENCE_SPLIT_2x5_OVER_4 = [[0, 1], [2, 3, 4], [5, 6], [7, 8, 9]]
+REFERENCE_TOPOLOGY_ERROR = r"requires xfmr_wp_topo=\(m, 1\)"
 
 
-def test_terra_m1_auto_uses_contiguous_balanced_chunks():
-    rank_to_indices, global_to_local = get_window_indices(
-        num_windows_h=2, num_windows_w=5, wp_group_h=4, wp_group_w=1, mode="terra_m1_ragged_auto")
-    per_rank_ids = [_flat_ids(rank_to_indices[rank], 5) for rank in range(4)]
-    assert per_rank_ids == [[0, 1], [2, 3, 4], [5, 6], [7, 8, 9]]
-    assert sorted(global_to_local) == [(row, col) for row in range(2) for col in range(5)]
-    assert max(map(len, per_rank_ids)) - min(map(len, per_rank_ids)) <= 1
-    assert all(ids == list(range(ids[0], ids[-1] + 1)) for ids in per_rank_ids)
+def _row_major_ids(coords, n_cols):
+    """(row, col) window coordinates -> flat row-major window ids."""
+    return [r * n_cols + c for r, c in coords]
 
 
-def test_terra_m1_mode_rejects_two_dimensional_wp_topology():
-    with pytest.raises(ValueError, match=r"requires xfmr_wp_topo=\(m, 1\)"):
+def test_auto_ragged_split_reproduces_reference_vector():
+    owners, lookup = get_window_indices(num_windows_h=2, num_windows_w=5, wp_group_h=4, wp_group_w=1,
+                                        mode="terra_m1_ragged_auto")
+    split = [_row_major_ids(owners[r], 5) for r in range(4)]
+    assert split == REFERENCE_SPLIT_2x5_OVER_4
+    # every window is owned exactly once, by a contiguous run of ids whose
+    # lengths differ by at most one between ranks
+    assert sorted(i for ids in split for i in ids) == list(range(10))
+    assert set(lookup) == {(r, c) for r in range(2) for c in range(5)}
+    sizes = [len(ids) for ids in split]
+    assert max(sizes) - min(sizes) <= 1
+    for ids in split:
+        assert ids == list(range(ids[0], ids[0] + len(ids)))
+
+
+def test_auto_ragged_split_refuses_2d_topology():
+    with pytest.raises(ValueError, match=REFERENCE_TOPOLOGY_ERROR):
         get_window_indices(num_windows_h=4, num_windows_w=4, wp_group_h=2, wp_group_w=2,
                            mode="terra_m1_ragged_auto")
 
@@ -62,5 +76,5 @@ def test_slab_geometry_of_c5():
     first, rows, vb, ve = slab_geometry(255, 64, 7, 1)
     assert (first, rows, vb, ve) == (36, 37, 27, 2358)
     r2i, _ = get_window_indices(255, 64, 7, 1, mode="terra_m1_ragged_row_major")
-    flat = _flat_ids(r2i[1], 64)
+    flat = _row_major_ids(r2i[1], 64)
     assert flat[0] - first * 64 == vb and flat[-1] + 1 - first * 64 == ve
