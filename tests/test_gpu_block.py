@@ -119,5 +119,5 @@ def test_c2_basic_layer_wmsa_then_swmsa_with_mlp(dev):
 
 def test_window_attention_rejects_wrong_out(dev):
     q = workloads.activations((4, 64, 64), 320, torch.bfloat16).to(dev)
-    with pytest.raises(ValueError, match="dtype"):
+    with pytest.raises(ValueError, match="out must be a torch.bfloat16 tensor"):
         kernels.window_attention(q, q, q, 2, (8, 8), 0.2, out=torch.empty(4, 64, 64, device=dev))
