@@ -350,7 +350,7 @@ def main():
             mlp_fused = mlp._fusable(y_blk)
             if args.config == "c3" and not mlp_fused:
                 raise RuntimeError("the fused MLP kernel does not serve this configuration")
-        if mlp_fused:  # bf16 with C = 192 or 384; other shapes run torch's sequence only
+        if mlp_fused:  # bf16 with C in {128, 192, 384, 768}; other shapes run torch's sequence only
             last_call["mlp"] = (kernels.swin_mlp, (y_blk,), dict(out=torch.empty_like(y_blk), **mlp._fused_args()))
             iso["mlp"] = isolated_us("mlp")
         mlp.use_fused_mlp = False
@@ -501,8 +501,9 @@ def main():
     t_attn_half = t_blk if fused else ms * 1e3
     if mlp_fused:
         res["mlp_half"] = {
-            "kernel": (f"swin_mlp_kernel<{C}, {'true' if C <= 192 else 'false'}> (LayerNorm + fc1 + exact GELU + fc2 "
-                       "+ residual, hidden layer on chip)"),
+            "kernel": ((f"swin_mlp_wide_kernel<{C}>" if C in (128, 768) else
+                        f"swin_mlp_kernel<{C}, {'true' if C <= 192 else 'false'}>")
+                       + " (LayerNorm + fc1 + exact GELU + fc2 + residual, hidden layer on chip)"),
             "us": iso["mlp"],
             "TFLOP_s": mlp_flops / (iso["mlp"] * 1e-6) / 1e12,
             "mfma_frac": mlp_flops / (iso["mlp"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,

@@ -154,7 +154,7 @@ typedef struct terra_swin_block_desc {
 /* Description of one fused MLP half-block call (terra_swin_mlp_fwd). */
 typedef struct terra_swin_mlp_desc {
   int32_t tokens;     /* rows of x (any count; B*H*W for a [B, H, W, C] grid) */
-  int32_t channels;   /* C: 192 or 384                                     */
+  int32_t channels;   /* C: 128, 192, 384 or 768                           */
   int32_t hidden;     /* fc1 out features: 4 * C (mlp_ratio 4)             */
   int32_t layernorm;  /* 1: norm2 = LayerNorm(gamma, beta); 0: none        */
   float ln_eps;       /* LayerNorm eps                                     */

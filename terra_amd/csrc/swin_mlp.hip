@@ -499,6 +499,428 @@ __global__ __launch_bounds__(kMlpThreads) void swin_mlp_kernel(const MlpParams p
   }
 }
 
+// ============================================================================
+// swin_mlp_wide_kernel: the same MLP half for C = 128 (c2) and C = 768 (the
+// reference model's C, c4).
+// ============================================================================
+//
+// The same per-tile scheme as swin_mlp_kernel (64-token tiles, LayerNorm
+// tile, hidden chunks of 32 features per wave on chip, fc2 accumulators
+// across the chunks), sized for these widths:
+//   C = 128: 8 waves, hidden chunks of 256 (two per tile), fc2 split in two
+//            along k (as C = 192), raw rows double-buffered in LDS;
+//   C = 768: 8 waves, hidden chunks of 256 (twelve per tile), each wave owns
+//            96 fc2 output features (no k split).  The raw rows land in the
+//            LayerNorm tile and are normalised in place (a 96 KB tile; a
+//            second one does not fit beside the hidden chunk), the residual
+//            is read back from global memory in the epilogue, and the output
+//            rows are staged in the same tile for whole-line stores.
+// Row pitches here are multiples of 256 bytes (a whole bank period), so a
+// 16-byte chunk c of row r sits in slot r * pitch + (c ^ (r & 15)) (XOR
+// within aligned groups of 16 chunks): the 16 rows of a fragment read land
+// on 16 different 16-byte bank groups.  The affine parameters and biases are
+// read from global memory (L1-resident).
+
+template <int C>
+struct WideShape {
+  static constexpr int kWaves = 8;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int H = 4 * C;
+  static constexpr int kCpr = C / 8;                  // 16-byte chunks per x row
+  static constexpr int kHC = 32 * kWaves;             // hidden features per chunk
+  static constexpr int kHCpr = kHC / 8;               // chunks per hidden row
+  static constexpr int kChunks = H / kHC;
+  static constexpr int kNF = C / 32;                  // fc2 feature groups of 32
+  static constexpr int kFPW = kNF >= kWaves ? kNF / kWaves : 1;  // groups per wave
+  static constexpr int kKS = kNF >= kWaves ? 1 : kWaves / kNF;   // fc2 k split
+  static constexpr int kKR = kHC / kKS;               // fc2 k range per wave and chunk
+  static constexpr bool kRaw = C <= 384;              // raw rows in LDS (double-buffered)
+  static constexpr int kTile = 64 * C * 2;
+  static constexpr int kHid = 64 * kHC * 2;
+  static constexpr int kLds = kGeluBytes + (kRaw ? 3 : 1) * kTile + kHid;
+  static_assert(kChunks * kHC == H && kKS * kKR == kHC && kKS <= 2, "chunking");
+  static_assert(kFPW * kWaves * (kKS == 1 ? 1 : 0) + (kKS == 2 ? kNF * 2 : 0) == (kKS == 1 ? kNF : kWaves),
+                "fc2 split");
+  static_assert(kCpr % 16 == 0 && kHCpr % 16 == 0, "256-byte row pitches");
+  static_assert(kKS == 1 || 64 * C * 4 <= kHid, "the fc2 reduction reuses the hidden chunk");
+  static_assert(kLds <= 160 * 1024, "LDS");
+};
+
+template <int kPitch>
+__device__ __forceinline__ int wide_slot(int row, int chunk) {
+  return row * kPitch + (chunk ^ (row & 15));
+}
+
+// Rows [64 t, +64) of x -> LDS tile (wide_slot layout), direct global->LDS;
+// rows past the end load row 0 (never stored).
+template <int C>
+__device__ __forceinline__ void wide_fetch(const MlpParams& p, int t, uint8_t* dst, int wave, int lane) {
+  using S = WideShape<C>;
+  constexpr int kRounds = S::kCpr * 64 / (64 * S::kWaves);
+  static_assert(kRounds * S::kWaves == S::kCpr, "whole wave-rounds");
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int blk = r * S::kWaves + wave;
+    const int sl = blk * 64 + lane;
+    const int row = sl / S::kCpr;
+    const int ch = (sl - row * S::kCpr) ^ (row & 15);
+    const int tok = t * 64 + row;
+    const uint8_t* src = p.x + ((int64_t)(tok < p.tokens ? tok : 0) * S::kCpr + ch) * 16;
+    dma_to_lds16(src, __builtin_amdgcn_readfirstlane(lds_address(dst + blk * 1024)));
+  }
+}
+
+template <int C>
+__device__ __forceinline__ void wide_store(const MlpParams& p, int t, const uint8_t* xr, int tid) {
+  using S = WideShape<C>;
+  constexpr int kPasses = 64 * S::kCpr / S::kThreads;
+  static_assert(kPasses * S::kThreads == 64 * S::kCpr, "whole passes");
+  const int64_t first = (int64_t)t * 64;
+  const int rows = p.tokens - (int)first < 64 ? p.tokens - (int)first : 64;
+  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(p.y + first * S::kCpr * 16, (uint32_t)(rows * S::kCpr * 16));
+#pragma unroll
+  for (int r = 0; r < kPasses; ++r) {
+    const int q = r * S::kThreads + tid;  // consecutive lanes, consecutive chunks of the tile's rows
+    const int row = q / S::kCpr, ch = q - row * S::kCpr;
+    const u32x4 val =
+        __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(xr + wide_slot<S::kCpr>(row, ch) * 16));
+    stream_store_sc1(val, out, (uint32_t)q * 16);  // rows past the end fall outside the range
+  }
+}
+
+// LayerNorm of the tile's raw rows (xr) into xn (may be xr: in place, each
+// lane rewriting only the chunks it read).  Eight lanes per token; two-pass
+// fp32 statistics, values re-read from LDS for each pass; without LayerNorm
+// the identity.
+template <int C>
+__device__ __forceinline__ void wide_layernorm(const MlpParams& p, const uint8_t* xr, uint8_t* xn, int tid) {
+  using S = WideShape<C>;
+  constexpr int kCPL = S::kCpr / 8;
+  const int sub = tid & 7;
+  const float* gptr = p.layernorm ? p.gamma : nullptr;
+  const float* bptr = p.layernorm ? p.beta : nullptr;
+  asm volatile("" : "+s"(gptr), "+s"(bptr));  // read per tile, not held in registers
+  auto chunk = [&](int t, int k, float (&v)[8]) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(xr + wide_slot<S::kCpr>(t, sub + 8 * k) * 16);
+    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
+      v[2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
+    }
+  };
+  for (int t = tid >> 3; t < 64; t += S::kThreads / 8) {  // uniform per wave
+    float mean = 0.f, rstd = 1.f;
+    if (p.layernorm) {
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k) {
+        float v[8];
+        chunk(t, k, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += v[e];
+      }
+      mean = group8_sum(sum) * p.inv_c;
+      float sq = 0.f;
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k) {
+        float v[8];
+        chunk(t, k, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[e] - mean;
+          sq += d * d;
+        }
+      }
+      rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      float v[8];
+      chunk(t, k, v);
+      const int c0 = (sub + 8 * k) * 8;
+      float yv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 gq = gptr != nullptr ? *reinterpret_cast<const f32x4*>(gptr + c0 + 4 * h) : f32x4{1.f, 1.f, 1.f, 1.f};
+        const f32x4 bq = bptr != nullptr ? *reinterpret_cast<const f32x4*>(bptr + c0 + 4 * h) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yv[4 * h + e] = (v[4 * h + e] - mean) * rstd * gq[e] + bq[e];
+      }
+      *reinterpret_cast<uint4*>(xn + wide_slot<S::kCpr>(t, sub + 8 * k) * 16) =
+          make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
+                     pack_bf16x2(yv[6], yv[7]));
+    }
+  }
+}
+
+template <int C>
+__global__ __launch_bounds__(WideShape<C>::kThreads) void swin_mlp_wide_kernel(const MlpParams p) {
+  using S = WideShape<C>;
+  constexpr int H = S::H, kCpr = S::kCpr, kHCpr = S::kHCpr;
+  constexpr int kSteps1 = C / 32;          // fc1 k-steps
+  constexpr int kSteps2 = S::kKR / 32;     // fc2 k-steps per chunk
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint16_t* s_gelu = reinterpret_cast<uint16_t*>(smem);
+  uint8_t* tiles = smem + kGeluBytes;
+  uint8_t* xbuf = tiles;                                        // raw rows (kRaw: two tiles)
+  uint8_t* xn = S::kRaw ? tiles + 2 * S::kTile : tiles;         // LayerNorm tile (kRaw off: also the raw rows)
+  uint8_t* hb = xn + S::kTile;                                  // hidden chunk [64][kHC] bf16
+
+  const int tid0 = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  if ((int)blockIdx.x >= p.tiles) return;  // uniform
+  for (int e = tid0; e < 2 * kGeluSpan; e += S::kThreads) {
+    const uint32_t sign = e >= kGeluSpan ? 0x8000u : 0u;
+    const uint32_t bits = sign | (kGeluLo + (uint32_t)(e - (sign ? kGeluSpan : 0)));
+    const float xv = bf16_bits_to_f32((uint16_t)bits);
+    s_gelu[e] = f32_to_bf16_bits(xv * 0.5f * (1.f + erff(xv * 0.70710678118654752f)));
+  }
+  const int fr = S::kKS == 1 ? wave : wave % S::kNF;  // fc2 feature groups fr * kFPW + f
+  const int kh = S::kKS == 1 ? 0 : wave / S::kNF;     // fc2 k part
+  const __amdgpu_buffer_rsrc_t w1r = buffer_rsrc(p.w1, (uint32_t)(H * C * 2));
+  const __amdgpu_buffer_rsrc_t w2r = buffer_rsrc(p.w2, (uint32_t)(H * C * 2));
+
+  int t = blockIdx.x, prev = -1, par = 0;
+  wide_fetch<C>(p, t, S::kRaw ? xbuf : xn, wave, tid0 & 63);
+  for (;;) {
+    // Lane-derived addresses are recomputed per tile (the thread id passes
+    // through an empty asm) rather than hoisted and held across the loop.
+    int tid = tid0;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
+    const int g = lane >> 4, c16 = lane & 15;
+    // Per-lane bases of fragment reads: chunk 16 a + 4 b + g of row 16 tt + c16
+    // is at fa(b) + 256 a + tt * 16 * pitch * 16 (wide_slot with row & 15 = c16).
+    auto fa = [&](int pitch, int b) { return (uint32_t)((c16 * pitch + ((4 * b + g) ^ c16)) * 16); };
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile's rows have landed
+    lds_barrier();
+    uint8_t* xr = S::kRaw ? xbuf + par * S::kTile : xn;
+    const int next = t + (int)gridDim.x;
+    if constexpr (S::kRaw) {
+      if (prev >= 0) wide_store<C>(p, prev, xbuf + (par ^ 1) * S::kTile, tid);  // the previous tile's rows
+    }
+    wide_layernorm<C>(p, xr, xn, tid);
+    lds_barrier();  // xn complete
+
+    f32x4 acc2[S::kFPW][2][4];
+#pragma unroll
+    for (int f = 0; f < S::kFPW; ++f)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int fb = 32 * (fr * S::kFPW + f) + 16 * i + 4 * g;
+        const f32x4 b = (kh == 0 && p.b2 != nullptr) ? *reinterpret_cast<const f32x4*>(p.b2 + fb)
+                                                      : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc2[f][i][tt] = b;
+      }
+    for (int chk = 0; chk < S::kChunks; ++chk) {
+      // ---- fc1 + bias: hidden [chk kHC + 32 wave, +32) x 64 tokens ----------
+      const int rt1 = chk * (S::kHC / 16) + 2 * wave;
+      f32x4 acc1[2][4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const f32x4 b = p.b1 != nullptr ? *reinterpret_cast<const f32x4*>(p.b1 + 16 * (rt1 + i) + 4 * g)
+                                         : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc1[i][tt] = b;
+      }
+      {
+        uint4 wf[3][2];  // weight ring: step ks in slot ks % 3, loaded two steps ahead
+#pragma unroll
+        for (int s0 = 0; s0 < 2; ++s0)
+#pragma unroll
+          for (int i = 0; i < 2; ++i) wf[s0][i] = packed_frag<C>(w1r, rt1 + i, s0, lane);
+#pragma unroll
+        for (int ks = 0; ks < kSteps1; ++ks) {
+          if (ks + 2 < kSteps1) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) wf[(ks + 2) % 3][i] = packed_frag<C>(w1r, rt1 + i, ks + 2, lane);
+          }
+          asm volatile("" ::: "memory");  // keeps the weight loads two steps ahead
+          uint4 xf[4];
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            xf[tt] = *reinterpret_cast<const uint4*>(xn + fa(kCpr, ks & 3) + (ks >> 2) * 256 + tt * (16 * kCpr * 16));
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+              acc1[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[ks % 3][i]),
+                                                                    __builtin_bit_cast(bf16x8, xf[tt]), acc1[i][tt],
+                                                                    0, 0, 0);
+        }
+      }
+      if constexpr (S::kRaw) {
+        // The next tile's rows stream in under the GELU epilogue.
+        if (chk == 0 && next < p.tiles) wide_fetch<C>(p, next, xbuf + (par ^ 1) * S::kTile, wave, lane);
+      }
+      // ---- bf16 -> GELU -> bf16 into the hidden chunk -------------------------
+      {
+        uint32_t hp[2][4][2], gp[2][4][2];
+        u16x2 dmax = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+            hp[i][tt][0] = pack_bf16x2(acc1[i][tt][0], acc1[i][tt][1]);
+            hp[i][tt][1] = pack_bf16x2(acc1[i][tt][2], acc1[i][tt][3]);
+            asm volatile("" : "+v"(hp[i][tt][0]), "+v"(hp[i][tt][1]));
+            gp[i][tt][0] = gelu_pair_table(hp[i][tt][0], s_gelu, dmax);
+            gp[i][tt][1] = gelu_pair_table(hp[i][tt][1], s_gelu, dmax);
+          }
+        const uint32_t dm = dmax.x > dmax.y ? dmax.x : dmax.y;
+        if (__builtin_amdgcn_ballot_w64(dm >= (uint32_t)kGeluSpan) != 0) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+              for (int q = 0; q < 2; ++q)
+                gp[i][tt][q] = gelu_bf16(hp[i][tt][q] & 0xffffu, s_gelu) | (gelu_bf16(hp[i][tt][q] >> 16, s_gelu) << 16);
+        }
+        // lane (c16, g) of (i, tt): hidden 32 wave + 16 i + 4 g .. + 3 of token 16 tt + c16
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+            const int row = 16 * tt + c16;
+            const int ch = (32 * wave + 16 * i + 4 * g) >> 3;
+            *reinterpret_cast<uint2*>(hb + wide_slot<kHCpr>(row, ch) * 16 + (g & 1) * 8) =
+                make_uint2(gp[i][tt][0], gp[i][tt][1]);
+          }
+      }
+      lds_barrier();  // hidden chunk complete
+      // ---- fc2 partial: feature groups fr kFPW + f, hidden [kh kKR, +kKR) of the chunk ----
+      {
+        const int ks0 = (chk * S::kHC + kh * S::kKR) / 32;
+        uint4 wf[3][S::kFPW][2];
+#pragma unroll
+        for (int s0 = 0; s0 < 2; ++s0)
+#pragma unroll
+          for (int f = 0; f < S::kFPW; ++f)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) wf[s0][f][i] = packed_frag<H>(w2r, 2 * (fr * S::kFPW + f) + i, ks0 + s0, lane);
+#pragma unroll
+        for (int s = 0; s < kSteps2; ++s) {
+          if (s + 2 < kSteps2) {
+#pragma unroll
+            for (int f = 0; f < S::kFPW; ++f)
+#pragma unroll
+              for (int i = 0; i < 2; ++i)
+                wf[(s + 2) % 3][f][i] = packed_frag<H>(w2r, 2 * (fr * S::kFPW + f) + i, ks0 + s + 2, lane);
+          }
+          asm volatile("" ::: "memory");
+          const int kc = (kh * S::kKR) / 8 + 4 * s;  // first chunk of this k-step within the hidden row
+          uint4 hf[4];
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            hf[tt] = *reinterpret_cast<const uint4*>(hb + fa(kHCpr, (kc >> 2) & 3) + (kc >> 4) * 256 +
+                                                     tt * (16 * kHCpr * 16));
+#pragma unroll
+          for (int f = 0; f < S::kFPW; ++f)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+              for (int tt = 0; tt < 4; ++tt)
+                acc2[f][i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, wf[s % 3][f][i]), __builtin_bit_cast(bf16x8, hf[tt]), acc2[f][i][tt],
+                    0, 0, 0);
+        }
+      }
+      lds_barrier();  // the chunk is consumed before the next one overwrites it
+    }
+
+    // ---- fc2 k-split reduction (C = 128), + residual -------------------------
+    // lane (c16, g) of (f, i, tt): features 32 (fr kFPW + f) + 16 i + 4 g + r of token 16 tt + c16.
+    if constexpr (S::kKS == 2) {
+      float* red = reinterpret_cast<float*>(hb);  // [64][C] fp32, 16-byte chunks XOR-swizzled by c16
+      const int rc = ((8 * fr + g) ^ c16);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          if ((tt >> 1) != kh) *reinterpret_cast<f32x4*>(red + (16 * tt + c16) * C + 4 * (rc ^ (4 * i))) = acc2[0][i][tt];
+      lds_barrier();
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          if ((tt >> 1) == kh)
+            acc2[0][i][tt] += *reinterpret_cast<const f32x4*>(red + (16 * tt + c16) * C + 4 * (rc ^ (4 * i)));
+    }
+    const __amdgpu_buffer_rsrc_t xres =
+        buffer_rsrc(p.x + (int64_t)t * 64 * C * 2,
+                    (uint32_t)((p.tokens - t * 64 < 64 ? p.tokens - t * 64 : 64) * C * 2));
+#pragma unroll
+    for (int f = 0; f < S::kFPW; ++f)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          if (S::kKS == 2 && (tt >> 1) != kh) continue;
+          const int row = 16 * tt + c16;
+          const int fb = 32 * (fr * S::kFPW + f) + 16 * i + 4 * g;
+          uint8_t* addr = xr + wide_slot<kCpr>(row, fb >> 3) * 16 + (fb & 7) * 2;
+          uint2 xv;
+          if constexpr (S::kRaw) {
+            xv = *reinterpret_cast<const uint2*>(addr);
+          } else {  // from global memory (rows past the end read 0 and are not stored)
+            const stream_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(xres, (uint32_t)(row * C + fb) * 2, 0, 0);
+            xv = make_uint2(v[0], v[1]);
+          }
+          const f32x4& a = acc2[f][i][tt];
+          uint2 out;
+          out.x = pack_bf16x2(bf16_bits_to_f32((uint16_t)(xv.x & 0xffffu)) + (float)(__bf16)a[0],
+                              bf16_bits_to_f32((uint16_t)(xv.x >> 16)) + (float)(__bf16)a[1]);
+          out.y = pack_bf16x2(bf16_bits_to_f32((uint16_t)(xv.y & 0xffffu)) + (float)(__bf16)a[2],
+                              bf16_bits_to_f32((uint16_t)(xv.y >> 16)) + (float)(__bf16)a[3]);
+          *reinterpret_cast<uint2*>(addr) = out;
+        }
+    if constexpr (!S::kRaw) {
+      lds_barrier();                                 // output rows complete
+      wide_store<C>(p, t, xr, tid);
+      if (next >= p.tiles) break;
+      lds_barrier();                                 // the rows are read out before the next load
+      wide_fetch<C>(p, next, xn, wave, lane);
+      t = next;
+    } else {
+      prev = t;
+      if (next >= p.tiles) {
+        lds_barrier();                               // output rows complete
+        wide_store<C>(p, t, xr, tid);
+        break;
+      }
+      t = next;
+      par ^= 1;
+    }
+  }
+}
+
+template <int C>
+int launch_mlp_wide(const MlpParams& p, hipStream_t s) {
+  using S = WideShape<C>;
+  auto kern = swin_mlp_wide_kernel<C>;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  constexpr int kMaxDevices = 64;
+  static int cache[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(TERRA_ERR_LAUNCH, "cannot query the current device");
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, S::kThreads, S::kLds) != hipSuccess)
+      return fail(TERRA_ERR_LAUNCH, "cannot size the MLP grid for this device");
+    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  const int blocks = p.tiles < cache[dev] ? p.tiles : cache[dev];
+  kern<<<blocks, S::kThreads, S::kLds, s>>>(p);
+  return TERRA_OK;
+}
+
 template <int C, bool kDB>
 int launch_mlp(const MlpParams& p, hipStream_t s) {
   constexpr int lds = mlp_lds_bytes<C, kDB>();
@@ -546,8 +968,8 @@ extern "C" int terra_swin_mlp_fwd(const void* x, void* y, int dtype, const terra
   if (dtype != TERRA_DTYPE_BF16) return fail(TERRA_ERR_UNSUPPORTED, "the fused MLP is built for bf16 activations");
   const terra_swin_mlp_desc& d = *desc;
   if (d.tokens <= 0) return fail(TERRA_ERR_SHAPE, "tokens must be positive");
-  if (d.channels != 192 && d.channels != 384)
-    return fail(TERRA_ERR_UNSUPPORTED, "channels %d not in {192, 384}", d.channels);
+  if (d.channels != 128 && d.channels != 192 && d.channels != 384 && d.channels != 768)
+    return fail(TERRA_ERR_UNSUPPORTED, "channels %d not in {128, 192, 384, 768}", d.channels);
   if (d.hidden != 4 * d.channels)
     return fail(TERRA_ERR_UNSUPPORTED, "hidden %d != 4 * channels (%d)", d.hidden, 4 * d.channels);
   if (!(d.ln_eps >= 0.f)) return fail(TERRA_ERR_SHAPE, "ln_eps must be >= 0");
@@ -574,7 +996,13 @@ extern "C" int terra_swin_mlp_fwd(const void* x, void* y, int dtype, const terra
   p.tiles = (d.tokens + 63) / 64;
   p.layernorm = d.layernorm != 0;
   hipStream_t s = (hipStream_t)stream;
-  const int st = d.channels == 192 ? launch_mlp<192, true>(p, s) : launch_mlp<384, false>(p, s);
+  int st;
+  switch (d.channels) {
+    case 128: st = launch_mlp_wide<128>(p, s); break;
+    case 192: st = launch_mlp<192, true>(p, s); break;
+    case 384: st = launch_mlp<384, false>(p, s); break;
+    default: st = launch_mlp_wide<768>(p, s); break;
+  }
   if (st != TERRA_OK) return st;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "terra_swin_mlp_fwd launch failed: %s", hipGetErrorString(e));

@@ -522,12 +522,13 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
     return out
 
 
-MLP_CHANNELS = (192, 384)
+MLP_CHANNELS = (128, 192, 384, 768)
 
 
 def swin_mlp_supported(x: torch.Tensor, channels: int, hidden: int) -> bool:
     """Whether :func:`swin_mlp` serves this call (bf16 device tensor,
-    C in {192, 384}, hidden = 4 C)."""
+    C in {128, 192, 384, 768}: the widths of the benchmark configurations,
+    hidden = 4 C)."""
     return (x.device.type == "cuda" and x.dtype == torch.bfloat16 and channels in MLP_CHANNELS
             and hidden == 4 * channels)
 

@@ -1,7 +1,7 @@
 """Drop-in ``SequentialMlp`` (models/mlp.py:138-172), the MLP half of a Swin
 block: ``x + fc2(GELU(fc1(norm2(x))))`` per token.
 
-For bf16 activations with C in {192, 384} and hidden = 4C, the forward is one
+For bf16 activations with C in {128, 192, 384, 768} and hidden = 4C, the forward is one
 HIP kernel (``kernels.swin_mlp``): LayerNorm, fc1 on MFMA, exact GELU, fc2 on
 MFMA and the residual add, with the hidden layer kept on chip.  The module
 packs ``fc1.weight`` / ``fc2.weight`` with ``kernels.pack_linear`` and caches
@@ -46,7 +46,7 @@ class SequentialMlp(torch.nn.Module):
         self.use_fused_mlp = True
 
     def _fusable(self, x: torch.Tensor) -> bool:
-        """One kernel serves the call: bf16 rows of C in {192, 384}, hidden
+        """One kernel serves the call: bf16 rows of C in {128, 192, 384, 768}, hidden
         4C, out C, the exact GELU, a plain LayerNorm over C (or none), biased
         linears of the activation dtype, and no gradient needed."""
         if not self.use_fused_mlp or x.dim() < 1:

@@ -296,7 +296,7 @@ def _mlp_call(d, dtype=L.DTYPE_BF16, x=FAKE, y=ctypes.c_void_p(1 << 24), w1=FAKE
 @pytest.mark.parametrize("kw,dtype,code,text", [
     ({}, L.DTYPE_F32, -5, "bf16 activations"),
     ({}, 9, -2, "unknown dtype"),
-    ({"channels": 256, "hidden": 1024}, L.DTYPE_BF16, -5, "not in {192, 384}"),
+    ({"channels": 256, "hidden": 1024}, L.DTYPE_BF16, -5, "not in {128, 192, 384, 768}"),
     ({"hidden": 576}, L.DTYPE_BF16, -5, "4 * channels"),
     ({"tokens": 0}, L.DTYPE_BF16, -3, "tokens must be positive"),
     ({"ln_eps": -1.0}, L.DTYPE_BF16, -3, "ln_eps"),

@@ -55,7 +55,7 @@ def _check(y, x, ref):
     assert (y == ref).double().mean().item() >= 0.9
 
 
-@pytest.mark.parametrize("C", [192, 384])
+@pytest.mark.parametrize("C", [128, 192, 384, 768])
 @pytest.mark.parametrize("ln", [True, False])
 @pytest.mark.parametrize("tokens", [1, 63, 1000])
 def test_mlp_kernel_matches_oracle(dev, C, ln, tokens):
@@ -66,11 +66,13 @@ def test_mlp_kernel_matches_oracle(dev, C, ln, tokens):
     _check(y, x, ref)
 
 
-@pytest.mark.parametrize("C,tokens", [(192, 256 * 64 * 3 + 37), (384, 256 * 64 * 2 + 5)])
+@pytest.mark.parametrize("C,tokens", [(192, 256 * 64 * 3 + 37), (384, 256 * 64 * 2 + 5), (128, 256 * 64 * 3 + 37),
+                                      (768, 256 * 64 * 2 + 5)])
 def test_mlp_kernel_many_tiles_per_workgroup(dev, C, tokens):
     """Several 64-token tiles per persistent workgroup (double-buffered rows
-    for C = 192) and a ragged last tile: sampled rows against the oracle, and
-    every sampled row bit-equal to a launch over the sampled rows alone."""
+    for C = 128 and 192; for C = 768 the rows share the LayerNorm tile) and a
+    ragged last tile: sampled rows against the oracle, and every sampled row
+    bit-equal to a launch over the sampled rows alone."""
     p = _params(C, 21 + C)
     x = workloads.activations((tokens, C), 23, torch.bfloat16)
     xd = x.to(dev)
@@ -83,9 +85,11 @@ def test_mlp_kernel_many_tiles_per_workgroup(dev, C, tokens):
     assert torch.equal(y_rows.cpu(), y.cpu()[idx])
 
 
-def test_mlp_kernel_c3_size_row_independence(dev):
-    """The c3 grid (512 x 1024 tokens, C = 192), as the bench runs it."""
-    cfg = workloads.CONFIGS["c3"]
+@pytest.mark.parametrize("name", ["c2", "c3", "c4"])
+def test_mlp_kernel_config_size_row_independence(dev, name):
+    """The token grids of c2 (C = 128), c3 (C = 192) and c4 (C = 768) at full
+    size, as the bench runs them."""
+    cfg = workloads.CONFIGS[name]
     C = cfg.channels
     tokens = cfg.batch * cfg.height * cfg.width
     p = _params(C, 31)
@@ -96,8 +100,9 @@ def test_mlp_kernel_c3_size_row_independence(dev):
     assert torch.equal(_run(x[idx].contiguous(), p, dev), y[idx])
 
 
-def test_mlp_kernel_in_place(dev):
-    C, tokens = 192, 777
+@pytest.mark.parametrize("C", [192, 768])
+def test_mlp_kernel_in_place(dev, C):
+    tokens = 777
     p = _params(C, 41)
     x = workloads.activations((tokens, C), 43, torch.bfloat16).to(dev)
     y = _run(x, p, dev)
@@ -107,7 +112,7 @@ def test_mlp_kernel_in_place(dev):
     assert torch.equal(x2, y)
 
 
-@pytest.mark.parametrize("C", [192, 384])
+@pytest.mark.parametrize("C", [128, 192, 384, 768])
 def test_gelu_table_every_finite_bf16_input(dev, C):
     """fc1 = [I; 0] and fc2 = [I, 0] without LayerNorm make the MLP
     y = bf16(x + GELU(x)) exactly (one unit product per accumulation), so
@@ -166,7 +171,7 @@ def test_gelu_table_special_values(dev):
     assert torch.equal(y[0], ref0)
 
 
-@pytest.mark.parametrize("C", [192, 384])
+@pytest.mark.parametrize("C", [128, 192, 384, 768])
 def test_module_fused_matches_torch_bf16_module(dev, C):
     """SequentialMlp's kernel path against the same module run as the
     reference's torch sequence in bf16 on the GPU (use_fused_mlp = False),
@@ -208,11 +213,11 @@ def test_module_caches_packed_weights_until_a_parameter_changes(dev):
 
 
 def test_module_unsupported_shapes_run_the_torch_sequence(dev):
-    """C = 128 (c2) and fp32 activations are outside the kernel: the module
-    runs norm2 / fc1 / GELU / fc2 / + x as torch ops (the reference's
-    sequence), and gradients flow through it."""
-    m = SequentialMlp(128, 512).to(dev)
-    x = workloads.activations((2, 49, 128), 81).to(dev).requires_grad_(True)
+    """fp32 activations (c1) are outside the kernel: the module runs norm2 /
+    fc1 / GELU / fc2 / + x as torch ops (the reference's sequence), and
+    gradients flow through it."""
+    m = SequentialMlp(96, 384).to(dev)
+    x = workloads.activations((2, 49, 96), 81).to(dev).requires_grad_(True)
     y = m(x)
     ref = so.mlp(x.detach().cpu(), {k: v.cpu() for k, v in m.state_dict().items()})
     assert torch.allclose(y.detach().cpu(), ref, rtol=1e-4, atol=1e-4)
