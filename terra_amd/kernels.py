@@ -122,6 +122,14 @@ class WindowMask:
     land_bits: Optional[torch.Tensor] = None
 
 
+def autocast_bf16(x: torch.Tensor) -> bool:
+    """Whether a bf16 autocast region is active for x's device type: there
+    F.linear casts fp32 weights to bf16 (core/runtime/run_model.py:424-448
+    runs the reference's forward under torch.amp.autocast("cuda", bf16))."""
+    dt = x.device.type
+    return torch.is_autocast_enabled(dt) and torch.get_autocast_dtype(dt) == torch.bfloat16
+
+
 def _require_device(*tensors: torch.Tensor) -> torch.device:
     dev = tensors[0].device
     for t in tensors:

@@ -48,7 +48,8 @@ class SequentialMlp(torch.nn.Module):
     def _fusable(self, x: torch.Tensor) -> bool:
         """One kernel serves the call: bf16 rows of C in {128, 192, 384, 768}, hidden
         4C, out C, the exact GELU, a plain LayerNorm over C (or none), biased
-        linears of the activation dtype, and no gradient needed."""
+        linears of the activation dtype (or fp32 under bf16 autocast), and no
+        gradient needed."""
         if not self.use_fused_mlp or x.dim() < 1:
             return False
         C = x.shape[-1]
@@ -63,22 +64,26 @@ class SequentialMlp(torch.nn.Module):
                 return False
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
-        return all(l.weight.dtype == x.dtype and l.bias is not None for l in (fc1, fc2))
+        # Weights of the activation dtype, or fp32 weights inside a bf16
+        # autocast region (where F.linear would cast them to bf16).
+        w_ok = all(l.weight.dtype == x.dtype for l in (fc1, fc2)) or (
+            kernels.autocast_bf16(x) and all(l.weight.dtype == torch.float32 for l in (fc1, fc2)))
+        return w_ok and all(l.bias is not None for l in (fc1, fc2))
 
     def _fused_args(self) -> dict:
         tensors = [self.fc1.weight, self.fc1.bias, self.fc2.weight, self.fc2.bias]
         if config.use_layernorm:
             tensors += [self.norm2.weight, self.norm2.bias]
-        key = tuple((t.data_ptr(), t._version, t.device) if t is not None else None for t in tensors)
+        key = tuple((t.data_ptr(), t._version, t.device, t.dtype) if t is not None else None for t in tensors)
         cached = getattr(self, "_fused_cache", None)
         if cached is not None and cached[0] == key:
             return cached[1]
         with torch.no_grad():
             f32 = lambda t: None if t is None else t.detach().to(torch.float32).contiguous()  # noqa: E731
             args = dict(
-                fc1_weight=kernels.pack_linear(self.fc1.weight.detach().contiguous()),
+                fc1_weight=kernels.pack_linear(self.fc1.weight.detach().to(torch.bfloat16).contiguous()),
                 fc1_bias=f32(self.fc1.bias),
-                fc2_weight=kernels.pack_linear(self.fc2.weight.detach().contiguous()),
+                fc2_weight=kernels.pack_linear(self.fc2.weight.detach().to(torch.bfloat16).contiguous()),
                 fc2_bias=f32(self.fc2.bias),
                 ln_weight=f32(self.norm2.weight) if config.use_layernorm else None,
                 ln_bias=f32(self.norm2.bias) if config.use_layernorm else None,

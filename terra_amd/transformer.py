@@ -123,12 +123,17 @@ class SequentialSwinTransformer(torch.nn.Module):
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
         lins = (attn.q_linear, attn.k_linear, attn.v_linear, attn.proj)
-        return all(l.weight.dtype == x.dtype for l in lins) and attn.q_linear.bias is not None
+        # Weights of the activation dtype, or fp32 weights inside a bf16
+        # autocast region (where F.linear would cast them to bf16).
+        w_ok = all(l.weight.dtype == x.dtype for l in lins) or (
+            kernels.autocast_bf16(x) and all(l.weight.dtype == torch.float32 for l in lins))
+        return w_ok and attn.q_linear.bias is not None
 
     def _fused_args(self) -> dict:
-        """Fragment-packed q|k|v and proj weights and fp32 copies of the small
-        parameters, cached until any of them changes (data pointer or in-place
-        version)."""
+        """Fragment-packed bf16 q|k|v and proj weights (cast from fp32 weights
+        under autocast, as F.linear would) and fp32 copies of the small
+        parameters, cached until any of them changes (data pointer, in-place
+        version or dtype)."""
         attn = self.attn
         tensors = [attn.q_linear.weight, attn.k_linear.weight, attn.v_linear.weight, attn.q_linear.bias,
                    attn.k_linear.bias, attn.v_linear.bias, attn.proj.weight, attn.proj.bias]
@@ -136,17 +141,18 @@ class SequentialSwinTransformer(torch.nn.Module):
             tensors += [self.norm1.weight, self.norm1.bias]
         if attn.use_relative_position_bias:
             tensors.append(attn.relative_position_bias_table)
-        key = tuple((t.data_ptr(), t._version, t.device) if t is not None else None for t in tensors)
+        key = tuple((t.data_ptr(), t._version, t.device, t.dtype) if t is not None else None for t in tensors)
         cached = getattr(self, "_fused_cache", None)
         if cached is not None and cached[0] == key:
             return cached[1]
         with torch.no_grad():
             f32 = lambda t: None if t is None else t.detach().to(torch.float32).contiguous()  # noqa: E731
-            w_qkv = torch.cat([attn.q_linear.weight, attn.k_linear.weight, attn.v_linear.weight], 0).detach()
+            bf16 = lambda t: t.detach().to(torch.bfloat16).contiguous()  # noqa: E731
+            w_qkv = torch.cat([bf16(attn.q_linear.weight), bf16(attn.k_linear.weight), bf16(attn.v_linear.weight)], 0)
             args = dict(
                 qkv_weight=kernels.pack_linear(w_qkv.contiguous()),
                 qkv_bias=f32(torch.cat([attn.q_linear.bias, attn.k_linear.bias, attn.v_linear.bias], 0)),
-                proj_weight=kernels.pack_linear(attn.proj.weight.detach().contiguous()),
+                proj_weight=kernels.pack_linear(bf16(attn.proj.weight)),
                 packed_weights=True,
                 proj_bias=f32(attn.proj.bias),
                 ln_weight=f32(self.norm1.weight) if config.use_layernorm else None,

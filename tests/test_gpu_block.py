@@ -121,3 +121,36 @@ def test_window_attention_rejects_wrong_out(dev):
     q = workloads.activations((4, 64, 64), 320, torch.bfloat16).to(dev)
     with pytest.raises(ValueError, match="out must be a torch.bfloat16 tensor"):
         kernels.window_attention(q, q, q, 2, (8, 8), 0.2, out=torch.empty(4, 64, 64, device=dev))
+
+
+def test_c4_chain_alternating_blocks_with_mlp(dev):
+    """Four blocks at the reference model's width (C=768, 12 heads of dim 64,
+    window 8): W-MSA and SW-MSA alternating by layer index (shift from
+    models/transformer.py:88), each followed by its MLP half, in the order
+    BasicLayer runs them (models/reference_model/parallel_layers.py:151-153),
+    through the drop-ins (fused MLP kernel, five-stage attention half) against
+    the oracle chain, on a reduced grid."""
+    cfg = workloads.CONFIGS["c4"].scaled(32, 64)
+    dtype = torch.bfloat16
+    layers = []
+    for layer in range(4):
+        layers.append(gain_block(workloads.block_for(cfg, layer), seed=430 + 10 * layer))
+        m = workloads.mlp_for(cfg, layer)
+        with torch.no_grad():
+            m.fc1.weight.mul_(4.0)
+            m.fc2.weight.mul_(4.0)
+        layers.append(m)
+    assert [b.shift_size for b in layers[::2]] == [0, 4, 0, 4]
+    x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 440, dtype)
+    y = x.to(dev)
+    with torch.no_grad():
+        for b in layers:
+            y = b.to(dev).to(dtype)(y)
+    r = x.float()
+    for b in layers:
+        p = params_of(b)
+        if hasattr(b, "fc1"):
+            r = so.mlp(r, p)
+        else:
+            r = so.swin_block_attention(r, cfg.height, cfg.width, cfg.window, b.shift_size, cfg.heads, p)
+    assert_block_matches(y, r.view(cfg.batch, cfg.height * cfg.width, cfg.channels), x, 2e-2, 3e-2)
