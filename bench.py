@@ -389,8 +389,9 @@ def main():
         t_blk = statistics.mean(per_launch)
         blk_tflops = block_flops / (t_blk * 1e-6) / 1e12
         roofline = {
-            "kernel": (f"swin_block_{'pp_' if cfg.heads == 6 else ''}kernel<{cfg.heads}> (fused LN + qkv + window "
-                       "attention + proj + residual, gather/scatter)"),
+            "kernel": (("swin_block_hd64_kernel" if cfg.channels == 768 else
+                        f"swin_block_{'pp_' if cfg.heads == 6 else ''}kernel<{cfg.heads}>") +
+                       " (fused LN + qkv + window attention + proj + residual, gather/scatter)"),
             "bound": "mfma",
             "achieved": blk_tflops,
             "peak": MFMA_BF16_PEAK_TFLOPS,
@@ -478,7 +479,8 @@ def main():
         # dq, dk, dv (7 N C elt per window); FLOPs: S recomputed, dP, dV, dQ,
         # dK (10 N^2 C per window).
         "attention_backward": {
-            "kernel": "window_attn_bwd_kernel<32, 2>",
+            "kernel": ("window_attn_bwd_kernel<64, 1>" if cfg.channels // cfg.heads == 64 else
+                       "window_attn_bwd_kernel<32, 2>"),
             "us": iso["attention_backward"],
             "GB_s": bwd_bytes / (iso["attention_backward"] * 1e-6) / 1e9,
             "hbm_frac": bwd_bytes / (iso["attention_backward"] * 1e-6) / 1e9 / HBM_PEAK_GBS,

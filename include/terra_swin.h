@@ -140,7 +140,7 @@ typedef struct terra_swin_attn_bwd_desc {
  * tokens of x; tokens of windows that are not emitted keep x. */
 typedef struct terra_swin_block_desc {
   terra_swin_geom geom;
-  int32_t heads;        /* C / heads == 32; 6 or 12 heads               */
+  int32_t heads;        /* 6 or 12 heads of dim 32, or 12 of dim 64     */
   float scale;          /* q k^T scale (head_dim^-0.5 in the reference) */
   float ln_eps;         /* LayerNorm eps                                */
   float mask_value;     /* -100.0 in the reference                      */
@@ -241,7 +241,8 @@ int terra_swin_attn_bwd(const void* q, const void* k, const void* v, const void*
                         float* dbias_table, const float* explicit_mask,
                         const uint64_t* land_bits, void* stream);
 
-/* Fused Swin attention half-block (bf16, 8x8 windows, head dim 32).
+/* Fused Swin attention half-block (bf16, 8x8 windows; C = 192 with 6 heads,
+ * C = 384 with 12, or C = 768 with 12 heads of dim 64).
  * Replaces SequentialSwinTransformer.forward   models/transformer.py:142-300:
  *           x = self.norm1(x)                   models/transformer.py:98, 150
  *           roll(-s) + window_partition         models/transformer.py:179-225

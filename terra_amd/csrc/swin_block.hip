@@ -800,6 +800,460 @@ __global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockPara
   }
 }
 
+// ============================================================================
+// swin_block_hd64_kernel: 12 heads of dim 64, C = 768 (the reference model's
+// block, c4).  Eight waves, one window at a time: wave s < 4 owns heads 3s and
+// 3s + 1, wave s + 4 head 3s + 2, so each SIMD (holding waves s and s + 4)
+// does three heads.
+// ============================================================================
+//
+// At C = 768 one [64][C] bf16 tile is 96 KB, so the workgroup keeps a single
+// tile that holds, in turn, the window's raw rows, their LayerNorm (computed
+// in place), the attention output O and the output rows:
+//
+//   rows -> tile (direct global -> LDS), LayerNorm in place      (all waves)
+//   per head: K^T, V, then Q^T from the tile into MFMA operand fragments
+//           (three passes over the 24 k-steps); a two-head wave runs its
+//           first head's attention before its second head's projections
+//           and keeps that O in registers
+//   barrier (every wave has read the LayerNorm tile)
+//   the heads' O into columns [64h, 64h + 64) of the tile (the last head's
+//           attention one query tile at a time)
+//   barrier
+//   wave w: output features [96w, 96w + 96) = O W_p^T + b_p
+//   barrier (every wave has read O)
+//   y = x + proj (the residual x read back from global memory) into the
+//   tile, rows scattered back to the grid.
+//
+// Tiles with 96-chunk (1536-byte) rows use the 256-byte-pitch swizzle: chunk
+// c of row r at slot r * 96 + (c ^ (r & 15)).
+namespace hd64 {
+constexpr int kH = 12, kD = 64, kC = kH * kD, kCpr = kC / 8, kKS = kC / 32;
+constexpr int kWaves = 8, kThreads = 64 * kWaves;
+constexpr int kTile = 64 * kC * 2;
+constexpr int kStage = 4 * 64 * kD * 2;  // O of the four first heads of the two-head waves
+constexpr int kLds = kTile + kStage + kH * kTableMax * 4;
+static_assert(kLds <= 160 * 1024, "LDS");
+
+__device__ __forceinline__ int slot(int row, int chunk) { return row * kCpr + (chunk ^ (row & 15)); }
+
+// Byte offset of the 16-byte operand chunk 4 ks + g of row 16 tt + c16.
+__device__ __forceinline__ uint32_t frag_off(int tt, int ks, int lane) {
+  const int g = lane >> 4, c16 = lane & 15;
+  return (uint32_t)(((16 * tt + c16) * kCpr + 16 * (ks >> 2) + ((4 * (ks & 3) + g) ^ c16)) * 16);
+}
+
+// The window's 64 rows -> the tile (frame-padding rows load grid token 0 and
+// are never used).
+__device__ __forceinline__ void fetch(const BlockParams& p, const UnitLoc u, uint8_t* tile, int wave, int lane) {
+  constexpr int kRounds = kCpr * 64 / (64 * kWaves);  // 12
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int blk = r * kWaves + wave;
+    const int sl = blk * 64 + lane;
+    const int row = sl / kCpr;
+    const int ch = (sl - row * kCpr) ^ (row & 15);
+    const int t = grid_token(p, u, row >> 3, row & 7);
+    const uint8_t* src = p.x + (int64_t)(t >= 0 ? t : 0) * (kCpr * 16) + ch * 16;
+    dma_to_lds16(src, __builtin_amdgcn_readfirstlane(lds_address(tile + blk * 1024)));
+  }
+}
+
+// LayerNorm of the raw rows in place (eight lanes per token, two-pass fp32
+// statistics re-reading LDS; frame-padding tokens become zeros; without
+// LayerNorm the rows are kept, padding zeroed).
+__device__ __forceinline__ void layernorm_in_place(const BlockParams& p, const UnitLoc u, uint8_t* tile, int tid) {
+  constexpr int kCPL = kCpr / 8;  // 12 chunks per lane
+  const int sub = tid & 7;
+  auto chunk = [&](int t, int k, float (&v)[8]) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(tile + slot(t, sub + 8 * k) * 16);
+    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
+      v[2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
+    }
+  };
+  const float* gptr = p.gamma;
+  const float* bptr = p.beta;
+  asm volatile("" : "+s"(gptr), "+s"(bptr));  // read per window, not held in registers
+  for (int t = tid >> 3; t < 64; t += kThreads / 8) {  // uniform per wave
+    const bool in = grid_token(p, u, t >> 3, t & 7) >= 0;
+    if (!in || !p.layernorm) {
+      if (!in) {
+#pragma unroll
+        for (int k = 0; k < kCPL; ++k)
+          *reinterpret_cast<uint4*>(tile + slot(t, sub + 8 * k) * 16) = make_uint4(0u, 0u, 0u, 0u);
+      }
+      continue;
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      float v[8];
+      chunk(t, k, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += v[e];
+    }
+    const float mean = group8_sum(sum) * p.inv_c;
+    float sq = 0.f;
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      float v[8];
+      chunk(t, k, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[e] - mean;
+        sq += d * d;
+      }
+    }
+    const float rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      float v[8];
+      chunk(t, k, v);
+      const int c0 = (sub + 8 * k) * 8;
+      float yv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 gq = gptr != nullptr ? *reinterpret_cast<const f32x4*>(gptr + c0 + 4 * h) : f32x4{1.f, 1.f, 1.f, 1.f};
+        const f32x4 bq = bptr != nullptr ? *reinterpret_cast<const f32x4*>(bptr + c0 + 4 * h) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yv[4 * h + e] = (v[4 * h + e] - mean) * rstd * gq[e] + bq[e];
+      }
+      *reinterpret_cast<uint4*>(tile + slot(t, sub + 8 * k) * 16) =
+          make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
+                     pack_bf16x2(yv[6], yv[7]));
+    }
+  }
+}
+
+// One projection pass over the 24 k-steps: NF feature tiles (row tiles
+// rt0 .. rt0 + NF - 1 of the packed weight) for NT token tiles from tt0,
+// with the bias as the accumulator init.  kV: computed as xn W^T (A = xn
+// rows; lane holds tokens 4g + r of feature c, the V^T operand layout);
+// otherwise W xn^T (lane holds features 4g + r of token c).  The weights of
+// the next k-step are requested before this step's MFMAs, then this step's
+// xn fragments are read: a deeper ring does not fit next to the K and V
+// fragments a wave holds while it computes Q.
+template <int NF, int NT, bool kV, bool kPacked>
+__device__ __forceinline__ void pass(const BlockParams& p, const uint16_t* w, const float* bias, int rt0, int tt0,
+                                     const uint8_t* tile, int lane, f32x4 (&acc)[NF][NT]) {
+  const int g = lane >> 4, c16 = lane & 15;
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    f32x4 b = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (bias != nullptr) {
+      if constexpr (kV) {
+        const float bv = bias[16 * (rt0 + f) + c16];
+        b = f32x4{bv, bv, bv, bv};
+      } else {
+        b = load_f32x4(bias + 16 * (rt0 + f) + 4 * g);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[f][t] = b;
+  }
+  uint4 ring[2][NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) ring[0][f] = weight_frag<kC, kPacked>(w, rt0 + f, 0, lane);
+  for (int ks0 = 0; ks0 < kKS; ks0 += 2) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ks = ks0 + j;
+      if (ks + 1 < kKS) {
+#pragma unroll
+        for (int f = 0; f < NF; ++f) ring[(j + 1) & 1][f] = weight_frag<kC, kPacked>(w, rt0 + f, ks + 1, lane);
+      }
+      asm volatile("" ::: "memory");
+      uint4 xf[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) xf[t] = *reinterpret_cast<const uint4*>(tile + frag_off(tt0 + t, ks, lane));
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const bf16x8 x8 = __builtin_bit_cast(bf16x8, xf[t]);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          const bf16x8 w8 = __builtin_bit_cast(bf16x8, ring[j][f]);
+          acc[f][t] = kV ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, w8, acc[f][t], 0, 0, 0)
+                         : __builtin_amdgcn_mfma_f32_16x16x32_bf16(w8, x8, acc[f][t], 0, 0, 0);
+        }
+      }
+    }
+  }
+}
+
+// Scores, softmax and O^T = V^T P^T of query tile `it` of an 8x8 window
+// against its 64 keys, head dim 64 (two 32-channel k-steps).  As
+// attend_qtiles: the relative-position bias (tabr) is the accumulator init,
+// mask terms are added to the MFMA result, the row sum runs on the matrix
+// cores, the Q operand carries scale * log2(e).
+template <int kMask, class VFrag>
+__device__ __forceinline__ void attend_tile(f32x4 (&o)[4], float& inv, int it, const uint4 (&kf)[4][2],
+                                            const uint4 (&qf)[2], const float* tabr, const WindowMaskState& m,
+                                            const f32x4 (&land_term)[4], uint64_t rid_pack, int rid_q,
+                                            float mask_term, VFrag vfrag) {
+  f32x4 s[4];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[jt][r] = tabr[30 * (3 - it + jt) + r];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+      s[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt][kk]),
+                                                      __builtin_bit_cast(bf16x8, qf[kk]), s[jt], 0, 0, 0);
+  if constexpr (kMask == kMaskShift) {
+    const bool land = m.land != 0ull;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rid_j = (int)((rid_pack >> (4 * (4 * jt + r))) & 15ull);
+        s[jt][r] += (rid_j != rid_q ? mask_term : 0.f) + (land ? land_term[jt][r] : 0.f);
+      }
+  } else if constexpr (kMask == kMaskLand) {
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) s[jt] += land_term[jt];
+  }
+  float mx = s[0][0];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[jt][r]);
+  mx = xor_max(mx);
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[jt][r] = __builtin_amdgcn_exp2f(s[jt][r] - mx);
+  const bf16x8 ones = ones_frag();
+  f32x4 rs = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) o[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int js = 0; js < 2; ++js) {
+    uint32_t wds[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2)
+      wds[e / 2] = pack_bf16x2(s[2 * js + (e >> 2)][e & 3], s[2 * js + (e >> 2)][(e & 3) + 1]);
+    const bf16x8 pf = __builtin_bit_cast(bf16x8, wds);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+      o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag(ct, js), pf, o[ct], 0, 0, 0);
+    rs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, rs, 0, 0, 0);
+  }
+  inv = __builtin_amdgcn_rcpf(rs[0]);
+}
+
+// y rows of the window (in the tile) -> the grid tokens they came from;
+// frame-padding rows are dropped.
+__device__ __forceinline__ void store(const BlockParams& p, const UnitLoc u, const uint8_t* tile, int tid) {
+  constexpr int kPasses = 64 * kCpr / kThreads;  // 12
+  const __amdgpu_buffer_rsrc_t out =
+      buffer_rsrc(p.y + (int64_t)u.b * p.H * p.W * (kCpr * 16), (uint32_t)((int64_t)p.H * p.W * (kCpr * 16)));
+#pragma unroll
+  for (int r = 0; r < kPasses; ++r) {
+    const int q = r * kThreads + tid;
+    const int row = q / kCpr, ch = q - row * kCpr;
+    const int t = grid_token(p, u, row >> 3, row & 7);
+    const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(tile + slot(row, ch) * 16));
+    const uint32_t off = t >= 0 ? (uint32_t)(t - u.b * p.H * p.W) * (kCpr * 16) + ch * 16 : 0xfffffff0u;
+    stream_store_sc1(val, out, off);  // padding rows fall outside the range
+  }
+}
+
+}  // namespace hd64
+
+namespace hd64 {
+
+// K, V and Q^T (times scale * log2 e) of head h as MFMA operand fragments:
+// kf[tt][kk] (K rows of key tile tt, channels 32 kk ..), vf[ct][js] (V^T
+// operand), qf[it][kk] (Q operand of query tile it).
+template <bool kPacked>
+__device__ __forceinline__ void head_qkv64(const BlockParams& p, const uint8_t* tile, int h, int lane,
+                                           uint4 (&kf)[4][2], uint4 (&vf)[4][2], uint4 (&qf)[4][2]) {
+  {
+    f32x4 acc[4][4];
+    pass<4, 4, false, kPacked>(p, p.w_qkv, p.b_qkv, kC / 16 + 4 * h, 0, tile, lane, acc);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) kf[tt][kk] = pack_frag(acc[2 * kk][tt], acc[2 * kk + 1][tt]);
+  }
+  {
+    f32x4 acc[4][4];
+    pass<4, 4, true, kPacked>(p, p.w_qkv, p.b_qkv, kC / 8 + 4 * h, 0, tile, lane, acc);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int js = 0; js < 2; ++js) vf[ct][js] = pack_frag(acc[ct][2 * js], acc[ct][2 * js + 1]);
+  }
+  {
+    f32x4 acc[4][4];
+    pass<4, 4, false, kPacked>(p, p.w_qkv, p.b_qkv, 4 * h, 0, tile, lane, acc);
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        qf[it][kk] = pack_frag(acc[2 * kk][it] * p.a.scale_l2e, acc[2 * kk + 1][it] * p.a.scale_l2e);
+  }
+}
+
+// Byte offset of channels cc .. cc + 3 (cc a multiple of 4, < 64) of row
+// `row` in a head's 8 KB staging slice (128-byte rows, chunk ^ (row & 7)).
+__device__ __forceinline__ uint32_t stage_off(int row, int cc) {
+  return (uint32_t)(row * 128 + (((cc >> 3) ^ (row & 7)) << 4) + (cc & 7) * 2);
+}
+
+// Attention of head h (all four query tiles) from its fragments.  O goes to
+// columns [64h, 64h + 64) of the tile, or with kStage to the head's staging
+// slice `stage` (the tile still holds the LayerNorm rows other waves read).
+template <bool kStage>
+__device__ __forceinline__ void head_attention64(const BlockParams& p, const UnitLoc cur, const float* tabs, int h,
+                                                 int lane, const uint4 (&kf)[4][2], const uint4 (&vf)[4][2],
+                                                 const uint4 (&qf)[4][2], uint8_t* tile, uint8_t* stage) {
+  // A fresh lane id: the mask terms are computed here, not hoisted.
+  asm volatile("" : "+v"(lane));
+  const int g = lane >> 4, c16 = lane & 15;
+  const WindowMaskState m = block_mask_state(p, cur);
+  const float* tabr = lane_bias_rev(tabs + h * kTableMax, lane);
+  auto vsrc = [&](int ct, int js) -> bf16x8 { return __builtin_bit_cast(bf16x8, vf[ct][js]); };
+  auto run = [&](auto mode, const f32x4 (&land_term)[4], uint64_t rid_pack) {
+    constexpr int kMask = decltype(mode)::value;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int rid_q = kMask == kMaskShift ? 3 * region(cur.wr * 8 + 2 * it + (c16 >> 3), p.Hp, 8, p.shift_h) +
+                                                  region(cur.wc * 8 + (c16 & 7), p.Wp, 8, p.shift_w)
+                                            : 0;
+      f32x4 o[4];
+      float inv;
+      attend_tile<kMask>(o, inv, it, kf, qf[it], tabr, m, land_term, rid_pack, rid_q, p.a.mask_l2e, vsrc);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const f32x4 v = o[ct] * inv;
+        uint2 pk;
+        pk.x = pack_bf16x2(v[0], v[1]);
+        pk.y = pack_bf16x2(v[2], v[3]);
+        if constexpr (kStage) {
+          *reinterpret_cast<uint2*>(stage + stage_off(16 * it + c16, 16 * ct + 4 * g)) = pk;
+        } else {
+          const int cc = kD * h + 16 * ct + 4 * g;
+          *reinterpret_cast<uint2*>(tile + slot(16 * it + c16, cc >> 3) * 16 + (cc & 7) * 2) = pk;
+        }
+      }
+    }
+  };
+  f32x4 land_term[4];
+  if (m.use_shift) {
+    uint64_t rid_pack = 0;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        rid_pack |= (uint64_t)(3 * region(cur.wr * 8 + 2 * jt + (g >> 1), p.Hp, 8, p.shift_h) +
+                               region(cur.wc * 8 + 4 * (g & 1) + r, p.Wp, 8, p.shift_w))
+                    << (4 * (4 * jt + r));
+    if (m.land != 0ull) land_terms(land_term, m.land, g, p.a.mask_l2e);
+    run(MaskMode<kMaskShift>{}, land_term, rid_pack);
+  } else if (m.land != 0ull) {
+    land_terms(land_term, m.land, g, p.a.mask_l2e);
+    run(MaskMode<kMaskLand>{}, land_term, 0ull);
+  } else {
+    run(MaskMode<kMaskNone>{}, land_term, 0ull);
+  }
+}
+
+}  // namespace hd64
+
+template <bool kPacked>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void swin_block_hd64_kernel(const BlockParams p) {
+  using namespace hd64;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* tile = smem;
+  float* tabs = reinterpret_cast<float*>(smem + kTile + kStage);
+  const int tid0 = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  const int s4 = wave & 3;
+  const bool two = wave < 4;                 // waves 0..3: heads 3s, 3s + 1; waves 4..7: head 3s + 2
+  const int h_first = two ? 3 * s4 : 3 * s4 + 2;
+  if ((int)blockIdx.x >= p.units) return;  // uniform across the workgroup
+  for (int e = tid0; e < kH * kTableMax; e += kThreads) {
+    const int hh = e / kTableMax, i = e - hh * kTableMax;
+    const int ri = kTableRev - i;  // reversed column (lane_bias_rev)
+    tabs[e] = (p.bias_table != nullptr && ri < 225) ? p.bias_table[ri * kH + hh] * kLog2e : 0.f;
+  }
+  __syncthreads();
+
+  for (int unit = blockIdx.x; unit < p.units; unit += gridDim.x) {
+    // Lane-derived addresses are recomputed per window (the thread id passes
+    // through an empty asm) rather than hoisted and held across the loop.
+    int tid = tid0;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const UnitLoc cur = locate(p, unit);
+    fetch(p, cur, tile, wave, lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    if (cur.computed) {  // uniform across the workgroup
+      layernorm_in_place(p, cur, tile, tid);
+      lds_barrier();
+      uint8_t* stage = smem + kTile + s4 * (64 * kD * 2);  // a two-head wave's first O
+      if (two) {
+        uint4 kf[4][2], vf[4][2], qf[4][2];
+        head_qkv64<kPacked>(p, tile, h_first, lane, kf, vf, qf);
+        head_attention64<true>(p, cur, tabs, h_first, lane, kf, vf, qf, tile, stage);
+      }
+      {
+        const int h = two ? h_first + 1 : h_first;
+        uint4 kf[4][2], vf[4][2], qf[4][2];
+        head_qkv64<kPacked>(p, tile, h, lane, kf, vf, qf);
+        lds_barrier();  // every wave has read the LayerNorm tile; O overwrites it
+        if (two) {  // the staged O (written by this wave) -> its tile columns
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            const int i = 64 * r + lane, row = i >> 3, ch = i & 7;
+            const uint4 v = *reinterpret_cast<const uint4*>(stage + row * 128 + ((ch ^ (row & 7)) << 4));
+            *reinterpret_cast<uint4*>(tile + slot(row, 8 * h_first + ch) * 16) = v;
+          }
+        }
+        head_attention64<false>(p, cur, tabs, h, lane, kf, vf, qf, tile, stage);
+      }
+      lds_barrier();  // O complete
+      // ---- proj: output features [96 w, 96 w + 96), then the residual ------
+      f32x4 ya[6][4];
+      pass<6, 4, false, kPacked>(p, p.w_proj, p.b_proj, 6 * wave, 0, tile, lane, ya);
+      lds_barrier();  // every wave has read O; the output rows overwrite it
+      const __amdgpu_buffer_rsrc_t xin =
+          buffer_rsrc(p.x + (int64_t)cur.b * p.H * p.W * (kCpr * 16), (uint32_t)((int64_t)p.H * p.W * (kCpr * 16)));
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int row = 16 * tt + c16;
+        const int t = grid_token(p, cur, row >> 3, row & 7);
+        const uint32_t base = t >= 0 ? (uint32_t)(t - cur.b * p.H * p.W) * (kCpr * 16) : 0xfffffff0u;
+#pragma unroll
+        for (int ft = 0; ft < 6; ++ft) {
+          const int fb = 96 * wave + 16 * ft + 4 * g;
+          const stream_u32x2 xv = __builtin_amdgcn_raw_buffer_load_b64(xin, base + fb * 2, 0, 0);
+          const f32x4& a = ya[ft][tt];
+          uint2 out;
+          out.x = pack_bf16x2(bf16_bits_to_f32((uint16_t)(xv[0] & 0xffffu)) + (float)(__bf16)a[0],
+                              bf16_bits_to_f32((uint16_t)(xv[0] >> 16)) + (float)(__bf16)a[1]);
+          out.y = pack_bf16x2(bf16_bits_to_f32((uint16_t)(xv[1] & 0xffffu)) + (float)(__bf16)a[2],
+                              bf16_bits_to_f32((uint16_t)(xv[1] >> 16)) + (float)(__bf16)a[3]);
+          *reinterpret_cast<uint2*>(tile + slot(row, fb >> 3) * 16 + (fb & 7) * 2) = out;
+        }
+      }
+    }
+    // Rows of a window the frame does not emit pass through unchanged (they
+    // were fetched into the tile as they are).
+    lds_barrier();  // output rows complete
+    store(p, cur, tile, tid);
+    lds_barrier();  // the rows are read out before the next window's load
+  }
+}
+
 template <class K>
 int launch_persistent(K kernel, int threads, int lds, int units, const BlockParams& p, hipStream_t s,
                       int* resident) {
@@ -842,6 +1296,19 @@ int launch_block(const BlockParams& p, hipStream_t s) {
   return p.packed ? launch_block_layout<kH, true>(p, s) : launch_block_layout<kH, false>(p, s);
 }
 
+template <bool kPacked>
+int launch_block_hd64_layout(const BlockParams& p, hipStream_t s) {
+  static int resident[64] = {0};
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&swin_block_hd64_kernel<kPacked>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, hd64::kLds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  return launch_persistent(swin_block_hd64_kernel<kPacked>, hd64::kThreads, hd64::kLds, p.units, p, s, resident);
+}
+
+int launch_block_hd64(const BlockParams& p, hipStream_t s) {
+  return p.packed ? launch_block_hd64_layout<true>(p, s) : launch_block_hd64_layout<false>(p, s);
+}
+
 // packed[(rt * K/32 + ks) * 64 + lane] (16 bytes) = w[16 rt + lane%16][32 ks
 // + 8 (lane/16) .. + 8]: one thread per 16-byte fragment chunk.
 __global__ __launch_bounds__(256) void pack_linear_kernel(const uint4* __restrict__ w, uint4* __restrict__ packed,
@@ -881,10 +1348,12 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   if (st != TERRA_OK) return st;
   const terra_swin_geom& q = d.geom;
   if (q.window != 8) return fail(TERRA_ERR_UNSUPPORTED, "the fused block kernel needs 8x8 windows (got %d)", q.window);
-  if (d.heads != 6 && d.heads != 12)
+  const bool hd64 = d.heads == 12 && q.channels == 768;
+  if (!hd64 && d.heads != 6 && d.heads != 12)
     return fail(TERRA_ERR_UNSUPPORTED, "the fused block kernel supports 6 or 12 heads (got %d)", d.heads);
-  if (q.channels != 32 * d.heads)
-    return fail(TERRA_ERR_UNSUPPORTED, "the fused block kernel needs head dim 32 (channels %d, heads %d)",
+  if (!hd64 && q.channels != 32 * d.heads)
+    return fail(TERRA_ERR_UNSUPPORTED,
+                "the fused block kernel needs head dim 32, or 12 heads of dim 64 (channels %d, heads %d)",
                 q.channels, d.heads);
   if (d.layernorm != 0 && !(d.ln_eps >= 0.f))
     return fail(TERRA_ERR_SHAPE, "ln_eps must be a non-negative number");
@@ -956,7 +1425,7 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   p.fd_nWw = FastDiv((uint32_t)dims.nWw);
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const int ls = d.heads == 6 ? launch_block<6>(p, s) : launch_block<12>(p, s);
+  const int ls = hd64 ? launch_block_hd64(p, s) : (d.heads == 6 ? launch_block<6>(p, s) : launch_block<12>(p, s));
   if (ls != TERRA_OK) return ls;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "block kernel launch failed: %s", hipGetErrorString(e));

@@ -425,15 +425,16 @@ def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return tuple(outs)
 
 
-# Shapes the fused block kernel is built for: 8x8 windows, head dim 32.
-BLOCK_HEADS = (6, 12)
+# (heads, channels) the fused half-block serves: head dim 32 with 6 or 12
+# heads, and the reference model's 12 heads of dim 64.
+BLOCK_SHAPES = ((6, 192), (12, 384), (12, 768))
 
 
 def swin_block_supported(x: torch.Tensor, geom: WindowGeometry, num_heads: int) -> bool:
     """Whether :func:`swin_block` serves this call (bf16 device tensor, 8x8
-    windows, head dim 32 with 6 or 12 heads)."""
+    windows, (heads, channels) in BLOCK_SHAPES)."""
     return (x.device.type == "cuda" and x.dtype == torch.bfloat16 and geom.window == 8
-            and num_heads in BLOCK_HEADS and geom.channels == 32 * num_heads)
+            and (num_heads, geom.channels) in BLOCK_SHAPES)
 
 
 def pack_linear(weight: torch.Tensor) -> torch.Tensor:

@@ -79,7 +79,7 @@ def test_attention_bias_gather_bit_exact(dev, dtype, ws, C, heads, kernel):
             assert ((got[:, ~hit] - miss).abs() <= tol).all(), (kernel, e, h)
 
 
-@pytest.mark.parametrize("C,heads", [(192, 6), (384, 12)])
+@pytest.mark.parametrize("C,heads", [(192, 6), (384, 12), (768, 12)])
 def test_fused_block_bias_gather_bit_exact(dev, C, heads):
     """The fused half-block kernel's gather, through its q/k/v and proj: no
     LayerNorm, q and k weights zero (q = k = 0), v and proj weights the
@@ -88,6 +88,7 @@ def test_fused_block_bias_gather_bit_exact(dev, C, heads):
     key each query was paired with."""
     ws, N, T = 8, 64, 225
     H, W = 16, 24
+    d = C // heads
     geom = WindowGeometry(1, H, W, C, ws)
     hh, ww = torch.meshgrid(torch.arange(H), torch.arange(W), indexing="ij")
     tok = ((hh % ws) * ws + (ww % ws)).double()  # index within the window
@@ -104,7 +105,7 @@ def test_fused_block_bias_gather_bit_exact(dev, C, heads):
         for h in range(heads):
             if e0 + h < T:
                 table[e0 + h, h] = 0.0
-        y = kernels.swin_block(x, geom, heads, 32 ** -0.5, w_qkv, None, w_proj, None, layernorm=False,
+        y = kernels.swin_block(x, geom, heads, d ** -0.5, w_qkv, None, w_proj, None, layernorm=False,
                                bias_table=table.to(dev))
         yw = so.partition_frame((y.double() - x.double()).cpu(), ws)  # [nW, N, C]
         for h in range(heads):
@@ -112,5 +113,5 @@ def test_fused_block_bias_gather_bit_exact(dev, C, heads):
             if e >= T:
                 continue
             want, _ = _expected(idx, e, key_vals)
-            assert torch.equal(yw[:, :, 32 * h:32 * (h + 1)],
-                               torch.from_numpy(want)[None, :, None].expand(yw.shape[0], N, 32)), (e, h)
+            assert torch.equal(yw[:, :, d * h:d * (h + 1)],
+                               torch.from_numpy(want)[None, :, None].expand(yw.shape[0], N, d)), (e, h)

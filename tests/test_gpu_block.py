@@ -128,8 +128,8 @@ def test_c4_chain_alternating_blocks_with_mlp(dev):
     window 8): W-MSA and SW-MSA alternating by layer index (shift from
     models/transformer.py:88), each followed by its MLP half, in the order
     BasicLayer runs them (models/reference_model/parallel_layers.py:151-153),
-    through the drop-ins (fused MLP kernel, five-stage attention half) against
-    the oracle chain, on a reduced grid."""
+    through the drop-ins (fused MLP kernel, fused attention half-block)
+    against the oracle chain, on a reduced grid."""
     cfg = workloads.CONFIGS["c4"].scaled(32, 64)
     dtype = torch.bfloat16
     layers = []

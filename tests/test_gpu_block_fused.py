@@ -8,8 +8,8 @@ elementwise |y_fused - y_five_stage| <= one bf16 ulp of y (2^-7 |y|) + 2e-2 of
 the max-abs attention delta (y - x).  Against the fp32 oracle: the 2e-2
 max-abs relative bound of the other bf16 block tests on y, and 3e-2 normwise
 on the delta.  The weights are scaled up (gain) so that the delta is O(1) and
-these checks see the attention, not the residual (q/k/v gain 4: logits of
-standard deviation ~1; proj gain 16).  Pass-through tokens
+these checks see the attention, not the residual (q/k/v gain 4, 2 at
+C = 768: logits of standard deviation ~1-5; proj gain 16, 8 at C = 768).  Pass-through tokens
 (windows the frame does not emit) are bit-exact copies of x.
 """
 import pytest
@@ -34,7 +34,9 @@ def _rel(out, ref):
 
 
 def _block(dev, H, W, C, heads, layer, land=None, pad=(0, 0, 0, 0), win_row_begin=0, win_rows=None, valid=None,
-           bias=True, gain_qkv=4.0, gain_proj=16.0):
+           bias=True, gain_qkv=None, gain_proj=None):
+    gain_qkv = gain_qkv or (2.0 if C == 768 else 4.0)
+    gain_proj = gain_proj or (8.0 if C == 768 else 16.0)
     blk = SequentialSwinTransformer(layer_idx=layer, height=H, width=W, embedding_dim=C, window_size=8,
                                     num_heads=heads, init_seed_base=workloads.SEED_BASE, land_mask=land, pad=pad,
                                     win_row_begin=win_row_begin, win_rows=win_rows, valid_windows=valid,
@@ -97,6 +99,10 @@ CASES = [  # (H, W, C, heads, layer, land, pad, win_row_begin, win_rows, valid, 
     (40, 64, 384, 12, 1, True, (0, 8, 0, 0), 0, 5, (3, 37), True),    # c5 semantics: slab, pad windows
     (16, 48, 384, 12, 0, True, (0, 0, 0, 0), 0, None, None, True),    # 12 heads, W-MSA + land
     (20, 24, 192, 6, 1, True, (2, 2, 0, 8), 1, 1, None, True),        # pad on all sides, window-row band
+    (32, 64, 768, 12, 1, True, (0, 0, 0, 0), 0, None, None, True),    # C=768, 12 heads of dim 64: SW-MSA + land
+    (24, 40, 768, 12, 0, False, (0, 0, 0, 0), 0, None, None, False),  # dim 64, W-MSA, no bias table
+    (40, 64, 768, 12, 1, True, (0, 8, 0, 0), 0, 5, (3, 37), True),    # dim 64, c5-style slab and pad windows
+    (20, 24, 768, 12, 1, True, (2, 2, 0, 8), 1, 1, None, True),       # dim 64, pad on all sides, row band
 ]
 
 
@@ -134,8 +140,9 @@ def test_fused_pass_through_tokens_are_exact(dev, case):
     assert not torch.equal(y[emitted], x[emitted])
 
 
-def test_fused_in_place_equals_out_of_place(dev):
-    H, W, C, heads = 32, 48, 192, 6
+@pytest.mark.parametrize("C,heads", [(192, 6), (768, 12)])
+def test_fused_in_place_equals_out_of_place(dev, C, heads):
+    H, W = 32, 48
     land = workloads.land_mask(H, W, seed=403)
     blk = _block(dev, H, W, C, heads, 1, land)
     x = workloads.activations((1, H, W, C), 404, torch.bfloat16).to(dev)
@@ -166,26 +173,30 @@ def test_fused_without_layernorm(dev, monkeypatch):
     _assert_matches_oracle(y_f, ref, x)
 
 
-def test_fused_deterministic(dev):
-    blk = _block(dev, 32, 64, 192, 6, 1, workloads.land_mask(32, 64, seed=406))
-    x = workloads.activations((1, 32 * 64, 192), 407, torch.bfloat16).to(dev)
+@pytest.mark.parametrize("C,heads", [(192, 6), (768, 12)])
+def test_fused_deterministic(dev, C, heads):
+    blk = _block(dev, 32, 64, C, heads, 1, workloads.land_mask(32, 64, seed=406))
+    x = workloads.activations((1, 32 * 64, C), 407, torch.bfloat16).to(dev)
     with torch.no_grad():
         a = blk(x)
         b = blk(x)
     assert torch.equal(a, b)
 
 
-def test_fused_full_size_c3(dev):
-    """The benchmark configuration end to end with gained weights (the
-    attention term is O(1)): fused kernel vs the five-stage path and vs the
-    oracle, on y and normwise on y - x."""
-    cfg = workloads.CONFIGS["c3"]
-    land = workloads.land_mask(cfg.height, cfg.width, seed=42)
-    blk = gain_block(workloads.block_for(cfg, 1, land=land)).to(dev).to(torch.bfloat16)
+@pytest.mark.parametrize("name,layer", [("c3", 1), ("c4", 0), ("c4", 1)])
+def test_fused_full_size(dev, name, layer):
+    """The benchmark configuration (c3) and the reference model's block (c4,
+    C = 768, 12 heads of dim 64; W-MSA and SW-MSA) end to end with gained
+    weights (the attention term is O(1)): fused kernel vs the five-stage path
+    and vs the oracle, on y and normwise on y - x."""
+    cfg = workloads.CONFIGS[name]
+    land = workloads.land_mask(cfg.height, cfg.width, seed=42) if name == "c3" else None
+    blk = gain_block(workloads.block_for(cfg, layer, land=land)).to(dev).to(torch.bfloat16)
     x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 1003, torch.bfloat16)
     y_f, y_u = _both_paths(blk, x.to(dev))
     _assert_paths_agree(y_f, y_u, x.to(dev))
-    ref = so.swin_block_attention(x, cfg.height, cfg.width, cfg.window, 4, cfg.heads, _params(blk), land=land)
+    ref = so.swin_block_attention(x, cfg.height, cfg.width, cfg.window, blk.shift_size, cfg.heads, _params(blk),
+                                  land=land)
     assert_block_matches(y_f, ref, x, 2e-2, 3e-2)
 
 
@@ -197,9 +208,10 @@ def test_pack_linear_layout(dev):
     assert torch.equal(got, want)
 
 
-def test_fused_packed_equals_unpacked(dev):
+@pytest.mark.parametrize("C,heads", [(192, 6), (768, 12)])
+def test_fused_packed_equals_unpacked(dev, C, heads):
     """The weight layout changes only addresses: identical output bits."""
-    H, W, C, heads = 16, 32, 192, 6
+    H, W = 16, 32
     blk = _block(dev, H, W, C, heads, 1, workloads.land_mask(H, W, seed=421))
     x = workloads.activations((1, H, W, C), 422, torch.bfloat16).to(dev)
     geom = blk.geometry(1)
