@@ -390,7 +390,7 @@ def main():
         blk_tflops = block_flops / (t_blk * 1e-6) / 1e12
         roofline = {
             "kernel": (("swin_block_hd64_kernel" if cfg.channels == 768 else
-                        f"swin_block_{'pp_' if cfg.heads == 6 else ''}kernel<{cfg.heads}>") +
+                        "swin_block_dw_kernel" if cfg.heads == 6 else f"swin_block_kernel<{cfg.heads}>") +
                        " (fused LN + qkv + window attention + proj + residual, gather/scatter)"),
             "bound": "mfma",
             "achieved": blk_tflops,

@@ -1,5 +1,6 @@
 // Fused Swin attention half-block forward for gfx950: bf16 activations,
-// 8x8 windows, head dim 32 (C = 32 * heads).
+// 8x8 windows; 6 or 12 heads of dim 32 (C = 192, 384) or 12 heads of dim 64
+// (C = 768).
 //
 // One kernel computes, for every window of the (padded, shifted) frame,
 //
@@ -13,13 +14,13 @@
 // crop).  Only x is read from and y written to HBM (2 * B*H*W*C*2 bytes);
 // the weights (4*C*C*2 bytes) are re-read from L2 by every window.
 //
-// Both kernels are persistent over windows and keep every [64][C] bf16 tile
-// in LDS with 16-byte chunks XOR-swizzled per row (tile_slot).  A window's
-// raw rows arrive by direct global -> LDS loads issued while the previous
-// window is computed; they stay in LDS for the residual add and are
-// overwritten by the output rows, which are streamed back to the grid.
+// The kernels are persistent over windows and keep every [64][C] bf16 tile in
+// LDS with 16-byte chunks XOR-swizzled per row.  A window's raw rows arrive by
+// direct global -> LDS loads issued while earlier windows are computed; at
+// C <= 384 they stay in LDS for the residual add and are overwritten by the
+// output rows, which are streamed back to the grid.
 //
-// One wave owns one head h of a window.  It computes, for all 64 tokens,
+// A wave computes a (window, head) unit: for all 64 tokens,
 //
 //   Q^T = W_q,h xn^T, K^T = W_k,h xn^T   (A = weight rows, B = xn rows)
 //   V   = xn W_v,h^T                     (A = xn rows,     B = weight rows)
@@ -31,16 +32,17 @@
 // both sides; V's accumulators give the V^T operand of O^T = V^T P^T under
 // the key permutation that P^T inherits from the S^T accumulators.  So q, k
 // and v never leave registers.  O goes through LDS (all heads of a token are
-// the proj input), and wave h computes output features [32h, 32h + 32) of
-// the projection as Y^T = W_p O^T.
+// the proj input), and the projection runs as Y^T = W_p O^T over row tiles of
+// output features.
 //
-// swin_block_pp_kernel (6 heads, C = 192, the benchmark shape): two groups of
-// six such waves in one 12-wave workgroup per CU, each group on its own
-// window, one phase apart, so that MFMA phases of one group overlap VALU
-// phases of the other.
+// swin_block_dw_kernel (6 heads, C = 192, the benchmark shape): a pair of
+// windows at a time, eight waves, three (window, head) units per SIMD.
 //
-// swin_block_kernel (12 heads, C = 384): one group, one window at a time
-// (two groups' buffers do not fit LDS at this width).
+// swin_block_kernel (12 heads, C = 384): one wave per head, one window at a
+// time.
+//
+// swin_block_hd64_kernel (12 heads of dim 64, C = 768): one window at a time,
+// eight waves, three heads per SIMD.
 //
 // Windows that the frame does not emit (outside the slab's window rows, or
 // outside the valid-window range) pass x through unchanged, which is what
@@ -459,11 +461,12 @@ __device__ __forceinline__ void head_qkv(const BlockParams& p, const uint8_t* xn
 }
 
 // Attention of head h from the register fragments, one query tile at a time;
-// O (bf16) goes to columns [32h, 32h + 32) of `o_tile`.
-template <int C>
+// O (bf16) goes to columns [32h, 32h + 32) of `o_tile`, or with kHold to
+// hold[it][ct] (channels 32h + 16ct + 4g .. + 3 of query 16 it + c).
+template <int C, bool kHold = false>
 __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitLoc cur, const float* tab, int h,
                                                int lane, const uint4 (&kf4)[4], const uint4 (&vf)[2][2],
-                                               const uint4 (&qf)[4], uint8_t* o_tile) {
+                                               const uint4 (&qf)[4], uint8_t* o_tile, uint2 (*hold)[2] = nullptr) {
   constexpr int cpr = C / 8;
   const int g = lane >> 4, c16 = lane & 15;
   const WindowMaskState m = block_mask_state(p, cur);
@@ -504,7 +507,10 @@ __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitL
           uint2 pk;
           pk.x = pack_bf16x2(v[0], v[1]);
           pk.y = pack_bf16x2(v[2], v[3]);
-          *reinterpret_cast<uint2*>(o_tile + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
+          if constexpr (kHold)
+            hold[it0 + q][ct] = pk;
+          else
+            *reinterpret_cast<uint2*>(o_tile + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
         }
       }
     }
@@ -689,115 +695,313 @@ void swin_block_kernel(const BlockParams p) {
 }
 
 // ============================================================================
-// swin_block_pp_kernel: two groups of one-wave-per-head, two windows in
-// flight (6 heads, C = 192; 12 waves, one workgroup per CU)
+// swin_block_dw_kernel: 6 heads (C = 192, c3), a pair of windows at a time.
+// Eight waves, two per SIMD, up to 256 VGPRs each; the 12 (window, head)
+// units of a pair split three per SIMD: wave s < 4 owns units 3s and 3s + 1,
+// wave s + 4 unit 3s + 2 (unit u = window u / 6, head u % 6).
 // ============================================================================
 //
-// Group g (waves [6g, 6g + 6)) takes the workgroup's windows 2k + g.  A
-// window passes through four phases separated by workgroup barriers:
+// LDS: two row buffers for a pair (pair k's rows, which become its output
+// rows; the other buffer holds pair k - 1's output rows, then receives pair
+// k + 1's), one LayerNorm buffer that later holds the pair's attention
+// output O, and the tables.  Per pair k:
 //
-//   A  store the previous window's output rows; LayerNorm      (VALU, LDS)
-//   B  q, k, v into registers; issue the next window's rows    (MFMA)
-//   C  attention, O -> LDS                                     (VALU, exp)
-//   D  proj + residual into the raw rows                       (MFMA)
+//   wait for the pair's rows; LayerNorm -> the LayerNorm buffer (waves
+//           4wi .. 4wi + 3 take window wi)
+//   barrier
+//   wave s < 4: q/k/v of unit 3s (one pass over the window's LayerNorm
+//           rows: six row tiles x four token tiles, so each LayerNorm
+//           fragment feeds six MFMAs and each weight fragment four), its
+//           attention (O kept in registers), q/k/v of unit 3s + 1
+//   wave s + 4: q/k/v and attention of unit 3s + 2 (O kept in registers);
+//           pair k - 1's output rows out of the other buffer
+//   barrier (every LayerNorm row has been read)
+//   pair k + 1's rows into the other buffer (all waves); the held O and unit
+//           3s + 1's attention -> the O buffer
+//   barrier
+//   wave w: output features [48 (w & 3), + 48) of window w >> 2 = O W_p^T +
+//           b_p, plus the residual, in place over the window's rows
 //
-// Group 1 runs one phase behind group 0, so every barrier interval pairs an
-// MFMA phase of one group with a VALU phase of the other, and each SIMD
-// (which holds waves of both groups) overlaps them.  Per group LDS: two row
-// buffers (window k's raw rows, later its output; the other receives window
-// k + 1 during phase B) and one LayerNorm / O tile.
+// The tiles use the 384-byte-row swizzle (tile_slot).
+namespace dw {
+constexpr int kH = 6, kC = 192, kCpr = kC / 8, kKS = kC / 32;
+constexpr int kWaves = 8, kThreads = 64 * kWaves;
+constexpr int kTile = 64 * kC * 2;  // one window's rows
+constexpr int kPair = 2 * kTile;
+constexpr int kOffO = 2 * kPair;    // two row buffers, then the LayerNorm / O buffer
+constexpr int kOffTabs = kOffO + kPair;
+constexpr int kLds = kOffTabs + (kH * kTableMax + kC + kC + 3 * kC + kC) * 4;
+static_assert(kLds <= 160 * 1024, "LDS");
 
-template <int kH>
-constexpr int block_pp_lds_bytes() {
-  return 6 * 64 * 32 * kH * 2 + kH * kTableMax * 4 + 2 * 32 * kH * 4 + 4 * 32 * kH * 4;
-}
-
-template <int kH, bool kPacked>
-__global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockParams p) {
-  constexpr int C = 32 * kH;
-  constexpr int cpr = C / 8;
-  constexpr int tile = 64 * C * 2;
-  constexpr int kGroupThreads = 64 * kH;
-  static_assert(cpr % 8 == 0, "rows must be whole groups of 8 chunks (swizzle)");
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  float* tabs = reinterpret_cast<float*>(smem + 6 * tile);
-  float* s_gamma = tabs + kH * kTableMax;
-  float* s_beta = s_gamma + C;
-  float* s_bqkv = s_beta + C;    // [3C]
-  float* s_bproj = s_bqkv + 3 * C;  // [C]
-
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int grp = wave >= kH ? 1 : 0;
-  const int h = wave - grp * kH;  // this wave's head
-  uint8_t* gbuf = smem + grp * 3 * tile;
-  uint8_t* xn = gbuf + 2 * tile;
-
-  if ((int)blockIdx.x >= p.units) return;  // uniform across the workgroup
-  stage_tables<kH, 2 * kGroupThreads>(p, tabs, s_gamma, s_beta, tid, s_bqkv, s_bproj);
-
-  // Windows of group g: unit blockIdx.x + (2k + g) * gridDim.x, k < count[g].
-  const int stride = 2 * (int)gridDim.x;
-  const int first0 = blockIdx.x, first1 = blockIdx.x + gridDim.x;
-  const int n0 = first0 < p.units ? (p.units - 1 - first0) / stride + 1 : 0;
-  const int n1 = first1 < p.units ? (p.units - 1 - first1) / stride + 1 : 0;
-  const int n_mine = grp ? n1 : n0;
-  const int first_mine = grp ? first1 : first0;
-  // Group g ends with the store of its last window, in phase A of cycle n_g
-  // (slot g + 4 n_g).
-  const int slots = (4 * n0 + 1) > (4 * n1 + 2) ? (4 * n0 + 1) : (4 * n1 + 2);
-
-  if (n_mine > 0) fetch_window<cpr, kH>(p, locate(p, first_mine), gbuf, h, lane);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
-  uint4 kf4[4], vf[2][2], qf[4];  // phase B -> phase C
-  for (int t = 0; t < slots; ++t) {
-    const int q = t - grp;  // group-local slot
-    // Lane-derived addresses are recomputed per slot rather than held in
-    // registers across the loop.
-    int lane_i = lane;
-    asm volatile("" : "+v"(lane_i));
-    if (q >= 0) {
-      const int k = q >> 2, ph = q & 3;
-      const bool have = k < n_mine;
-      const UnitLoc cur = locate(p, first_mine + k * stride);
-      uint8_t* xr = gbuf + (k & 1) * tile;
-      if (ph == 0) {
-        if (k >= 1) store_window<cpr, kGroupThreads>(p, locate(p, first_mine + (k - 1) * stride),
-                                                     gbuf + ((k - 1) & 1) * tile, h * 64 + lane_i);
-        if (have && cur.computed)
-          layernorm_window<cpr, kGroupThreads>(p, cur, xr, xn, s_gamma, s_beta, h * 64 + lane_i);
-      } else if (ph == 1) {
-        if (have) {
-          // MFMA phases run at raised wave priority: in each slot the
-          // arbiter then issues this group's matrix instructions ahead of the
-          // other group's VALU phase, which fills the MFMA shadow.
-          __builtin_amdgcn_s_setprio(1);
-          if (cur.computed) head_qkv<C, kPacked>(p, xn, h, lane_i, kf4, vf, qf, s_bqkv);
-          __builtin_amdgcn_s_setprio(0);
-          // The next window's rows, behind the q/k/v loads; the buffer's last
-          // reader was phase A's store.
-          if (k + 1 < n_mine)
-            fetch_window<cpr, kH>(p, locate(p, first_mine + (k + 1) * stride), gbuf + ((k + 1) & 1) * tile, h,
-                                  lane_i);
-        }
-      } else if (ph == 2) {
-        if (have && cur.computed)
-          head_attention<C>(p, cur, tabs + h * kTableMax, h, lane_i, kf4, vf, qf, xn);
-      } else {
-        __builtin_amdgcn_s_setprio(1);
-        if (have && cur.computed) head_proj<C, kPacked>(p, xn, xr, h, lane_i, s_bproj);
-        __builtin_amdgcn_s_setprio(0);
-        // The next window's rows have landed before phase A reads them.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+// q, k, v of head h for the window's 64 tokens in one pass: accumulator j
+// (row tiles: Q^T 2h + j, K^T C/16 + 2h + j - 2, V C/8 + 2h + j - 4) starts
+// at the bias; the V tiles are computed as xn W^T (lane holds tokens 4g + r
+// of feature c), the others as W xn^T.  The results are packed into the
+// operand fragments of head_attention.
+template <bool kPacked>
+__device__ __forceinline__ void unit_qkv(const BlockParams& p, const uint8_t* xn, int h, int lane, uint4 (&kf4)[4],
+                                         uint4 (&vf)[2][2], uint4 (&qf)[4], const float* bqkv) {
+  constexpr int kDepth = 3;  // weight ring (registers): loads two k-steps ahead
+  const int g = lane >> 4, c16 = lane & 15;
+  const int sw = (c16 >> 1) & 7;
+  auto rt = [&](int j) { return (j >> 1) * (kC / 16) + 2 * h + (j & 1); };
+  f32x4 acc[6][4];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    f32x4 b;
+    if (j < 4) {
+      b = load_f32x4(bqkv + (j >> 1) * kC + 32 * h + 16 * (j & 1) + 4 * g);
+    } else {
+      const float bv = bqkv[2 * kC + 32 * h + 16 * (j & 1) + c16];
+      b = f32x4{bv, bv, bv, bv};
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) acc[j][tt] = b;
+  }
+  uint32_t xoff[2][4];
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) xoff[e][tt] = ((16 * tt + c16) * kCpr + ((4 * e + g) ^ sw)) * 16;
+  auto xn_frag = [&](int tt, int ks) -> uint4 {
+    return *reinterpret_cast<const uint4*>(xn + xoff[ks & 1][tt] + (ks >> 1) * 128);
+  };
+  uint4 ring[kDepth][6];
+#pragma unroll
+  for (int st = 0; st < kDepth - 1; ++st)
+#pragma unroll
+    for (int j = 0; j < 6; ++j) ring[st][j] = weight_frag<kC, kPacked>(p.w_qkv, rt(j), st, lane);
+  uint4 xf[2][4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) xf[0][tt] = xn_frag(tt, 0);
+#pragma unroll
+  for (int ks = 0; ks < kKS; ++ks) {
+    if (ks + kDepth - 1 < kKS) {
+#pragma unroll
+      for (int j = 0; j < 6; ++j)
+        ring[(ks + kDepth - 1) % kDepth][j] = weight_frag<kC, kPacked>(p.w_qkv, rt(j), ks + kDepth - 1, lane);
+    }
+    if (ks + 1 < kKS) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) xf[(ks + 1) & 1][tt] = xn_frag(tt, ks + 1);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const bf16x8 x8 = __builtin_bit_cast(bf16x8, xf[ks & 1][tt]);
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        const bf16x8 w8 = __builtin_bit_cast(bf16x8, ring[ks % kDepth][j]);
+        acc[j][tt] = j < 4 ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(w8, x8, acc[j][tt], 0, 0, 0)
+                           : __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, w8, acc[j][tt], 0, 0, 0);
       }
     }
-    // LDS hand-off only: the next window's rows stay in flight across the
-    // slots between phase B and phase D, and the output stores are not waited.
-    lds_barrier();
   }
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    kf4[tt] = pack_frag(acc[2][tt], acc[3][tt]);
+    qf[tt] = pack_frag(acc[0][tt] * p.a.scale_l2e, acc[1][tt] * p.a.scale_l2e);
+  }
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int js = 0; js < 2; ++js) vf[ct][js] = pack_frag(acc[4 + ct][2 * js], acc[4 + ct][2 * js + 1]);
+}
+
+// The weight fragments of proj_rows (row tiles 3 q4 .. 3 q4 + 2, all k-steps).
+template <bool kPacked>
+__device__ __forceinline__ void proj_weights(const BlockParams& p, int q4, int lane, uint4 (&wf)[kKS][3]) {
+#pragma unroll
+  for (int ks = 0; ks < kKS; ++ks)
+#pragma unroll
+    for (int ft = 0; ft < 3; ++ft) wf[ks][ft] = weight_frag<kC, kPacked>(p.w_proj, 3 * q4 + ft, ks, lane);
+}
+
+// Output features [48 q4, 48 q4 + 48) of a window = O W_p^T + b_p (Y^T =
+// W_p O^T, three row tiles x four token tiles; weights wf from proj_weights),
+// then y = bf16(x + bf16(Y)) in place over the window's raw rows.
+__device__ __forceinline__ void proj_rows(const uint8_t* o_tile, uint8_t* tile, int q4, int lane,
+                                          const float* bproj, const uint4 (&wf)[kKS][3]) {
+  const int g = lane >> 4, c16 = lane & 15;
+  const int sw = (c16 >> 1) & 7;
+  f32x4 ya[3][4];
+#pragma unroll
+  for (int ft = 0; ft < 3; ++ft) {
+    const f32x4 b = load_f32x4(bproj + 48 * q4 + 16 * ft + 4 * g);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) ya[ft][tt] = b;
+  }
+  uint32_t ooff[2][4];
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) ooff[e][tt] = ((16 * tt + c16) * kCpr + ((4 * e + g) ^ sw)) * 16;
+  auto o_frag = [&](int tt, int ks) -> uint4 {
+    return *reinterpret_cast<const uint4*>(o_tile + ooff[ks & 1][tt] + (ks >> 1) * 128);
+  };
+  uint4 of[2][4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) of[0][tt] = o_frag(tt, 0);
+#pragma unroll
+  for (int ks = 0; ks < kKS; ++ks) {
+    if (ks + 1 < kKS) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) of[(ks + 1) & 1][tt] = o_frag(tt, ks + 1);
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int ft = 0; ft < 3; ++ft)
+        ya[ft][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[ks][ft]),
+                                                             __builtin_bit_cast(bf16x8, of[ks & 1][tt]), ya[ft][tt],
+                                                             0, 0, 0);
+  }
+  // Y^T lane (c, g) element r: feature 48 q4 + 16 ft + 4g + r of token 16 tt + c.
+#pragma unroll
+  for (int ft = 0; ft < 3; ++ft) {
+    const int fb = 48 * q4 + 16 * ft + 4 * g;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+      residual_add4(tile + tile_slot(16 * tt + c16, fb >> 3, kCpr) * 16 + (fb & 7) * 2, ya[ft][tt]);
+  }
+}
+
+// The output rows of a pair's windows (u0, u0 + 1; those < p.units) -> the
+// grid tokens they came from, by kW waves (wave index wv); frame-padding rows
+// are dropped.  Wave wv reads exactly the LDS slots that fetch_window<kCpr,
+// kW> fills from wave wv, so once its own reads have completed a wave may
+// load new rows over them with no wait on the other waves.
+template <int kW>
+__device__ __forceinline__ void store_pair(const BlockParams& p, int u0, const uint8_t* buf, int wv, int lane) {
+  constexpr int kRounds = 64 * kCpr / (64 * kW);
+  static_assert(kRounds * 64 * kW == 64 * kCpr, "whole wave-rounds of 64 slots");
+#pragma unroll
+  for (int wi = 0; wi < 2; ++wi) {
+    if (u0 + wi >= p.units) continue;
+    const UnitLoc u = locate(p, u0 + wi);
+    const __amdgpu_buffer_rsrc_t out =
+        buffer_rsrc(p.y + (int64_t)u.b * p.H * p.W * (kCpr * 16), (uint32_t)((int64_t)p.H * p.W * (kCpr * 16)));
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      const int sl = (r * kW + wv) * 64 + lane;
+      const int row = sl / kCpr;
+      const int ch = (sl - row * kCpr) ^ ((row >> 1) & 7);  // the chunk tile_slot places in slot sl
+      const int t = grid_token(p, u, row >> 3, row & 7);
+      const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(buf + wi * kTile + sl * 16));
+      // Frame-padding rows fall outside the range.
+      stream_store_sc1(val, out, t >= 0 ? (uint32_t)(t - u.b * p.H * p.W) * (kCpr * 16) + ch * 16 : 0xfffffff0u);
+    }
+  }
+}
+
+}  // namespace dw
+
+template <bool kPacked>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void swin_block_dw_kernel(const BlockParams p) {
+  using namespace dw;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* obuf = smem + kOffO;
+  float* tabs = reinterpret_cast<float*>(smem + kOffTabs);
+  float* s_gamma = tabs + kH * kTableMax;
+  float* s_beta = s_gamma + kC;
+  float* s_bqkv = s_beta + kC;
+  float* s_bproj = s_bqkv + 3 * kC;
+  const int tid0 = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  const int s4 = wave & 3, wwin = wave >> 2;
+  const bool two = wave < 4;  // waves 0..3: units 3s, 3s + 1; waves 4..7: unit 3s + 2
+  const int pairs = (p.units + 1) >> 1;
+  if ((int)blockIdx.x >= pairs) return;  // uniform across the workgroup
+  stage_tables<kH, kThreads>(p, tabs, s_gamma, s_beta, tid0, s_bqkv, s_bproj);
+  const int n = (pairs - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
+  auto first_unit = [&](int k) { return 2 * ((int)blockIdx.x + k * (int)gridDim.x); };
+  {  // the first pair's rows
+    const int u0 = first_unit(0);
+#pragma unroll
+    for (int wi = 0; wi < 2; ++wi)
+      if (u0 + wi < p.units) fetch_window<kCpr, kWaves>(p, locate(p, u0 + wi), smem + wi * kTile, wave, tid0 & 63);
+  }
+
+  for (int k = 0; k < n; ++k) {
+    // Lane-derived addresses are recomputed per pair (the thread id passes
+    // through an empty asm) rather than hoisted and held across the loop.
+    int tid = tid0;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    uint8_t* rows = smem + (k & 1) * kPair;          // pair k's rows, later its output rows
+    uint8_t* other = smem + ((k + 1) & 1) * kPair;   // pair k - 1's output rows, then pair k + 1's rows
+    const int u0 = first_unit(k);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the pair's rows
+    lds_barrier();
+    {
+      const int u = u0 + wwin;
+      if (u < p.units) {
+        const UnitLoc cur = locate(p, u);
+        if (cur.computed)
+          layernorm_window<kCpr, kThreads / 2>(p, cur, rows + wwin * kTile, obuf + wwin * kTile, s_gamma, s_beta,
+                                               tid & (kThreads / 2 - 1));
+      }
+    }
+    lds_barrier();  // LayerNorm rows ready
+    const int ub = 3 * s4 + 1;  // waves 0..3: the unit whose attention follows the barrier
+    const int wib = ub >= kH ? 1 : 0, hb = ub - wib * kH;
+    const UnitLoc curb = locate(p, u0 + wib);
+    const bool onb = two && u0 + wib < p.units && curb.computed;
+    uint4 kf4[4], vf[2][2], qf[4];
+    // O of the unit whose attention runs before the barrier (unit 3s for
+    // waves 0..3, 3s + 2 for waves 4..7), held until the LayerNorm rows are
+    // free.
+    uint2 oa[4][2];
+    const int ua = 3 * s4 + (two ? 0 : 2), wia = ua >= kH ? 1 : 0, ha = ua - wia * kH;
+    const UnitLoc cura = locate(p, u0 + wia);
+    const bool ona = u0 + wia < p.units && cura.computed;
+    if (ona) {
+      unit_qkv<kPacked>(p, obuf + wia * kTile, ha, lane, kf4, vf, qf, s_bqkv);
+      head_attention<kC, true>(p, cura, tabs + ha * kTableMax, ha, lane, kf4, vf, qf, nullptr, oa);
+    }
+    if (two) {
+      if (onb) unit_qkv<kPacked>(p, obuf + wib * kTile, hb, lane, kf4, vf, qf, s_bqkv);
+    } else if (k > 0) {
+      store_pair<4>(p, first_unit(k - 1), other, wave - 4, lane);  // pair k - 1's output rows
+    }
+    lds_barrier();  // every LayerNorm row has been read: O may replace them
+    // Pair k + 1's rows into the other buffer, issued ahead of the attention
+    // (no vector-memory work of its own), so that they queue in front of no
+    // q/k/v weight load.
+    if (k + 1 < n) {
+      const int u1 = first_unit(k + 1);
+#pragma unroll
+      for (int wi = 0; wi < 2; ++wi)
+        if (u1 + wi < p.units) fetch_window<kCpr, kWaves>(p, locate(p, u1 + wi), other + wi * kTile, wave, lane);
+    }
+    if (ona) {
+      uint8_t* ot = obuf + wia * kTile;
+#pragma unroll
+      for (int it = 0; it < 4; ++it)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const int cc = 32 * ha + 16 * ct + 4 * g;
+          *reinterpret_cast<uint2*>(ot + tile_slot(16 * it + c16, cc >> 3, kCpr) * 16 + (cc & 7) * 2) = oa[it][ct];
+        }
+    }
+    if (onb) head_attention<kC>(p, curb, tabs + hb * kTableMax, hb, lane, kf4, vf, qf, obuf + wib * kTile);
+    lds_barrier();  // O complete
+    {
+      const int u = u0 + wwin;
+      if (u < p.units) {
+        const UnitLoc cur = locate(p, u);
+        if (cur.computed) {
+          uint4 wproj[kKS][3];  // all of them up front: one wait, after the next pair's rows
+          proj_weights<kPacked>(p, s4, lane, wproj);
+          proj_rows(obuf + wwin * kTile, rows + wwin * kTile, s4, lane, s_bproj, wproj);
+        }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  lds_barrier();
+  store_pair<kWaves>(p, first_unit(n - 1), smem + ((n - 1) & 1) * kPair, wave, tid0 & 63);
 }
 
 // ============================================================================
@@ -815,10 +1019,10 @@ __global__ __launch_bounds__(128 * kH) void swin_block_pp_kernel(const BlockPara
 //   per head: K^T, V, then Q^T from the tile into MFMA operand fragments
 //           (three passes over the 24 k-steps); a two-head wave runs its
 //           first head's attention before its second head's projections
-//           and keeps that O in registers
+//           and writes that O to an LDS staging area
 //   barrier (every wave has read the LayerNorm tile)
-//   the heads' O into columns [64h, 64h + 64) of the tile (the last head's
-//           attention one query tile at a time)
+//   the staged O and the last head's O into columns [64h, 64h + 64) of the
+//           tile
 //   barrier
 //   wave w: output features [96w, 96w + 96) = O W_p^T + b_p
 //   barrier (every wave has read O)
@@ -1275,20 +1479,11 @@ int launch_persistent(K kernel, int threads, int lds, int units, const BlockPara
 template <int kH, bool kPacked>
 int launch_block_layout(const BlockParams& p, hipStream_t s) {
   static int resident[64] = {0};
-  if constexpr (kH == 6) {
-    constexpr int lds = block_pp_lds_bytes<kH>();
-    static const hipError_t attr =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&swin_block_pp_kernel<kH, kPacked>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
-    return launch_persistent(swin_block_pp_kernel<kH, kPacked>, 128 * kH, lds, p.units, p, s, resident);
-  } else {
-    constexpr int lds = block_lds_bytes<kH>();
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&swin_block_kernel<kH, kPacked>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
-    return launch_persistent(swin_block_kernel<kH, kPacked>, 64 * kH, lds, p.units, p, s, resident);
-  }
+  constexpr int lds = block_lds_bytes<kH>();
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&swin_block_kernel<kH, kPacked>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  return launch_persistent(swin_block_kernel<kH, kPacked>, 64 * kH, lds, p.units, p, s, resident);
 }
 
 template <int kH>
@@ -1303,6 +1498,19 @@ int launch_block_hd64_layout(const BlockParams& p, hipStream_t s) {
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, hd64::kLds);
   if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
   return launch_persistent(swin_block_hd64_kernel<kPacked>, hd64::kThreads, hd64::kLds, p.units, p, s, resident);
+}
+
+template <bool kPacked>
+int launch_block_dw_layout(const BlockParams& p, hipStream_t s) {
+  static int resident[64] = {0};
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&swin_block_dw_kernel<kPacked>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, dw::kLds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  return launch_persistent(swin_block_dw_kernel<kPacked>, dw::kThreads, dw::kLds, (p.units + 1) / 2, p, s, resident);
+}
+
+int launch_block_dw(const BlockParams& p, hipStream_t s) {
+  return p.packed ? launch_block_dw_layout<true>(p, s) : launch_block_dw_layout<false>(p, s);
 }
 
 int launch_block_hd64(const BlockParams& p, hipStream_t s) {
@@ -1425,7 +1633,7 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   p.fd_nWw = FastDiv((uint32_t)dims.nWw);
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const int ls = hd64 ? launch_block_hd64(p, s) : (d.heads == 6 ? launch_block<6>(p, s) : launch_block<12>(p, s));
+  const int ls = hd64 ? launch_block_hd64(p, s) : (d.heads == 6 ? launch_block_dw(p, s) : launch_block<12>(p, s));
   if (ls != TERRA_OK) return ls;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "block kernel launch failed: %s", hipGetErrorString(e));
