@@ -66,15 +66,13 @@ def parse():
     return ap.parse_args()
 
 
-PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "swin_block_c3_pmc.md")
-
-
-def measured_traffic():
-    """HBM bytes per launch of the fused block kernel from the committed
-    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of
-    known size), or None when that summary is absent."""
+def measured_traffic(config):
+    """HBM bytes per launch of the fused block kernel on `config` from the
+    committed rocprofv3 counter summary profiles/swin_block_<config>_pmc.md
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size), or None when
+    there is no such summary."""
     try:
-        with open(PROFILE_TRAFFIC) as f:
+        with open(os.path.join(ROOT, "profiles", f"swin_block_{config}_pmc.md")) as f:
             for line in f:
                 if line.strip().startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":", 1)[1].strip())
@@ -397,7 +395,7 @@ def main():
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": blk_tflops / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": measured_traffic() if args.config == "c3" else None,
+            "traffic": measured_traffic(args.config),
             "algorithmic_flops_per_launch": block_flops,
             "algorithmic_bytes_per_launch": block_bytes,
             "avg_launch_us": t_blk,
