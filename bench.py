@@ -387,7 +387,8 @@ def main():
         t_blk = statistics.mean(per_launch)
         blk_tflops = block_flops / (t_blk * 1e-6) / 1e12
         roofline = {
-            "kernel": (("swin_block_hd64_kernel" if cfg.channels == 768 else
+            "kernel": (("swin_block_w7_kernel" if cfg.window == 7 else
+                        "swin_block_hd64_kernel" if cfg.channels == 768 else
                         "swin_block_dw_kernel" if cfg.heads == 6 else f"swin_block_kernel<{cfg.heads}>") +
                        " (fused LN + qkv + window attention + proj + residual, gather/scatter)"),
             "bound": "mfma",

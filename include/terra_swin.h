@@ -140,7 +140,7 @@ typedef struct terra_swin_attn_bwd_desc {
  * tokens of x; tokens of windows that are not emitted keep x. */
 typedef struct terra_swin_block_desc {
   terra_swin_geom geom;
-  int32_t heads;        /* 6 or 12 heads of dim 32, or 12 of dim 64     */
+  int32_t heads;        /* see terra_swin_block_fwd for the shapes      */
   float scale;          /* q k^T scale (head_dim^-0.5 in the reference) */
   float ln_eps;         /* LayerNorm eps                                */
   float mask_value;     /* -100.0 in the reference                      */
@@ -241,8 +241,9 @@ int terra_swin_attn_bwd(const void* q, const void* k, const void* v, const void*
                         float* dbias_table, const float* explicit_mask,
                         const uint64_t* land_bits, void* stream);
 
-/* Fused Swin attention half-block (bf16, 8x8 windows; C = 192 with 6 heads,
- * C = 384 with 12, or C = 768 with 12 heads of dim 64).
+/* Fused Swin attention half-block (bf16; 8x8 windows with C = 192 and 6 heads,
+ * C = 384 and 12, or C = 768 and 12 heads of dim 64; 7x7 windows with C = 128
+ * and 4 heads).
  * Replaces SequentialSwinTransformer.forward   models/transformer.py:142-300:
  *           x = self.norm1(x)                   models/transformer.py:98, 150
  *           roll(-s) + window_partition         models/transformer.py:179-225
@@ -256,7 +257,7 @@ int terra_swin_attn_bwd(const void* q, const void* k, const void* v, const void*
  * x, y: [B, H, W, C] bf16 contiguous; y may equal x (in place) but must not
  * overlap it otherwise.  qkv_weight [3C, C] and proj_weight [C, C] bf16
  * (nn.Linear layout); qkv_bias [3C], proj_bias [C], ln_gamma / ln_beta [C]
- * fp32 or NULL; bias_table fp32 [225, heads] or NULL.  Rounding follows the
+ * fp32 or NULL; bias_table fp32 [(2 window - 1)^2, heads] or NULL.  Rounding follows the
  * bf16 module: LayerNorm output, q/k/v, P, O and the proj output are rounded
  * to bf16, and the residual add is fp32 rounded once.
  */

@@ -151,7 +151,7 @@ __device__ __forceinline__ WindowMaskState block_mask_state(const BlockParams& p
   WindowMaskState m;
   m.wr = u.wr;
   m.wc = u.wc;
-  m.use_shift = p.shift_mask && ((u.wr + 2) * 8 > p.Hp || (u.wc + 2) * 8 > p.Wp);
+  m.use_shift = p.shift_mask && ((u.wr + 2) * p.a.window_h > p.Hp || (u.wc + 2) * p.a.window_w > p.Wp);
   // The land word through the scalar (constant) path: a vector load would be
   // waited for together with the next window's rows in flight.
   m.land = p.land_bits != nullptr
@@ -1005,6 +1005,396 @@ void swin_block_dw_kernel(const BlockParams p) {
 }
 
 // ============================================================================
+// swin_block_w7_kernel: 7x7 windows, 4 heads of dim 32, C = 128 (c2), a pair
+// of windows at a time.  Eight waves, one (window, head) unit each (unit w:
+// window w / 4, head w % 4).
+// ============================================================================
+//
+// A window's 49 tokens occupy rows 0..48 of a 64-row tile (rows 49..63 are
+// zero after the LayerNorm; their q / k / v are computed and never used:
+// keys >= 49 are excluded from the softmax, queries >= 49 are not stored).
+// The attention runs on the generic-geometry softmax of the attention core
+// (bias by relative index base(i) - off(j), shift regions and land keys per
+// token).  LDS: two row buffers for a pair (pair k's rows, overwritten by its
+// output rows; the other holds pair k - 1's output rows, then receives pair
+// k + 1's), one LayerNorm buffer that later holds O, and the tables.  Per pair:
+//
+//   wait for the pair's rows; LayerNorm (waves 4wi .. 4wi + 3 take window wi)
+//   barrier
+//   every wave: q/k/v of its unit (one pass: six row tiles x four token
+//           tiles, four k-steps) and its attention, O kept in registers; its
+//           share of pair k - 1's output rows out of the other buffer
+//   barrier (every LayerNorm row has been read)
+//   its share of pair k + 1's rows into the other buffer; O -> the O buffer
+//   barrier
+//   wave w: output features [32 (w & 3), + 32) of window w >> 2 = O W_p^T +
+//           b_p, plus the residual, in place over the window's rows
+//
+// Rows are 256 bytes (16 chunks): chunk c of row r sits in slot r * 16 +
+// (c ^ (r & 15)), so the 16 rows of a fragment read hit 16 different 16-byte
+// bank groups.
+namespace w7 {
+constexpr int kWs = 7, kN = kWs * kWs, kH = 4, kC = 128, kCpr = kC / 8, kKS = kC / 32;
+constexpr int kWaves = 8, kThreads = 64 * kWaves;
+constexpr int kTile = 64 * kC * 2;
+constexpr int kPair = 2 * kTile;
+constexpr int kOffO = 2 * kPair;
+constexpr int kOffTabs = kOffO + kPair;
+constexpr int kTab = 172;  // >= (2 * 7 - 1)^2 = 169, multiple of 4
+constexpr int kLds = kOffTabs + (kH * kTab + kC + kC + 3 * kC + kC) * 4;
+static_assert(kLds <= 160 * 1024, "LDS");
+
+__device__ __forceinline__ int slot(int row, int chunk) { return row * kCpr + (chunk ^ (row & 15)); }
+
+// Grid token of row `row` of window u (token (row / 7, row % 7)), or -1 for a
+// frame-padding token or a row past the window's 49.
+__device__ __forceinline__ int token(const BlockParams& p, const UnitLoc u, int row) {
+  if (row >= kN) return -1;
+  const int ti = row / kWs, tj = row - ti * kWs;
+  int ph = u.wr * kWs + ti + p.shift_h;
+  int pw = u.wc * kWs + tj + p.shift_w;
+  if (ph >= p.Hp) ph -= p.Hp;
+  if (pw >= p.Wp) pw -= p.Wp;
+  const int sh = ph - p.pad_top, sw = pw - p.pad_left;
+  if ((unsigned)sh >= (unsigned)p.H || (unsigned)sw >= (unsigned)p.W) return -1;
+  return (u.b * p.H + sh) * p.W + sw;
+}
+
+// The window's rows -> tile by kW waves (wave index wv), direct global -> LDS:
+// instruction r of wave wv fills slots (r * kW + wv) * 64 + lane.  Rows that
+// are not grid tokens load token 0 (never used).
+template <int kW>
+__device__ __forceinline__ void fetch(const BlockParams& p, const UnitLoc u, uint8_t* tile, int wv, int lane) {
+  constexpr int kRounds = 64 * kCpr / (64 * kW);
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int blk = r * kW + wv;
+    const int sl = blk * 64 + lane;
+    const int row = sl / kCpr;
+    const int ch = (sl - row * kCpr) ^ (row & 15);
+    const int t = token(p, u, row);
+    const uint8_t* src = p.x + (int64_t)(t >= 0 ? t : 0) * (kCpr * 16) + ch * 16;
+    dma_to_lds16(src, __builtin_amdgcn_readfirstlane(lds_address(tile + blk * 1024)));
+  }
+}
+
+// The window's rows (tile) -> the grid tokens they came from, by kW waves;
+// wave wv reads exactly the slots fetch<kW> fills from wave wv.
+template <int kW>
+__device__ __forceinline__ void store(const BlockParams& p, const UnitLoc u, const uint8_t* tile, int wv, int lane) {
+  constexpr int kRounds = 64 * kCpr / (64 * kW);
+  const __amdgpu_buffer_rsrc_t out =
+      buffer_rsrc(p.y + (int64_t)u.b * p.H * p.W * (kCpr * 16), (uint32_t)((int64_t)p.H * p.W * (kCpr * 16)));
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int sl = (r * kW + wv) * 64 + lane;
+    const int row = sl / kCpr;
+    const int ch = (sl - row * kCpr) ^ (row & 15);
+    const int t = token(p, u, row);
+    const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(tile + sl * 16));
+    // Rows that are not grid tokens fall outside the range.
+    stream_store_sc1(val, out, t >= 0 ? (uint32_t)(t - u.b * p.H * p.W) * (kCpr * 16) + ch * 16 : 0xfffffff0u);
+  }
+}
+
+// LayerNorm of the raw rows xr -> xn (bf16), 8 lanes per token, two-pass fp32
+// statistics over values held in registers; rows that are not grid tokens
+// become zeros; without LayerNorm the rows are copied.
+template <int kT>
+__device__ __forceinline__ void layernorm(const BlockParams& p, const UnitLoc u, const uint8_t* xr, uint8_t* xn,
+                                          const float* s_gamma, const float* s_beta, int tid) {
+  constexpr int kCPL = kCpr / 8;  // 2 chunks per lane
+  const int sub = tid & 7;
+  for (int t = tid >> 3; t < 64; t += kT / 8) {  // uniform per wave
+    const bool in = token(p, u, t) >= 0;
+    float v[kCPL][8];
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(xr + slot(t, sub + 8 * k) * 16);
+      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[k][2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
+        v[k][2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
+      }
+    }
+    float mean = 0.f, rstd = 1.f;
+    if (p.layernorm) {
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += v[k][e];
+      mean = group8_sum(sum) * p.inv_c;
+      float sq = 0.f;
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[k][e] - mean;
+          sq += d * d;
+        }
+      rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      const int c0 = (sub + 8 * k) * 8;
+      float yv[8];
+#pragma unroll
+      for (int q = 0; q < 8; q += 4) {
+        const float4 gm = *reinterpret_cast<const float4*>(s_gamma + c0 + q);
+        const float4 bt = *reinterpret_cast<const float4*>(s_beta + c0 + q);
+        if (p.layernorm) {
+          yv[q + 0] = (v[k][q + 0] - mean) * rstd * gm.x + bt.x;
+          yv[q + 1] = (v[k][q + 1] - mean) * rstd * gm.y + bt.y;
+          yv[q + 2] = (v[k][q + 2] - mean) * rstd * gm.z + bt.z;
+          yv[q + 3] = (v[k][q + 3] - mean) * rstd * gm.w + bt.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) yv[q + e] = v[k][q + e];
+        }
+      }
+      const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
+                                 pack_bf16x2(yv[6], yv[7]));
+      *reinterpret_cast<uint4*>(xn + slot(t, sub + 8 * k) * 16) = in ? o : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+}
+
+// q, k, v of head h for the tile's 64 rows in one pass (accumulator j: Q^T
+// row tiles 2h + j, K^T C/16 + 2h + j - 2, V C/8 + 2h + j - 4, the V tiles
+// as xn W^T), packed into attention operand fragments; Q unscaled (the
+// softmax applies scale * log2e).
+template <bool kPacked>
+__device__ __forceinline__ void unit_qkv(const BlockParams& p, const uint8_t* xn, int h, int lane, uint4 (&kf)[4][1],
+                                         uint4 (&vf)[2][2], uint4 (&qf)[4][1], const float* bqkv) {
+  const int g = lane >> 4, c16 = lane & 15;
+  auto rt = [&](int j) { return (j >> 1) * (kC / 16) + 2 * h + (j & 1); };
+  f32x4 acc[6][4];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    f32x4 b;
+    if (j < 4) {
+      b = load_f32x4(bqkv + (j >> 1) * kC + 32 * h + 16 * (j & 1) + 4 * g);
+    } else {
+      const float bv = bqkv[2 * kC + 32 * h + 16 * (j & 1) + c16];
+      b = f32x4{bv, bv, bv, bv};
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) acc[j][tt] = b;
+  }
+  auto xn_frag = [&](int tt, int ks) -> uint4 {
+    const int row = 16 * tt + c16;
+    return *reinterpret_cast<const uint4*>(xn + slot(row, 4 * ks + g) * 16);
+  };
+  uint4 ring[2][6];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) ring[0][j] = weight_frag<kC, kPacked>(p.w_qkv, rt(j), 0, lane);
+  uint4 xf[2][4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) xf[0][tt] = xn_frag(tt, 0);
+#pragma unroll
+  for (int ks = 0; ks < kKS; ++ks) {
+    if (ks + 1 < kKS) {
+#pragma unroll
+      for (int j = 0; j < 6; ++j) ring[(ks + 1) & 1][j] = weight_frag<kC, kPacked>(p.w_qkv, rt(j), ks + 1, lane);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) xf[(ks + 1) & 1][tt] = xn_frag(tt, ks + 1);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const bf16x8 x8 = __builtin_bit_cast(bf16x8, xf[ks & 1][tt]);
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        const bf16x8 w8 = __builtin_bit_cast(bf16x8, ring[ks & 1][j]);
+        acc[j][tt] = j < 4 ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(w8, x8, acc[j][tt], 0, 0, 0)
+                           : __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, w8, acc[j][tt], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    kf[tt][0] = pack_frag(acc[2][tt], acc[3][tt]);
+    qf[tt][0] = pack_frag(acc[0][tt], acc[1][tt]);
+  }
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int js = 0; js < 2; ++js) vf[ct][js] = pack_frag(acc[4 + ct][2 * js], acc[4 + ct][2 * js + 1]);
+}
+
+// Attention of head h of window u from the unit's fragments; O (bf16) held in
+// opk[it][ct] (channels 32h + 16 ct + 4g .. + 3 of query 16 it + c).
+__device__ __forceinline__ void unit_attention(const BlockParams& p, const UnitLoc u, const float* tab, int lane,
+                                               const uint4 (&kf)[4][1], const uint4 (&vf)[2][2],
+                                               const uint4 (&qf)[4][1], uint2 (&opk)[4][2]) {
+  const WindowMaskState m = block_mask_state(p, u);
+  LaneGeom<false> lg;
+  lane_geom_init<false>(lg, p.a, m, tab, lane);
+  auto vsrc = [&](int ct, int js) -> bf16x8 { return __builtin_bit_cast(bf16x8, vf[ct][js]); };
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    f32x4 sc[2][4];
+    const uint4 (&qp)[2][1] = *reinterpret_cast<const uint4(*)[2][1]>(&qf[2 * half]);
+    scores_pair<true, 32>(sc, kf, qp);
+    float inv[2];
+    softmax_half<false, false>(sc, inv, half, p.a, m, lg, nullptr, lane);
+    f32x4 o[2][2];
+    pv_half<true, 32>(o, sc, lane, vsrc);
+#pragma unroll
+    for (int il = 0; il < 2; ++il)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const f32x4 v = o[ct][il] * inv[il];
+        opk[2 * half + il][ct] = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      }
+  }
+}
+
+// Output features [32 q4, 32 q4 + 32) of a window = O W_p^T + b_p (two row
+// tiles x four token tiles), then y = bf16(x + bf16(Y)) in place over the
+// window's raw rows.
+template <bool kPacked>
+__device__ __forceinline__ void proj_rows(const BlockParams& p, const uint8_t* o_tile, uint8_t* tile, int q4,
+                                          int lane, const float* bproj) {
+  const int g = lane >> 4, c16 = lane & 15;
+  f32x4 ya[2][4];
+#pragma unroll
+  for (int ft = 0; ft < 2; ++ft) {
+    const f32x4 b = load_f32x4(bproj + 32 * q4 + 16 * ft + 4 * g);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) ya[ft][tt] = b;
+  }
+  uint4 wf[kKS][2];
+#pragma unroll
+  for (int ks = 0; ks < kKS; ++ks)
+#pragma unroll
+    for (int ft = 0; ft < 2; ++ft) wf[ks][ft] = weight_frag<kC, kPacked>(p.w_proj, 2 * q4 + ft, ks, lane);
+#pragma unroll
+  for (int ks = 0; ks < kKS; ++ks) {
+    uint4 of[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+      of[tt] = *reinterpret_cast<const uint4*>(o_tile + slot(16 * tt + c16, 4 * ks + g) * 16);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int ft = 0; ft < 2; ++ft)
+        ya[ft][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[ks][ft]),
+                                                             __builtin_bit_cast(bf16x8, of[tt]), ya[ft][tt], 0, 0, 0);
+  }
+#pragma unroll
+  for (int ft = 0; ft < 2; ++ft) {
+    const int fb = 32 * q4 + 16 * ft + 4 * g;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+      residual_add4(tile + slot(16 * tt + c16, fb >> 3) * 16 + (fb & 7) * 2, ya[ft][tt]);
+  }
+}
+
+}  // namespace w7
+
+template <bool kPacked>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void swin_block_w7_kernel(const BlockParams p) {
+  using namespace w7;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* obuf = smem + kOffO;
+  float* tabs = reinterpret_cast<float*>(smem + kOffTabs);
+  float* s_gamma = tabs + kH * kTab;
+  float* s_beta = s_gamma + kC;
+  float* s_bqkv = s_beta + kC;
+  float* s_bproj = s_bqkv + 3 * kC;
+  const int tid0 = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  const int wwin = wave >> 2, h = wave & 3;  // this wave's unit: window wwin of the pair, head h
+  const int pairs = (p.units + 1) >> 1;
+  if ((int)blockIdx.x >= pairs) return;  // uniform across the workgroup
+  // Bias columns (x log2e, index e = relative index) and the small parameters.
+  for (int e = tid0; e < kH * kTab; e += kThreads) {
+    const int hh = e / kTab, i = e - hh * kTab;
+    tabs[e] = (p.bias_table != nullptr && i < (2 * kWs - 1) * (2 * kWs - 1)) ? p.bias_table[i * kH + hh] * kLog2e
+                                                                             : 0.f;
+  }
+  for (int c = tid0; c < kC; c += kThreads) {
+    s_gamma[c] = p.gamma != nullptr ? p.gamma[c] : 1.f;
+    s_beta[c] = p.beta != nullptr ? p.beta[c] : 0.f;
+    s_bproj[c] = p.b_proj != nullptr ? p.b_proj[c] : 0.f;
+  }
+  for (int c = tid0; c < 3 * kC; c += kThreads) s_bqkv[c] = p.b_qkv != nullptr ? p.b_qkv[c] : 0.f;
+  __syncthreads();
+  const int n = (pairs - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
+  auto first_unit = [&](int k) { return 2 * ((int)blockIdx.x + k * (int)gridDim.x); };
+  {  // the first pair's rows
+    const int u0 = first_unit(0);
+#pragma unroll
+    for (int wi = 0; wi < 2; ++wi)
+      if (u0 + wi < p.units) fetch<kWaves>(p, locate(p, u0 + wi), smem + wi * kTile, wave, tid0 & 63);
+  }
+
+  for (int k = 0; k < n; ++k) {
+    // Lane-derived addresses are recomputed per pair (the thread id passes
+    // through an empty asm) rather than hoisted and held across the loop.
+    int tid = tid0;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    uint8_t* rows = smem + (k & 1) * kPair;         // pair k's rows, later its output rows
+    uint8_t* other = smem + ((k + 1) & 1) * kPair;  // pair k - 1's output rows, then pair k + 1's rows
+    const int u0 = first_unit(k);
+    const UnitLoc cur = locate(p, u0 + wwin);
+    const bool live = u0 + wwin < p.units;
+    const bool on = live && cur.computed;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the pair's rows
+    lds_barrier();
+    if (on)
+      layernorm<kThreads / 2>(p, cur, rows + wwin * kTile, obuf + wwin * kTile, s_gamma, s_beta,
+                              tid & (kThreads / 2 - 1));
+    lds_barrier();  // LayerNorm rows ready
+    uint2 opk[4][2];
+    if (on) {
+      uint4 kf[4][1], vf[2][2], qf[4][1];
+      unit_qkv<kPacked>(p, obuf + wwin * kTile, h, lane, kf, vf, qf, s_bqkv);
+      unit_attention(p, cur, tabs + h * kTab, lane, kf, vf, qf, opk);
+    }
+    if (k > 0) {  // pair k - 1's output rows
+      const int up = first_unit(k - 1);
+#pragma unroll
+      for (int wi = 0; wi < 2; ++wi)
+        if (up + wi < p.units) store<kWaves>(p, locate(p, up + wi), other + wi * kTile, wave, lane);
+    }
+    lds_barrier();  // every LayerNorm row has been read: O may replace them
+    if (k + 1 < n) {  // pair k + 1's rows, over the slots this wave has just stored
+      const int u1 = first_unit(k + 1);
+#pragma unroll
+      for (int wi = 0; wi < 2; ++wi)
+        if (u1 + wi < p.units) fetch<kWaves>(p, locate(p, u1 + wi), other + wi * kTile, wave, lane);
+    }
+    if (on) {
+      uint8_t* ot = obuf + wwin * kTile;
+#pragma unroll
+      for (int it = 0; it < 4; ++it)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const int cc = 32 * h + 16 * ct + 4 * g;
+          *reinterpret_cast<uint2*>(ot + slot(16 * it + c16, cc >> 3) * 16 + (cc & 7) * 2) = opk[it][ct];
+        }
+    }
+    lds_barrier();  // O complete
+    if (on) proj_rows<kPacked>(p, obuf + wwin * kTile, rows + wwin * kTile, h, lane, s_bproj);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  lds_barrier();
+  {  // the last pair's output rows
+    const int u0 = first_unit(n - 1);
+#pragma unroll
+    for (int wi = 0; wi < 2; ++wi)
+      if (u0 + wi < p.units) store<kWaves>(p, locate(p, u0 + wi), smem + ((n - 1) & 1) * kPair + wi * kTile, wave,
+                                           tid0 & 63);
+  }
+}
+
+// ============================================================================
 // swin_block_hd64_kernel: 12 heads of dim 64, C = 768 (the reference model's
 // block, c4).  Eight waves, one window at a time: wave s < 4 owns heads 3s and
 // 3s + 1, wave s + 4 head 3s + 2, so each SIMD (holding waves s and s + 4)
@@ -1513,6 +1903,19 @@ int launch_block_dw(const BlockParams& p, hipStream_t s) {
   return p.packed ? launch_block_dw_layout<true>(p, s) : launch_block_dw_layout<false>(p, s);
 }
 
+template <bool kPacked>
+int launch_block_w7_layout(const BlockParams& p, hipStream_t s) {
+  static int resident[64] = {0};
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&swin_block_w7_kernel<kPacked>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, w7::kLds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  return launch_persistent(swin_block_w7_kernel<kPacked>, w7::kThreads, w7::kLds, (p.units + 1) / 2, p, s, resident);
+}
+
+int launch_block_w7(const BlockParams& p, hipStream_t s) {
+  return p.packed ? launch_block_w7_layout<true>(p, s) : launch_block_w7_layout<false>(p, s);
+}
+
 int launch_block_hd64(const BlockParams& p, hipStream_t s) {
   return p.packed ? launch_block_hd64_layout<true>(p, s) : launch_block_hd64_layout<false>(p, s);
 }
@@ -1555,11 +1958,15 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   const int st = validate_geom(&d.geom, &dims);
   if (st != TERRA_OK) return st;
   const terra_swin_geom& q = d.geom;
-  if (q.window != 8) return fail(TERRA_ERR_UNSUPPORTED, "the fused block kernel needs 8x8 windows (got %d)", q.window);
+  const bool w7 = q.window == 7 && d.heads == 4 && q.channels == 128;
+  if (q.window != 8 && !w7)
+    return fail(TERRA_ERR_UNSUPPORTED,
+                "the fused block kernel needs 8x8 windows, or 7x7 windows with 4 heads of dim 32 (window %d, heads %d, "
+                "channels %d)", q.window, d.heads, q.channels);
   const bool hd64 = d.heads == 12 && q.channels == 768;
-  if (!hd64 && d.heads != 6 && d.heads != 12)
+  if (!hd64 && !w7 && d.heads != 6 && d.heads != 12)
     return fail(TERRA_ERR_UNSUPPORTED, "the fused block kernel supports 6 or 12 heads (got %d)", d.heads);
-  if (!hd64 && q.channels != 32 * d.heads)
+  if (!hd64 && !w7 && q.channels != 32 * d.heads)
     return fail(TERRA_ERR_UNSUPPORTED,
                 "the fused block kernel needs head dim 32, or 12 heads of dim 64 (channels %d, heads %d)",
                 q.channels, d.heads);
@@ -1596,8 +2003,8 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   p.a.frame_w = (int32_t)dims.Wp;
   p.a.shift_h = q.shift_h;
   p.a.shift_w = q.shift_w;
-  p.a.window_h = p.a.window_w = 8;
-  p.a.N = p.a.n_geo = p.a.n_real = 64;
+  p.a.window_h = p.a.window_w = q.window;
+  p.a.N = p.a.n_geo = p.a.n_real = q.window * q.window;
   p.x = static_cast<const uint8_t*>(x);
   p.y = static_cast<uint8_t*>(y);
   p.gamma = ln_gamma;
@@ -1633,7 +2040,8 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   p.fd_nWw = FastDiv((uint32_t)dims.nWw);
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const int ls = hd64 ? launch_block_hd64(p, s) : (d.heads == 6 ? launch_block_dw(p, s) : launch_block<12>(p, s));
+  const int ls = w7 ? launch_block_w7(p, s)
+                 : hd64 ? launch_block_hd64(p, s) : (d.heads == 6 ? launch_block_dw(p, s) : launch_block<12>(p, s));
   if (ls != TERRA_OK) return ls;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "block kernel launch failed: %s", hipGetErrorString(e));

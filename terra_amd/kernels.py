@@ -425,16 +425,17 @@ def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return tuple(outs)
 
 
-# (heads, channels) the fused half-block serves: head dim 32 with 6 or 12
-# heads, and the reference model's 12 heads of dim 64.
-BLOCK_SHAPES = ((6, 192), (12, 384), (12, 768))
+# (window, heads, channels) the fused half-block serves: 8x8 windows with 6
+# or 12 heads of dim 32 or the reference model's 12 heads of dim 64, and 7x7
+# windows with 4 heads of dim 32.
+BLOCK_SHAPES = ((8, 6, 192), (8, 12, 384), (8, 12, 768), (7, 4, 128))
 
 
 def swin_block_supported(x: torch.Tensor, geom: WindowGeometry, num_heads: int) -> bool:
-    """Whether :func:`swin_block` serves this call (bf16 device tensor, 8x8
-    windows, (heads, channels) in BLOCK_SHAPES)."""
-    return (x.device.type == "cuda" and x.dtype == torch.bfloat16 and geom.window == 8
-            and (num_heads, geom.channels) in BLOCK_SHAPES)
+    """Whether :func:`swin_block` serves this call (bf16 device tensor,
+    (window, heads, channels) in BLOCK_SHAPES)."""
+    return (x.device.type == "cuda" and x.dtype == torch.bfloat16
+            and (geom.window, num_heads, geom.channels) in BLOCK_SHAPES)
 
 
 def pack_linear(weight: torch.Tensor) -> torch.Tensor:
@@ -498,8 +499,9 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
     table = None
     if bias_table is not None:
         _require_device(x, bias_table)
-        if tuple(bias_table.shape) != (225, num_heads):
-            raise ValueError(f"bias table must be [225, {num_heads}], got {tuple(bias_table.shape)}")
+        n_rel = (2 * geom.window - 1) ** 2
+        if tuple(bias_table.shape) != (n_rel, num_heads):
+            raise ValueError(f"bias table must be [{n_rel}, {num_heads}], got {tuple(bias_table.shape)}")
         table = bias_table.detach().to(torch.float32).contiguous()
     d = _lib.SwinBlockDesc()
     d.geom = geom.to_c()

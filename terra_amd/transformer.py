@@ -1,7 +1,8 @@
 """Drop-in ``SequentialSwinTransformer`` (models/transformer.py:71-356).
 
-The attention half of a Swin block on one GPU.  For bf16 activations, 8x8
-windows and C / heads in {192 / 6, 384 / 12, 768 / 12} the whole half-block is one HIP
+The attention half of a Swin block on one GPU.  For bf16 activations and
+(window, heads, C) in kernels.BLOCK_SHAPES (8x8 windows with 6, 12 or 12 heads
+at C = 192, 384, 768; 7x7 windows with 4 heads at C = 128) the whole half-block is one HIP
 kernel (``kernels.swin_block``: gather + LayerNorm + q/k/v + attention + proj
 + residual + scatter).  Otherwise:
 
@@ -112,8 +113,8 @@ class SequentialSwinTransformer(torch.nn.Module):
                 and row_bytes % 16 == 0 and row_bytes <= 1536)
 
     def _fusable_block(self, x: torch.Tensor, geom: WindowGeometry) -> bool:
-        """The whole half-block runs as one kernel: bf16, 8x8 windows, (heads,
-        C) in kernels.BLOCK_SHAPES, a plain LayerNorm (or none), biased q/k/v, and
+        """The whole half-block runs as one kernel: bf16, (window, heads, C) in
+        kernels.BLOCK_SHAPES, a plain LayerNorm (or none), biased q/k/v, and
         no gradient needed (the fused kernel is forward-only)."""
         attn = self.attn
         if not self.use_fused_block or not kernels.swin_block_supported(x, geom, attn.num_heads):

@@ -230,6 +230,7 @@ def _block_call(d, dtype=L.DTYPE_BF16, x=FAKE, land=None):
     ({}, {}, L.DTYPE_F32, -5, "bf16 only"),
     ({}, {}, 9, -2, "unknown dtype"),
     ({"window": 4}, {}, L.DTYPE_BF16, -5, "8x8 windows"),
+    ({"window": 7, "height": 14, "width": 14}, {}, L.DTYPE_BF16, -5, "7x7 windows with 4 heads"),
     ({"channels": 128}, {"heads": 4}, L.DTYPE_BF16, -5, "6 or 12 heads"),
     ({"channels": 384}, {"heads": 6}, L.DTYPE_BF16, -5, "head dim 32"),
     ({"height": 12}, {}, L.DTYPE_BF16, -3, "not a multiple of window"),

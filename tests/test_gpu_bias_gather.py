@@ -79,15 +79,15 @@ def test_attention_bias_gather_bit_exact(dev, dtype, ws, C, heads, kernel):
             assert ((got[:, ~hit] - miss).abs() <= tol).all(), (kernel, e, h)
 
 
-@pytest.mark.parametrize("C,heads", [(192, 6), (384, 12), (768, 12)])
-def test_fused_block_bias_gather_bit_exact(dev, C, heads):
+@pytest.mark.parametrize("C,heads,ws", [(192, 6, 8), (384, 12, 8), (768, 12, 8), (128, 4, 7)])
+def test_fused_block_bias_gather_bit_exact(dev, C, heads, ws):
     """The fused half-block kernel's gather, through its q/k/v and proj: no
     LayerNorm, q and k weights zero (q = k = 0), v and proj weights the
     identity, so y = x + (attention output) exactly.  Token values are the
     token's index within its window (W-MSA, shift 0), so y - x reads back the
     key each query was paired with."""
-    ws, N, T = 8, 64, 225
-    H, W = 16, 24
+    N, T = ws * ws, (2 * ws - 1) ** 2
+    H, W = 2 * ws, 3 * ws
     d = C // heads
     geom = WindowGeometry(1, H, W, C, ws)
     hh, ww = torch.meshgrid(torch.arange(H), torch.arange(W), indexing="ij")

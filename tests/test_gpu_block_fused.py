@@ -34,10 +34,10 @@ def _rel(out, ref):
 
 
 def _block(dev, H, W, C, heads, layer, land=None, pad=(0, 0, 0, 0), win_row_begin=0, win_rows=None, valid=None,
-           bias=True, gain_qkv=None, gain_proj=None):
+           bias=True, gain_qkv=None, gain_proj=None, window=8):
     gain_qkv = gain_qkv or (2.0 if C == 768 else 4.0)
     gain_proj = gain_proj or (8.0 if C == 768 else 16.0)
-    blk = SequentialSwinTransformer(layer_idx=layer, height=H, width=W, embedding_dim=C, window_size=8,
+    blk = SequentialSwinTransformer(layer_idx=layer, height=H, width=W, embedding_dim=C, window_size=window,
                                     num_heads=heads, init_seed_base=workloads.SEED_BASE, land_mask=land, pad=pad,
                                     win_row_begin=win_row_begin, win_rows=win_rows, valid_windows=valid,
                                     use_relative_position_bias=bias)
@@ -120,11 +120,41 @@ def test_fused_matches_five_stage_and_oracle(dev, case):
     _assert_matches_oracle(y_f, ref, x)
 
 
-def _emitted_tokens(B, H, W, pad, r0, rows, valid, shift):
+def _emitted_tokens(B, H, W, pad, r0, rows, valid, shift, window=8):
     ones = torch.ones(B, H, W, 1)
-    win = so.partition_frame(ones, 8, shift, shift, pad, r0, rows, valid)
-    back = so.reverse_frame(win, B, H, W, 8, shift, shift, pad, r0, rows, valid)
+    win = so.partition_frame(ones, window, shift, shift, pad, r0, rows, valid)
+    back = so.reverse_frame(win, B, H, W, window, shift, shift, pad, r0, rows, valid)
     return back.view(B, H * W) > 0
+
+
+# 7x7 windows, 4 heads of dim 32 (c2's block), shift 3 on odd layers:
+# (H, W, layer, land, pad, win_row_begin, win_rows, valid, bias)
+CASES_W7 = [
+    (28, 42, 1, True, (0, 0, 0, 0), 0, None, None, True),     # SW-MSA + land
+    (21, 28, 0, False, (0, 0, 0, 0), 0, None, None, False),   # W-MSA, no bias table
+    (35, 42, 1, True, (0, 7, 0, 0), 0, 4, (2, 20), True),     # slab rows, pad windows
+    (19, 26, 1, True, (1, 1, 0, 2), 1, 1, None, True),       # pad on all sides, one window row
+]
+
+
+@pytest.mark.parametrize("case", CASES_W7)
+def test_fused_w7_matches_five_stage_and_oracle(dev, case):
+    H, W, layer, land_on, pad, r0, rows, valid, bias = case
+    C, heads = 128, 4
+    land = workloads.land_mask(H, W, seed=450) if land_on else None
+    blk = _block(dev, H, W, C, heads, layer, land, pad, r0, rows, valid, bias, window=7)
+    assert blk.shift_size == (3 if layer % 2 else 0)
+    x = workloads.activations((2, H * W, C), 451, torch.bfloat16)
+    xd = x.to(dev)
+    y_f, y_u = _both_paths(blk, xd)
+    _assert_paths_agree(y_f, y_u, xd)
+    ref = so.swin_block_attention(x, H, W, 7, blk.shift_size, heads, _params(blk), land=land, pad=pad,
+                                  win_row_begin=r0, win_rows=rows, valid=valid)
+    _assert_matches_oracle(y_f, ref, x)
+    if rows is not None or valid is not None:  # tokens of windows the frame does not emit pass through
+        emitted = _emitted_tokens(2, H, W, pad, r0, rows, valid, blk.shift_size, window=7).to(dev)
+        assert (~emitted).any()
+        assert torch.equal(y_f[~emitted], xd[~emitted])
 
 
 @pytest.mark.parametrize("case", [c for c in CASES if c[8] is not None or c[9] is not None])
@@ -140,11 +170,11 @@ def test_fused_pass_through_tokens_are_exact(dev, case):
     assert not torch.equal(y[emitted], x[emitted])
 
 
-@pytest.mark.parametrize("C,heads", [(192, 6), (768, 12)])
-def test_fused_in_place_equals_out_of_place(dev, C, heads):
-    H, W = 32, 48
+@pytest.mark.parametrize("C,heads,window", [(192, 6, 8), (768, 12, 8), (128, 4, 7)])
+def test_fused_in_place_equals_out_of_place(dev, C, heads, window):
+    H, W = 4 * window, 6 * window
     land = workloads.land_mask(H, W, seed=403)
-    blk = _block(dev, H, W, C, heads, 1, land)
+    blk = _block(dev, H, W, C, heads, 1, land, window=window)
     x = workloads.activations((1, H, W, C), 404, torch.bfloat16).to(dev)
     geom = blk.geometry(1)
     mask = blk.window_mask(geom)
@@ -173,22 +203,24 @@ def test_fused_without_layernorm(dev, monkeypatch):
     _assert_matches_oracle(y_f, ref, x)
 
 
-@pytest.mark.parametrize("C,heads", [(192, 6), (768, 12)])
-def test_fused_deterministic(dev, C, heads):
-    blk = _block(dev, 32, 64, C, heads, 1, workloads.land_mask(32, 64, seed=406))
-    x = workloads.activations((1, 32 * 64, C), 407, torch.bfloat16).to(dev)
+@pytest.mark.parametrize("C,heads,window", [(192, 6, 8), (768, 12, 8), (128, 4, 7)])
+def test_fused_deterministic(dev, C, heads, window):
+    H, W = 4 * window, 8 * window
+    blk = _block(dev, H, W, C, heads, 1, workloads.land_mask(H, W, seed=406), window=window)
+    x = workloads.activations((1, H * W, C), 407, torch.bfloat16).to(dev)
     with torch.no_grad():
         a = blk(x)
         b = blk(x)
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("name,layer", [("c3", 1), ("c4", 0), ("c4", 1)])
+@pytest.mark.parametrize("name,layer", [("c3", 1), ("c4", 0), ("c4", 1), ("c2", 0), ("c2", 1)])
 def test_fused_full_size(dev, name, layer):
-    """The benchmark configuration (c3) and the reference model's block (c4,
-    C = 768, 12 heads of dim 64; W-MSA and SW-MSA) end to end with gained
-    weights (the attention term is O(1)): fused kernel vs the five-stage path
-    and vs the oracle, on y and normwise on y - x."""
+    """The benchmark configuration (c3), the reference model's block (c4,
+    C = 768, 12 heads of dim 64) and c2 (7x7 windows, 4 heads of dim 32),
+    W-MSA and SW-MSA, end to end with gained weights (the attention term is
+    O(1)): fused kernel vs the five-stage path and vs the oracle, on y and
+    normwise on y - x."""
     cfg = workloads.CONFIGS[name]
     land = workloads.land_mask(cfg.height, cfg.width, seed=42) if name == "c3" else None
     blk = gain_block(workloads.block_for(cfg, layer, land=land)).to(dev).to(torch.bfloat16)
@@ -208,11 +240,11 @@ def test_pack_linear_layout(dev):
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("C,heads", [(192, 6), (768, 12)])
-def test_fused_packed_equals_unpacked(dev, C, heads):
+@pytest.mark.parametrize("C,heads,window", [(192, 6, 8), (768, 12, 8), (128, 4, 7)])
+def test_fused_packed_equals_unpacked(dev, C, heads, window):
     """The weight layout changes only addresses: identical output bits."""
-    H, W = 16, 32
-    blk = _block(dev, H, W, C, heads, 1, workloads.land_mask(H, W, seed=421))
+    H, W = 2 * window, 4 * window
+    blk = _block(dev, H, W, C, heads, 1, workloads.land_mask(H, W, seed=421), window=window)
     x = workloads.activations((1, H, W, C), 422, torch.bfloat16).to(dev)
     geom = blk.geometry(1)
     mask = blk.window_mask(geom)
