@@ -132,8 +132,20 @@ __global__ __launch_bounds__(kThreads) void partition_kernel(const uint8_t* __re
 // (reduced over the 8 lanes with xor shuffles); y = (x - mean) * rstd *
 // gamma + beta in fp32, rounded once to the activation type.  Tokens that
 // partition would pad (frame padding, pad windows) are written as pad_value.
+// Rows of more than 48 chunks (C > 384 in bf16) take 16 lanes per token, so
+// that a lane holds at most 6 chunks: at 12 chunks per lane (C = 768) the
+// register footprint left too few waves to cover the load latency (43 % of
+// the HBM peak on c4).
 constexpr int kLnLanes = 8;
-constexpr int kLnTokensPerBlock = kThreads / kLnLanes;
+
+// Sum over the kL lanes of a token (DPP; the 16-lane step adds the row
+// mirror of the 8-lane sums).
+template <int kL>
+__device__ __forceinline__ float group_sum(float v) {
+  v = group8_sum(v);
+  if constexpr (kL == 16) v += dpp_move<0x140>(v);
+  return v;
+}
 
 template <int DT> struct LnElt;
 template <> struct LnElt<TERRA_DTYPE_F32> { static constexpr int kPerChunk = 4; };
@@ -194,24 +206,34 @@ struct LnParams {
 
 constexpr int kLnMaxChannels = 12 * kLnLanes * 8;  // 768: the widest bf16 row (1536 bytes)
 
-template <int DT, int CPL>
+template <int DT, int CPL, int kL>
 __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* __restrict__ x,
                                                                 uint8_t* __restrict__ win,
                                                                 const CopyGeom g, const LnParams ln) {
+  constexpr int kTokensPerBlock = kThreads / kL;
   constexpr int E = LnElt<DT>::kPerChunk;
-  // gamma / beta of all C channels, staged once per workgroup.
+  // gamma / beta of all C channels, staged once per workgroup.  Their loads
+  // are issued first and the row loads right after (vector memory completes
+  // in order, so the staging waits for gamma / beta only); the barrier is
+  // LDS-only, and the rows stay in flight across it.
   __shared__ __attribute__((aligned(16))) float s_gamma[kLnMaxChannels];
   __shared__ __attribute__((aligned(16))) float s_beta[kLnMaxChannels];
+  constexpr int kGB = kLnMaxChannels / kThreads;
+  static_assert(kGB * kThreads == kLnMaxChannels, "whole staging rounds");
   const int C = ln.chunks * E;
-  for (int c = threadIdx.x; c < C; c += kThreads) {
-    s_gamma[c] = ln.gamma != nullptr ? ln.gamma[c] : 1.f;
-    s_beta[c] = ln.beta != nullptr ? ln.beta[c] : 0.f;
+  float gv[kGB], bv[kGB];
+#pragma unroll
+  for (int i = 0; i < kGB; ++i) {
+    const int c = threadIdx.x + i * kThreads;
+    gv[i] = (ln.gamma != nullptr && c < C) ? ln.gamma[c] : 1.f;
+    bv[i] = (ln.beta != nullptr && c < C) ? ln.beta[c] : 0.f;
   }
-  __syncthreads();
+  asm volatile("" ::: "memory");  // the gamma / beta loads before the row loads
 
-  const uint32_t tok = blockIdx.x * kLnTokensPerBlock + threadIdx.x / kLnLanes;
-  const int sub = threadIdx.x & (kLnLanes - 1);
-  if (tok >= ln.tokens) return;  // whole 8-lane groups leave together
+  const uint32_t tok_raw = blockIdx.x * kTokensPerBlock + threadIdx.x / kL;
+  const bool live = tok_raw < ln.tokens;  // whole lane groups share it
+  const uint32_t tok = live ? tok_raw : 0u;
+  const int sub = threadIdx.x & (kL - 1);
   uint32_t w, t, b, wl, wr, wc, ti, tj;
   g.fd_N.divmod(tok, w, t);
   g.fd_nWe.divmod(w, b, wl);
@@ -233,12 +255,23 @@ __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* _
   u32x4 raw[CPL];
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
-    const int c = sub + kLnLanes * k;
+    const int c = sub + kL * k;
     raw[k] = __builtin_nontemporal_load((in && c < ln.chunks) ? src + c : reinterpret_cast<const u32x4*>(x));
   }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < kGB; ++i) {
+    const int c = threadIdx.x + i * kThreads;
+    if (c < C) {
+      s_gamma[c] = gv[i];
+      s_beta[c] = bv[i];
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (!live) return;
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
-    const int c = sub + kLnLanes * k;
+    const int c = sub + kL * k;
     unpack_chunk<DT>((in && c < ln.chunks) ? raw[k] : u32x4(0u), v[k]);
   }
   float sum = 0.f;
@@ -246,27 +279,27 @@ __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* _
   for (int k = 0; k < CPL; ++k)
 #pragma unroll
     for (int e = 0; e < E; ++e) sum += v[k][e];  // absent chunks hold zeros
-  const float mean = group8_sum(sum) * ln.inv_c;
+  const float mean = group_sum<kL>(sum) * ln.inv_c;
   float sq = 0.f;
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
-    const bool present = sub + kLnLanes * k < ln.chunks;
+    const bool present = sub + kL * k < ln.chunks;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const float d = v[k][e] - mean;
       sq += present ? d * d : 0.f;
     }
   }
-  const float rstd = rsqrtf(group8_sum(sq) * ln.inv_c + ln.eps);
+  const float rstd = rsqrtf(group_sum<kL>(sq) * ln.inv_c + ln.eps);
 
-  const uint32_t first = blockIdx.x * kLnTokensPerBlock;
+  const uint32_t first = blockIdx.x * kTokensPerBlock;
   const __amdgpu_buffer_rsrc_t out =
       buffer_rsrc(win + (int64_t)first * g.row_bytes,
-                  (uint32_t)(min(ln.tokens - first, (uint32_t)kLnTokensPerBlock) * g.row_bytes));
+                  (uint32_t)(min(ln.tokens - first, (uint32_t)kTokensPerBlock) * g.row_bytes));
   const uint32_t row_off = (tok - first) * (uint32_t)g.row_bytes;
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
-    const int c = sub + kLnLanes * k;
+    const int c = sub + kL * k;
     if (c < ln.chunks) {
       u32x4 val;
       if (in) {
@@ -462,10 +495,11 @@ void launch_partition(const void* x, void* win, const CopyGeom& g, hipStream_t s
   partition_kernel<VB><<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g);
 }
 
-template <int DT, int CPL>
+template <int DT, int CPL, int kL = kLnLanes>
 void launch_partition_ln(const void* x, void* win, const CopyGeom& g, const LnParams& ln, hipStream_t s) {
-  const uint32_t blocks = (ln.tokens + kLnTokensPerBlock - 1) / kLnTokensPerBlock;
-  partition_ln_kernel<DT, CPL><<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g, ln);
+  constexpr uint32_t kTokensPerBlock = kThreads / kL;
+  const uint32_t blocks = (ln.tokens + kTokensPerBlock - 1) / kTokensPerBlock;
+  partition_ln_kernel<DT, CPL, kL><<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g, ln);
 }
 
 template <int DT>
@@ -476,8 +510,8 @@ void dispatch_partition_ln(int cpl, const void* x, void* win, const CopyGeom& g,
   else if (cpl <= 3) launch_partition_ln<DT, 3>(x, win, g, ln, s);
   else if (cpl <= 4) launch_partition_ln<DT, 4>(x, win, g, ln, s);
   else if (cpl <= 6) launch_partition_ln<DT, 6>(x, win, g, ln, s);
-  else if (cpl <= 8) launch_partition_ln<DT, 8>(x, win, g, ln, s);
-  else launch_partition_ln<DT, 12>(x, win, g, ln, s);
+  else if (cpl <= 8) launch_partition_ln<DT, 4, 16>(x, win, g, ln, s);  // 16 lanes per token
+  else launch_partition_ln<DT, 6, 16>(x, win, g, ln, s);
 }
 
 template <int VB, int DT>

@@ -107,6 +107,8 @@ LN_CASES = [  # (B, H, W, C, ws, shift, pad, win_row_begin, win_rows, valid)
     (2, 20, 16, 384, 8, 4, (0, 4, 0, 0), 0, 2, (3, 4)),
     (1, 16, 16, 768, 8, 4, (0, 8, 0, 0), 0, 2, (1, 3)),
     (1, 6, 6, 64, 4, 2, (1, 1, 1, 1), 0, None, None),
+    (1, 8, 16, 512, 8, 4, (0, 0, 0, 0), 0, None, None),   # 16 lanes per token, 4 chunks each
+    (2, 8, 8, 640, 8, 0, (0, 0, 0, 0), 0, None, None),    # 16 lanes per token, last chunk group partial
 ]
 
 
