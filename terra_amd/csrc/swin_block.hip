@@ -187,7 +187,8 @@ __device__ __forceinline__ void fetch_window(const BlockParams& p, const UnitLoc
 
 // LayerNorm of the window rows xr -> xn (bf16).  Eight lanes own a token;
 // lane `sub` holds chunks sub + 8k, k < cpr/8.  Statistics are two-pass fp32
-// (reduced over the 8 lanes), y = (x - mean) * rsqrt(var + eps) * gamma + beta
+// (reduced over the 8 lanes), y = (x rstd - mean rstd) gamma + beta (two
+// FMAs per value, rstd = rsqrt(var + eps))
 // rounded once, with the per-lane summation order of terra_swin_partition_ln.
 // Frame-padding tokens get zeros.  With p.layernorm == 0 the rows
 // are copied.
@@ -254,6 +255,7 @@ __device__ __forceinline__ void layernorm_window(const BlockParams& p, const Uni
       }
     }
     const float rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+    const float nmr = -mean * rstd;
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
       float v[8];
@@ -264,10 +266,11 @@ __device__ __forceinline__ void layernorm_window(const BlockParams& p, const Uni
       for (int q = 0; q < 8; q += 4) {
         const float4 gm = *reinterpret_cast<const float4*>(s_gamma + c0 + q);
         const float4 bt = *reinterpret_cast<const float4*>(s_beta + c0 + q);
-        yv[q + 0] = (v[q + 0] - mean) * rstd * gm.x + bt.x;
-        yv[q + 1] = (v[q + 1] - mean) * rstd * gm.y + bt.y;
-        yv[q + 2] = (v[q + 2] - mean) * rstd * gm.z + bt.z;
-        yv[q + 3] = (v[q + 3] - mean) * rstd * gm.w + bt.w;
+        // (x - mean) rstd as x rstd + (-mean rstd): two FMAs per value.
+        yv[q + 0] = __builtin_fmaf(__builtin_fmaf(v[q + 0], rstd, nmr), gm.x, bt.x);
+        yv[q + 1] = __builtin_fmaf(__builtin_fmaf(v[q + 1], rstd, nmr), gm.y, bt.y);
+        yv[q + 2] = __builtin_fmaf(__builtin_fmaf(v[q + 2], rstd, nmr), gm.z, bt.z);
+        yv[q + 3] = __builtin_fmaf(__builtin_fmaf(v[q + 3], rstd, nmr), gm.w, bt.w);
       }
       const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
                                  pack_bf16x2(yv[6], yv[7]));
@@ -713,7 +716,8 @@ void swin_block_kernel(const BlockParams p) {
 //           rows: six row tiles x four token tiles, so each LayerNorm
 //           fragment feeds six MFMAs and each weight fragment four), its
 //           attention (O kept in registers), q/k/v of unit 3s + 1
-//   wave s + 4: q/k/v and attention of unit 3s + 2 (O kept in registers);
+//   wave s + 4: pair k - 1's output rows out of the other buffer, then q/k/v
+//           and attention of unit 3s + 2 (O kept in registers);
 //           pair k - 1's output rows out of the other buffer
 //   barrier (every LayerNorm row has been read)
 //   pair k + 1's rows into the other buffer (all waves); the held O and unit
@@ -866,6 +870,125 @@ __device__ __forceinline__ void proj_rows(const uint8_t* o_tile, uint8_t* tile, 
   }
 }
 
+// LayerNorm of a window's rows xr -> xn by 256 threads: eight lanes per token,
+// each lane group taking tokens t and t + 32 side by side (two independent
+// reduction chains in flight); fp32 two-pass statistics over values held in
+// registers, y = (x rstd - mean rstd) gamma + beta rounded once; frame-padding
+// tokens become zeros; without LayerNorm the rows are copied.
+__device__ __forceinline__ void layernorm_pair_rows(const BlockParams& p, const UnitLoc u, const uint8_t* xr,
+                                                    uint8_t* xn, const float* s_gamma, const float* s_beta,
+                                                    int tid) {
+  constexpr int kCPL = kCpr / 8;  // 3 chunks per lane
+  const int sub = tid & 7, t0 = tid >> 3;
+  if (!p.layernorm) {  // rows copied bit for bit, frame padding zeroed
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int t = t0 + 32 * q;
+      const bool in = grid_token(p, u, t >> 3, t & 7) >= 0;
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
+        *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) = in ? raw : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+    return;
+  }
+  float v[2][kCPL][8];
+  bool in[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int t = t0 + 32 * q;
+    in[q] = grid_token(p, u, t >> 3, t & 7) >= 0;
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
+      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[q][k][2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
+        v[q][k][2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
+      }
+    }
+  }
+  float mean[2], rstd[2];
+  {
+    float sum[2] = {0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum[q] += v[q][k][e];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) mean[q] = group8_sum(sum[q]) * p.inv_c;
+    float sq[2] = {0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[q][k][e] - mean[q];
+          sq[q] += d * d;
+        }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) rstd[q] = rsqrtf(group8_sum(sq[q]) * p.inv_c + p.eps);
+  }
+#pragma unroll
+  for (int k = 0; k < kCPL; ++k) {
+    const int c0 = (sub + 8 * k) * 8;
+    const float4 gm0 = *reinterpret_cast<const float4*>(s_gamma + c0);
+    const float4 gm1 = *reinterpret_cast<const float4*>(s_gamma + c0 + 4);
+    const float4 bt0 = *reinterpret_cast<const float4*>(s_beta + c0);
+    const float4 bt1 = *reinterpret_cast<const float4*>(s_beta + c0 + 4);
+    const float gm[8] = {gm0.x, gm0.y, gm0.z, gm0.w, gm1.x, gm1.y, gm1.z, gm1.w};
+    const float bt[8] = {bt0.x, bt0.y, bt0.z, bt0.w, bt1.x, bt1.y, bt1.z, bt1.w};
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int t = t0 + 32 * q;
+      const float nmr = -mean[q] * rstd[q];
+      float yv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) yv[e] = __builtin_fmaf(__builtin_fmaf(v[q][k][e], rstd[q], nmr), gm[e], bt[e]);
+      const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
+                                 pack_bf16x2(yv[6], yv[7]));
+      *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) = in[q] ? o : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+}
+
+// Whether every token of window u is an in-bounds grid token that no cyclic
+// shift wraps (97.7 % of c3's windows); then row r is grid token base +
+// (r >> 3) W + (r & 7), with base image-relative.
+__device__ __forceinline__ bool interior(const BlockParams& p, const UnitLoc u, int& base) {
+  const int sh0 = u.wr * 8 + p.shift_h - p.pad_top, sw0 = u.wc * 8 + p.shift_w - p.pad_left;
+  base = sh0 * p.W + sw0;
+  return u.wr * 8 + p.shift_h + 8 <= p.Hp && u.wc * 8 + p.shift_w + 8 <= p.Wp && sh0 >= 0 && sh0 + 8 <= p.H &&
+         sw0 >= 0 && sw0 + 8 <= p.W;
+}
+
+// The 64 rows of window u -> tile, as fetch_window<kCpr, kW> (the same slots
+// from the same wave), with the interior fast path.
+template <int kW>
+__device__ __forceinline__ void fetch_rows(const BlockParams& p, const UnitLoc u, uint8_t* tile, int wv, int lane) {
+  int base;
+  if (!interior(p, u, base)) {  // uniform per wave
+    fetch_window<kCpr, kW>(p, u, tile, wv, lane);
+    return;
+  }
+  constexpr int kRounds = 64 * kCpr / (64 * kW);
+  const uint8_t* img = p.x + ((int64_t)u.b * p.H * p.W + base) * (kCpr * 16);
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int blk = r * kW + wv;
+    const int sl = blk * 64 + lane;
+    const int row = sl / kCpr;
+    const int ch = (sl - row * kCpr) ^ ((row >> 1) & 7);
+    dma_to_lds16(img + ((row >> 3) * p.W + (row & 7)) * (kCpr * 16) + ch * 16,
+                 __builtin_amdgcn_readfirstlane(lds_address(tile + blk * 1024)));
+  }
+}
+
 // The output rows of a pair's windows (u0, u0 + 1; those < p.units) -> the
 // grid tokens they came from, by kW waves (wave index wv); frame-padding rows
 // are dropped.  Wave wv reads exactly the LDS slots that fetch_window<kCpr,
@@ -881,6 +1004,18 @@ __device__ __forceinline__ void store_pair(const BlockParams& p, int u0, const u
     const UnitLoc u = locate(p, u0 + wi);
     const __amdgpu_buffer_rsrc_t out =
         buffer_rsrc(p.y + (int64_t)u.b * p.H * p.W * (kCpr * 16), (uint32_t)((int64_t)p.H * p.W * (kCpr * 16)));
+    int base;
+    if (interior(p, u, base)) {  // uniform per wave
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+        const int sl = (r * kW + wv) * 64 + lane;
+        const int row = sl / kCpr;
+        const int ch = (sl - row * kCpr) ^ ((row >> 1) & 7);
+        const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(buf + wi * kTile + sl * 16));
+        stream_store_sc1(val, out, (uint32_t)(base + (row >> 3) * p.W + (row & 7)) * (kCpr * 16) + ch * 16);
+      }
+      continue;
+    }
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
       const int sl = (r * kW + wv) * 64 + lane;
@@ -920,7 +1055,7 @@ void swin_block_dw_kernel(const BlockParams p) {
     const int u0 = first_unit(0);
 #pragma unroll
     for (int wi = 0; wi < 2; ++wi)
-      if (u0 + wi < p.units) fetch_window<kCpr, kWaves>(p, locate(p, u0 + wi), smem + wi * kTile, wave, tid0 & 63);
+      if (u0 + wi < p.units) fetch_rows<kWaves>(p, locate(p, u0 + wi), smem + wi * kTile, wave, tid0 & 63);
   }
 
   for (int k = 0; k < n; ++k) {
@@ -939,8 +1074,8 @@ void swin_block_dw_kernel(const BlockParams p) {
       if (u < p.units) {
         const UnitLoc cur = locate(p, u);
         if (cur.computed)
-          layernorm_window<kCpr, kThreads / 2>(p, cur, rows + wwin * kTile, obuf + wwin * kTile, s_gamma, s_beta,
-                                               tid & (kThreads / 2 - 1));
+          layernorm_pair_rows(p, cur, rows + wwin * kTile, obuf + wwin * kTile, s_gamma, s_beta,
+                              tid & (kThreads / 2 - 1));
       }
     }
     lds_barrier();  // LayerNorm rows ready
@@ -956,15 +1091,15 @@ void swin_block_dw_kernel(const BlockParams p) {
     const int ua = 3 * s4 + (two ? 0 : 2), wia = ua >= kH ? 1 : 0, ha = ua - wia * kH;
     const UnitLoc cura = locate(p, u0 + wia);
     const bool ona = u0 + wia < p.units && cura.computed;
+    // Waves 4..7 store pair k - 1's output rows first, so that on each SIMD
+    // their q/k/v overlaps the other wave's attention and their attention
+    // the other wave's second q/k/v.
+    if (!two && k > 0) store_pair<4>(p, first_unit(k - 1), other, wave - 4, lane);
     if (ona) {
       unit_qkv<kPacked>(p, obuf + wia * kTile, ha, lane, kf4, vf, qf, s_bqkv);
       head_attention<kC, true>(p, cura, tabs + ha * kTableMax, ha, lane, kf4, vf, qf, nullptr, oa);
     }
-    if (two) {
-      if (onb) unit_qkv<kPacked>(p, obuf + wib * kTile, hb, lane, kf4, vf, qf, s_bqkv);
-    } else if (k > 0) {
-      store_pair<4>(p, first_unit(k - 1), other, wave - 4, lane);  // pair k - 1's output rows
-    }
+    if (onb) unit_qkv<kPacked>(p, obuf + wib * kTile, hb, lane, kf4, vf, qf, s_bqkv);
     lds_barrier();  // every LayerNorm row has been read: O may replace them
     // Pair k + 1's rows into the other buffer, issued ahead of the attention
     // (no vector-memory work of its own), so that they queue in front of no
@@ -973,7 +1108,7 @@ void swin_block_dw_kernel(const BlockParams p) {
       const int u1 = first_unit(k + 1);
 #pragma unroll
       for (int wi = 0; wi < 2; ++wi)
-        if (u1 + wi < p.units) fetch_window<kCpr, kWaves>(p, locate(p, u1 + wi), other + wi * kTile, wave, lane);
+        if (u1 + wi < p.units) fetch_rows<kWaves>(p, locate(p, u1 + wi), other + wi * kTile, wave, lane);
     }
     if (ona) {
       uint8_t* ot = obuf + wia * kTile;
