@@ -418,6 +418,12 @@ __device__ __forceinline__ void dma_to_lds16(const void* src, uint32_t lds_base)
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" : : "v"(src), "{m0}"(lds_base) : "memory");
 }
 
+// The same load without the streaming hint: the lines stay in L2 for a
+// kernel that reads the rows again from global memory (its residual add).
+__device__ __forceinline__ void dma_to_lds16_cached(const void* src, uint32_t lds_base) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_base) : "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }

@@ -1573,7 +1573,8 @@ __device__ __forceinline__ uint32_t frag_off(int tt, int ks, int lane) {
 }
 
 // The window's 64 rows -> the tile (frame-padding rows load grid token 0 and
-// are never used).
+// are never used), without the streaming hint: the residual add reads the
+// rows again from global memory, so they stay in L2.
 __device__ __forceinline__ void fetch(const BlockParams& p, const UnitLoc u, uint8_t* tile, int wave, int lane) {
   constexpr int kRounds = kCpr * 64 / (64 * kWaves);  // 12
 #pragma unroll
@@ -1584,7 +1585,7 @@ __device__ __forceinline__ void fetch(const BlockParams& p, const UnitLoc u, uin
     const int ch = (sl - row * kCpr) ^ (row & 15);
     const int t = grid_token(p, u, row >> 3, row & 7);
     const uint8_t* src = p.x + (int64_t)(t >= 0 ? t : 0) * (kCpr * 16) + ch * 16;
-    dma_to_lds16(src, __builtin_amdgcn_readfirstlane(lds_address(tile + blk * 1024)));
+    dma_to_lds16_cached(src, __builtin_amdgcn_readfirstlane(lds_address(tile + blk * 1024)));
   }
 }
 

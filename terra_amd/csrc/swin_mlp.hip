@@ -566,7 +566,12 @@ __device__ __forceinline__ void wide_fetch(const MlpParams& p, int t, uint8_t* d
     const int ch = (sl - row * S::kCpr) ^ (row & 15);
     const int tok = t * 64 + row;
     const uint8_t* src = p.x + ((int64_t)(tok < p.tokens ? tok : 0) * S::kCpr + ch) * 16;
-    dma_to_lds16(src, __builtin_amdgcn_readfirstlane(lds_address(dst + blk * 1024)));
+    // At C = 768 the epilogue reads the rows again from global memory for
+    // the residual: no streaming hint, so they stay in L2.
+    if constexpr (S::kRaw)
+      dma_to_lds16(src, __builtin_amdgcn_readfirstlane(lds_address(dst + blk * 1024)));
+    else
+      dma_to_lds16_cached(src, __builtin_amdgcn_readfirstlane(lds_address(dst + blk * 1024)));
   }
 }
 
