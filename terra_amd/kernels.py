@@ -8,6 +8,8 @@ without ``libterra_swin.so``, raises.
 from __future__ import annotations
 
 import ctypes
+import weakref
+from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Optional, Sequence, Tuple, Union
 
@@ -474,63 +476,143 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
     image] int64) adds ``mask_value`` on land keys.  ``packed_weights``: the
     two weights come from :func:`pack_linear` (flat).  ``out`` may be ``x``.
     """
-    dev = _require_device(x, qkv_weight, proj_weight)
-    code = _dtype_code(x, (torch.bfloat16,))
-    C = geom.channels
-    if tuple(x.shape) != (geom.batch, geom.height, geom.width, C) or not x.is_contiguous():
-        raise ValueError(f"x must be a contiguous [{geom.batch}, {geom.height}, {geom.width}, {C}] tensor")
-    for name, t, shape in (("qkv_weight", qkv_weight, (3 * C, C)), ("proj_weight", proj_weight, (C, C))):
-        ok_shape = t.numel() == shape[0] * shape[1] if packed_weights else tuple(t.shape) == shape
-        if not ok_shape or t.dtype != x.dtype or not t.is_contiguous():
-            raise ValueError(f"{name} must be a contiguous {x.dtype} tensor of shape {shape}"
-                             + (" (packed)" if packed_weights else ""))
+    given = (qkv_weight, qkv_bias, proj_weight, proj_bias, ln_weight, ln_bias, bias_table, land_bits)
+    key = ("block", tuple(map(id, given)), geom, num_heads, float(scale), float(ln_eps), bool(layernorm),
+           bool(shift_mask), float(mask_value), bool(packed_weights), x.shape, x.dtype, x.device)
+    return _prepared(key, given, lambda: _BlockLaunch(
+        x, geom, num_heads, scale, qkv_weight, qkv_bias, proj_weight, proj_bias, ln_weight, ln_bias, ln_eps,
+        layernorm, bias_table, shift_mask, land_bits, mask_value, packed_weights))(x, out)
 
-    def f32(t, n, name):
-        if t is None:
-            return None
-        _require_device(x, t)
-        if t.numel() != n:
-            raise ValueError(f"{name} must have {n} elements")
-        return t.detach().reshape(-1).to(torch.float32).contiguous()
 
-    params = (f32(ln_weight, C, "ln_weight") if layernorm else None,
-              f32(ln_bias, C, "ln_bias") if layernorm else None,
-              f32(qkv_bias, 3 * C, "qkv_bias"), f32(proj_bias, C, "proj_bias"))
-    table = None
-    if bias_table is not None:
-        _require_device(x, bias_table)
-        n_rel = (2 * geom.window - 1) ** 2
-        if tuple(bias_table.shape) != (n_rel, num_heads):
-            raise ValueError(f"bias table must be [{n_rel}, {num_heads}], got {tuple(bias_table.shape)}")
-        table = bias_table.detach().to(torch.float32).contiguous()
-    d = _lib.SwinBlockDesc()
-    d.geom = geom.to_c()
-    d.heads, d.scale, d.ln_eps, d.mask_value = num_heads, float(scale), float(ln_eps), float(mask_value)
-    d.layernorm, d.shift_mask = int(bool(layernorm)), int(bool(shift_mask))
-    d.land_windows = 0
-    d.packed_weights = int(bool(packed_weights))
-    if land_bits is not None:
-        _require_device(x, land_bits)
-        if land_bits.dtype != torch.int64 or land_bits.dim() != 1:
-            raise ValueError("land_bits must be a 1-D int64 tensor (one 64-bit key mask per window)")
-        n_land = land_bits.shape[0]
-        if n_land == 0 or geom.num_windows % n_land != 0 or n_land % geom.windows_per_image != 0:
-            raise ValueError(f"land_bits must hold the emitted windows of one image ({geom.windows_per_image}) "
-                             f"or of several whole images dividing the batch (got {n_land} for "
-                             f"{geom.num_windows} windows)")
-        land_bits = land_bits.contiguous()
-        d.land_windows = n_land
-    if out is None:
-        out = torch.empty_like(x)
-    elif tuple(out.shape) != tuple(x.shape) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
-        raise ValueError("out must be a contiguous tensor like x")
-    with torch.cuda.device(dev):
-        st = _lib.load().terra_swin_block_fwd(_ptr(x), _ptr(out), code, ctypes.byref(d), _ptr(params[0]),
-                                              _ptr(params[1]), _ptr(qkv_weight), _ptr(params[2]),
-                                              _ptr(proj_weight), _ptr(params[3]), _ptr(table), _ptr(land_bits),
-                                              _stream(dev))
-    _lib.check(st, "terra_swin_block_fwd")
-    return out
+# Prepared launches, keyed by the ids of the parameter tensors, the call's
+# scalars and the activation shape.  An entry holds weak references to those
+# tensors and their data pointers, and serves a call only while each
+# reference still names the tensor passed and its data pointer is unchanged
+# (so a reused id or a rebound ``.data`` builds a new entry).  Entries are
+# made only when the kernel reads the caller's tensors themselves (no
+# conversion copies), so in-place updates of them are seen by later calls,
+# and an entry keeps no tensor memory alive.
+_LAUNCHES: "OrderedDict" = OrderedDict()
+_LAUNCHES_MAX = 256
+
+
+def _prepared(key, given, build) -> "_Launch":
+    launch = _LAUNCHES.get(key)
+    if launch is None or not launch.serves(given):
+        launch = build()
+        if launch.keep is None:  # the kernel reads the caller's tensors as they are
+            launch.watch(given)
+            _LAUNCHES[key] = launch
+            if len(_LAUNCHES) > _LAUNCHES_MAX:
+                _LAUNCHES.popitem(last=False)
+    return launch
+
+
+class _Launch:
+    """A validated library call for one activation shape, dtype and device:
+    descriptor and parameter pointers built once; each call checks only x
+    and out.  Subclasses set desc, ptrs, fn, name, shape, dtype, device,
+    code and keep (the converted copies the pointers name, or None)."""
+
+    refs = ()
+    keep = None
+
+    def watch(self, given) -> None:
+        self.refs = tuple((None, 0) if t is None else (weakref.ref(t), t.data_ptr()) for t in given)
+
+    def serves(self, given) -> bool:
+        for (ref, ptr), t in zip(self.refs, given):
+            if t is None:
+                if ref is not None:
+                    return False
+            elif ref is None or ref() is not t or t.data_ptr() != ptr:
+                return False
+        return True
+
+    def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor]) -> torch.Tensor:
+        if x.shape != self.shape or x.dtype != self.dtype or x.device != self.device or not x.is_contiguous():
+            raise ValueError(f"x must be a contiguous {self.dtype} tensor of shape {tuple(self.shape)} on "
+                             f"{self.device}")
+        if out is None:
+            out = torch.empty_like(x)
+        elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous() or out.device != self.device:
+            raise ValueError("out must be a contiguous tensor like x")
+        dev = self.device
+        args = (x.data_ptr(), out.data_ptr(), self.code, ctypes.byref(self.desc)) + self.ptrs
+        if dev.index is not None and dev.index != torch.cuda.current_device():
+            with torch.cuda.device(dev):
+                st = self.fn(*args, _stream(dev))
+        else:
+            st = self.fn(*args, _stream(dev))
+        _lib.check(st, self.name)
+        return out
+
+
+class _BlockLaunch(_Launch):
+    """terra_swin_block_fwd with its checks (see :func:`swin_block`)."""
+
+    def __init__(self, x, geom, num_heads, scale, qkv_weight, qkv_bias, proj_weight, proj_bias, ln_weight, ln_bias,
+                 ln_eps, layernorm, bias_table, shift_mask, land_bits, mask_value, packed_weights):
+        dev = _require_device(x, qkv_weight, proj_weight)
+        code = _dtype_code(x, (torch.bfloat16,))
+        C = geom.channels
+        if tuple(x.shape) != (geom.batch, geom.height, geom.width, C) or not x.is_contiguous():
+            raise ValueError(f"x must be a contiguous [{geom.batch}, {geom.height}, {geom.width}, {C}] tensor")
+        for name, t, shape in (("qkv_weight", qkv_weight, (3 * C, C)), ("proj_weight", proj_weight, (C, C))):
+            ok_shape = t.numel() == shape[0] * shape[1] if packed_weights else tuple(t.shape) == shape
+            if not ok_shape or t.dtype != x.dtype or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous {x.dtype} tensor of shape {shape}"
+                                 + (" (packed)" if packed_weights else ""))
+        copies = []
+
+        def f32(t, n, name):
+            if t is None:
+                return None
+            _require_device(x, t)
+            if t.numel() != n:
+                raise ValueError(f"{name} must have {n} elements")
+            r = t.detach().reshape(-1).to(torch.float32).contiguous()
+            if r.data_ptr() != t.data_ptr():
+                copies.append(r)
+            return r
+
+        params = (f32(ln_weight, C, "ln_weight") if layernorm else None,
+                  f32(ln_bias, C, "ln_bias") if layernorm else None,
+                  f32(qkv_bias, 3 * C, "qkv_bias"), f32(proj_bias, C, "proj_bias"))
+        table = None
+        if bias_table is not None:
+            _require_device(x, bias_table)
+            n_rel = (2 * geom.window - 1) ** 2
+            if tuple(bias_table.shape) != (n_rel, num_heads):
+                raise ValueError(f"bias table must be [{n_rel}, {num_heads}], got {tuple(bias_table.shape)}")
+            table = bias_table.detach().to(torch.float32).contiguous()
+            if table.data_ptr() != bias_table.data_ptr():
+                copies.append(table)
+        d = _lib.SwinBlockDesc()
+        d.geom = geom.to_c()
+        d.heads, d.scale, d.ln_eps, d.mask_value = num_heads, float(scale), float(ln_eps), float(mask_value)
+        d.layernorm, d.shift_mask = int(bool(layernorm)), int(bool(shift_mask))
+        d.land_windows = 0
+        d.packed_weights = int(bool(packed_weights))
+        if land_bits is not None:
+            _require_device(x, land_bits)
+            if land_bits.dtype != torch.int64 or land_bits.dim() != 1:
+                raise ValueError("land_bits must be a 1-D int64 tensor (one 64-bit key mask per window)")
+            n_land = land_bits.shape[0]
+            if n_land == 0 or geom.num_windows % n_land != 0 or n_land % geom.windows_per_image != 0:
+                raise ValueError(f"land_bits must hold the emitted windows of one image ({geom.windows_per_image}) "
+                                 f"or of several whole images dividing the batch (got {n_land} for "
+                                 f"{geom.num_windows} windows)")
+            if not land_bits.is_contiguous():
+                land_bits = land_bits.contiguous()
+                copies.append(land_bits)
+            d.land_windows = n_land
+        self.desc = d
+        self.shape, self.dtype, self.device, self.code = x.shape, x.dtype, dev, code
+        self.keep = tuple(copies) or None  # converted copies live as long as this (uncached) launch
+        self.ptrs = (_ptr(params[0]), _ptr(params[1]), _ptr(qkv_weight), _ptr(params[2]), _ptr(proj_weight),
+                     _ptr(params[3]), _ptr(table), _ptr(land_bits))
+        self.fn, self.name = _lib.load().terra_swin_block_fwd, "terra_swin_block_fwd"
 
 
 MLP_CHANNELS = (128, 192, 384, 768)
@@ -557,43 +639,57 @@ def swin_mlp(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_bias: Optional[torch
     of the nn.Linear weights [4C, C] / [C, 4C]; biases and the LayerNorm
     affine are passed as fp32 (or None).  ``out`` may be ``x``.
     """
-    dev = _require_device(x, fc1_weight, fc2_weight)
-    code = _dtype_code(x, (torch.bfloat16,))
-    if not x.is_contiguous() or x.dim() < 1:
-        raise ValueError("x must be a contiguous [..., C] tensor")
-    C = x.shape[-1]
-    H = fc1_weight.numel() // C if C else 0
-    if not swin_mlp_supported(x, C, H):
-        raise ValueError(f"the fused MLP serves bf16 rows of C in {MLP_CHANNELS} with hidden 4C "
-                         f"(got {x.dtype}, C {C}, hidden {H})")
-    tokens = x.numel() // C
-    if tokens == 0:
+    given = (fc1_weight, fc1_bias, fc2_weight, fc2_bias, ln_weight, ln_bias)
+    key = ("mlp", tuple(map(id, given)), float(ln_eps), bool(layernorm), x.shape, x.dtype, x.device)
+    launch = _prepared(key, given, lambda: _MlpLaunch(x, fc1_weight, fc1_bias, fc2_weight, fc2_bias, ln_weight,
+                                                      ln_bias, ln_eps, layernorm))
+    if launch.desc is None:  # no tokens
         return x.clone() if out is None else out
-    for name, t, n in (("fc1_weight", fc1_weight, H * C), ("fc2_weight", fc2_weight, C * H)):
-        if t.numel() != n or t.dtype != x.dtype or not t.is_contiguous():
-            raise ValueError(f"{name} must be a contiguous packed {x.dtype} tensor of {n} elements")
+    return launch(x, out)
 
-    def f32(t, n, name):
-        if t is None:
-            return None
-        _require_device(x, t)
-        if t.numel() != n:
-            raise ValueError(f"{name} must have {n} elements")
-        return t.detach().reshape(-1).to(torch.float32).contiguous()
 
-    params = (f32(ln_weight, C, "ln_weight") if layernorm else None,
-              f32(ln_bias, C, "ln_bias") if layernorm else None,
-              f32(fc1_bias, H, "fc1_bias"), f32(fc2_bias, C, "fc2_bias"))
-    d = _lib.SwinMlpDesc()
-    d.tokens, d.channels, d.hidden = int(tokens), int(C), int(H)
-    d.layernorm, d.ln_eps = int(bool(layernorm)), float(ln_eps)
-    if out is None:
-        out = torch.empty_like(x)
-    elif tuple(out.shape) != tuple(x.shape) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
-        raise ValueError("out must be a contiguous tensor like x")
-    with torch.cuda.device(dev):
-        st = _lib.load().terra_swin_mlp_fwd(_ptr(x), _ptr(out), code, ctypes.byref(d), _ptr(params[0]),
-                                            _ptr(params[1]), _ptr(fc1_weight), _ptr(params[2]), _ptr(fc2_weight),
-                                            _ptr(params[3]), _stream(dev))
-    _lib.check(st, "terra_swin_mlp_fwd")
-    return out
+class _MlpLaunch(_Launch):
+    """terra_swin_mlp_fwd with its checks (see :func:`swin_mlp`)."""
+
+    def __init__(self, x, fc1_weight, fc1_bias, fc2_weight, fc2_bias, ln_weight, ln_bias, ln_eps, layernorm):
+        dev = _require_device(x, fc1_weight, fc2_weight)
+        code = _dtype_code(x, (torch.bfloat16,))
+        if not x.is_contiguous() or x.dim() < 1:
+            raise ValueError("x must be a contiguous [..., C] tensor")
+        C = x.shape[-1]
+        H = fc1_weight.numel() // C if C else 0
+        if not swin_mlp_supported(x, C, H):
+            raise ValueError(f"the fused MLP serves bf16 rows of C in {MLP_CHANNELS} with hidden 4C "
+                             f"(got {x.dtype}, C {C}, hidden {H})")
+        self.shape, self.dtype, self.device, self.code = x.shape, x.dtype, dev, code
+        tokens = x.numel() // C
+        self.desc = None
+        if tokens == 0:
+            return
+        for name, t, n in (("fc1_weight", fc1_weight, H * C), ("fc2_weight", fc2_weight, C * H)):
+            if t.numel() != n or t.dtype != x.dtype or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous packed {x.dtype} tensor of {n} elements")
+        copies = []
+
+        def f32(t, n, name):
+            if t is None:
+                return None
+            _require_device(x, t)
+            if t.numel() != n:
+                raise ValueError(f"{name} must have {n} elements")
+            r = t.detach().reshape(-1).to(torch.float32).contiguous()
+            if r.data_ptr() != t.data_ptr():
+                copies.append(r)
+            return r
+
+        params = (f32(ln_weight, C, "ln_weight") if layernorm else None,
+                  f32(ln_bias, C, "ln_bias") if layernorm else None,
+                  f32(fc1_bias, H, "fc1_bias"), f32(fc2_bias, C, "fc2_bias"))
+        d = _lib.SwinMlpDesc()
+        d.tokens, d.channels, d.hidden = int(tokens), int(C), int(H)
+        d.layernorm, d.ln_eps = int(bool(layernorm)), float(ln_eps)
+        self.desc = d
+        self.keep = tuple(copies) or None
+        self.ptrs = (_ptr(params[0]), _ptr(params[1]), _ptr(fc1_weight), _ptr(params[2]), _ptr(fc2_weight),
+                     _ptr(params[3]))
+        self.fn, self.name = _lib.load().terra_swin_mlp_fwd, "terra_swin_mlp_fwd"

@@ -78,6 +78,7 @@ class SequentialSwinTransformer(torch.nn.Module):
         else:
             self.land_mask = None
         self._land_bits_cache = {}
+        self._mask_cache = None
         # Run the whole half-block as one kernel where the shapes allow it
         # (see _fusable_block); False forces the five-stage path.
         self.use_fused_block = True
@@ -89,25 +90,30 @@ class SequentialSwinTransformer(torch.nn.Module):
 
     def window_mask(self, geom: WindowGeometry):
         """Mask argument of the attention core for this block, or None."""
-        shift = ShiftMask.from_geometry(geom) if (self.shift_size > 0 and self.use_attn_mask) else None
+        lm = self.land_mask
+        key = (geom, self.shift_size > 0 and self.use_attn_mask,
+               None if lm is None else (lm.device, lm.data_ptr(), lm._version))
+        cached = self._mask_cache
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        shift = ShiftMask.from_geometry(geom) if key[1] else None
         land = None
-        if self.land_mask is not None:
-            key = (self.land_mask.device, self.land_mask.data_ptr(), self.land_mask._version)
-            land = self._land_bits_cache.get(key)
+        if lm is not None:
+            land = self._land_bits_cache.get(key[2])
             if land is None:
-                land = land_window_bits(self.land_mask, WindowGeometry(
+                land = land_window_bits(lm, WindowGeometry(
                     1, geom.height, geom.width, 1, geom.window, geom.shift_h, geom.shift_w, geom.pad,
                     geom.win_row_begin, geom.win_rows, geom.valid))
-                self._land_bits_cache = {key: land}
-        if shift is None and land is None:
-            return None
-        return WindowMask(shift=shift, land_bits=land)
+                self._land_bits_cache = {key[2]: land}
+        mask = None if shift is None and land is None else WindowMask(shift=shift, land_bits=land)
+        self._mask_cache = (key, mask)
+        return mask
 
     def _fusable_norm(self, dtype: torch.dtype) -> bool:
         """norm1 is a plain LayerNorm over C that the gather kernel computes
         for activations of `dtype` (rows of whole 16-byte chunks, <= 1536 B)."""
         n = self.norm1
-        row_bytes = self.embedding_dim * torch.empty((), dtype=dtype).element_size()
+        row_bytes = self.embedding_dim * dtype.itemsize
         return (type(n) is torch.nn.LayerNorm and tuple(n.normalized_shape) == (self.embedding_dim,)
                 and dtype in (torch.float32, torch.float16, torch.bfloat16)
                 and row_bytes % 16 == 0 and row_bytes <= 1536)

@@ -259,3 +259,40 @@ def test_fused_packed_equals_unpacked(dev, C, heads, window):
                                packed_weights=True, **args)
         b = kernels.swin_block(x, geom, heads, attn.scale, shift_mask=True, land_bits=mask.land_bits, **plain)
     assert torch.equal(a, b)
+
+
+def test_fused_launch_cache_follows_parameter_changes(dev):
+    """kernels.swin_block reuses a prepared launch for the same parameter
+    tensors: an in-place update of one of them, a rebound ``.data`` and a
+    new batch size must each give the bits a fresh launch (fresh tensors)
+    gives, and the module must pick up an in-place update of its own
+    parameters."""
+    H, W, C, heads = 16, 32, 192, 6
+    blk = _block(dev, H, W, C, heads, 1, workloads.land_mask(H, W, seed=423))
+    x = workloads.activations((2, H, W, C), 424, torch.bfloat16).to(dev)
+    geom = blk.geometry(2)
+    mask = blk.window_mask(geom)
+    args = dict(blk._fused_args())
+    run = lambda xx, g, a: kernels.swin_block(xx, g, heads, blk.attn.scale, shift_mask=True,  # noqa: E731
+                                              land_bits=mask.land_bits, **a)
+    fresh = lambda a: {k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in a.items()}  # noqa: E731
+    with torch.no_grad():
+        y0 = run(x, geom, args)
+        assert torch.equal(run(x, geom, args), y0)
+        args["proj_bias"].add_(0.25)  # same tensor, same memory
+        y1 = run(x, geom, args)
+        assert not torch.equal(y1, y0)
+        assert torch.equal(y1, run(x, geom, fresh(args)))
+        args["qkv_bias"].data = args["qkv_bias"].data * 2.0  # same tensor object, new memory
+        y2 = run(x, geom, args)
+        assert not torch.equal(y2, y1)
+        assert torch.equal(y2, run(x, geom, fresh(args)))
+        g1 = blk.geometry(1)
+        assert torch.equal(run(x[:1].contiguous(), g1, args), y2[:1])
+        xs = x.view(2, H * W, C)
+        ya = blk(xs)
+        blk.attn.proj.bias.add_(0.5)
+        yb = blk(xs)
+        y_f, y_u = _both_paths(blk, xs)
+    assert torch.equal(yb, y_f) and not torch.equal(ya, yb)
+    _assert_paths_agree(y_f, y_u, xs)
