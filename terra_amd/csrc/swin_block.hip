@@ -870,11 +870,61 @@ __device__ __forceinline__ void proj_rows(const uint8_t* o_tile, uint8_t* tile, 
   }
 }
 
+// Whether window u's 64 tokens are eight whole 8-token runs of the grid that
+// neither wrap nor touch frame padding; base: the grid index of its first
+// token (then token r of the window is base + (r >> 3) W + (r & 7)).
+__device__ __forceinline__ bool interior(const BlockParams& p, const UnitLoc u, int& base) {
+  const int sh0 = u.wr * 8 + p.shift_h - p.pad_top, sw0 = u.wc * 8 + p.shift_w - p.pad_left;
+  base = sh0 * p.W + sw0;
+  return u.wr * 8 + p.shift_h + 8 <= p.Hp && u.wc * 8 + p.shift_w + 8 <= p.Wp && sh0 >= 0 && sh0 + 8 <= p.H &&
+         sw0 >= 0 && sw0 + 8 <= p.W;
+}
+
+// x rstd - mean rstd, times gamma plus beta, of the 24 bf16 values in w (a
+// lane's three chunks of one token), rounded once, to xn; zeros for a
+// frame-padding token (kAllIn: the window has none).
+template <bool kAllIn>
+__device__ __forceinline__ void layernorm_store(const uint32_t (&w)[2][kCpr / 8][4], const float (&mean)[2],
+                                                const float (&rstd)[2], const bool (&in)[2], uint8_t* xn,
+                                                const float* s_gamma, const float* s_beta, int t0, int sub) {
+#pragma unroll
+  for (int k = 0; k < kCpr / 8; ++k) {
+    const int c0 = (sub + 8 * k) * 8;
+    const float4 gm0 = *reinterpret_cast<const float4*>(s_gamma + c0);
+    const float4 gm1 = *reinterpret_cast<const float4*>(s_gamma + c0 + 4);
+    const float4 bt0 = *reinterpret_cast<const float4*>(s_beta + c0);
+    const float4 bt1 = *reinterpret_cast<const float4*>(s_beta + c0 + 4);
+    const float gm[8] = {gm0.x, gm0.y, gm0.z, gm0.w, gm1.x, gm1.y, gm1.z, gm1.w};
+    const float bt[8] = {bt0.x, bt0.y, bt0.z, bt0.w, bt1.x, bt1.y, bt1.z, bt1.w};
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int t = t0 + 32 * q;
+      const float nmr = -mean[q] * rstd[q];
+      float yv[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = __uint_as_float(w[q][k][i] << 16), hi = __uint_as_float(w[q][k][i] & 0xffff0000u);
+        yv[2 * i] = __builtin_fmaf(__builtin_fmaf(lo, rstd[q], nmr), gm[2 * i], bt[2 * i]);
+        yv[2 * i + 1] = __builtin_fmaf(__builtin_fmaf(hi, rstd[q], nmr), gm[2 * i + 1], bt[2 * i + 1]);
+      }
+      uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
+                           pack_bf16x2(yv[6], yv[7]));
+      if (!kAllIn && !in[q]) o = make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) = o;
+    }
+  }
+}
+
 // LayerNorm of a window's rows xr -> xn by 256 threads: eight lanes per token,
 // each lane group taking tokens t and t + 32 side by side (two independent
-// reduction chains in flight); fp32 two-pass statistics over values held in
-// registers, y = (x rstd - mean rstd) gamma + beta rounded once; frame-padding
-// tokens become zeros; without LayerNorm the rows are copied.
+// reduction chains in flight).  fp32 statistics in one pass of bf16 dot
+// products over the packed rows (sum against (1, 1), sum of squares against
+// the values themselves: the products are exact in fp32); where the mean is
+// large against the spread (mean^2 > 64 var, so that the single pass could
+// lose more than a part in 10^4 of the variance) the wave recomputes the
+// variance from the centred values.  y = (x rstd - mean rstd) gamma + beta
+// rounded once; frame-padding tokens become zeros; without LayerNorm the rows
+// are copied.
 __device__ __forceinline__ void layernorm_pair_rows(const BlockParams& p, const UnitLoc u, const uint8_t* xr,
                                                     uint8_t* xn, const float* s_gamma, const float* s_beta,
                                                     int tid) {
@@ -893,78 +943,67 @@ __device__ __forceinline__ void layernorm_pair_rows(const BlockParams& p, const 
     }
     return;
   }
-  float v[2][kCPL][8];
-  bool in[2];
+  uint32_t w[2][kCPL][4];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int t = t0 + 32 * q;
-    in[q] = grid_token(p, u, t >> 3, t & 7) >= 0;
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
       const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
-      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[q][k][2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
-        v[q][k][2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
-      }
+      w[q][k][0] = raw.x;
+      w[q][k][1] = raw.y;
+      w[q][k][2] = raw.z;
+      w[q][k][3] = raw.w;
     }
   }
-  float mean[2], rstd[2];
-  {
-    float sum[2] = {0.f, 0.f};
+  const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
+  float mean[2], var[2], rstd[2];
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+  for (int q = 0; q < 2; ++q) {
+    float s1[2] = {0.f, 0.f}, s2[2] = {0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < kCPL; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bf16x2 x2 = __builtin_bit_cast(bf16x2, w[q][k][i]);
+        s1[i & 1] = __builtin_amdgcn_fdot2_f32_bf16(x2, ones, s1[i & 1], false);
+        s2[i & 1] = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, s2[i & 1], false);
+      }
+    mean[q] = group8_sum(s1[0] + s1[1]) * p.inv_c;
+    var[q] = group8_sum(s2[0] + s2[1]) * p.inv_c - mean[q] * mean[q];
+  }
+  const bool far = mean[0] * mean[0] > 64.f * var[0] || mean[1] * mean[1] > 64.f * var[1];
+  if (__builtin_amdgcn_ballot_w64(far)) {  // uniform per wave
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      float sq = 0.f;
+      asm volatile("" : "+v"(mean[q]));  // keeps this rare pass a branch, not computed on every path
 #pragma unroll
       for (int k = 0; k < kCPL; ++k)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sum[q] += v[q][k][e];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) mean[q] = group8_sum(sum[q]) * p.inv_c;
-    float sq[2] = {0.f, 0.f};
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int k = 0; k < kCPL; ++k)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float d = v[q][k][e] - mean[q];
-          sq[q] += d * d;
+        for (int i = 0; i < 4; ++i) {
+          const float dl = __uint_as_float(w[q][k][i] << 16) - mean[q];
+          const float dh = __uint_as_float(w[q][k][i] & 0xffff0000u) - mean[q];
+          sq = __builtin_fmaf(dl, dl, sq);
+          sq = __builtin_fmaf(dh, dh, sq);
         }
-#pragma unroll
-    for (int q = 0; q < 2; ++q) rstd[q] = rsqrtf(group8_sum(sq[q]) * p.inv_c + p.eps);
+      var[q] = group8_sum(sq) * p.inv_c;
+    }
   }
 #pragma unroll
-  for (int k = 0; k < kCPL; ++k) {
-    const int c0 = (sub + 8 * k) * 8;
-    const float4 gm0 = *reinterpret_cast<const float4*>(s_gamma + c0);
-    const float4 gm1 = *reinterpret_cast<const float4*>(s_gamma + c0 + 4);
-    const float4 bt0 = *reinterpret_cast<const float4*>(s_beta + c0);
-    const float4 bt1 = *reinterpret_cast<const float4*>(s_beta + c0 + 4);
-    const float gm[8] = {gm0.x, gm0.y, gm0.z, gm0.w, gm1.x, gm1.y, gm1.z, gm1.w};
-    const float bt[8] = {bt0.x, bt0.y, bt0.z, bt0.w, bt1.x, bt1.y, bt1.z, bt1.w};
+  for (int q = 0; q < 2; ++q) rstd[q] = rsqrtf(fmaxf(var[q], 0.f) + p.eps);
+  int base;
+  bool in[2] = {true, true};
+  if (interior(p, u, base)) {  // uniform per wave: no frame padding in the window
+    layernorm_store<true>(w, mean, rstd, in, xn, s_gamma, s_beta, t0, sub);
+  } else {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int t = t0 + 32 * q;
-      const float nmr = -mean[q] * rstd[q];
-      float yv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) yv[e] = __builtin_fmaf(__builtin_fmaf(v[q][k][e], rstd[q], nmr), gm[e], bt[e]);
-      const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
-                                 pack_bf16x2(yv[6], yv[7]));
-      *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) = in[q] ? o : make_uint4(0u, 0u, 0u, 0u);
+      in[q] = grid_token(p, u, t >> 3, t & 7) >= 0;
     }
+    layernorm_store<false>(w, mean, rstd, in, xn, s_gamma, s_beta, t0, sub);
   }
-}
-
-// Whether every token of window u is an in-bounds grid token that no cyclic
-// shift wraps (97.7 % of c3's windows); then row r is grid token base +
-// (r >> 3) W + (r & 7), with base image-relative.
-__device__ __forceinline__ bool interior(const BlockParams& p, const UnitLoc u, int& base) {
-  const int sh0 = u.wr * 8 + p.shift_h - p.pad_top, sw0 = u.wc * 8 + p.shift_w - p.pad_left;
-  base = sh0 * p.W + sw0;
-  return u.wr * 8 + p.shift_h + 8 <= p.Hp && u.wc * 8 + p.shift_w + 8 <= p.Wp && sh0 >= 0 && sh0 + 8 <= p.H &&
-         sw0 >= 0 && sw0 + 8 <= p.W;
 }
 
 // The 64 rows of window u -> tile, as fetch_window<kCpr, kW> (the same slots

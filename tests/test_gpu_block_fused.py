@@ -296,3 +296,24 @@ def test_fused_launch_cache_follows_parameter_changes(dev):
         y_f, y_u = _both_paths(blk, xs)
     assert torch.equal(yb, y_f) and not torch.equal(ya, yb)
     _assert_paths_agree(y_f, y_u, xs)
+
+
+@pytest.mark.parametrize("C,heads,window", [(192, 6, 8), (384, 12, 8), (768, 12, 8), (128, 4, 7)])
+def test_fused_layernorm_large_mean(dev, C, heads, window):
+    """Tokens whose mean is large against their spread (every other grid row
+    offset by 10, so mean^2 / var ~ 100 there, beyond the 64 at which the
+    LayerNorm recomputes the variance from centred values, and ~0 elsewhere).
+    Fused kernel against the five-stage path and the oracle.  (At larger
+    offsets the bf16 rounding of y itself, 2^-9 |y|, dominates the normwise
+    check on y - x.)"""
+    H, W = 2 * window, 4 * window
+    land = workloads.land_mask(H, W, seed=425)
+    blk = _block(dev, H, W, C, heads, 1, land, window=window)
+    x = workloads.activations((1, H, W, C), 426, torch.float32)
+    x[:, ::2] += 10.0
+    x = x.to(torch.bfloat16).view(1, H * W, C)
+    xd = x.to(dev)
+    y_f, y_u = _both_paths(blk, xd)
+    _assert_paths_agree(y_f, y_u, xd)
+    ref = so.swin_block_attention(x, H, W, window, blk.shift_size, heads, _params(blk), land=land)
+    _assert_matches_oracle(y_f, ref, x)
