@@ -87,6 +87,80 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// ---- LayerNorm statistics from packed bf16 rows -----------------------------
+// A lane's partial moments of one token's values, accumulated from the packed
+// bf16 pairs by dot products (v_dot2_f32_bf16 against (1, 1) and against the
+// pair itself): the products are exact in fp32 and only the sums round.  Two
+// chains each (even / odd words), so consecutive words do not wait on each
+// other.
+struct Bf16Moments {
+  float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;
+
+  template <int kOdd>
+  __device__ __forceinline__ void add(uint32_t w) {
+    const bf16x2 x2 = __builtin_bit_cast(bf16x2, w);
+    const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
+    if (kOdd) {
+      s1b = __builtin_amdgcn_fdot2_f32_bf16(x2, ones, s1b, false);
+      s2b = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, s2b, false);
+    } else {
+      s1a = __builtin_amdgcn_fdot2_f32_bf16(x2, ones, s1a, false);
+      s2a = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, s2a, false);
+    }
+  }
+  __device__ __forceinline__ void add4(const uint4& r) {
+    add<0>(r.x);
+    add<1>(r.y);
+    add<0>(r.z);
+    add<1>(r.w);
+  }
+};
+
+// mean and var of a token whose values lie on an 8-lane group (inv_c = 1 / C),
+// from each lane's moments: var = E[x^2] - mean^2, which loses accuracy to
+// cancellation when the mean is large against the spread (the sums carry a
+// relative error of a few 2^-24 of mean^2 + var).  token_stats_recheck says
+// whether any lane of the wave has mean^2 > 64 var, i.e. could be off by more
+// than about 1e-4 of var; the wave then recomputes var from centred values
+// (centred_sq4 over the same chunks, group8_sum, times inv_c).  Every lane of
+// the wave must take part.
+__device__ __forceinline__ void token_stats8(const Bf16Moments& m, float inv_c, float& mean, float& var) {
+  mean = group8_sum(m.s1a + m.s1b) * inv_c;
+  var = group8_sum(m.s2a + m.s2b) * inv_c - mean * mean;
+}
+
+__device__ __forceinline__ bool token_stats_recheck(float mean, float var) {
+  return __builtin_amdgcn_ballot_w64(mean * mean > 64.f * var) != 0;
+}
+
+// sq + the sum of (x - mean)^2 over the eight bf16 values of a chunk.
+__device__ __forceinline__ float centred_sq4(const uint4& r, float mean, float sq) {
+  const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float dl = __uint_as_float(w4[i] << 16) - mean;
+    const float dh = __uint_as_float(w4[i] & 0xffff0000u) - mean;
+    sq = __builtin_fmaf(dl, dl, sq);
+    sq = __builtin_fmaf(dh, dh, sq);
+  }
+  return sq;
+}
+
+// y = (x rstd - mean rstd) gamma + beta of a chunk's eight bf16 values (two
+// FMAs per value: nmr = -mean rstd), rounded once to bf16.
+__device__ __forceinline__ uint4 normalize_chunk(const uint4& r, float rstd, float nmr, const float (&gm)[8],
+                                                 const float (&bt)[8]) {
+  const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = __uint_as_float(w4[i] << 16), hi = __uint_as_float(w4[i] & 0xffff0000u);
+    o[i] = pack_bf16x2(__builtin_fmaf(__builtin_fmaf(lo, rstd, nmr), gm[2 * i], bt[2 * i]),
+                       __builtin_fmaf(__builtin_fmaf(hi, rstd, nmr), gm[2 * i + 1], bt[2 * i + 1]));
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 // Mask state of one window (uniform across the wave).
 struct WindowMaskState {
   bool use_shift;     // window touches the last window row / column of the frame

@@ -186,94 +186,53 @@ __device__ __forceinline__ void fetch_window(const BlockParams& p, const UnitLoc
 }
 
 // LayerNorm of the window rows xr -> xn (bf16).  Eight lanes own a token;
-// lane `sub` holds chunks sub + 8k, k < cpr/8.  Statistics are two-pass fp32
-// (reduced over the 8 lanes), y = (x rstd - mean rstd) gamma + beta (two
-// FMAs per value, rstd = rsqrt(var + eps))
-// rounded once, with the per-lane summation order of terra_swin_partition_ln.
-// Frame-padding tokens get zeros.  With p.layernorm == 0 the rows
-// are copied.
+// lane `sub` holds chunks sub + 8k, k < cpr/8.  fp32 statistics from bf16 dot
+// products over the packed rows (Bf16Moments, token_stats8; the variance is
+// recomputed from centred values where the mean is large against the
+// spread), then y = (x rstd - mean rstd) gamma + beta (two FMAs per value,
+// rstd = rsqrt(var + eps)) rounded once; the rows are read from LDS once for
+// the statistics and once for the output.  Frame-padding tokens get zeros.
+// With p.layernorm == 0 the rows are copied.
 template <int kCpr, int kThreads>
 __device__ __forceinline__ void layernorm_window(const BlockParams& p, const UnitLoc u, const uint8_t* xr,
                                                  uint8_t* xn, const float* s_gamma, const float* s_beta, int tid) {
   constexpr int kTokPass = kThreads / 8;
   constexpr int kCPL = kCpr / 8;
   const int sub = tid & 7;
-  auto chunk = [&](int t, int k, float (&v)[8]) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
-    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
-      v[2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
-    }
-  };
+  auto raw = [&](int t, int k) { return *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16); };
   for (int t = tid >> 3; t < 64; t += kTokPass) {  // uniform per wave
     const bool in = grid_token(p, u, t >> 3, t & 7) >= 0;
     if (!p.layernorm) {
 #pragma unroll
-      for (int k = 0; k < kCPL; ++k) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
+      for (int k = 0; k < kCPL; ++k)
         *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) =
-            in ? raw : make_uint4(0u, 0u, 0u, 0u);
-      }
+            in ? raw(t, k) : make_uint4(0u, 0u, 0u, 0u);
       continue;
     }
-    // Narrow rows (<= 3 chunks per lane) keep their values in registers;
-    // wider rows re-read LDS for each pass.  Same arithmetic either way.
-    constexpr bool kHold = kCPL <= 3;
-    float vh[kHold ? kCPL : 1][8];
-    if constexpr (kHold) {
+    Bf16Moments m;
 #pragma unroll
-      for (int k = 0; k < kCPL; ++k) chunk(t, k, vh[k]);
+    for (int k = 0; k < kCPL; ++k) m.add4(raw(t, k));
+    float mean, var;
+    token_stats8(m, p.inv_c, mean, var);
+    if (token_stats_recheck(mean, var)) {  // uniform per wave
+      asm volatile("" : "+v"(mean));  // keeps this rare pass a branch, not computed on every path
+      float sq = 0.f;
+#pragma unroll
+      for (int k = 0; k < kCPL; ++k) sq = centred_sq4(raw(t, k), mean, sq);
+      var = group8_sum(sq) * p.inv_c;
     }
-    auto values = [&](int k, float (&v)[8]) {
-      if constexpr (kHold) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = vh[k][e];
-      } else {
-        chunk(t, k, v);
-      }
-    };
-    float sum = 0.f;
-#pragma unroll
-    for (int k = 0; k < kCPL; ++k) {
-      float v[8];
-      values(k, v);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sum += v[e];
-    }
-    const float mean = group8_sum(sum) * p.inv_c;
-    float sq = 0.f;
-#pragma unroll
-    for (int k = 0; k < kCPL; ++k) {
-      float v[8];
-      values(k, v);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float d = v[e] - mean;
-        sq += d * d;
-      }
-    }
-    const float rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+    const float rstd = rsqrtf(fmaxf(var, 0.f) + p.eps);
     const float nmr = -mean * rstd;
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
-      float v[8];
-      values(k, v);
       const int c0 = (sub + 8 * k) * 8;
-      float yv[8];
-#pragma unroll
-      for (int q = 0; q < 8; q += 4) {
-        const float4 gm = *reinterpret_cast<const float4*>(s_gamma + c0 + q);
-        const float4 bt = *reinterpret_cast<const float4*>(s_beta + c0 + q);
-        // (x - mean) rstd as x rstd + (-mean rstd): two FMAs per value.
-        yv[q + 0] = __builtin_fmaf(__builtin_fmaf(v[q + 0], rstd, nmr), gm.x, bt.x);
-        yv[q + 1] = __builtin_fmaf(__builtin_fmaf(v[q + 1], rstd, nmr), gm.y, bt.y);
-        yv[q + 2] = __builtin_fmaf(__builtin_fmaf(v[q + 2], rstd, nmr), gm.z, bt.z);
-        yv[q + 3] = __builtin_fmaf(__builtin_fmaf(v[q + 3], rstd, nmr), gm.w, bt.w);
-      }
-      const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
-                                 pack_bf16x2(yv[6], yv[7]));
+      const float4 gm0 = *reinterpret_cast<const float4*>(s_gamma + c0);
+      const float4 gm1 = *reinterpret_cast<const float4*>(s_gamma + c0 + 4);
+      const float4 bt0 = *reinterpret_cast<const float4*>(s_beta + c0);
+      const float4 bt1 = *reinterpret_cast<const float4*>(s_beta + c0 + 4);
+      const float gm[8] = {gm0.x, gm0.y, gm0.z, gm0.w, gm1.x, gm1.y, gm1.z, gm1.w};
+      const float bt[8] = {bt0.x, bt0.y, bt0.z, bt0.w, bt1.x, bt1.y, bt1.z, bt1.w};
+      const uint4 o = normalize_chunk(raw(t, k), rstd, nmr, gm, bt);
       *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) = in ? o : make_uint4(0u, 0u, 0u, 0u);
     }
   }
@@ -880,11 +839,11 @@ __device__ __forceinline__ bool interior(const BlockParams& p, const UnitLoc u, 
          sw0 >= 0 && sw0 + 8 <= p.W;
 }
 
-// x rstd - mean rstd, times gamma plus beta, of the 24 bf16 values in w (a
-// lane's three chunks of one token), rounded once, to xn; zeros for a
-// frame-padding token (kAllIn: the window has none).
+// (x rstd - mean rstd) gamma + beta of a lane's three chunks of tokens t0 and
+// t0 + 32 (w), rounded once, to xn; zeros for a frame-padding token (kAllIn:
+// the window has none).
 template <bool kAllIn>
-__device__ __forceinline__ void layernorm_store(const uint32_t (&w)[2][kCpr / 8][4], const float (&mean)[2],
+__device__ __forceinline__ void layernorm_store(const uint4 (&w)[2][kCpr / 8], const float (&mean)[2],
                                                 const float (&rstd)[2], const bool (&in)[2], uint8_t* xn,
                                                 const float* s_gamma, const float* s_beta, int t0, int sub) {
 #pragma unroll
@@ -898,33 +857,20 @@ __device__ __forceinline__ void layernorm_store(const uint32_t (&w)[2][kCpr / 8]
     const float bt[8] = {bt0.x, bt0.y, bt0.z, bt0.w, bt1.x, bt1.y, bt1.z, bt1.w};
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int t = t0 + 32 * q;
-      const float nmr = -mean[q] * rstd[q];
-      float yv[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float lo = __uint_as_float(w[q][k][i] << 16), hi = __uint_as_float(w[q][k][i] & 0xffff0000u);
-        yv[2 * i] = __builtin_fmaf(__builtin_fmaf(lo, rstd[q], nmr), gm[2 * i], bt[2 * i]);
-        yv[2 * i + 1] = __builtin_fmaf(__builtin_fmaf(hi, rstd[q], nmr), gm[2 * i + 1], bt[2 * i + 1]);
-      }
-      uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
-                           pack_bf16x2(yv[6], yv[7]));
+      uint4 o = normalize_chunk(w[q][k], rstd[q], -mean[q] * rstd[q], gm, bt);
       if (!kAllIn && !in[q]) o = make_uint4(0u, 0u, 0u, 0u);
-      *reinterpret_cast<uint4*>(xn + tile_slot(t, sub + 8 * k, kCpr) * 16) = o;
+      *reinterpret_cast<uint4*>(xn + tile_slot(t0 + 32 * q, sub + 8 * k, kCpr) * 16) = o;
     }
   }
 }
 
 // LayerNorm of a window's rows xr -> xn by 256 threads: eight lanes per token,
 // each lane group taking tokens t and t + 32 side by side (two independent
-// reduction chains in flight).  fp32 statistics in one pass of bf16 dot
-// products over the packed rows (sum against (1, 1), sum of squares against
-// the values themselves: the products are exact in fp32); where the mean is
-// large against the spread (mean^2 > 64 var, so that the single pass could
-// lose more than a part in 10^4 of the variance) the wave recomputes the
-// variance from the centred values.  y = (x rstd - mean rstd) gamma + beta
-// rounded once; frame-padding tokens become zeros; without LayerNorm the rows
-// are copied.
+// reduction chains in flight), the values held in registers.  fp32 statistics
+// from bf16 dot products (Bf16Moments, token_stats8), recomputed from centred
+// values where the mean is large against the spread; y = (x rstd - mean rstd)
+// gamma + beta rounded once; frame-padding tokens become zeros; without
+// LayerNorm the rows are copied.
 __device__ __forceinline__ void layernorm_pair_rows(const BlockParams& p, const UnitLoc u, const uint8_t* xr,
                                                     uint8_t* xn, const float* s_gamma, const float* s_beta,
                                                     int tid) {
@@ -943,50 +889,27 @@ __device__ __forceinline__ void layernorm_pair_rows(const BlockParams& p, const 
     }
     return;
   }
-  uint32_t w[2][kCPL][4];
+  uint4 w[2][kCPL];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int t = t0 + 32 * q;
+  for (int q = 0; q < 2; ++q)
 #pragma unroll
-    for (int k = 0; k < kCPL; ++k) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + tile_slot(t, sub + 8 * k, kCpr) * 16);
-      w[q][k][0] = raw.x;
-      w[q][k][1] = raw.y;
-      w[q][k][2] = raw.z;
-      w[q][k][3] = raw.w;
-    }
-  }
-  const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
+    for (int k = 0; k < kCPL; ++k)
+      w[q][k] = *reinterpret_cast<const uint4*>(xr + tile_slot(t0 + 32 * q, sub + 8 * k, kCpr) * 16);
   float mean[2], var[2], rstd[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    float s1[2] = {0.f, 0.f}, s2[2] = {0.f, 0.f};
+    Bf16Moments m;
 #pragma unroll
-    for (int k = 0; k < kCPL; ++k)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bf16x2 x2 = __builtin_bit_cast(bf16x2, w[q][k][i]);
-        s1[i & 1] = __builtin_amdgcn_fdot2_f32_bf16(x2, ones, s1[i & 1], false);
-        s2[i & 1] = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, s2[i & 1], false);
-      }
-    mean[q] = group8_sum(s1[0] + s1[1]) * p.inv_c;
-    var[q] = group8_sum(s2[0] + s2[1]) * p.inv_c - mean[q] * mean[q];
+    for (int k = 0; k < kCPL; ++k) m.add4(w[q][k]);
+    token_stats8(m, p.inv_c, mean[q], var[q]);
   }
-  const bool far = mean[0] * mean[0] > 64.f * var[0] || mean[1] * mean[1] > 64.f * var[1];
-  if (__builtin_amdgcn_ballot_w64(far)) {  // uniform per wave
+  if (token_stats_recheck(mean[0], var[0]) | token_stats_recheck(mean[1], var[1])) {  // uniform per wave
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      float sq = 0.f;
       asm volatile("" : "+v"(mean[q]));  // keeps this rare pass a branch, not computed on every path
+      float sq = 0.f;
 #pragma unroll
-      for (int k = 0; k < kCPL; ++k)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float dl = __uint_as_float(w[q][k][i] << 16) - mean[q];
-          const float dh = __uint_as_float(w[q][k][i] & 0xffff0000u) - mean[q];
-          sq = __builtin_fmaf(dl, dl, sq);
-          sq = __builtin_fmaf(dh, dh, sq);
-        }
+      for (int k = 0; k < kCPL; ++k) sq = centred_sq4(w[q][k], mean[q], sq);
       var[q] = group8_sum(sq) * p.inv_c;
     }
   }
@@ -1271,9 +1194,12 @@ __device__ __forceinline__ void store(const BlockParams& p, const UnitLoc u, con
   }
 }
 
-// LayerNorm of the raw rows xr -> xn (bf16), 8 lanes per token, two-pass fp32
-// statistics over values held in registers; rows that are not grid tokens
-// become zeros; without LayerNorm the rows are copied.
+// LayerNorm of the raw rows xr -> xn (bf16), 8 lanes per token, the values
+// held in registers: fp32 statistics from bf16 dot products (Bf16Moments,
+// token_stats8; the variance recomputed from centred values where the mean is
+// large against the spread), y = (x rstd - mean rstd) gamma + beta rounded
+// once; rows that are not grid tokens become zeros; without LayerNorm the rows
+// are copied.
 template <int kT>
 __device__ __forceinline__ void layernorm(const BlockParams& p, const UnitLoc u, const uint8_t* xr, uint8_t* xn,
                                           const float* s_gamma, const float* s_beta, int tid) {
@@ -1281,55 +1207,39 @@ __device__ __forceinline__ void layernorm(const BlockParams& p, const UnitLoc u,
   const int sub = tid & 7;
   for (int t = tid >> 3; t < 64; t += kT / 8) {  // uniform per wave
     const bool in = token(p, u, t) >= 0;
-    float v[kCPL][8];
+    uint4 w[kCPL];
 #pragma unroll
-    for (int k = 0; k < kCPL; ++k) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + slot(t, sub + 8 * k) * 16);
-      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[k][2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
-        v[k][2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
-      }
-    }
-    float mean = 0.f, rstd = 1.f;
-    if (p.layernorm) {
-      float sum = 0.f;
+    for (int k = 0; k < kCPL; ++k) w[k] = *reinterpret_cast<const uint4*>(xr + slot(t, sub + 8 * k) * 16);
+    if (!p.layernorm) {
 #pragma unroll
       for (int k = 0; k < kCPL; ++k)
+        *reinterpret_cast<uint4*>(xn + slot(t, sub + 8 * k) * 16) = in ? w[k] : make_uint4(0u, 0u, 0u, 0u);
+      continue;
+    }
+    Bf16Moments m;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sum += v[k][e];
-      mean = group8_sum(sum) * p.inv_c;
+    for (int k = 0; k < kCPL; ++k) m.add4(w[k]);
+    float mean, var;
+    token_stats8(m, p.inv_c, mean, var);
+    if (token_stats_recheck(mean, var)) {  // uniform per wave
+      asm volatile("" : "+v"(mean));  // keeps this rare pass a branch, not computed on every path
       float sq = 0.f;
 #pragma unroll
-      for (int k = 0; k < kCPL; ++k)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float d = v[k][e] - mean;
-          sq += d * d;
-        }
-      rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+      for (int k = 0; k < kCPL; ++k) sq = centred_sq4(w[k], mean, sq);
+      var = group8_sum(sq) * p.inv_c;
     }
+    const float rstd = rsqrtf(fmaxf(var, 0.f) + p.eps);
+    const float nmr = -mean * rstd;
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
       const int c0 = (sub + 8 * k) * 8;
-      float yv[8];
-#pragma unroll
-      for (int q = 0; q < 8; q += 4) {
-        const float4 gm = *reinterpret_cast<const float4*>(s_gamma + c0 + q);
-        const float4 bt = *reinterpret_cast<const float4*>(s_beta + c0 + q);
-        if (p.layernorm) {
-          yv[q + 0] = (v[k][q + 0] - mean) * rstd * gm.x + bt.x;
-          yv[q + 1] = (v[k][q + 1] - mean) * rstd * gm.y + bt.y;
-          yv[q + 2] = (v[k][q + 2] - mean) * rstd * gm.z + bt.z;
-          yv[q + 3] = (v[k][q + 3] - mean) * rstd * gm.w + bt.w;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) yv[q + e] = v[k][q + e];
-        }
-      }
-      const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
-                                 pack_bf16x2(yv[6], yv[7]));
+      const float4 gm0 = *reinterpret_cast<const float4*>(s_gamma + c0);
+      const float4 gm1 = *reinterpret_cast<const float4*>(s_gamma + c0 + 4);
+      const float4 bt0 = *reinterpret_cast<const float4*>(s_beta + c0);
+      const float4 bt1 = *reinterpret_cast<const float4*>(s_beta + c0 + 4);
+      const float gm[8] = {gm0.x, gm0.y, gm0.z, gm0.w, gm1.x, gm1.y, gm1.z, gm1.w};
+      const float bt[8] = {bt0.x, bt0.y, bt0.z, bt0.w, bt1.x, bt1.y, bt1.z, bt1.w};
+      const uint4 o = normalize_chunk(w[k], rstd, nmr, gm, bt);
       *reinterpret_cast<uint4*>(xn + slot(t, sub + 8 * k) * 16) = in ? o : make_uint4(0u, 0u, 0u, 0u);
     }
   }
@@ -1628,21 +1538,16 @@ __device__ __forceinline__ void fetch(const BlockParams& p, const UnitLoc u, uin
   }
 }
 
-// LayerNorm of the raw rows in place (eight lanes per token, two-pass fp32
-// statistics re-reading LDS; frame-padding tokens become zeros; without
-// LayerNorm the rows are kept, padding zeroed).
+// LayerNorm of the raw rows in place (eight lanes per token; fp32 statistics
+// from bf16 dot products over the packed rows, Bf16Moments / token_stats8,
+// the variance recomputed from centred values where the mean is large against
+// the spread; the rows are read from LDS once for the statistics and once for
+// the output; frame-padding tokens become zeros; without LayerNorm the rows
+// are kept, padding zeroed).
 __device__ __forceinline__ void layernorm_in_place(const BlockParams& p, const UnitLoc u, uint8_t* tile, int tid) {
   constexpr int kCPL = kCpr / 8;  // 12 chunks per lane
   const int sub = tid & 7;
-  auto chunk = [&](int t, int k, float (&v)[8]) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(tile + slot(t, sub + 8 * k) * 16);
-    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
-      v[2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
-    }
-  };
+  auto raw = [&](int t, int k) { return *reinterpret_cast<const uint4*>(tile + slot(t, sub + 8 * k) * 16); };
   const float* gptr = p.gamma;
   const float* bptr = p.beta;
   asm volatile("" : "+s"(gptr), "+s"(bptr));  // read per window, not held in registers
@@ -1656,43 +1561,35 @@ __device__ __forceinline__ void layernorm_in_place(const BlockParams& p, const U
       }
       continue;
     }
-    float sum = 0.f;
+    Bf16Moments m;
 #pragma unroll
-    for (int k = 0; k < kCPL; ++k) {
-      float v[8];
-      chunk(t, k, v);
+    for (int k = 0; k < kCPL; ++k) m.add4(raw(t, k));
+    float mean, var;
+    token_stats8(m, p.inv_c, mean, var);
+    if (token_stats_recheck(mean, var)) {  // uniform over the active lanes
+      asm volatile("" : "+v"(mean));  // keeps this rare pass a branch, not computed on every path
+      float sq = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sum += v[e];
+      for (int k = 0; k < kCPL; ++k) sq = centred_sq4(raw(t, k), mean, sq);
+      var = group8_sum(sq) * p.inv_c;
     }
-    const float mean = group8_sum(sum) * p.inv_c;
-    float sq = 0.f;
+    const float rstd = rsqrtf(fmaxf(var, 0.f) + p.eps);
+    const float nmr = -mean * rstd;
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
-      float v[8];
-      chunk(t, k, v);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float d = v[e] - mean;
-        sq += d * d;
-      }
-    }
-    const float rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
-#pragma unroll
-    for (int k = 0; k < kCPL; ++k) {
-      float v[8];
-      chunk(t, k, v);
       const int c0 = (sub + 8 * k) * 8;
-      float yv[8];
+      float gm[8], bt[8];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const f32x4 gq = gptr != nullptr ? *reinterpret_cast<const f32x4*>(gptr + c0 + 4 * h) : f32x4{1.f, 1.f, 1.f, 1.f};
         const f32x4 bq = bptr != nullptr ? *reinterpret_cast<const f32x4*>(bptr + c0 + 4 * h) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) yv[4 * h + e] = (v[4 * h + e] - mean) * rstd * gq[e] + bq[e];
+        for (int e = 0; e < 4; ++e) {
+          gm[4 * h + e] = gq[e];
+          bt[4 * h + e] = bq[e];
+        }
       }
-      *reinterpret_cast<uint4*>(tile + slot(t, sub + 8 * k) * 16) =
-          make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
-                     pack_bf16x2(yv[6], yv[7]));
+      *reinterpret_cast<uint4*>(tile + slot(t, sub + 8 * k) * 16) = normalize_chunk(raw(t, k), rstd, nmr, gm, bt);
     }
   }
 }
