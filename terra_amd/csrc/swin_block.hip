@@ -1063,16 +1063,9 @@ void swin_block_dw_kernel(const BlockParams p) {
     }
     if (onb) unit_qkv<kPacked>(p, obuf + wib * kTile, hb, lane, kf4, vf, qf, s_bqkv);
     lds_barrier();  // every LayerNorm row has been read: O may replace them
-    // Pair k + 1's rows into the other buffer, issued ahead of the attention
-    // (no vector-memory work of its own), so that they queue in front of no
-    // q/k/v weight load.
-    if (k + 1 < n) {
-      const int u1 = first_unit(k + 1);
-#pragma unroll
-      for (int wi = 0; wi < 2; ++wi)
-        if (u1 + wi < p.units) fetch_rows<kWaves>(p, locate(p, u1 + wi), other + wi * kTile, wave, lane);
-    }
-    if (ona) {
+    const bool onp = u0 + wwin < p.units && locate(p, u0 + wwin).computed;  // this wave's proj
+    auto write_held_o = [&]() {
+      if (!ona) return;
       uint8_t* ot = obuf + wia * kTile;
 #pragma unroll
       for (int it = 0; it < 4; ++it)
@@ -1081,19 +1074,28 @@ void swin_block_dw_kernel(const BlockParams p) {
           const int cc = 32 * ha + 16 * ct + 4 * g;
           *reinterpret_cast<uint2*>(ot + tile_slot(16 * it + c16, cc >> 3, kCpr) * 16 + (cc & 7) * 2) = oa[it][ct];
         }
-    }
-    if (onb) head_attention<kC>(p, curb, tabs + hb * kTableMax, hb, lane, kf4, vf, qf, obuf + wib * kTile);
-    lds_barrier();  // O complete
-    {
-      const int u = u0 + wwin;
-      if (u < p.units) {
-        const UnitLoc cur = locate(p, u);
-        if (cur.computed) {
-          uint4 wproj[kKS][3];  // all of them up front: one wait, after the next pair's rows
-          proj_weights<kPacked>(p, s4, lane, wproj);
-          proj_rows(obuf + wwin * kTile, rows + wwin * kTile, s4, lane, s_bproj, wproj);
-        }
+    };
+    if (!two) {
+      // Waves 4..7, whose unit is done: pair k + 1's rows into the other
+      // buffer (the slots each of them stored from), in flight while waves
+      // 0..3 run the second attention.  Waves 0..3 then request their proj
+      // weights with no row loads queued ahead of them.
+      if (k + 1 < n) {
+        const int u1 = first_unit(k + 1);
+#pragma unroll
+        for (int wi = 0; wi < 2; ++wi)
+          if (u1 + wi < p.units) fetch_rows<4>(p, locate(p, u1 + wi), other + wi * kTile, wave - 4, lane);
       }
+      write_held_o();
+    } else {
+      write_held_o();
+      if (onb) head_attention<kC>(p, curb, tabs + hb * kTableMax, hb, lane, kf4, vf, qf, obuf + wib * kTile);
+    }
+    lds_barrier();  // O complete
+    if (onp) {
+      uint4 wproj[kKS][3];  // all of them up front: one wait
+      proj_weights<kPacked>(p, s4, lane, wproj);
+      proj_rows(obuf + wwin * kTile, rows + wwin * kTile, s4, lane, s_bproj, wproj);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
