@@ -257,6 +257,9 @@ def main():
         setattr(kernels, n, timed(k, orig[n]))
 
     prewarm = {"s": 0.0, "steps": 0}
+    # c1 and c2 fit in L2 + the Infinity Cache: their steps are timed cold, a
+    # 512 MiB write between steps (outside each step's event pair).
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if args.config in ("c1", "c2") else None
 
     def run(steps, warmup, prewarm_s=0.0):
         with torch.no_grad():
@@ -275,6 +278,18 @@ def main():
                 blk(x)
             torch.cuda.synchronize()
             recording["on"] = True
+            if flush is not None:
+                pairs = []
+                for i in range(steps):
+                    flush.fill_(i & 0xFF)
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    blk(x)
+                    e1.record()
+                    pairs.append((e0, e1))
+                torch.cuda.synchronize()
+                recording["on"] = False
+                return sum(a.elapsed_time(b) for a, b in pairs) / steps
             t0 = torch.cuda.Event(enable_timing=True)
             t1 = torch.cuda.Event(enable_timing=True)
             t0.record()
@@ -450,6 +465,8 @@ def main():
             "windows": B_,
             "tokens": tokens,
             "parallelism": "single GPU",
+            "cache": ("cold: a 512 MiB write between steps, each step between its own events" if flush is not None
+                      else "working set larger than L2 + Infinity Cache; steps back to back"),
         },
         "roofline": roofline,
         # The unfused path, for comparison.  Its kernels are timed alone, back to
