@@ -486,9 +486,10 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
 
 # Prepared launches, keyed by the ids of the parameter tensors, the call's
 # scalars and the activation shape.  An entry holds weak references to those
-# tensors and their data pointers, and serves a call only while each
-# reference still names the tensor passed and its data pointer is unchanged
-# (so a reused id or a rebound ``.data`` builds a new entry).  Entries are
+# tensors with their data pointers and sizes, and serves a call only while
+# each reference still names the tensor passed and its data pointer and size
+# are unchanged (so a reused id, a rebound ``.data`` or an in-place resize
+# builds a new entry).  Entries are
 # made only when the kernel reads the caller's tensors themselves (no
 # conversion copies), so in-place updates of them are seen by later calls,
 # and an entry keeps no tensor memory alive.
@@ -518,14 +519,14 @@ class _Launch:
     keep = None
 
     def watch(self, given) -> None:
-        self.refs = tuple((None, 0) if t is None else (weakref.ref(t), t.data_ptr()) for t in given)
+        self.refs = tuple((None, 0, 0) if t is None else (weakref.ref(t), t.data_ptr(), t.numel()) for t in given)
 
     def serves(self, given) -> bool:
-        for (ref, ptr), t in zip(self.refs, given):
+        for (ref, ptr, n), t in zip(self.refs, given):
             if t is None:
                 if ref is not None:
                     return False
-            elif ref is None or ref() is not t or t.data_ptr() != ptr:
+            elif ref is None or ref() is not t or t.data_ptr() != ptr or t.numel() != n:
                 return False
         return True
 
