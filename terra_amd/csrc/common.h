@@ -101,6 +101,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 typedef uint32_t stream_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t stream_u32x2 __attribute__((ext_vector_type(2)));
 
+// A 16-byte store with the nt policy.  For 128-byte row slices spread over
+// a strided tensor (the attention backward's gradients: three tensors, one
+// slice per token row and head pair) it measured 272 us against 278 us with
+// sc1 and 288 us with sc0 or no policy bits (c3); contiguous streams favour
+// sc1 (above).
+template <typename T>
+__device__ __forceinline__ void stream_store_nt(const T& v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  static_assert(sizeof(T) == 16, "16-byte stores");
+  stream_u32x4 w;
+  __builtin_memcpy(&w, &v, 16);
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, kCacheNt);
+}
+
 // Stores `v` at byte offset `off` of the descriptor's range.
 template <typename T>
 __device__ __forceinline__ void stream_store_sc1(T v, __amdgpu_buffer_rsrc_t r, uint32_t off) {

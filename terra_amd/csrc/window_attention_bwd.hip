@@ -339,7 +339,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
           const int row = row0 + kRowStep * u;
           if (!kWs8 && row >= n_rows) continue;
           const uint4 val = *reinterpret_cast<const uint4*>(src[t] + tile_slot(row, chunk0, lcpr) * 16);
-          stream_store_sc1(val, out, (uint32_t)(row * stride[t] + col) * 2);
+          stream_store_nt(val, out, (uint32_t)(row * stride[t] + col) * 2);
         }
       }
     }
