@@ -187,9 +187,12 @@ __device__ __forceinline__ void mlp_store(const MlpParams& p, int t, const uint8
   }
 }
 
-// LayerNorm of the 64 raw rows -> xn (bf16).  Eight lanes per token, two-pass
-// fp32 statistics over values held in registers; with layernorm == 0 the
-// identity (mean 0, rstd 1, gamma 1, beta 0).
+// LayerNorm of the 64 raw rows -> xn (bf16).  Eight lanes per token, the
+// values held in registers; fp32 statistics from bf16 dot products
+// (Bf16Moments, token_stats8; the variance recomputed from centred values
+// where the mean is large against the spread); y = (x rstd - mean rstd)
+// gamma + beta rounded once.  With layernorm == 0 the identity (mean 0,
+// rstd 1, gamma 1, beta 0: the bits are copied).
 template <int C, bool kAffineLds>
 __device__ __forceinline__ void mlp_layernorm(const MlpParams& p, const uint8_t* xr, uint8_t* xn, const float* s_gamma,
                                               const float* s_beta, int tid) {
@@ -204,35 +207,26 @@ __device__ __forceinline__ void mlp_layernorm(const MlpParams& p, const uint8_t*
   constexpr int kCpr = C / 8, kCPL = kCpr / 8;
   const int sub = tid & 7;
   for (int t = tid >> 3; t < 64; t += kMlpThreads / 8) {  // uniform per wave
-    float v[kCPL][8];
+    uint4 w[kCPL];
 #pragma unroll
-    for (int k = 0; k < kCPL; ++k) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + mlp_slot(t, sub + 8 * k) * 16);
-      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[k][2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
-        v[k][2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
-      }
-    }
+    for (int k = 0; k < kCPL; ++k) w[k] = *reinterpret_cast<const uint4*>(xr + mlp_slot(t, sub + 8 * k) * 16);
     float mean = 0.f, rstd = 1.f;
     if (p.layernorm) {
-      float sum = 0.f;
+      Bf16Moments m;
 #pragma unroll
-      for (int k = 0; k < kCPL; ++k)
+      for (int k = 0; k < kCPL; ++k) m.add4(w[k]);
+      float var;
+      token_stats8(m, p.inv_c, mean, var);
+      if (token_stats_recheck(mean, var)) {  // uniform per wave
+        asm volatile("" : "+v"(mean));  // keeps this rare pass a branch, not computed on every path
+        float sq = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sum += v[k][e];
-      mean = group8_sum(sum) * p.inv_c;
-      float sq = 0.f;
-#pragma unroll
-      for (int k = 0; k < kCPL; ++k)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float d = v[k][e] - mean;
-          sq += d * d;
-        }
-      rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+        for (int k = 0; k < kCPL; ++k) sq = centred_sq4(w[k], mean, sq);
+        var = group8_sum(sq) * p.inv_c;
+      }
+      rstd = rsqrtf(fmaxf(var, 0.f) + p.eps);
     }
+    const float nmr = -mean * rstd;
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
       const int c0 = (sub + 8 * k) * 8;
@@ -247,12 +241,7 @@ __device__ __forceinline__ void mlp_layernorm(const MlpParams& p, const uint8_t*
           bv[4 * h + e] = bq[e];
         }
       }
-      float yv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) yv[e] = (v[k][e] - mean) * rstd * gv[e] + bv[e];
-      const uint4 o = make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
-                                 pack_bf16x2(yv[6], yv[7]));
-      *reinterpret_cast<uint4*>(xn + mlp_slot(t, sub + 8 * k) * 16) = o;
+      *reinterpret_cast<uint4*>(xn + mlp_slot(t, sub + 8 * k) * 16) = normalize_chunk(w[k], rstd, nmr, gv, bv);
     }
   }
 }
@@ -594,9 +583,11 @@ __device__ __forceinline__ void wide_store(const MlpParams& p, int t, const uint
 }
 
 // LayerNorm of the tile's raw rows (xr) into xn (may be xr: in place, each
-// lane rewriting only the chunks it read).  Eight lanes per token; two-pass
-// fp32 statistics, values re-read from LDS for each pass; without LayerNorm
-// the identity.
+// lane rewriting only the chunks it read).  Eight lanes per token; fp32
+// statistics from bf16 dot products (Bf16Moments, token_stats8; the variance
+// recomputed from centred values where the mean is large against the
+// spread), the rows read from LDS once for the statistics and once for the
+// output; without LayerNorm the identity.
 template <int C>
 __device__ __forceinline__ void wide_layernorm(const MlpParams& p, const uint8_t* xr, uint8_t* xn, int tid) {
   using S = WideShape<C>;
@@ -605,56 +596,43 @@ __device__ __forceinline__ void wide_layernorm(const MlpParams& p, const uint8_t
   const float* gptr = p.layernorm ? p.gamma : nullptr;
   const float* bptr = p.layernorm ? p.beta : nullptr;
   asm volatile("" : "+s"(gptr), "+s"(bptr));  // read per tile, not held in registers
-  auto chunk = [&](int t, int k, float (&v)[8]) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(xr + wide_slot<S::kCpr>(t, sub + 8 * k) * 16);
-    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = bf16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
-      v[2 * i + 1] = bf16_bits_to_f32((uint16_t)(w4[i] >> 16));
-    }
+  auto raw = [&](int t, int k) {
+    return *reinterpret_cast<const uint4*>(xr + wide_slot<S::kCpr>(t, sub + 8 * k) * 16);
   };
   for (int t = tid >> 3; t < 64; t += S::kThreads / 8) {  // uniform per wave
     float mean = 0.f, rstd = 1.f;
     if (p.layernorm) {
-      float sum = 0.f;
+      Bf16Moments m;
 #pragma unroll
-      for (int k = 0; k < kCPL; ++k) {
-        float v[8];
-        chunk(t, k, v);
+      for (int k = 0; k < kCPL; ++k) m.add4(raw(t, k));
+      float var;
+      token_stats8(m, p.inv_c, mean, var);
+      if (token_stats_recheck(mean, var)) {  // uniform per wave
+        asm volatile("" : "+v"(mean));  // keeps this rare pass a branch, not computed on every path
+        float sq = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sum += v[e];
+        for (int k = 0; k < kCPL; ++k) sq = centred_sq4(raw(t, k), mean, sq);
+        var = group8_sum(sq) * p.inv_c;
       }
-      mean = group8_sum(sum) * p.inv_c;
-      float sq = 0.f;
-#pragma unroll
-      for (int k = 0; k < kCPL; ++k) {
-        float v[8];
-        chunk(t, k, v);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float d = v[e] - mean;
-          sq += d * d;
-        }
-      }
-      rstd = rsqrtf(group8_sum(sq) * p.inv_c + p.eps);
+      rstd = rsqrtf(fmaxf(var, 0.f) + p.eps);
     }
+    const float nmr = -mean * rstd;
 #pragma unroll
     for (int k = 0; k < kCPL; ++k) {
-      float v[8];
-      chunk(t, k, v);
       const int c0 = (sub + 8 * k) * 8;
-      float yv[8];
+      float gv[8], bv[8];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const f32x4 gq = gptr != nullptr ? *reinterpret_cast<const f32x4*>(gptr + c0 + 4 * h) : f32x4{1.f, 1.f, 1.f, 1.f};
         const f32x4 bq = bptr != nullptr ? *reinterpret_cast<const f32x4*>(bptr + c0 + 4 * h) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) yv[4 * h + e] = (v[4 * h + e] - mean) * rstd * gq[e] + bq[e];
+        for (int e = 0; e < 4; ++e) {
+          gv[4 * h + e] = gq[e];
+          bv[4 * h + e] = bq[e];
+        }
       }
       *reinterpret_cast<uint4*>(xn + wide_slot<S::kCpr>(t, sub + 8 * k) * 16) =
-          make_uint4(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]), pack_bf16x2(yv[4], yv[5]),
-                     pack_bf16x2(yv[6], yv[7]));
+          normalize_chunk(raw(t, k), rstd, nmr, gv, bv);
     }
   }
 }
