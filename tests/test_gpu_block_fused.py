@@ -317,3 +317,23 @@ def test_fused_layernorm_large_mean(dev, C, heads, window):
     _assert_paths_agree(y_f, y_u, xd)
     ref = so.swin_block_attention(x, H, W, window, blk.shift_size, heads, _params(blk), land=land)
     _assert_matches_oracle(y_f, ref, x)
+
+
+@pytest.mark.parametrize("C,heads,window", [(192, 6, 8), (384, 12, 8), (768, 12, 8), (128, 4, 7)])
+@pytest.mark.parametrize("layer", [0, 1])
+def test_fused_windows_all_on_land(dev, C, heads, window, layer):
+    """A window whose keys are all on land runs unmasked (the land term is the
+    same constant on every score, which the softmax cancels).  Land on the
+    left half of the grid gives all-land, mixed and land-free windows, W-MSA
+    and SW-MSA (shift-boundary windows keep their masks).  Fused kernel
+    against the five-stage path and the oracle."""
+    H, W = 4 * window, 6 * window
+    land = torch.zeros(H, W, dtype=torch.bool)
+    land[:, : 3 * window] = True
+    blk = _block(dev, H, W, C, heads, layer, land, window=window)
+    x = workloads.activations((1, H * W, C), 427, torch.bfloat16)
+    xd = x.to(dev)
+    y_f, y_u = _both_paths(blk, xd)
+    _assert_paths_agree(y_f, y_u, xd)
+    ref = so.swin_block_attention(x, H, W, window, blk.shift_size, heads, _params(blk), land=land)
+    _assert_matches_oracle(y_f, ref, x)
