@@ -261,6 +261,30 @@ def main():
     # 512 MiB write between steps (outside each step's event pair).
     flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if args.config in ("c1", "c2") else None
 
+    def steps_once(steps):
+        """The step `steps` times; ms per step.  Cold configurations: a
+        512 MiB write before each step and each step between its own events;
+        otherwise all steps back to back between one event pair."""
+        if flush is not None:
+            pairs = []
+            for i in range(steps):
+                flush.fill_(i & 0xFF)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                blk(x)
+                e1.record()
+                pairs.append((e0, e1))
+            torch.cuda.synchronize()
+            return sum(a.elapsed_time(b) for a, b in pairs) / steps
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            blk(x)
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps
+
     def run(steps, warmup, prewarm_s=0.0):
         with torch.no_grad():
             # Time-based pre-warm: the step repeated for `prewarm_s` seconds,
@@ -277,28 +301,15 @@ def main():
             for _ in range(warmup):
                 blk(x)
             torch.cuda.synchronize()
+            # The timed steps carry no per-launch events (an event pair around
+            # every launch adds about 3 % to a step); the same number of steps
+            # then runs again with events around each kernel launch, which
+            # give the per-launch times of the roofline.
+            ms = steps_once(steps)
             recording["on"] = True
-            if flush is not None:
-                pairs = []
-                for i in range(steps):
-                    flush.fill_(i & 0xFF)
-                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    e0.record()
-                    blk(x)
-                    e1.record()
-                    pairs.append((e0, e1))
-                torch.cuda.synchronize()
-                recording["on"] = False
-                return sum(a.elapsed_time(b) for a, b in pairs) / steps
-            t0 = torch.cuda.Event(enable_timing=True)
-            t1 = torch.cuda.Event(enable_timing=True)
-            t0.record()
-            for _ in range(steps):
-                blk(x)
-            t1.record()
-            torch.cuda.synchronize()
+            steps_once(steps)
             recording["on"] = False
-        return t0.elapsed_time(t1) / steps
+        return ms
 
     def isolated_us(key, reps=5, per=20):
         """Median over `reps` loops of `per` back-to-back launches of one
@@ -449,6 +460,8 @@ def main():
         "prewarm": {"seconds": prewarm["s"], "steps": prewarm["steps"],
                     "note": "untimed steps before the counted warm-up, so the clock has settled"},
         "ms_per_step": ms,
+        "timing": ("the timed steps carry no per-launch events; a second pass of as many steps records events "
+                   "around each kernel launch for the roofline's launch times"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
