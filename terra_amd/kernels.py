@@ -179,6 +179,8 @@ def swin_partition(x: torch.Tensor, geom: WindowGeometry, pad_value: float = 0.0
         out = torch.empty(shape, dtype=x.dtype, device=dev)
     elif tuple(out.shape) != shape or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
         raise ValueError(f"out must be a contiguous {x.dtype} tensor of shape {shape} on {dev}")
+    if geom.batch == 0:  # an empty batch: nothing to launch (torch returns the empty result)
+        return out
     c_geom = geom.to_c()
     with torch.cuda.device(dev):
         st = _lib.load().terra_swin_partition(_ptr(x), _ptr(out), code, ctypes.byref(c_geom),
@@ -217,6 +219,8 @@ def swin_partition_ln(x: torch.Tensor, geom: WindowGeometry, weight: Optional[to
         out = torch.empty(shape, dtype=x.dtype, device=dev)
     elif tuple(out.shape) != shape or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
         raise ValueError(f"out must be a contiguous {x.dtype} tensor of shape {shape} on {dev}")
+    if geom.batch == 0:
+        return out
     c_geom = geom.to_c()
     with torch.cuda.device(dev):
         st = _lib.load().terra_swin_partition_ln(_ptr(x), _ptr(out), code, ctypes.byref(c_geom), _ptr(params[0]),
@@ -247,6 +251,8 @@ def swin_reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional
     elif out.numel() != geom.batch * geom.height * geom.width * geom.channels or out.dtype != windows.dtype \
             or not out.is_contiguous() or out.device != dev:
         raise ValueError(f"out must be a contiguous {windows.dtype} tensor with {shape} elements on {dev}")
+    if geom.batch == 0:
+        return out.view(shape)
     c_geom = geom.to_c()
     with torch.cuda.device(dev):
         st = _lib.load().terra_swin_reverse(_ptr(windows), _ptr(out), _ptr(residual), code,
@@ -291,6 +297,8 @@ def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_head
     elif out.dtype != q.dtype or out.device != dev:
         raise ValueError(f"out must be a {q.dtype} tensor on {dev} (got {out.dtype} on {out.device})")
     os_ = _row_stride(out, "out", num_windows, tokens, channels)
+    if num_windows == 0:
+        return out
 
     d = _attn_desc(q, num_heads, window_size, scale, n_real, mask_value, pad_key_value, (qs, ks, vs, os_))
     table = _bias_table(bias_table, d)
@@ -406,6 +414,8 @@ def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             raise ValueError(f"{n} must be a {q.dtype} tensor on {dev}")
         outs.append(t)
     out_strides = tuple(_row_stride(t, n, num_windows, tokens, channels) for t, n in zip(outs, ("dq", "dk", "dv")))
+    if num_windows == 0:  # no windows: empty gradients, nothing added to dbias
+        return tuple(outs)
     bd = _lib.SwinAttnBwdDesc()
     bd.fwd = _attn_desc(q, num_heads, window_size, scale, n_real, mask_value, pad_key_value,
                         (strides[0], strides[1], strides[2], strides[3]))
@@ -476,6 +486,13 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
     image] int64) adds ``mask_value`` on land keys.  ``packed_weights``: the
     two weights come from :func:`pack_linear` (flat).  ``out`` may be ``x``.
     """
+    if geom.batch == 0 and x.numel() == 0:  # an empty batch: nothing to launch
+        _require_device(x)
+        if out is None:
+            return torch.empty_like(x)
+        if out.shape != x.shape or out.dtype != x.dtype:
+            raise ValueError("out must be a contiguous tensor like x")
+        return out
     given = (qkv_weight, qkv_bias, proj_weight, proj_bias, ln_weight, ln_bias, bias_table, land_bits)
     key = ("block", tuple(map(id, given)), geom, num_heads, float(scale), float(ln_eps), bool(layernorm),
            bool(shift_mask), float(mask_value), bool(packed_weights), x.shape, x.dtype, x.device)
