@@ -138,7 +138,8 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
         const int row = row0 + kRowStep * u;
         const int off = tile_slot(row, chunk0, cpr) * 16;
         const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(qs + off));
-        stream_store_sc1(val, out, (uint32_t)(row * p.o_stride + chunk0 * 8) * 2);
+        // nt: 128-byte slices of a strided tensor (40.7-41.0 against 41.4-41.5 us at c4 with sc1)
+        stream_store_nt(val, out, (uint32_t)(row * p.o_stride + chunk0 * 8) * 2);
       }
     }
     if (next >= units) break;
