@@ -632,17 +632,19 @@ struct MaskMode {
 // with raw q, logit_scale = scale * log2(e) (> 0) and the terms are divided by
 // scale.
 // land_term[jt][r]: mask term of land key 16jt + 4g + r, else 0 (read only
-// when the window has land keys); mask_term: the shift-region term.  kf[jt]:
-// K operand of key tile jt; vfrag(ct, js): V^T operand (keys 32js +
-// 16(e/4) + 4g + e%4); qf[q], rid_q[q]: Q operand and query region id of tile
-// it0 + q.  Returns per tile the unnormalised O^T tiles and 1 / (sum over keys
-// of the bf16 probabilities that enter P V), so that the normalised weights
-// sum to 1.
-template <int kMask, int NQ, class VFrag>
-__device__ __forceinline__ void attend_qtiles(f32x4 (&o)[NQ][2], float (&inv)[NQ], int it0, const uint4 (&kf)[4],
-                                              const uint4 (&qf)[NQ], const float* tabr, const WindowMaskState& m,
-                                              const f32x4 (&land_term)[4], uint64_t rid_pack, const int (&rid_q)[NQ],
-                                              float mask_term, float logit_scale, VFrag vfrag) {
+// when the window has land keys); mask_term: the shift-region term.
+// kf[jt][c]: K operand of key tile jt, k-step c (KF = head dim / 32 steps);
+// vfrag(ct, js): V^T operand of column tile ct (CT = head dim / 16 tiles;
+// keys 32js + 16(e/4) + 4g + e%4); qf[q][c], rid_q[q]: Q operand and query
+// region id of tile it0 + q.  Returns per tile the unnormalised O^T tiles and
+// 1 / (sum over keys of the bf16 probabilities that enter P V), so that the
+// normalised weights sum to 1.
+template <int kMask, int NQ, int KF, int CT, class VFrag>
+__device__ __forceinline__ void attend_qtiles(f32x4 (&o)[NQ][CT], float (&inv)[NQ], int it0,
+                                              const uint4 (&kf)[4][KF], const uint4 (&qf)[NQ][KF], const float* tabr,
+                                              const WindowMaskState& m, const f32x4 (&land_term)[4],
+                                              uint64_t rid_pack, const int (&rid_q)[NQ], float mask_term,
+                                              float logit_scale, VFrag vfrag) {
   // The NQ query tiles advance through each stage together, which gives the
   // scheduler independent MFMA / VALU chains to interleave.
   f32x4 s[NQ][4];
@@ -653,11 +655,13 @@ __device__ __forceinline__ void attend_qtiles(f32x4 (&o)[NQ][2], float (&inv)[NQ
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[q][jt][r] = tabr[30 * (3 - it0 - q + jt) + r];
 #pragma unroll
-  for (int q = 0; q < NQ; ++q)
+  for (int c = 0; c < KF; ++c)
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-      s[q][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt]),
-                                                         __builtin_bit_cast(bf16x8, qf[q]), s[q][jt], 0, 0, 0);
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+        s[q][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt][c]),
+                                                           __builtin_bit_cast(bf16x8, qf[q][c]), s[q][jt], 0, 0, 0);
   // Mask terms after the MFMA, on its result.
   if constexpr (kMask == kMaskShift) {  // boundary windows: region test per element, plus land keys
     const bool land = m.land != 0ull;
@@ -700,7 +704,8 @@ __device__ __forceinline__ void attend_qtiles(f32x4 (&o)[NQ][2], float (&inv)[NQ
   f32x4 rs[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
-    o[q][0] = o[q][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[q][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
     rs[q] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 #pragma unroll
@@ -713,13 +718,24 @@ __device__ __forceinline__ void attend_qtiles(f32x4 (&o)[NQ][2], float (&inv)[NQ
         wds[e / 2] = pack_bf16x2(s[q][2 * js + (e >> 2)][e & 3], s[q][2 * js + (e >> 2)][(e & 3) + 1]);
       const bf16x8 pf = __builtin_bit_cast(bf16x8, wds);
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
+      for (int ct = 0; ct < CT; ++ct)
         o[q][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag(ct, js), pf, o[q][ct], 0, 0, 0);
       rs[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, rs[q], 0, 0, 0);
     }
   }
 #pragma unroll
   for (int q = 0; q < NQ; ++q) inv[q] = __builtin_amdgcn_rcpf(rs[q][0]);
+}
+
+// Head dim 32: one k-step, two column tiles (K and Q operands as plain arrays).
+template <int kMask, int NQ, class VFrag>
+__device__ __forceinline__ void attend_qtiles(f32x4 (&o)[NQ][2], float (&inv)[NQ], int it0, const uint4 (&kf)[4],
+                                              const uint4 (&qf)[NQ], const float* tabr, const WindowMaskState& m,
+                                              const f32x4 (&land_term)[4], uint64_t rid_pack, const int (&rid_q)[NQ],
+                                              float mask_term, float logit_scale, VFrag vfrag) {
+  attend_qtiles<kMask, NQ, 1, 2>(o, inv, it0, reinterpret_cast<const uint4(&)[4][1]>(kf),
+                                 reinterpret_cast<const uint4(&)[NQ][1]>(qf), tabr, m, land_term, rid_pack, rid_q,
+                                 mask_term, logit_scale, vfrag);
 }
 
 }  // namespace

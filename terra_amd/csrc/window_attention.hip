@@ -161,23 +161,26 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
 
 constexpr int kRingBufs = 3;
 
-template <int G>
+template <int D, int G>
 constexpr int ring_lds_bytes() {
-  return kRingBufs * 3 * kNPad * (G * 4) * 16 + G * kTableMax * (int)sizeof(float);
+  return kRingBufs * 3 * kNPad * (G * D / 8) * 16 + G * kTableMax * (int)sizeof(float);
 }
 
-template <int G>
+template <int D, int G>
 __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  constexpr int D = 32;
+  constexpr int KF = D / 32;                      // k-steps of the score MFMA
+  constexpr int CT = D / 16;                      // output column tiles of P V
   constexpr int nthreads = G * 256;
   constexpr int cpr = G * D / 8;                  // chunks per row (multiple of 8)
   constexpr int tile_bytes = kNPad * cpr * 16;
   constexpr int unit_bytes = 3 * tile_bytes;
   constexpr int kRounds = unit_bytes / (nthreads * 16);  // 16-byte loads per thread per unit
   constexpr int kBlocksPerTile = tile_bytes / 1024;
+  constexpr int kOPer = kNPad * cpr / nthreads;   // O chunks per thread
   static_assert(cpr % 8 == 0 && kRounds * nthreads * 16 == unit_bytes, "whole 1 KB blocks per wave");
-  static_assert(kRounds == 3, "the vmcnt wait below counts 3 loads per thread per unit");
+  static_assert(kRounds == 3 || kRounds == 6, "the vmcnt wait below counts 3 or 6 loads per thread per unit");
+  static_assert(kOPer * nthreads == kNPad * cpr, "whole O chunks per thread");
   float* tables = reinterpret_cast<float*>(smem + kRingBufs * unit_bytes);
 
   const int tid = threadIdx.x;
@@ -237,8 +240,8 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
   issue(w, 0);
   if (w + wstride < windows) issue(w + wstride, 1);
   const float* tabr = lane_bias_rev(tab, lane);  // bias of element (it, jt, r) at tabr[30 (3 - it + jt) + r]
-  const int hc = head * 4;                        // first chunk of this head
-  const int orow = tid / cpr, ochunk = tid - (tid / cpr) * cpr;  // this thread's O chunk
+  const int hc = head * (D / 8);                  // first chunk of this head
+  const int orow = tid / cpr, ochunk = tid - (tid / cpr) * cpr;  // this thread's first O chunk
   for (int n = 0;; ++n) {
     const int buf = n % kRingBufs;
     const bool more = w + wstride < windows;
@@ -246,8 +249,12 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
     // loads are outstanding.  Loads complete in order among themselves, but
     // not in order with stores, so the count covers later loads only: with
     // the previous unit's O store still pending, vmcnt(3) waits for more.
-    if (more) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (more) {
+      if constexpr (kRounds == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     lds_barrier();                                // every wave's part of the unit is in LDS
     // Unit n + 2 goes into the buffer of unit n - 1, whose O every thread has
     // read out before the barrier above.
@@ -265,11 +272,14 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
       m.use_mask = m.use_shift || m.land != 0ull;
     }
     {
-      uint4 kf[4];
+      uint4 kf[4][KF], qp[1][KF];
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        kf[t] = *reinterpret_cast<const uint4*>(ks + tile_slot(16 * t + c16, hc + g, cpr) * 16);
-      const uint4 qf = *reinterpret_cast<const uint4*>(qs + tile_slot(16 * it + c16, hc + g, cpr) * 16);
+      for (int c = 0; c < KF; ++c) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          kf[t][c] = *reinterpret_cast<const uint4*>(ks + tile_slot(16 * t + c16, hc + 4 * c + g, cpr) * 16);
+        qp[0][c] = *reinterpret_cast<const uint4*>(qs + tile_slot(16 * it + c16, hc + 4 * c + g, cpr) * 16);
+      }
       auto vfrag = [&](int ct, int js) -> bf16x8 {
         const int cc = head * D + 16 * ct + 4 * (c16 & 3);  // channel of this source lane
         uint2 part[2];
@@ -281,9 +291,8 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
         const uint32_t wd[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
         return __builtin_bit_cast(bf16x8, wd);
       };
-      f32x4 o[1][2];
+      f32x4 o[1][CT];
       float inv[1];
-      const uint4 qp[1] = {qf};
       f32x4 land_term[4];                          // read by attend_qtiles only for windows with land keys
       if (m.use_shift) {                           // wave-uniform mask mode of the window
         uint64_t rid_pack = 0;
@@ -315,7 +324,7 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
       __builtin_amdgcn_wave_barrier();
       const int i = 16 * it + c16;
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
+      for (int ct = 0; ct < CT; ++ct) {
         const f32x4 v = o[0][ct] * inv[0];
         const int cc = head * D + 16 * ct + 4 * g;  // 4 channels, 8 bytes
         uint2 pk;
@@ -326,14 +335,17 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
     }
     lds_barrier();                                // O complete
     {
-      // One whole-line store per thread (kNPad * cpr chunks == nthreads).
-      static_assert(kNPad * cpr == nthreads, "one O chunk per thread");
+      // Whole-line stores, kOPer chunks per thread (rows orow + u nthreads / cpr).
       const uint16_t* slice = reinterpret_cast<const uint16_t*>(p.o) + (int64_t)w * kNPad * p.o_stride + hg * G * D;
       const __amdgpu_buffer_rsrc_t out =
           buffer_rsrc(slice, (uint32_t)(((int64_t)(kNPad - 1) * p.o_stride + G * D) * 2));
-      const u32x4 val =
-          __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(qs + tile_slot(orow, ochunk, cpr) * 16));
-      stream_store_sc1(val, out, (uint32_t)(orow * p.o_stride + ochunk * 8) * 2);
+#pragma unroll
+      for (int u = 0; u < kOPer; ++u) {
+        const int row = orow + u * (nthreads / cpr);
+        const u32x4 val =
+            __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(qs + tile_slot(row, ochunk, cpr) * 16));
+        stream_store_sc1(val, out, (uint32_t)(row * p.o_stride + ochunk * 8) * 2);
+      }
     }
     if (!more) break;
     w += wstride;
@@ -544,10 +556,10 @@ int launch_tile(const AttnParams& p, hipStream_t s) {
 // Persistent grid of the ring kernel: as many workgroups as the device holds
 // at once, rounded down to a multiple of the head groups (each workgroup keeps
 // one head group), never more than the work.
-template <int G>
+template <int D, int G>
 int launch_ring(const AttnParams& p, hipStream_t s) {
-  constexpr int lds = ring_lds_bytes<G>();
-  auto kern = window_attn_ring_kernel<G>;
+  constexpr int lds = ring_lds_bytes<D, G>();
+  auto kern = window_attn_ring_kernel<D, G>;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
@@ -695,14 +707,15 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
   const int G = tile_group(d.heads, D);
   const bool tile = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
                     d.n_real == 64 && d.mask_mode != TERRA_MASK_EXPLICIT && G > 0;
-  // Head dim 32 with an even head count: the ring kernel (two heads per
-  // workgroup).  It adds bias and masks in raw-score units (bias / scale), so
+  // The ring kernel: head dim 32 with an even head count (two heads per
+  // workgroup) or head dim 64 (one head per workgroup), 128-byte row slices
+  // either way.  It adds bias and masks in raw-score units (bias / scale), so
   // it needs a positive, not tiny scale.
-  const bool ring = tile && D == 32 && d.heads % 2 == 0 && d.scale >= 0x1p-20f;
+  const bool ring = tile && ((D == 32 && d.heads % 2 == 0) || D == 64) && d.scale >= 0x1p-20f;
   if (ring) {
-    p.group = 2;
-    p.groups = d.heads / 2;
-    const int st = launch_ring<2>(p, s);
+    p.group = D == 32 ? 2 : 1;
+    p.groups = d.heads / p.group;
+    const int st = D == 32 ? launch_ring<32, 2>(p, s) : launch_ring<64, 1>(p, s);
     if (st != TERRA_OK) return st;
   } else if (tile) {
     p.group = G;
