@@ -17,10 +17,15 @@
 // tiles are processed in two halves (it = 0,1 then 2,3): at most 32 score
 // registers are live and a wave fits in 128 VGPRs.
 //
-// Two kernels share that core:
+// Three kernels share that core:
 //
-//   window_attn_tile_kernel   bf16, 8x8 windows, no padded tokens, analytic
-//       masks.  A persistent workgroup loops over (window, group of G heads)
+//   window_attn_ring_kernel   bf16, 8x8 windows, no padded tokens, analytic
+//       masks, head dim 32 with an even head count (two heads per workgroup)
+//       or head dim 64 (one head per workgroup): 128-byte row slices loaded
+//       straight into a ring of three LDS buffers, two units ahead (below).
+//
+//   window_attn_tile_kernel   the other bf16 8x8 cases (an odd number of heads
+//       of dim 32, a tiny scale).  A persistent workgroup loops over (window, group of G heads)
 //       units, two waves per head (one per query half).  The group's q, k, v
 //       rows (a contiguous slice of G*D channels, whole 128-byte lines) are
 //       streamed into LDS with nontemporal loads while the previous unit is
