@@ -24,8 +24,11 @@
 //       or head dim 64 (one head per workgroup): 128-byte row slices loaded
 //       straight into a ring of three LDS buffers, two units ahead (below).
 //
-//   window_attn_tile_kernel   the other bf16 8x8 cases (an odd number of heads
-//       of dim 32, a tiny scale).  A persistent workgroup loops over (window, group of G heads)
+//   window_attn_tile_kernel   the same bf16 8x8 shapes when the scale is
+//       below 2^-20, where bias / scale would leave the fp32 range of the
+//       ring kernel's raw-score units (an odd head count of dim 32 has no
+//       128-byte group and runs the wave kernel).  A persistent workgroup
+//       loops over (window, group of G heads)
 //       units, two waves per head (one per query half).  The group's q, k, v
 //       rows (a contiguous slice of G*D channels, whole 128-byte lines) are
 //       streamed into LDS with nontemporal loads while the previous unit is

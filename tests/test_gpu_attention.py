@@ -81,7 +81,7 @@ def test_core_no_mask(dev, dtype, ws, C, heads, with_bias):
 @pytest.mark.parametrize("H,W,ws,s,C,heads", [(56, 56, 7, 3, 96, 3), (32, 48, 8, 4, 192, 6), (16, 24, 8, 4, 128, 2),
                                                (28, 42, 7, 3, 128, 4)])
 def test_core_shift_mask_analytic_and_dense(dev, dtype, H, W, ws, s, C, heads):
-    """The analytic mask (8x8 bf16 with an even head count: the tile kernels;
+    """The analytic mask (8x8 bf16 with an even head count: the ring kernel;
     otherwise the per-wave kernel) against the dense mask and the oracle."""
     nW = (H // ws) * (W // ws)
     B = 2
@@ -138,6 +138,31 @@ def test_core_padded_keys_tile(dev, heads):
     ref = so.window_attention_core(q, k, v, heads, (C // heads) ** -0.5, table, (ws, ws), None, n_real=49,
                                    compute_dtype=torch.float32)
     _check(out, ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("C,heads", [(192, 6), (128, 4), (128, 2), (192, 3)])
+@pytest.mark.parametrize("shifted", [False, True])
+def test_core_tiny_scale(dev, C, heads, shifted):
+    """A scale below 2^-20 on bf16 8x8 windows: the ring kernel adds bias and
+    masks in raw-score units (bias / scale), so these shapes run the window-tile
+    kernel instead (head dim 32 with 6 and 4 heads, head dim 64 with 2 and 3).
+    q and k are scaled by 2^10 so the logits stay O(1) and the bias and mask
+    still move the outputs."""
+    H, W, ws, s = 16, 32, 8, 4
+    nW = (H // ws) * (W // ws)
+    scale = 2.0 ** -21
+    q, k, v, table = _inputs(2 * nW, ws * ws, C, heads, ws, torch.bfloat16, 240, qkv_scale=1024.0)
+    dense = so.shift_mask(H, W, ws, s) if shifted else None
+    mask = ShiftMask(H, W, s, s, 0, H // ws, W // ws) if shifted else None
+    out = kernels.window_attention(q.to(dev), k.to(dev), v.to(dev), heads, (ws, ws), scale,
+                                   bias_table=table.to(dev), mask=mask)
+    ref = so.window_attention_core(q, k, v, heads, scale, table, (ws, ws), dense, compute_dtype=torch.float32)
+    _check(out, ref, torch.bfloat16)
+    # The same call with the scale folded into q (exact: powers of two) and a
+    # normal scale runs the ring kernel; the two kernels agree to rounding.
+    out_ring = kernels.window_attention((q * 2.0 ** -11).to(dev), k.to(dev), v.to(dev), heads, (ws, ws), 2.0 ** -10,
+                                        bias_table=table.to(dev), mask=mask)
+    _assert_same_masking(out, out_ring, torch.bfloat16)
 
 
 def test_core_strided_qkv_equals_contiguous(dev):
