@@ -25,14 +25,16 @@
 //       straight into a ring of three LDS buffers, two units ahead (below).
 //
 //   window_attn_tile_kernel   the same bf16 8x8 shapes when the scale is
-//       below 2^-20, where bias / scale would leave the fp32 range of the
-//       ring kernel's raw-score units (an odd head count of dim 32 has no
-//       128-byte group and runs the wave kernel).  A persistent workgroup
-//       loops over (window, group of G heads)
-//       units, two waves per head (one per query half).  The group's q, k, v
-//       rows (a contiguous slice of G*D channels, whole 128-byte lines) are
-//       streamed into LDS with nontemporal loads while the previous unit is
-//       computed; O is staged in LDS over Q and streamed out as whole lines.
+//       below 2^-20 (zero included): the ring kernel divides the bias and
+//       mask terms by the scale, and as it goes to zero they would swamp the
+//       raw scores' low bits, then overflow.  This kernel adds them after
+//       scaling.  (An odd head count of dim 32 has no 128-byte group and
+//       runs the wave kernel.)  A persistent workgroup loops over (window,
+//       group of G heads) units, two waves per head (one per query half).
+//       The group's q, k, v rows (a contiguous slice of G*D channels, whole
+//       128-byte lines) are streamed into LDS with nontemporal loads while
+//       the previous unit is computed; O is staged in LDS over Q and streamed
+//       out as whole lines.
 //       The relative-position index of lane element (it, jt, r) is
 //       lane_base + 30*(it - jt) - r, so the bias comes from LDS with
 //       compile-time offsets.
@@ -717,8 +719,8 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
                     d.n_real == 64 && d.mask_mode != TERRA_MASK_EXPLICIT && G > 0;
   // The ring kernel: head dim 32 with an even head count (two heads per
   // workgroup) or head dim 64 (one head per workgroup), 128-byte row slices
-  // either way.  It adds bias and masks in raw-score units (bias / scale), so
-  // it needs a positive, not tiny scale.
+  // either way.  It adds bias and masks in raw-score units (divided by the
+  // scale), so it takes scales of 2^-20 and above.
   const bool ring = tile && ((D == 32 && d.heads % 2 == 0) || D == 64) && d.scale >= 0x1p-20f;
   if (ring) {
     p.group = D == 32 ? 2 : 1;

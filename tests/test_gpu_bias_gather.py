@@ -39,16 +39,21 @@ def _expected(idx: np.ndarray, e: int, vals: np.ndarray):
     return out, hit
 
 
-@pytest.mark.parametrize("dtype,ws,C,heads,kernel", [
-    (torch.bfloat16, 8, 192, 6, "ring (head dim 32, even heads)"),
-    (torch.bfloat16, 8, 96, 3, "per-wave (odd head count)"),
-    (torch.bfloat16, 8, 768, 12, "tile<64> (head dim 64)"),
-    (torch.bfloat16, 7, 128, 4, "per-wave (7x7 windows)"),
-    (torch.float32, 8, 64, 2, "per-wave fp32"),
-    (torch.float32, 7, 96, 3, "per-wave fp32, 7x7"),
+@pytest.mark.parametrize("dtype,ws,C,heads,tiny_scale,kernel", [
+    (torch.bfloat16, 8, 192, 6, False, "ring (head dim 32, even heads)"),
+    (torch.bfloat16, 8, 96, 3, False, "per-wave (odd head count)"),
+    (torch.bfloat16, 8, 768, 12, False, "ring (head dim 64)"),
+    (torch.bfloat16, 8, 192, 6, True, "window-tile (head dim 32, scale below 2^-20)"),
+    (torch.bfloat16, 8, 768, 12, True, "window-tile (head dim 64, scale below 2^-20)"),
+    (torch.bfloat16, 7, 128, 4, False, "per-wave (7x7 windows)"),
+    (torch.float32, 8, 64, 2, False, "per-wave fp32"),
+    (torch.float32, 7, 96, 3, False, "per-wave fp32, 7x7"),
 ])
-def test_attention_bias_gather_bit_exact(dev, dtype, ws, C, heads, kernel):
+def test_attention_bias_gather_bit_exact(dev, dtype, ws, C, heads, tiny_scale, kernel):
     N, d, T = ws * ws, C // heads, (2 * ws - 1) ** 2
+    # q = k = 0: the logits are the bias whatever the scale; a scale below
+    # 2^-20 selects the window-tile kernel for bf16 8x8 windows.
+    scale = 2.0 ** -21 if tiny_scale else d ** -0.5
     B_ = 3
     idx = brute.relative_index(ws, ws)
     key_vals = np.arange(N, dtype=np.float64)
@@ -62,7 +67,7 @@ def test_attention_bias_gather_bit_exact(dev, dtype, ws, C, heads, kernel):
         for h in range(heads):
             if e0 + h < T:
                 table[e0 + h, h] = 0.0
-        out = kernels.window_attention(q, q, v, heads, (ws, ws), d ** -0.5, bias_table=table.to(dev)).double().cpu()
+        out = kernels.window_attention(q, q, v, heads, (ws, ws), scale, bias_table=table.to(dev)).double().cpu()
         for h in range(heads):
             e = e0 + h
             if e >= T:
