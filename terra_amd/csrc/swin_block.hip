@@ -709,7 +709,7 @@ static_assert(kLds <= 160 * 1024, "LDS");
 template <bool kPacked>
 __device__ __forceinline__ void unit_qkv(const BlockParams& p, const uint8_t* xn, int h, int lane, uint4 (&kf4)[4],
                                          uint4 (&vf)[2][2], uint4 (&qf)[4], const float* bqkv) {
-  constexpr int kDepth = 3;  // weight ring (registers): loads two k-steps ahead
+  constexpr int kDepth = 4;  // weight ring (registers): loads three k-steps ahead
   const int g = lane >> 4, c16 = lane & 15;
   const int sw = (c16 >> 1) & 7;
   auto rt = [&](int j) { return (j >> 1) * (kC / 16) + 2 * h + (j & 1); };
@@ -1278,17 +1278,23 @@ __device__ __forceinline__ void unit_qkv(const BlockParams& p, const uint8_t* xn
     const int row = 16 * tt + c16;
     return *reinterpret_cast<const uint4*>(xn + slot(row, 4 * ks + g) * 16);
   };
-  uint4 ring[2][6];
+  constexpr int kDepth = 2;  // weight ring (registers): loads one k-step ahead (deeper measured the same)
+  uint4 ring[kDepth][6];
 #pragma unroll
-  for (int j = 0; j < 6; ++j) ring[0][j] = weight_frag<kC, kPacked>(p.w_qkv, rt(j), 0, lane);
+  for (int st = 0; st < kDepth - 1; ++st)
+#pragma unroll
+    for (int j = 0; j < 6; ++j) ring[st][j] = weight_frag<kC, kPacked>(p.w_qkv, rt(j), st, lane);
   uint4 xf[2][4];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) xf[0][tt] = xn_frag(tt, 0);
 #pragma unroll
   for (int ks = 0; ks < kKS; ++ks) {
-    if (ks + 1 < kKS) {
+    if (ks + kDepth - 1 < kKS) {
 #pragma unroll
-      for (int j = 0; j < 6; ++j) ring[(ks + 1) & 1][j] = weight_frag<kC, kPacked>(p.w_qkv, rt(j), ks + 1, lane);
+      for (int j = 0; j < 6; ++j)
+        ring[(ks + kDepth - 1) % kDepth][j] = weight_frag<kC, kPacked>(p.w_qkv, rt(j), ks + kDepth - 1, lane);
+    }
+    if (ks + 1 < kKS) {
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) xf[(ks + 1) & 1][tt] = xn_frag(tt, ks + 1);
     }
@@ -1298,7 +1304,7 @@ __device__ __forceinline__ void unit_qkv(const BlockParams& p, const uint8_t* xn
       const bf16x8 x8 = __builtin_bit_cast(bf16x8, xf[ks & 1][tt]);
 #pragma unroll
       for (int j = 0; j < 6; ++j) {
-        const bf16x8 w8 = __builtin_bit_cast(bf16x8, ring[ks & 1][j]);
+        const bf16x8 w8 = __builtin_bit_cast(bf16x8, ring[ks % kDepth][j]);
         acc[j][tt] = j < 4 ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(w8, x8, acc[j][tt], 0, 0, 0)
                            : __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, w8, acc[j][tt], 0, 0, 0);
       }
@@ -1609,7 +1615,7 @@ __device__ __forceinline__ void layernorm_in_place(const BlockParams& p, const U
 // the next k-step are requested before this step's MFMAs, then this step's
 // xn fragments are read: a deeper ring does not fit next to the K and V
 // fragments a wave holds while it computes Q.
-template <int NF, int NT, bool kV, bool kPacked>
+template <int NF, int NT, bool kV, bool kPacked, int kDepth = 2>
 __device__ __forceinline__ void pass(const BlockParams& p, const uint16_t* w, const float* bias, int rt0, int tt0,
                                      const uint8_t* tile, int lane, f32x4 (&acc)[NF][NT]) {
   const int g = lane >> 4, c16 = lane & 15;
@@ -1627,16 +1633,21 @@ __device__ __forceinline__ void pass(const BlockParams& p, const uint16_t* w, co
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[f][t] = b;
   }
-  uint4 ring[2][NF];
+  // kDepth: weight ring depth (registers), loads kDepth - 1 k-steps ahead.
+  static_assert(kKS % kDepth == 0, "whole ring turns");
+  uint4 ring[kDepth][NF];
 #pragma unroll
-  for (int f = 0; f < NF; ++f) ring[0][f] = weight_frag<kC, kPacked>(w, rt0 + f, 0, lane);
-  for (int ks0 = 0; ks0 < kKS; ks0 += 2) {
+  for (int st = 0; st < kDepth - 1; ++st)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int f = 0; f < NF; ++f) ring[st][f] = weight_frag<kC, kPacked>(w, rt0 + f, st, lane);
+  for (int ks0 = 0; ks0 < kKS; ks0 += kDepth) {
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j) {
       const int ks = ks0 + j;
-      if (ks + 1 < kKS) {
+      if (ks + kDepth - 1 < kKS) {
 #pragma unroll
-        for (int f = 0; f < NF; ++f) ring[(j + 1) & 1][f] = weight_frag<kC, kPacked>(w, rt0 + f, ks + 1, lane);
+        for (int f = 0; f < NF; ++f)
+          ring[(j + kDepth - 1) % kDepth][f] = weight_frag<kC, kPacked>(w, rt0 + f, ks + kDepth - 1, lane);
       }
       asm volatile("" ::: "memory");
       uint4 xf[NT];
@@ -1742,13 +1753,16 @@ namespace hd64 {
 
 // K, V and Q^T (times scale * log2 e) of head h as MFMA operand fragments:
 // kf[tt][kk] (K rows of key tile tt, channels 32 kk ..), vf[ct][js] (V^T
-// operand), qf[it][kk] (Q operand of query tile it).
+// operand), qf[it][kk] (Q operand of query tile it).  The weights run two
+// k-steps ahead: each window streams 4.7 MB of weights from L2, and that
+// latency outweighs the few VGPRs the deeper ring spills (c4 202-204 -> 193-196
+// us).
 template <bool kPacked>
 __device__ __forceinline__ void head_qkv64(const BlockParams& p, const uint8_t* tile, int h, int lane,
                                            uint4 (&kf)[4][2], uint4 (&vf)[4][2], uint4 (&qf)[4][2]) {
   {
     f32x4 acc[4][4];
-    pass<4, 4, false, kPacked>(p, p.w_qkv, p.b_qkv, kC / 16 + 4 * h, 0, tile, lane, acc);
+    pass<4, 4, false, kPacked, 3>(p, p.w_qkv, p.b_qkv, kC / 16 + 4 * h, 0, tile, lane, acc);
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
@@ -1756,7 +1770,7 @@ __device__ __forceinline__ void head_qkv64(const BlockParams& p, const uint8_t* 
   }
   {
     f32x4 acc[4][4];
-    pass<4, 4, true, kPacked>(p, p.w_qkv, p.b_qkv, kC / 8 + 4 * h, 0, tile, lane, acc);
+    pass<4, 4, true, kPacked, 3>(p, p.w_qkv, p.b_qkv, kC / 8 + 4 * h, 0, tile, lane, acc);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
@@ -1764,7 +1778,7 @@ __device__ __forceinline__ void head_qkv64(const BlockParams& p, const uint8_t* 
   }
   {
     f32x4 acc[4][4];
-    pass<4, 4, false, kPacked>(p, p.w_qkv, p.b_qkv, 4 * h, 0, tile, lane, acc);
+    pass<4, 4, false, kPacked, 3>(p, p.w_qkv, p.b_qkv, 4 * h, 0, tile, lane, acc);
 #pragma unroll
     for (int it = 0; it < 4; ++it)
 #pragma unroll
