@@ -490,7 +490,7 @@ def swin_block(x: torch.Tensor, geom: WindowGeometry, num_heads: int, scale: flo
         _require_device(x)
         if out is None:
             return torch.empty_like(x)
-        if out.shape != x.shape or out.dtype != x.dtype:
+        if out.shape != x.shape or out.dtype != x.dtype or out.device != x.device:
             raise ValueError("out must be a contiguous tensor like x")
         return out
     given = (qkv_weight, qkv_bias, proj_weight, proj_bias, ln_weight, ln_bias, bias_table, land_bits)
