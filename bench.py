@@ -483,6 +483,7 @@ def main():
         "prewarm": {"seconds": prewarm["s"], "steps": prewarm["steps"],
                     "note": "untimed steps before the counted warm-up, so the clock has settled"},
         "ms_per_step": ms,
+        "windows_per_s": B_ / (ms * 1e-3),
         "timing": ("the timed steps carry no per-launch events; a second pass of as many steps records events "
                    "around each kernel launch for the roofline's launch times"),
         "higher_is_better": True,
