@@ -58,6 +58,14 @@ __device__ __forceinline__ int region(int coord, int extent, int ws, int shift) 
   return coord < extent - ws ? 0 : (coord < extent - shift ? 1 : 2);
 }
 
+// max(a, b) propagating NaN (IEEE 754-2019 maximum).  On gfx950 a chain of
+// these becomes v_maximum3_f32, two inputs per instruction, with nothing
+// else: with fmaxf (maxNum) the compiler quiets every operand it cannot prove
+// canonical first (MFMA results, values from other lanes), one extra VALU op
+// each.  A softmax row max is the same either way, except that a NaN score
+// now makes its row NaN, as torch's max does.
+__device__ __forceinline__ float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Reductions over the 4 lanes l, l^16, l^32, l^48 that share a query row.
 // v_permlane16_swap / v_permlane32_swap with both operands = v return the
 // value of the own 16-lane (32-lane) half and of the partner half, so one
@@ -65,10 +73,10 @@ __device__ __forceinline__ int region(int coord, int extent, int ws, int shift) 
 __device__ __forceinline__ float xor_max(float v) {
   const uint32_t b = __float_as_uint(v);
   const auto p16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
-  v = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+  v = max_nan(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
   const uint32_t c = __float_as_uint(v);
   const auto p32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
-  return fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+  return max_nan(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
 }
 
 __device__ __forceinline__ float xor_sum(float v) {
@@ -358,7 +366,7 @@ __device__ __forceinline__ void softmax_half(f32x4 (&s)[2][4], float (&inv)[2], 
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[il][jt][r]);
+      for (int r = 0; r < 4; ++r) mx = max_nan(mx, s[il][jt][r]);
     mx = xor_max(mx);
     float sum = 0.f;
 #pragma unroll
@@ -687,7 +695,7 @@ __device__ __forceinline__ void attend_qtiles(f32x4 (&o)[NQ][CT], float (&inv)[N
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) mx[q] = fmaxf(mx[q], s[q][jt][r]);
+      for (int r = 0; r < 4; ++r) mx[q] = max_nan(mx[q], s[q][jt][r]);
   }
 #pragma unroll
   for (int q = 0; q < NQ; ++q) mx[q] = xor_max(mx[q]);

@@ -1705,7 +1705,7 @@ __device__ __forceinline__ void attend_tile(f32x4 (&o)[4], float& inv, int it, c
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[jt][r]);
+    for (int r = 0; r < 4; ++r) mx = max_nan(mx, s[jt][r]);
   mx = xor_max(mx);
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)

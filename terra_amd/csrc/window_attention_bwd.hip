@@ -509,9 +509,9 @@ __global__ __launch_bounds__(256) void window_attn_bwd_generic_kernel(const BwdP
   }
   float mx = z[0];
 #pragma unroll
-  for (int k = 1; k < 16; ++k) mx = fmaxf(mx, z[k]);
-  mx = fmaxf(mx, __shfl_xor(mx, 1));
-  mx = fmaxf(mx, __shfl_xor(mx, 2));
+  for (int k = 1; k < 16; ++k) mx = max_nan(mx, z[k]);
+  mx = max_nan(mx, __shfl_xor(mx, 1));
+  mx = max_nan(mx, __shfl_xor(mx, 2));
   float sum = 0.f;
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
