@@ -1064,7 +1064,12 @@ void swin_block_dw_kernel(const BlockParams p) {
     if (!two && k > 0) store_pair<4>(p, first_unit(k - 1), other, wave - 4, lane);
     if (ona) {
       unit_qkv<kPacked>(p, obuf + wia * kTile, ha, lane, kf4, vf, qf, s_bqkv);
+      // The attention at raised wave priority: its dependent MFMA / exp /
+      // shuffle chain sets the pace, and the other wave on the SIMD fills the
+      // gaps with its q/k/v MFMAs (c3 248-250 -> 245-248 us A/B).
+      __builtin_amdgcn_s_setprio(1);
       head_attention<kC, true>(p, cura, tabs + ha * kTableMax, ha, lane, kf4, vf, qf, nullptr, oa);
+      __builtin_amdgcn_s_setprio(0);
     }
     if (onb) unit_qkv<kPacked>(p, obuf + wib * kTile, hb, lane, kf4, vf, qf, s_bqkv);
     lds_barrier();  // every LayerNorm row has been read: O may replace them
@@ -1094,7 +1099,11 @@ void swin_block_dw_kernel(const BlockParams p) {
       write_held_o();
     } else {
       write_held_o();
-      if (onb) head_attention<kC>(p, curb, tabs + hb * kTableMax, hb, lane, kf4, vf, qf, obuf + wib * kTile);
+      if (onb) {
+        __builtin_amdgcn_s_setprio(1);
+        head_attention<kC>(p, curb, tabs + hb * kTableMax, hb, lane, kf4, vf, qf, obuf + wib * kTile);
+        __builtin_amdgcn_s_setprio(0);
+      }
     }
     lds_barrier();  // O complete
     if (onp) {
@@ -1452,7 +1461,9 @@ void swin_block_w7_kernel(const BlockParams p) {
     if (on) {
       uint4 kf[4][1], vf[2][2], qf[4][1];
       unit_qkv<kPacked>(p, obuf + wwin * kTile, h, lane, kf, vf, qf, s_bqkv);
+      __builtin_amdgcn_s_setprio(1);  // as in the six-head kernel (c2 34.0-34.3 -> 33.1-33.8 us A/B)
       unit_attention(p, cur, tabs + h * kTab, lane, kf, vf, qf, opk);
+      __builtin_amdgcn_s_setprio(0);
     }
     if (k > 0) {  // pair k - 1's output rows
       const int up = first_unit(k - 1);
