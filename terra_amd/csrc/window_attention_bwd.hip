@@ -273,6 +273,10 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
     if (next < units) fetch(next);
 
     // ---- phase 2: keys [32*half, 32*half + 32) of head `head` -----------------
+    // Phase 2 (the dK / dV MFMAs) at raised wave priority, so that a wave of
+    // the other workgroup in its softmax fills the gaps (276-279 against
+    // 281-283 us at c3, A/B).
+    __builtin_amdgcn_s_setprio(1);
     {
       f32x4 av[D / 16][2], ak[D / 16][2];
 #pragma unroll
@@ -323,6 +327,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       }
     }
     lds_barrier();
+    __builtin_amdgcn_s_setprio(0);
     // ---- dq (V tile), dk (K tile), dv (dout tile) -> memory, whole rows -------
     {
       const int col = hg * G * D + chunk0 * 8;
