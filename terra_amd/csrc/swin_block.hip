@@ -908,7 +908,8 @@ __device__ __forceinline__ void layernorm_pair_rows(const BlockParams& p, const 
     for (int k = 0; k < kCPL; ++k) m.add4(w[q][k]);
     token_stats8(m, p.inv_c, mean[q], var[q]);
   }
-  if (token_stats_recheck(mean[0], var[0]) | token_stats_recheck(mean[1], var[1])) {  // uniform per wave
+  // Both ballots, no short circuit: one uniform branch.
+  if ((int)token_stats_recheck(mean[0], var[0]) | (int)token_stats_recheck(mean[1], var[1])) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       asm volatile("" : "+v"(mean[q]));  // keeps this rare pass a branch, not computed on every path
