@@ -165,6 +165,33 @@ def test_core_tiny_scale(dev, C, heads, shifted):
     _assert_same_masking(out, out_ring, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype,ws,C,heads,scale", [
+    (torch.bfloat16, 8, 192, 6, None),       # ring kernel, head dim 32
+    (torch.bfloat16, 8, 128, 2, None),       # ring kernel, head dim 64
+    (torch.bfloat16, 8, 192, 6, 2.0 ** -21),  # window-tile kernel
+    (torch.bfloat16, 7, 96, 3, None),        # per-wave kernel
+    (torch.float32, 8, 64, 2, None),         # per-wave kernel, fp32
+])
+def test_core_nan_query_spoils_only_its_row(dev, dtype, ws, C, heads, scale):
+    """A NaN in one query makes that query's row of that head NaN, as torch's
+    softmax does (its row max is NaN); every other output is unchanged."""
+    B_, N, D = 6, ws * ws, C // heads
+    scale = D ** -0.5 if scale is None else scale
+    q, k, v, table = _inputs(B_, N, C, heads, ws, dtype, 250)
+    clean = kernels.window_attention(q.to(dev), k.to(dev), v.to(dev), heads, (ws, ws), scale,
+                                     bias_table=table.to(dev)).float().cpu()
+    w, i, h = 3, 5, heads - 1
+    q_nan = q.clone()
+    q_nan[w, i, h * D] = float("nan")
+    out = kernels.window_attention(q_nan.to(dev), k.to(dev), v.to(dev), heads, (ws, ws), scale,
+                                   bias_table=table.to(dev)).float().cpu()
+    spoiled = torch.zeros_like(out, dtype=torch.bool)
+    spoiled[w, i, h * D:(h + 1) * D] = True
+    assert torch.isnan(out[spoiled]).all()
+    assert not torch.isnan(out[~spoiled]).any()
+    assert torch.equal(out[~spoiled], clean[~spoiled])
+
+
 def test_core_strided_qkv_equals_contiguous(dev):
     B_, N, C, heads, ws = 32, 64, 192, 6, 8
     qkv = workloads.activations((B_, N, 3 * C), 240, torch.bfloat16).to(dev)
