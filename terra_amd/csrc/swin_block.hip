@@ -1765,10 +1765,10 @@ namespace hd64 {
 
 // K, V and Q^T (times scale * log2 e) of head h as MFMA operand fragments:
 // kf[tt][kk] (K rows of key tile tt, channels 32 kk ..), vf[ct][js] (V^T
-// operand), qf[it][kk] (Q operand of query tile it).  The weights run two
-// k-steps ahead: each window streams 4.7 MB of weights from L2, and that
-// latency outweighs the few VGPRs the deeper ring spills (c4 202-204 -> 193-196
-// us).
+// operand), qf[it][kk] (Q operand of query tile it).  The K and V passes
+// run their weights two k-steps ahead (each window streams 4.7 MB of weights
+// from L2: c4 202-204 -> 193-196 us); the Q pass, which runs beside the first
+// head's K and V fragments, keeps one step so that nothing spills.
 template <bool kPacked>
 __device__ __forceinline__ void head_qkv64(const BlockParams& p, const uint8_t* tile, int h, int lane,
                                            uint4 (&kf)[4][2], uint4 (&vf)[4][2], uint4 (&qf)[4][2]) {
@@ -1790,7 +1790,7 @@ __device__ __forceinline__ void head_qkv64(const BlockParams& p, const uint8_t* 
   }
   {
     f32x4 acc[4][4];
-    pass<4, 4, false, kPacked, 3>(p, p.w_qkv, p.b_qkv, 4 * h, 0, tile, lane, acc);
+    pass<4, 4, false, kPacked, 2>(p, p.w_qkv, p.b_qkv, 4 * h, 0, tile, lane, acc);
 #pragma unroll
     for (int it = 0; it < 4; ++it)
 #pragma unroll
