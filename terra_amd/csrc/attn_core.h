@@ -305,11 +305,23 @@ __device__ __forceinline__ void softmax_half(f32x4 (&s)[2][4], float (&inv)[2], 
       const int ig = i < p.n_geo ? i : p.n_geo - 1;
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
+        float mrow[4];
+        if constexpr (kWs8) {
+          // 8x8 windows: n_geo == 64, and the launcher takes this path only
+          // for a 16-byte aligned mask, so a lane's four keys are one load.
+          const float4 e4 = *reinterpret_cast<const float4*>(emask + i * 64 + 16 * jt + 4 * g);
+          mrow[0] = e4.x; mrow[1] = e4.y; mrow[2] = e4.z; mrow[3] = e4.w;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = 16 * jt + 4 * g + r;
+            mrow[r] = emask[ig * p.n_geo + (j < p.n_geo ? j : p.n_geo - 1)];
+          }
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = 16 * jt + 4 * g + r;
-          const int jg = j < p.n_geo ? j : p.n_geo - 1;
-          const float me = emask[ig * p.n_geo + jg] * kLog2e;
+          const float me = mrow[r] * kLog2e;
           const bool land_j = (lg.land_lane >> (16 * jt + r)) & 1ull;
           const bool jin = kWs8 || j < p.n_geo;
           s[il][jt][r] += ((i_geo[il] && jin) ? me : 0.f) + ((land_j && jin) ? p.mask_l2e : 0.f);

@@ -696,9 +696,11 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   int st;
   if (dtype == TERRA_DTYPE_BF16) {
     // MFMA tiles for every bf16 window; the 8x8 closed-form geometry where it
-    // applies.  Two heads per workgroup for head dim 32 (128-byte row
-    // slices), else one.
-    const bool ws8 = d.window_h == 8 && d.window_w == 8 && d.tokens == 64 && d.n_real == 64;
+    // applies (with a dense mask, only a 16-byte aligned one: that geometry
+    // reads four mask entries per load).  Two heads per workgroup for head
+    // dim 32 (128-byte row slices), else one.
+    const bool ws8 = d.window_h == 8 && d.window_w == 8 && d.tokens == 64 && d.n_real == 64 &&
+                     (!expl || (reinterpret_cast<uintptr_t>(explicit_mask) & 15) == 0);
     const int G = (D == 32 && d.heads % 2 == 0) ? 2 : 1;
     p.group = G;
     p.groups = d.heads / G;

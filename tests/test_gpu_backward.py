@@ -91,6 +91,35 @@ def test_attention_backward_matches_oracle(dev, C, heads, kind):
     _close(dbias, rtab)
 
 
+@pytest.mark.parametrize("aligned", [True, False])
+def test_attention_backward_random_dense_mask(dev, aligned):
+    """A random dense mask, asymmetric in (query, key) unlike the shift mask,
+    so a transposed or shifted mask read fails: continuous offsets in
+    [-8, 0) plus -100 on a third of the pairs.  A 16-byte aligned mask takes
+    the 8x8 closed-form geometry (four mask entries per load); a view at a
+    one-float offset takes the generic geometry.  Both match the oracle."""
+    B, H, W, C, heads = 2, 32, 48, 192, 6
+    nW = (H // 8) * (W // 8)
+    B_ = B * nW
+    q, k, v, dout, table = _inputs(B_, C, heads, 330)
+    gen = workloads.generator(331)
+    dense = -8.0 * torch.rand(nW, 64, 64, generator=gen)
+    dense = torch.where(torch.rand(nW, 64, 64, generator=gen) < 1 / 3, torch.full_like(dense, -100.0), dense)
+    off = 0 if aligned else 1
+    flat = torch.zeros(nW * 64 * 64 + 4, device=dev)
+    mask = flat[off:off + nW * 64 * 64].view(nW, 64, 64)
+    mask.copy_(dense.to(dev))
+    assert (mask.data_ptr() % 16 == 0) == aligned
+    dbias = torch.zeros(225, heads, device=dev)
+    dq, dk, dv = kernels.window_attention_backward(q.to(dev), k.to(dev), v.to(dev), dout.to(dev), heads, (8, 8),
+                                                   (C // heads) ** -0.5, bias_table=table.to(dev), mask=mask,
+                                                   dbias=dbias)
+    (rq, rk, rv), rtab = _oracle_grads(q, k, v, dout, heads, table, dense)
+    for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
+        _close(got, ref)
+    _close(dbias, rtab)
+
+
 def test_attention_backward_no_bias_table(dev):
     B_, C, heads = 24, 192, 6
     q, k, v, dout, _ = _inputs(B_, C, heads, 310)
