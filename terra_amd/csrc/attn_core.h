@@ -307,8 +307,9 @@ __device__ __forceinline__ void softmax_half(f32x4 (&s)[2][4], float (&inv)[2], 
       for (int jt = 0; jt < 4; ++jt) {
         float mrow[4];
         if constexpr (kWs8) {
-          // 8x8 windows: n_geo == 64, and the launcher takes this path only
-          // for a 16-byte aligned mask, so a lane's four keys are one load.
+          // 8x8 windows: n_geo == 64, and the launchers take this path only
+          // for a 16-byte aligned mask (global or staged in LDS), so a lane's
+          // four keys are one load.
           const float4 e4 = *reinterpret_cast<const float4*>(emask + i * 64 + 16 * jt + 4 * g);
           mrow[0] = e4.x; mrow[1] = e4.y; mrow[2] = e4.z; mrow[3] = e4.w;
         } else {
@@ -534,11 +535,12 @@ __device__ __forceinline__ int tile_slot(int row, int chunk, int cpr) {
 // of the Q, K and V tiles, the wave computes query tiles 2*half and 2*half + 1
 // (K and Q fragments by row, V^T fragments by transposed reads), and O
 // overwrites the wave's own Q rows of that head.  `tab` is the head's bias
-// column (x log2e) with kTableMax entries.
-template <int D, int kCpr>
+// column (x log2e) with kTableMax entries; `emask` (kExplicit) the window's
+// [64][64] dense mask in LDS.
+template <int D, int kCpr, bool kExplicit = false>
 __device__ __forceinline__ void tile_attention_wave(uint8_t* qs, const uint8_t* ks, const uint8_t* vs, int col_head,
                                                     int half, const AttnParams& p, const WindowMaskState& m,
-                                                    const float* tab, int lane) {
+                                                    const float* tab, int lane, const float* emask = nullptr) {
   const int g = lane >> 4, c16 = lane & 15;
   LaneGeom<true> lg;
   lane_geom_init<true>(lg, p, m, tab, lane);
@@ -575,7 +577,7 @@ __device__ __forceinline__ void tile_attention_wave(uint8_t* qs, const uint8_t* 
   f32x4 s[2][4];
   scores_pair<true, D>(s, kf, qp);
   float inv[2];
-  softmax_half<true, false>(s, inv, half, p, m, lg, nullptr, lane);
+  softmax_half<true, kExplicit>(s, inv, half, p, m, lg, emask, lane);
   f32x4 o[D / 16][2];
   pv_half<true, D>(o, s, lane, vfrag);
 #pragma unroll

@@ -28,7 +28,8 @@
 //       below 2^-20 (zero included): the ring kernel divides the bias and
 //       mask terms by the scale, and as it goes to zero they would swamp the
 //       raw scores' low bits, then overflow.  This kernel adds them after
-//       scaling.  (An odd head count of dim 32 has no 128-byte group and
+//       scaling.  It also takes a dense [nW, 64, 64] mask (16-byte aligned),
+//       staged into LDS with each unit's rows.  (An odd head count of dim 32 has no 128-byte group and
 //       runs the wave kernel.)  A persistent workgroup loops over (window,
 //       group of G heads) units, two waves per head (one per query half).
 //       The group's q, k, v rows (a contiguous slice of G*D channels, whole
@@ -40,7 +41,7 @@
 //       compile-time offsets.
 //
 //   window_attn_wave_kernel   everything else (fp32, any window up to 8x8,
-//       padded tokens and keys, explicit dense masks): one wavefront per
+//       padded tokens and keys, dense masks not taken above): one wavefront per
 //       (window, head), K and Q fragments loaded straight from global memory,
 //       V staged in the wave's LDS.
 #include "common.h"
@@ -55,7 +56,10 @@ namespace {
 
 constexpr int kTileMaxRowBytes = 384;  // G*D*2 <= 384 (<= 192 bf16 channels)
 
-template <int D, int G>
+// Dense-mask bytes per unit in LDS (kExplicit): the window's [64][64] fp32 mask.
+constexpr int kMaskTileBytes = kNPad * kNPad * (int)sizeof(float);
+
+template <int D, int G, bool kExplicit>
 __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int nthreads = G * 128;              // two waves per head
@@ -65,7 +69,8 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
   uint8_t* qs = smem;                            // Q, later O
   uint8_t* ks = smem + tile_bytes;
   uint8_t* vs = smem + 2 * tile_bytes;
-  float* tables = reinterpret_cast<float*>(smem + 3 * tile_bytes);
+  float* mtile = reinterpret_cast<float*>(smem + 3 * tile_bytes);  // dense mask (kExplicit)
+  float* tables = reinterpret_cast<float*>(smem + 3 * tile_bytes + (kExplicit ? kMaskTileBytes : 0));
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -81,10 +86,21 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
   static_assert(kRowStep * cpr == nthreads && kRowStep * kPer == kNPad, "row tiling");
   const int row0 = tid / cpr, chunk0 = tid % cpr;
 
-  // q, k, v of one unit -> registers (nontemporal: every byte is read once).
+  // q, k, v of one unit -> registers (nontemporal: every byte is read once);
+  // with a dense mask also the window's mask (cached: windows share it).
+  constexpr int kMPer = (kMaskTileBytes / 16 + nthreads - 1) / nthreads;  // 16-byte pieces per thread
   uint4 buf[3][kPer];
+  float4 mbuf[kExplicit ? kMPer : 1];
   auto fetch = [&](int unit) {
     const int w = unit / p.groups, hg = unit - w * p.groups;
+    if constexpr (kExplicit) {
+      const float* mw = p.explicit_mask + (int64_t)(w % p.mask_windows) * kNPad * kNPad;
+#pragma unroll
+      for (int u = 0; u < kMPer; ++u) {
+        const int e = tid + u * nthreads;
+        if (e < kMaskTileBytes / 16) mbuf[u] = *reinterpret_cast<const float4*>(mw + 4 * e);
+      }
+    }
     const int64_t row_base = (int64_t)w * kNPad + row0;
     const int col = hg * G * D + chunk0 * 8;
     const uint16_t* src[3] = {reinterpret_cast<const uint16_t*>(p.q) + row_base * p.q_stride + col,
@@ -117,6 +133,13 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
       *reinterpret_cast<uint4*>(ks + off) = buf[1][u];
       *reinterpret_cast<uint4*>(vs + off) = buf[2][u];
     }
+    if constexpr (kExplicit) {
+#pragma unroll
+      for (int u = 0; u < kMPer; ++u) {
+        const int e = tid + u * nthreads;
+        if (e < kMaskTileBytes / 16) *reinterpret_cast<float4*>(mtile + 4 * e) = mbuf[u];
+      }
+    }
     if (hg != table_group) {  // bias column of this head (x log2e); the two waves split it
       table_group = hg;
       const int h = hg * G + head;
@@ -134,7 +157,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
 
     // ---- this wave: one head, query tiles 2*half, 2*half + 1 ---------------
     const WindowMaskState m = window_mask_state(p, w, true);
-    tile_attention_wave<D, cpr>(qs, ks, vs, head, half, p, m, tab, lane);
+    tile_attention_wave<D, cpr, kExplicit>(qs, ks, vs, head, half, p, m, tab, lane, mtile);
     __syncthreads();
 
     // ---- stream O out (whole lines) ------------------------------------------
@@ -531,7 +554,7 @@ void launch_wave(const AttnParams& p, hipStream_t s) {
 
 // Resident workgroups of the persistent tile kernel: as many as the device's
 // CUs hold at once (LDS and VGPR limited), queried per device once.
-template <int D, int G>
+template <int D, int G, bool kExplicit>
 int tile_grid(int lds) {
   constexpr int kMaxDevices = 64;
   static int cache[kMaxDevices] = {0};
@@ -540,7 +563,7 @@ int tile_grid(int lds) {
   if (cache[dev] == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, window_attn_tile_kernel<D, G>, G * 128, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, window_attn_tile_kernel<D, G, kExplicit>, G * 128, lds) !=
         hipSuccess)
       return 0;
     cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
@@ -548,18 +571,19 @@ int tile_grid(int lds) {
   return cache[dev];
 }
 
-template <int D, int G>
+template <int D, int G, bool kExplicit>
 int launch_tile(const AttnParams& p, hipStream_t s) {
-  constexpr int lds = 3 * kNPad * G * D * 2 + G * kTableMax * (int)sizeof(float);
+  constexpr int lds = 3 * kNPad * G * D * 2 + G * kTableMax * (int)sizeof(float) + (kExplicit ? kMaskTileBytes : 0);
   // The >64 KiB dynamic-LDS opt-in is a per-kernel attribute: set it once.
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&window_attn_tile_kernel<D, G>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+      reinterpret_cast<const void*>(&window_attn_tile_kernel<D, G, kExplicit>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      lds);
   if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
-  const int resident = tile_grid<D, G>(lds);
+  const int resident = tile_grid<D, G, kExplicit>(lds);
   if (resident <= 0) return fail(TERRA_ERR_LAUNCH, "cannot size the tile kernel grid for this device");
   const int units = (p.items / p.heads) * p.groups;
   const int blocks = units < resident ? units : resident;
-  window_attn_tile_kernel<D, G><<<blocks, G * 128, lds, s>>>(p);
+  window_attn_tile_kernel<D, G, kExplicit><<<blocks, G * 128, lds, s>>>(p);
   return TERRA_OK;
 }
 
@@ -608,18 +632,19 @@ int tile_group(int heads, int D) {
   return 0;
 }
 
+template <bool kExplicit>
 int dispatch_tile(const AttnParams& p, int D, hipStream_t s) {
   if (D == 32) {
     switch (p.group) {
-      case 6: return launch_tile<32, 6>(p, s);
-      case 4: return launch_tile<32, 4>(p, s);
-      default: return launch_tile<32, 2>(p, s);
+      case 6: return launch_tile<32, 6, kExplicit>(p, s);
+      case 4: return launch_tile<32, 4, kExplicit>(p, s);
+      default: return launch_tile<32, 2, kExplicit>(p, s);
     }
   }
   switch (p.group) {
-    case 3: return launch_tile<64, 3>(p, s);
-    case 2: return launch_tile<64, 2>(p, s);
-    default: return launch_tile<64, 1>(p, s);
+    case 3: return launch_tile<64, 3, kExplicit>(p, s);
+    case 2: return launch_tile<64, 2, kExplicit>(p, s);
+    default: return launch_tile<64, 1, kExplicit>(p, s);
   }
 }
 
@@ -713,15 +738,17 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
   p.win_row_begin = d.win_row_begin; p.win_rows = d.win_rows; p.win_cols = d.win_cols;
 
   hipStream_t s = (hipStream_t)stream;
-  // bf16 8x8 windows without padded tokens or a dense mask: window-tile kernel.
+  // bf16 8x8 windows without padded tokens: window-tile kernel (a dense mask
+  // only when 16-byte aligned: it is staged in 16-byte pieces).
   const int G = tile_group(d.heads, D);
+  const bool expl = d.mask_mode == TERRA_MASK_EXPLICIT;
   const bool tile = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
-                    d.n_real == 64 && d.mask_mode != TERRA_MASK_EXPLICIT && G > 0;
+                    d.n_real == 64 && G > 0 && (!expl || (reinterpret_cast<uintptr_t>(explicit_mask) & 15) == 0);
   // The ring kernel: head dim 32 with an even head count (two heads per
   // workgroup) or head dim 64 (one head per workgroup), 128-byte row slices
   // either way.  It adds bias and masks in raw-score units (divided by the
   // scale), so it takes scales of 2^-20 and above.
-  const bool ring = tile && ((D == 32 && d.heads % 2 == 0) || D == 64) && d.scale >= 0x1p-20f;
+  const bool ring = tile && !expl && ((D == 32 && d.heads % 2 == 0) || D == 64) && d.scale >= 0x1p-20f;
   if (ring) {
     p.group = D == 32 ? 2 : 1;
     p.groups = d.heads / p.group;
@@ -730,11 +757,10 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
   } else if (tile) {
     p.group = G;
     p.groups = d.heads / G;
-    const int st = dispatch_tile(p, D, s);
+    const int st = expl ? dispatch_tile<true>(p, D, s) : dispatch_tile<false>(p, D, s);
     if (st != TERRA_OK) return st;
   } else {
     p.group = p.groups = 0;
-    const bool expl = d.mask_mode == TERRA_MASK_EXPLICIT;
     if (dtype == TERRA_DTYPE_BF16) {
       if (D == 32) expl ? launch_wave<true, 32, true>(p, s) : launch_wave<true, 32, false>(p, s);
       else expl ? launch_wave<true, 64, true>(p, s) : launch_wave<true, 64, false>(p, s);

@@ -8,8 +8,9 @@ Tolerances (written per the path's contract):
                     probabilities to bf16 before P@V, as autocast does).
 The same mask given in closed form or as a dense tensor: bit for bit in fp32
 (one kernel); in bf16 the closed-form path runs the ring kernel (bias and
-masks added in raw-score units) and the dense one the generic kernel, so they
-agree to rounding (see _assert_same_masking).
+masks added in raw-score units) and the dense one the window-tile kernel
+(8x8 windows, 16-byte aligned mask) or the per-wave kernel, both adding the
+terms after scaling, so they agree to rounding (see _assert_same_masking).
 """
 import pytest
 import torch
@@ -94,6 +95,38 @@ def test_core_shift_mask_analytic_and_dense(dev, dtype, H, W, ws, s, C, heads):
     cd = torch.float64 if dtype == torch.float32 else torch.float32
     ref = so.window_attention_core(q, k, v, heads, (C // heads) ** -0.5, table, (ws, ws), dense, compute_dtype=cd)
     _check(out_a, ref, dtype)
+
+
+@pytest.mark.parametrize("C,heads,land", [(192, 6, False), (192, 6, True), (128, 2, False), (96, 3, False)])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_core_random_dense_mask(dev, C, heads, land, aligned):
+    """A random dense mask, asymmetric in (query, key) unlike the shift mask,
+    so a transposed or shifted mask read fails: continuous offsets in [-8, 0)
+    plus -100 on a third of the pairs, optionally with land keys on top.
+    bf16 8x8 windows: an aligned mask runs the window-tile kernel with the
+    mask staged in LDS (head dim 32 and 64), a mask at a one-float offset, or
+    an odd head count of dim 32, the per-wave kernel."""
+    H, W, ws = 32, 48, 8
+    nW = (H // ws) * (W // ws)
+    q, k, v, table = _inputs(2 * nW, 64, C, heads, ws, torch.bfloat16, 230, qkv_scale=2.0)
+    gen = workloads.generator(231)
+    dense = -8.0 * torch.rand(nW, 64, 64, generator=gen)
+    dense = torch.where(torch.rand(nW, 64, 64, generator=gen) < 1 / 3, torch.full_like(dense, -100.0), dense)
+    off = 0 if aligned else 1
+    flat = torch.zeros(nW * 64 * 64 + 4, device=dev)
+    emask = flat[off:off + nW * 64 * 64].view(nW, 64, 64)
+    emask.copy_(dense.to(dev))
+    assert (emask.data_ptr() % 16 == 0) == aligned
+    mask, total = emask, dense
+    if land:
+        g = WindowGeometry(1, H, W, 1, ws, 4, 4)
+        lm = workloads.land_mask(H, W, seed=9)
+        mask = WindowMask(shift=emask, land_bits=utils.land_window_bits(lm.to(dev), g))
+        total = so.fold_land(dense, so.land_key_flags(lm, ws, 4, 4))
+    out = _run(dev, q, k, v, heads, ws, table, mask=mask)
+    ref = so.window_attention_core(q, k, v, heads, (C // heads) ** -0.5, table, (ws, ws), total,
+                                   compute_dtype=torch.float32)
+    _check(out, ref, torch.bfloat16)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
