@@ -622,13 +622,18 @@ int launch_ring(const AttnParams& p, hipStream_t s) {
 // 128-byte lines (128, 256 or 384 bytes); 0 if there is none.  Small groups
 // mean small workgroups (2*G waves, ~26 KB of LDS for G*D = 64), so three
 // independent pipelines share a CU and their load and compute phases
-// interleave (c3: 145 us with G = 2 against 166 us with G = 6).
-int tile_group(int heads, int D) {
+// interleave (c3: 145 us with G = 2 against 166 us with G = 6).  With a
+// dense mask, which every unit stages whole, the largest such divisor: the
+// mask is then staged once per window (c3: 179-180 us with G = 6 against
+// 217-219 us with G = 2).
+int tile_group(int heads, int D, bool largest) {
   static const int kG32[] = {2, 4, 6};  // head dim 32
   static const int kG64[] = {1, 2, 3};  // head dim 64
   const int* cand = D == 32 ? kG32 : kG64;
-  for (int i = 0; i < 3; ++i)
+  for (int n = 0; n < 3; ++n) {
+    const int i = largest ? 2 - n : n;
     if (heads % cand[i] == 0) return cand[i];
+  }
   return 0;
 }
 
@@ -740,8 +745,8 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
   hipStream_t s = (hipStream_t)stream;
   // bf16 8x8 windows without padded tokens: window-tile kernel (a dense mask
   // only when 16-byte aligned: it is staged in 16-byte pieces).
-  const int G = tile_group(d.heads, D);
   const bool expl = d.mask_mode == TERRA_MASK_EXPLICIT;
+  const int G = tile_group(d.heads, D, expl);
   const bool tile = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
                     d.n_real == 64 && G > 0 && (!expl || (reinterpret_cast<uintptr_t>(explicit_mask) & 15) == 0);
   // The ring kernel: head dim 32 with an even head count (two heads per
