@@ -185,7 +185,8 @@ int terra_swin_partition(const void* x, void* windows, int dtype,
  * * gamma + beta, rounded once to the activation dtype (f32 / f16 / bf16).
  * gamma, beta: C floats each, or NULL for 1 / 0.  Padding applies to the
  * normalised grid: frame padding and pad windows are written as pad_value.
- * Needs C * element size to be a multiple of 16 bytes and at most 1536.
+ * Needs C * element size to be a multiple of 16 bytes and at most 4096, and
+ * C <= 1024.
  */
 int terra_swin_partition_ln(const void* x, void* windows, int dtype,
                             const terra_swin_geom* geom, const float* gamma,

@@ -41,23 +41,41 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libterra_swin.so)")
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compile every HIP source into the shared library; returns its path."""
-    from ._lib import LIB_PATH  # noqa: WPS433 (path only; does not open the library)
-
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    fd, tmp = tempfile.mkstemp(prefix="libterra_swin.", suffix=".so.tmp", dir=HERE)
-    os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, *srcs, "-o", tmp]
+def _run(cmd, verbose: bool) -> str:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(line for line in proc.stdout.splitlines() if "packed-fp32-ops" not in line)
     if proc.returncode != 0:
-        os.unlink(tmp)
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{out}")
-    if verbose and out.strip():
-        print(out, flush=True)
+    return out
+
+
+def build_library(verbose: bool = False, jobs: int = 0) -> str:
+    """Compile every HIP source (one hipcc process per source, in parallel)
+    and link them into the shared library; returns its path."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from ._lib import LIB_PATH  # noqa: WPS433 (path only; does not open the library)
+
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 8)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="_build.", dir=HERE) as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+        cmds = [[hipcc(), *compile_flags, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            outs = list(pool.map(lambda c: _run(c, verbose), cmds))
+        fd, tmp = tempfile.mkstemp(prefix="libterra_swin.", suffix=".so.tmp", dir=HERE)
+        os.close(fd)
+        try:
+            outs.append(_run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose))
+        except RuntimeError:
+            os.unlink(tmp)
+            raise
+    if verbose:
+        for out in outs:
+            if out.strip():
+                print(out, flush=True)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

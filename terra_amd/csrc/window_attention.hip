@@ -212,7 +212,8 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
   constexpr int kBlocksPerTile = tile_bytes / 1024;
   constexpr int kOPer = kNPad * cpr / nthreads;   // O chunks per thread
   static_assert(cpr % 8 == 0 && kRounds * nthreads * 16 == unit_bytes, "whole 1 KB blocks per wave");
-  static_assert(kRounds == 3 || kRounds == 6, "the vmcnt wait below counts 3 or 6 loads per thread per unit");
+  static_assert(kRounds == 3 || kRounds == 6 || kRounds == 12,
+                "the vmcnt wait below counts 3, 6 or 12 loads per thread per unit");
   static_assert(kOPer * nthreads == kNPad * cpr, "whole O chunks per thread");
   float* tables = reinterpret_cast<float*>(smem + kRingBufs * unit_bytes);
 
@@ -284,7 +285,8 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
     // the previous unit's O store still pending, vmcnt(3) waits for more.
     if (more) {
       if constexpr (kRounds == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+      else if constexpr (kRounds == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
@@ -438,37 +440,46 @@ __global__ __launch_bounds__(kThreads) void window_attn_wave_kernel(const AttnPa
     const int e = lane + 64 * u;
     tabv[u] = (p.bias_table != nullptr && e < p.table_size) ? p.bias_table[(int64_t)e * p.heads + h] : 0.f;
   }
-  // K and Q fragments straight from global memory.
+  // K and Q fragments straight from global memory.  Heads of more than 128
+  // bytes per row (bf16 D = 128, fp32 D = 64 and 128) load them per query
+  // half instead, K again for the second half (from cache), so that one
+  // half's fragments, scores and O accumulators fit the register file.
   constexpr int kKF = kBf16 ? D / 32 : D / 16;
+  constexpr bool kPerHalf = D * (int)sizeof(T) > 128;
+  auto load_frags = [&](const T* base, int64_t stride, int t0, int nt, uint4(*dst)[kKF]) {
+#pragma unroll
+    for (int t = 0; t < nt; ++t) {
+      const int row = 16 * (t0 + t) + c16;
+#pragma unroll
+      for (int s = 0; s < kKF; ++s) {
+        const int col = kBf16 ? 32 * s + 8 * g : g * (D / 4) + 4 * s;
+        dst[t][s] = row < N ? *reinterpret_cast<const uint4*>(base + (int64_t)row * stride + col)
+                            : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
   uint4 kf[4][kKF];
-  uint4 qf[4][kKF];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int row = 16 * t + c16;
-#pragma unroll
-    for (int s = 0; s < kKF; ++s) {
-      const int col = kBf16 ? 32 * s + 8 * g : g * (D / 4) + 4 * s;
-      kf[t][s] = row < N ? *reinterpret_cast<const uint4*>(kw + (int64_t)row * p.k_stride + col) : make_uint4(0, 0, 0, 0);
-    }
+  uint4 qf[kPerHalf ? 2 : 4][kKF];
+  if constexpr (!kPerHalf) {
+    load_frags(kw, p.k_stride, 0, 4, kf);
+    load_frags(qw, p.q_stride, 0, 4, qf);
   }
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int row = 16 * t + c16;
-#pragma unroll
-    for (int s = 0; s < kKF; ++s) {
-      const int col = kBf16 ? 32 * s + 8 * g : g * (D / 4) + 4 * s;
-      qf[t][s] = row < N ? *reinterpret_cast<const uint4*>(qw + (int64_t)row * p.q_stride + col) : make_uint4(0, 0, 0, 0);
-    }
-  }
-  // V tile as 16-byte chunks (rows beyond N are zero).
+  // V tile as 16-byte chunks (rows beyond N are zero), moved to LDS in
+  // batches of at most 16 chunks per lane.
   constexpr int kChunksPerRow = D * (int)sizeof(T) / 16;
   constexpr int kVLoads = kNPad * kChunksPerRow / 64;
-  uint4 vr[kVLoads];
-#pragma unroll
-  for (int u = 0; u < kVLoads; ++u) {
+  constexpr int kVBatch = kVLoads < 16 ? kVLoads : 16;
+  static_assert(kVLoads % kVBatch == 0, "whole V batches");
+  auto v_chunk = [&](int u, int& row, int& col) {
     const int chunk = lane + 64 * u;
-    const int row = chunk / kChunksPerRow;
-    const int col = (chunk % kChunksPerRow) * (16 / (int)sizeof(T));
+    row = chunk / kChunksPerRow;
+    col = (chunk % kChunksPerRow) * (16 / (int)sizeof(T));
+  };
+  uint4 vr[kVBatch];
+#pragma unroll
+  for (int u = 0; u < kVBatch; ++u) {
+    int row, col;
+    v_chunk(u, row, col);
     vr[u] = row < N ? *reinterpret_cast<const uint4*>(vw + (int64_t)row * p.v_stride + col) : make_uint4(0, 0, 0, 0);
   }
 
@@ -483,11 +494,22 @@ __global__ __launch_bounds__(kThreads) void window_attn_wave_kernel(const AttnPa
   }
   T* vt = lds.v[wave];
 #pragma unroll
-  for (int u = 0; u < kVLoads; ++u) {
-    const int chunk = lane + 64 * u;
-    const int row = chunk / kChunksPerRow;
-    const int col = (chunk % kChunksPerRow) * (16 / (int)sizeof(T));
-    *reinterpret_cast<uint4*>(vt + row * kPitch + col) = vr[u];
+  for (int u0 = 0; u0 < kVLoads; u0 += kVBatch) {
+    if (u0 > 0) {
+#pragma unroll
+      for (int u = 0; u < kVBatch; ++u) {
+        int row, col;
+        v_chunk(u0 + u, row, col);
+        vr[u] = row < N ? *reinterpret_cast<const uint4*>(vw + (int64_t)row * p.v_stride + col)
+                        : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kVBatch; ++u) {
+      int row, col;
+      v_chunk(u0 + u, row, col);
+      *reinterpret_cast<uint4*>(vt + row * kPitch + col) = vr[u];
+    }
   }
   // Order this wave's LDS writes before its later LDS reads.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -515,8 +537,13 @@ __global__ __launch_bounds__(kThreads) void window_attn_wave_kernel(const AttnPa
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     f32x4 s[2][4];
-    const uint4 (&qp)[2][kKF] = *reinterpret_cast<const uint4(*)[2][kKF]>(&qf[2 * half]);
-    scores_pair<kBf16, D>(s, kf, qp);
+    if constexpr (kPerHalf) {
+      load_frags(kw, p.k_stride, 0, 4, kf);
+      load_frags(qw, p.q_stride, 2 * half, 2, qf);
+      scores_pair<kBf16, D>(s, kf, *reinterpret_cast<const uint4(*)[2][kKF]>(&qf[0]));
+    } else {
+      scores_pair<kBf16, D>(s, kf, *reinterpret_cast<const uint4(*)[2][kKF]>(&qf[2 * half]));
+    }
     float inv[2];
     softmax_half<false, kExplicit>(s, inv, half, p, m, lg, emask, lane);
     f32x4 o[D / 16][2];
@@ -675,7 +702,7 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
   if (d.channels % d.heads != 0)
     return fail(TERRA_ERR_SHAPE, "channels %d not divisible by heads %d", d.channels, d.heads);
   const int D = d.channels / d.heads;
-  if (D != 32 && D != 64) return fail(TERRA_ERR_UNSUPPORTED, "head dim %d not in {32, 64}", D);
+  if (D != 32 && D != 64 && D != 128) return fail(TERRA_ERR_UNSUPPORTED, "head dim %d not in {32, 64, 128}", D);
   if (d.window_h <= 0 || d.window_w <= 0 || d.window_h > 8 || d.window_w > 8)
     return fail(TERRA_ERR_UNSUPPORTED, "window %dx%d outside 1..8", d.window_h, d.window_w);
   const int n_geo = d.window_h * d.window_w;
@@ -746,18 +773,21 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
   // bf16 8x8 windows without padded tokens: window-tile kernel (a dense mask
   // only when 16-byte aligned: it is staged in 16-byte pieces).
   const bool expl = d.mask_mode == TERRA_MASK_EXPLICIT;
-  const int G = tile_group(d.heads, D, expl);
-  const bool tile = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
-                    d.n_real == 64 && G > 0 && (!expl || (reinterpret_cast<uintptr_t>(explicit_mask) & 15) == 0);
+  const bool ws8 = dtype == TERRA_DTYPE_BF16 && d.window_h == 8 && d.window_w == 8 && d.tokens == 64 &&
+                   d.n_real == 64;
+  // Head dim 128 has no window-tile instance (its head slice alone is 256
+  // bytes per row): a small scale or a dense mask runs the wave kernel.
+  const int G = D <= 64 ? tile_group(d.heads, D, expl) : 0;
+  const bool tile = ws8 && G > 0 && (!expl || (reinterpret_cast<uintptr_t>(explicit_mask) & 15) == 0);
   // The ring kernel: head dim 32 with an even head count (two heads per
-  // workgroup) or head dim 64 (one head per workgroup), 128-byte row slices
-  // either way.  It adds bias and masks in raw-score units (divided by the
-  // scale), so it takes scales of 2^-20 and above.
-  const bool ring = tile && !expl && ((D == 32 && d.heads % 2 == 0) || D == 64) && d.scale >= 0x1p-20f;
+  // workgroup), head dim 64 or 128 (one head per workgroup), row slices of
+  // 128 or 256 bytes.  It adds bias and masks in raw-score units (divided by
+  // the scale), so it takes scales of 2^-20 and above.
+  const bool ring = ws8 && !expl && ((D == 32 && d.heads % 2 == 0) || D == 64 || D == 128) && d.scale >= 0x1p-20f;
   if (ring) {
     p.group = D == 32 ? 2 : 1;
     p.groups = d.heads / p.group;
-    const int st = D == 32 ? launch_ring<32, 2>(p, s) : launch_ring<64, 1>(p, s);
+    const int st = D == 32 ? launch_ring<32, 2>(p, s) : D == 64 ? launch_ring<64, 1>(p, s) : launch_ring<128, 1>(p, s);
     if (st != TERRA_OK) return st;
   } else if (tile) {
     p.group = G;
@@ -768,10 +798,12 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
     p.group = p.groups = 0;
     if (dtype == TERRA_DTYPE_BF16) {
       if (D == 32) expl ? launch_wave<true, 32, true>(p, s) : launch_wave<true, 32, false>(p, s);
-      else expl ? launch_wave<true, 64, true>(p, s) : launch_wave<true, 64, false>(p, s);
+      else if (D == 64) expl ? launch_wave<true, 64, true>(p, s) : launch_wave<true, 64, false>(p, s);
+      else expl ? launch_wave<true, 128, true>(p, s) : launch_wave<true, 128, false>(p, s);
     } else {
       if (D == 32) expl ? launch_wave<false, 32, true>(p, s) : launch_wave<false, 32, false>(p, s);
-      else expl ? launch_wave<false, 64, true>(p, s) : launch_wave<false, 64, false>(p, s);
+      else if (D == 64) expl ? launch_wave<false, 64, true>(p, s) : launch_wave<false, 64, false>(p, s);
+      else expl ? launch_wave<false, 128, true>(p, s) : launch_wave<false, 128, false>(p, s);
     }
   }
   const hipError_t e = hipGetLastError();

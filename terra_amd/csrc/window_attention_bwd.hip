@@ -1,5 +1,5 @@
 // Backward of the window-attention core (bf16, windows up to 8x8 in rows of
-// up to 64 tokens, head dim 32/64).
+// up to 64 tokens, head dim 32/64/128).
 //
 // Per window w and head h, with z = (q k^T) * scale + bias + M the natural
 // logits and P = softmax(z) (recomputed here from q, k and the masks, the
@@ -165,13 +165,18 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
   };
 
   // Persistent loop, software-pipelined: the loads of unit n + gridDim.x are
-  // issued once unit n's phase 1 is done and land during its phase 2.
+  // issued once unit n's phase 1 is done and land during its phase 2.  Head
+  // dim 128 loads each unit at its start instead: its 32 chunks per thread
+  // held through phase 2 beside the 128 dK / dV accumulator registers would
+  // not fit the register file.
+  constexpr bool kPrefetch = D <= 64;
   int unit = blockIdx.x;  // < units: the grid is never larger than the work
-  fetch(unit);
+  if constexpr (kPrefetch) fetch(unit);
   for (;;) {
     const int w = unit / p.groups;
     // ---- q, k, v, dout rows of the head group -> LDS --------------------------
     {
+      if constexpr (!kPrefetch) fetch(unit);
       lds_barrier();  // the previous unit is done with every tile
       uint8_t* dst[4] = {qs, ks, vs, dos};
 #pragma unroll
@@ -270,7 +275,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       }
     }
     const int next = unit + (int)gridDim.x;
-    if (next < units) fetch(next);
+    if (kPrefetch && next < units) fetch(next);
 
     // ---- phase 2: keys [32*half, 32*half + 32) of head `head` -----------------
     // Phase 2 (the dK / dV MFMAs) at raised wave priority, so that a wave of
@@ -428,7 +433,8 @@ int launch_bwd_tiles(const BwdParams& bp, hipStream_t s, int D, int G, bool expl
   if (D == 32)
     return G == 2 ? (expl ? launch_bwd<32, 2, true, kWs8>(bp, s) : launch_bwd<32, 2, false, kWs8>(bp, s))
                   : (expl ? launch_bwd<32, 1, true, kWs8>(bp, s) : launch_bwd<32, 1, false, kWs8>(bp, s));
-  return expl ? launch_bwd<64, 1, true, kWs8>(bp, s) : launch_bwd<64, 1, false, kWs8>(bp, s);
+  if (D == 64) return expl ? launch_bwd<64, 1, true, kWs8>(bp, s) : launch_bwd<64, 1, false, kWs8>(bp, s);
+  return expl ? launch_bwd<128, 1, true, kWs8>(bp, s) : launch_bwd<128, 1, false, kWs8>(bp, s);
 }
 
 // ============================================================================
@@ -442,9 +448,23 @@ int launch_bwd_tiles(const BwdParams& bp, hipStream_t s, int D, int G, bool expl
 // >= n_real replaced by pad_key_value (their gradient is zero: masked_fill),
 // keys >= tokens excluded.
 
+// The P and dz tiles overlay the V rows (dead once phase 1 has formed dP)
+// where separate tiles would not fit the 160 KB of LDS (D = 128).
+template <int D>
+constexpr bool generic_bwd_overlay() {
+  return (4 * kNPad * (D + 1) + 2 * kNPad * (kNPad + 1) + kTableMax) * (int)sizeof(float) > 160 * 1024;
+}
+
+template <int D>
+constexpr int generic_bwd_pz_floats() {
+  return generic_bwd_overlay<D>() && kNPad * (D + 1) > 2 * kNPad * (kNPad + 1) ? kNPad * (D + 1)
+                                                                             : 2 * kNPad * (kNPad + 1);
+}
+
 template <int D>
 constexpr int generic_bwd_lds_bytes() {
-  return (4 * kNPad * (D + 1) + 2 * kNPad * (kNPad + 1) + kTableMax) * (int)sizeof(float);
+  return ((generic_bwd_overlay<D>() ? 3 : 4) * kNPad * (D + 1) + generic_bwd_pz_floats<D>() + kTableMax) *
+         (int)sizeof(float);
 }
 
 template <int D, bool kExplicit>
@@ -453,13 +473,16 @@ __global__ __launch_bounds__(256) void window_attn_bwd_generic_kernel(const BwdP
   const AttnParams& p = bp.a;
   constexpr int PD = D + 1;                     // odd row pitches: conflict-free column walks
   constexpr int PP = kNPad + 1;
+  // q, k, v, dout rows, then the P and dz tiles; with the overlay q, k, dout,
+  // then V in the region that P and dz take over.
+  constexpr bool kOverlay = generic_bwd_overlay<D>();
   float* qs = smf;
   float* ks = qs + kNPad * PD;
-  float* vs = ks + kNPad * PD;
-  float* ds = vs + kNPad * PD;                  // dout
-  float* ps = ds + kNPad * PD;                  // P
-  float* zs = ps + kNPad * PP;                  // dz
-  float* dtab = zs + kNPad * PP;                // this window-head's bias gradient
+  float* vs = ks + (kOverlay ? 2 : 1) * kNPad * PD;
+  float* ds = kOverlay ? ks + kNPad * PD : vs + kNPad * PD;  // dout
+  float* ps = kOverlay ? vs : ds + kNPad * PD;               // P
+  float* zs = ps + kNPad * PP;                               // dz
+  float* dtab = ps + generic_bwd_pz_floats<D>();             // this window-head's bias gradient
   const int tid = threadIdx.x;
   const int w = blockIdx.x / p.heads, h = blockIdx.x - (blockIdx.x / p.heads) * p.heads;
   const int N = p.N, ng = p.n_geo, ww = p.window_w, wh = p.window_h;
@@ -541,6 +564,7 @@ __global__ __launch_bounds__(256) void window_attn_bwd_generic_kernel(const BwdP
   }
   dsum += __shfl_xor(dsum, 1);
   dsum += __shfl_xor(dsum, 2);
+  if constexpr (kOverlay) __syncthreads();  // every thread has read V: P and dz overwrite it
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
     const int j = jq + 4 * k;
@@ -618,7 +642,7 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   if (d.channels % d.heads != 0)
     return fail(TERRA_ERR_SHAPE, "channels %d not divisible by heads %d", d.channels, d.heads);
   const int D = d.channels / d.heads;
-  if (D != 32 && D != 64) return fail(TERRA_ERR_UNSUPPORTED, "head dim %d not in {32, 64}", D);
+  if (D != 32 && D != 64 && D != 128) return fail(TERRA_ERR_UNSUPPORTED, "head dim %d not in {32, 64, 128}", D);
   const int elt = dtype == TERRA_DTYPE_BF16 ? 2 : 4;
   const int32_t strides[7] = {d.q_stride, d.k_stride, d.v_stride, desc->dout_stride,
                               desc->dq_stride, desc->dk_stride, desc->dv_stride};
@@ -707,8 +731,9 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
     st = ws8 ? launch_bwd_tiles<true>(bp, s, D, G, expl) : launch_bwd_tiles<false>(bp, s, D, G, expl);
   } else {
     p.group = p.groups = 0;
-    st = D == 32 ? (expl ? launch_bwd_generic<32, true>(bp, s) : launch_bwd_generic<32, false>(bp, s))
-                 : (expl ? launch_bwd_generic<64, true>(bp, s) : launch_bwd_generic<64, false>(bp, s));
+    st = D == 32   ? (expl ? launch_bwd_generic<32, true>(bp, s) : launch_bwd_generic<32, false>(bp, s))
+         : D == 64 ? (expl ? launch_bwd_generic<64, true>(bp, s) : launch_bwd_generic<64, false>(bp, s))
+                   : (expl ? launch_bwd_generic<128, true>(bp, s) : launch_bwd_generic<128, false>(bp, s));
   }
   if (st != TERRA_OK) return st;
   const hipError_t e = hipGetLastError();

@@ -204,7 +204,10 @@ struct LnParams {
   uint32_t tokens;     // destination tokens
 };
 
-constexpr int kLnMaxChannels = 12 * kLnLanes * 8;  // 768: the widest bf16 row (1536 bytes)
+// Widest fused LayerNorm row: C <= 1024 channels (gamma / beta staged whole)
+// and at most 256 chunks of 16 bytes (fp32 C = 1024: 4096 bytes).
+constexpr int kLnMaxChannels = 1024;
+constexpr int kLnMaxChunks = 256;
 
 template <int DT, int CPL, int kL>
 __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* __restrict__ x,
@@ -511,7 +514,10 @@ void dispatch_partition_ln(int cpl, const void* x, void* win, const CopyGeom& g,
   else if (cpl <= 4) launch_partition_ln<DT, 4>(x, win, g, ln, s);
   else if (cpl <= 6) launch_partition_ln<DT, 6>(x, win, g, ln, s);
   else if (cpl <= 8) launch_partition_ln<DT, 4, 16>(x, win, g, ln, s);  // 16 lanes per token
-  else launch_partition_ln<DT, 6, 16>(x, win, g, ln, s);
+  else if (cpl <= 12) launch_partition_ln<DT, 6, 16>(x, win, g, ln, s);
+  else if (cpl <= 16) launch_partition_ln<DT, 8, 16>(x, win, g, ln, s);  // bf16 C = 1024
+  else if (cpl <= 24) launch_partition_ln<DT, 12, 16>(x, win, g, ln, s);
+  else launch_partition_ln<DT, 16, 16>(x, win, g, ln, s);                // fp32 C = 1024
 }
 
 template <int VB, int DT>
@@ -581,9 +587,9 @@ extern "C" int terra_swin_partition_ln(const void* x, void* windows, int dtype, 
     if (p != nullptr && (uintptr_t)p % 4 != 0) return fail(TERRA_ERR_ALIGN, "gamma / beta must be 4-byte aligned");
   const int chunks = (int)(g.row_bytes / 16);
   const int cpl = (chunks + kLnLanes - 1) / kLnLanes;
-  if (cpl > 12)
-    return fail(TERRA_ERR_UNSUPPORTED, "fused LayerNorm handles rows up to %d bytes (got %lld)", 12 * kLnLanes * 16,
-                (long long)g.row_bytes);
+  if (chunks > kLnMaxChunks || geom->channels > kLnMaxChannels)
+    return fail(TERRA_ERR_UNSUPPORTED, "fused LayerNorm handles up to %d channels in rows of up to %d bytes (got %d "
+                "channels, %lld bytes)", kLnMaxChannels, kLnMaxChunks * 16, geom->channels, (long long)g.row_bytes);
   g.pad_pattern = pad_pattern(dtype, pad_value);
   LnParams ln;
   ln.gamma = gamma;

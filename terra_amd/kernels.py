@@ -376,12 +376,12 @@ def attention_backward_supported(q: torch.Tensor, num_heads: int, window_size: T
                                  n_real: Optional[int] = None) -> bool:
     """Whether :func:`window_attention_backward` serves this shape: the
     forward's (bf16 or fp32, windows up to 8x8 in at most 64 token rows,
-    head dim 32 or 64)."""
+    head dim 32, 64 or 128)."""
     tokens, channels = q.shape[-2], q.shape[-1]
     wh, ww = (int(w) for w in window_size)
     return (q.dtype in (torch.bfloat16, torch.float32) and 1 <= wh <= 8 and 1 <= ww <= 8
             and wh * ww <= tokens <= 64 and (n_real is None or 1 <= int(n_real) <= tokens)
-            and channels % num_heads == 0 and channels // num_heads in (32, 64))
+            and channels % num_heads == 0 and channels // num_heads in (32, 64, 128))
 
 
 def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dout: torch.Tensor,

@@ -111,12 +111,13 @@ class SequentialSwinTransformer(torch.nn.Module):
 
     def _fusable_norm(self, dtype: torch.dtype) -> bool:
         """norm1 is a plain LayerNorm over C that the gather kernel computes
-        for activations of `dtype` (rows of whole 16-byte chunks, <= 1536 B)."""
+        for activations of `dtype` (C <= 1024 in rows of whole 16-byte chunks,
+        <= 4096 B)."""
         n = self.norm1
         row_bytes = self.embedding_dim * dtype.itemsize
         return (type(n) is torch.nn.LayerNorm and tuple(n.normalized_shape) == (self.embedding_dim,)
                 and dtype in (torch.float32, torch.float16, torch.bfloat16)
-                and row_bytes % 16 == 0 and row_bytes <= 1536)
+                and row_bytes % 16 == 0 and row_bytes <= 4096 and self.embedding_dim <= 1024)
 
     def _fusable_block(self, x: torch.Tensor, geom: WindowGeometry) -> bool:
         """The whole half-block runs as one kernel: bf16, (window, heads, C) in

@@ -202,9 +202,9 @@ def test_partition_ln_rejects_bad_arguments():
     assert lib.terra_swin_partition_ln(None, FAKE, L.DTYPE_BF16, ctypes.byref(g), None, None, 1e-5, 0.0, None) == -1
     g6 = _geom(channels=6)  # 12-byte rows
     assert lib.terra_swin_partition_ln(FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(g6), None, None, 1e-5, 0.0, None) == -4
-    big = _geom(channels=1024)  # 2048-byte rows
+    big = _geom(channels=1032)  # more than 1024 channels
     assert lib.terra_swin_partition_ln(FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(big), None, None, 1e-5, 0.0, None) == -5
-    assert "1536" in L.last_error()
+    assert "1024 channels" in L.last_error()
     assert lib.terra_swin_partition_ln(FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(g), None, None, -1.0, 0.0, None) == -3
 
 

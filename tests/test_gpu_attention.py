@@ -66,7 +66,8 @@ def _run(dev, q, k, v, heads, ws, table, mask=None, n_real=None, **kw):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("ws,C,heads", [(7, 96, 3), (8, 192, 6), (8, 768, 12), (7, 128, 4), (6, 64, 2)])
+@pytest.mark.parametrize("ws,C,heads", [(7, 96, 3), (8, 192, 6), (8, 768, 12), (7, 128, 4), (6, 64, 2),
+                                         (8, 1024, 8), (7, 256, 2)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_core_no_mask(dev, dtype, ws, C, heads, with_bias):
     B_, N = 24, ws * ws
@@ -80,7 +81,7 @@ def test_core_no_mask(dev, dtype, ws, C, heads, with_bias):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("H,W,ws,s,C,heads", [(56, 56, 7, 3, 96, 3), (32, 48, 8, 4, 192, 6), (16, 24, 8, 4, 128, 2),
-                                               (28, 42, 7, 3, 128, 4)])
+                                               (28, 42, 7, 3, 128, 4), (16, 24, 8, 4, 256, 2)])
 def test_core_shift_mask_analytic_and_dense(dev, dtype, H, W, ws, s, C, heads):
     """The analytic mask (8x8 bf16 with an even head count: the ring kernel;
     otherwise the per-wave kernel) against the dense mask and the oracle."""
@@ -97,15 +98,16 @@ def test_core_shift_mask_analytic_and_dense(dev, dtype, H, W, ws, s, C, heads):
     _check(out_a, ref, dtype)
 
 
-@pytest.mark.parametrize("C,heads,land", [(192, 6, False), (192, 6, True), (128, 2, False), (96, 3, False)])
+@pytest.mark.parametrize("C,heads,land", [(192, 6, False), (192, 6, True), (128, 2, False), (96, 3, False),
+                                          (256, 2, False), (256, 2, True)])
 @pytest.mark.parametrize("aligned", [True, False])
 def test_core_random_dense_mask(dev, C, heads, land, aligned):
     """A random dense mask, asymmetric in (query, key) unlike the shift mask,
     so a transposed or shifted mask read fails: continuous offsets in [-8, 0)
     plus -100 on a third of the pairs, optionally with land keys on top.
     bf16 8x8 windows: an aligned mask runs the window-tile kernel with the
-    mask staged in LDS (head dim 32 and 64), a mask at a one-float offset, or
-    an odd head count of dim 32, the per-wave kernel."""
+    mask staged in LDS (head dim 32 and 64), a mask at a one-float offset, an
+    odd head count of dim 32, or head dim 128, the per-wave kernel."""
     H, W, ws = 32, 48, 8
     nW = (H // ws) * (W // ws)
     q, k, v, table = _inputs(2 * nW, 64, C, heads, ws, torch.bfloat16, 230, qkv_scale=2.0)
@@ -130,7 +132,7 @@ def test_core_random_dense_mask(dev, C, heads, land, aligned):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("H,W,ws,s,C,heads", [(32, 64, 8, 4, 192, 6), (28, 42, 7, 3, 128, 4)])
+@pytest.mark.parametrize("H,W,ws,s,C,heads", [(32, 64, 8, 4, 192, 6), (28, 42, 7, 3, 128, 4), (32, 64, 8, 4, 256, 2)])
 def test_core_land_bits(dev, dtype, H, W, ws, s, C, heads):
     land = workloads.land_mask(H, W, seed=9)
     g = WindowGeometry(1, H, W, 1, ws, s, s)
@@ -161,10 +163,10 @@ def test_core_padded_tokens_and_keys(dev, dtype):
     _check(out, ref, dtype)
 
 
-@pytest.mark.parametrize("heads", [4, 2])
+@pytest.mark.parametrize("heads", [4, 2, 1])
 def test_core_padded_keys_tile(dev, heads):
     """Padded keys without a dense mask: 49 real tokens of 7x7 windows in
-    64-token rows, head dim 32 and 64, bf16."""
+    64-token rows, head dim 32, 64 and 128, bf16."""
     B_, N, C, ws = 16, 64, 128, 7
     q, k, v, table = _inputs(B_, N, C, heads, ws, torch.bfloat16, 235)
     out = _run(dev, q, k, v, heads, ws, table, n_real=49)
@@ -173,12 +175,13 @@ def test_core_padded_keys_tile(dev, heads):
     _check(out, ref, torch.bfloat16)
 
 
-@pytest.mark.parametrize("C,heads", [(192, 6), (128, 4), (128, 2), (192, 3)])
+@pytest.mark.parametrize("C,heads", [(192, 6), (128, 4), (128, 2), (192, 3), (256, 2)])
 @pytest.mark.parametrize("shifted", [False, True])
 def test_core_tiny_scale(dev, C, heads, shifted):
     """A scale below 2^-20 on bf16 8x8 windows: the ring kernel adds bias and
     masks in raw-score units (bias / scale), so these shapes run the window-tile
-    kernel instead (head dim 32 with 6 and 4 heads, head dim 64 with 2 and 3).
+    kernel instead (head dim 32 with 6 and 4 heads, head dim 64 with 2 and 3),
+    and head dim 128 the per-wave kernel.
     q and k are scaled by 2^10 so the logits stay O(1) and the bias and mask
     still move the outputs."""
     H, W, ws, s = 16, 32, 8, 4
@@ -201,6 +204,9 @@ def test_core_tiny_scale(dev, C, heads, shifted):
 @pytest.mark.parametrize("dtype,ws,C,heads,scale", [
     (torch.bfloat16, 8, 192, 6, None),       # ring kernel, head dim 32
     (torch.bfloat16, 8, 128, 2, None),       # ring kernel, head dim 64
+    (torch.bfloat16, 8, 256, 2, None),       # ring kernel, head dim 128
+    (torch.bfloat16, 8, 256, 2, 2.0 ** -21),  # per-wave kernel, head dim 128
+    (torch.float32, 8, 256, 2, None),        # per-wave kernel, fp32, head dim 128
     (torch.bfloat16, 8, 192, 6, 2.0 ** -21),  # window-tile kernel
     (torch.bfloat16, 7, 96, 3, None),        # per-wave kernel
     (torch.float32, 8, 64, 2, None),         # per-wave kernel, fp32
@@ -257,7 +263,7 @@ def test_core_reference_autocast_distance(dev):
     assert e_kernel <= e_ref * 1.5 + 1e-6, (e_kernel, e_ref)
 
 
-@pytest.mark.parametrize("name", ["c3", "c5"])
+@pytest.mark.parametrize("name", ["c3", "c5", "g1"])
 def test_core_full_size_sampled_windows(dev, name):
     """Full-size launch (every window computed); a seeded sample of windows is
     checked against the oracle, and the whole output must be finite."""

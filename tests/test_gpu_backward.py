@@ -70,11 +70,12 @@ def _mask_case(kind, B, H, W, seed):
     return WindowMask(shift=ShiftMask.from_geometry(g), land_bits=bits), total
 
 
-@pytest.mark.parametrize("C,heads", [(192, 6), (128, 2), (96, 3)])
+@pytest.mark.parametrize("C,heads", [(192, 6), (128, 2), (96, 3), (256, 2)])
 @pytest.mark.parametrize("kind", ["none", "shift", "explicit", "land"])
 def test_attention_backward_matches_oracle(dev, C, heads, kind):
     """8x8 windows: two heads of dim 32 per workgroup (192, 6), one of dim 64
-    (128, 2) and one of dim 32 (96, 3: LDS rows padded to the 8-chunk swizzle)."""
+    (128, 2), one of dim 32 (96, 3: LDS rows padded to the 8-chunk swizzle)
+    and one of dim 128 (256, 2)."""
     B, H, W = 2, 32, 48
     B_ = B * (H // 8) * (W // 8)
     q, k, v, dout, table = _inputs(B_, C, heads, 300)
@@ -91,14 +92,15 @@ def test_attention_backward_matches_oracle(dev, C, heads, kind):
     _close(dbias, rtab)
 
 
+@pytest.mark.parametrize("C,heads", [(192, 6), (256, 2)])
 @pytest.mark.parametrize("aligned", [True, False])
-def test_attention_backward_random_dense_mask(dev, aligned):
+def test_attention_backward_random_dense_mask(dev, aligned, C, heads):
     """A random dense mask, asymmetric in (query, key) unlike the shift mask,
     so a transposed or shifted mask read fails: continuous offsets in
     [-8, 0) plus -100 on a third of the pairs.  A 16-byte aligned mask takes
     the 8x8 closed-form geometry (four mask entries per load); a view at a
     one-float offset takes the generic geometry.  Both match the oracle."""
-    B, H, W, C, heads = 2, 32, 48, 192, 6
+    B, H, W = 2, 32, 48
     nW = (H // 8) * (W // 8)
     B_ = B * nW
     q, k, v, dout, table = _inputs(B_, C, heads, 330)
@@ -199,7 +201,8 @@ def _close_dtype(got, ref, dtype):
 
 
 @pytest.mark.parametrize("dtype,C,heads", [(torch.float32, 96, 3), (torch.bfloat16, 96, 3),
-                                           (torch.bfloat16, 128, 4)])
+                                           (torch.bfloat16, 128, 4), (torch.float32, 256, 2),
+                                           (torch.bfloat16, 256, 2)])
 @pytest.mark.parametrize("kind", ["none", "shift", "explicit", "land"])
 def test_generic_backward_7x7_matches_oracle(dev, dtype, C, heads, kind):
     """7x7 windows (c1, c2), every mask form: fp32 through the plain kernel,
@@ -238,10 +241,11 @@ def test_generic_backward_7x7_matches_oracle(dev, dtype, C, heads, kind):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_generic_backward_padded_tokens_and_keys(dev, dtype):
+@pytest.mark.parametrize("C,heads", [(128, 4), (256, 2)])
+def test_generic_backward_padded_tokens_and_keys(dev, dtype, C, heads):
     """a10: 49 real tokens of 7x7 windows in 64-token rows, keys >= 49 filled
-    with -10000 (no gradient through them)."""
-    B_, N, C, heads, ws = 8, 64, 128, 4, 7
+    with -10000 (no gradient through them); head dim 32 and 128."""
+    B_, N, ws = 8, 64, 7
     q = workloads.activations((B_, N, C), 370).to(dtype)
     k = workloads.activations((B_, N, C), 371).to(dtype)
     v = workloads.activations((B_, N, C), 372).to(dtype)
@@ -361,5 +365,40 @@ def test_block_backward_matches_oracle(dev, layer_idx, use_land):
             ref_scale = params["attn.q_linear.bias"].grad.norm().item()
             got = p.grad.double().norm().item()
             assert got <= 3e-2 * ref_scale, (got, ref_scale)
+            continue
+        assert _normwise(p.grad, params[name].grad) <= 3e-2, name
+
+
+@pytest.mark.parametrize("full", [False, True])
+def test_block_backward_head_dim_128(dev, full):
+    """TERRA's pretrain block (C=1024, 8 heads of dim 128, window 8, SW-MSA),
+    bf16 backward against the fp32 oracle under autograd: on a reduced grid,
+    and at full size (288x544 tokens) on the input gradient and the attention
+    parameters."""
+    cfg = workloads.CONFIGS["g1"] if full else workloads.CONFIGS["g1"].scaled(16, 32)
+    H, W, C, heads = cfg.height, cfg.width, cfg.channels, cfg.heads
+    blk = workloads.block_for(cfg, 1)
+    with torch.no_grad():
+        for lin in (blk.attn.q_linear, blk.attn.k_linear):
+            lin.weight.mul_(4.0)
+        blk.attn.proj.weight.mul_(8.0)
+        blk.attn.relative_position_bias_table.mul_(25.0)
+    params = {n: p.detach().to(torch.bfloat16).float().clone().requires_grad_(True)
+              for n, p in blk.named_parameters()}
+    blk = blk.to(dev).to(torch.bfloat16)
+    x = workloads.activations((1, H * W, C), 390).to(torch.bfloat16)
+    gy = workloads.activations((1, H * W, C), 391).to(torch.bfloat16)
+    xd = x.to(dev).requires_grad_(True)
+    y = blk(xd)
+    y.backward(gy.to(dev))
+    xr = x.float().requires_grad_(True)
+    yr = so.swin_block_attention(xr, H, W, 8, blk.shift_size, heads, params)
+    yr.backward(gy.float())
+    assert _normwise(y.detach(), yr.detach()) <= 2e-2
+    assert _normwise(xd.grad, xr.grad) <= 3e-2
+    for name, p in blk.named_parameters():
+        assert p.grad is not None, name
+        if name == "attn.k_linear.bias":  # exactly 0 in exact arithmetic (see above)
+            assert p.grad.double().norm().item() <= 3e-2 * params["attn.q_linear.bias"].grad.norm().item()
             continue
         assert _normwise(p.grad, params[name].grad) <= 3e-2, name

@@ -45,6 +45,9 @@ def _expected(idx: np.ndarray, e: int, vals: np.ndarray):
     (torch.bfloat16, 8, 768, 12, False, "ring (head dim 64)"),
     (torch.bfloat16, 8, 192, 6, True, "window-tile (head dim 32, scale below 2^-20)"),
     (torch.bfloat16, 8, 768, 12, True, "window-tile (head dim 64, scale below 2^-20)"),
+    (torch.bfloat16, 8, 1024, 8, False, "ring (head dim 128)"),
+    (torch.bfloat16, 8, 1024, 8, True, "per-wave (head dim 128, scale below 2^-20)"),
+    (torch.float32, 8, 256, 2, False, "per-wave fp32, head dim 128"),
     (torch.bfloat16, 7, 128, 4, False, "per-wave (7x7 windows)"),
     (torch.float32, 8, 64, 2, False, "per-wave fp32"),
     (torch.float32, 7, 96, 3, False, "per-wave fp32, 7x7"),

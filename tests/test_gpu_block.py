@@ -81,6 +81,25 @@ def test_block_c4_shape(dev, layer):
     assert_block_matches(y, ref, x, *TOL[torch.bfloat16])
 
 
+@pytest.mark.parametrize("layer", [0, 1])
+def test_block_g1_shape(dev, layer):
+    """TERRA's shipped pretrain block (C=1024, 8 heads of dim 128, window 8,
+    288x544 tokens) at full size, W-MSA and SW-MSA."""
+    cfg = workloads.CONFIGS["g1"]
+    y, ref, x = _block_case(dev, cfg, layer, torch.bfloat16, seed=305)
+    assert_block_matches(y, ref, x, *TOL[torch.bfloat16])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_block_g1_small_with_land(dev, dtype):
+    """Head dim 128 in fp32 (the contract's 1e-5) and bf16, SW-MSA with a land
+    mask, on a reduced grid."""
+    cfg = workloads.CONFIGS["g1"].scaled(16, 32)
+    land = workloads.land_mask(16, 32, seed=306)
+    y, ref, x = _block_case(dev, cfg, 1, dtype, land=land, seed=307)
+    assert_block_matches(y, ref, x, *TOL[dtype])
+
+
 def test_block_c4_small_sw_msa_with_land(dev):
     """C=768, 12 heads, SW-MSA with a land mask on a small grid."""
     cfg = workloads.CONFIGS["c4"].scaled(32, 48)
