@@ -19,7 +19,7 @@ the training path's attention-core backward on the step's q / k / v;
 `mlp_half` the block's MLP half (SequentialMlp) as one kernel against the same
 module through torch's ops, and `full_block` both halves together.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--config c1..c5]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--config c1..c5|g1]
 
 The other configurations (default c3) run the same measurement: c5 through
 the 12-head fused kernel; c1, c2 and c4 (fp32, 7x7 windows, head dim 64)
@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="c3", choices=("c1", "c2", "c3", "c4", "c5"))
+    ap.add_argument("--config", default="c3", choices=("c1", "c2", "c3", "c4", "c5", "g1"))
     ap.add_argument("--prewarm-s", type=float, default=3.0,
                     help="seconds of untimed steps before the counted warm-up (clock settling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -532,8 +532,8 @@ def main():
         # dq, dk, dv (7 N C elt per window); FLOPs: S recomputed, dP, dV, dQ,
         # dK (10 N^2 C per window).
         "attention_backward": {
-            "kernel": ("window_attn_bwd_kernel<64, 1>" if cfg.channels // cfg.heads == 64 else
-                       "window_attn_bwd_kernel<32, 2>"),
+            "kernel": (f"window_attn_bwd_kernel<{cfg.channels // cfg.heads}, 1>" if cfg.channels // cfg.heads != 32
+                       else "window_attn_bwd_kernel<32, 2>"),
             "us": iso["attention_backward"],
             "GB_s": bwd_bytes / (iso["attention_backward"] * 1e-6) / 1e9,
             "hbm_frac": bwd_bytes / (iso["attention_backward"] * 1e-6) / 1e9 / HBM_PEAK_GBS,

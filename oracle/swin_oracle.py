@@ -23,6 +23,13 @@ brute-force loops, closed forms, library special cases, known answers):
   window_attention_autocast_bf16       brute.attention_autocast_bf16 (loops rounding
                                        to bf16 at the same points); the fp32 core
                                        must fail the same check
+  linear_autocast_bf16                 an exact case (products and sums of small
+                                       integers) and the bf16 rounding of the
+                                       fp32 result (tests/test_oracle.py)
+  swin_block_attention_autocast_bf16   composed of the pinned pieces here; with
+                                       bf16-exact inputs whose every intermediate
+                                       is exact it equals swin_block_attention
+                                       (tests/test_oracle.py)
   swin_block_attention                 brute.swin_block (float64 token loops: own
                                        LayerNorm, frame walk, region ids, relative
                                        index, softmax, reverse), with pad, slab,
@@ -301,6 +308,44 @@ def swin_block_attention(x: torch.Tensor, H: int, W: int, window_size: int, shif
     y = reverse_frame(o, B, H, W, window_size, shift, shift, pad, win_row_begin, win_rows, valid,
                       residual=shortcut)
     return y.view(B, H * W, C)
+
+
+def linear_autocast_bf16(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
+    """F.linear under CUDA autocast(bf16): input, weight and bias cast to bf16,
+    products accumulated in fp32 (the GEMM's accumulator, with the bias added in
+    its fp32 epilogue), the result rounded once to bf16.  Returns bf16."""
+    y = x.to(torch.bfloat16).float() @ weight.to(torch.bfloat16).float().t()
+    if bias is not None:
+        y = y + bias.to(torch.bfloat16).float()
+    return y.to(torch.bfloat16)
+
+
+def swin_block_attention_autocast_bf16(x: torch.Tensor, H: int, W: int, window_size: int, shift: int,
+                                       num_heads: int, params: dict, land: Optional[torch.Tensor] = None,
+                                       eps: float = 1e-5) -> torch.Tensor:
+    """SequentialSwinTransformer.forward (models/transformer.py:138-298) as the
+    reference runs it under CUDA autocast(bf16) (core/runtime/run_model.py:
+    424-448) on bf16 activations: LayerNorm in fp32 (autocast's fp32 list),
+    the q/k/v and proj Linears as linear_autocast_bf16, the core as
+    window_attention_autocast_bf16, and the residual sum of two bf16 tensors
+    rounded to bf16.  Composed of the pinned restatements above; returns bf16
+    [B, H*W, C]."""
+    B, L, C = x.shape
+    p = {k_: v_.detach().float().cpu() for k_, v_ in params.items()}
+    xb = x.to(torch.bfloat16)
+    xn = F.layer_norm(xb.float(), (C,), p["norm1.weight"], p["norm1.bias"], eps).view(B, H, W, C)
+    win = partition_frame(xn, window_size, shift, shift)
+    q = linear_autocast_bf16(win, p["attn.q_linear.weight"], p["attn.q_linear.bias"])
+    k = linear_autocast_bf16(win, p["attn.k_linear.weight"], p["attn.k_linear.bias"])
+    v = linear_autocast_bf16(win, p["attn.v_linear.weight"], p["attn.v_linear.bias"])
+    mask = shift_mask(H, W, window_size, shift) if shift > 0 else None
+    if land is not None:
+        mask = fold_land(mask, land_key_flags(land, window_size, shift, shift))
+    o = window_attention_autocast_bf16(q, k, v, num_heads, (C // num_heads) ** -0.5,
+                                       p.get("attn.relative_position_bias_table"), (window_size, window_size), mask)
+    o = linear_autocast_bf16(o, p["attn.proj.weight"], p["attn.proj.bias"])
+    y = reverse_frame(o.float(), B, H, W, window_size, shift, shift)
+    return (xb.float().view(B, H, W, C) + y).to(torch.bfloat16).view(B, H * W, C)
 
 
 def mlp(x: torch.Tensor, params: dict, use_layernorm: bool = True) -> torch.Tensor:

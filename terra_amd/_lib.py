@@ -37,7 +37,9 @@ STATUS_NAMES = {
 }
 
 LIB_NAME = "libterra_swin.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# TERRA_SWIN_LIB names another build of the same library (the host
+# AddressSanitizer build of the C-ABI checks); by default the in-tree one.
+LIB_PATH = os.environ.get("TERRA_SWIN_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 # Symbols the header declares; tests check the library exports each of them.
 EXPORTED_SYMBOLS = (

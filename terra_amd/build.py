@@ -51,15 +51,26 @@ def _run(cmd, verbose: bool) -> str:
     return out
 
 
-def build_library(verbose: bool = False, jobs: int = 0) -> str:
+# Host-side AddressSanitizer (the C-ABI validation code; device code is built
+# as usual): each flag applies to the host compilation only.
+ASAN_HOST_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+ASAN_LIB_PATH = os.path.join(HERE, "libterra_swin_asan.so")
+
+
+def build_library(verbose: bool = False, jobs: int = 0, asan_host: bool = False) -> str:
     """Compile every HIP source (one hipcc process per source, in parallel)
-    and link them into the shared library; returns its path."""
+    and link them into the shared library; returns its path.  ``asan_host``
+    builds ``libterra_swin_asan.so`` instead, its host code under
+    AddressSanitizer (load it with the sanitizer runtime preloaded and
+    TERRA_SWIN_LIB naming it)."""
     from concurrent.futures import ThreadPoolExecutor
 
-    from ._lib import LIB_PATH  # noqa: WPS433 (path only; does not open the library)
+    from ._lib import LIB_PATH as default_path  # noqa: WPS433 (path only; does not open the library)
 
+    LIB_PATH = ASAN_LIB_PATH if asan_host else default_path
+    extra = ASAN_HOST_FLAGS if asan_host else []
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 8)
-    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"] + extra
     with tempfile.TemporaryDirectory(prefix="_build.", dir=HERE) as tmpdir:
         objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
         cmds = [[hipcc(), *compile_flags, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
@@ -68,7 +79,8 @@ def build_library(verbose: bool = False, jobs: int = 0) -> str:
         fd, tmp = tempfile.mkstemp(prefix="libterra_swin.", suffix=".so.tmp", dir=HERE)
         os.close(fd)
         try:
-            outs.append(_run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose))
+            outs.append(_run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *extra, *objs, "-o", tmp],
+                             verbose))
         except RuntimeError:
             os.unlink(tmp)
             raise
@@ -80,7 +92,20 @@ def build_library(verbose: bool = False, jobs: int = 0) -> str:
     return LIB_PATH
 
 
+def asan_runtime() -> str:
+    """Path of the clang AddressSanitizer runtime that hipcc links against."""
+    out = subprocess.run([hipcc(), "-print-file-name=libclang_rt.asan-x86_64.so"], stdout=subprocess.PIPE,
+                         stderr=subprocess.DEVNULL, text=True).stdout.strip()
+    if out and os.path.isabs(out) and os.path.exists(out):
+        return out
+    import glob
+
+    for cand in sorted(glob.glob("/opt/rocm/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so")):
+        return cand
+    raise RuntimeError("clang AddressSanitizer runtime not found")
+
+
 if __name__ == "__main__":
-    path = build_library(verbose=True)
+    path = build_library(verbose=True, asan_host="--asan-host" in sys.argv)
     print(path)
     sys.exit(0)

@@ -68,6 +68,7 @@ struct BlockParams {
   int32_t packed;            // weights in MFMA fragment order (terra_swin_pack_linear)
   int32_t layernorm;         // 0: xn = x
   int32_t shift_mask;        // analytic shift mask on/off
+  int32_t land_shortcut;     // all-land windows may run unmasked (finite, moderate mask_value)
   float eps, inv_c;
   int32_t H, W, Hp, Wp, shift_h, shift_w, pad_top, pad_left;
   int32_t nWw, win_row_begin, win_rows, valid_begin, valid_end, nWe;
@@ -160,9 +161,12 @@ __device__ __forceinline__ WindowMaskState block_mask_state(const BlockParams& p
                : 0ull;
   // Every key of a window on land, and no shift boundary: the mask adds the
   // same constant to every score, which the softmax cancels, so the window
-  // runs unmasked (22 % of c3's windows).
+  // runs unmasked (22 % of c3's windows).  Only for a finite mask value of
+  // at most 2^12 in magnitude (land_shortcut, set on the host): a larger one
+  // swamps the fp32 scores it is added to (the reference then gives uniform
+  // weights), and -inf gives NaN rows.
   const uint64_t keys = p.a.n_geo >= 64 ? ~0ull : (1ull << p.a.n_geo) - 1ull;
-  if (!m.use_shift && (m.land & keys) == keys) m.land = 0ull;
+  if (p.land_shortcut && !m.use_shift && (m.land & keys) == keys) m.land = 0ull;
   m.use_mask = m.use_shift || m.land != 0ull;
   return m;
 }
@@ -991,7 +995,8 @@ __device__ __forceinline__ void store_pair(const BlockParams& p, int u0, const u
       const int ch = (sl - row * kCpr) ^ ((row >> 1) & 7);  // the chunk tile_slot places in slot sl
       const int t = grid_token(p, u, row >> 3, row & 7);
       const u32x4 val = __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(buf + wi * kTile + sl * 16));
-      // Frame-padding rows fall outside the range.
+      // Frame-padding rows store at the out-of-range marker 0xfffffff0
+      // (chosen per element, so no offset wraps back into range) and are dropped.
       stream_store_sc1(val, out, t >= 0 ? (uint32_t)(t - u.b * p.H * p.W) * (kCpr * 16) + ch * 16 : 0xfffffff0u);
     }
   }
@@ -1930,11 +1935,14 @@ void swin_block_hd64_kernel(const BlockParams p) {
       for (int tt = 0; tt < 4; ++tt) {
         const int row = 16 * tt + c16;
         const int t = grid_token(p, cur, row >> 3, row & 7);
-        const uint32_t base = t >= 0 ? (uint32_t)(t - cur.b * p.H * p.W) * (kCpr * 16) : 0xfffffff0u;
+        const uint32_t base = (uint32_t)(t - cur.b * p.H * p.W) * (kCpr * 16);
 #pragma unroll
         for (int ft = 0; ft < 6; ++ft) {
           const int fb = 96 * wave + 16 * ft + 4 * g;
-          const stream_u32x2 xv = __builtin_amdgcn_raw_buffer_load_b64(xin, base + fb * 2, 0, 0);
+          // Frame-padding rows (t < 0) read at the out-of-range marker
+          // 0xfffffff0 (+ 8 bytes does not wrap), which the buffer range
+          // check turns into zeros; those rows are not stored.
+          const stream_u32x2 xv = __builtin_amdgcn_raw_buffer_load_b64(xin, t >= 0 ? base + fb * 2 : 0xfffffff0u, 0, 0);
           const f32x4& a = ya[ft][tt];
           uint2 out;
           out.x = pack_bf16x2(bf16_bits_to_f32((uint16_t)(xv[0] & 0xffffu)) + (float)(__bf16)a[0],
@@ -2124,6 +2132,9 @@ extern "C" int terra_swin_block_fwd(const void* x, void* y, int dtype, const ter
   p.packed = d.packed_weights != 0;
   p.layernorm = d.layernorm != 0;
   p.shift_mask = d.shift_mask != 0;
+  // The all-land shortcut cancels a constant mask term exactly only while
+  // that term is finite and small enough not to swamp the fp32 scores.
+  p.land_shortcut = fabsf(d.mask_value) <= 4096.f;
   p.eps = d.ln_eps;
   p.inv_c = 1.f / (float)q.channels;
   p.H = q.height;

@@ -99,12 +99,15 @@ class SequentialSwinTransformer(torch.nn.Module):
         shift = ShiftMask.from_geometry(geom) if key[1] else None
         land = None
         if lm is not None:
-            land = self._land_bits_cache.get(key[2])
+            # The bits depend on the frame (shift, padding, emitted rows, valid
+            # windows) as well as on the land grid: both key the cache.
+            land_geom = WindowGeometry(1, geom.height, geom.width, 1, geom.window, geom.shift_h, geom.shift_w,
+                                       geom.pad, geom.win_row_begin, geom.win_rows, geom.valid)
+            land_key = (land_geom, key[2])
+            land = self._land_bits_cache.get(land_key)
             if land is None:
-                land = land_window_bits(lm, WindowGeometry(
-                    1, geom.height, geom.width, 1, geom.window, geom.shift_h, geom.shift_w, geom.pad,
-                    geom.win_row_begin, geom.win_rows, geom.valid))
-                self._land_bits_cache = {key[2]: land}
+                land = land_window_bits(lm, land_geom)
+                self._land_bits_cache = {land_key: land}
         mask = None if shift is None and land is None else WindowMask(shift=shift, land_bits=land)
         self._mask_cache = (key, mask)
         return mask

@@ -31,8 +31,9 @@ AUTOCAST = dict(device_type="cuda", dtype=torch.bfloat16)
 
 def _bf16_weights(params: dict) -> dict:
     """The oracle's parameters as F.linear sees them under bf16 autocast:
-    Linear weights rounded to bf16, everything else fp32."""
-    return {k: (v.bfloat16().float() if k.endswith("weight") and ("linear" in k or "proj" in k or "fc" in k) else v)
+    Linear weights and biases rounded to bf16, everything else fp32."""
+    return {k: (v.bfloat16().float() if k.endswith(("weight", "bias")) and ("linear" in k or "proj" in k or "fc" in k)
+                else v)
             for k, v in params.items()}
 
 
@@ -67,6 +68,32 @@ def test_block_autocast_bf16_activations_run_the_fused_kernel(dev, name, layer, 
     ref = so.swin_block_attention(x, cfg.height, cfg.width, cfg.window, blk.shift_size, cfg.heads,
                                   _bf16_weights(params_of(blk)), land=lm)
     assert_block_matches(y, ref, x, 2e-2, 3e-2)
+
+
+@pytest.mark.parametrize("layer", [0, 1])
+def test_block_autocast_against_reference_autocast_sequence(dev, layer):
+    """The fused kernel under autocast against the reference's own autocast op
+    sequence (oracle.swin_block_attention_autocast_bf16: bf16 q/k/v with bf16
+    biases, bf16 logits, bf16 P, bf16 proj), within the bf16 tolerances, and at
+    least as close to the fp32 restatement as that sequence is (the kernel
+    keeps the logits in fp32 and rounds neither q * scale nor q k^T)."""
+    cfg = workloads.CONFIGS["c3"].scaled(32, 64)
+    lm = workloads.land_mask(cfg.height, cfg.width, seed=708)
+    blk = gain_block(workloads.block_for(cfg, layer, land=lm)).to(dev)
+    x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 709, torch.bfloat16)
+    with torch.no_grad(), torch.amp.autocast(**AUTOCAST), _Count("swin_block") as calls:
+        y = blk(x.to(dev))
+    assert calls.n == 1
+    p = params_of(blk)
+    ac = so.swin_block_attention_autocast_bf16(x, cfg.height, cfg.width, cfg.window, blk.shift_size, cfg.heads, p,
+                                               land=lm)
+    assert_block_matches(y, ac.float(), x, 2e-2, 3e-2)
+    ref = so.swin_block_attention(x, cfg.height, cfg.width, cfg.window, blk.shift_size, cfg.heads,
+                                  _bf16_weights(p), land=lm).double()
+    d_ref = ref - x.double()
+    e_kernel = (torch.linalg.vector_norm(y.double().cpu() - x.double() - d_ref) / torch.linalg.vector_norm(d_ref)).item()
+    e_ac = (torch.linalg.vector_norm(ac.double() - x.double() - d_ref) / torch.linalg.vector_norm(d_ref)).item()
+    assert e_kernel <= 1.5 * e_ac + 1e-3, (e_kernel, e_ac)
 
 
 @pytest.mark.parametrize("name", ["c3", "c4", "c2"])

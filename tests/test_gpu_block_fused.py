@@ -337,3 +337,29 @@ def test_fused_windows_all_on_land(dev, C, heads, window, layer):
     _assert_paths_agree(y_f, y_u, xd)
     ref = so.swin_block_attention(x, H, W, window, blk.shift_size, heads, _params(blk), land=land)
     _assert_matches_oracle(y_f, ref, x)
+
+
+@pytest.mark.parametrize("C,heads,window", [(192, 6, 8), (768, 12, 8)])
+def test_fused_all_land_large_mask_value(dev, C, heads, window):
+    """With a mask value of -1e4 the all-land shortcut is off (it applies only
+    for finite values of magnitude <= 2^12), so all-land windows take the land
+    term like every other window: the fused kernel against the five-stage
+    kernels given the same mask value."""
+    H, W = 4 * window, 6 * window
+    land = torch.zeros(H, W, dtype=torch.bool)
+    land[:, : 3 * window] = True
+    blk = _block(dev, H, W, C, heads, 0, land, window=window)
+    x = workloads.activations((1, H, W, C), 428, torch.bfloat16).to(dev)
+    geom = blk.geometry(1)
+    mask = blk.window_mask(geom)
+    mv = -1e4
+    with torch.no_grad():
+        y_f = kernels.swin_block(x, geom, heads, blk.attn.scale, land_bits=mask.land_bits, mask_value=mv,
+                                 **blk._fused_args())
+        win = kernels.swin_partition_ln(x, geom, blk.norm1.weight, blk.norm1.bias, blk.norm1.eps)
+        qkv = blk.attn.qkv(win)
+        o = kernels.window_attention(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], heads, (window, window),
+                                     blk.attn.scale, bias_table=blk.attn.relative_position_bias_table,
+                                     mask=mask, mask_value=mv)
+        y_u = kernels.swin_reverse(blk.attn.proj(o), geom, residual=x)
+    _assert_paths_agree(y_f.view(1, H * W, C), y_u.view(1, H * W, C), x.view(1, H * W, C))

@@ -128,3 +128,27 @@ def test_mlp_workload_is_seeded_and_named_like_the_reference():
     assert a.fc1.weight.shape == (4 * cfg.channels, cfg.channels)
     assert all(torch.equal(a.state_dict()[k], b.state_dict()[k]) for k in a.state_dict())
     assert not torch.equal(a.fc1.weight, workloads.mlp_for(cfg, 0).fc1.weight)
+
+
+def test_window_mask_land_bits_follow_the_frame(monkeypatch):
+    """The block's cached land bits are rebuilt when the frame changes (here
+    the emitted window rows) even though the land grid is the same tensor."""
+    import terra_amd.transformer as tr
+
+    seen = []
+
+    def fake_bits(land, geom):  # host stand-in for the HIP gather: records the frame it was asked for
+        seen.append(geom.win_row_begin)
+        return torch.tensor([geom.win_row_begin, geom.rows], dtype=torch.int64)
+
+    monkeypatch.setattr(tr, "land_window_bits", fake_bits)
+    land = torch.zeros(32, 16, dtype=torch.bool)
+    blk = SequentialSwinTransformer(layer_idx=1, height=32, width=16, embedding_dim=16, window_size=8, num_heads=2,
+                                    land_mask=land, win_row_begin=0, win_rows=2)
+    m0 = blk.window_mask(blk.geometry(1))
+    assert m0.land_bits.tolist() == [0, 2]
+    assert blk.window_mask(blk.geometry(1)) is m0  # unchanged frame: cached
+    blk.win_row_begin = 1
+    m1 = blk.window_mask(blk.geometry(1))
+    assert m1.land_bits.tolist() == [1, 2]
+    assert seen == [0, 1]

@@ -392,3 +392,66 @@ def test_block_oracle_matches_token_loops(case):
                             win_row_begin=r0, win_rows=rows, valid=valid)
     np.testing.assert_allclose(got.view(B, H, W, C).numpy(), want, rtol=1e-10, atol=1e-10)
     assert not np.allclose(want, x.numpy())  # the attention half changed the tokens it owns
+
+
+def test_linear_autocast_bf16_known_answers():
+    """linear_autocast_bf16: small integers give the exact integer product;
+    1 + 2^-8 (exact in the fp32 accumulator) rounds to even, 1.0, in bf16, and
+    a bias of 1 + 2^-8 is rounded to bf16 (1.0) before it is added."""
+    gen = torch.Generator().manual_seed(93)
+    x = torch.randint(-3, 4, (5, 7), generator=gen).float()
+    w = torch.randint(-3, 4, (4, 7), generator=gen).float()
+    b = torch.randint(-5, 6, (4,), generator=gen).float()
+    got = so.linear_autocast_bf16(x, w, b)
+    assert got.dtype == torch.bfloat16
+    want = x.long() @ w.long().t() + b.long()
+    assert torch.equal(got.float(), want.float())
+    one = so.linear_autocast_bf16(torch.tensor([[1.0, 2.0 ** -8]]), torch.tensor([[1.0, 1.0]]), None)
+    assert one.item() == 1.0
+    three_ulp = so.linear_autocast_bf16(torch.tensor([[1.0, 3 * 2.0 ** -8]]), torch.tensor([[1.0, 1.0]]), None)
+    assert three_ulp.item() == 1.0 + 2.0 ** -6  # 1 + 3/256 rounds to the even neighbour 1 + 4/256
+    biased = so.linear_autocast_bf16(torch.tensor([[0.0]]), torch.tensor([[1.0]]), torch.tensor([1.0 + 2.0 ** -8]))
+    assert biased.item() == 1.0
+
+
+def test_block_autocast_composition_exact_regime():
+    """swin_block_attention_autocast_bf16 equals the fp32 block oracle where
+    every value it rounds is exact in bf16: rows of +-1 with zero mean (a
+    LayerNorm output of exactly +-1 with eps 0), q and k weights zero (uniform
+    probabilities 2^-6), v and proj the identity, zero biases and table; o is
+    then a window mean k / 64 and y = x + o, both exact.  A dropped residual,
+    a transposed or missing proj, or a wrong window map changes y.  In a
+    generic case (random weights, bias table, shift mask, land) the two agree
+    to bf16 tolerance but not bit for bit (the roundings are really there)."""
+    B, H, W, C, nH, ws, s = 1, 8, 8, 8, 2, 4, 2
+    gen = torch.Generator().manual_seed(94)
+    half = torch.randint(0, 2, (B, H, W, C // 2), generator=gen).float() * 2 - 1
+    x = torch.cat([half, -half], -1)[..., torch.randperm(C, generator=gen)]  # +-1, zero mean per token
+    eye = torch.eye(C)
+    zeros = torch.zeros(C, C)
+    p = {"norm1.weight": torch.ones(C), "norm1.bias": torch.zeros(C), "attn.proj.weight": eye,
+         "attn.proj.bias": torch.zeros(C), "attn.q_linear.weight": zeros, "attn.q_linear.bias": torch.zeros(C),
+         "attn.k_linear.weight": zeros, "attn.k_linear.bias": torch.zeros(C), "attn.v_linear.weight": eye,
+         "attn.v_linear.bias": torch.zeros(C), "attn.relative_position_bias_table": torch.zeros((2 * ws - 1) ** 2, nH)}
+    xs = x.view(B, H * W, C)
+    got = so.swin_block_attention_autocast_bf16(xs, H, W, ws, 0, nH, p, eps=0.0).float()
+    win_mean = so.partition_frame(x, ws).mean(1, keepdim=True).expand(-1, ws * ws, -1)
+    want = x + so.reverse_frame(win_mean, B, H, W, ws)
+    assert torch.equal(got.view(B, H, W, C), want)
+    # the fp32 oracle: identical in this regime up to its LayerNorm eps
+    ref = so.swin_block_attention(xs, H, W, ws, 0, nH, p)
+    assert (ref.view(B, H, W, C) - want).abs().max().item() <= 1e-4
+    # generic case
+    x = _rand((B, H * W, C), 95) * 2
+    for i, n in enumerate("qkv"):
+        p[f"attn.{n}_linear.weight"] = _rand((C, C), 96 + i)
+        p[f"attn.{n}_linear.bias"] = _rand((C,), 99 + i) * 0.2
+    p["attn.proj.weight"] = _rand((C, C), 102)
+    p["attn.relative_position_bias_table"] = _rand(((2 * ws - 1) ** 2, nH), 103)
+    land = _rand((H, W), 104) > 0.5
+    ac = so.swin_block_attention_autocast_bf16(x, H, W, ws, s, nH, p, land=land).double()
+    pb = {k_: (v_.bfloat16().float() if "linear" in k_ or "proj" in k_ else v_) for k_, v_ in p.items()}
+    ref = so.swin_block_attention(x.bfloat16().float(), H, W, ws, s, nH, pb, land=land).double()
+    d_ref = ref - x.bfloat16().double()
+    assert (torch.linalg.vector_norm(ac - ref) / torch.linalg.vector_norm(d_ref)).item() <= 3e-2
+    assert not torch.equal(ac, ref.bfloat16().double())
