@@ -228,6 +228,42 @@ def cpu_baseline(cfg, blk, land, budget_s: float):
     }
 
 
+def training_step_us(cfg, dev, warmup: int = 2, reps: int = 5):
+    """Median time (us) of one fp32-parameter, bf16-autocast forward + backward
+    of the attention half and the MLP half on `cfg` (see main)."""
+    import torch
+
+    from terra_amd import workloads
+
+    land = workloads.land_mask(cfg.height, cfg.width, seed=42) if cfg.land else None
+    blk = workloads.block_for(cfg, 1 if cfg.shift else 0, land=land).to(dev)
+    mlp = workloads.mlp_for(cfg, 1).to(dev)
+    x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 1004).to(dev)
+    gy = workloads.activations(tuple(x.shape), 1005).to(dev)
+    params = list(blk.parameters()) + list(mlp.parameters())
+
+    def step():
+        xd = x.detach().requires_grad_(True)
+        with torch.amp.autocast(device_type="cuda", dtype=torch.bfloat16):
+            y = mlp(blk(xd))
+        y.backward(gy)
+        for p in params:
+            p.grad = None
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        step()
+        e1.record()
+        torch.cuda.synchronize()
+        samples.append(1e3 * e0.elapsed_time(e1))
+    return statistics.median(samples)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -404,6 +440,14 @@ def main():
         last_call["mlp_torch"] = (mlp, (y_blk,), {})
         iso["mlp_torch"] = isolated_us("mlp_torch")
         mlp.use_fused_mlp = True
+        # A training step of the whole block (attention half + MLP half) as the
+        # reference trains it (core/runtime/run_model.py:424-448): fp32 input
+        # and parameters under bf16 autocast, forward then backward of a
+        # synthetic output gradient (no optimizer update).  The LayerNorms and
+        # their backward, partition / reverse and the attention core with its
+        # backward run on the HIP kernels; the projection, fc1 and fc2 GEMMs
+        # and their backward on hipBLASLt through torch.
+        train = training_step_us(cfg, dev)
     finally:
         for n in names:
             setattr(kernels, n, orig[n])
@@ -584,6 +628,12 @@ def main():
         t_mlp = iso["mlp_torch"]
     # The whole Swin block (attention half + MLP half).
     res["full_block"] = {"us": t_attn_half + t_mlp, "tokens_per_s": tokens / ((t_attn_half + t_mlp) * 1e-6)}
+    res["training_step"] = {
+        "us": train, "tokens_per_s": tokens / (train * 1e-6),
+        "what": ("forward + backward of the attention half and the MLP half, fp32 input and parameters under bf16 "
+                 "autocast (the reference's training mode), synthetic output gradient, no optimizer update; "
+                 "median of 5 after 2 warm-up steps"),
+    }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg, blk, land if land is not None else
                                            torch.zeros(cfg.height, cfg.width, dtype=torch.bool), args.cpu_seconds)

@@ -193,6 +193,30 @@ int terra_swin_partition_ln(const void* x, void* windows, int dtype,
                             const float* beta, float eps, float pad_value,
                             void* stream);
 
+/* Backward of terra_swin_partition_ln (with pad_value constant: padded slots
+ * carry no gradient), plus an optional residual gradient.
+ * Replaces the autograd backward of
+ *           x = self.norm1(x)      (nn.LayerNorm)        models/transformer.py:98, 150
+ *           roll + window_partition                     models/transformer.py:179-225
+ * as the training step runs it (core/runtime/run_model.py:362-617), and of
+ * norm2 in SequentialMlp (models/mlp.py:159) with an identity frame (window 1,
+ * no shift, x viewed as [1, tokens, 1, C]).
+ * For every grid token t of x [B, H, W, C]: g = the gradient in dwindows
+ * [B * nW_emitted, ws*ws, C] of the slot partition wrote t to (0 where the
+ * frame does not emit t or emits a pad window), and
+ *   dx[t] = rstd (gamma g - mean_c(gamma g) - xhat mean_c(gamma g xhat))
+ *           (+ dresidual[t] if dresidual != NULL)
+ * with mean, rstd and xhat = (x - mean) rstd recomputed from x as the forward
+ * computes them (fp32), rounded once to the activation dtype.  When dgamma /
+ * dbeta are not NULL the call ADDS sum_t g xhat and sum_t g into them (fp32
+ * [C]; the caller zeroes them; float atomics, so the summation order varies).
+ * gamma: C floats or NULL (1).  dx may equal dresidual but must not overlap x.
+ * C <= 1024 in rows of whole 16-byte chunks of at most 4096 bytes.
+ */
+int terra_swin_partition_ln_bwd(const void* dwindows, const void* x, const void* dresidual, void* dx,
+                                int dtype, const terra_swin_geom* geom, const float* gamma, float eps,
+                                float* dgamma, float* dbeta, void* stream);
+
 /* Fused window reverse + inverse cyclic shift + crop (+ residual add).
  * Replaces  window_reverse(attn_windows, ws, H, W)    models/utils.py:41-45
  *           torch.roll(shifted_x, (s, s), dims=(1, 2))  models/transformer.py:246

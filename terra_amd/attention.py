@@ -86,24 +86,50 @@ class WindowAttention(torch.nn.Module):
         self.proj = make_linear_with_seed(self.dim, self.dim, bias=True, init_seed=seed(4))
         self.softmax = torch.nn.Softmax(dim=-1)
 
+    def _cached(self, name: str, tensors, build):
+        """``build()`` cached under ``name`` until any of ``tensors`` changes
+        (data pointer, in-place version or dtype).  Only for calls without
+        gradients: the result is detached."""
+        key = tuple(None if t is None else (t.data_ptr(), t._version, t.dtype, t.device) for t in tensors)
+        cache = self.__dict__.setdefault("_derived", {})
+        hit = cache.get(name)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        with torch.no_grad():
+            val = build()
+        cache[name] = (key, val)
+        return val
+
     def qkv(self, x: torch.Tensor) -> torch.Tensor:
         """The three projections as one GEMM: [B_, N, C] -> [B_, N, 3C]."""
-        w = torch.cat([self.q_linear.weight, self.k_linear.weight, self.v_linear.weight], 0)
-        b = None
-        if self.q_linear.bias is not None:
-            b = torch.cat([self.q_linear.bias, self.k_linear.bias, self.v_linear.bias], 0)
+        lins = (self.q_linear, self.k_linear, self.v_linear)
+        has_bias = self.q_linear.bias is not None
+        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
+            w = torch.cat([l.weight for l in lins], 0)
+            b = torch.cat([l.bias for l in lins], 0) if has_bias else None
+        else:  # the concatenated weights, kept until a parameter changes
+            w, b = self._cached("qkv", [l.weight for l in lins] + [l.bias for l in lins], lambda: (
+                torch.cat([l.weight for l in lins], 0), torch.cat([l.bias for l in lins], 0) if has_bias else None))
         return F.linear(x, w, b)
+
+    def _table(self) -> Optional[torch.Tensor]:
+        """The bias table as the core takes it: the parameter itself when a
+        gradient may flow into it, else an fp32 copy kept until it changes."""
+        if not self.use_relative_position_bias:
+            return None
+        t = self.relative_position_bias_table
+        if t.dtype == torch.float32 or (torch.is_grad_enabled() and t.requires_grad):
+            return t
+        return self._cached("table", [t], lambda: t.detach().to(torch.float32).contiguous())
 
     def core(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
              mask: Union[None, torch.Tensor, ShiftMask, WindowMask] = None,
              n_real: Optional[int] = None) -> torch.Tensor:
         """Fused core on projected q/k/v [B_, N, C] (row strides may exceed C)."""
-        table = self.relative_position_bias_table if self.use_relative_position_bias else None
         return autograd.window_attention(q, k, v, self.num_heads, self.window_size, self.scale,
-                                         bias_table=table, mask=mask, n_real=n_real)
+                                         bias_table=self._table(), mask=mask, n_real=n_real)
 
     def forward(self, x: torch.Tensor, mask=None) -> torch.Tensor:
-        table = self.relative_position_bias_table if self.use_relative_position_bias else None
         o = autograd.window_attention_qkv(self.qkv(x), self.num_heads, self.window_size, self.scale,
-                                          bias_table=table, mask=mask)
+                                          bias_table=self._table(), mask=mask)
         return self.proj(o)

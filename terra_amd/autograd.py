@@ -59,6 +59,94 @@ class _Reverse(torch.autograd.Function):
         return d_windows, None, (grad if ctx.has_residual else None)
 
 
+class _PartitionLN(torch.autograd.Function):
+    """LayerNorm over C + pad + roll + partition (terra_swin_partition_ln),
+    backward by terra_swin_partition_ln_bwd: dx, and the weight / bias
+    gradients summed over the tokens."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, geom, eps):
+        ctx.geom, ctx.eps = geom, eps
+        ctx.save_for_backward(x, weight, bias)
+        return kernels.swin_partition_ln(x, geom, weight, bias, eps)
+
+    @staticmethod
+    def backward(ctx, grad: torch.Tensor):
+        x, weight, bias = ctx.saved_tensors
+        dw = db = None
+        if weight is not None and ctx.needs_input_grad[1]:
+            dw = torch.zeros(weight.shape, dtype=torch.float32, device=x.device)
+        if bias is not None and ctx.needs_input_grad[2]:
+            db = torch.zeros(bias.shape, dtype=torch.float32, device=x.device)
+        dx = kernels.swin_partition_ln_backward(grad.contiguous(), x, ctx.geom, weight, ctx.eps, dweight=dw, dbias=db)
+        return (dx, None if dw is None else dw.to(weight.dtype), None if db is None else db.to(bias.dtype), None, None)
+
+
+def partition_ln(x: torch.Tensor, geom: WindowGeometry, weight: Optional[torch.Tensor],
+                 bias: Optional[torch.Tensor], eps: float) -> torch.Tensor:
+    """:func:`kernels.swin_partition_ln` with gradients for x and the
+    LayerNorm affine parameters."""
+    if _needs_grad(x, weight, bias):
+        return _PartitionLN.apply(x, weight, bias, geom, eps)
+    return kernels.swin_partition_ln(x, geom, weight, bias, eps)
+
+
+class _Mlp(torch.autograd.Function):
+    """SequentialMlp.forward (models/mlp.py:152-172) for training:
+    y = x + fc2(GELU(fc1(LayerNorm(x)))).  The LayerNorm forward and its
+    backward (with the residual gradient added in the same kernel) run on
+    terra_swin_partition_ln / _bwd over the token rows; the four GEMMs of
+    the backward on hipBLASLt through torch, in the dtypes autocast gave the
+    forward's GEMMs; the GELU derivative is the exact (erf) one."""
+
+    @staticmethod
+    def forward(ctx, x, ln_w, ln_b, w1, b1, w2, b2, eps):
+        C = x.shape[-1]
+        rows = x.reshape(-1, C).contiguous()
+        geom = kernels.rows_geometry(rows.shape[0], C)
+        xn = kernels.swin_partition_ln(rows.view(1, -1, 1, C), geom, ln_w, ln_b, eps).view(-1, C)
+        h1 = torch.nn.functional.linear(xn, w1, b1)
+        a = torch.nn.functional.gelu(h1)
+        h2 = torch.nn.functional.linear(a, w2, b2)
+        y = rows + h2
+        ctx.eps, ctx.geom, ctx.shape = eps, geom, x.shape
+        ctx.autocast = torch.is_autocast_enabled(x.device.type)
+        ctx.save_for_backward(rows, ln_w, ln_b, xn, h1, a, w1, w2)
+        return y.view(x.shape[:-1] + (y.shape[-1],))
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor):
+        rows, ln_w, ln_b, xn, h1, a, w1, w2 = ctx.saved_tensors
+        C = rows.shape[-1]
+        dy = dy.reshape(-1, dy.shape[-1])
+        gemm_dtype = h1.dtype  # the forward GEMMs' dtype (bf16 under autocast)
+        dh2 = dy.to(gemm_dtype)
+        w2c, w1c = w2.to(gemm_dtype), w1.to(gemm_dtype)
+        da = dh2 @ w2c
+        dw2 = (dh2.t() @ a.to(gemm_dtype)) if ctx.needs_input_grad[5] else None
+        db2 = dh2.float().sum(0) if ctx.needs_input_grad[6] else None
+        dh1 = torch.ops.aten.gelu_backward(da, h1)
+        dxn = dh1 @ w1c
+        dw1 = (dh1.t() @ xn.to(gemm_dtype)) if ctx.needs_input_grad[3] else None
+        db1 = dh1.float().sum(0) if ctx.needs_input_grad[4] else None
+        dlw = torch.zeros(C, dtype=torch.float32, device=rows.device) if (
+            ln_w is not None and ctx.needs_input_grad[1]) else None
+        dlb = torch.zeros(C, dtype=torch.float32, device=rows.device) if (
+            ln_b is not None and ctx.needs_input_grad[2]) else None
+        dx = kernels.swin_partition_ln_backward(
+            dxn.to(rows.dtype).contiguous().view(-1, 1, C), rows.view(1, -1, 1, C), ctx.geom, ln_w, ctx.eps,
+            dresidual=dy.to(rows.dtype).contiguous(), dweight=dlw, dbias=dlb)
+        cast = lambda g, p: None if g is None else g.to(p.dtype)  # noqa: E731
+        return (dx.view(ctx.shape), cast(dlw, ln_w), cast(dlb, ln_b), cast(dw1, w1), cast(db1, w1),
+                cast(dw2, w2), cast(db2, w2), None)
+
+
+def mlp(x: torch.Tensor, ln_w: Optional[torch.Tensor], ln_b: Optional[torch.Tensor], w1: torch.Tensor,
+        b1: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor, eps: float) -> torch.Tensor:
+    """The MLP half with gradients (see :class:`_Mlp`)."""
+    return _Mlp.apply(x, ln_w, ln_b, w1, b1, w2, b2, eps)
+
+
 def partition(x: torch.Tensor, geom: WindowGeometry) -> torch.Tensor:
     """:func:`kernels.swin_partition` with a gradient (reverse)."""
     if _needs_grad(x):

@@ -219,10 +219,12 @@ __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* _
   // are issued first and the row loads right after (vector memory completes
   // in order, so the staging waits for gamma / beta only); the barrier is
   // LDS-only, and the rows stay in flight across it.
-  __shared__ __attribute__((aligned(16))) float s_gamma[kLnMaxChannels];
-  __shared__ __attribute__((aligned(16))) float s_beta[kLnMaxChannels];
-  constexpr int kGB = kLnMaxChannels / kThreads;
-  static_assert(kGB * kThreads == kLnMaxChannels, "whole staging rounds");
+  // Sized for the widest row this instance serves (CPL chunks on each of kL
+  // lanes), so narrow rows stage and hold no more than they use.
+  constexpr int kMaxC = CPL * kL * E;
+  __shared__ __attribute__((aligned(16))) float s_gamma[kMaxC];
+  __shared__ __attribute__((aligned(16))) float s_beta[kMaxC];
+  constexpr int kGB = (kMaxC + kThreads - 1) / kThreads;
   const int C = ln.chunks * E;
   float gv[kGB], bv[kGB];
 #pragma unroll
@@ -322,6 +324,160 @@ __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* _
       }
       stream_store_sc1(val, out, row_off + c * 16);
     }
+  }
+}
+
+// ---- backward of the fused LayerNorm + pad + roll + partition ---------------
+// Gather form over the grid tokens, like reverse_kernel: token (b, h, w) reads
+// the gradient g of the window slot partition wrote it to (zero when the
+// frame does not emit it or emits a pad window there), recomputes the
+// forward's statistics from its row of x (two-pass fp32, as
+// partition_ln_kernel), and writes
+//   dx = rstd (gamma g - mean_c(gamma g) - xhat mean_c(gamma g xhat)) (+ dres)
+// rounded once to the activation dtype, xhat = (x - mean) rstd.  The kL lanes
+// of a token hold its chunks as in the forward.  Workgroups loop over the
+// tokens (grid-stride) and keep per-lane sums of g xhat and g for the
+// channels they hold; at the end each workgroup reduces them in LDS and adds
+// them to dgamma / dbeta with one float atomic per channel.
+struct LnBwdParams {
+  const float* gamma;  // C floats or NULL (1)
+  float* dgamma;       // C floats, accumulated, or NULL
+  float* dbeta;        // C floats, accumulated, or NULL
+  float eps;
+  float inv_c;
+  int32_t chunks;      // 16-byte chunks per token row
+  uint32_t tokens;     // grid tokens B * H * W
+};
+
+template <int DT, int CPL, int kL, bool kRes>
+__global__ __launch_bounds__(kThreads) void partition_ln_bwd_kernel(const uint8_t* __restrict__ dwin,
+                                                                    const uint8_t* __restrict__ x, uint8_t* dx,
+                                                                    const uint8_t* dres, const CopyGeom g,
+                                                                    const LnBwdParams ln) {
+  constexpr int kTokensPerPass = kThreads / kL;
+  constexpr int E = LnElt<DT>::kPerChunk;
+  constexpr int kMaxC = CPL * kL * E;
+  __shared__ __attribute__((aligned(16))) float s_gamma[kMaxC];
+  __shared__ float s_dg[kMaxC];
+  __shared__ float s_db[kMaxC];
+  const int C = ln.chunks * E;
+  for (int c = threadIdx.x; c < kMaxC; c += kThreads) {
+    s_gamma[c] = (ln.gamma != nullptr && c < C) ? ln.gamma[c] : 1.f;
+    s_dg[c] = 0.f;
+    s_db[c] = 0.f;
+  }
+  __syncthreads();
+  const int sub = threadIdx.x & (kL - 1);
+  float acc_g[CPL][E], acc_b[CPL][E];  // this lane's sums of g xhat and g over its tokens
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc_g[k][e] = acc_b[k][e] = 0.f;
+
+  for (uint32_t tok = blockIdx.x * kTokensPerPass + threadIdx.x / kL; tok < ln.tokens;
+       tok += gridDim.x * kTokensPerPass) {  // uniform per lane group
+    uint32_t rest, sw, b, sh;
+    g.fd_W.divmod(tok, rest, sw);
+    g.fd_H.divmod(rest, b, sh);
+    int fi = (int)sh + g.pad_top - g.shift_h;
+    int fj = (int)sw + g.pad_left - g.shift_w;
+    if (fi < 0) fi += g.Hp;
+    if (fj < 0) fj += g.Wp;
+    uint32_t wr, ti, wc, tj;
+    g.fd_ws.divmod((uint32_t)fi, wr, ti);
+    g.fd_ws.divmod((uint32_t)fj, wc, tj);
+    const int wr_l = (int)wr - g.win_row_begin;
+    const int wl = wr_l * g.nWw + (int)wc;
+    const bool have = (unsigned)wr_l < (unsigned)g.win_rows &&
+                      (g.valid_end <= 0 || (wl >= g.valid_begin && wl < g.valid_end));
+    const int64_t slot = have ? ((int64_t)b * g.win_rows * g.nWw + wl) * g.N + (int64_t)(ti * g.ws + tj) : 0;
+    const u32x4* xs = reinterpret_cast<const u32x4*>(x + (int64_t)tok * g.row_bytes);
+    const u32x4* gs = reinterpret_cast<const u32x4*>(dwin + slot * g.row_bytes);
+    const u32x4* rs = reinterpret_cast<const u32x4*>(dres + (kRes ? (int64_t)tok * g.row_bytes : 0));
+    // Unconditional loads: chunks past the row read chunk 0 and count as zeros.
+    u32x4 xr[CPL], gr[CPL], rr[kRes ? CPL : 1];
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = sub + kL * k < ln.chunks ? sub + kL * k : 0;
+      xr[k] = __builtin_nontemporal_load(xs + c);
+      gr[k] = __builtin_nontemporal_load(gs + c);
+      if constexpr (kRes) rr[k] = __builtin_nontemporal_load(rs + c);
+    }
+    float v[CPL][E], gv[CPL][E];
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const bool pc = sub + kL * k < ln.chunks;
+      unpack_chunk<DT>(pc ? xr[k] : u32x4(0u), v[k]);
+      unpack_chunk<DT>((pc && have) ? gr[k] : u32x4(0u), gv[k]);
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k)
+#pragma unroll
+      for (int e = 0; e < E; ++e) sum += v[k][e];  // absent chunks hold zeros
+    const float mean = group_sum<kL>(sum) * ln.inv_c;
+    float sq = 0.f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const bool pc = sub + kL * k < ln.chunks;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float d = v[k][e] - mean;
+        sq += pc ? d * d : 0.f;
+      }
+    }
+    const float rstd = rsqrtf(group_sum<kL>(sq) * ln.inv_c + ln.eps);
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = sub + kL * k;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float xh = (v[k][e] - mean) * rstd;
+        const float gm = c < ln.chunks ? s_gamma[c * E + e] : 0.f;
+        acc_g[k][e] += gv[k][e] * xh;
+        acc_b[k][e] += gv[k][e];
+        const float dxh = gv[k][e] * gm;
+        v[k][e] = xh;    // from here on: xhat
+        gv[k][e] = dxh;  // from here on: gamma g
+        s1 += dxh;
+        s2 += dxh * xh;
+      }
+    }
+    s1 = group_sum<kL>(s1) * ln.inv_c;
+    s2 = group_sum<kL>(s2) * ln.inv_c;
+    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(dx + (int64_t)tok * g.row_bytes, (uint32_t)g.row_bytes);
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = sub + kL * k;
+      if (c >= ln.chunks) continue;
+      float y[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) y[e] = rstd * (gv[k][e] - s1 - v[k][e] * s2);
+      if constexpr (kRes) {
+        float r[E];
+        unpack_chunk<DT>(rr[k], r);
+#pragma unroll
+        for (int e = 0; e < E; ++e) y[e] += r[e];
+      }
+      stream_store_sc1(pack_chunk<DT>(y), out, (uint32_t)c * 16);
+    }
+  }
+  if (ln.dgamma == nullptr && ln.dbeta == nullptr) return;  // uniform
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int c = sub + kL * k;
+    if (c >= ln.chunks) continue;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      atomicAdd(&s_dg[c * E + e], acc_g[k][e]);
+      atomicAdd(&s_db[c * E + e], acc_b[k][e]);
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < C; c += kThreads) {
+    if (ln.dgamma != nullptr) unsafeAtomicAdd(ln.dgamma + c, s_dg[c]);
+    if (ln.dbeta != nullptr) unsafeAtomicAdd(ln.dbeta + c, s_db[c]);
   }
 }
 
@@ -520,6 +676,51 @@ void dispatch_partition_ln(int cpl, const void* x, void* win, const CopyGeom& g,
   else launch_partition_ln<DT, 16, 16>(x, win, g, ln, s);                // fp32 C = 1024
 }
 
+// Resident workgroups of the LayerNorm backward (grid-stride over the
+// tokens), queried per device and instance once.
+template <int DT, int CPL, int kL, bool kRes>
+int launch_partition_ln_bwd(const void* dwin, const void* x, void* dx, const void* dres, const CopyGeom& g,
+                            const LnBwdParams& ln, hipStream_t s) {
+  auto kern = partition_ln_bwd_kernel<DT, CPL, kL, kRes>;
+  constexpr int kMaxDevices = 64;
+  static int cache[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(TERRA_ERR_LAUNCH, "cannot query the current device");
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, 0) != hipSuccess)
+      return fail(TERRA_ERR_LAUNCH, "cannot size the LayerNorm backward grid for this device");
+    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  constexpr uint32_t kTokensPerPass = kThreads / kL;
+  const uint32_t need = (ln.tokens + kTokensPerPass - 1) / kTokensPerPass;
+  const uint32_t blocks = need < (uint32_t)cache[dev] ? need : (uint32_t)cache[dev];
+  kern<<<blocks, kThreads, 0, s>>>((const uint8_t*)dwin, (const uint8_t*)x, (uint8_t*)dx, (const uint8_t*)dres, g,
+                                   ln);
+  return TERRA_OK;
+}
+
+template <int DT, bool kRes>
+int dispatch_partition_ln_bwd(int cpl, const void* dwin, const void* x, void* dx, const void* dres,
+                              const CopyGeom& g, const LnBwdParams& ln, hipStream_t s) {
+  if (cpl <= 1) return launch_partition_ln_bwd<DT, 1, 8, kRes>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 2) return launch_partition_ln_bwd<DT, 2, 8, kRes>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 3) return launch_partition_ln_bwd<DT, 3, 8, kRes>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 4) return launch_partition_ln_bwd<DT, 4, 8, kRes>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 8) return launch_partition_ln_bwd<DT, 4, 16, kRes>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 12) return launch_partition_ln_bwd<DT, 6, 16, kRes>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 16 || DT != TERRA_DTYPE_F32) return launch_partition_ln_bwd<DT, 8, 16, kRes>(dwin, x, dx, dres, g, ln, s);
+  // fp32 rows of more than 512 channels (16-bit rows of at most 1024 channels
+  // never get here)
+  if constexpr (DT == TERRA_DTYPE_F32) {
+    if (cpl <= 24) return launch_partition_ln_bwd<DT, 12, 16, kRes>(dwin, x, dx, dres, g, ln, s);
+    return launch_partition_ln_bwd<DT, 16, 16, kRes>(dwin, x, dx, dres, g, ln, s);
+  }
+  return TERRA_OK;
+}
+
 template <int VB, int DT>
 void launch_reverse(const void* win, void* y, const void* res, const CopyGeom& g, hipStream_t s) {
   const uint32_t blocks = (g.total + kThreads * kUnroll - 1) / (kThreads * kUnroll);
@@ -631,4 +832,58 @@ extern "C" int terra_swin_reverse(const void* windows, void* y, const void* resi
     default: launch_reverse<1, TERRA_DTYPE_U8>(windows, y, nullptr, g, s); break;
   }
   return launch_status("terra_swin_reverse");
+}
+
+extern "C" int terra_swin_partition_ln_bwd(const void* dwindows, const void* x, const void* dresidual, void* dx,
+                                           int dtype, const terra_swin_geom* geom, const float* gamma, float eps,
+                                           float* dgamma, float* dbeta, void* stream) {
+  clear_error();
+  if (dwindows == nullptr || x == nullptr || dx == nullptr) return fail(TERRA_ERR_NULL, "dwindows, x or dx is NULL");
+  if (dtype != TERRA_DTYPE_F32 && dtype != TERRA_DTYPE_BF16 && dtype != TERRA_DTYPE_F16)
+    return fail(TERRA_ERR_DTYPE, "fused LayerNorm backward supports f32, f16 and bf16 (got dtype %d)", dtype);
+  if (!(eps >= 0.f)) return fail(TERRA_ERR_SHAPE, "eps must be non-negative");
+  CopyGeom g;
+  int vb = 0;
+  const int st = prepare(geom, dtype, false, &g, &vb, dwindows, x, dx);
+  if (st != TERRA_OK) return st;
+  if (vb != 16 || (dresidual != nullptr && ((uintptr_t)dresidual & 15u) != 0))
+    return fail(TERRA_ERR_ALIGN, "fused LayerNorm backward needs 16-byte aligned rows and tensors");
+  for (const float* p : {gamma, (const float*)dgamma, (const float*)dbeta})
+    if (p != nullptr && (uintptr_t)p % 4 != 0) return fail(TERRA_ERR_ALIGN, "gamma / dgamma / dbeta must be 4-byte aligned");
+  const int chunks = (int)(g.row_bytes / 16);
+  if (chunks > kLnMaxChunks || geom->channels > kLnMaxChannels)
+    return fail(TERRA_ERR_UNSUPPORTED, "fused LayerNorm backward handles up to %d channels in rows of up to %d bytes",
+                kLnMaxChannels, kLnMaxChunks * 16);
+  const int64_t grid_bytes = (int64_t)geom->batch * geom->height * geom->width * g.row_bytes;
+  const uintptr_t xa = (uintptr_t)x, da = (uintptr_t)dx;
+  if (xa < da + (uintptr_t)grid_bytes && da < xa + (uintptr_t)grid_bytes)
+    return fail(TERRA_ERR_SHAPE, "dx must not overlap x");
+  LnBwdParams ln;
+  ln.gamma = gamma;
+  ln.dgamma = dgamma;
+  ln.dbeta = dbeta;
+  ln.eps = eps;
+  ln.inv_c = 1.0f / (float)geom->channels;
+  ln.chunks = chunks;
+  ln.tokens = (uint32_t)((int64_t)geom->batch * geom->height * geom->width);
+  const int cpl = (chunks + kLnLanes - 1) / kLnLanes;
+  hipStream_t s = (hipStream_t)stream;
+  int rc;
+  const bool res = dresidual != nullptr;
+  switch (dtype) {
+    case TERRA_DTYPE_F32:
+      rc = res ? dispatch_partition_ln_bwd<TERRA_DTYPE_F32, true>(cpl, dwindows, x, dx, dresidual, g, ln, s)
+               : dispatch_partition_ln_bwd<TERRA_DTYPE_F32, false>(cpl, dwindows, x, dx, nullptr, g, ln, s);
+      break;
+    case TERRA_DTYPE_F16:
+      rc = res ? dispatch_partition_ln_bwd<TERRA_DTYPE_F16, true>(cpl, dwindows, x, dx, dresidual, g, ln, s)
+               : dispatch_partition_ln_bwd<TERRA_DTYPE_F16, false>(cpl, dwindows, x, dx, nullptr, g, ln, s);
+      break;
+    default:
+      rc = res ? dispatch_partition_ln_bwd<TERRA_DTYPE_BF16, true>(cpl, dwindows, x, dx, dresidual, g, ln, s)
+               : dispatch_partition_ln_bwd<TERRA_DTYPE_BF16, false>(cpl, dwindows, x, dx, nullptr, g, ln, s);
+      break;
+  }
+  if (rc != TERRA_OK) return rc;
+  return launch_status("terra_swin_partition_ln_bwd");
 }

@@ -229,6 +229,59 @@ def swin_partition_ln(x: torch.Tensor, geom: WindowGeometry, weight: Optional[to
     return out
 
 
+def swin_partition_ln_backward(dwindows: torch.Tensor, x: torch.Tensor, geom: WindowGeometry,
+                               weight: Optional[torch.Tensor], eps: float,
+                               dresidual: Optional[torch.Tensor] = None, dweight: Optional[torch.Tensor] = None,
+                               dbias: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Gradient of :func:`swin_partition_ln` with respect to ``x`` [B, H, W, C]
+    given the windows' gradient ``dwindows`` [B * nW, ws*ws, C] (plus
+    ``dresidual``, the gradient reaching x by another path, if given).
+    ``dweight`` / ``dbias``: fp32 [C] tensors the LayerNorm weight and bias
+    gradients are ADDED into, or None.  ``out`` may be ``dresidual``."""
+    dev = _require_device(dwindows, x)
+    code = _dtype_code(x, (torch.float32, torch.float16, torch.bfloat16))
+    shape = (geom.batch, geom.height, geom.width, geom.channels)
+    if tuple(x.shape) != shape or not x.is_contiguous():
+        raise ValueError(f"x must be a contiguous {shape} tensor")
+    n = geom.window * geom.window
+    if dwindows.dtype != x.dtype or dwindows.numel() != geom.num_windows * n * geom.channels \
+            or not dwindows.is_contiguous():
+        raise ValueError(f"dwindows must be a contiguous {x.dtype} tensor of {geom.num_windows} x {n} x "
+                         f"{geom.channels} elements")
+    for name, t in (("dresidual", dresidual), ("out", out)):
+        if t is not None and (t.dtype != x.dtype or t.numel() != x.numel() or not t.is_contiguous()
+                              or t.device != dev):
+            raise ValueError(f"{name} must be a contiguous {x.dtype} tensor like x on {dev}")
+    w32 = None
+    if weight is not None:
+        _require_device(x, weight)
+        if weight.dim() != 1 or weight.shape[0] != geom.channels:
+            raise ValueError(f"LayerNorm weight must be [{geom.channels}]")
+        w32 = weight.detach().to(torch.float32).contiguous()
+    for name, t in (("dweight", dweight), ("dbias", dbias)):
+        if t is not None and (t.dtype != torch.float32 or tuple(t.shape) != (geom.channels,) or not t.is_contiguous()
+                              or t.device != dev):
+            raise ValueError(f"{name} must be a contiguous fp32 [{geom.channels}] tensor on {dev}")
+    if out is None:
+        out = torch.empty(shape, dtype=x.dtype, device=dev)
+    if geom.batch == 0:
+        return out.view(shape)
+    c_geom = geom.to_c()
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_partition_ln_bwd(_ptr(dwindows), _ptr(x), _ptr(dresidual), _ptr(out), code,
+                                                     ctypes.byref(c_geom), _ptr(w32), float(eps), _ptr(dweight),
+                                                     _ptr(dbias), _stream(dev))
+    _lib.check(st, "terra_swin_partition_ln_bwd")
+    return out.view(shape)
+
+
+def rows_geometry(tokens: int, channels: int) -> WindowGeometry:
+    """The identity frame over ``tokens`` rows of C channels (x viewed as
+    [1, tokens, 1, C], window 1, no shift): partition and its LayerNorm /
+    backward variants then act on plain token rows."""
+    return WindowGeometry(1, tokens, 1, channels, 1)
+
+
 def swin_reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional[torch.Tensor] = None,
                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused window_reverse + roll(+shift) + crop (+ residual) to [B, H, W, C]."""

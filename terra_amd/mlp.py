@@ -8,7 +8,9 @@ packs ``fc1.weight`` / ``fc2.weight`` with ``kernels.pack_linear`` and caches
 the packed weights and fp32 copies of the small parameters until a
 parameter's data pointer or in-place version changes.
 
-Other shapes and dtypes, and any call that needs a gradient, run the
+A call that needs a gradient runs autograd.mlp: the LayerNorm forward and
+backward (residual gradient included) on the HIP LayerNorm kernels over the
+token rows, the GEMMs on hipBLASLt.  Other shapes and dtypes run the
 reference's own sequence of torch modules on the device (norm2, fc1, act,
 fc2, residual).  Parameter names (``norm2``, ``fc1``, ``fc2``) and the seeded
 initialisation follow the reference so its checkpoints load.
@@ -19,7 +21,7 @@ from typing import Optional
 
 import torch
 
-from . import config, kernels
+from . import autograd, config, kernels
 from .attention import make_linear_with_seed
 
 
@@ -70,6 +72,24 @@ class SequentialMlp(torch.nn.Module):
             kernels.autocast_bf16(x) and all(l.weight.dtype == torch.float32 for l in (fc1, fc2)))
         return w_ok and all(l.bias is not None for l in (fc1, fc2))
 
+    def _trainable(self, x: torch.Tensor) -> bool:
+        """A call that needs gradients through a plain LayerNorm over C <= 1024
+        (rows of whole 16-byte chunks), the exact GELU and biased linears:
+        the LayerNorm and its backward run on the HIP kernels
+        (autograd.mlp), the GEMMs on hipBLASLt."""
+        if not (torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))):
+            return False
+        C = x.shape[-1]
+        if not config.use_layernorm or type(self.norm2) is not torch.nn.LayerNorm:
+            return False
+        if tuple(self.norm2.normalized_shape) != (C,) or C > 1024 or (C * x.element_size()) % 16 != 0:
+            return False
+        if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            return False
+        if type(self.act) is not torch.nn.GELU or self.act.approximate != "none":
+            return False
+        return all(l.bias is not None for l in (self.fc1, self.fc2)) and self.fc2.out_features == C
+
     def _fused_args(self) -> dict:
         tensors = [self.fc1.weight, self.fc1.bias, self.fc2.weight, self.fc2.bias]
         if config.use_layernorm:
@@ -100,6 +120,10 @@ class SequentialMlp(torch.nn.Module):
             raise RuntimeError("terra_amd: SequentialMlp runs on device tensors only (got a CPU tensor)")
         if self._fusable(x):
             return kernels.swin_mlp(x.contiguous(), out=out, **self._fused_args())
+        if self._trainable(x):
+            n = self.norm2
+            return autograd.mlp(x, n.weight, n.bias, self.fc1.weight, self.fc1.bias, self.fc2.weight,
+                                self.fc2.bias, n.eps)
         shortcut = x
         if config.use_layernorm:
             x = self.norm2(x)

@@ -189,13 +189,23 @@ class SequentialSwinTransformer(torch.nn.Module):
                                    shift_mask=mask is not None and mask.shift is not None,
                                    land_bits=None if mask is None else mask.land_bits, **self._fused_args())
             return y.view(B, H * W, C)
-        # Training: norm1 is torch's LayerNorm (its own backward), then the
-        # partition / reverse permutations with their adjoint as gradient.
+        # Training: the partition / reverse permutations and the LayerNorm
+        # with their HIP backward kernels.
         training = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
         if config.use_layernorm and not training and self._fusable_norm(grid.dtype):
-            x_windows = kernels.swin_partition_ln(grid, geom, self.norm1.weight, self.norm1.bias, self.norm1.eps)
+            n = self.norm1
+            ln_w, ln_b = n.weight, n.bias
+            if (ln_w is not None and ln_w.dtype != torch.float32) or (ln_b is not None and ln_b.dtype != torch.float32):
+                ln_w, ln_b = self.attn._cached("norm1", [n.weight, n.bias], lambda: tuple(
+                    None if t is None else t.detach().to(torch.float32).contiguous() for t in (n.weight, n.bias)))
+            x_windows = kernels.swin_partition_ln(grid, geom, ln_w, ln_b, n.eps)
+        elif config.use_layernorm and self._fusable_norm(grid.dtype):
+            # Training: the fused LayerNorm + partition, whose backward kernel
+            # also gives the LayerNorm weight and bias gradients.
+            n = self.norm1
+            x_windows = autograd.partition_ln(grid, geom, n.weight, n.bias, n.eps)
         else:
-            if config.use_layernorm:  # a norm layer the gather does not fuse here runs on its own
+            if config.use_layernorm:  # a norm layer the gather does not fuse runs on its own
                 grid = self.norm1(grid.view(B, L, C)).contiguous().view(B, H, W, C)
             x_windows = autograd.partition(grid, geom)
         attn_windows = self.attn(x_windows, mask=self.window_mask(geom))

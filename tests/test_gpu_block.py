@@ -173,3 +173,78 @@ def test_c4_chain_alternating_blocks_with_mlp(dev):
         else:
             r = so.swin_block_attention(r, cfg.height, cfg.width, cfg.window, b.shift_size, cfg.heads, p)
     assert_block_matches(y, r.view(cfg.batch, cfg.height * cfg.width, cfg.channels), x, 2e-2, 3e-2)
+
+
+def test_c4_stack_24_blocks_full_size(dev):
+    """The c4 model's Swin stack at full size: 24 blocks at 128x256 tokens
+    (C=768, 12 heads of dim 64, window 8), W-MSA and SW-MSA alternating by
+    layer index (models/transformer.py:88), each followed by its MLP half, in
+    BasicLayer's order (models/reference_model/parallel_layers.py:151-153).
+    - every half: the fused kernel against the five-stage path (torch's ops
+      for the MLP) on the same input, and every output finite;
+    - the first two block pairs against the oracle chain;
+    - end to end: the fused chain against the five-stage chain run
+      separately, normwise on y - x (error growth through depth).
+    Weights: the reference init with q/k x4 (O(1) logits), proj x4, bias
+    table x25, fc1 and fc2 x2, so each half changes its input visibly while
+    the residual stream stays bounded over 48 halves."""
+    cfg = workloads.CONFIGS["c4"]
+    dtype = torch.bfloat16
+    halves = []
+    for layer in range(24):
+        blk = workloads.block_for(cfg, layer)
+        with torch.no_grad():
+            for lin in (blk.attn.q_linear, blk.attn.k_linear):
+                lin.weight.mul_(4.0)
+            blk.attn.proj.weight.mul_(4.0)
+            blk.attn.relative_position_bias_table.mul_(25.0)
+        m = workloads.mlp_for(cfg, layer)
+        with torch.no_grad():
+            m.fc1.weight.mul_(2.0)
+            m.fc2.weight.mul_(2.0)
+        halves += [blk, m]
+    assert [b.shift_size for b in halves[::2]] == [0, 4] * 12
+    x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 450, dtype)
+    gpu = [h.to(dev).to(dtype) for h in halves]
+
+    def run(h, inp, fused):
+        if hasattr(h, "fc1"):
+            h.use_fused_mlp = fused
+        else:
+            h.use_fused_block = fused
+        try:
+            with torch.no_grad():
+                return h(inp)
+        finally:
+            h.use_fused_mlp = h.use_fused_block = True
+
+    y = x.to(dev)
+    y_five = x.to(dev)
+    outs = []
+    for i, h in enumerate(gpu):
+        y_f = run(h, y, True)
+        y_u = run(h, y, False)
+        assert torch.isfinite(y_f.float()).all() and torch.isfinite(y_u.float()).all(), i
+        d_u = (y_u.float() - y.float())
+        tol = 2.0 ** -7 * y_u.float().abs() + 2e-2 * d_u.abs().max()
+        assert bool(((y_f.float() - y_u.float()).abs() <= tol).all()), (i, float((y_f.float() - y_u.float()).abs().max()))
+        y = y_f
+        y_five = run(h, y_five, False)
+        if i == 3:
+            outs.append(y.cpu())
+    # the first two block pairs (four halves) against the oracle chain
+    r = x.float()
+    for h in halves[:4]:
+        p = params_of(h)
+        if hasattr(h, "fc1"):
+            r = so.mlp(r, p)
+        else:
+            r = so.swin_block_attention(r, cfg.height, cfg.width, cfg.window, h.shift_size, cfg.heads, p)
+    assert_block_matches(outs[0], r.view_as(x), x, 2e-2, 3e-2)
+    # end to end through 48 halves: the two chains stay together
+    d_f = y.double().cpu() - x.double()
+    d_u = y_five.double().cpu() - x.double()
+    assert torch.isfinite(d_f).all()
+    growth = (torch.linalg.vector_norm(d_f - d_u) / torch.linalg.vector_norm(d_u)).item()
+    print(f"24-block stack: |y - x| max {d_u.abs().max().item():.3f}, fused vs five-stage normwise {growth:.3e}")
+    assert growth <= 5e-2, growth
