@@ -107,6 +107,7 @@ class WindowAttention(torch.nn.Module):
         if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
             w = torch.cat([l.weight for l in lins], 0)
             b = torch.cat([l.bias for l in lins], 0) if has_bias else None
+            return autograd.linear(x, w, b)
         else:  # the concatenated weights, kept until a parameter changes
             w, b = self._cached("qkv", [l.weight for l in lins] + [l.bias for l in lins], lambda: (
                 torch.cat([l.weight for l in lins], 0), torch.cat([l.bias for l in lins], 0) if has_bias else None))
@@ -132,4 +133,4 @@ class WindowAttention(torch.nn.Module):
     def forward(self, x: torch.Tensor, mask=None) -> torch.Tensor:
         o = autograd.window_attention_qkv(self.qkv(x), self.num_heads, self.window_size, self.scale,
                                           bias_table=self._table(), mask=mask)
-        return self.proj(o)
+        return autograd.linear(o, self.proj.weight, self.proj.bias)
