@@ -127,6 +127,15 @@ __device__ __forceinline__ f32x4 load_f32x4(const float* p) {
   return f32x4{v.x, v.y, v.z, v.w};
 }
 
+// This lane's index in its wave, computed where it is used: a volatile asm
+// is neither hoisted out of a loop nor merged with another call, so a
+// persistent loop does not hold the value (or spill it) across its body.
+__device__ __forceinline__ int lane_index() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // The 16-byte A/B-operand fragment of weight rows [16*rt, 16*rt + 16),
 // input channels [32*ks, 32*ks + 32) for this lane (row rt*16 + lane%16,
 // channels 32ks + 8*(lane/16) ..): strided rows of the nn.Linear layout, or
@@ -382,10 +391,15 @@ __device__ __forceinline__ void head_qkv(const BlockParams& p, const uint8_t* xn
       for (int dt = 0; dt < 2; ++dt) {
         f32x4 b = f32x4{0.f, 0.f, 0.f, 0.f};
         if (bqkv != nullptr) {
+          // Buffer loads (a 32-bit lane offset against a scalar descriptor):
+          // 64-bit per-lane bias addresses held across the passes spilled.
+          const __amdgpu_buffer_rsrc_t br = buffer_rsrc(bqkv, 3 * C * 4);
           if (pass != 1) {
-            b = load_f32x4(bqkv + bias0(pass) + 16 * dt + 4 * g);
+            b = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              br, (uint32_t)(16 * dt + 4 * g) * 4, bias0(pass) * 4, 0));
           } else {
-            const float bv = bqkv[bias0(pass) + 16 * dt + c16];
+            const float bv = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(br, (uint32_t)(16 * dt + c16) * 4, bias0(pass) * 4, 0));
             b = f32x4{bv, bv, bv, bv};
           }
         }
@@ -518,7 +532,9 @@ __device__ __forceinline__ void head_proj(const BlockParams& p, const uint8_t* o
   f32x4 ya[2][4];
 #pragma unroll
   for (int ft = 0; ft < 2; ++ft) {
-    const f32x4 bp = bproj != nullptr ? load_f32x4(bproj + f0 + 16 * ft + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 bp = bproj != nullptr ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            buffer_rsrc(bproj, C * 4), (uint32_t)(16 * ft + 4 * g) * 4, f0 * 4, 0))
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) ya[ft][tt] = bp;
   }
@@ -629,10 +645,10 @@ void swin_block_kernel(const BlockParams p) {
     const int next = unit + (int)gridDim.x;
     UnitLoc nxt = cur;
     if (next < p.units) nxt = locate(p, next);
+    nxt.computed = __builtin_amdgcn_readfirstlane(nxt.computed);  // a scalar, not a lane register
     // Lane-derived addresses are recomputed per window rather than held in
-    // registers across the persistent loop.
-    int lane_i = lane;
-    asm volatile("" : "+v"(lane_i));
+    // registers across the persistent loop (the lane index itself included).
+    const int lane_i = lane_index();
     const int tid_i = wave * 64 + lane_i;
     if (have_prev) store_window<cpr, nthreads>(p, prev, xr_next, tid_i);  // the previous window's rows
 
@@ -643,7 +659,7 @@ void swin_block_kernel(const BlockParams p) {
       head_qkv<C, kPacked>(p, xn, wave, lane_i, kf4, vf, qf, p.b_qkv);
       // Next window's rows stream in behind the q/k/v loads (the attention
       // phase issues no vector-memory loads of its own).
-      if (next < p.units) fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane_i);
+      if (next < p.units) fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane_index());
       lds_barrier();     // every wave has read xn; O overwrites it
       head_attention<C>(p, cur, tabs + wave * kTableMax, wave, lane_i, kf4, vf, qf, xn);
       lds_barrier();     // O complete
@@ -660,9 +676,7 @@ void swin_block_kernel(const BlockParams p) {
     par ^= 1;
   }
   lds_barrier();         // output rows complete in the last window's buffer
-  int lane_f = lane;
-  asm volatile("" : "+v"(lane_f));
-  store_window<cpr, nthreads>(p, prev, xbuf + par * tile, wave * 64 + lane_f);
+  store_window<cpr, nthreads>(p, prev, xbuf + par * tile, wave * 64 + lane_index());
 }
 
 // ============================================================================
