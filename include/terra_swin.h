@@ -327,6 +327,56 @@ int terra_swin_mlp_fwd(const void* x, void* y, int dtype,
                        const void* fc2_weight, const float* fc2_bias,
                        void* stream);
 
+/* Epilogues of terra_swin_linear. */
+enum terra_linear_epilogue {
+  TERRA_LINEAR_STORE = 0, /* y = bf16(x W^T + b)                            */
+  TERRA_LINEAR_GELU = 1   /* y = GELU(bf16(x W^T + b)), nn.GELU (erf form)   */
+};
+
+/* Token-row linear layer (bf16, fp32 accumulation) with a fused epilogue:
+ *   y[m] = epilogue(x[m] W^T + b)        for rows m < rows
+ * x [rows, in_features] with row stride x_stride elements (a multiple of 8),
+ * y [rows, out_features] with row stride y_stride (a multiple of 4); W the
+ * bf16 nn.Linear weight [out_features, in_features] in the layout of
+ * terra_swin_pack_linear; bias fp32 [out_features] or NULL.  in_features a
+ * multiple of 64, out_features a multiple of 256 up to 4096; x_stride * 512
+ * bytes under 4 GiB.  y must not overlap x.
+ * Rounding: the sum plus bias is rounded once to bf16; TERRA_LINEAR_GELU then
+ * applies nn.GELU to that bf16 value in fp32 and rounds to bf16.
+ * Replaces  self.fc1(x); self.act(x)        models/mlp.py:162-165
+ *           (nn.Linear, nn.GELU())          models/mlp.py:138-150
+ * and, with TERRA_LINEAR_STORE, any nn.Linear over token rows
+ *           (q/k/v models/attention.py:223-228, 244-246).
+ */
+int terra_swin_linear(const void* x, void* y, int dtype, int64_t rows,
+                      int in_features, int out_features,
+                      int64_t x_stride, int64_t y_stride,
+                      const void* weight_packed, const float* bias,
+                      int epilogue, void* stream);
+
+/* Linear layer plus residual add (bf16), optionally scattering the rows from
+ * window order back to the token grid:
+ *   y[t(m)] = bf16(residual[t(m)] + bf16(x[m] W^T + b))
+ * x [rows, in_features] contiguous; W, bias as for terra_swin_linear.
+ * geom NULL: t(m) = m; residual and y are [rows, out_features].
+ *   Replaces  x = self.fc2(x); x = shortcut + x      models/mlp.py:168-171
+ * geom non-NULL (8x8 windows, every frame window emitted: no window-row or
+ * valid-window range): x holds the window tokens [B * nW, 64, C] in the order
+ * of terra_swin_partition, rows = B * nW * 64, out_features = C; residual and
+ * y are [B, H, W, C] and t(m) is the grid token the partition read row m
+ * from (frame-padding rows are dropped).
+ *   Replaces  x = self.proj(x)                       models/attention.py:281
+ *             window_reverse(attn_windows, ws, H, W) models/utils.py:41-45
+ *             torch.roll(x, (s, s), (1, 2))          models/transformer.py:246
+ *             x = shortcut + x                       models/transformer.py:296-298
+ * y may equal residual but must not overlap it otherwise, nor overlap x.
+ */
+int terra_swin_linear_residual(const void* x, const void* residual, void* y,
+                               int dtype, int64_t rows,
+                               int in_features, int out_features,
+                               const void* weight_packed, const float* bias,
+                               const terra_swin_geom* geom, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

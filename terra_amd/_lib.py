@@ -54,6 +54,8 @@ EXPORTED_SYMBOLS = (
     "terra_swin_block_fwd",
     "terra_swin_pack_linear",
     "terra_swin_mlp_fwd",
+    "terra_swin_linear",
+    "terra_swin_linear_residual",
 )
 
 
@@ -203,6 +205,13 @@ def load() -> ctypes.CDLL:
         lib.terra_swin_mlp_fwd.restype = ctypes.c_int
         lib.terra_swin_mlp_fwd.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(SwinMlpDesc), vp, vp, vp, vp, vp, vp,
                                            vp]
+        i64 = ctypes.c_int64
+        lib.terra_swin_linear.restype = ctypes.c_int
+        lib.terra_swin_linear.argtypes = [vp, vp, ctypes.c_int, i64, ctypes.c_int, ctypes.c_int, i64, i64, vp, vp,
+                                          ctypes.c_int, vp]
+        lib.terra_swin_linear_residual.restype = ctypes.c_int
+        lib.terra_swin_linear_residual.argtypes = [vp, vp, vp, ctypes.c_int, i64, ctypes.c_int, ctypes.c_int, vp, vp,
+                                                   ctypes.POINTER(SwinGeom), vp]
         version = lib.terra_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"terra_amd: {LIB_PATH} has ABI version {version}, expected {ABI_VERSION}; rebuild it")

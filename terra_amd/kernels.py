@@ -689,6 +689,100 @@ class _BlockLaunch(_Launch):
 MLP_CHANNELS = (128, 192, 384, 768)
 
 
+LINEAR_OUT_MULTIPLE = 256  # output features per tile of the linear kernels
+LINEAR_MAX_OUT = 4096      # output features the linear kernels stage their bias for
+
+
+def linear_supported(x: torch.Tensor, in_features: int, out_features: int) -> bool:
+    """Whether :func:`linear` / :func:`linear_residual` serve this layer: bf16
+    device rows, in_features a multiple of 64, out_features a multiple of 256
+    up to 4096."""
+    return (x.device.type == "cuda" and x.dtype == torch.bfloat16 and in_features > 0 and in_features % 64 == 0
+            and 0 < out_features <= LINEAR_MAX_OUT and out_features % LINEAR_OUT_MULTIPLE == 0)
+
+
+def _linear_checks(x: torch.Tensor, weight_packed: torch.Tensor, out_features: int, bias: Optional[torch.Tensor]):
+    dev = _require_device(x, weight_packed)
+    code = _dtype_code(x, (torch.bfloat16,))
+    if x.dim() < 1 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous [..., in_features] tensor")
+    k = x.shape[-1]
+    if not linear_supported(x, k, out_features):
+        raise ValueError(f"the linear kernels serve bf16 rows with in_features % 64 == 0 and out_features % 256 == 0, <= 4096 "
+                         f"(got {x.dtype}, {k} -> {out_features})")
+    if weight_packed.dtype != x.dtype or weight_packed.numel() != out_features * k or not weight_packed.is_contiguous():
+        raise ValueError(f"weight_packed must be a contiguous packed {x.dtype} tensor of {out_features * k} elements "
+                         "(pack_linear of the [out, in] weight)")
+    if bias is not None:
+        _require_device(x, bias)
+        if bias.dtype != torch.float32 or bias.numel() != out_features or not bias.is_contiguous():
+            raise ValueError(f"bias must be a contiguous fp32 tensor of {out_features} elements")
+    return dev, code, k, x.numel() // k if k else 0
+
+
+def linear(x: torch.Tensor, weight_packed: torch.Tensor, out_features: int, bias: Optional[torch.Tensor] = None,
+           gelu: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``bf16(x W^T + b)`` over the token rows of ``x`` [..., in] (bf16), or
+    with ``gelu`` ``GELU(bf16(x W^T + b))`` (nn.GELU, erf form, rounded to
+    bf16): fc1 + act of SequentialMlp (models/mlp.py:162-165) in one kernel.
+    ``weight_packed`` is :func:`pack_linear` of the [out, in] weight, ``bias``
+    fp32 or None."""
+    dev, code, k, rows = _linear_checks(x, weight_packed, out_features, bias)
+    shape = (*x.shape[:-1], out_features)
+    if out is None:
+        out = torch.empty(shape, dtype=x.dtype, device=dev)
+    elif tuple(out.shape) != shape or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
+        raise ValueError(f"out must be a contiguous {x.dtype} tensor of shape {shape} on {dev}")
+    if rows == 0:
+        return out
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_linear(_ptr(x), _ptr(out), code, int(rows), int(k), int(out_features), int(k),
+                                           int(out_features), _ptr(weight_packed), _ptr(bias), 1 if gelu else 0,
+                                           _stream(dev))
+    _lib.check(st, "terra_swin_linear")
+    return out
+
+
+def linear_residual(x: torch.Tensor, weight_packed: torch.Tensor, out_features: int, residual: torch.Tensor,
+                    bias: Optional[torch.Tensor] = None, geom: Optional[WindowGeometry] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``residual + bf16(x W^T + b)`` rounded to bf16.
+
+    Without ``geom``: per token row (fc2 + shortcut, models/mlp.py:168-171);
+    ``residual`` / ``out`` have ``x``'s rows.  With ``geom`` (8x8 windows,
+    every frame window emitted): ``x`` holds the window tokens [B*nW, 64, in]
+    and each row goes back to the grid token it was partitioned from, i.e.
+    proj + window_reverse + roll + shortcut (models/attention.py:281,
+    models/utils.py:41-45, models/transformer.py:246, 296-298); ``residual`` /
+    ``out`` are [B, H, W, C].  ``out`` may be ``residual``."""
+    dev, code, k, rows = _linear_checks(x, weight_packed, out_features, bias)
+    _require_device(x, residual)
+    if geom is None:
+        shape = (*x.shape[:-1], out_features)
+    else:
+        if geom.channels != out_features:
+            raise ValueError(f"geom.channels ({geom.channels}) must equal out_features ({out_features})")
+        shape = (geom.batch, geom.height, geom.width, geom.channels)
+    n_out = 1
+    for d in shape:
+        n_out *= d
+    if residual.dtype != x.dtype or residual.numel() != n_out or not residual.is_contiguous():
+        raise ValueError(f"residual must be a contiguous {x.dtype} tensor of {n_out} elements")
+    if out is None:
+        out = torch.empty(shape, dtype=x.dtype, device=dev)
+    elif out.numel() != n_out or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
+        raise ValueError(f"out must be a contiguous {x.dtype} tensor of {n_out} elements on {dev}")
+    if rows == 0:
+        return out.view(shape)
+    c_geom = None if geom is None else geom.to_c()
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_linear_residual(_ptr(x), _ptr(residual), _ptr(out), code, int(rows), int(k),
+                                                    int(out_features), _ptr(weight_packed), _ptr(bias),
+                                                    None if c_geom is None else ctypes.byref(c_geom), _stream(dev))
+    _lib.check(st, "terra_swin_linear_residual")
+    return out.view(shape)
+
+
 def swin_mlp_supported(x: torch.Tensor, channels: int, hidden: int) -> bool:
     """Whether :func:`swin_mlp` serves this call (bf16 device tensor,
     C in {128, 192, 384, 768}: the widths of the benchmark configurations,

@@ -328,3 +328,45 @@ def test_mlp_wrapper_raises_on_cpu_tensors():
     from terra_amd.mlp import SequentialMlp
     with pytest.raises(RuntimeError, match="device tensors only"):
         SequentialMlp(192, 768)(x.float())
+
+
+def _lin_call(x=FAKE, y=ctypes.c_void_p(1 << 30), dtype=L.DTYPE_BF16, rows=512, k=1024, n=1024, xs=None, ys=None,
+              w=FAKE, b=None, epi=0):
+    return L.load().terra_swin_linear(x, y, dtype, rows, k, n, k if xs is None else xs, n if ys is None else ys, w,
+                                      b, epi, None)
+
+
+def test_linear_rejects_bad_arguments():
+    assert _lin_call(x=None) == -1
+    assert _lin_call(w=None) == -1
+    assert _lin_call(dtype=L.DTYPE_F32) == -5 and "bf16 only" in L.last_error()
+    assert _lin_call(dtype=9) == -2
+    assert _lin_call(n=192) == -3 and "multiple" in L.last_error()
+    assert _lin_call(k=48) == -3
+    assert _lin_call(rows=-1) == -3
+    assert _lin_call(xs=1000) == -3 and "row strides" in L.last_error()
+    assert _lin_call(ys=1022) == -3
+    assert _lin_call(x=ctypes.c_void_p((1 << 20) + 8)) == -4
+    assert _lin_call(b=ctypes.c_void_p((1 << 20) + 4)) == -4
+    assert _lin_call(epi=7) == -3 and "epilogue" in L.last_error()
+    assert _lin_call(y=ctypes.c_void_p((1 << 20) + 4096)) == -3 and "overlaps" in L.last_error()
+    assert _lin_call(rows=0) == 0  # nothing to do, nothing launched
+
+
+def _lin_res_call(x=FAKE, r=ctypes.c_void_p(1 << 31), y=ctypes.c_void_p(1 << 31), rows=512, k=1024, n=1024, geom=None):
+    return L.load().terra_swin_linear_residual(x, r, y, L.DTYPE_BF16, rows, k, n, FAKE, None,
+                                               None if geom is None else ctypes.byref(geom), None)
+
+
+def test_linear_residual_rejects_bad_arguments():
+    assert _lin_res_call(r=None) == -1
+    assert _lin_res_call(r=ctypes.c_void_p((1 << 31) + 4)) == -4
+    assert _lin_res_call(y=ctypes.c_void_p((1 << 31) + 4096)) == -3 and "overlaps residual" in L.last_error()
+    full = kernels.WindowGeometry(1, 16, 24, 1024, 8, 4, 4).to_c()
+    slab = kernels.WindowGeometry(1, 16, 24, 1024, 8, 4, 4, (0, 0, 0, 0), 0, 1).to_c()
+    assert _lin_res_call(rows=3 * 64, geom=slab) == -5 and "every window of the frame" in L.last_error()
+    w7 = kernels.WindowGeometry(1, 14, 21, 1024, 7).to_c()
+    assert _lin_res_call(rows=6 * 49, geom=w7) == -5 and "8x8 windows" in L.last_error()
+    assert _lin_res_call(rows=5 * 64, geom=full) == -3 and "window tokens" in L.last_error()
+    other_c = kernels.WindowGeometry(1, 16, 24, 768, 8).to_c()
+    assert _lin_res_call(rows=6 * 64, geom=other_c) == -3 and "out_features" in L.last_error()
