@@ -291,9 +291,9 @@ def main():
 
     # Events around the fused kernel on its launch stream (torch's current
     # stream, which the C ABI receives as its hipStream_t).
-    events = {"swin_block": [], "partition": [], "window_attention": [], "reverse": []}
-    names = ("swin_block", "swin_partition_ln", "window_attention", "swin_reverse")
-    keys = ("swin_block", "partition", "window_attention", "reverse")
+    events = {"swin_block": [], "partition": [], "window_attention": [], "reverse": [], "proj_scatter": []}
+    names = ("swin_block", "swin_partition_ln", "window_attention", "swin_reverse", "linear_residual")
+    keys = ("swin_block", "partition", "window_attention", "reverse", "proj_scatter")
     orig = {n: getattr(kernels, n) for n in names}
     recording = {"on": False}
     last_call = {}
@@ -403,7 +403,22 @@ def main():
             blk.use_fused_block = True
         else:
             ms_five = ms
+        # At C = 1024 the step projects, reverses and adds the residual in one
+        # linear-kernel launch; the reverse kernel alone is then timed on the
+        # same windows and grid, and the launch against torch's proj (hipBLASLt)
+        # followed by the reverse kernel.
+        scatter = "proj_scatter" in last_call
+        if scatter:
+            fn, a, kw = last_call["proj_scatter"]
+            o_, r_, geom_s = a[0], a[3], kw["geom"]
+            last_call["reverse"] = (orig["swin_reverse"], (o_, geom_s), dict(residual=r_, out=torch.empty_like(r_)))
+            pw, pb = blk.attn.proj.weight.detach(), blk.attn.proj.bias.detach()
+            last_call["proj_torch"] = (lambda: orig["swin_reverse"](
+                torch.nn.functional.linear(o_, pw, pb), geom_s, residual=r_), (), {})
         iso = {k: isolated_us(k) for k in ("partition", "window_attention", "reverse")}
+        if scatter:
+            iso["proj_scatter"] = isolated_us("proj_scatter")
+            iso["proj_torch"] = isolated_us("proj_torch")
         # The plain gather (pad + roll + partition, no LayerNorm) on the same
         # frame: the partition kernel of a block whose LayerNorm is not fused.
         x_grid, geom_ = last_call["partition"][1][0], last_call["partition"][1][1]
@@ -436,6 +451,11 @@ def main():
         if mlp_fused:  # bf16 with C in {128, 192, 384, 768}; other shapes run torch's sequence only
             last_call["mlp"] = (kernels.swin_mlp, (y_blk,), dict(out=torch.empty_like(y_blk), **mlp._fused_args()))
             iso["mlp"] = isolated_us("mlp")
+        with torch.no_grad():
+            mlp_gemm = (not mlp_fused) and mlp._gemm_path(y_blk)
+        if mlp_gemm:  # C = 1024: HIP LayerNorm, fc1 + GELU on the linear kernel, fc2 + x on hipBLASLt
+            last_call["mlp_gemm"] = (mlp, (y_blk,), {})
+            iso["mlp_gemm"] = isolated_us("mlp_gemm")
         mlp.use_fused_mlp = False
         last_call["mlp_torch"] = (mlp, (y_blk,), {})
         iso["mlp_torch"] = isolated_us("mlp_torch")
@@ -622,10 +642,34 @@ def main():
             "algorithmic_bytes_per_launch": mlp_bytes,
         }
         t_mlp = iso["mlp"]
+    elif mlp_gemm:
+        res["mlp_half"] = {
+            "kernel": "HIP LayerNorm over the token rows + linear_kernel (fc1 + exact GELU epilogue) + hipBLASLt fc2 + x",
+            "us": iso["mlp_gemm"],
+            "TFLOP_s": mlp_flops / (iso["mlp_gemm"] * 1e-6) / 1e12,
+            "mfma_frac": mlp_flops / (iso["mlp_gemm"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "torch_us": iso["mlp_torch"],
+            "speedup_vs_torch": iso["mlp_torch"] / iso["mlp_gemm"],
+            "algorithmic_flops_per_launch": mlp_flops,
+        }
+        t_mlp = iso["mlp_gemm"]
     else:
         res["mlp_half"] = {"kernel": None, "torch_us": iso["mlp_torch"],
                            "note": "no fused MLP kernel for this shape: torch's op sequence timed"}
         t_mlp = iso["mlp_torch"]
+    if scatter:
+        proj_flops = 2.0 * B_ * N * C * C
+        proj_bytes = B_ * N * C * elt + 2 * grid_bytes  # O read, x read, y written
+        res["proj_scatter"] = {
+            "kernel": "linear_kernel<residual> (proj + bias, window reverse + inverse roll + residual, one launch)",
+            "us": iso["proj_scatter"],
+            "TFLOP_s": proj_flops / (iso["proj_scatter"] * 1e-6) / 1e12,
+            "mfma_frac": proj_flops / (iso["proj_scatter"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "GB_s": proj_bytes / (iso["proj_scatter"] * 1e-6) / 1e9,
+            "torch_proj_then_reverse_us": iso["proj_torch"],
+            "algorithmic_flops_per_launch": proj_flops,
+            "algorithmic_bytes_per_launch": proj_bytes,
+        }
     # The whole Swin block (attention half + MLP half).
     res["full_block"] = {"us": t_attn_half + t_mlp, "tokens_per_s": tokens / ((t_attn_half + t_mlp) * 1e-6)}
     res["training_step"] = {

@@ -130,7 +130,20 @@ class WindowAttention(torch.nn.Module):
         return autograd.window_attention(q, k, v, self.num_heads, self.window_size, self.scale,
                                          bias_table=self._table(), mask=mask, n_real=n_real)
 
+    def attend(self, x: torch.Tensor, mask=None) -> torch.Tensor:
+        """Everything of forward but the output projection: q/k/v and the
+        fused core, O [B_, N, C] (models/attention.py:244-278)."""
+        return autograd.window_attention_qkv(self.qkv(x), self.num_heads, self.window_size, self.scale,
+                                             bias_table=self._table(), mask=mask)
+
     def forward(self, x: torch.Tensor, mask=None) -> torch.Tensor:
-        o = autograd.window_attention_qkv(self.qkv(x), self.num_heads, self.window_size, self.scale,
-                                          bias_table=self._table(), mask=mask)
-        return autograd.linear(o, self.proj.weight, self.proj.bias)
+        return autograd.linear(self.attend(x, mask=mask), self.proj.weight, self.proj.bias)
+
+    def proj_packed(self):
+        """proj's weight in the fragment-packed layout of the linear kernels
+        (bf16; autocast's cast of an fp32 weight) and its bias as fp32,
+        cached until either changes; for calls without gradients."""
+        w, b = self.proj.weight, self.proj.bias
+        return self._cached("proj_packed", [w, b], lambda: (
+            kernels.pack_linear(w.detach().to(torch.bfloat16).contiguous()),
+            None if b is None else b.detach().to(torch.float32).contiguous()))

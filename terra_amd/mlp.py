@@ -8,6 +8,11 @@ packs ``fc1.weight`` / ``fc2.weight`` with ``kernels.pack_linear`` and caches
 the packed weights and fp32 copies of the small parameters until a
 parameter's data pointer or in-place version changes.
 
+Inference at other widths with C % 64 == 0 and 4C <= 4096 (C = 1024, the
+width of TERRA's pretrain blocks): the LayerNorm on the HIP LayerNorm kernel
+over the token rows, fc1 + exact GELU on the linear kernel's GELU epilogue,
+fc2 + residual on hipBLASLt.
+
 A call that needs a gradient runs autograd.mlp: the LayerNorm forward and
 backward (residual gradient included) on the HIP LayerNorm kernels over the
 token rows, the GEMMs on hipBLASLt.  Other shapes and dtypes run the
@@ -20,6 +25,7 @@ from __future__ import annotations
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 
 from . import autograd, config, kernels
 from .attention import make_linear_with_seed
@@ -90,6 +96,57 @@ class SequentialMlp(torch.nn.Module):
             return False
         return all(l.bias is not None for l in (self.fc1, self.fc2)) and self.fc2.out_features == C
 
+    def _gemm_path(self, x: torch.Tensor) -> bool:
+        """Inference for widths the one-kernel MLP does not take (C = 1024,
+        TERRA's pretrain width): bf16 rows, C a multiple of 64 with 4C <= 4096,
+        hidden 4C, a plain LayerNorm, the exact GELU, biased bf16 linears (or
+        fp32 ones under bf16 autocast), no gradient.  The LayerNorm runs on
+        the HIP LayerNorm kernel over the token rows and fc1 + GELU on the
+        linear kernel with the GELU epilogue; fc2 + residual on hipBLASLt,
+        which is faster than the linear kernel for the 4C -> C product."""
+        if not self.use_fused_mlp or x.dim() < 1 or x.dtype != torch.bfloat16 or x.device.type != "cuda":
+            return False
+        C = x.shape[-1]
+        fc1, fc2 = self.fc1, self.fc2
+        if fc1.in_features != C or fc1.out_features != 4 * C or fc2.out_features != C:
+            return False
+        if not kernels.linear_supported(x, C, 4 * C) or C > 1024:
+            return False
+        if not config.use_layernorm or type(self.norm2) is not torch.nn.LayerNorm or self.norm2.weight is None \
+                or tuple(self.norm2.normalized_shape) != (C,):
+            return False
+        if type(self.act) is not torch.nn.GELU or self.act.approximate != "none":
+            return False
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        w_ok = all(l.weight.dtype == x.dtype for l in (fc1, fc2)) or (
+            kernels.autocast_bf16(x) and all(l.weight.dtype == torch.float32 for l in (fc1, fc2)))
+        return w_ok and all(l.bias is not None for l in (fc1, fc2))
+
+    def _gemm_forward(self, x: torch.Tensor) -> torch.Tensor:
+        a = self._fused_args()
+        C = x.shape[-1]
+        rows = x.contiguous().view(-1, C)
+        n = rows.shape[0]
+        xn = kernels.swin_partition_ln(rows.view(1, n, 1, C), kernels.rows_geometry(n, C), a["ln_weight"],
+                                       a["ln_bias"], a["ln_eps"]).view(n, C)
+        h = kernels.linear(xn, a["fc1_weight"], 4 * C, a["fc1_bias"], gelu=True)
+        w2, b2 = self._fc2_bf16()
+        return (F.linear(h, w2, b2) + rows).view(x.shape)
+
+    def _fc2_bf16(self):
+        """fc2's weight and bias as bf16 (autocast's cast of fp32 ones), cached."""
+        w, b = self.fc2.weight, self.fc2.bias
+        if w.dtype == torch.bfloat16 and b.dtype == torch.bfloat16:
+            return w, b
+        key = (w.data_ptr(), w._version, b.data_ptr(), b._version)
+        hit = getattr(self, "_fc2_cache", None)
+        if hit is None or hit[0] != key:
+            with torch.no_grad():
+                hit = (key, (w.detach().to(torch.bfloat16), b.detach().to(torch.bfloat16)))
+            self._fc2_cache = hit
+        return hit[1]
+
     def _fused_args(self) -> dict:
         tensors = [self.fc1.weight, self.fc1.bias, self.fc2.weight, self.fc2.bias]
         if config.use_layernorm:
@@ -120,6 +177,8 @@ class SequentialMlp(torch.nn.Module):
             raise RuntimeError("terra_amd: SequentialMlp runs on device tensors only (got a CPU tensor)")
         if self._fusable(x):
             return kernels.swin_mlp(x.contiguous(), out=out, **self._fused_args())
+        if self._gemm_path(x):
+            return self._gemm_forward(x)
         if self._trainable(x):
             n = self.norm2
             return autograd.mlp(x, n.weight, n.bias, self.fc1.weight, self.fc1.bias, self.fc2.weight,

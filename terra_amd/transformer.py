@@ -122,6 +122,26 @@ class SequentialSwinTransformer(torch.nn.Module):
                 and dtype in (torch.float32, torch.float16, torch.bfloat16)
                 and row_bytes % 16 == 0 and row_bytes <= 4096 and self.embedding_dim <= 1024)
 
+    def _proj_scatter(self, x_windows: torch.Tensor, shortcut: torch.Tensor, geom: WindowGeometry) -> bool:
+        """Whether the output projection, the window reverse and the residual
+        add can run as one linear-kernel launch: bf16 windows and shortcut,
+        8x8 windows, C a multiple of 256 (the kernel's feature tile; C = 1024
+        for TERRA's pretrain blocks), every window of the frame emitted, a
+        biased nn.Linear proj of the activation dtype (or fp32 under bf16
+        autocast)."""
+        C = geom.channels
+        if x_windows.dtype != torch.bfloat16 or shortcut.dtype != torch.bfloat16 or geom.window != 8:
+            return False
+        if not kernels.linear_supported(x_windows, C, C):
+            return False
+        if geom.win_row_begin != 0 or geom.valid is not None or geom.rows != geom.frame_h // geom.window:
+            return False
+        proj = self.attn.proj
+        if type(proj) is not torch.nn.Linear or proj.bias is None:
+            return False
+        return proj.weight.dtype == torch.bfloat16 or (
+            kernels.autocast_bf16(x_windows) and proj.weight.dtype == torch.float32)
+
     def _fusable_block(self, x: torch.Tensor, geom: WindowGeometry) -> bool:
         """The whole half-block runs as one kernel: bf16, (window, heads, C) in
         kernels.BLOCK_SHAPES, a plain LayerNorm (or none), biased q/k/v, and
@@ -208,7 +228,16 @@ class SequentialSwinTransformer(torch.nn.Module):
             if config.use_layernorm:  # a norm layer the gather does not fuse runs on its own
                 grid = self.norm1(grid.view(B, L, C)).contiguous().view(B, H, W, C)
             x_windows = autograd.partition(grid, geom)
-        attn_windows = self.attn(x_windows, mask=self.window_mask(geom))
+        if not training and self._proj_scatter(x_windows, shortcut, geom):
+            # proj + window reverse + inverse roll + residual in one kernel.
+            o = self.attn.attend(x_windows, mask=self.window_mask(geom))
+            if o.dtype == torch.bfloat16:
+                w, b = self.attn.proj_packed()
+                y = kernels.linear_residual(o.contiguous(), w, C, shortcut.contiguous().view(B, H, W, C), b, geom=geom)
+                return y.view(B, H * W, C)
+            attn_windows = autograd.linear(o, self.attn.proj.weight, self.attn.proj.bias)
+        else:
+            attn_windows = self.attn(x_windows, mask=self.window_mask(geom))
         out_dtype = torch.promote_types(attn_windows.dtype, shortcut.dtype)
         y = autograd.reverse(attn_windows.to(out_dtype).contiguous(), geom,
                              residual=shortcut.to(out_dtype).contiguous().view(B, H, W, C))

@@ -90,6 +90,23 @@ def test_block_g1_shape(dev, layer):
     assert_block_matches(y, ref, x, *TOL[torch.bfloat16])
 
 
+def test_block_g1_takes_the_proj_scatter_kernel(dev, monkeypatch):
+    """bf16 inference at C = 1024 projects, reverses and adds the residual in
+    one linear-kernel launch (and matches the oracle: the g1 tests above)."""
+    calls = []
+    real = kernels.linear_residual
+
+    def spy(*a, **k):
+        calls.append(k.get("geom"))
+        return real(*a, **k)
+
+    monkeypatch.setattr(kernels, "linear_residual", spy)
+    cfg = workloads.CONFIGS["g1"].scaled(16, 32)
+    y, ref, x = _block_case(dev, cfg, 1, torch.bfloat16, seed=308)
+    assert len(calls) == 1 and calls[0] is not None
+    assert_block_matches(y, ref, x, *TOL[torch.bfloat16])
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_block_g1_small_with_land(dev, dtype):
     """Head dim 128 in fp32 (the contract's 1e-5) and bf16, SW-MSA with a land

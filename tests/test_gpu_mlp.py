@@ -231,3 +231,31 @@ def test_module_mlp_switch_off_is_identity(dev, monkeypatch):
     assert not any(p.requires_grad for p in m.parameters())
     x = workloads.activations((1, 64, 192), 91, torch.bfloat16).to(dev)
     assert m(x) is x
+
+
+@pytest.mark.parametrize("tokens", [1, 300, 2 * 288 * 544 // 64])
+def test_module_c1024_linear_kernels_match_oracle(dev, tokens):
+    """C = 1024 (TERRA's pretrain width): the module runs the HIP LayerNorm,
+    fc1 + GELU on the linear kernel and fc2 + x on hipBLASLt; against the
+    oracle and against the module's own torch sequence in bf16."""
+    C = 1024
+    m = SequentialMlp(C, 4 * C, init_seed_base=workloads.SEED_BASE).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        m.norm2.weight.uniform_(0.5, 1.5)
+        m.norm2.bias.uniform_(-0.1, 0.1)
+        m.fc1.bias.uniform_(-0.2, 0.2)
+        m.fc2.weight.mul_(8.0)
+    x = workloads.activations((1, tokens, C), 91, torch.bfloat16).to(dev)
+    with torch.no_grad():
+        assert m._gemm_path(x)
+        y = m(x)
+        m.use_fused_mlp = False
+        ref_mod = m(x)
+        m.use_fused_mlp = True
+    d = (ref_mod.float() - x.float()).abs().max()
+    assert ((y.float() - ref_mod.float()).abs() <= 2.0 ** -6 * ref_mod.float().abs() + 2e-2 * d).all()
+    p = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    p = {k: (v if "fc" in k and "weight" in k else v.float()) for k, v in p.items()}
+    rows = torch.arange(tokens) if tokens <= 300 else torch.randperm(tokens, generator=workloads.generator(9))[:300]
+    xr = x.view(-1, C).cpu()[rows]
+    _check(y.view(-1, C).cpu()[rows], xr, so.mlp_bf16(xr, p))
