@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="c3", choices=("c1", "c2", "c3", "c4", "c5", "g1"))
+    ap.add_argument("--config", default="c3", choices=("c1", "c2", "c3", "c4", "c5", "g1", "w32"))
     ap.add_argument("--prewarm-s", type=float, default=3.0,
                     help="seconds of untimed steps before the counted warm-up (clock settling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -194,12 +194,12 @@ def cpu_baseline(cfg, blk, land, budget_s: float):
             with torch.inference_mode():
                 for _ in range(2):
                     so.swin_block_attention(x, rows, cfg.width, cfg.window, blk.shift_size, cfg.heads, params,
-                                            land=land_s)
+                                            land=land_s, use_attn_mask=cfg.attn_mask)
                 t_end = time.perf_counter() + budget
                 while len(times) < 5 and (time.perf_counter() < t_end or len(times) < 1):
                     t0 = time.perf_counter()
                     so.swin_block_attention(x, rows, cfg.width, cfg.window, blk.shift_size, cfg.heads, params,
-                                            land=land_s)
+                                            land=land_s, use_attn_mask=cfg.attn_mask)
                     times.append(time.perf_counter() - t0)
         finally:
             torch.set_num_threads(prev)
@@ -437,7 +437,9 @@ def main():
         last_call["attention_backward"] = (kernels.window_attention_backward, (q_, k_, v_, dout) + tuple(a[3:]), dict(
             bias_table=kw.get("bias_table"), mask=kw.get("mask"), dq=dqkv[..., :C_], dk=dqkv[..., C_:2 * C_],
             dv=dqkv[..., 2 * C_:], dbias=dbias))
-        iso["attention_backward"] = isolated_us("attention_backward")
+        has_bwd = kernels.attention_backward_supported(q_, cfg.heads, (cfg.window, cfg.window), None)
+        if has_bwd:  # windows of more than 64 tokens have no backward kernel
+            iso["attention_backward"] = isolated_us("attention_backward")
         # The block's MLP half (row f4's buildable part): the SequentialMlp that
         # follows the attention half, on the step's output, as one kernel; and
         # the same module through torch's ops (the reference's norm2 / fc1 /
@@ -467,7 +469,7 @@ def main():
         # their backward, partition / reverse and the attention core with its
         # backward run on the HIP kernels; the projection, fc1 and fc2 GEMMs
         # and their backward on hipBLASLt through torch.
-        train = training_step_us(cfg, dev)
+        train = training_step_us(cfg, dev) if has_bwd else None
     finally:
         for n in names:
             setattr(kernels, n, orig[n])
@@ -520,6 +522,23 @@ def main():
             "hbm_GB_s": block_bytes / (t_blk * 1e-6) / 1e9,
             "hbm_frac": block_bytes / (t_blk * 1e-6) / 1e9 / HBM_PEAK_GBS,
         }
+    elif N > 64:
+        # Windows of more than 64 tokens (w32: 1024): the flash core does
+        # 4 N^2 C flops per window on 4 N C elements, MFMA-bound.
+        t_att = iso["window_attention"]
+        roofline = {
+            "kernel": "window_attn_flash_kernel<%d> (online-softmax core, five-stage path)" % (C // cfg.heads),
+            "bound": "mfma",
+            "achieved": core_flops / (t_att * 1e-6) / 1e12,
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": core_flops / (t_att * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "traffic": None,
+            "algorithmic_flops_per_launch": core_flops,
+            "algorithmic_bytes_per_launch": core_bytes,
+            "avg_launch_us": t_att,
+            "hbm_GB_s": core_bytes / (t_att * 1e-6) / 1e9,
+        }
     else:
         # The step is the five-stage path; its dominant HIP kernel is the
         # window attention core, HBM-bound (N / elt flop per byte).
@@ -557,8 +576,11 @@ def main():
         "data": "synthetic (seeded N(0,1) activations, trunc-normal(0.02) weights, seeded smoothed-noise land mask)",
         "config": {
             "workload": (f"{cfg.name}: {'SW' if cfg.shift else 'W'}-MSA attention half of a Swin block (LayerNorm, "
-                         f"roll+partition, q/k/v, window attention with relative-position bias"
-                         f"{' + shift' if cfg.shift else ''}{'/land' if cfg.land else ''} mask, proj, reverse+roll, "
+                         f"roll+partition, q/k/v, window attention"
+                         + (f" with relative-position bias{' + shift' if cfg.shift else ''}"
+                            f"{'/land' if cfg.land else ''} mask" if cfg.rel_bias or cfg.attn_mask else
+                            " without relative-position bias or mask")
+                         + ", proj, reverse+roll, "
                          f"residual) {'as one fused kernel' if fused else 'through the five-stage path'}, "
                          f"B={cfg.batch}, {cfg.height}x{cfg.width} tokens, C={C}, "
                          f"{cfg.heads} heads, window {cfg.window}, shift {cfg.shift}"
@@ -604,7 +626,7 @@ def main():
             "TFLOP_s": bwd_flops / (iso["attention_backward"] * 1e-6) / 1e12,
             "algorithmic_bytes_per_launch": bwd_bytes,
             "algorithmic_flops_per_launch": bwd_flops,
-        },
+        } if has_bwd else {"kernel": None, "note": "no backward kernel for windows of more than 64 tokens"},
     }
     # The targets the hot path is held to, with this run's figures: the
     # attention core (HBM-bound) >= 70 % of HBM, partition and reverse >= 80 %,
@@ -677,7 +699,7 @@ def main():
         "what": ("forward + backward of the attention half and the MLP half, fp32 input and parameters under bf16 "
                  "autocast (the reference's training mode), synthetic output gradient, no optimizer update; "
                  "median of 5 after 2 warm-up steps"),
-    }
+    } if train is not None else {"us": None, "note": "no backward for windows of more than 64 tokens"}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg, blk, land if land is not None else
                                            torch.zeros(cfg.height, cfg.width, dtype=torch.bool), args.cpu_seconds)

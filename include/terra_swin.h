@@ -103,12 +103,19 @@ enum terra_mask_mode {
  *     the caller's explicit_mask[w % mask_windows] (TERRA_MASK_EXPLICIT);
  *   - the land term: mask_value for every key j whose bit j is set in
  *     land_bits[w % mask_windows] (land_bits == NULL disables it).
+ *
+ * Windows of more than 64 tokens (TERRA's window-32 configuration,
+ * configs/model/correctness/credit_hierarchical_swin_correctness_seq.yaml:
+ * 21-30, 1024 tokens) run on a tiled online-softmax kernel, forward only:
+ * bf16, tokens a multiple of 128 up to 4096, D in {64, 128}, n_real ==
+ * tokens, no bias table, mask_mode TERRA_MASK_NONE and no land bits; the
+ * rest returns TERRA_ERR_UNSUPPORTED.
  */
 typedef struct terra_swin_attn_desc {
   int32_t num_windows; /* B_                                       */
-  int32_t tokens;      /* N  (<= 64)                               */
+  int32_t tokens;      /* N  (<= 64, or see below)                 */
   int32_t channels;    /* C                                        */
-  int32_t heads;       /* nH (D = C / nH in {32, 64})              */
+  int32_t heads;       /* nH (D = C / nH in {32, 64, 128})         */
   int32_t window_h, window_w; /* window_h * window_w == tokens     */
   int32_t n_real;      /* keys >= n_real get pad_key_value         */
   int32_t q_stride, k_stride, v_stride, o_stride; /* elements per token row */

@@ -519,6 +519,13 @@ __device__ __forceinline__ void dma_to_lds16_cached(const void* src, uint32_t ld
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_base) : "memory");
 }
 
+// The cached load from a wave-uniform base (SGPRs) plus a 32-bit lane offset
+// (a VGPR): lane l writes LDS bytes [lds_base + 16 l, + 16).  Loop-invariant
+// lane offsets stay in registers and only the base moves.
+__device__ __forceinline__ void dma_to_lds16_at(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }

@@ -90,13 +90,6 @@ __device__ __forceinline__ int lin_lane() {
 __device__ __forceinline__ int lin_swz(int row) { return (row ^ (row >> 3)) & 7; }
 __device__ __forceinline__ int lin_slot(int row, int c) { return row * 8 + (c ^ lin_swz(row)); }
 
-// One 16-byte global -> LDS load per lane from a wave-uniform base (SGPRs)
-// plus a 32-bit lane offset: lane l writes LDS bytes [lds + 16 l, + 16).
-// The caller waits for it with an explicit vmcnt.
-__device__ __forceinline__ void lin_dma(const uint8_t* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
-}
-
 // Grid token of window-order row m (window m / 64, token m % 64 of an 8x8
 // window), or -1 for a frame-padding token: the position the partition read
 // the row from (pad, then a cyclic shift by (shift_h, shift_w)).
@@ -192,10 +185,10 @@ void linear_kernel(const LinParams p) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int blk = wave + 8 * q;
-      lin_dma(wbase + ((int64_t)(blk >> 1) * ksteps + 2 * issue_st + (blk & 1)) * 1024, woff, base + blk * 1024);
+      dma_to_lds16_at(wbase + ((int64_t)(blk >> 1) * ksteps + 2 * issue_st + (blk & 1)) * 1024, woff, base + blk * 1024);
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) lin_dma(xbase + issue_st * 128, xoff[q], base + kLinWBytes + (wave + 8 * q) * 1024);
+    for (int q = 0; q < 4; ++q) dma_to_lds16_at(xbase + issue_st * 128, xoff[q], base + kLinWBytes + (wave + 8 * q) * 1024);
     if (++issue_st == nst) {
       issue_st = 0;
       issue_valid = set_sources(++issue_tile);

@@ -388,6 +388,313 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
 }
 
 // ============================================================================
+// flash kernel: windows of more than 64 tokens (TERRA's ws-32 configuration:
+// 1024 tokens per window), bf16, no bias and no mask
+// ============================================================================
+//
+// One workgroup per (window, head, block of 32 W queries), W = 4 waves of 32
+// queries (two 16-query tiles); the window's keys stream through LDS in tiles of 64
+// (K and V straight from memory by global->LDS loads, two buffers each).  A
+// wave holds its Q^T fragments in registers for the whole loop; per key tile
+// it forms S^T = K Q^T one tile ahead, exponentiates the scores of the
+// current tile against a lazily updated row offset (online softmax in
+// raw-score units times scale * log2(e)), adds V^T P^T with P packed from the
+// S^T accumulators (the same k-slot order and transposed V reads as the 8x8
+// kernels), and sums P per row in fp32.  The query blocks of one (window,
+// head) are workgroups b = 8 i + x, i consecutive, so they run together on
+// XCD x and share the window's K and V from that XCD's L2.  The global->LDS
+// loads cost issue time on the waves that make them, whatever their latency,
+// so they go out spread over the score MFMAs.  Eight-wave workgroups (256
+// queries, half the loads per MFMA) measured slower: one workgroup per CU
+// then keeps both waves of a SIMD in the same phase between barriers, where
+// two four-wave workgroups drift apart and fill each other's gaps.
+constexpr int kFlashQ = 128;  // queries per workgroup (W = 4)
+constexpr int kFlashK = 64;   // keys per LDS tile
+
+// 16-byte slot of (key row, chunk) in a flash K or V tile of cpr chunks per
+// row.  256-byte rows (head dim 128) are a whole bank period, so the chunk is
+// XORed with row & 15: the 16 rows of a fragment read hit 16 distinct 16-byte
+// bank groups (and 8 consecutive rows 8 distinct ones).  128-byte rows take
+// the 8x8 kernels' (row >> 1) & 7.
+template <int cpr>
+__device__ __forceinline__ int flash_slot(int row, int chunk) {
+  return row * cpr + (chunk ^ (cpr >= 16 ? (row & 15) : ((row >> 1) & 7)));
+}
+
+template <int D>
+constexpr int flash_lds_bytes() {
+  return 2 * 2 * kFlashK * D * 2;  // two K and two V tiles
+}
+
+template <int D, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void window_attn_flash_kernel(const AttnParams p) {
+  constexpr int KF = D / 32;                 // k-steps of S^T = K Q^T
+  constexpr int CT = D / 16;                 // column tiles of O^T
+  constexpr int cpr = D / 8;                 // 16-byte chunks per key row of one head
+  constexpr int kTile = kFlashK * D * 2;     // one K (or V) tile
+  constexpr int kBlocks = kTile / 1024;      // its 1 KB blocks
+  constexpr int kHalf = kBlocks / W;         // loads per thread per K (or V) tile
+  static_assert(cpr % 8 == 0 && kHalf * W == kBlocks, "whole 1 KB blocks per wave");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  // Block b -> (unit, query block): within each run of 8 * qblocks blocks,
+  // unit (b / (8 qblocks)) * 8 + b % 8 takes query blocks (b / 8) % qblocks,
+  // all on XCD b % 8; units past the last whole group of 8 map linearly.
+  const int qblocks = p.N / (32 * W);
+  const int b = (int)blockIdx.x;
+  const int full = (p.items / 8) * 8 * qblocks;
+  int unit, qb;
+  if (b < full) {
+    unit = (b / (8 * qblocks)) * 8 + (b & 7);
+    qb = (b >> 3) % qblocks;
+  } else {
+    unit = (p.items / 8) * 8 + (b - full) / qblocks;
+    qb = (b - full) % qblocks;
+  }
+  const int w = unit / p.heads, h = unit - w * p.heads;
+  const int q0 = qb * 32 * W + wave * 32;     // this wave's first query
+  const uint16_t* qbase = reinterpret_cast<const uint16_t*>(p.q) + (int64_t)w * p.N * p.q_stride + h * D;
+  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(p.k) + (int64_t)w * p.N * p.k_stride + h * D;
+  const uint16_t* vbase = reinterpret_cast<const uint16_t*>(p.v) + (int64_t)w * p.N * p.v_stride + h * D;
+
+  // Q^T operand fragments: qf[t][c] = Q[q0 + 16 t + c16][32 c + 8 g .. + 8].
+  uint4 qf[2][KF];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int c = 0; c < KF; ++c)
+      qf[t][c] = *reinterpret_cast<const uint4*>(qbase + (int64_t)(q0 + 16 * t + c16) * p.q_stride + 32 * c + 8 * g);
+
+  // LDS holds K tiles in buffers 0 and 1 and V tiles in buffers 2 and 3
+  // (kTile bytes each).  K runs one key tile ahead of V: iteration kt
+  // computes the scores of tile kt + 1, whose MFMAs interleave with the
+  // softmax of tile kt, and O^T += V^T P^T of tile kt.  It reads K buffer
+  // (kt + 1) & 1 and V buffer 2 + (kt & 1) while the DMA fills K buffer kt & 1
+  // (tile kt + 2) and V buffer 2 + ((kt + 1) & 1) (tile kt + 1).
+  // Round r of a K (or V) tile moves 1 KB block blk = W r + wave; its lane
+  // holds slot blk * 64 + lane, which is flash_slot(row, chunk) of key row
+  // row.  The lane's byte offset from the tile's first row is the same for
+  // every key tile (at most 63 row strides, below 2^31 by the host's check).
+  uint32_t koff[kHalf], voff[kHalf];
+#pragma unroll
+  for (int r = 0; r < kHalf; ++r) {
+    const int sl = (r * W + wave) * 64 + lane;
+    const int row = sl / cpr;
+    const int ch = flash_slot<cpr>(row, sl - row * cpr) - row * cpr;  // the XOR is its own inverse
+    koff[r] = (uint32_t)(row * p.k_stride * 2 + ch * 16);
+    voff[r] = (uint32_t)(row * p.v_stride * 2 + ch * 16);
+  }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  // Round r of K tile kt into K buffer b (V tile kt into V buffer 2 + b).
+  auto issue_k = [&](int kt, int b, int r) {
+    dma_to_lds16_at(kbase + (int64_t)kt * kFlashK * p.k_stride, koff[r], lds0 + b * kTile + (r * W + wave) * 1024);
+  };
+  auto issue_v = [&](int kt, int b, int r) {
+    dma_to_lds16_at(vbase + (int64_t)kt * kFlashK * p.v_stride, voff[r], lds0 + (2 + b) * kTile + (r * W + wave) * 1024);
+  };
+  // S^T = K Q^T of key tile kt: lane (c16, g) of s[t][jt] holds keys
+  // 16 jt + 4 g + r of query 16 t + c16.
+  auto scores = [&](int kt, f32x4 (&s)[2][4], auto&& after_kstep) {
+    const uint8_t* ks = smem + (kt & 1) * kTile;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) s[t][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KF; ++c) {
+      uint4 kf[4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+        kf[jt] = *reinterpret_cast<const uint4*>(ks + flash_slot<cpr>(16 * jt + c16, 4 * c + g) * 16);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+          s[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[jt]),
+                                                             __builtin_bit_cast(bf16x8, qf[t][c]), s[t][jt], 0, 0, 0);
+      after_kstep(c);
+    }
+  };
+
+  f32x4 o[2][CT];
+  // Each lane's share of its query row's sum of P (its 16 keys of every
+  // tile, fp32, before the bf16 rounding of the O update); the four lanes of
+  // a row add their shares at the end.
+  float rs[2] = {0.f, 0.f};
+  // mu: each row's exponent offset, in log2 units (score * scale * log2 e).
+  // It follows the row max lazily: P = 2^(score * scale * log2 e - mu) may
+  // reach 2^kSlack before mu moves up (and O and the row sum are rescaled),
+  // which keeps the same relative bf16 precision and skips the rescale of
+  // most key tiles.
+  constexpr float kSlack = 8.f;
+  float mu[2] = {-__builtin_inff(), -__builtin_inff()};
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[t][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float c_l2e = p.scale_l2e;
+  const int nk = p.N / kFlashK;  // >= 2: the host asks for a multiple of kFlashQ tokens
+
+  // Iteration kt: softmax and O update of key tile kt (scores sc), with the
+  // scores of tile kt + 1 computed into sn on the way when kNext.
+  auto step = [&](int kt, f32x4 (&sc)[2][4], f32x4 (&sn)[2][4], auto next) {
+    constexpr bool kNext = decltype(next)::value;
+    float mt[2];
+    bool grow = false;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float mx = sc[t][0][0];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = max_nan(mx, sc[t][jt][r]);
+      mt[t] = xor_max(mx) * c_l2e;
+      grow |= mt[t] > mu[t] + kSlack;  // always on the first tile (mu = -inf)
+    }
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float mn = max_nan(mu[t], mt[t]);
+        const float corr = __builtin_amdgcn_exp2f(mu[t] - mn);  // 0 on the first tile, 1 where mu stays
+        mu[t] = mn;
+        rs[t] *= corr;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) o[t][ct] *= corr;
+      }
+    }
+    // P = 2^(score * scale * log2 e - mu), a share of it after each k-step of
+    // the next tile's score MFMAs (in program order, so that the exponentials
+    // issue between the MFMAs).
+    auto exps = [&](int c, int of) {
+#pragma unroll
+      for (int e = 0; e < 32; ++e) {
+        if (e * of / 32 != c) continue;
+        const int t = e >> 4, jt = (e >> 2) & 3, r = e & 3;
+        sc[t][jt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][jt][r], c_l2e, -mu[t]));
+        rs[t] += sc[t][jt][r];
+      }
+    };
+    // The loads of K tile kt + 2 and V tile kt + 1 (rounds j < kHalf of K,
+    // then of V) go out spread over the k-steps of the score MFMAs, not in
+    // one burst.  Past the last K tile the rounds reload tile nk - 1 into
+    // the free buffer (nothing reads it), which keeps this block branch-free.
+    constexpr int kPer = 2 * kHalf / KF;  // load rounds per k-step
+    static_assert(kPer * KF == 2 * kHalf, "whole load rounds per k-step");
+    if constexpr (kNext)
+      scores(kt + 1, sn, [&](int c) {
+        exps(c, KF);
+#pragma unroll
+        for (int j = c * kPer; j < (c + 1) * kPer; ++j) {
+          if (j < kHalf) issue_k(min(kt + 2, nk - 1), kt & 1, j);
+          else issue_v(kt + 1, (kt + 1) & 1, j - kHalf);
+        }
+      });
+    else exps(0, 1);
+    // The V reads below stay after the score MFMAs (their registers would
+    // otherwise be live across them).
+    __builtin_amdgcn_sched_barrier(0);
+    // O^T += V^T P^T; V^T fragments by transposed reads (keys 32 js + 16 (e/4) + 4 g + e % 4).
+    const uint8_t* vs = smem + (2 + (kt & 1)) * kTile;
+    auto vfrag = [&](int ct, int js) -> bf16x8 {
+      const int cc = 16 * ct + 4 * (c16 & 3);
+      uint2 part[2];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int row = 32 * js + 16 * h2 + 4 * g + (c16 >> 2);
+        part[h2] = lds_read_tr16(vs + flash_slot<cpr>(row, cc >> 3) * 16 + (cc & 7) * 2);
+      }
+      const uint32_t wd[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
+      return __builtin_bit_cast(bf16x8, wd);
+    };
+#pragma unroll
+    for (int js = 0; js < 2; ++js) {
+      bf16x8 pf[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        uint32_t wds[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+          wds[e / 2] = pack_bf16x2(sc[t][2 * js + (e >> 2)][e & 3], sc[t][2 * js + (e >> 2)][(e & 3) + 1]);
+        pf[t] = __builtin_bit_cast(bf16x8, wds);
+      }
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const bf16x8 vf = vfrag(ct, js);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) o[t][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[t], o[t][ct], 0, 0, 0);
+      }
+    }
+    // Schedule the V fragment reads two column tiles ahead of their MFMAs,
+    // so that the LDS latency hides behind the MFMAs in flight.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads: column tiles 0 and 1
+#pragma unroll
+    for (int i = 0; i < 2 * CT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA: column tile i, both query tiles
+      if (i + 2 < 2 * CT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS reads: column tile i + 2
+    }
+  };
+
+#pragma unroll
+  for (int r = 0; r < kHalf; ++r) issue_k(0, 0, r);
+#pragma unroll
+  for (int r = 0; r < kHalf; ++r) issue_v(0, 0, r);
+#pragma unroll
+  for (int r = 0; r < kHalf; ++r) issue_k(1, 1, r);
+  // The Q loads and K tile 0 have landed when at most the V tile 0 and K tile
+  // 1 loads are outstanding (loads complete in order).
+  if constexpr (kHalf == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if constexpr (kHalf == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  static_assert(kHalf == 4 || kHalf == 2 || kHalf == 1, "head dim 128 or 64, 4 or 8 waves");
+  lds_barrier();
+  f32x4 sc[2][4], sn[2][4];
+  scores(0, sc, [](int) {});
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's parts of V tile kt and K tile kt + 1
+    lds_barrier();  // all of them are in LDS; every wave is done with iteration kt - 1
+    step(kt, sc, sn, std::true_type{});
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) sc[t][jt] = sn[t][jt];
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V tile nk - 1
+  lds_barrier();
+  step(nk - 1, sc, sn, std::false_type{});
+  // O^T lane (c16, g) of (t, ct): channels 16 ct + 4 g .. + 3 of query q0 + 16 t + c16.
+  uint16_t* obase = reinterpret_cast<uint16_t*>(p.o) + (int64_t)w * p.N * p.o_stride + h * D;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float inv = __builtin_amdgcn_rcpf(xor_sum(rs[t]));
+    uint16_t* orow = obase + (int64_t)(q0 + 16 * t + c16) * p.o_stride;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const f32x4 v = o[t][ct] * inv;
+      uint2 pk;
+      pk.x = pack_bf16x2(v[0], v[1]);
+      pk.y = pack_bf16x2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(orow + 16 * ct + 4 * g) = pk;
+    }
+  }
+}
+
+template <int D, int W>
+int launch_flash(const AttnParams& p, hipStream_t s) {
+  constexpr int lds = flash_lds_bytes<D>();
+  auto kern = window_attn_flash_kernel<D, W>;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  const int64_t blocks = (int64_t)p.items * (p.N / (32 * W));
+  if (blocks >= (1ll << 31)) return fail(TERRA_ERR_SHAPE, "too many query blocks for one launch");
+  kern<<<(int)blocks, 64 * W, lds, s>>>(p);
+  return TERRA_OK;
+}
+
+// ============================================================================
 // per-wave kernel (generic path)
 // ============================================================================
 
@@ -683,6 +990,60 @@ int dispatch_tile(const AttnParams& p, int D, hipStream_t s) {
 }  // namespace
 }  // namespace terra
 
+namespace terra {
+namespace {
+
+// Windows of more than 64 tokens: the flash kernel, which serves bf16 square
+// windows of up to 64x64 tokens, a multiple of 128 tokens per window, head
+// dim 64 or 128, without relative-position bias, masks or padded keys (TERRA's
+// ws-32 configuration sets use_relative_position_bias and use_attn_mask off).
+int flash_fwd(const void* q, const void* k, const void* v, void* o, int dtype, const terra_swin_attn_desc& d, int D,
+              const float* bias_table, const float* explicit_mask, const uint64_t* land_bits, void* stream) {
+  if (dtype != TERRA_DTYPE_BF16)
+    return fail(TERRA_ERR_UNSUPPORTED, "windows of more than %d tokens run in bf16 only", kNPad);
+  if (d.tokens % kFlashQ != 0 || d.tokens > 4096)
+    return fail(TERRA_ERR_UNSUPPORTED, "windows of more than %d tokens need a multiple of %d tokens up to 4096 (got %d)",
+                kNPad, kFlashQ, d.tokens);
+  if (D != 64 && D != 128)
+    return fail(TERRA_ERR_UNSUPPORTED, "windows of more than %d tokens need head dim 64 or 128 (got %d)", kNPad, D);
+  if (d.window_h <= 0 || d.window_w <= 0 || d.window_h * d.window_w != d.tokens)
+    return fail(TERRA_ERR_SHAPE, "window %dx%d does not have %d tokens", d.window_h, d.window_w, d.tokens);
+  if (d.n_real != d.tokens)
+    return fail(TERRA_ERR_UNSUPPORTED, "windows of more than %d tokens take no padded keys", kNPad);
+  if (bias_table != nullptr || explicit_mask != nullptr || land_bits != nullptr || d.mask_mode != TERRA_MASK_NONE)
+    return fail(TERRA_ERR_UNSUPPORTED,
+                "windows of more than %d tokens take no relative-position bias and no mask", kNPad);
+  if (d.q_stride < d.channels || d.k_stride < d.channels || d.v_stride < d.channels || d.o_stride < d.channels)
+    return fail(TERRA_ERR_SHAPE, "row strides must be >= channels");
+  if (d.q_stride % 8 || d.k_stride % 8 || d.v_stride % 8 || d.o_stride % 8)
+    return fail(TERRA_ERR_ALIGN, "row strides must be multiples of 8 elements");
+  for (const void* ptr : {q, k, v, (const void*)o})
+    if ((uintptr_t)ptr % 16 != 0) return fail(TERRA_ERR_ALIGN, "q/k/v/o must be 16-byte aligned");
+  const int64_t items = (int64_t)d.num_windows * d.heads;
+  if (items * (d.tokens / kFlashQ) >= (1ll << 31)) return fail(TERRA_ERR_SHAPE, "too many window-heads for one launch");
+  if ((int64_t)(kFlashK - 1) * std::max(d.k_stride, d.v_stride) * 2 + D * 2 >= (1ll << 31))
+    return fail(TERRA_ERR_SHAPE, "k/v row strides too large for windows of more than %d tokens", kNPad);
+  AttnParams p{};
+  p.q = q; p.k = k; p.v = v; p.o = o;
+  p.q_stride = d.q_stride; p.k_stride = d.k_stride; p.v_stride = d.v_stride; p.o_stride = d.o_stride;
+  p.items = (int32_t)items;
+  p.heads = d.heads;
+  p.N = d.tokens;
+  p.n_geo = d.tokens;
+  p.n_real = d.tokens;
+  p.window_h = d.window_h; p.window_w = d.window_w;
+  p.scale_l2e = d.scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  const int st = D == 64 ? launch_flash<64, 4>(p, s) : launch_flash<128, 4>(p, s);
+  if (st != TERRA_OK) return st;
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "terra_swin_attn_fwd launch failed: %s", hipGetErrorString(e));
+  return TERRA_OK;
+}
+
+}  // namespace
+}  // namespace terra
+
 using namespace terra;
 
 extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
@@ -698,10 +1059,10 @@ extern "C" int terra_swin_attn_fwd(const void* q, const void* k, const void* v, 
   const terra_swin_attn_desc& d = *desc;
   if (d.num_windows <= 0 || d.tokens <= 0 || d.channels <= 0 || d.heads <= 0)
     return fail(TERRA_ERR_SHAPE, "num_windows/tokens/channels/heads must be positive");
-  if (d.tokens > kNPad) return fail(TERRA_ERR_UNSUPPORTED, "tokens per window %d > %d", d.tokens, kNPad);
   if (d.channels % d.heads != 0)
     return fail(TERRA_ERR_SHAPE, "channels %d not divisible by heads %d", d.channels, d.heads);
   const int D = d.channels / d.heads;
+  if (d.tokens > kNPad) return flash_fwd(q, k, v, o, dtype, d, D, bias_table, explicit_mask, land_bits, stream);
   if (D != 32 && D != 64 && D != 128) return fail(TERRA_ERR_UNSUPPORTED, "head dim %d not in {32, 64, 128}", D);
   if (d.window_h <= 0 || d.window_w <= 0 || d.window_h > 8 || d.window_w > 8)
     return fail(TERRA_ERR_UNSUPPORTED, "window %dx%d outside 1..8", d.window_h, d.window_w);

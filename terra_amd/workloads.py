@@ -16,6 +16,11 @@ Configurations (shape and semantics of each; sizes as benchmarked):
       halo rows below the slab, supplied as zero padding (pad_bottom = 8 keeps
       the frame a whole number of windows; its 38th window row is not emitted);
       the width is the full global width, so W stays cyclic.
+  w32 bf16, the g1 grid with 32x32 windows (1024 tokens, 153 windows), shift 16
+      (odd blocks), no relative-position bias and no mask: the block of
+      configs/model/correctness/credit_hierarchical_swin_correctness_seq.yaml
+      (:21-30: window_size 32, use_attn_mask False, use_relative_position_bias
+      False), whose attention core is MFMA-bound (4 N^2 C flops per window).
   g1  bf16, B=1, 288x544 token grid, C=1024, 8 heads of dim 128, window 8,
       shift 4 (odd blocks), shift mask and relative-position bias on, no land:
       the block every credit_hierarchical_swin pretrain config TERRA ships
@@ -53,6 +58,8 @@ class SwinConfig:
     win_rows: Optional[int] = None
     valid: Optional[Tuple[int, int]] = None
     mlp_ratio: Optional[int] = None
+    attn_mask: bool = True       # the block's use_attn_mask
+    rel_bias: bool = True        # the block's use_relative_position_bias
     note: str = field(default="", compare=False)
 
     @property
@@ -82,7 +89,8 @@ class SwinConfig:
     def scaled(self, height: int, width: int, batch: Optional[int] = None) -> "SwinConfig":
         """Same semantics on a smaller grid (parity tests at oracle-friendly sizes)."""
         return SwinConfig(self.name + f"@{height}x{width}", batch or self.batch, height, width, self.channels,
-                          self.heads, self.window, self.shift, self.dtype, self.land, mlp_ratio=self.mlp_ratio)
+                          self.heads, self.window, self.shift, self.dtype, self.land, mlp_ratio=self.mlp_ratio,
+                          attn_mask=self.attn_mask, rel_bias=self.rel_bias)
 
 
 def _c5() -> SwinConfig:
@@ -100,6 +108,9 @@ CONFIGS = {
     "c5": _c5(),
     "g1": SwinConfig("g1", 1, 288, 544, 1024, 8, 8, 4, torch.bfloat16, mlp_ratio=4,
                      note="TERRA's shipped pretrain block (credit_hierarchical_swin, C=1024, 8 heads, ws 8)"),
+    "w32": SwinConfig("w32", 1, 288, 544, 1024, 8, 32, 16, torch.bfloat16, mlp_ratio=4, attn_mask=False,
+                      rel_bias=False,
+                      note="TERRA's ws-32 correctness block (C=1024, 8 heads, ws 32, no bias, no mask)"),
 }
 
 
@@ -181,6 +192,7 @@ def block_for(cfg: SwinConfig, layer_idx: int, land: Optional[torch.Tensor] = No
 
     blk = SequentialSwinTransformer(layer_idx=layer_idx, height=cfg.height, width=cfg.width,
                                     embedding_dim=cfg.channels, window_size=cfg.window, num_heads=cfg.heads,
+                                    use_attn_mask=cfg.attn_mask, use_relative_position_bias=cfg.rel_bias,
                                     land_mask=land, pad=cfg.pad, win_row_begin=cfg.win_row_begin,
                                     win_rows=cfg.win_rows, valid_windows=cfg.valid)
     init_block_params(blk, layer_idx)

@@ -99,7 +99,18 @@ def _desc(**kw):
 
 
 @pytest.mark.parametrize("kw,code,text", [
-    (dict(tokens=81, window_h=9, window_w=9, n_real=81), -5, "tokens per window"),
+    (dict(tokens=81, window_h=9, window_w=9, n_real=81), -5, "multiple of 128"),
+    # windows of more than 64 tokens (the flash kernel): what it does not serve
+    (dict(tokens=256, window_h=16, window_w=16, n_real=256, channels=96, heads=3, q_stride=96, k_stride=96,
+          v_stride=96, o_stride=96), -5, "head dim 64 or 128"),
+    (dict(tokens=256, window_h=16, window_w=8, n_real=256, channels=128, q_stride=128, k_stride=128, v_stride=128,
+          o_stride=128), -3, "does not have 256 tokens"),
+    (dict(tokens=256, window_h=16, window_w=16, n_real=200, channels=128, q_stride=128, k_stride=128,
+          v_stride=128, o_stride=128), -5, "no padded keys"),
+    (dict(tokens=256, window_h=16, window_w=16, n_real=256, channels=128, q_stride=128, k_stride=128,
+          v_stride=128, o_stride=128, mask_mode=1), -5, "no mask"),
+    (dict(tokens=256, window_h=16, window_w=16, n_real=256, channels=128, q_stride=128, k_stride=1 << 26,
+          v_stride=128, o_stride=128), -3, "too large"),
     (dict(heads=3), -3, "not divisible"),
     (dict(channels=48, heads=3, q_stride=48, k_stride=48, v_stride=48, o_stride=48), -5, "head dim"),
     (dict(window_h=9), -5, "outside 1..8"),

@@ -321,3 +321,85 @@ def test_kernels_against_committed_golden_fixture(dev):
                                    mask=WindowMask(shift=ShiftMask.from_geometry(g), land_bits=bits))
     err = np.abs(out.cpu().double().numpy() - z["o"].astype(np.float64)).max()
     assert err <= 1e-5, err
+
+
+# ---- windows of more than 64 tokens (TERRA's ws-32 configuration) ----------
+
+@pytest.mark.parametrize("ws,C,heads,B_", [(32, 1024, 8, 2), (32, 512, 8, 3), (16, 256, 2, 4), (32, 256, 2, 1)])
+def test_flash_large_windows_match_oracle(dev, ws, C, heads, B_):
+    """ws x ws windows (1024 tokens at ws 32), head dim 128 or 64, no bias and
+    no mask (credit_hierarchical_swin_correctness_seq.yaml:21-30 turns both
+    off): the flash kernel's online softmax against the oracle's full-row
+    softmax, bf16 tolerance.  Scores are spread (q, k scaled by 2) so that the
+    running max moves across key tiles and the rescaling is exercised."""
+    N = ws * ws
+    q, k, v, _ = _inputs(B_, N, C, heads, ws, torch.bfloat16, 700 + ws, qkv_scale=2.0)
+    scale = (C // heads) ** -0.5
+    out = kernels.window_attention(q.to(dev), k.to(dev), v.to(dev), heads, (ws, ws), scale)
+    ref = so.window_attention_core(q.float(), k.float(), v.float(), heads, scale, window_size=(ws, ws))
+    _check(out, ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("wh,ww,C,heads,B_", [(24, 16, 256, 2, 2), (16, 8, 512, 4, 3)])
+def test_flash_non_square_windows_match_oracle(dev, wh, ww, C, heads, B_):
+    """Non-square windows, a token count that is an odd multiple of 128
+    (24 x 16), and 16 x 8, the smallest window the flash kernel serves (one
+    query block, two key tiles)."""
+    N = wh * ww
+    q, k, v, _ = _inputs(B_, N, C, heads, max(wh, ww), torch.bfloat16, 730 + N, qkv_scale=2.0)
+    scale = (C // heads) ** -0.5
+    out = kernels.window_attention(q.to(dev), k.to(dev), v.to(dev), heads, (wh, ww), scale)
+    ref = so.window_attention_core(q.float(), k.float(), v.float(), heads, scale, window_size=(wh, ww))
+    _check(out, ref, torch.bfloat16)
+
+
+def test_flash_strided_qkv_and_row_independence(dev):
+    """q | k | v as column blocks of one [B_, N, 3C] tensor (the module's
+    layout), and a window's result independent of the others."""
+    ws, C, heads, B_ = 32, 256, 2, 3
+    N = ws * ws
+    qkv = workloads.activations((B_, N, 3 * C), 711, torch.bfloat16)
+    scale = (C // heads) ** -0.5
+    qd = qkv.to(dev)
+    out = kernels.window_attention(qd[..., :C], qd[..., C:2 * C], qd[..., 2 * C:], heads, (ws, ws), scale)
+    ref = so.window_attention_core(qkv[..., :C].float(), qkv[..., C:2 * C].float(), qkv[..., 2 * C:].float(), heads,
+                                   scale, window_size=(ws, ws))
+    _check(out, ref, torch.bfloat16)
+    one = kernels.window_attention(qd[1:2, :, :C], qd[1:2, :, C:2 * C], qd[1:2, :, 2 * C:], heads, (ws, ws), scale)
+    assert torch.equal(one.cpu(), out[1:2].cpu())
+
+
+def test_flash_rejects_what_it_does_not_serve(dev):
+    ws, C, heads = 32, 256, 2
+    N = ws * ws
+    q, k, v, table = _inputs(1, N, C, heads, ws, torch.bfloat16, 720)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    with pytest.raises(ValueError, match="no relative-position bias and no mask"):
+        kernels.window_attention(qd, kd, vd, heads, (ws, ws), 0.1, bias_table=table.to(dev))
+    with pytest.raises(ValueError, match="bf16 only"):
+        kernels.window_attention(qd.float(), kd.float(), vd.float(), heads, (ws, ws), 0.1)
+    q12, k12, v12, _ = _inputs(1, 144, C, heads, 12, torch.bfloat16, 721)
+    with pytest.raises(ValueError, match="multiple of 128"):
+        kernels.window_attention(q12.to(dev), k12.to(dev), v12.to(dev), heads, (12, 12), 0.1)
+
+
+@pytest.mark.parametrize("layer", [0, 1])
+def test_block_ws32_without_bias_or_mask(dev, layer):
+    """A block of TERRA's ws-32 configuration (C and heads scaled down to 256
+    and 2, head dim 128 as in the config), W-MSA and SW-MSA (shift 16, no
+    mask), through the module: LayerNorm gather, q/k/v, the flash core, proj,
+    reverse + residual (as one linear-kernel launch: C % 256 == 0, every
+    frame window emitted), against the oracle block."""
+    from helpers import assert_block_matches, gain_block, params_of
+    from terra_amd.transformer import SequentialSwinTransformer
+    C, heads, ws, H, W = 256, 2, 32, 64, 96
+    blk = SequentialSwinTransformer(layer_idx=layer, height=H, width=W, embedding_dim=C, window_size=ws,
+                                    num_heads=heads, use_attn_mask=False, use_relative_position_bias=False)
+    workloads.init_block_params(blk, layer)
+    gain_block(blk)
+    blk = blk.to(dev).to(torch.bfloat16)
+    x = workloads.activations((1, H * W, C), 730 + layer, torch.bfloat16)
+    with torch.no_grad():
+        y = blk(x.to(dev))
+    ref = so.swin_block_attention(x, H, W, ws, blk.shift_size, heads, params_of(blk), use_attn_mask=False)
+    assert_block_matches(y, ref, x, 2e-2, 3e-2)
