@@ -22,7 +22,7 @@
 //   window_attn_ring_kernel   bf16, 8x8 windows, no padded tokens, analytic
 //       masks, head dim 32 with an even head count (two heads per workgroup)
 //       or head dim 64 (one head per workgroup): 128-byte row slices loaded
-//       straight into a ring of three LDS buffers, two units ahead (below).
+//       straight into two LDS buffers, one unit ahead (below).
 //
 //   window_attn_tile_kernel   the same bf16 8x8 shapes when the scale is
 //       below 2^-20 (zero included): the ring kernel divides the bias and
@@ -187,12 +187,16 @@ __global__ __launch_bounds__(G * 128) void window_attn_tile_kernel(const AttnPar
 // One workgroup per (window, head group of G heads), persistent, and a fixed
 // head group per workgroup (the grid is a multiple of the number of groups).
 // Four waves per head, one 16-query tile each.  q, k, v of a unit go straight
-// from memory into one of three LDS buffers by direct global->LDS loads,
-// issued two units ahead, so a workgroup never holds loads in registers and
-// always has two units in flight.  The additive terms are in raw-score units
-// (bias / scale), added as the accumulator init of S^T (attend_qtiles).
+// from memory into one of two LDS buffers by direct global->LDS loads,
+// issued one unit ahead, so a workgroup never holds loads in registers.  Two
+// buffers rather than three (two units ahead): at head dim 64 a third
+// four-wave workgroup then fits per CU, with more bytes in flight per CU
+// than the deeper ring kept (c4's core 38.8-39.1 -> 37.4-37.9 us); c3's core
+// measured 127-128 -> 124-127 us, g1's the same.  The additive terms are in
+// raw-score units (bias / scale), added as the accumulator init of S^T
+// (attend_qtiles).
 
-constexpr int kRingBufs = 3;
+constexpr int kRingBufs = 2;
 
 template <int D, int G>
 constexpr int ring_lds_bytes() {
@@ -212,8 +216,6 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
   constexpr int kBlocksPerTile = tile_bytes / 1024;
   constexpr int kOPer = kNPad * cpr / nthreads;   // O chunks per thread
   static_assert(cpr % 8 == 0 && kRounds * nthreads * 16 == unit_bytes, "whole 1 KB blocks per wave");
-  static_assert(kRounds == 3 || kRounds == 6 || kRounds == 12,
-                "the vmcnt wait below counts 3, 6 or 12 loads per thread per unit");
   static_assert(kOPer * nthreads == kNPad * cpr, "whole O chunks per thread");
   float* tables = reinterpret_cast<float*>(smem + kRingBufs * unit_bytes);
 
@@ -272,28 +274,20 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
 
   int w = w0;                                     // < windows: the grid is never larger than the work
   issue(w, 0);
-  if (w + wstride < windows) issue(w + wstride, 1);
   const float* tabr = lane_bias_rev(tab, lane);  // bias of element (it, jt, r) at tabr[30 (3 - it + jt) + r]
   const int hc = head * (D / 8);                  // first chunk of this head
   const int orow = tid / cpr, ochunk = tid - (tid / cpr) * cpr;  // this thread's first O chunk
   for (int n = 0;; ++n) {
     const int buf = n % kRingBufs;
     const bool more = w + wstride < windows;
-    // This unit's loads are complete once at most the next unit's kRounds
-    // loads are outstanding.  Loads complete in order among themselves, but
-    // not in order with stores, so the count covers later loads only: with
-    // the previous unit's O store still pending, vmcnt(3) waits for more.
-    if (more) {
-      if constexpr (kRounds == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-      else if constexpr (kRounds == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
+    // This unit's loads were the last loads issued; the previous unit's O
+    // stores came after them, and loads and stores do not complete in order
+    // with each other, so the wait is for everything.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();                                // every wave's part of the unit is in LDS
-    // Unit n + 2 goes into the buffer of unit n - 1, whose O every thread has
+    // Unit n + 1 goes into the buffer of unit n - 1, whose O every thread has
     // read out before the barrier above.
-    if (w + 2 * wstride < windows) issue(w + 2 * wstride, (n + 2) % kRingBufs);
+    if (more) issue(w + wstride, (n + 1) % kRingBufs);
     uint8_t* qs = smem + buf * unit_bytes;
     const uint8_t* ks = qs + tile_bytes;
     const uint8_t* vs = qs + 2 * tile_bytes;
