@@ -577,6 +577,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // the free buffer (nothing reads it), which keeps this block branch-free.
     constexpr int kPer = 2 * kHalf / KF;  // load rounds per k-step
     static_assert(kPer * KF == 2 * kHalf, "whole load rounds per k-step");
+    // The MFMA phases at raised wave priority: the SIMD's other wave (of the
+    // other workgroup) fills their gaps (711-713 -> 697-701 us at w32).
+    __builtin_amdgcn_s_setprio(1);
     if constexpr (kNext)
       scores(kt + 1, sn, [&](int c) {
         exps(c, KF);
@@ -629,6 +632,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA: column tile i, both query tiles
       if (i + 2 < 2 * CT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS reads: column tile i + 2
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
 #pragma unroll
