@@ -107,11 +107,13 @@ def run_kernels(cfg, blk, x, steps):
         for _ in range(steps):
             kernels.swin_partition(grid, geom)
         dqkv = torch.empty_like(qkv)
-        dbias = torch.zeros_like(blk.attn.relative_position_bias_table, dtype=torch.float32)
-        for _ in range(steps):
+        table = blk.attn.relative_position_bias_table if blk.attn.use_relative_position_bias else None
+        dbias = torch.zeros_like(table, dtype=torch.float32) if table is not None else None
+        has_bwd = kernels.attention_backward_supported(qkv[..., :C], blk.attn.num_heads, blk.attn.window_size)
+        for _ in range(steps if has_bwd else 0):
             kernels.window_attention_backward(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], o, blk.attn.num_heads,
                                               blk.attn.window_size, blk.attn.scale,
-                                              bias_table=blk.attn.relative_position_bias_table, mask=mask,
+                                              bias_table=table, mask=mask,
                                               dq=dqkv[..., :C], dk=dqkv[..., C:2 * C], dv=dqkv[..., 2 * C:],
                                               dbias=dbias)
         y = blk(x)
