@@ -440,7 +440,7 @@ def main():
             bias_table=kw.get("bias_table"), mask=kw.get("mask"), dq=dqkv[..., :C_], dk=dqkv[..., C_:2 * C_],
             dv=dqkv[..., 2 * C_:], dbias=dbias))
         has_bwd = kernels.attention_backward_supported(q_, cfg.heads, (cfg.window, cfg.window), None)
-        if has_bwd:  # windows of more than 64 tokens have no backward kernel
+        if has_bwd:
             iso["attention_backward"] = isolated_us("attention_backward")
         # The block's MLP half (row f4's buildable part): the SequentialMlp that
         # follows the attention half, on the step's output, as one kernel; and
@@ -619,16 +619,25 @@ def main():
         # call, timed alone.  Algorithmic bytes: read q, k, v, dout and write
         # dq, dk, dv (7 N C elt per window); FLOPs: S recomputed, dP, dV, dQ,
         # dK (10 N^2 C per window).
+        # Windows of more than 64 tokens: three MFMA-bound passes (row
+        # statistics, dK / dV over query tiles, dQ over key tiles), so also
+        # their fraction of the dense bf16 MFMA peak (on the 10 N^2 C
+        # algorithmic FLOPs; the passes compute 18 N^2 C with the recomputed
+        # forward).
         "attention_backward": {
-            "kernel": (f"window_attn_bwd_kernel<{cfg.channels // cfg.heads}, 1>" if cfg.channels // cfg.heads != 32
-                       else "window_attn_bwd_kernel<32, 2>"),
+            "kernel": ((f"window_attn_bwd_kernel<{cfg.channels // cfg.heads}, 1>" if cfg.channels // cfg.heads != 32
+                        else "window_attn_bwd_kernel<32, 2>") if N <= 64 else
+                       "flash backward: window_attn_flash_kernel<%d, 4, stats> + window_attn_flash_dkv_kernel<%d> + "
+                       "window_attn_flash_dq_kernel<%d>" % ((cfg.channels // cfg.heads,) * 3)),
             "us": iso["attention_backward"],
             "GB_s": bwd_bytes / (iso["attention_backward"] * 1e-6) / 1e9,
             "hbm_frac": bwd_bytes / (iso["attention_backward"] * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "TFLOP_s": bwd_flops / (iso["attention_backward"] * 1e-6) / 1e12,
             "algorithmic_bytes_per_launch": bwd_bytes,
             "algorithmic_flops_per_launch": bwd_flops,
-        } if has_bwd else {"kernel": None, "note": "no backward kernel for windows of more than 64 tokens"},
+            **({"mfma_frac": bwd_flops / (iso["attention_backward"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS}
+               if N > 64 else {}),
+        } if has_bwd else {"kernel": None, "note": "no backward kernel at this shape"},
     }
     # The targets the hot path is held to, with this run's figures: the
     # attention core (HBM-bound) >= 70 % of HBM, partition and reverse >= 80 %,

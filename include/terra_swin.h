@@ -106,10 +106,10 @@ enum terra_mask_mode {
  *
  * Windows of more than 64 tokens (TERRA's window-32 configuration,
  * configs/model/correctness/credit_hierarchical_swin_correctness_seq.yaml:
- * 21-30, 1024 tokens) run on a tiled online-softmax kernel, forward only:
- * bf16, tokens a multiple of 128 up to 4096, D in {64, 128}, n_real ==
- * tokens, no bias table, mask_mode TERRA_MASK_NONE and no land bits; the
- * rest returns TERRA_ERR_UNSUPPORTED.
+ * 21-30, 1024 tokens) run on a tiled online-softmax kernel: bf16, tokens a
+ * multiple of 128 up to 4096, D in {64, 128}, n_real == tokens, a positive
+ * finite scale, no bias table, mask_mode TERRA_MASK_NONE and no land bits;
+ * the rest returns TERRA_ERR_UNSUPPORTED.
  */
 typedef struct terra_swin_attn_desc {
   int32_t num_windows; /* B_                                       */
@@ -251,9 +251,13 @@ int terra_swin_attn_fwd(const void* q, const void* k, const void* v, void* o,
                         const uint64_t* land_bits, void* stream);
 
 /* Backward of terra_swin_attn_fwd, for the shapes the forward takes (bf16 or
- * f32, windows up to 8x8 in at most 64 token rows, padded keys, head dim 32
- * or 64; any mask mode, land bits).  bf16 8x8 windows without padded keys run
- * on an MFMA kernel, the rest on a plain fp32 one.
+ * f32, windows up to 8x8 in at most 64 token rows, padded keys, head dim 32,
+ * 64 or 128; any mask mode, land bits).  bf16 8x8 windows without padded keys
+ * run on an MFMA kernel, the rest on a plain fp32 one.  Windows of more than
+ * 64 tokens take the forward's tiled path and its limits (bf16, head dim 64
+ * or 128, no bias, mask or padded keys): three passes, the row statistics of
+ * the forward (kept in dq until the last pass, so dq must not overlap q, k, v
+ * or dout), dk / dv over query tiles, then dq over key tiles.
  * Replaces the autograd backward of the same ATen sequence
  *           models/attention.py:256-278 (matmul, bias gather + add, mask add,
  *           softmax, matmul), as run by the training step

@@ -220,7 +220,8 @@ def _check_backward(q: torch.Tensor, num_heads: int, window_size: Tuple[int, int
     if not kernels.attention_backward_supported(q, num_heads, window_size, n_real):
         raise NotImplementedError(
             "terra_amd: the attention backward kernels are built for bf16 / fp32 activations, windows up to 8x8 "
-            f"in at most 64 token rows and head dim 32, 64 or 128 (got {q.dtype}, window {tuple(window_size)}, "
+            "in at most 64 token rows and head dim 32, 64 or 128, and for bf16 windows of a multiple of 128 tokens "
+            f"up to 4096 with head dim 64 or 128 (got {q.dtype}, window {tuple(window_size)}, "
             f"{q.shape[-2]} tokens, n_real {n_real}, head dim {q.shape[-1] // num_heads})")
 
 

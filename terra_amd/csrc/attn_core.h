@@ -526,6 +526,12 @@ __device__ __forceinline__ void dma_to_lds16_at(const void* sbase, uint32_t voff
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
 }
 
+// One 4-byte global -> LDS load per lane from a wave-uniform base plus a
+// 32-bit lane offset: lane l writes LDS bytes [lds_base + 4 l, + 4).
+__device__ __forceinline__ void dma_to_lds4_at(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -768,4 +774,12 @@ __device__ __forceinline__ void attend_qtiles(f32x4 (&o)[NQ][2], float (&inv)[NQ
 }
 
 }  // namespace
+
+// The backward of windows of more than 64 tokens (window_attention.hip), for
+// terra_swin_attn_bwd: the same arguments, validated there for that path.
+__attribute__((visibility("hidden"))) int flash_attention_backward(
+    const void* q, const void* k, const void* v, const void* dout, void* dq, void* dk, void* dv, int dtype,
+    const terra_swin_attn_bwd_desc* desc, const float* bias_table, float* dbias_table, const float* explicit_mask,
+    const uint64_t* land_bits, void* stream);
+
 }  // namespace terra

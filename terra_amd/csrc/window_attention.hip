@@ -47,6 +47,9 @@
 #include "common.h"
 #include "attn_core.h"
 
+#include <cmath>
+#include <utility>
+
 namespace terra {
 namespace {
 
@@ -420,8 +423,22 @@ constexpr int flash_lds_bytes() {
   return 2 * 2 * kFlashK * D * 2;  // two K and two V tiles
 }
 
-template <int D, int W>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void window_attn_flash_kernel(const AttnParams p) {
+// Extra arguments of the flash kernel's statistics mode (the first pass of
+// the backward): per query row i and head h it writes LSE'_i = log2 of the
+// softmax denominator in the log2-domain logit units (so that P = 2^(s c -
+// LSE'), c = scale log2 e) and D_i = sum_d dout[i, d] o[i, d], as two floats
+// at the start of row i's head-h slice of `stats` (bf16 elements, row stride
+// stats_stride: the caller's dq, which the last pass overwrites).
+struct FlashStatsArgs {
+  const void* dout;
+  int64_t dout_stride;
+  void* stats;
+  int64_t stats_stride;
+};
+
+template <int D, int W, bool kStats>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void window_attn_flash_kernel(
+    const AttnParams p, const FlashStatsArgs sa) {
   constexpr int KF = D / 32;                 // k-steps of S^T = K Q^T
   constexpr int CT = D / 16;                 // column tiles of O^T
   constexpr int cpr = D / 8;                 // 16-byte chunks per key row of one head
@@ -663,6 +680,32 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   lds_barrier();
   step(nk - 1, sc, sn, std::false_type{});
   // O^T lane (c16, g) of (t, ct): channels 16 ct + 4 g .. + 3 of query q0 + 16 t + c16.
+  if constexpr (kStats) {
+    const uint16_t* dobase = reinterpret_cast<const uint16_t*>(sa.dout) + (int64_t)w * p.N * sa.dout_stride + h * D;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float l = xor_sum(rs[t]);
+      const float inv = __builtin_amdgcn_rcpf(l);
+      const int64_t row = q0 + 16 * t + c16;
+      float dsum = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const uint2 dv = *reinterpret_cast<const uint2*>(dobase + row * sa.dout_stride + 16 * ct + 4 * g);
+        dsum = __builtin_fmaf(o[t][ct][0], __uint_as_float(dv.x << 16), dsum);
+        dsum = __builtin_fmaf(o[t][ct][1], __uint_as_float(dv.x & 0xffff0000u), dsum);
+        dsum = __builtin_fmaf(o[t][ct][2], __uint_as_float(dv.y << 16), dsum);
+        dsum = __builtin_fmaf(o[t][ct][3], __uint_as_float(dv.y & 0xffff0000u), dsum);
+      }
+      const float dd = xor_sum(dsum) * inv;
+      const float lse = mu[t] + __builtin_amdgcn_logf(l);  // log2
+      if (g == 0) {
+        float2* dst = reinterpret_cast<float2*>(reinterpret_cast<uint16_t*>(sa.stats) +
+                                                ((int64_t)w * p.N + row) * sa.stats_stride + h * D);
+        *dst = make_float2(lse, dd);
+      }
+    }
+    return;
+  }
   uint16_t* obase = reinterpret_cast<uint16_t*>(p.o) + (int64_t)w * p.N * p.o_stride + h * D;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -679,16 +722,392 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   }
 }
 
-template <int D, int W>
-int launch_flash(const AttnParams& p, hipStream_t s) {
+template <int D, int W, bool kStats = false>
+int launch_flash(const AttnParams& p, hipStream_t s, const FlashStatsArgs& sa = FlashStatsArgs{}) {
   constexpr int lds = flash_lds_bytes<D>();
-  auto kern = window_attn_flash_kernel<D, W>;
+  auto kern = window_attn_flash_kernel<D, W, kStats>;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
   const int64_t blocks = (int64_t)p.items * (p.N / (32 * W));
   if (blocks >= (1ll << 31)) return fail(TERRA_ERR_SHAPE, "too many query blocks for one launch");
-  kern<<<(int)blocks, 64 * W, lds, s>>>(p);
+  kern<<<(int)blocks, 64 * W, lds, s>>>(p, sa);
+  return TERRA_OK;
+}
+
+// ============================================================================
+// flash backward: windows of more than 64 tokens
+// ============================================================================
+//
+// Per (window, head), after the statistics pass (the kernel above with
+// kStats: LSE'_i and D_i = rowsum(dout * o) per query, kept in dq):
+//   dK/dV pass, one workgroup per 64 keys (16 per wave, K and V fragments in
+//     registers), the window's queries streaming through LDS in tiles of 64
+//     (q, dout and their statistics, direct global->LDS, two buffers):
+//       S = Q K^T, dP = dO V^T (row reads of the tiles), P = 2^(S c - LSE'),
+//       dS = P (dP - D), dV^T += dO^T P, dK^T += Q^T dS (transposed reads);
+//   dQ pass, one workgroup per 128 queries (32 per wave, Q and dO fragments
+//     in registers), the keys streaming through LDS in tiles of 64 (K and V):
+//       S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - D),
+//       dQ^T += K^T dS^T, then dq = scale dQ (over the statistics).
+// dK = scale dS^T Q and dV = P^T dO are the autograd of o = softmax(scale
+// q k^T) v (models/attention.py:256-278 without bias and mask); P and dS
+// enter the MFMAs in bf16, as the module's bf16 matmuls do.
+
+struct FlashBwdPtrs {
+  const void* dout;
+  void* dq;
+  void* dk;
+  void* dv;
+  int64_t dout_stride, dq_stride, dk_stride, dv_stride;
+  float scale;
+};
+
+constexpr int kBwdKeys = 64;  // keys per dK/dV workgroup (16 per wave)
+constexpr int kBwdQ = 64;     // queries per LDS tile of the dK/dV pass
+
+template <int D>
+constexpr int flash_dkv_lds_bytes() {
+  return 2 * (2 * kBwdQ * D * 2 + kBwdQ * 8);  // two stages of q, dout and LSE' / D
+}
+
+// Block b -> (unit, block of the unit): blocks of one (window, head) are
+// b = 8 i + x with i consecutive, on XCD x, so they share the unit's rows in
+// that XCD's L2; units past the last whole group of 8 map linearly.
+__device__ __forceinline__ void flash_block_map(int b, int items, int per_unit, int& unit, int& blk) {
+  const int full = (items / 8) * 8 * per_unit;
+  if (b < full) {
+    unit = (b / (8 * per_unit)) * 8 + (b & 7);
+    blk = (b >> 3) % per_unit;
+  } else {
+    unit = (items / 8) * 8 + (b - full) / per_unit;
+    blk = (b - full) % per_unit;
+  }
+}
+
+// The A operand of a transposed product from a row-major [rows][D] tile of
+// 256- or 128-byte rows: M = columns 16 mt .. + 15, k = rows 32 js + 16 (e/4)
+// + 4 g + e % 4 (the order the accumulators of the row products pack in).
+template <int cpr>
+__device__ __forceinline__ bf16x8 flash_tr_frag(const uint8_t* tile, int mt, int js, int g, int c16) {
+  const int cc = 16 * mt + 4 * (c16 & 3);
+  uint2 part[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    const int row = 32 * js + 16 * h2 + 4 * g + (c16 >> 2);
+    part[h2] = lds_read_tr16(tile + flash_slot<cpr>(row, cc >> 3) * 16 + (cc & 7) * 2);
+  }
+  const uint32_t wd[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
+  return __builtin_bit_cast(bf16x8, wd);
+}
+
+__device__ __forceinline__ bf16x8 pack_frag8(const f32x4& a, const f32x4& b) {
+  const uint32_t wd[4] = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
+                          pack_bf16x2(b[2], b[3])};
+  return __builtin_bit_cast(bf16x8, wd);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void window_attn_flash_dkv_kernel(
+    const AttnParams p, const FlashBwdPtrs bp) {
+  constexpr int KF = D / 32, CT = D / 16, cpr = D / 8;
+  constexpr int kTile = kBwdQ * D * 2;           // one q (or dout) tile
+  constexpr int kPer = kTile / 1024 / 4;         // its 1 KB loads per wave
+  constexpr int kStage = 2 * kTile + kBwdQ * 8;  // q, dout, LSE' [64], D [64]
+  static_assert(kPer * 4 * 1024 == kTile, "whole 1 KB blocks per wave");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  int unit, kb;
+  flash_block_map((int)blockIdx.x, p.items, p.N / kBwdKeys, unit, kb);
+  const int w = unit / p.heads, h = unit - w * p.heads;
+  const int k0 = kb * kBwdKeys + 16 * wave;  // this wave's first key
+  const int64_t wrow = (int64_t)w * p.N;
+  const uint16_t* qbase = reinterpret_cast<const uint16_t*>(p.q) + wrow * p.q_stride + h * D;
+  const uint16_t* dobase = reinterpret_cast<const uint16_t*>(bp.dout) + wrow * bp.dout_stride + h * D;
+  const uint16_t* stbase = reinterpret_cast<const uint16_t*>(bp.dq) + wrow * bp.dq_stride + h * D;
+
+  // B operands of the wave's 16 keys: kfr[c] = K[k0 + c16][32 c + 8 g .. + 8], vfr the same of V.
+  uint4 kfr[KF], vfr[KF];
+#pragma unroll
+  for (int c = 0; c < KF; ++c) {
+    kfr[c] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.k) + (wrow + k0 + c16) * p.k_stride +
+                                             h * D + 32 * c + 8 * g);
+    vfr[c] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.v) + (wrow + k0 + c16) * p.v_stride +
+                                             h * D + 32 * c + 8 * g);
+  }
+  // Loads of query tile qt: round r of the q (dout) tile moves 1 KB block 4 r
+  // + wave, lane slot (4 r + wave) * 64 + lane = flash_slot(row, chunk);
+  // waves 0 and 1 move the 64 LSE' and D values (4 bytes per lane).
+  uint32_t qoff[kPer], dooff[kPer];
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int sl = (r * 4 + wave) * 64 + lane;
+    const int row = sl / cpr;
+    const int ch = flash_slot<cpr>(row, sl - row * cpr) - row * cpr;  // the XOR is its own inverse
+    qoff[r] = (uint32_t)(row * p.q_stride * 2 + ch * 16);
+    dooff[r] = (uint32_t)(row * bp.dout_stride * 2 + ch * 16);
+  }
+  const uint32_t soff = (uint32_t)(lane * bp.dq_stride * 2 + (wave & 1) * 4);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  auto issue = [&](int qt, int buf) {
+    const uint32_t st = lds0 + buf * kStage;
+    const int64_t r0 = (int64_t)qt * kBwdQ;
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      dma_to_lds16_at(qbase + r0 * p.q_stride, qoff[r], st + (r * 4 + wave) * 1024);
+      dma_to_lds16_at(dobase + r0 * bp.dout_stride, dooff[r], st + kTile + (r * 4 + wave) * 1024);
+    }
+    if (wave < 2) dma_to_lds4_at(stbase + r0 * bp.dq_stride, soff, st + 2 * kTile + wave * 256);
+  };
+
+  f32x4 dka[CT], dva[CT];
+#pragma unroll
+  for (int mt = 0; mt < CT; ++mt) {
+    dka[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dva[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float c_l2e = p.scale_l2e;
+  const int nq = p.N / kBwdQ;
+  issue(0, 0);
+  for (int qt = 0; qt < nq; ++qt) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's part of tile qt (and the K / V loads)
+    lds_barrier();  // the whole tile is in LDS; every wave is done with tile qt - 1
+    if (qt + 1 < nq) issue(qt + 1, (qt + 1) & 1);
+    const uint8_t* qs = smem + (qt & 1) * kStage;
+    const uint8_t* dos = qs + kTile;
+    const float* lse = reinterpret_cast<const float*>(qs + 2 * kTile);
+    const float* dd = lse + kBwdQ;
+    // S = Q K^T and dP = dO V^T: lane (c16, g) of tile i holds key k0 + c16
+    // against queries 16 i + 4 g + r.
+    f32x4 sa[4], dp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sa[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dp[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int c = 0; c < KF; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 qa = *reinterpret_cast<const uint4*>(qs + flash_slot<cpr>(16 * i + c16, 4 * c + g) * 16);
+        const uint4 da = *reinterpret_cast<const uint4*>(dos + flash_slot<cpr>(16 * i + c16, 4 * c + g) * 16);
+        sa[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa),
+                                                        __builtin_bit_cast(bf16x8, kfr[c]), sa[i], 0, 0, 0);
+        dp[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, da),
+                                                        __builtin_bit_cast(bf16x8, vfr[c]), dp[i], 0, 0, 0);
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse + 16 * i + 4 * g);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(dd + 16 * i + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i][r], c_l2e, -l4[r]));
+        sa[i][r] = pv;
+        dp[i][r] = pv * (dp[i][r] - d4[r]);
+      }
+    }
+    // dV^T += dO^T P and dK^T += Q^T dS, 32 queries per k-step.
+#pragma unroll
+    for (int js = 0; js < 2; ++js) {
+      const bf16x8 pf = pack_frag8(sa[2 * js], sa[2 * js + 1]);
+      const bf16x8 sf = pack_frag8(dp[2 * js], dp[2 * js + 1]);
+#pragma unroll
+      for (int mt = 0; mt < CT; ++mt) {
+        dva[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(flash_tr_frag<cpr>(dos, mt, js, g, c16), pf, dva[mt], 0, 0, 0);
+        dka[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(flash_tr_frag<cpr>(qs, mt, js, g, c16), sf, dka[mt], 0, 0, 0);
+      }
+    }
+  }
+  // dK^T / dV^T lane (c16, g) of tile mt: channels 16 mt + 4 g .. + 3 of key k0 + c16.
+  uint16_t* dkrow = reinterpret_cast<uint16_t*>(bp.dk) + (wrow + k0 + c16) * bp.dk_stride + h * D;
+  uint16_t* dvrow = reinterpret_cast<uint16_t*>(bp.dv) + (wrow + k0 + c16) * bp.dv_stride + h * D;
+#pragma unroll
+  for (int mt = 0; mt < CT; ++mt) {
+    const f32x4 kv = dka[mt] * bp.scale;
+    uint2 pk;
+    pk.x = pack_bf16x2(kv[0], kv[1]);
+    pk.y = pack_bf16x2(kv[2], kv[3]);
+    *reinterpret_cast<uint2*>(dkrow + 16 * mt + 4 * g) = pk;
+    pk.x = pack_bf16x2(dva[mt][0], dva[mt][1]);
+    pk.y = pack_bf16x2(dva[mt][2], dva[mt][3]);
+    *reinterpret_cast<uint2*>(dvrow + 16 * mt + 4 * g) = pk;
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void window_attn_flash_dq_kernel(
+    const AttnParams p, const FlashBwdPtrs bp) {
+  constexpr int KF = D / 32, CT = D / 16, cpr = D / 8;
+  constexpr int kTile = kFlashK * D * 2;  // one K (or V) tile
+  constexpr int kHalf = kTile / 1024 / 4;
+  static_assert(kHalf * 4 * 1024 == kTile, "whole 1 KB blocks per wave");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  int unit, qb;
+  flash_block_map((int)blockIdx.x, p.items, p.N / kFlashQ, unit, qb);
+  const int w = unit / p.heads, h = unit - w * p.heads;
+  const int q0 = qb * kFlashQ + wave * 32;  // this wave's first query
+  const int64_t wrow = (int64_t)w * p.N;
+  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(p.k) + wrow * p.k_stride + h * D;
+  const uint16_t* vbase = reinterpret_cast<const uint16_t*>(p.v) + wrow * p.v_stride + h * D;
+
+  // B operands of the wave's queries: qf[t][c] = Q[q0 + 16 t + c16][32 c + 8 g ..], df the same of dO;
+  // each lane's query row statistics (LSE', D) from dq, which this wave
+  // overwrites at the end.
+  uint4 qf[2][KF], df[2][KF];
+  float lse[2], dd[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t row = wrow + q0 + 16 * t + c16;
+#pragma unroll
+    for (int c = 0; c < KF; ++c) {
+      qf[t][c] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.q) + row * p.q_stride + h * D +
+                                                 32 * c + 8 * g);
+      df[t][c] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(bp.dout) + row * bp.dout_stride +
+                                                 h * D + 32 * c + 8 * g);
+    }
+    const float2 st =
+        *reinterpret_cast<const float2*>(reinterpret_cast<const uint16_t*>(bp.dq) + row * bp.dq_stride + h * D);
+    lse[t] = st.x;
+    dd[t] = st.y;
+  }
+  // Key tile kt -> K buffer 2 (kt & 1), V buffer 2 (kt & 1) + 1: round r
+  // moves block 4 r + wave of each.
+  uint32_t koff[kHalf], voff[kHalf];
+#pragma unroll
+  for (int r = 0; r < kHalf; ++r) {
+    const int sl = (r * 4 + wave) * 64 + lane;
+    const int row = sl / cpr;
+    const int ch = flash_slot<cpr>(row, sl - row * cpr) - row * cpr;
+    koff[r] = (uint32_t)(row * p.k_stride * 2 + ch * 16);
+    voff[r] = (uint32_t)(row * p.v_stride * 2 + ch * 16);
+  }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  auto issue = [&](int kt, int buf) {
+    const uint32_t st = lds0 + buf * 2 * kTile;
+#pragma unroll
+    for (int r = 0; r < kHalf; ++r) {
+      dma_to_lds16_at(kbase + (int64_t)kt * kFlashK * p.k_stride, koff[r], st + (r * 4 + wave) * 1024);
+      dma_to_lds16_at(vbase + (int64_t)kt * kFlashK * p.v_stride, voff[r], st + kTile + (r * 4 + wave) * 1024);
+    }
+  };
+
+  f32x4 o[2][CT];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[t][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float c_l2e = p.scale_l2e;
+  const int nk = p.N / kFlashK;
+  issue(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's part of tile kt (and the Q / dO loads)
+    lds_barrier();  // the whole tile is in LDS; every wave is done with tile kt - 1
+    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+    const uint8_t* ks = smem + (kt & 1) * 2 * kTile;
+    const uint8_t* vs = ks + kTile;
+    // S^T = K Q^T, dP^T = V dO^T: lane (c16, g) holds keys 16 jt + 4 g + r of query 16 t + c16.
+    f32x4 s[2][4], dp[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        s[t][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[t][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int c = 0; c < KF; ++c) {
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(ks + flash_slot<cpr>(16 * jt + c16, 4 * c + g) * 16);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          s[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf),
+                                                             __builtin_bit_cast(bf16x8, qf[t][c]), s[t][jt], 0, 0, 0);
+      }
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const uint4 vf = *reinterpret_cast<const uint4*>(vs + flash_slot<cpr>(16 * jt + c16, 4 * c + g) * 16);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          dp[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vf),
+                                                              __builtin_bit_cast(bf16x8, df[t][c]), dp[t][jt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][jt][r], c_l2e, -lse[t]));
+          dp[t][jt][r] = pv * (dp[t][jt][r] - dd[t]);
+        }
+    // dQ^T += K^T dS^T, 32 keys per k-step.
+#pragma unroll
+    for (int js = 0; js < 2; ++js) {
+      bf16x8 sf[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) sf[t] = pack_frag8(dp[t][2 * js], dp[t][2 * js + 1]);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const bf16x8 kt_frag = flash_tr_frag<cpr>(ks, ct, js, g, c16);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) o[t][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt_frag, sf[t], o[t][ct], 0, 0, 0);
+      }
+    }
+  }
+  // dQ^T lane (c16, g) of (t, ct): channels 16 ct + 4 g .. + 3 of query q0 + 16 t + c16.
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    uint16_t* row = reinterpret_cast<uint16_t*>(bp.dq) + (wrow + q0 + 16 * t + c16) * bp.dq_stride + h * D;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const f32x4 v = o[t][ct] * bp.scale;
+      uint2 pk;
+      pk.x = pack_bf16x2(v[0], v[1]);
+      pk.y = pack_bf16x2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(row + 16 * ct + 4 * g) = pk;
+    }
+  }
+}
+
+template <int D>
+int launch_flash_bwd(const AttnParams& p, const FlashBwdPtrs& bp, hipStream_t s) {
+  // pass 1: row statistics into dq
+  const FlashStatsArgs sa{bp.dout, bp.dout_stride, bp.dq, bp.dq_stride};
+  int st = launch_flash<D, 4, true>(p, s, sa);
+  if (st != TERRA_OK) return st;
+  // pass 2: dK, dV
+  {
+    constexpr int lds = flash_dkv_lds_bytes<D>();
+    auto kern = window_attn_flash_dkv_kernel<D>;
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+    const int64_t blocks = (int64_t)p.items * (p.N / kBwdKeys);
+    if (blocks >= (1ll << 31)) return fail(TERRA_ERR_SHAPE, "too many key blocks for one launch");
+    kern<<<(int)blocks, 256, lds, s>>>(p, bp);
+  }
+  // pass 3: dQ over the statistics
+  {
+    constexpr int lds = flash_lds_bytes<D>();
+    auto kern = window_attn_flash_dq_kernel<D>;
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return fail(TERRA_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+    const int64_t blocks = (int64_t)p.items * (p.N / kFlashQ);
+    kern<<<(int)blocks, 256, lds, s>>>(p, bp);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "flash backward launch failed: %s", hipGetErrorString(e));
   return TERRA_OK;
 }
 
@@ -991,12 +1410,14 @@ int dispatch_tile(const AttnParams& p, int D, hipStream_t s) {
 namespace terra {
 namespace {
 
-// Windows of more than 64 tokens: the flash kernel, which serves bf16 square
-// windows of up to 64x64 tokens, a multiple of 128 tokens per window, head
-// dim 64 or 128, without relative-position bias, masks or padded keys (TERRA's
-// ws-32 configuration sets use_relative_position_bias and use_attn_mask off).
-int flash_fwd(const void* q, const void* k, const void* v, void* o, int dtype, const terra_swin_attn_desc& d, int D,
-              const float* bias_table, const float* explicit_mask, const uint64_t* land_bits, void* stream) {
+// The checks shared by the forward and the backward of windows of more than
+// 64 tokens: bf16, a multiple of 128 tokens per window up to 4096 (any
+// window_h x window_w with that product), head dim 64 or 128, a positive
+// finite scale (the row max commutes with the scaling), no relative-position
+// bias, masks or padded keys (TERRA's ws-32 configuration sets
+// use_relative_position_bias and use_attn_mask off).
+int flash_checks(int dtype, const terra_swin_attn_desc& d, int D, const float* bias_table,
+                 const float* explicit_mask, const uint64_t* land_bits) {
   if (dtype != TERRA_DTYPE_BF16)
     return fail(TERRA_ERR_UNSUPPORTED, "windows of more than %d tokens run in bf16 only", kNPad);
   if (d.tokens % kFlashQ != 0 || d.tokens > 4096)
@@ -1011,6 +1432,18 @@ int flash_fwd(const void* q, const void* k, const void* v, void* o, int dtype, c
   if (bias_table != nullptr || explicit_mask != nullptr || land_bits != nullptr || d.mask_mode != TERRA_MASK_NONE)
     return fail(TERRA_ERR_UNSUPPORTED,
                 "windows of more than %d tokens take no relative-position bias and no mask", kNPad);
+  if (!(d.scale > 0.f) || !std::isfinite(d.scale))
+    return fail(TERRA_ERR_UNSUPPORTED, "windows of more than %d tokens need a positive finite scale", kNPad);
+  const int64_t items = (int64_t)d.num_windows * d.heads;
+  if (items * (d.tokens / kFlashQ) * 2 >= (1ll << 31)) return fail(TERRA_ERR_SHAPE, "too many window-heads for one launch");
+  return TERRA_OK;
+}
+
+// Windows of more than 64 tokens: the flash kernel.
+int flash_fwd(const void* q, const void* k, const void* v, void* o, int dtype, const terra_swin_attn_desc& d, int D,
+              const float* bias_table, const float* explicit_mask, const uint64_t* land_bits, void* stream) {
+  const int chk = flash_checks(dtype, d, D, bias_table, explicit_mask, land_bits);
+  if (chk != TERRA_OK) return chk;
   if (d.q_stride < d.channels || d.k_stride < d.channels || d.v_stride < d.channels || d.o_stride < d.channels)
     return fail(TERRA_ERR_SHAPE, "row strides must be >= channels");
   if (d.q_stride % 8 || d.k_stride % 8 || d.v_stride % 8 || d.o_stride % 8)
@@ -1018,7 +1451,6 @@ int flash_fwd(const void* q, const void* k, const void* v, void* o, int dtype, c
   for (const void* ptr : {q, k, v, (const void*)o})
     if ((uintptr_t)ptr % 16 != 0) return fail(TERRA_ERR_ALIGN, "q/k/v/o must be 16-byte aligned");
   const int64_t items = (int64_t)d.num_windows * d.heads;
-  if (items * (d.tokens / kFlashQ) >= (1ll << 31)) return fail(TERRA_ERR_SHAPE, "too many window-heads for one launch");
   if ((int64_t)(kFlashK - 1) * std::max(d.k_stride, d.v_stride) * 2 + D * 2 >= (1ll << 31))
     return fail(TERRA_ERR_SHAPE, "k/v row strides too large for windows of more than %d tokens", kNPad);
   AttnParams p{};
@@ -1040,6 +1472,61 @@ int flash_fwd(const void* q, const void* k, const void* v, void* o, int dtype, c
 }
 
 }  // namespace
+
+int flash_attention_backward(const void* q, const void* k, const void* v, const void* dout, void* dq, void* dk,
+                             void* dv, int dtype, const terra_swin_attn_bwd_desc* desc, const float* bias_table,
+                             float* dbias_table, const float* explicit_mask, const uint64_t* land_bits,
+                             void* stream) {
+  const terra_swin_attn_desc& d = desc->fwd;
+  if (d.channels % d.heads != 0)
+    return fail(TERRA_ERR_SHAPE, "channels %d not divisible by heads %d", d.channels, d.heads);
+  const int D = d.channels / d.heads;
+  const int chk = flash_checks(dtype, d, D, bias_table, explicit_mask, land_bits);
+  if (chk != TERRA_OK) return chk;
+  if (dbias_table != nullptr) return fail(TERRA_ERR_SHAPE, "dbias_table without bias_table");
+  const int64_t strides[7] = {d.q_stride, d.k_stride, d.v_stride, desc->dout_stride,
+                              desc->dq_stride, desc->dk_stride, desc->dv_stride};
+  for (int i = 0; i < 7; ++i) {
+    if (strides[i] < d.channels) return fail(TERRA_ERR_SHAPE, "row strides must be >= channels");
+    if (strides[i] % 8 != 0) return fail(TERRA_ERR_ALIGN, "row strides must be multiples of 8 elements");
+    // 32-bit lane offsets of the global->LDS loads: 63 rows of a tile
+    if (63 * strides[i] * 2 + D * 2 >= (1ll << 31))
+      return fail(TERRA_ERR_SHAPE, "row strides too large for windows of more than %d tokens", kNPad);
+  }
+  for (const void* ptr : {q, k, v, dout, (const void*)dq, (const void*)dk, (const void*)dv})
+    if ((uintptr_t)ptr % 16 != 0) return fail(TERRA_ERR_ALIGN, "q/k/v/dout/dq/dk/dv must be 16-byte aligned");
+  // dq holds the row statistics between the passes, so it must not share
+  // memory with what the passes read.
+  const int64_t rows = (int64_t)d.num_windows * d.tokens;
+  auto span = [&](const void* ptr, int64_t stride) {
+    const uintptr_t b = (uintptr_t)ptr;
+    return std::make_pair(b, b + (uintptr_t)(((rows - 1) * stride + d.channels) * 2));
+  };
+  const auto sq = span(dq, desc->dq_stride);
+  const std::pair<uintptr_t, uintptr_t> inputs[4] = {span(q, d.q_stride), span(k, d.k_stride), span(v, d.v_stride),
+                                                     span(dout, desc->dout_stride)};
+  for (const auto& in : inputs)
+    if (sq.first < in.second && in.first < sq.second)
+      return fail(TERRA_ERR_SHAPE, "dq must not overlap q, k, v or dout for windows of more than %d tokens", kNPad);
+  AttnParams p{};
+  p.q = q; p.k = k; p.v = v; p.o = nullptr;
+  p.q_stride = d.q_stride; p.k_stride = d.k_stride; p.v_stride = d.v_stride;
+  p.items = (int32_t)((int64_t)d.num_windows * d.heads);
+  p.heads = d.heads;
+  p.N = d.tokens;
+  p.n_geo = d.tokens;
+  p.n_real = d.tokens;
+  p.window_h = d.window_h; p.window_w = d.window_w;
+  p.scale_l2e = d.scale * kLog2e;
+  FlashBwdPtrs bp{};
+  bp.dout = dout; bp.dq = dq; bp.dk = dk; bp.dv = dv;
+  bp.dout_stride = desc->dout_stride; bp.dq_stride = desc->dq_stride;
+  bp.dk_stride = desc->dk_stride; bp.dv_stride = desc->dv_stride;
+  bp.scale = d.scale;
+  hipStream_t s = (hipStream_t)stream;
+  return D == 64 ? launch_flash_bwd<64>(p, bp, s) : launch_flash_bwd<128>(p, bp, s);
+}
+
 }  // namespace terra
 
 using namespace terra;

@@ -633,7 +633,9 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   const terra_swin_attn_desc& d = desc->fwd;
   if (d.num_windows <= 0 || d.tokens <= 0 || d.heads <= 0 || d.channels <= 0)
     return fail(TERRA_ERR_SHAPE, "num_windows/tokens/channels/heads must be positive");
-  if (d.tokens > kNPad) return fail(TERRA_ERR_UNSUPPORTED, "tokens per window %d > %d", d.tokens, kNPad);
+  if (d.tokens > kNPad)
+    return flash_attention_backward(q, k, v, dout, dq, dk, dv, dtype, desc, bias_table, dbias_table, explicit_mask,
+                                    land_bits, stream);
   if (d.window_h <= 0 || d.window_w <= 0 || d.window_h > 8 || d.window_w > 8)
     return fail(TERRA_ERR_UNSUPPORTED, "window %dx%d outside 1..8", d.window_h, d.window_w);
   if (d.window_h * d.window_w > d.tokens)

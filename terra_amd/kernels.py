@@ -429,12 +429,19 @@ def attention_backward_supported(q: torch.Tensor, num_heads: int, window_size: T
                                  n_real: Optional[int] = None) -> bool:
     """Whether :func:`window_attention_backward` serves this shape: the
     forward's (bf16 or fp32, windows up to 8x8 in at most 64 token rows,
-    head dim 32, 64 or 128)."""
+    head dim 32, 64 or 128; or bf16 windows of a multiple of 128 tokens up to
+    4096 without padded keys, head dim 64 or 128, the flash path, which also
+    takes no bias and no mask)."""
     tokens, channels = q.shape[-2], q.shape[-1]
     wh, ww = (int(w) for w in window_size)
+    if channels % num_heads != 0:
+        return False
+    if tokens > 64:
+        return (q.dtype == torch.bfloat16 and tokens % 128 == 0 and tokens <= 4096 and wh * ww == tokens
+                and (n_real is None or int(n_real) == tokens) and channels // num_heads in (64, 128))
     return (q.dtype in (torch.bfloat16, torch.float32) and 1 <= wh <= 8 and 1 <= ww <= 8
             and wh * ww <= tokens <= 64 and (n_real is None or 1 <= int(n_real) <= tokens)
-            and channels % num_heads == 0 and channels // num_heads in (32, 64, 128))
+            and channels // num_heads in (32, 64, 128))
 
 
 def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dout: torch.Tensor,

@@ -151,7 +151,15 @@ def _bwd_desc(dout_stride=64, dq_stride=64, dk_stride=64, dv_stride=64, **kw):
 
 
 @pytest.mark.parametrize("kw,code,text", [
-    (dict(tokens=81, window_h=9, window_w=9, n_real=81), -5, "tokens per window"),
+    (dict(tokens=81, window_h=9, window_w=9, n_real=81), -5, "multiple of 128"),
+    # windows of more than 64 tokens (the flash backward): what it does not serve
+    (dict(tokens=256, window_h=16, window_w=16, n_real=256, channels=128, q_stride=128, k_stride=128, v_stride=128,
+          o_stride=128, dout_stride=128, dq_stride=128, dk_stride=128, dv_stride=128, scale=-0.1), -5,
+     "positive finite scale"),
+    (dict(tokens=256, window_h=16, window_w=16, n_real=256, channels=128, q_stride=128, k_stride=128, v_stride=128,
+          o_stride=128, dout_stride=128, dq_stride=1 << 26, dk_stride=128, dv_stride=128), -3, "too large"),
+    (dict(tokens=256, window_h=16, window_w=16, n_real=256, channels=128, q_stride=128, k_stride=128, v_stride=128,
+          o_stride=128, dout_stride=128, dq_stride=128, dk_stride=128, dv_stride=128, mask_mode=1), -5, "no mask"),
     (dict(window_h=9), -5, "outside 1..8"),
     (dict(n_real=0), -3, "n_real"),
     (dict(heads=3), -3, "not divisible"),

@@ -402,3 +402,132 @@ def test_block_backward_head_dim_128(dev, full):
             assert p.grad.double().norm().item() <= 3e-2 * params["attn.q_linear.bias"].grad.norm().item()
             continue
         assert _normwise(p.grad, params[name].grad) <= 3e-2, name
+
+
+# ---------------------------------------------------------------------------
+# Windows of more than 64 tokens (window 32: TERRA's correctness configuration)
+# ---------------------------------------------------------------------------
+
+def _flash_inputs(B_, N, C, seed, qkv_scale=2.0):
+    q = workloads.activations((B_, N, C), seed) * qkv_scale
+    k = workloads.activations((B_, N, C), seed + 1) * qkv_scale
+    v = workloads.activations((B_, N, C), seed + 2)
+    dout = workloads.activations((B_, N, C), seed + 3)
+    return tuple(t.to(torch.bfloat16) for t in (q, k, v, dout))
+
+
+def _flash_oracle_grads(q, k, v, dout, heads, window):
+    leaves = [t.float().clone().requires_grad_(True) for t in (q, k, v)]
+    C = q.shape[-1]
+    out = so.window_attention_core(*leaves, heads, (C // heads) ** -0.5, None, window, None,
+                                   compute_dtype=torch.float32)
+    (out * dout.float()).sum().backward()
+    return [t.grad for t in leaves]
+
+
+@pytest.mark.parametrize("wh,ww,C,heads,B_", [(32, 32, 256, 2, 2), (16, 16, 128, 2, 3), (24, 16, 256, 2, 2),
+                                               (16, 8, 512, 4, 2), (32, 32, 128, 1, 1)])
+def test_flash_backward_matches_oracle(dev, wh, ww, C, heads, B_):
+    """dq, dk, dv of the windows of more than 64 tokens (statistics pass, dK/dV
+    pass over query tiles, dQ pass over key tiles) against fp32 autograd of the
+    oracle's full-row softmax: 32 x 32 at head dim 128 and 64, 16 x 16 at 64,
+    non-square 24 x 16 (384 tokens) and the smallest window, 16 x 8.  Scores
+    spread (q, k x 2) so the softmax is far from uniform."""
+    N = wh * ww
+    q, k, v, dout = _flash_inputs(B_, N, C, 900 + N + C)
+    scale = (C // heads) ** -0.5
+    dq, dk, dv = kernels.window_attention_backward(q.to(dev), k.to(dev), v.to(dev), dout.to(dev), heads, (wh, ww),
+                                                   scale)
+    rq, rk, rv = _flash_oracle_grads(q, k, v, dout, heads, (wh, ww))
+    for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
+        assert torch.isfinite(got.float()).all()
+        _close(got, ref)
+        assert _normwise(got, ref) <= 1e-2
+
+
+def test_flash_backward_into_qkv_buffer_and_window_independence(dev):
+    """q | k | v as column blocks of one [B_, N, 3C] tensor and the gradients
+    into column blocks of one buffer (the autograd QKV path), equal to the
+    separate-tensor call bit for bit; a window's gradients independent of the
+    other windows."""
+    B_, ws, C, heads = 3, 32, 256, 2
+    N = ws * ws
+    q, k, v, dout = (t.to(dev) for t in _flash_inputs(B_, N, C, 950))
+    scale = (C // heads) ** -0.5
+    ref = kernels.window_attention_backward(q, k, v, dout, heads, (ws, ws), scale)
+    qkv = torch.cat([q, k, v], dim=-1)
+    dqkv = torch.empty_like(qkv)
+    kernels.window_attention_backward(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], dout, heads, (ws, ws), scale,
+                                      dq=dqkv[..., :C], dk=dqkv[..., C:2 * C], dv=dqkv[..., 2 * C:])
+    for i, r in enumerate(ref):
+        assert torch.equal(dqkv[..., i * C:(i + 1) * C], r)
+    one = kernels.window_attention_backward(q[1:2], k[1:2], v[1:2], dout[1:2], heads, (ws, ws), scale)
+    for a, r in zip(one, ref):
+        assert torch.equal(a, r[1:2])
+
+
+def test_flash_backward_autograd(dev):
+    """The attention autograd function at window 32 (forward on the flash
+    kernel, backward on the three flash passes) against fp32 autograd."""
+    B_, ws, C, heads = 2, 32, 256, 2
+    N = ws * ws
+    q, k, v, dout = _flash_inputs(B_, N, C, 960)
+    scale = (C // heads) ** -0.5
+    leaves = [t.to(dev).requires_grad_(True) for t in (q, k, v)]
+    out = autograd.window_attention(*leaves, heads, (ws, ws), scale)
+    out.backward(dout.to(dev))
+    refs = _flash_oracle_grads(q, k, v, dout, heads, (ws, ws))
+    for t, r in zip(leaves, refs):
+        _close(t.grad, r)
+
+
+def test_flash_backward_rejects_what_it_does_not_serve(dev):
+    B_, ws, C, heads = 1, 16, 128, 2
+    N = ws * ws
+    q, k, v, dout = (t.to(dev) for t in _flash_inputs(B_, N, C, 970))
+    table = torch.zeros(31 * 31, heads, device=dev)
+    with pytest.raises(ValueError, match="no relative-position bias and no mask"):
+        kernels.window_attention_backward(q, k, v, dout, heads, (ws, ws), 0.1, bias_table=table)
+    with pytest.raises(ValueError, match="bf16 only"):
+        kernels.window_attention_backward(q.float(), k.float(), v.float(), dout.float(), heads, (ws, ws), 0.1)
+    with pytest.raises(ValueError, match="must not overlap"):
+        kernels.window_attention_backward(q, k, v, dout, heads, (ws, ws), 0.1, dq=dout)
+    with pytest.raises(ValueError, match="positive finite scale"):
+        kernels.window_attention_backward(q, k, v, dout, heads, (ws, ws), -0.1)
+    assert not kernels.attention_backward_supported(q.float(), heads, (ws, ws))
+    assert kernels.attention_backward_supported(q, heads, (ws, ws))
+    assert not kernels.attention_backward_supported(q[:, :192], heads, (16, 12))
+
+
+@pytest.mark.parametrize("layer_idx", [0, 1])
+def test_block_backward_window_32(dev, layer_idx):
+    """SequentialSwinTransformer.backward at window 32 with bias and mask off
+    (TERRA's correctness configuration, C and heads scaled to 256 and 2, head
+    dim 128), bf16, against the fp32 oracle block under autograd."""
+    H, W, C, heads, ws = 64, 96, 256, 2, 32
+    blk = SequentialSwinTransformer(layer_idx=layer_idx, height=H, width=W, embedding_dim=C, window_size=ws,
+                                    num_heads=heads, use_attn_mask=False, use_relative_position_bias=False)
+    workloads.init_block_params(blk, layer_idx)
+    with torch.no_grad():
+        for lin in (blk.attn.q_linear, blk.attn.k_linear):
+            lin.weight.mul_(4.0)
+        blk.attn.proj.weight.mul_(8.0)
+    params = {n: p.detach().to(torch.bfloat16).float().clone().requires_grad_(True)
+              for n, p in blk.named_parameters()}
+    blk = blk.to(dev).to(torch.bfloat16)
+    x = workloads.activations((1, H * W, C), 980 + layer_idx).to(torch.bfloat16)
+    gy = workloads.activations((1, H * W, C), 990 + layer_idx).to(torch.bfloat16)
+    xd = x.to(dev).requires_grad_(True)
+    y = blk(xd)
+    y.backward(gy.to(dev))
+    xr = x.float().requires_grad_(True)
+    yr = so.swin_block_attention(xr, H, W, ws, blk.shift_size, heads, params, use_attn_mask=False)
+    yr.backward(gy.float())
+    assert _normwise(y.detach(), yr.detach()) <= 2e-2
+    assert _normwise(xd.grad, xr.grad) <= 3e-2
+    for name, p in blk.named_parameters():
+        assert p.grad is not None, name
+        if name == "attn.k_linear.bias":  # exactly 0 in exact arithmetic (see test_block_backward_matches_oracle)
+            assert p.grad.double().norm().item() <= 3e-2 * params["attn.q_linear.bias"].grad.norm().item()
+            continue
+        assert _normwise(p.grad, params[name].grad) <= 3e-2, name
