@@ -532,6 +532,16 @@ __device__ __forceinline__ void dma_to_lds4_at(const void* sbase, uint32_t voff,
   asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
 }
 
+// 16-byte slot of (key row, chunk) in a tile of cpr chunks per
+// row.  256-byte rows (head dim 128) are a whole bank period, so the chunk is
+// XORed with row & 15: the 16 rows of a fragment read hit 16 distinct 16-byte
+// bank groups (and 8 consecutive rows 8 distinct ones).  128-byte rows take
+// the 8x8 kernels' (row >> 1) & 7.
+template <int cpr>
+__device__ __forceinline__ int flash_slot(int row, int chunk) {
+  return row * cpr + (chunk ^ (cpr >= 16 ? (row & 15) : ((row >> 1) & 7)));
+}
+
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }

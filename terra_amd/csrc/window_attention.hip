@@ -408,15 +408,6 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
 constexpr int kFlashQ = 128;  // queries per workgroup (W = 4)
 constexpr int kFlashK = 64;   // keys per LDS tile
 
-// 16-byte slot of (key row, chunk) in a flash K or V tile of cpr chunks per
-// row.  256-byte rows (head dim 128) are a whole bank period, so the chunk is
-// XORed with row & 15: the 16 rows of a fragment read hit 16 distinct 16-byte
-// bank groups (and 8 consecutive rows 8 distinct ones).  128-byte rows take
-// the 8x8 kernels' (row >> 1) & 7.
-template <int cpr>
-__device__ __forceinline__ int flash_slot(int row, int chunk) {
-  return row * cpr + (chunk ^ (cpr >= 16 ? (row & 15) : ((row >> 1) & 7)));
-}
 
 template <int D>
 constexpr int flash_lds_bytes() {
