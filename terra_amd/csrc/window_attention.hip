@@ -248,7 +248,7 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
 
   // This thread's part of a unit's loads: one 1 KB block of one tensor per
   // wave and round, LDS slot s of the block holding (row, chunk) with
-  // tile_slot(row, chunk) = block * 64 + s.  Per round: the tensor, its row
+  // flash_slot(row, chunk) = block * 64 + s.  Per round: the tensor, its row
   // stride, the element offset inside the window's rows and the LDS block.
   const uint16_t* src_base[kRounds];
   int64_t src_stride[kRounds];
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
     const int t = blk / kBlocksPerTile;           // 0 q, 1 k, 2 v
     const int sl = (blk - t * kBlocksPerTile) * 64 + lane;
     const int row = sl / cpr;
-    const int ch = (sl - row * cpr) ^ ((row >> 1) & 7);
+    const int ch = flash_slot<cpr>(row, sl - row * cpr) - row * cpr;  // the XOR is its own inverse
     src_base[r] = t == 0 ? reinterpret_cast<const uint16_t*>(p.q)
                          : t == 1 ? reinterpret_cast<const uint16_t*>(p.k) : reinterpret_cast<const uint16_t*>(p.v);
     src_stride[r] = t == 0 ? p.q_stride : t == 1 ? p.k_stride : p.v_stride;
@@ -309,8 +309,8 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
       for (int c = 0; c < KF; ++c) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          kf[t][c] = *reinterpret_cast<const uint4*>(ks + tile_slot(16 * t + c16, hc + 4 * c + g, cpr) * 16);
-        qp[0][c] = *reinterpret_cast<const uint4*>(qs + tile_slot(16 * it + c16, hc + 4 * c + g, cpr) * 16);
+          kf[t][c] = *reinterpret_cast<const uint4*>(ks + flash_slot<cpr>(16 * t + c16, hc + 4 * c + g) * 16);
+        qp[0][c] = *reinterpret_cast<const uint4*>(qs + flash_slot<cpr>(16 * it + c16, hc + 4 * c + g) * 16);
       }
       auto vfrag = [&](int ct, int js) -> bf16x8 {
         const int cc = head * D + 16 * ct + 4 * (c16 & 3);  // channel of this source lane
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
           const int row = 32 * js + 16 * h2 + 4 * g + (c16 >> 2);
-          part[h2] = lds_read_tr16(vs + tile_slot(row, cc >> 3, cpr) * 16 + (cc & 7) * 2);
+          part[h2] = lds_read_tr16(vs + flash_slot<cpr>(row, cc >> 3) * 16 + (cc & 7) * 2);
         }
         const uint32_t wd[4] = {part[0].x, part[0].y, part[1].x, part[1].y};
         return __builtin_bit_cast(bf16x8, wd);
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
         uint2 pk;
         pk.x = pack_bf16x2(v[0], v[1]);
         pk.y = pack_bf16x2(v[2], v[3]);
-        *reinterpret_cast<uint2*>(qs + tile_slot(i, cc >> 3, cpr) * 16 + (cc & 7) * 2) = pk;
+        *reinterpret_cast<uint2*>(qs + flash_slot<cpr>(i, cc >> 3) * 16 + (cc & 7) * 2) = pk;
       }
     }
     lds_barrier();                                // O complete
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(G * 256) void window_attn_ring_kernel(const AttnPar
       for (int u = 0; u < kOPer; ++u) {
         const int row = orow + u * (nthreads / cpr);
         const u32x4 val =
-            __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(qs + tile_slot(row, ochunk, cpr) * 16));
+            __builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(qs + flash_slot<cpr>(row, ochunk) * 16));
         stream_store_sc1(val, out, (uint32_t)(row * p.o_stride + ochunk * 8) * 2);
       }
     }
