@@ -448,7 +448,7 @@ __device__ __forceinline__ void head_qkv(const BlockParams& p, const uint8_t* xn
 // Attention of head h from the register fragments, one query tile at a time;
 // O (bf16) goes to columns [32h, 32h + 32) of `o_tile`, or with kHold to
 // hold[it][ct] (channels 32h + 16ct + 4g .. + 3 of query 16 it + c).
-template <int C, bool kHold = false>
+template <int C, bool kHold = false, int kNQt = 4>
 __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitLoc cur, const float* tab, int h,
                                                int lane, const uint4 (&kf4)[4], const uint4 (&vf)[2][2],
                                                const uint4 (&qf)[4], uint8_t* o_tile, uint2 (*hold)[2] = nullptr) {
@@ -458,14 +458,14 @@ __device__ __forceinline__ void head_attention(const BlockParams& p, const UnitL
   const float* tabr = lane_bias_rev(tab, lane);
   auto vsrc = [&](int ct, int js) -> bf16x8 { return __builtin_bit_cast(bf16x8, vf[ct][js]); };
   // The four query tiles under one mask mode (a wave-uniform choice per
-  // window, outside the loop).
-  // All four query tiles advance together: the most independent work to
-  // overlap the MFMA, exp and cross-lane latencies of a tile (measured faster
-  // than two at a time, although the register budget then spills one 16-byte
-  // value per window).
+  // window, outside the loop), kNQt of them through each stage together: the
+  // more, the more independent work to overlap the MFMA, exp and cross-lane
+  // latencies of a tile (four measured faster than two in the six-head
+  // kernel; in the twelve-head kernel two leave its 168 registers unspilled
+  // at the same speed).
   auto run = [&](auto mode, const f32x4 (&land_term)[4], uint64_t rid_pack) {
     constexpr int kMask = decltype(mode)::value;
-    constexpr int kNQ = 4;
+    constexpr int kNQ = kNQt;
 #pragma unroll
     for (int it0 = 0; it0 < 4; it0 += kNQ) {
       __builtin_amdgcn_sched_barrier(0);  // kNQ query tiles at a time (register pressure)
@@ -661,7 +661,9 @@ void swin_block_kernel(const BlockParams p) {
       // phase issues no vector-memory loads of its own).
       if (next < p.units) fetch_window<cpr, kH>(p, nxt, xr_next, wave, lane_index());
       lds_barrier();     // every wave has read xn; O overwrites it
-      head_attention<C>(p, cur, tabs + wave * kTableMax, wave, lane_i, kf4, vf, qf, xn);
+      // Two query tiles at a time: four spilled one VGPR at three waves per
+      // SIMD (168 registers); two leave none (c5 411-420 -> 410-411 us A/B).
+      head_attention<C, false, 2>(p, cur, tabs + wave * kTableMax, wave, lane_i, kf4, vf, qf, xn);
       lds_barrier();     // O complete
       head_proj<C, kPacked>(p, xn, xr, wave, lane_i, p.b_proj);
     } else if (next < p.units) {
