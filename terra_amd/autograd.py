@@ -134,7 +134,7 @@ class _Linear(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             dw = weight_grad(dy2, xc.reshape(-1, xc.shape[-1])).to(wd)
         if bd is not None and ctx.needs_input_grad[2]:
-            db = dy2.float().sum(0).to(bd)
+            db = dy2.sum(0, dtype=torch.float32).to(bd)
         return dx, dw, db
 
 
@@ -178,11 +178,11 @@ class _Mlp(torch.autograd.Function):
         w2c, w1c = w2.to(gemm_dtype), w1.to(gemm_dtype)
         da = dh2 @ w2c
         dw2 = weight_grad(dh2, a.to(gemm_dtype)) if ctx.needs_input_grad[5] else None
-        db2 = dh2.float().sum(0) if ctx.needs_input_grad[6] else None
+        db2 = dh2.sum(0, dtype=torch.float32) if ctx.needs_input_grad[6] else None
         dh1 = torch.ops.aten.gelu_backward(da, h1)
         dxn = dh1 @ w1c
         dw1 = weight_grad(dh1, xn.to(gemm_dtype)) if ctx.needs_input_grad[3] else None
-        db1 = dh1.float().sum(0) if ctx.needs_input_grad[4] else None
+        db1 = dh1.sum(0, dtype=torch.float32) if ctx.needs_input_grad[4] else None
         dlw = torch.zeros(C, dtype=torch.float32, device=rows.device) if (
             ln_w is not None and ctx.needs_input_grad[1]) else None
         dlb = torch.zeros(C, dtype=torch.float32, device=rows.device) if (
