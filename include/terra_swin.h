@@ -200,6 +200,20 @@ int terra_swin_partition_ln(const void* x, void* windows, int dtype,
                             const float* beta, float eps, float pad_value,
                             void* stream);
 
+/* terra_swin_partition_ln with windows of another dtype than x: fp32 x and
+ * bf16 windows (x_dtype == windows_dtype is terra_swin_partition_ln).  Each
+ * value is the fp32 LayerNorm output rounded once to bf16 (round to nearest
+ * even), bit for bit what terra_swin_partition_ln in fp32 followed by a cast
+ * to bf16 gives.  Replaces, in the training step's bf16 autocast region
+ * (core/runtime/run_model.py:424-448), norm1 + roll + window_partition
+ * (models/transformer.py:150-225) in fp32 and the cast autocast applies to
+ * their output at the q/k/v Linear (models/attention.py:244-246), and
+ * norm2 (models/mlp.py:159) with the cast at fc1.
+ */
+int terra_swin_partition_ln_mixed(const void* x, int x_dtype, void* windows, int windows_dtype,
+                                  const terra_swin_geom* geom, const float* gamma, const float* beta,
+                                  float eps, float pad_value, void* stream);
+
 /* Backward of terra_swin_partition_ln (with pad_value constant: padded slots
  * carry no gradient), plus an optional residual gradient.
  * Replaces the autograd backward of
@@ -223,6 +237,18 @@ int terra_swin_partition_ln(const void* x, void* windows, int dtype,
 int terra_swin_partition_ln_bwd(const void* dwindows, const void* x, const void* dresidual, void* dx,
                                 int dtype, const terra_swin_geom* geom, const float* gamma, float eps,
                                 float* dgamma, float* dbeta, void* stream);
+
+/* terra_swin_partition_ln_bwd with a windows gradient of another dtype than
+ * x: a bf16 gradient (of the bf16 windows terra_swin_partition_ln_mixed
+ * writes) for fp32 x, dresidual and dx (x_dtype == dwindows_dtype is
+ * terra_swin_partition_ln_bwd).  The gradient's bf16 values enter the fp32
+ * arithmetic exactly, so the result equals terra_swin_partition_ln_bwd on the
+ * gradient cast to fp32 (the backward of autocast's cast).
+ */
+int terra_swin_partition_ln_bwd_mixed(const void* dwindows, int dwindows_dtype, const void* x,
+                                      const void* dresidual, void* dx, int x_dtype,
+                                      const terra_swin_geom* geom, const float* gamma, float eps,
+                                      float* dgamma, float* dbeta, void* stream);
 
 /* Fused window reverse + inverse cyclic shift + crop (+ residual add).
  * Replaces  window_reverse(attn_windows, ws, H, W)    models/utils.py:41-45

@@ -47,7 +47,9 @@ EXPORTED_SYMBOLS = (
     "terra_last_error",
     "terra_swin_partition",
     "terra_swin_partition_ln",
+    "terra_swin_partition_ln_mixed",
     "terra_swin_partition_ln_bwd",
+    "terra_swin_partition_ln_bwd_mixed",
     "terra_swin_reverse",
     "terra_swin_attn_fwd",
     "terra_swin_attn_bwd",
@@ -190,6 +192,12 @@ def load() -> ctypes.CDLL:
         lib.terra_swin_partition_ln_bwd.restype = ctypes.c_int
         lib.terra_swin_partition_ln_bwd.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinGeom), vp,
                                                     ctypes.c_float, vp, vp, vp]
+        lib.terra_swin_partition_ln_mixed.restype = ctypes.c_int
+        lib.terra_swin_partition_ln_mixed.argtypes = [vp, ctypes.c_int, vp, ctypes.c_int, ctypes.POINTER(SwinGeom),
+                                                      vp, vp, ctypes.c_float, ctypes.c_float, vp]
+        lib.terra_swin_partition_ln_bwd_mixed.restype = ctypes.c_int
+        lib.terra_swin_partition_ln_bwd_mixed.argtypes = [vp, ctypes.c_int, vp, vp, vp, ctypes.c_int,
+                                                          ctypes.POINTER(SwinGeom), vp, ctypes.c_float, vp, vp, vp]
         lib.terra_swin_reverse.restype = ctypes.c_int
         lib.terra_swin_reverse.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinGeom), vp]
         lib.terra_swin_attn_fwd.restype = ctypes.c_int

@@ -62,13 +62,15 @@ class _Reverse(torch.autograd.Function):
 class _PartitionLN(torch.autograd.Function):
     """LayerNorm over C + pad + roll + partition (terra_swin_partition_ln),
     backward by terra_swin_partition_ln_bwd: dx, and the weight / bias
-    gradients summed over the tokens."""
+    gradients summed over the tokens.  With out_dtype bf16 for fp32 x the
+    windows are the fp32 output rounded once to bf16 and their gradient
+    arrives in bf16 (the _mixed entry points)."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, geom, eps):
+    def forward(ctx, x, weight, bias, geom, eps, out_dtype):
         ctx.geom, ctx.eps = geom, eps
         ctx.save_for_backward(x, weight, bias)
-        return kernels.swin_partition_ln(x, geom, weight, bias, eps)
+        return kernels.swin_partition_ln(x, geom, weight, bias, eps, out_dtype=out_dtype)
 
     @staticmethod
     def backward(ctx, grad: torch.Tensor):
@@ -79,16 +81,25 @@ class _PartitionLN(torch.autograd.Function):
         if bias is not None and ctx.needs_input_grad[2]:
             db = torch.zeros(bias.shape, dtype=torch.float32, device=x.device)
         dx = kernels.swin_partition_ln_backward(grad.contiguous(), x, ctx.geom, weight, ctx.eps, dweight=dw, dbias=db)
-        return (dx, None if dw is None else dw.to(weight.dtype), None if db is None else db.to(bias.dtype), None, None)
+        return (dx, None if dw is None else dw.to(weight.dtype), None if db is None else db.to(bias.dtype), None, None,
+                None)
+
+
+def linear_input_dtype(x: torch.Tensor) -> torch.dtype:
+    """The dtype F.linear computes in for an input like x: bf16 inside a bf16
+    autocast region (which casts its fp32 input to bf16), else x's own."""
+    return torch.bfloat16 if kernels.autocast_bf16(x) and x.dtype == torch.float32 else x.dtype
 
 
 def partition_ln(x: torch.Tensor, geom: WindowGeometry, weight: Optional[torch.Tensor],
-                 bias: Optional[torch.Tensor], eps: float) -> torch.Tensor:
+                 bias: Optional[torch.Tensor], eps: float, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """:func:`kernels.swin_partition_ln` with gradients for x and the
-    LayerNorm affine parameters."""
+    LayerNorm affine parameters.  ``out_dtype`` bf16 for fp32 x writes the
+    bf16 copy a following Linear under bf16 autocast would cast to (and takes
+    its bf16 gradient), instead of fp32 windows and a cast each way."""
     if _needs_grad(x, weight, bias):
-        return _PartitionLN.apply(x, weight, bias, geom, eps)
-    return kernels.swin_partition_ln(x, geom, weight, bias, eps)
+        return _PartitionLN.apply(x, weight, bias, geom, eps, out_dtype)
+    return kernels.swin_partition_ln(x, geom, weight, bias, eps, out_dtype=out_dtype)
 
 
 def weight_grad(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
@@ -158,7 +169,10 @@ class _Mlp(torch.autograd.Function):
         C = x.shape[-1]
         rows = x.reshape(-1, C).contiguous()
         geom = kernels.rows_geometry(rows.shape[0], C)
-        xn = kernels.swin_partition_ln(rows.view(1, -1, 1, C), geom, ln_w, ln_b, eps).view(-1, C)
+        # Under bf16 autocast fc1 takes a bf16 copy of the fp32 LayerNorm
+        # output: the kernel writes that copy directly.
+        xn = kernels.swin_partition_ln(rows.view(1, -1, 1, C), geom, ln_w, ln_b, eps,
+                                       out_dtype=linear_input_dtype(rows)).view(-1, C)
         h1 = torch.nn.functional.linear(xn, w1, b1)
         a = torch.nn.functional.gelu(h1)
         h2 = torch.nn.functional.linear(a, w2, b2)
@@ -187,8 +201,9 @@ class _Mlp(torch.autograd.Function):
             ln_w is not None and ctx.needs_input_grad[1]) else None
         dlb = torch.zeros(C, dtype=torch.float32, device=rows.device) if (
             ln_b is not None and ctx.needs_input_grad[2]) else None
+        # dxn in xn's dtype (bf16 under autocast, read exactly by the kernel).
         dx = kernels.swin_partition_ln_backward(
-            dxn.to(rows.dtype).contiguous().view(-1, 1, C), rows.view(1, -1, 1, C), ctx.geom, ln_w, ctx.eps,
+            dxn.to(xn.dtype).contiguous().view(-1, 1, C), rows.view(1, -1, 1, C), ctx.geom, ln_w, ctx.eps,
             dresidual=dy.to(rows.dtype).contiguous(), dweight=dlw, dbias=dlb)
         cast = lambda g, p: None if g is None else g.to(p.dtype)  # noqa: E731
         return (dx.view(ctx.shape), cast(dlw, ln_w), cast(dlb, ln_b), cast(dw1, w1), cast(db1, w1),

@@ -73,6 +73,7 @@ struct CopyGeom {
   int32_t valid_begin, valid_end;  // valid_end <= 0: all valid
   int32_t N;
   int64_t row_bytes;               // C * elt
+  int64_t win_row_bytes;           // C * elt of the windows (the LayerNorm kernels' mixed-dtype forms)
   FastDiv fd_cv, fd_N, fd_nWe, fd_nWw, fd_ws, fd_W, fd_H;
   uint32_t total;                  // chunks in the destination
   uint32_t pad_pattern;
@@ -209,10 +210,15 @@ struct LnParams {
 constexpr int kLnMaxChannels = 1024;
 constexpr int kLnMaxChunks = 256;
 
-template <int DT, int CPL, int kL>
+// DTO: the windows' dtype, DT's or (DT = f32) bf16: each fp32 chunk of four
+// values then leaves as eight bytes, the LayerNorm output rounded once to
+// bf16 (what bf16 autocast casts the fp32 output to before the next Linear).
+template <int DT, int CPL, int kL, int DTO = DT>
 __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* __restrict__ x,
                                                                 uint8_t* __restrict__ win,
                                                                 const CopyGeom g, const LnParams ln) {
+  static_assert(DTO == DT || (DT == TERRA_DTYPE_F32 && DTO == TERRA_DTYPE_BF16), "output dtype");
+  constexpr bool kCast = DTO != DT;
   constexpr int kTokensPerBlock = kThreads / kL;
   constexpr int E = LnElt<DT>::kPerChunk;
   // gamma / beta of all C channels, staged once per workgroup.  Their loads
@@ -299,16 +305,15 @@ __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* _
 
   const uint32_t first = blockIdx.x * kTokensPerBlock;
   const __amdgpu_buffer_rsrc_t out =
-      buffer_rsrc(win + (int64_t)first * g.row_bytes,
-                  (uint32_t)(min(ln.tokens - first, (uint32_t)kTokensPerBlock) * g.row_bytes));
-  const uint32_t row_off = (tok - first) * (uint32_t)g.row_bytes;
+      buffer_rsrc(win + (int64_t)first * g.win_row_bytes,
+                  (uint32_t)(min(ln.tokens - first, (uint32_t)kTokensPerBlock) * g.win_row_bytes));
+  const uint32_t row_off = (tok - first) * (uint32_t)g.win_row_bytes;
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
     const int c = sub + kL * k;
     if (c < ln.chunks) {
-      u32x4 val;
+      float y[E];
       if (in) {
-        float y[E];
 #pragma unroll
         for (int q = 0; q < E; q += 4) {
           const float4 gm = *reinterpret_cast<const float4*>(s_gamma + c * E + q);
@@ -318,11 +323,18 @@ __global__ __launch_bounds__(kThreads) void partition_ln_kernel(const uint8_t* _
           y[q + 2] = (v[k][q + 2] - mean) * rstd * gm.z + bt.z;
           y[q + 3] = (v[k][q + 3] - mean) * rstd * gm.w + bt.w;
         }
-        val = pack_chunk<DT>(y);
-      } else {
-        val = u32x4(g.pad_pattern);
       }
-      stream_store_sc1(val, out, row_off + c * 16);
+      if constexpr (kCast) {  // four fp32 values -> four bf16, eight bytes
+        u32x2 val = u32x2(g.pad_pattern);
+        if (in) {
+          val[0] = f32_to_bf16_bits(y[0]) | ((uint32_t)f32_to_bf16_bits(y[1]) << 16);
+          val[1] = f32_to_bf16_bits(y[2]) | ((uint32_t)f32_to_bf16_bits(y[3]) << 16);
+        }
+        stream_store_sc1(val, out, row_off + c * 8);
+      } else {
+        const u32x4 val = in ? pack_chunk<DT>(y) : u32x4(g.pad_pattern);
+        stream_store_sc1(val, out, row_off + c * 16);
+      }
     }
   }
 }
@@ -349,11 +361,16 @@ struct LnBwdParams {
   uint32_t tokens;     // grid tokens B * H * W
 };
 
-template <int DT, int CPL, int kL, bool kRes>
+// DTG: the windows' gradient dtype, DT's or (DT = f32) bf16 (the gradient
+// of the bf16 windows partition_ln_kernel<f32, .., bf16> writes): each chunk
+// of four values is read as eight bytes.
+template <int DT, int CPL, int kL, bool kRes, int DTG = DT>
 __global__ __launch_bounds__(kThreads) void partition_ln_bwd_kernel(const uint8_t* __restrict__ dwin,
                                                                     const uint8_t* __restrict__ x, uint8_t* dx,
                                                                     const uint8_t* dres, const CopyGeom g,
                                                                     const LnBwdParams ln) {
+  static_assert(DTG == DT || (DT == TERRA_DTYPE_F32 && DTG == TERRA_DTYPE_BF16), "gradient dtype");
+  constexpr bool kCast = DTG != DT;
   constexpr int kTokensPerPass = kThreads / kL;
   constexpr int E = LnElt<DT>::kPerChunk;
   constexpr int kMaxC = CPL * kL * E;
@@ -392,15 +409,20 @@ __global__ __launch_bounds__(kThreads) void partition_ln_bwd_kernel(const uint8_
                       (g.valid_end <= 0 || (wl >= g.valid_begin && wl < g.valid_end));
     const int64_t slot = have ? ((int64_t)b * g.win_rows * g.nWw + wl) * g.N + (int64_t)(ti * g.ws + tj) : 0;
     const u32x4* xs = reinterpret_cast<const u32x4*>(x + (int64_t)tok * g.row_bytes);
-    const u32x4* gs = reinterpret_cast<const u32x4*>(dwin + slot * g.row_bytes);
+    const u32x4* gs = reinterpret_cast<const u32x4*>(dwin + slot * g.win_row_bytes);
+    const u32x2* gs2 = reinterpret_cast<const u32x2*>(dwin + slot * g.win_row_bytes);
     const u32x4* rs = reinterpret_cast<const u32x4*>(dres + (kRes ? (int64_t)tok * g.row_bytes : 0));
     // Unconditional loads: chunks past the row read chunk 0 and count as zeros.
-    u32x4 xr[CPL], gr[CPL], rr[kRes ? CPL : 1];
+    u32x4 xr[CPL], gr[kCast ? 1 : CPL], rr[kRes ? CPL : 1];
+    u32x2 gr2[kCast ? CPL : 1];
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
       const int c = sub + kL * k < ln.chunks ? sub + kL * k : 0;
       xr[k] = __builtin_nontemporal_load(xs + c);
-      gr[k] = __builtin_nontemporal_load(gs + c);
+      if constexpr (kCast)
+        gr2[k] = __builtin_nontemporal_load(gs2 + c);
+      else
+        gr[k] = __builtin_nontemporal_load(gs + c);
       if constexpr (kRes) rr[k] = __builtin_nontemporal_load(rs + c);
     }
     float v[CPL][E], gv[CPL][E];
@@ -408,7 +430,15 @@ __global__ __launch_bounds__(kThreads) void partition_ln_bwd_kernel(const uint8_
     for (int k = 0; k < CPL; ++k) {
       const bool pc = sub + kL * k < ln.chunks;
       unpack_chunk<DT>(pc ? xr[k] : u32x4(0u), v[k]);
-      unpack_chunk<DT>((pc && have) ? gr[k] : u32x4(0u), gv[k]);
+      if constexpr (kCast) {
+        const u32x2 w = (pc && have) ? gr2[k] : u32x2(0u);
+        gv[k][0] = __uint_as_float(w[0] << 16);
+        gv[k][1] = __uint_as_float(w[0] & 0xffff0000u);
+        gv[k][2] = __uint_as_float(w[1] << 16);
+        gv[k][3] = __uint_as_float(w[1] & 0xffff0000u);
+      } else {
+        unpack_chunk<DT>((pc && have) ? gr[k] : u32x4(0u), gv[k]);
+      }
     }
     float sum = 0.f;
 #pragma unroll
@@ -630,6 +660,7 @@ int prepare(const terra_swin_geom* geom, int dtype, bool dest_is_windows, CopyGe
   g->valid_end = q.valid_end > 0 ? q.valid_end : 0;
   g->N = (int32_t)N;
   g->row_bytes = row_bytes;
+  g->win_row_bytes = row_bytes;
   g->fd_cv = FastDiv((uint32_t)(row_bytes / v));
   g->fd_N = FastDiv((uint32_t)N);
   g->fd_nWe = FastDiv((uint32_t)nWe);
@@ -654,34 +685,34 @@ void launch_partition(const void* x, void* win, const CopyGeom& g, hipStream_t s
   partition_kernel<VB><<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g);
 }
 
-template <int DT, int CPL, int kL = kLnLanes>
+template <int DT, int CPL, int kL = kLnLanes, int DTO = DT>
 void launch_partition_ln(const void* x, void* win, const CopyGeom& g, const LnParams& ln, hipStream_t s) {
   constexpr uint32_t kTokensPerBlock = kThreads / kL;
   const uint32_t blocks = (ln.tokens + kTokensPerBlock - 1) / kTokensPerBlock;
-  partition_ln_kernel<DT, CPL, kL><<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g, ln);
+  partition_ln_kernel<DT, CPL, kL, DTO><<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g, ln);
 }
 
-template <int DT>
+template <int DT, int DTO = DT>
 void dispatch_partition_ln(int cpl, const void* x, void* win, const CopyGeom& g, const LnParams& ln,
                            hipStream_t s) {
-  if (cpl <= 1) launch_partition_ln<DT, 1>(x, win, g, ln, s);
-  else if (cpl <= 2) launch_partition_ln<DT, 2>(x, win, g, ln, s);
-  else if (cpl <= 3) launch_partition_ln<DT, 3>(x, win, g, ln, s);
-  else if (cpl <= 4) launch_partition_ln<DT, 4>(x, win, g, ln, s);
-  else if (cpl <= 6) launch_partition_ln<DT, 6>(x, win, g, ln, s);
-  else if (cpl <= 8) launch_partition_ln<DT, 4, 16>(x, win, g, ln, s);  // 16 lanes per token
-  else if (cpl <= 12) launch_partition_ln<DT, 6, 16>(x, win, g, ln, s);
-  else if (cpl <= 16) launch_partition_ln<DT, 8, 16>(x, win, g, ln, s);  // bf16 C = 1024
-  else if (cpl <= 24) launch_partition_ln<DT, 12, 16>(x, win, g, ln, s);
-  else launch_partition_ln<DT, 16, 16>(x, win, g, ln, s);                // fp32 C = 1024
+  if (cpl <= 1) launch_partition_ln<DT, 1, kLnLanes, DTO>(x, win, g, ln, s);
+  else if (cpl <= 2) launch_partition_ln<DT, 2, kLnLanes, DTO>(x, win, g, ln, s);
+  else if (cpl <= 3) launch_partition_ln<DT, 3, kLnLanes, DTO>(x, win, g, ln, s);
+  else if (cpl <= 4) launch_partition_ln<DT, 4, kLnLanes, DTO>(x, win, g, ln, s);
+  else if (cpl <= 6) launch_partition_ln<DT, 6, kLnLanes, DTO>(x, win, g, ln, s);
+  else if (cpl <= 8) launch_partition_ln<DT, 4, 16, DTO>(x, win, g, ln, s);  // 16 lanes per token
+  else if (cpl <= 12) launch_partition_ln<DT, 6, 16, DTO>(x, win, g, ln, s);
+  else if (cpl <= 16) launch_partition_ln<DT, 8, 16, DTO>(x, win, g, ln, s);  // bf16 C = 1024
+  else if (cpl <= 24) launch_partition_ln<DT, 12, 16, DTO>(x, win, g, ln, s);
+  else launch_partition_ln<DT, 16, 16, DTO>(x, win, g, ln, s);                // fp32 C = 1024
 }
 
 // Resident workgroups of the LayerNorm backward (grid-stride over the
 // tokens), queried per device and instance once.
-template <int DT, int CPL, int kL, bool kRes>
+template <int DT, int CPL, int kL, bool kRes, int DTG = DT>
 int launch_partition_ln_bwd(const void* dwin, const void* x, void* dx, const void* dres, const CopyGeom& g,
                             const LnBwdParams& ln, hipStream_t s) {
-  auto kern = partition_ln_bwd_kernel<DT, CPL, kL, kRes>;
+  auto kern = partition_ln_bwd_kernel<DT, CPL, kL, kRes, DTG>;
   constexpr int kMaxDevices = 64;
   static int cache[kMaxDevices] = {0};
   int dev = 0;
@@ -702,23 +733,24 @@ int launch_partition_ln_bwd(const void* dwin, const void* x, void* dx, const voi
   return TERRA_OK;
 }
 
-template <int DT, bool kRes>
+template <int DT, bool kRes, int DTG = DT>
 int dispatch_partition_ln_bwd(int cpl, const void* dwin, const void* x, void* dx, const void* dres,
                               const CopyGeom& g, const LnBwdParams& ln, hipStream_t s) {
-  if (cpl <= 1) return launch_partition_ln_bwd<DT, 1, 8, kRes>(dwin, x, dx, dres, g, ln, s);
-  if (cpl <= 2) return launch_partition_ln_bwd<DT, 2, 8, kRes>(dwin, x, dx, dres, g, ln, s);
-  if (cpl <= 3) return launch_partition_ln_bwd<DT, 3, 8, kRes>(dwin, x, dx, dres, g, ln, s);
-  if (cpl <= 4) return launch_partition_ln_bwd<DT, 4, 8, kRes>(dwin, x, dx, dres, g, ln, s);
-  if (cpl <= 8) return launch_partition_ln_bwd<DT, 4, 16, kRes>(dwin, x, dx, dres, g, ln, s);
-  if (cpl <= 12) return launch_partition_ln_bwd<DT, 6, 16, kRes>(dwin, x, dx, dres, g, ln, s);
-  if (cpl <= 16 || DT != TERRA_DTYPE_F32) return launch_partition_ln_bwd<DT, 8, 16, kRes>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 1) return launch_partition_ln_bwd<DT, 1, 8, kRes, DTG>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 2) return launch_partition_ln_bwd<DT, 2, 8, kRes, DTG>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 3) return launch_partition_ln_bwd<DT, 3, 8, kRes, DTG>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 4) return launch_partition_ln_bwd<DT, 4, 8, kRes, DTG>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 8) return launch_partition_ln_bwd<DT, 4, 16, kRes, DTG>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 12) return launch_partition_ln_bwd<DT, 6, 16, kRes, DTG>(dwin, x, dx, dres, g, ln, s);
+  if (cpl <= 16 || DT != TERRA_DTYPE_F32)
+    return launch_partition_ln_bwd<DT, 8, 16, kRes, DTG>(dwin, x, dx, dres, g, ln, s);
   // fp32 rows of more than 512 channels (16-bit rows of at most 1024 channels
   // never get here)
   if constexpr (DT == TERRA_DTYPE_F32) {
-    if (cpl <= 24) return launch_partition_ln_bwd<DT, 12, 16, kRes>(dwin, x, dx, dres, g, ln, s);
-    return launch_partition_ln_bwd<DT, 16, 16, kRes>(dwin, x, dx, dres, g, ln, s);
+    if (cpl <= 24) return launch_partition_ln_bwd<DT, 12, 16, kRes, DTG>(dwin, x, dx, dres, g, ln, s);
+    return launch_partition_ln_bwd<DT, 16, 16, kRes, DTG>(dwin, x, dx, dres, g, ln, s);
   }
-  return TERRA_OK;
+  return fail(TERRA_ERR_UNSUPPORTED, "fused LayerNorm backward: row too wide");
 }
 
 template <int VB, int DT>
@@ -770,13 +802,20 @@ extern "C" int terra_swin_partition(const void* x, void* windows, int dtype,
   return launch_status("terra_swin_partition");
 }
 
-extern "C" int terra_swin_partition_ln(const void* x, void* windows, int dtype, const terra_swin_geom* geom,
-                                       const float* gamma, const float* beta, float eps, float pad_value,
-                                       void* stream) {
-  clear_error();
+namespace terra {
+namespace {
+
+// terra_swin_partition_ln with windows of dtype wdt: x's dtype, or bf16 for
+// fp32 x (partition_ln_kernel's DTO).
+int partition_ln_impl(const void* x, int dtype, void* windows, int wdt, const terra_swin_geom* geom,
+                      const float* gamma, const float* beta, float eps, float pad_value, void* stream) {
   if (x == nullptr || windows == nullptr) return fail(TERRA_ERR_NULL, "x or windows is NULL");
   if (dtype != TERRA_DTYPE_F32 && dtype != TERRA_DTYPE_BF16 && dtype != TERRA_DTYPE_F16)
     return fail(TERRA_ERR_DTYPE, "fused LayerNorm supports f32, f16 and bf16 (got dtype %d)", dtype);
+  const bool cast = wdt != dtype;
+  if (cast && !(dtype == TERRA_DTYPE_F32 && wdt == TERRA_DTYPE_BF16))
+    return fail(TERRA_ERR_DTYPE, "fused LayerNorm: windows of dtype %d from x of dtype %d (mixed: f32 x, bf16 windows)",
+                wdt, dtype);
   if (!(eps >= 0.f)) return fail(TERRA_ERR_SHAPE, "eps must be non-negative");
   CopyGeom g;
   int vb = 0;
@@ -791,7 +830,8 @@ extern "C" int terra_swin_partition_ln(const void* x, void* windows, int dtype, 
   if (chunks > kLnMaxChunks || geom->channels > kLnMaxChannels)
     return fail(TERRA_ERR_UNSUPPORTED, "fused LayerNorm handles up to %d channels in rows of up to %d bytes (got %d "
                 "channels, %lld bytes)", kLnMaxChannels, kLnMaxChunks * 16, geom->channels, (long long)g.row_bytes);
-  g.pad_pattern = pad_pattern(dtype, pad_value);
+  g.win_row_bytes = (int64_t)geom->channels * dtype_size(wdt);
+  g.pad_pattern = pad_pattern(wdt, pad_value);
   LnParams ln;
   ln.gamma = gamma;
   ln.beta = beta;
@@ -801,11 +841,33 @@ extern "C" int terra_swin_partition_ln(const void* x, void* windows, int dtype, 
   ln.tokens = g.total / (uint32_t)chunks;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case TERRA_DTYPE_F32: dispatch_partition_ln<TERRA_DTYPE_F32>(cpl, x, windows, g, ln, s); break;
+    case TERRA_DTYPE_F32:
+      if (cast)
+        dispatch_partition_ln<TERRA_DTYPE_F32, TERRA_DTYPE_BF16>(cpl, x, windows, g, ln, s);
+      else
+        dispatch_partition_ln<TERRA_DTYPE_F32>(cpl, x, windows, g, ln, s);
+      break;
     case TERRA_DTYPE_F16: dispatch_partition_ln<TERRA_DTYPE_F16>(cpl, x, windows, g, ln, s); break;
     default: dispatch_partition_ln<TERRA_DTYPE_BF16>(cpl, x, windows, g, ln, s); break;
   }
   return launch_status("terra_swin_partition_ln");
+}
+
+}  // namespace
+}  // namespace terra
+
+extern "C" int terra_swin_partition_ln(const void* x, void* windows, int dtype, const terra_swin_geom* geom,
+                                       const float* gamma, const float* beta, float eps, float pad_value,
+                                       void* stream) {
+  clear_error();
+  return partition_ln_impl(x, dtype, windows, dtype, geom, gamma, beta, eps, pad_value, stream);
+}
+
+extern "C" int terra_swin_partition_ln_mixed(const void* x, int x_dtype, void* windows, int windows_dtype,
+                                             const terra_swin_geom* geom, const float* gamma, const float* beta,
+                                             float eps, float pad_value, void* stream) {
+  clear_error();
+  return partition_ln_impl(x, x_dtype, windows, windows_dtype, geom, gamma, beta, eps, pad_value, stream);
 }
 
 extern "C" int terra_swin_reverse(const void* windows, void* y, const void* residual, int dtype,
@@ -834,13 +896,22 @@ extern "C" int terra_swin_reverse(const void* windows, void* y, const void* resi
   return launch_status("terra_swin_reverse");
 }
 
-extern "C" int terra_swin_partition_ln_bwd(const void* dwindows, const void* x, const void* dresidual, void* dx,
-                                           int dtype, const terra_swin_geom* geom, const float* gamma, float eps,
-                                           float* dgamma, float* dbeta, void* stream) {
-  clear_error();
+namespace terra {
+namespace {
+
+// terra_swin_partition_ln_bwd with a windows gradient of dtype gdt: x's, or
+// bf16 for fp32 x (partition_ln_bwd_kernel's DTG).
+int partition_ln_bwd_impl(const void* dwindows, int gdt, const void* x, const void* dresidual, void* dx, int dtype,
+                          const terra_swin_geom* geom, const float* gamma, float eps, float* dgamma, float* dbeta,
+                          void* stream) {
   if (dwindows == nullptr || x == nullptr || dx == nullptr) return fail(TERRA_ERR_NULL, "dwindows, x or dx is NULL");
   if (dtype != TERRA_DTYPE_F32 && dtype != TERRA_DTYPE_BF16 && dtype != TERRA_DTYPE_F16)
     return fail(TERRA_ERR_DTYPE, "fused LayerNorm backward supports f32, f16 and bf16 (got dtype %d)", dtype);
+  const bool cast = gdt != dtype;
+  if (cast && !(dtype == TERRA_DTYPE_F32 && gdt == TERRA_DTYPE_BF16))
+    return fail(TERRA_ERR_DTYPE,
+                "fused LayerNorm backward: a windows gradient of dtype %d for x of dtype %d (mixed: f32 x, bf16 gradient)",
+                gdt, dtype);
   if (!(eps >= 0.f)) return fail(TERRA_ERR_SHAPE, "eps must be non-negative");
   CopyGeom g;
   int vb = 0;
@@ -858,6 +929,7 @@ extern "C" int terra_swin_partition_ln_bwd(const void* dwindows, const void* x, 
   const uintptr_t xa = (uintptr_t)x, da = (uintptr_t)dx;
   if (xa < da + (uintptr_t)grid_bytes && da < xa + (uintptr_t)grid_bytes)
     return fail(TERRA_ERR_SHAPE, "dx must not overlap x");
+  g.win_row_bytes = (int64_t)geom->channels * dtype_size(gdt);
   LnBwdParams ln;
   ln.gamma = gamma;
   ln.dgamma = dgamma;
@@ -872,8 +944,14 @@ extern "C" int terra_swin_partition_ln_bwd(const void* dwindows, const void* x, 
   const bool res = dresidual != nullptr;
   switch (dtype) {
     case TERRA_DTYPE_F32:
-      rc = res ? dispatch_partition_ln_bwd<TERRA_DTYPE_F32, true>(cpl, dwindows, x, dx, dresidual, g, ln, s)
-               : dispatch_partition_ln_bwd<TERRA_DTYPE_F32, false>(cpl, dwindows, x, dx, nullptr, g, ln, s);
+      if (cast)
+        rc = res ? dispatch_partition_ln_bwd<TERRA_DTYPE_F32, true, TERRA_DTYPE_BF16>(cpl, dwindows, x, dx, dresidual,
+                                                                                    g, ln, s)
+                 : dispatch_partition_ln_bwd<TERRA_DTYPE_F32, false, TERRA_DTYPE_BF16>(cpl, dwindows, x, dx, nullptr,
+                                                                                     g, ln, s);
+      else
+        rc = res ? dispatch_partition_ln_bwd<TERRA_DTYPE_F32, true>(cpl, dwindows, x, dx, dresidual, g, ln, s)
+                 : dispatch_partition_ln_bwd<TERRA_DTYPE_F32, false>(cpl, dwindows, x, dx, nullptr, g, ln, s);
       break;
     case TERRA_DTYPE_F16:
       rc = res ? dispatch_partition_ln_bwd<TERRA_DTYPE_F16, true>(cpl, dwindows, x, dx, dresidual, g, ln, s)
@@ -886,4 +964,23 @@ extern "C" int terra_swin_partition_ln_bwd(const void* dwindows, const void* x, 
   }
   if (rc != TERRA_OK) return rc;
   return launch_status("terra_swin_partition_ln_bwd");
+}
+
+}  // namespace
+}  // namespace terra
+
+extern "C" int terra_swin_partition_ln_bwd(const void* dwindows, const void* x, const void* dresidual, void* dx,
+                                           int dtype, const terra_swin_geom* geom, const float* gamma, float eps,
+                                           float* dgamma, float* dbeta, void* stream) {
+  clear_error();
+  return partition_ln_bwd_impl(dwindows, dtype, x, dresidual, dx, dtype, geom, gamma, eps, dgamma, dbeta, stream);
+}
+
+extern "C" int terra_swin_partition_ln_bwd_mixed(const void* dwindows, int dwindows_dtype, const void* x,
+                                                 const void* dresidual, void* dx, int x_dtype,
+                                                 const terra_swin_geom* geom, const float* gamma, float eps,
+                                                 float* dgamma, float* dbeta, void* stream) {
+  clear_error();
+  return partition_ln_bwd_impl(dwindows, dwindows_dtype, x, dresidual, dx, x_dtype, geom, gamma, eps, dgamma, dbeta,
+                               stream);
 }

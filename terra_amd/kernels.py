@@ -191,15 +191,20 @@ def swin_partition(x: torch.Tensor, geom: WindowGeometry, pad_value: float = 0.0
 
 def swin_partition_ln(x: torch.Tensor, geom: WindowGeometry, weight: Optional[torch.Tensor],
                       bias: Optional[torch.Tensor], eps: float, pad_value: float = 0.0,
-                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """Fused LayerNorm over C (nn.LayerNorm semantics, fp32 statistics) +
     pad + roll(-shift) + window_partition of ``x`` [B, H, W, C].
 
     Replaces ``norm1`` followed by the roll and partition of
-    models/transformer.py:150-182.  Returns windows ``[B * nW, ws*ws, C]``.
+    models/transformer.py:150-182.  Returns windows ``[B * nW, ws*ws, C]``
+    in ``out_dtype`` (default: x's dtype; bf16 for fp32 x gives the fp32
+    output rounded once, as autocast's cast at the next Linear would).
     """
     dev = _require_device(x)
     code = _dtype_code(x, (torch.float32, torch.float16, torch.bfloat16))
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if out_dtype != x.dtype and not (x.dtype == torch.float32 and out_dtype == torch.bfloat16):
+        raise ValueError(f"out_dtype {out_dtype} for x of {x.dtype}: the mixed form takes fp32 x and bf16 windows")
     if x.dim() != 4 or tuple(x.shape) != (geom.batch, geom.height, geom.width, geom.channels):
         raise ValueError(f"x shape {tuple(x.shape)} does not match geometry "
                          f"{(geom.batch, geom.height, geom.width, geom.channels)}")
@@ -216,15 +221,20 @@ def swin_partition_ln(x: torch.Tensor, geom: WindowGeometry, weight: Optional[to
         params.append(t.detach().to(torch.float32).contiguous())
     shape = (geom.num_windows, geom.window * geom.window, geom.channels)
     if out is None:
-        out = torch.empty(shape, dtype=x.dtype, device=dev)
-    elif tuple(out.shape) != shape or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
-        raise ValueError(f"out must be a contiguous {x.dtype} tensor of shape {shape} on {dev}")
+        out = torch.empty(shape, dtype=out_dtype, device=dev)
+    elif tuple(out.shape) != shape or out.dtype != out_dtype or not out.is_contiguous() or out.device != dev:
+        raise ValueError(f"out must be a contiguous {out_dtype} tensor of shape {shape} on {dev}")
     if geom.batch == 0:
         return out
     c_geom = geom.to_c()
     with torch.cuda.device(dev):
-        st = _lib.load().terra_swin_partition_ln(_ptr(x), _ptr(out), code, ctypes.byref(c_geom), _ptr(params[0]),
-                                                 _ptr(params[1]), float(eps), float(pad_value), _stream(dev))
+        if out_dtype == x.dtype:
+            st = _lib.load().terra_swin_partition_ln(_ptr(x), _ptr(out), code, ctypes.byref(c_geom), _ptr(params[0]),
+                                                     _ptr(params[1]), float(eps), float(pad_value), _stream(dev))
+        else:
+            st = _lib.load().terra_swin_partition_ln_mixed(_ptr(x), code, _ptr(out), _lib.DTYPE_BF16,
+                                                           ctypes.byref(c_geom), _ptr(params[0]), _ptr(params[1]),
+                                                           float(eps), float(pad_value), _stream(dev))
     _lib.check(st, "terra_swin_partition_ln")
     return out
 
@@ -237,17 +247,21 @@ def swin_partition_ln_backward(dwindows: torch.Tensor, x: torch.Tensor, geom: Wi
     given the windows' gradient ``dwindows`` [B * nW, ws*ws, C] (plus
     ``dresidual``, the gradient reaching x by another path, if given).
     ``dweight`` / ``dbias``: fp32 [C] tensors the LayerNorm weight and bias
-    gradients are ADDED into, or None.  ``out`` may be ``dresidual``."""
+    gradients are ADDED into, or None.  ``out`` may be ``dresidual``.
+    ``dwindows`` is in x's dtype, or bf16 for fp32 x (the gradient of the
+    bf16 windows ``swin_partition_ln(..., out_dtype=torch.bfloat16)`` gives,
+    read exactly)."""
     dev = _require_device(dwindows, x)
     code = _dtype_code(x, (torch.float32, torch.float16, torch.bfloat16))
     shape = (geom.batch, geom.height, geom.width, geom.channels)
     if tuple(x.shape) != shape or not x.is_contiguous():
         raise ValueError(f"x must be a contiguous {shape} tensor")
     n = geom.window * geom.window
-    if dwindows.dtype != x.dtype or dwindows.numel() != geom.num_windows * n * geom.channels \
+    mixed = dwindows.dtype == torch.bfloat16 and x.dtype == torch.float32
+    if (dwindows.dtype != x.dtype and not mixed) or dwindows.numel() != geom.num_windows * n * geom.channels \
             or not dwindows.is_contiguous():
-        raise ValueError(f"dwindows must be a contiguous {x.dtype} tensor of {geom.num_windows} x {n} x "
-                         f"{geom.channels} elements")
+        raise ValueError(f"dwindows must be a contiguous {x.dtype} (or, for fp32 x, bf16) tensor of "
+                         f"{geom.num_windows} x {n} x {geom.channels} elements")
     for name, t in (("dresidual", dresidual), ("out", out)):
         if t is not None and (t.dtype != x.dtype or t.numel() != x.numel() or not t.is_contiguous()
                               or t.device != dev):
@@ -268,9 +282,15 @@ def swin_partition_ln_backward(dwindows: torch.Tensor, x: torch.Tensor, geom: Wi
         return out.view(shape)
     c_geom = geom.to_c()
     with torch.cuda.device(dev):
-        st = _lib.load().terra_swin_partition_ln_bwd(_ptr(dwindows), _ptr(x), _ptr(dresidual), _ptr(out), code,
-                                                     ctypes.byref(c_geom), _ptr(w32), float(eps), _ptr(dweight),
-                                                     _ptr(dbias), _stream(dev))
+        if mixed:
+            st = _lib.load().terra_swin_partition_ln_bwd_mixed(_ptr(dwindows), _lib.DTYPE_BF16, _ptr(x),
+                                                               _ptr(dresidual), _ptr(out), code, ctypes.byref(c_geom),
+                                                               _ptr(w32), float(eps), _ptr(dweight), _ptr(dbias),
+                                                               _stream(dev))
+        else:
+            st = _lib.load().terra_swin_partition_ln_bwd(_ptr(dwindows), _ptr(x), _ptr(dresidual), _ptr(out), code,
+                                                         ctypes.byref(c_geom), _ptr(w32), float(eps), _ptr(dweight),
+                                                         _ptr(dbias), _stream(dev))
     _lib.check(st, "terra_swin_partition_ln_bwd")
     return out.view(shape)
 

@@ -223,7 +223,10 @@ class SequentialSwinTransformer(torch.nn.Module):
             # Training: the fused LayerNorm + partition, whose backward kernel
             # also gives the LayerNorm weight and bias gradients.
             n = self.norm1
-            x_windows = autograd.partition_ln(grid, geom, n.weight, n.bias, n.eps)
+            # Under bf16 autocast the q/k/v Linear would cast fp32 windows to
+            # bf16: the kernel writes that bf16 copy itself.
+            x_windows = autograd.partition_ln(grid, geom, n.weight, n.bias, n.eps,
+                                              out_dtype=autograd.linear_input_dtype(grid))
         else:
             if config.use_layernorm:  # a norm layer the gather does not fuse runs on its own
                 grid = self.norm1(grid.view(B, L, C)).contiguous().view(B, H, W, C)

@@ -227,6 +227,25 @@ def test_partition_ln_rejects_bad_arguments():
     assert lib.terra_swin_partition_ln(FAKE, FAKE, L.DTYPE_BF16, ctypes.byref(g), None, None, -1.0, 0.0, None) == -3
 
 
+def test_partition_ln_mixed_rejects_bad_arguments():
+    lib = L.load()
+    g = _geom(channels=8)
+    mixed = lib.terra_swin_partition_ln_mixed
+    # only fp32 x with bf16 windows mixes
+    assert mixed(FAKE, L.DTYPE_BF16, FAKE, L.DTYPE_F32, ctypes.byref(g), None, None, 1e-5, 0.0, None) == -2
+    assert "mixed" in L.last_error()
+    assert mixed(FAKE, L.DTYPE_F32, FAKE, L.DTYPE_F16, ctypes.byref(g), None, None, 1e-5, 0.0, None) == -2
+    assert mixed(None, L.DTYPE_F32, FAKE, L.DTYPE_BF16, ctypes.byref(g), None, None, 1e-5, 0.0, None) == -1
+    assert mixed(FAKE, L.DTYPE_F32, FAKE, L.DTYPE_BF16, ctypes.byref(g), None, None, -1.0, 0.0, None) == -3
+    bwd = lib.terra_swin_partition_ln_bwd_mixed
+    assert bwd(FAKE, L.DTYPE_F32, FAKE, None, FAKE, L.DTYPE_BF16, ctypes.byref(g), None, 1e-5, None, None,
+               None) == -2
+    assert bwd(None, L.DTYPE_BF16, FAKE, None, FAKE, L.DTYPE_F32, ctypes.byref(g), None, 1e-5, None, None,
+               None) == -1
+    assert bwd(FAKE, L.DTYPE_BF16, FAKE, None, FAKE, L.DTYPE_F32, ctypes.byref(g), None, -1.0, None, None,
+               None) == -3
+
+
 def _block_desc(geom_kw=None, **kw):
     d = L.SwinBlockDesc()
     gk = dict(channels=192, window=8)

@@ -209,3 +209,41 @@ def test_block_training_routes_layernorm_through_hip(dev):
         torch.nn.functional.layer_norm = orig_ln
     assert calls["bwd"] == 1 and ln_calls["n"] == 0
     assert blk.norm1.weight.grad is not None and torch.isfinite(blk.norm1.weight.grad.float()).all()
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("residual", [False, True])
+def test_partition_ln_mixed_equals_fp32_and_cast(dev, case, residual):
+    """The mixed-dtype forms (fp32 x, bf16 windows / bf16 windows gradient)
+    that bf16-autocast training uses: the forward equals the fp32 LayerNorm +
+    partition followed by a cast to bf16, and the backward equals the fp32
+    backward on the bf16 gradient cast to fp32, bit for bit (dγ / dβ up to
+    the atomics' summation order)."""
+    B, H, W, C, ws, s, pad, r0, rows, valid = case
+    g = _geom(*case)
+    x = (workloads.activations((B, H, W, C), 510) * 2 + 0.3).to(dev)
+    w = (workloads.activations((C,), 511) * 0.2 + 1.0).to(dev)
+    b = (workloads.activations((C,), 512) * 0.2).to(dev)
+    want = kernels.swin_partition_ln(x, g, w, b, 1e-5, pad_value=0.5).to(torch.bfloat16)
+    got = kernels.swin_partition_ln(x, g, w, b, 1e-5, pad_value=0.5, out_dtype=torch.bfloat16)
+    assert got.dtype == torch.bfloat16
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    gw = workloads.activations((g.num_windows, ws * ws, C), 513).to(torch.bfloat16).to(dev)
+    dres = workloads.activations((B, H, W, C), 514).to(dev) if residual else None
+    dw0, db0 = torch.zeros(C, device=dev), torch.zeros(C, device=dev)
+    dw1, db1 = torch.zeros(C, device=dev), torch.zeros(C, device=dev)
+    want_dx = kernels.swin_partition_ln_backward(gw.float(), x, g, w, 1e-5, dresidual=dres, dweight=dw0, dbias=db0)
+    got_dx = kernels.swin_partition_ln_backward(gw, x, g, w, 1e-5, dresidual=dres, dweight=dw1, dbias=db1)
+    assert got_dx.dtype == torch.float32
+    assert torch.equal(got_dx, want_dx)
+    assert _rel(dw1, dw0) < 1e-5 and _rel(db1, db0) < 1e-5
+
+
+def test_partition_ln_mixed_rejects_other_pairs(dev):
+    g = WindowGeometry(1, 8, 8, 64, 8)
+    x = torch.zeros((1, 8, 8, 64), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        kernels.swin_partition_ln(x, g, None, None, 1e-5, out_dtype=torch.float32)
+    with pytest.raises(ValueError):
+        kernels.swin_partition_ln_backward(torch.zeros((1, 64, 64), dtype=torch.float16, device=dev), x.float(), g,
+                                           None, 1e-5)
