@@ -43,12 +43,24 @@ class _Partition(torch.autograd.Function):
         return kernels.swin_reverse(grad.contiguous(), ctx.geom), None
 
 
+class ResidualLink:
+    """Hands a half-block's output gradient (the residual's gradient) from the
+    scatter's backward to the gather's backward, which adds it into dx in the
+    same kernel instead of autograd summing the two paths in a separate pass.
+    The scatter then takes its residual detached; the gather's backward runs
+    after the scatter's, since the gather's output feeds the scatter."""
+
+    def __init__(self):
+        self.grad: Optional[torch.Tensor] = None
+
+
 class _Reverse(torch.autograd.Function):
     @staticmethod
     def forward(ctx, windows: torch.Tensor, geom: WindowGeometry,
-                residual: Optional[torch.Tensor]) -> torch.Tensor:
+                residual: Optional[torch.Tensor], link: Optional[ResidualLink]) -> torch.Tensor:
         ctx.geom = geom
         ctx.has_residual = residual is not None
+        ctx.link = link
         return kernels.swin_reverse(windows, geom, residual=residual)
 
     @staticmethod
@@ -56,7 +68,10 @@ class _Reverse(torch.autograd.Function):
         grad = grad.contiguous()
         shape = (ctx.geom.batch, ctx.geom.height, ctx.geom.width, ctx.geom.channels)
         d_windows = kernels.swin_partition(grad.view(shape), ctx.geom)
-        return d_windows, None, (grad if ctx.has_residual else None)
+        if ctx.link is not None:
+            ctx.link.grad = grad.view(shape)
+            return d_windows, None, None, None
+        return d_windows, None, (grad if ctx.has_residual else None), None
 
 
 class _PartitionLN(torch.autograd.Function):
@@ -67,8 +82,8 @@ class _PartitionLN(torch.autograd.Function):
     arrives in bf16 (the _mixed entry points)."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, geom, eps, out_dtype):
-        ctx.geom, ctx.eps = geom, eps
+    def forward(ctx, x, weight, bias, geom, eps, out_dtype, link):
+        ctx.geom, ctx.eps, ctx.link = geom, eps, link
         ctx.save_for_backward(x, weight, bias)
         return kernels.swin_partition_ln(x, geom, weight, bias, eps, out_dtype=out_dtype)
 
@@ -80,9 +95,13 @@ class _PartitionLN(torch.autograd.Function):
             dw = torch.zeros(weight.shape, dtype=torch.float32, device=x.device)
         if bias is not None and ctx.needs_input_grad[2]:
             db = torch.zeros(bias.shape, dtype=torch.float32, device=x.device)
-        dx = kernels.swin_partition_ln_backward(grad.contiguous(), x, ctx.geom, weight, ctx.eps, dweight=dw, dbias=db)
+        dres = None
+        if ctx.link is not None and ctx.link.grad is not None:  # the residual's gradient, added in the kernel
+            dres, ctx.link.grad = ctx.link.grad.to(x.dtype).contiguous(), None
+        dx = kernels.swin_partition_ln_backward(grad.contiguous(), x, ctx.geom, weight, ctx.eps, dresidual=dres,
+                                                dweight=dw, dbias=db)
         return (dx, None if dw is None else dw.to(weight.dtype), None if db is None else db.to(bias.dtype), None, None,
-                None)
+                None, None)
 
 
 def linear_input_dtype(x: torch.Tensor) -> torch.dtype:
@@ -92,13 +111,16 @@ def linear_input_dtype(x: torch.Tensor) -> torch.dtype:
 
 
 def partition_ln(x: torch.Tensor, geom: WindowGeometry, weight: Optional[torch.Tensor],
-                 bias: Optional[torch.Tensor], eps: float, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+                 bias: Optional[torch.Tensor], eps: float, out_dtype: Optional[torch.dtype] = None,
+                 link: Optional[ResidualLink] = None) -> torch.Tensor:
     """:func:`kernels.swin_partition_ln` with gradients for x and the
     LayerNorm affine parameters.  ``out_dtype`` bf16 for fp32 x writes the
     bf16 copy a following Linear under bf16 autocast would cast to (and takes
-    its bf16 gradient), instead of fp32 windows and a cast each way."""
+    its bf16 gradient), instead of fp32 windows and a cast each way.
+    ``link``: the :class:`ResidualLink` of a :func:`reverse` whose residual
+    is x; its gradient is then added into dx by this backward's kernel."""
     if _needs_grad(x, weight, bias):
-        return _PartitionLN.apply(x, weight, bias, geom, eps, out_dtype)
+        return _PartitionLN.apply(x, weight, bias, geom, eps, out_dtype, link)
     return kernels.swin_partition_ln(x, geom, weight, bias, eps, out_dtype=out_dtype)
 
 
@@ -223,11 +245,16 @@ def partition(x: torch.Tensor, geom: WindowGeometry) -> torch.Tensor:
     return kernels.swin_partition(x, geom)
 
 
-def reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+def reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional[torch.Tensor] = None,
+            link: Optional[ResidualLink] = None) -> torch.Tensor:
     """:func:`kernels.swin_reverse` with gradients (partition for the windows,
-    identity for the residual)."""
+    identity for the residual).  With ``link`` (the residual is the input of
+    the :func:`partition_ln` holding the same link) the residual's gradient
+    goes through the link instead of autograd."""
+    if link is not None and residual is not None:
+        return _Reverse.apply(windows, geom, residual.detach(), link)
     if _needs_grad(windows, residual):
-        return _Reverse.apply(windows, geom, residual)
+        return _Reverse.apply(windows, geom, residual, None)
     return kernels.swin_reverse(windows, geom, residual=residual)
 
 

@@ -212,6 +212,7 @@ class SequentialSwinTransformer(torch.nn.Module):
         # Training: the partition / reverse permutations and the LayerNorm
         # with their HIP backward kernels.
         training = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+        link = None
         if config.use_layernorm and not training and self._fusable_norm(grid.dtype):
             n = self.norm1
             ln_w, ln_b = n.weight, n.bias
@@ -224,9 +225,12 @@ class SequentialSwinTransformer(torch.nn.Module):
             # also gives the LayerNorm weight and bias gradients.
             n = self.norm1
             # Under bf16 autocast the q/k/v Linear would cast fp32 windows to
-            # bf16: the kernel writes that bf16 copy itself.
+            # bf16: the kernel writes that bf16 copy itself.  When x needs a
+            # gradient, the residual's gradient is added in the LayerNorm
+            # backward's kernel (link).
+            link = autograd.ResidualLink() if training and x.requires_grad else None
             x_windows = autograd.partition_ln(grid, geom, n.weight, n.bias, n.eps,
-                                              out_dtype=autograd.linear_input_dtype(grid))
+                                              out_dtype=autograd.linear_input_dtype(grid), link=link)
         else:
             if config.use_layernorm:  # a norm layer the gather does not fuse runs on its own
                 grid = self.norm1(grid.view(B, L, C)).contiguous().view(B, H, W, C)
@@ -242,6 +246,10 @@ class SequentialSwinTransformer(torch.nn.Module):
         else:
             attn_windows = self.attn(x_windows, mask=self.window_mask(geom))
         out_dtype = torch.promote_types(attn_windows.dtype, shortcut.dtype)
-        y = autograd.reverse(attn_windows.to(out_dtype).contiguous(), geom,
-                             residual=shortcut.to(out_dtype).contiguous().view(B, H, W, C))
+        residual = shortcut.to(out_dtype).contiguous().view(B, H, W, C)
+        # The link carries the residual's gradient only when the residual is
+        # the LayerNorm's input itself (same dtype, no copy in between).
+        link = link if (config.use_layernorm and residual.data_ptr() == grid.data_ptr()
+                        and residual.dtype == grid.dtype) else None
+        y = autograd.reverse(attn_windows.to(out_dtype).contiguous(), geom, residual=residual, link=link)
         return y.view(B, H * W, C)
