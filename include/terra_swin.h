@@ -261,6 +261,40 @@ int terra_swin_partition_ln_bwd_mixed(const void* dwindows, int dwindows_dtype, 
 int terra_swin_reverse(const void* windows, void* y, const void* residual,
                        int dtype, const terra_swin_geom* geom, void* stream);
 
+/* terra_swin_reverse with windows of another dtype than y: bf16 windows into
+ * fp32 y and residual (windows_dtype == dtype is terra_swin_reverse).  Each
+ * bf16 value is widened exactly and added in fp32, bit for bit what
+ * terra_swin_reverse in fp32 on the windows cast to fp32 gives.  Replaces, in
+ * the training step's bf16 autocast region (core/runtime/run_model.py:424-448),
+ * window_reverse + roll of autocast's bf16 proj output (models/attention.py:281,
+ * models/utils.py:41-45, models/transformer.py:246) and the fp32 add
+ * x = shortcut + x (models/transformer.py:296-298), which type promotion makes
+ * fp32.  Needs C % 4 == 0, 16-byte aligned y / residual and 8-byte aligned
+ * windows.  y may alias residual.
+ */
+int terra_swin_reverse_mixed(const void* windows, int windows_dtype, void* y, const void* residual,
+                             int dtype, const terra_swin_geom* geom, void* stream);
+
+/* terra_swin_partition of fp32 x into bf16 windows, each value rounded once
+ * (round to nearest even): bit for bit terra_swin_partition in fp32 followed by
+ * a cast to bf16.  When column_sums is not NULL the call also ADDS, for each
+ * channel, the sum over every window token of the bf16 value written (as
+ * fp32; pad slots count pad_value) into column_sums (fp32 [C]; the caller
+ * zeroes it; float atomics, so the summation order varies).
+ * Replaces, in the training step under bf16 autocast
+ * (core/runtime/run_model.py:362-617, 424-448), the autograd backward of
+ * window_reverse + roll (models/utils.py:41-45, models/transformer.py:246: a
+ * partition of the fp32 grid gradient, pad_value 0), the cast of that gradient
+ * to bf16 at the proj Linear's backward and proj's bias gradient
+ * grad.sum(0) (models/attention.py:281); with an identity frame (window 1,
+ * no shift, x viewed as [1, tokens, 1, C]) the cast of the MLP half's output
+ * gradient at fc2's backward and fc2's bias gradient (models/mlp.py:168).
+ * Needs C % 4 == 0, C <= 1024, 16-byte aligned x and 8-byte aligned windows.
+ */
+int terra_swin_partition_mixed(const void* x, int x_dtype, void* windows, int windows_dtype,
+                               const terra_swin_geom* geom, float pad_value, float* column_sums,
+                               void* stream);
+
 /* Fused per-window multi-head attention core (bf16 or fp32 activations).
  * Replaces  q = q * self.scale                        models/attention.py:256
  *           attn = q @ k.transpose(-2, -1)            models/attention.py:258
@@ -302,6 +336,23 @@ int terra_swin_attn_bwd(const void* q, const void* k, const void* v, const void*
                         const terra_swin_attn_bwd_desc* desc, const float* bias_table,
                         float* dbias_table, const float* explicit_mask,
                         const uint64_t* land_bits, void* stream);
+
+/* terra_swin_attn_bwd that also ADDS the column sums of the dq, dk and dv it
+ * writes (over all windows and tokens, of the bf16 values stored, as fp32)
+ * into dq_sums, dk_sums and dv_sums (fp32 [C] each, or NULL; the caller
+ * zeroes them; float atomics, so the summation order varies): the bias
+ * gradients of the q / k / v Linears (models/attention.py:223-228), which the
+ * training step (core/runtime/run_model.py:362-617) otherwise sums from the
+ * gradients in a separate pass.  bf16 activations and windows of at most 64
+ * tokens (the MFMA tile kernel); other calls return TERRA_ERR_UNSUPPORTED when
+ * a sum is requested.
+ */
+int terra_swin_attn_bwd_sums(const void* q, const void* k, const void* v, const void* dout,
+                             void* dq, void* dk, void* dv, int dtype,
+                             const terra_swin_attn_bwd_desc* desc, const float* bias_table,
+                             float* dbias_table, const float* explicit_mask,
+                             const uint64_t* land_bits, float* dq_sums, float* dk_sums,
+                             float* dv_sums, void* stream);
 
 /* Fused Swin attention half-block (bf16; 8x8 windows with C = 192 and 6 heads,
  * C = 384 and 12, or C = 768 and 12 heads of dim 64; 7x7 windows with C = 128
@@ -413,6 +464,22 @@ int terra_swin_linear_residual(const void* x, const void* residual, void* y,
                                int in_features, int out_features,
                                const void* weight_packed, const float* bias,
                                const terra_swin_geom* geom, void* stream);
+
+/* Backward of the MLP half's activation in the training step
+ * (core/runtime/run_model.py:362-617): for rows x features tensors
+ *   dh = dout * (Phi(h) + h phi(h)),
+ *   Phi(h) = 0.5 (1 + erf(h / sqrt 2)),  phi(h) = exp(-h^2 / 2) / sqrt(2 pi),
+ * computed in fp32 and rounded once to dtype (bf16 or f32), i.e. the autograd
+ * backward of x = self.act(x) (nn.GELU, erf form, models/mlp.py:165) with h =
+ * fc1's output.  When column_sums is not NULL the call also ADDS each column's
+ * sum of the dh values written (as fp32) into column_sums (fp32 [features];
+ * the caller zeroes it; float atomics, so the summation order varies): fc1's
+ * bias gradient grad.sum(0) (models/mlp.py:162).  Needs features * element
+ * size to be a multiple of 16 bytes and at most 8192, 16-byte aligned
+ * tensors, and dh not overlapping dout or h.
+ */
+int terra_swin_gelu_bwd(const void* dout, const void* h, void* dh, int dtype, int64_t rows,
+                        int features, float* column_sums, void* stream);
 
 #ifdef __cplusplus
 }

@@ -51,11 +51,15 @@ EXPORTED_SYMBOLS = (
     "terra_swin_partition_ln_bwd",
     "terra_swin_partition_ln_bwd_mixed",
     "terra_swin_reverse",
+    "terra_swin_reverse_mixed",
+    "terra_swin_partition_mixed",
     "terra_swin_attn_fwd",
     "terra_swin_attn_bwd",
+    "terra_swin_attn_bwd_sums",
     "terra_swin_block_fwd",
     "terra_swin_pack_linear",
     "terra_swin_mlp_fwd",
+    "terra_swin_gelu_bwd",
     "terra_swin_linear",
     "terra_swin_linear_residual",
 )
@@ -200,11 +204,22 @@ def load() -> ctypes.CDLL:
                                                           ctypes.POINTER(SwinGeom), vp, ctypes.c_float, vp, vp, vp]
         lib.terra_swin_reverse.restype = ctypes.c_int
         lib.terra_swin_reverse.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinGeom), vp]
+        lib.terra_swin_gelu_bwd.restype = ctypes.c_int
+        lib.terra_swin_gelu_bwd.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int, vp, vp]
+        lib.terra_swin_reverse_mixed.restype = ctypes.c_int
+        lib.terra_swin_reverse_mixed.argtypes = [vp, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.POINTER(SwinGeom),
+                                                 vp]
+        lib.terra_swin_partition_mixed.restype = ctypes.c_int
+        lib.terra_swin_partition_mixed.argtypes = [vp, ctypes.c_int, vp, ctypes.c_int, ctypes.POINTER(SwinGeom),
+                                                   ctypes.c_float, vp, vp]
         lib.terra_swin_attn_fwd.restype = ctypes.c_int
         lib.terra_swin_attn_fwd.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinAttnDesc), vp, vp, vp, vp]
         lib.terra_swin_attn_bwd.restype = ctypes.c_int
         lib.terra_swin_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.POINTER(SwinAttnBwdDesc),
                                             vp, vp, vp, vp, vp]
+        lib.terra_swin_attn_bwd_sums.restype = ctypes.c_int
+        lib.terra_swin_attn_bwd_sums.argtypes = [vp, vp, vp, vp, vp, vp, vp, ctypes.c_int,
+                                                 ctypes.POINTER(SwinAttnBwdDesc), vp, vp, vp, vp, vp, vp, vp, vp]
         lib.terra_swin_block_fwd.restype = ctypes.c_int
         lib.terra_swin_block_fwd.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(SwinBlockDesc), vp, vp, vp, vp, vp,
                                              vp, vp, vp, vp]

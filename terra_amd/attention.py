@@ -100,14 +100,16 @@ class WindowAttention(torch.nn.Module):
         cache[name] = (key, val)
         return val
 
-    def qkv(self, x: torch.Tensor) -> torch.Tensor:
-        """The three projections as one GEMM: [B_, N, C] -> [B_, N, 3C]."""
+    def qkv(self, x: torch.Tensor, bias_sums: Optional[autograd.ColumnSumLink] = None) -> torch.Tensor:
+        """The three projections as one GEMM: [B_, N, C] -> [B_, N, 3C].
+        ``bias_sums``: a link the attention core's backward fills with the
+        bias gradient (see :meth:`attend`)."""
         lins = (self.q_linear, self.k_linear, self.v_linear)
         has_bias = self.q_linear.bias is not None
         if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
             w = torch.cat([l.weight for l in lins], 0)
             b = torch.cat([l.bias for l in lins], 0) if has_bias else None
-            return autograd.linear(x, w, b)
+            return autograd.linear(x, w, b, bias_sums=bias_sums)
         else:  # the concatenated weights, kept until a parameter changes
             w, b = self._cached("qkv", [l.weight for l in lins] + [l.bias for l in lins], lambda: (
                 torch.cat([l.weight for l in lins], 0), torch.cat([l.bias for l in lins], 0) if has_bias else None))
@@ -132,9 +134,12 @@ class WindowAttention(torch.nn.Module):
 
     def attend(self, x: torch.Tensor, mask=None) -> torch.Tensor:
         """Everything of forward but the output projection: q/k/v and the
-        fused core, O [B_, N, C] (models/attention.py:244-278)."""
-        return autograd.window_attention_qkv(self.qkv(x), self.num_heads, self.window_size, self.scale,
-                                             bias_table=self._table(), mask=mask)
+        fused core, O [B_, N, C] (models/attention.py:244-278).  In training
+        the core's backward kernel also sums the q | k | v gradient's columns,
+        which the projection's backward takes as its bias gradient."""
+        link = autograd.ColumnSumLink() if torch.is_grad_enabled() else None
+        return autograd.window_attention_qkv(self.qkv(x, bias_sums=link), self.num_heads, self.window_size,
+                                             self.scale, bias_table=self._table(), mask=mask, bias_sums=link)
 
     def forward(self, x: torch.Tensor, mask=None) -> torch.Tensor:
         return autograd.linear(self.attend(x, mask=mask), self.proj.weight, self.proj.bias)

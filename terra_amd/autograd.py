@@ -54,24 +54,48 @@ class ResidualLink:
         self.grad: Optional[torch.Tensor] = None
 
 
+class ColumnSumLink:
+    """Hands the column sums of a Linear's output gradient (its bias gradient)
+    from the backward that produces that gradient, which sums it in the same
+    kernel, to the Linear's backward, which then skips its own reduction."""
+
+    def __init__(self):
+        self.sums: Optional[torch.Tensor] = None
+
+
 class _Reverse(torch.autograd.Function):
+    """Window reverse + roll + residual.  With bf16 windows and an fp32
+    output (autocast's bf16 proj output added to an fp32 shortcut) the kernel
+    widens the windows itself, and the backward writes the windows' gradient
+    in bf16 (what the cast's backward gives), with the column sums a
+    :class:`ColumnSumLink` hands to the producing Linear's bias gradient."""
+
     @staticmethod
-    def forward(ctx, windows: torch.Tensor, geom: WindowGeometry,
-                residual: Optional[torch.Tensor], link: Optional[ResidualLink]) -> torch.Tensor:
+    def forward(ctx, windows: torch.Tensor, geom: WindowGeometry, residual: Optional[torch.Tensor],
+                link: Optional[ResidualLink], out_dtype: Optional[torch.dtype],
+                bias_sums: Optional[ColumnSumLink]) -> torch.Tensor:
         ctx.geom = geom
         ctx.has_residual = residual is not None
-        ctx.link = link
-        return kernels.swin_reverse(windows, geom, residual=residual)
+        ctx.link, ctx.bias_sums = link, bias_sums
+        ctx.win_dtype = windows.dtype
+        return kernels.swin_reverse(windows, geom, residual=residual, out_dtype=out_dtype)
 
     @staticmethod
     def backward(ctx, grad: torch.Tensor):
         grad = grad.contiguous()
         shape = (ctx.geom.batch, ctx.geom.height, ctx.geom.width, ctx.geom.channels)
-        d_windows = kernels.swin_partition(grad.view(shape), ctx.geom)
+        if ctx.win_dtype != grad.dtype:  # bf16 windows, fp32 output
+            sums = None
+            if ctx.bias_sums is not None:
+                sums = torch.zeros(ctx.geom.channels, dtype=torch.float32, device=grad.device)
+                ctx.bias_sums.sums = sums
+            d_windows = kernels.swin_partition(grad.view(shape), ctx.geom, out_dtype=ctx.win_dtype, column_sums=sums)
+        else:
+            d_windows = kernels.swin_partition(grad.view(shape), ctx.geom)
         if ctx.link is not None:
             ctx.link.grad = grad.view(shape)
-            return d_windows, None, None, None
-        return d_windows, None, (grad if ctx.has_residual else None), None
+            return d_windows, None, None, None, None, None
+        return d_windows, None, (grad if ctx.has_residual else None), None, None, None
 
 
 class _PartitionLN(torch.autograd.Function):
@@ -146,16 +170,19 @@ def weight_grad(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
 class _Linear(torch.autograd.Function):
     """F.linear for training, in the dtype bf16 autocast gives it (x, weight
     and bias cast to bf16 inside an autocast region, as F.linear's autocast
-    rule does), with the weight gradient from :func:`weight_grad`."""
+    rule does), with the weight gradient from :func:`weight_grad`.  The bias
+    gradient comes from a :class:`ColumnSumLink` when the output gradient's
+    producer summed it (in the order of its own kernel), else from a sum."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias):
+    def forward(ctx, x, weight, bias, bias_sums):
         dt = torch.bfloat16 if (torch.is_autocast_enabled(x.device.type)
                                 and torch.get_autocast_dtype(x.device.type) == torch.bfloat16) else x.dtype
         xc, wc = x.to(dt), weight.to(dt)
         bc = None if bias is None else bias.to(dt)
         ctx.save_for_backward(xc, wc)
         ctx.dtypes = (x.dtype, weight.dtype, None if bias is None else bias.dtype)
+        ctx.bias_sums = bias_sums
         return torch.nn.functional.linear(xc, wc, bc)
 
     @staticmethod
@@ -168,15 +195,21 @@ class _Linear(torch.autograd.Function):
             dx = (dy2 @ wc).view(xc.shape).to(xd)
         if ctx.needs_input_grad[1]:
             dw = weight_grad(dy2, xc.reshape(-1, xc.shape[-1])).to(wd)
+        sums = None
+        if ctx.bias_sums is not None:
+            sums, ctx.bias_sums.sums = ctx.bias_sums.sums, None
         if bd is not None and ctx.needs_input_grad[2]:
-            db = dy2.sum(0, dtype=torch.float32).to(bd)
-        return dx, dw, db
+            db = (sums if sums is not None and dy.dtype == wc.dtype else dy2.sum(0, dtype=torch.float32)).to(bd)
+        return dx, dw, db, None
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
-    """F.linear, through :class:`_Linear` when a gradient is needed."""
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+           bias_sums: Optional[ColumnSumLink] = None) -> torch.Tensor:
+    """F.linear, through :class:`_Linear` when a gradient is needed.
+    ``bias_sums``: a :class:`ColumnSumLink` the backward of the output's
+    consumer fills with the output gradient's column sums."""
     if _needs_grad(x, weight, bias):
-        return _Linear.apply(x, weight, bias)
+        return _Linear.apply(x, weight, bias, bias_sums)
     return torch.nn.functional.linear(x, weight, bias)
 
 
@@ -186,7 +219,10 @@ class _Mlp(torch.autograd.Function):
     backward (with the residual gradient added in the same kernel) run on
     terra_swin_partition_ln / _bwd over the token rows; the four GEMMs of
     the backward on hipBLASLt through torch, in the dtypes autocast gave the
-    forward's GEMMs; the GELU derivative is the exact (erf) one."""
+    forward's GEMMs.  The GELU derivative (the exact, erf one) runs on
+    terra_swin_gelu_bwd with fc1's bias gradient summed in the same pass;
+    under autocast the output gradient's cast to bf16 sums fc2's bias
+    gradient in its pass (terra_swin_partition_mixed over the token rows)."""
 
     @staticmethod
     def forward(ctx, x, ln_w, ln_b, w1, b1, w2, b2, eps):
@@ -212,15 +248,32 @@ class _Mlp(torch.autograd.Function):
         C = rows.shape[-1]
         dy = dy.reshape(-1, dy.shape[-1])
         gemm_dtype = h1.dtype  # the forward GEMMs' dtype (bf16 under autocast)
-        dh2 = dy.to(gemm_dtype)
+        T, c_out = dy.shape
+        db2 = None
+        if dy.dtype == torch.float32 and gemm_dtype == torch.bfloat16 and c_out % 4 == 0 and c_out <= 1024:
+            # The cast to the GEMMs' bf16 and fc2's bias gradient (the column
+            # sums of the bf16 values) in one pass over the token rows.
+            if ctx.needs_input_grad[6]:
+                db2 = torch.zeros(c_out, dtype=torch.float32, device=dy.device)
+            dh2 = kernels.swin_partition(dy.contiguous().view(1, T, 1, c_out), kernels.rows_geometry(T, c_out),
+                                         out_dtype=torch.bfloat16, column_sums=db2).view(T, c_out)
+        else:
+            dh2 = dy.to(gemm_dtype)
+            db2 = dh2.sum(0, dtype=torch.float32) if ctx.needs_input_grad[6] else None
         w2c, w1c = w2.to(gemm_dtype), w1.to(gemm_dtype)
         da = dh2 @ w2c
         dw2 = weight_grad(dh2, a.to(gemm_dtype)) if ctx.needs_input_grad[5] else None
-        db2 = dh2.sum(0, dtype=torch.float32) if ctx.needs_input_grad[6] else None
-        dh1 = torch.ops.aten.gelu_backward(da, h1)
+        db1 = None
+        if kernels.gelu_backward_supported(h1):
+            # The GELU derivative and fc1's bias gradient in one pass.
+            if ctx.needs_input_grad[4]:
+                db1 = torch.zeros(h1.shape[-1], dtype=torch.float32, device=h1.device)
+            dh1 = kernels.gelu_backward(da.contiguous(), h1.contiguous(), column_sums=db1)
+        else:
+            dh1 = torch.ops.aten.gelu_backward(da, h1)
+            db1 = dh1.sum(0, dtype=torch.float32) if ctx.needs_input_grad[4] else None
         dxn = dh1 @ w1c
         dw1 = weight_grad(dh1, xn.to(gemm_dtype)) if ctx.needs_input_grad[3] else None
-        db1 = dh1.sum(0, dtype=torch.float32) if ctx.needs_input_grad[4] else None
         dlw = torch.zeros(C, dtype=torch.float32, device=rows.device) if (
             ln_w is not None and ctx.needs_input_grad[1]) else None
         dlb = torch.zeros(C, dtype=torch.float32, device=rows.device) if (
@@ -248,16 +301,24 @@ def partition(x: torch.Tensor, geom: WindowGeometry) -> torch.Tensor:
 
 
 def reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional[torch.Tensor] = None,
-            link: Optional[ResidualLink] = None) -> torch.Tensor:
+            link: Optional[ResidualLink] = None, out_dtype: Optional[torch.dtype] = None,
+            bias_sums: Optional[ColumnSumLink] = None) -> torch.Tensor:
     """:func:`kernels.swin_reverse` with gradients (partition for the windows,
-    identity for the residual).  With ``link`` (the residual is the input of
-    the :func:`partition_ln` holding the same link) the residual's gradient
-    goes through the link instead of autograd."""
+    identity for the residual), in ``out_dtype`` (default: the windows'
+    dtype; bf16 windows into fp32 are widened by the kernel, other pairs by a
+    cast first).  With ``link`` (the residual is the input of the
+    :func:`partition_ln` holding the same link) the residual's gradient goes
+    through the link instead of autograd.  ``bias_sums``: the
+    :class:`ColumnSumLink` of the :func:`linear` whose output the windows are;
+    the bf16 backward fills it."""
+    odt = windows.dtype if out_dtype is None else out_dtype
+    if odt != windows.dtype and not (windows.dtype == torch.bfloat16 and odt == torch.float32):
+        windows = windows.to(odt)
     if link is not None and residual is not None:
-        return _Reverse.apply(windows, geom, residual.detach(), link)
+        return _Reverse.apply(windows, geom, residual.detach(), link, odt, bias_sums)
     if _needs_grad(windows, residual):
-        return _Reverse.apply(windows, geom, residual, None)
-    return kernels.swin_reverse(windows, geom, residual=residual)
+        return _Reverse.apply(windows, geom, residual, None, odt, bias_sums)
+    return kernels.swin_reverse(windows, geom, residual=residual, out_dtype=odt)
 
 
 def _check_backward(q: torch.Tensor, num_heads: int, window_size: Tuple[int, int], n_real: Optional[int]) -> None:
@@ -297,12 +358,15 @@ class _Attention(torch.autograd.Function):
 class _AttentionQKV(torch.autograd.Function):
     """One [B_, N, 3C] projection output as input: the gradients of q, k and v
     are written into one [B_, N, 3C] buffer (the input of the projection's
-    backward GEMM), with no slice copies."""
+    backward GEMM), with no slice copies.  With a :class:`ColumnSumLink` the
+    bf16 kernel also sums that buffer's columns (the projection's bias
+    gradient) while it writes it."""
 
     @staticmethod
-    def forward(ctx, qkv, table, num_heads, window_size, scale, mask, n_real, mask_value):
+    def forward(ctx, qkv, table, num_heads, window_size, scale, mask, n_real, mask_value, bias_sums):
         C = qkv.shape[-1] // 3
         ctx.cfg = (num_heads, window_size, scale, mask, n_real, mask_value)
+        ctx.bias_sums = bias_sums
         ctx.save_for_backward(qkv, table)
         return kernels.window_attention(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], num_heads, window_size,
                                         scale, bias_table=table, mask=mask, n_real=n_real, mask_value=mask_value)
@@ -317,12 +381,17 @@ class _AttentionQKV(torch.autograd.Function):
         dbias = None
         if table is not None and ctx.needs_input_grad[1]:
             dbias = torch.zeros(table.shape, dtype=torch.float32, device=table.device)
+        sums = None
+        if ctx.bias_sums is not None and kernels.attention_backward_sums_supported(qkv[..., :C], num_heads,
+                                                                                   window_size, n_real):
+            sums = torch.zeros(3 * C, dtype=torch.float32, device=qkv.device)
+            ctx.bias_sums.sums = sums
         kernels.window_attention_backward(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], grad.contiguous(),
                                           num_heads, window_size, scale, bias_table=table, mask=mask, n_real=n_real,
                                           mask_value=mask_value, dq=dqkv[..., :C], dk=dqkv[..., C:2 * C],
-                                          dv=dqkv[..., 2 * C:], dbias=dbias)
+                                          dv=dqkv[..., 2 * C:], dbias=dbias, column_sums=sums)
         dtable = None if dbias is None else dbias.to(table.dtype)
-        return dqkv, dtable, None, None, None, None, None, None
+        return dqkv, dtable, None, None, None, None, None, None, None
 
 
 def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
@@ -339,13 +408,16 @@ def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_head
 
 def window_attention_qkv(qkv: torch.Tensor, num_heads: int, window_size: Tuple[int, int], scale: float,
                          bias_table: Optional[torch.Tensor] = None, mask: MaskArg = None,
-                         n_real: Optional[int] = None, mask_value: float = kernels.MASK_VALUE) -> torch.Tensor:
+                         n_real: Optional[int] = None, mask_value: float = kernels.MASK_VALUE,
+                         bias_sums: Optional[ColumnSumLink] = None) -> torch.Tensor:
     """Attention over the column blocks q | k | v of one [B_, N, 3C] tensor,
-    with gradients (see :class:`_AttentionQKV`)."""
+    with gradients (see :class:`_AttentionQKV`).  ``bias_sums``: the
+    :class:`ColumnSumLink` of the :func:`linear` that produced ``qkv``."""
     C = qkv.shape[-1] // 3
     if _needs_grad(qkv, bias_table):
         if not qkv.is_contiguous():
             qkv = qkv.contiguous()
-        return _AttentionQKV.apply(qkv, bias_table, num_heads, tuple(window_size), scale, mask, n_real, mask_value)
+        return _AttentionQKV.apply(qkv, bias_table, num_heads, tuple(window_size), scale, mask, n_real, mask_value,
+                                   bias_sums)
     return kernels.window_attention(qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:], num_heads, window_size,
                                     scale, bias_table=bias_table, mask=mask, n_real=n_real, mask_value=mask_value)

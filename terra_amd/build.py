@@ -16,7 +16,7 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 SOURCES = ("abi.hip", "window_copy.hip", "window_attention.hip", "window_attention_bwd.hip", "swin_block.hip",
-           "swin_mlp.hip", "linear.hip")
+           "swin_mlp.hip", "linear.hip", "mlp_backward.hip")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -43,6 +43,7 @@ struct BwdParams {
   void* dv;
   int64_t dq_stride, dk_stride, dv_stride;
   float* dbias;         // fp32 [table_size, heads], accumulated; NULL: not wanted
+  float* dsum[3];       // fp32 [C] column sums of dq, dk, dv, accumulated; NULL: not wanted
   float scale;          // natural q k^T scale
   float mask_value;     // natural-unit mask and padded-key values (generic kernel)
   float pad_key_value;
@@ -105,6 +106,8 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
   uint8_t* pz = smem + 4 * tile_bytes;           // per head: P tile, then dz tile
   float* tables = reinterpret_cast<float*>(pz + 2 * G * kBwdTile);  // G bias columns (x log2e)
   float* dtab = tables + G * kTableMax;          // G bias-gradient columns
+  float* csum = dtab + G * kTableMax;            // column sums of dq | dk | dv (G * D each)
+  const bool sums = bp.dsum[0] != nullptr || bp.dsum[1] != nullptr || bp.dsum[2] != nullptr;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -129,6 +132,7 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
       dtab[head * kTableMax + e] = 0.f;
     }
   }
+  for (int e = tid; e < 3 * G * D; e += nthreads) csum[e] = 0.f;  // read after the loop's first barrier
 
   constexpr int kPer = kNPad * cpr / nthreads;   // chunks per thread per tensor
   constexpr int kRowStep = nthreads / cpr;
@@ -352,16 +356,40 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
           stream_store_nt(val, out, (uint32_t)(row * stride[t] + col) * 2);
         }
       }
+      // The unit's column sums of the bf16 values stored (the q / k / v
+      // Linear's bias gradient), as MFMAs of a ones operand with 16-column
+      // tiles read across the rows: every output row of ones^T T is the
+      // column sum.  Rows the window does not store are zeros in the tiles.
+      // Each wave takes whole column tiles, so its 16 sums go to LDS words no
+      // other wave adds to in this unit.
+      if (sums) {
+        constexpr int kColTiles = G * D / 16;
+        bf16x8 ones;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
+        for (int ti = wave; ti < 3 * kColTiles; ti += nthreads / 64) {
+          const int t = ti / kColTiles, col0 = 16 * (ti - t * kColTiles);
+          if (bp.dsum[t] == nullptr) continue;  // uniform
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int js = 0; js < 2; ++js)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, rows_frag<false>(src[t], lcpr, col0, js, lane), acc,
+                                                          0, 0, 0);
+          if (g == 0) atomicAdd(&csum[t * G * D + col0 + c16], acc[0]);
+        }
+      }
     }
     if (next >= units) break;
     unit = next;
   }
 
   // ---- bias gradient: registers -> LDS column -> global table ----------------
-  if (bp.dbias == nullptr) return;  // uniform
+  if (bp.dbias == nullptr && !sums) return;  // uniform
   // Lane element (il, jt, r) is the pair (query 16(2half+il) + c16, key 16jt + 4g + r).
   float* dcol = dtab + head * kTableMax;
-  if constexpr (kWs8) {
+  if (bp.dbias == nullptr) {
+    // column sums only
+  } else if constexpr (kWs8) {
     // relative index lane_base + 30*(it - jt) - r
     const int lane_base = 15 * ((c16 >> 3) - (g >> 1) + 7) + (c16 & 7) - 4 * (g & 1) + 7;
 #pragma unroll
@@ -389,15 +417,24 @@ __global__ __launch_bounds__(G * 128) void window_attn_bwd_kernel(const BwdParam
     }
   }
   lds_barrier();
-  for (int e = tid; e < G * p.table_size; e += nthreads) {
-    const int hh = e / p.table_size, idx = e - hh * p.table_size;
-    unsafeAtomicAdd(bp.dbias + (int64_t)idx * p.heads + hg * G + hh, dtab[hh * kTableMax + idx]);
+  if (bp.dbias != nullptr) {
+    for (int e = tid; e < G * p.table_size; e += nthreads) {
+      const int hh = e / p.table_size, idx = e - hh * p.table_size;
+      unsafeAtomicAdd(bp.dbias + (int64_t)idx * p.heads + hg * G + hh, dtab[hh * kTableMax + idx]);
+    }
+  }
+  if (sums) {
+    for (int e = tid; e < 3 * G * D; e += nthreads) {
+      const int t = e / (G * D);
+      if (bp.dsum[t] != nullptr) unsafeAtomicAdd(bp.dsum[t] + hg * G * D + (e - t * G * D), csum[e]);
+    }
   }
 }
 
 template <int D, int G>
 constexpr int bwd_lds_bytes() {
-  return 4 * kNPad * bwd_tile_cpr(G, D) * 16 + 2 * G * kBwdTile + 2 * G * kTableMax * (int)sizeof(float);
+  return 4 * kNPad * bwd_tile_cpr(G, D) * 16 + 2 * G * kBwdTile + 2 * G * kTableMax * (int)sizeof(float) +
+         3 * G * D * (int)sizeof(float);
 }
 
 template <int D, int G, bool kExplicit, bool kWs8>
@@ -619,11 +656,16 @@ int launch_bwd_generic(const BwdParams& bp, hipStream_t s) {
 
 using namespace terra;
 
-extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, const void* dout, void* dq,
-                                   void* dk, void* dv, int dtype, const terra_swin_attn_bwd_desc* desc,
-                                   const float* bias_table, float* dbias_table, const float* explicit_mask,
-                                   const uint64_t* land_bits, void* stream) {
-  clear_error();
+namespace {
+
+// terra_swin_attn_bwd, with the column sums of dq / dk / dv (dsum[t], C
+// floats each, accumulated; NULL: not wanted) from the bf16 tile kernel.
+int attn_bwd_impl(const void* q, const void* k, const void* v, const void* dout, void* dq, void* dk, void* dv,
+                  int dtype, const terra_swin_attn_bwd_desc* desc, const float* bias_table, float* dbias_table,
+                  const float* explicit_mask, const uint64_t* land_bits, float* const dsum[3], void* stream) {
+  const bool sums = dsum[0] != nullptr || dsum[1] != nullptr || dsum[2] != nullptr;
+  for (int t = 0; t < 3; ++t)
+    if (((uintptr_t)dsum[t] & 3u) != 0) return fail(TERRA_ERR_ALIGN, "column sums must be 4-byte aligned");
   if (desc == nullptr) return fail(TERRA_ERR_NULL, "desc is NULL");
   if (q == nullptr || k == nullptr || v == nullptr || dout == nullptr || dq == nullptr || dk == nullptr ||
       dv == nullptr)
@@ -633,6 +675,9 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   const terra_swin_attn_desc& d = desc->fwd;
   if (d.num_windows <= 0 || d.tokens <= 0 || d.heads <= 0 || d.channels <= 0)
     return fail(TERRA_ERR_SHAPE, "num_windows/tokens/channels/heads must be positive");
+  if (sums && (dtype != TERRA_DTYPE_BF16 || d.tokens > kNPad))
+    return fail(TERRA_ERR_UNSUPPORTED,
+                "column sums of dq / dk / dv come from the bf16 kernel for windows of at most %d tokens", kNPad);
   if (d.tokens > kNPad)
     return flash_attention_backward(q, k, v, dout, dq, dk, dv, dtype, desc, bias_table, dbias_table, explicit_mask,
                                     land_bits, stream);
@@ -713,6 +758,7 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   bp.dq = dq; bp.dk = dk; bp.dv = dv;
   bp.dq_stride = desc->dq_stride; bp.dk_stride = desc->dk_stride; bp.dv_stride = desc->dv_stride;
   bp.dbias = dbias_table;
+  for (int t = 0; t < 3; ++t) bp.dsum[t] = dsum[t];
   bp.scale = d.scale;
   bp.mask_value = d.mask_value;
   bp.pad_key_value = d.pad_key_value;
@@ -741,4 +787,27 @@ extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, 
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TERRA_ERR_LAUNCH, "terra_swin_attn_bwd launch failed: %s", hipGetErrorString(e));
   return TERRA_OK;
+}
+
+}  // namespace
+
+extern "C" int terra_swin_attn_bwd(const void* q, const void* k, const void* v, const void* dout, void* dq,
+                                   void* dk, void* dv, int dtype, const terra_swin_attn_bwd_desc* desc,
+                                   const float* bias_table, float* dbias_table, const float* explicit_mask,
+                                   const uint64_t* land_bits, void* stream) {
+  clear_error();
+  float* const none[3] = {nullptr, nullptr, nullptr};
+  return attn_bwd_impl(q, k, v, dout, dq, dk, dv, dtype, desc, bias_table, dbias_table, explicit_mask, land_bits,
+                       none, stream);
+}
+
+extern "C" int terra_swin_attn_bwd_sums(const void* q, const void* k, const void* v, const void* dout, void* dq,
+                                        void* dk, void* dv, int dtype, const terra_swin_attn_bwd_desc* desc,
+                                        const float* bias_table, float* dbias_table, const float* explicit_mask,
+                                        const uint64_t* land_bits, float* dq_sums, float* dk_sums, float* dv_sums,
+                                        void* stream) {
+  clear_error();
+  float* const sums[3] = {dq_sums, dk_sums, dv_sums};
+  return attn_bwd_impl(q, k, v, dout, dq, dk, dv, dtype, desc, bias_table, dbias_table, explicit_mask, land_bits,
+                       sums, stream);
 }

@@ -391,8 +391,13 @@ __global__ __launch_bounds__(kThreads) void partition_ln_bwd_kernel(const uint8_
 #pragma unroll
     for (int e = 0; e < E; ++e) acc_g[k][e] = acc_b[k][e] = 0.f;
 
-  for (uint32_t tok = blockIdx.x * kTokensPerPass + threadIdx.x / kL; tok < ln.tokens;
-       tok += gridDim.x * kTokensPerPass) {  // uniform per lane group
+  // Passes of kTokensPerPass tokens: `first` is uniform over the workgroup,
+  // so dx's buffer descriptor is one scalar value per pass (a descriptor
+  // built from each lane group's own token is not, and every store then
+  // became a loop over the wave's distinct descriptors).
+  for (uint32_t first = blockIdx.x * kTokensPerPass; first < ln.tokens; first += gridDim.x * kTokensPerPass) {
+    const uint32_t tok = first + threadIdx.x / kL;
+    if (tok >= ln.tokens) continue;  // uniform per lane group
     uint32_t rest, sw, b, sh;
     g.fd_W.divmod(tok, rest, sw);
     g.fd_H.divmod(rest, b, sh);
@@ -476,7 +481,10 @@ __global__ __launch_bounds__(kThreads) void partition_ln_bwd_kernel(const uint8_
     }
     s1 = group_sum<kL>(s1) * ln.inv_c;
     s2 = group_sum<kL>(s2) * ln.inv_c;
-    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(dx + (int64_t)tok * g.row_bytes, (uint32_t)g.row_bytes);
+    const __amdgpu_buffer_rsrc_t out =
+        buffer_rsrc(dx + (int64_t)first * g.row_bytes,
+                    (uint32_t)(min(ln.tokens - first, (uint32_t)kTokensPerPass) * g.row_bytes));
+    const uint32_t row_off = (tok - first) * (uint32_t)g.row_bytes;
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
       const int c = sub + kL * k;
@@ -490,7 +498,7 @@ __global__ __launch_bounds__(kThreads) void partition_ln_bwd_kernel(const uint8_
 #pragma unroll
         for (int e = 0; e < E; ++e) y[e] += r[e];
       }
-      stream_store_sc1(pack_chunk<DT>(y), out, (uint32_t)c * 16);
+      stream_store_sc1(pack_chunk<DT>(y), out, row_off + (uint32_t)c * 16);
     }
   }
   if (ln.dgamma == nullptr && ln.dbeta == nullptr) return;  // uniform
@@ -508,6 +516,104 @@ __global__ __launch_bounds__(kThreads) void partition_ln_bwd_kernel(const uint8_
   for (int c = threadIdx.x; c < C; c += kThreads) {
     if (ln.dgamma != nullptr) unsafeAtomicAdd(ln.dgamma + c, s_dg[c]);
     if (ln.dbeta != nullptr) unsafeAtomicAdd(ln.dbeta + c, s_db[c]);
+  }
+}
+
+// ---- fp32 rows -> bf16 windows: pad + roll + partition + cast --------------
+// The backward of reverse under bf16 autocast: the fp32 gradient of the grid
+// gathered into windows and rounded once to bf16 (bit-identical to
+// partition_kernel in fp32 followed by a cast), with (kSum) the column sums of
+// the bf16 values written, i.e. the bias gradient of the Linear whose output
+// the windows are.  kL lanes own one destination token, lane `sub` holding
+// chunks sub, sub + kL, ... of its fp32 row, as in partition_ln_kernel.
+// Workgroups loop over the tokens in passes (grid-stride, the resident
+// count), so each lane keeps its channels' sums in registers; at the end each
+// workgroup reduces them in LDS and adds them to the output with one float
+// atomic per channel.
+struct CastParams {
+  float* colsum;    // C floats, accumulated (kSum)
+  int32_t chunks;   // 16-byte fp32 chunks per token row
+  uint32_t tokens;  // destination (window) tokens
+};
+
+template <int CPL, int kL, bool kSum>
+__global__ __launch_bounds__(kThreads) void partition_cast_kernel(const uint8_t* __restrict__ x,
+                                                                  uint8_t* __restrict__ win, const CopyGeom g,
+                                                                  const CastParams cp) {
+  constexpr int kTokensPerPass = kThreads / kL;
+  constexpr int kMaxC = CPL * kL * 4;
+  __shared__ float s_sum[kSum ? kMaxC : 1];
+  if constexpr (kSum) {
+    for (int c = threadIdx.x; c < kMaxC; c += kThreads) s_sum[c] = 0.f;
+    __syncthreads();
+  }
+  const int sub = threadIdx.x & (kL - 1);
+  float acc[CPL][4];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[k][e] = 0.f;
+
+  for (uint32_t first = blockIdx.x * kTokensPerPass; first < cp.tokens; first += gridDim.x * kTokensPerPass) {
+    const uint32_t tok = first + threadIdx.x / kL;
+    if (tok >= cp.tokens) continue;  // uniform per lane group
+    uint32_t w, t, b, wl, wr, wc, ti, tj;
+    g.fd_N.divmod(tok, w, t);
+    g.fd_nWe.divmod(w, b, wl);
+    g.fd_nWw.divmod(wl, wr, wc);
+    g.fd_ws.divmod(t, ti, tj);
+    const bool valid = g.valid_end <= 0 || ((int)wl >= g.valid_begin && (int)wl < g.valid_end);
+    int ph = (int)((wr + g.win_row_begin) * g.ws + ti) + g.shift_h;
+    int pw = (int)(wc * g.ws + tj) + g.shift_w;
+    if (ph >= g.Hp) ph -= g.Hp;
+    if (pw >= g.Wp) pw -= g.Wp;
+    const int sh = ph - g.pad_top;
+    const int sw = pw - g.pad_left;
+    const bool in = valid && (unsigned)sh < (unsigned)g.H && (unsigned)sw < (unsigned)g.W;
+    const u32x4* src =
+        reinterpret_cast<const u32x4*>(x + (in ? (((int64_t)b * g.H + sh) * g.W + sw) * g.row_bytes : 0));
+    // Unconditional loads: absent chunks read chunk 0 of x and are not used.
+    u32x4 raw[CPL];
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = sub + kL * k;
+      raw[k] = __builtin_nontemporal_load((in && c < cp.chunks) ? src + c : reinterpret_cast<const u32x4*>(x));
+    }
+    // One descriptor per pass (uniform over the workgroup).
+    const __amdgpu_buffer_rsrc_t out =
+        buffer_rsrc(win + (int64_t)first * g.win_row_bytes,
+                    (uint32_t)(min(cp.tokens - first, (uint32_t)kTokensPerPass) * g.win_row_bytes));
+    const uint32_t row_off = (tok - first) * (uint32_t)g.win_row_bytes;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = sub + kL * k;
+      if (c >= cp.chunks) continue;
+      u32x2 val = u32x2(g.pad_pattern);
+      if (in) {
+        val[0] = f32_to_bf16_bits(__uint_as_float(raw[k][0])) |
+                 ((uint32_t)f32_to_bf16_bits(__uint_as_float(raw[k][1])) << 16);
+        val[1] = f32_to_bf16_bits(__uint_as_float(raw[k][2])) |
+                 ((uint32_t)f32_to_bf16_bits(__uint_as_float(raw[k][3])) << 16);
+      }
+      stream_store_sc1(val, out, row_off + (uint32_t)c * 8);
+      if constexpr (kSum) {  // the values as written
+        acc[k][0] += __uint_as_float(val[0] << 16);
+        acc[k][1] += __uint_as_float(val[0] & 0xffff0000u);
+        acc[k][2] += __uint_as_float(val[1] << 16);
+        acc[k][3] += __uint_as_float(val[1] & 0xffff0000u);
+      }
+    }
+  }
+  if constexpr (kSum) {
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = sub + kL * k;
+      if (c >= cp.chunks) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) atomicAdd(&s_sum[c * 4 + e], acc[k][e]);
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < cp.chunks * 4; c += kThreads) unsafeAtomicAdd(cp.colsum + c, s_sum[c]);
   }
 }
 
@@ -544,12 +650,20 @@ __device__ __forceinline__ typename Chunk<VB>::T add_chunk(typename Chunk<VB>::T
   return r;
 }
 
-template <int VB, int DT, bool kResidual>
+// DTW: the windows' dtype, DT's or (DT = f32) bf16: each fp32 chunk of four
+// values is then read as eight bytes of bf16 and widened exactly, so the sum
+// is the fp32 add torch's type promotion gives `shortcut + x` for an fp32
+// shortcut and autocast's bf16 proj output.
+template <int VB, int DT, bool kResidual, int DTW = DT>
 __global__ __launch_bounds__(kThreads) void reverse_kernel(const uint8_t* __restrict__ win,
                                                            uint8_t* y,
                                                            const uint8_t* residual,
                                                            const CopyGeom g) {
+  static_assert(DTW == DT || (DT == TERRA_DTYPE_F32 && DTW == TERRA_DTYPE_BF16 && VB == 16), "windows dtype");
+  constexpr bool kWiden = DTW != DT;
+  constexpr int kWinVB = kWiden ? VB / 2 : VB;
   using T = typename Chunk<VB>::T;
+  using TW = typename Chunk<kWinVB>::T;
   const uint32_t first = blockIdx.x * (kThreads * kUnroll);
   const uint32_t base = first + threadIdx.x;
   const __amdgpu_buffer_rsrc_t out =
@@ -577,14 +691,23 @@ __global__ __launch_bounds__(kThreads) void reverse_kernel(const uint8_t* __rest
     const bool valid = g.valid_end <= 0 || (wl >= g.valid_begin && wl < g.valid_end);
     have[u] = c < g.total && (unsigned)wr_l < (unsigned)g.win_rows && valid;
     const int64_t w = (int64_t)b * g.win_rows * g.nWw + wl;
-    src[u] = have[u] ? (w * g.N + (int64_t)(ti * g.ws + tj)) * g.row_bytes + (int64_t)cv * VB : 0;
+    src[u] = have[u] ? (w * g.N + (int64_t)(ti * g.ws + tj)) * g.win_row_bytes + (int64_t)cv * kWinVB : 0;
   }
+  TW wv[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) wv[u] = stream_load(reinterpret_cast<const TW*>(win + src[u]));
   T vals[kUnroll];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) vals[u] = stream_load(reinterpret_cast<const T*>(win + src[u]));
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u)
-    if (!have[u]) vals[u] = fill_chunk<VB>(0u);
+  for (int u = 0; u < kUnroll; ++u) {
+    if constexpr (kWiden) {  // bf16 -> fp32 is exact: the bits move up 16 places
+      TW w = wv[u];
+      if (!have[u]) w = TW(0u);
+      vals[u] = T{w[0] << 16, w[0] & 0xffff0000u, w[1] << 16, w[1] & 0xffff0000u};
+    } else {
+      vals[u] = wv[u];
+      if (!have[u]) vals[u] = fill_chunk<VB>(0u);
+    }
+  }
   if constexpr (kResidual) {
     T r[kUnroll];
 #pragma unroll
@@ -764,6 +887,70 @@ void launch_reverse(const void* win, void* y, const void* res, const CopyGeom& g
     }
   }
   reverse_kernel<VB, DT, false><<<blocks, kThreads, 0, s>>>((const uint8_t*)win, (uint8_t*)y, nullptr, g);
+}
+
+// Resident workgroups of a grid-stride kernel on the current device, at most
+// max_per_cu per CU, queried once per device and kernel instance.
+template <typename Kernel>
+int resident_blocks(Kernel kern, int max_per_cu, int* cache, int* out) {
+  constexpr int kMaxDevices = 64;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(TERRA_ERR_LAUNCH, "cannot query the current device");
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, 0) != hipSuccess)
+      return fail(TERRA_ERR_LAUNCH, "cannot size a grid-stride launch for this device");
+    per_cu = per_cu < 1 ? 1 : (per_cu > max_per_cu ? max_per_cu : per_cu);
+    cache[dev] = cus * per_cu;
+  }
+  *out = cache[dev];
+  return TERRA_OK;
+}
+
+template <int CPL, int kL, bool kSum>
+int launch_partition_cast(const void* x, void* win, const CopyGeom& g, const CastParams& cp, hipStream_t s) {
+  auto kern = partition_cast_kernel<CPL, kL, kSum>;
+  static int cache[64] = {0};
+  int resident = 0;
+  // With column sums every workgroup ends with one float atomic per channel
+  // into the same C addresses: four workgroups per CU measured 129 us at c3
+  // (fp32 -> bf16 with sums; 117 us without), against 137 with two, 205 with
+  // one and 144 with all seven resident.
+  const int st = resident_blocks(kern, kSum ? 4 : 64, cache, &resident);
+  if (st != TERRA_OK) return st;
+  constexpr uint32_t kTokensPerPass = kThreads / kL;
+  const uint32_t need = (cp.tokens + kTokensPerPass - 1) / kTokensPerPass;
+  const uint32_t blocks = need < (uint32_t)resident ? need : (uint32_t)resident;
+  kern<<<blocks, kThreads, 0, s>>>((const uint8_t*)x, (uint8_t*)win, g, cp);
+  return TERRA_OK;
+}
+
+template <bool kSum>
+int dispatch_partition_cast(int cpl, const void* x, void* win, const CopyGeom& g, const CastParams& cp,
+                            hipStream_t s) {
+  if (cpl <= 1) return launch_partition_cast<1, 8, kSum>(x, win, g, cp, s);
+  if (cpl <= 2) return launch_partition_cast<2, 8, kSum>(x, win, g, cp, s);
+  if (cpl <= 3) return launch_partition_cast<3, 8, kSum>(x, win, g, cp, s);
+  if (cpl <= 4) return launch_partition_cast<4, 8, kSum>(x, win, g, cp, s);
+  if (cpl <= 6) return launch_partition_cast<6, 8, kSum>(x, win, g, cp, s);
+  if (cpl <= 8) return launch_partition_cast<4, 16, kSum>(x, win, g, cp, s);
+  if (cpl <= 12) return launch_partition_cast<6, 16, kSum>(x, win, g, cp, s);
+  if (cpl <= 16) return launch_partition_cast<8, 16, kSum>(x, win, g, cp, s);
+  if (cpl <= 24) return launch_partition_cast<12, 16, kSum>(x, win, g, cp, s);
+  return launch_partition_cast<16, 16, kSum>(x, win, g, cp, s);  // fp32 C = 1024
+}
+
+// bf16 windows into fp32 y (reverse_kernel's DTW); 16-byte fp32 chunks.
+void launch_reverse_widen(const void* win, void* y, const void* res, const CopyGeom& g, hipStream_t s) {
+  const uint32_t blocks = (g.total + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  if (res != nullptr)
+    reverse_kernel<16, TERRA_DTYPE_F32, true, TERRA_DTYPE_BF16><<<blocks, kThreads, 0, s>>>(
+        (const uint8_t*)win, (uint8_t*)y, (const uint8_t*)res, g);
+  else
+    reverse_kernel<16, TERRA_DTYPE_F32, false, TERRA_DTYPE_BF16><<<blocks, kThreads, 0, s>>>(
+        (const uint8_t*)win, (uint8_t*)y, nullptr, g);
 }
 
 template <int VB>
@@ -983,4 +1170,59 @@ extern "C" int terra_swin_partition_ln_bwd_mixed(const void* dwindows, int dwind
   clear_error();
   return partition_ln_bwd_impl(dwindows, dwindows_dtype, x, dresidual, dx, x_dtype, geom, gamma, eps, dgamma, dbeta,
                                stream);
+}
+
+extern "C" int terra_swin_partition_mixed(const void* x, int x_dtype, void* windows, int windows_dtype,
+                                          const terra_swin_geom* geom, float pad_value, float* column_sums,
+                                          void* stream) {
+  clear_error();
+  if (x == nullptr || windows == nullptr) return fail(TERRA_ERR_NULL, "x or windows is NULL");
+  if (x_dtype != TERRA_DTYPE_F32 || windows_dtype != TERRA_DTYPE_BF16)
+    return fail(TERRA_ERR_DTYPE, "mixed partition: f32 x into bf16 windows only (got dtype %d into %d)", x_dtype,
+                windows_dtype);
+  CopyGeom g;
+  int vb = 0;
+  const int st = prepare(geom, TERRA_DTYPE_F32, true, &g, &vb, x, nullptr, nullptr);
+  if (st != TERRA_OK) return st;
+  if (vb != 16 || ((uintptr_t)windows & 7u) != 0 || ((uintptr_t)column_sums & 3u) != 0)
+    return fail(TERRA_ERR_ALIGN, "mixed partition needs C %% 4 == 0, 16-byte aligned x, 8-byte aligned windows and "
+                "4-byte aligned column sums");
+  const int chunks = (int)(g.row_bytes / 16);
+  if (chunks > kLnMaxChunks)
+    return fail(TERRA_ERR_UNSUPPORTED, "mixed partition handles up to %d channels (got %d)", kLnMaxChunks * 4,
+                geom->channels);
+  g.win_row_bytes = (int64_t)geom->channels * 2;
+  g.pad_pattern = pad_pattern(TERRA_DTYPE_BF16, pad_value);
+  CastParams cp;
+  cp.colsum = column_sums;
+  cp.chunks = chunks;
+  cp.tokens = g.total / (uint32_t)chunks;
+  if (cp.tokens == 0) return TERRA_OK;
+  const int cpl = (chunks + kLnLanes - 1) / kLnLanes;
+  hipStream_t s = (hipStream_t)stream;
+  const int rc = column_sums != nullptr ? dispatch_partition_cast<true>(cpl, x, windows, g, cp, s)
+                                        : dispatch_partition_cast<false>(cpl, x, windows, g, cp, s);
+  if (rc != TERRA_OK) return rc;
+  return launch_status("terra_swin_partition_mixed");
+}
+
+extern "C" int terra_swin_reverse_mixed(const void* windows, int windows_dtype, void* y, const void* residual,
+                                        int dtype, const terra_swin_geom* geom, void* stream) {
+  clear_error();
+  if (windows == nullptr || y == nullptr) return fail(TERRA_ERR_NULL, "windows or y is NULL");
+  if (dtype != TERRA_DTYPE_F32 || windows_dtype != TERRA_DTYPE_BF16)
+    return fail(TERRA_ERR_DTYPE, "mixed reverse: bf16 windows into f32 y only (got dtype %d into %d)", windows_dtype,
+                dtype);
+  CopyGeom g;
+  int vb = 0;
+  const int st = prepare(geom, TERRA_DTYPE_F32, false, &g, &vb, y, residual, nullptr);
+  if (st != TERRA_OK) return st;
+  if (vb != 16 || ((uintptr_t)windows & 7u) != 0)
+    return fail(TERRA_ERR_ALIGN, "mixed reverse needs C %% 4 == 0, 16-byte aligned y / residual and 8-byte aligned "
+                "windows");
+  g.win_row_bytes = (int64_t)geom->channels * 2;
+  g.pad_pattern = 0;
+  if (g.total == 0) return TERRA_OK;
+  launch_reverse_widen(windows, y, residual, g, (hipStream_t)stream);
+  return launch_status("terra_swin_reverse_mixed");
 }

@@ -161,11 +161,16 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 def swin_partition(x: torch.Tensor, geom: WindowGeometry, pad_value: float = 0.0,
-                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+                   column_sums: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused pad + roll(-shift) + window_partition of ``x`` [B, H, W, C].
 
     Returns windows ``[B * nW, ws*ws, C]`` (the layout of
-    ``window_partition(...).view(-1, ws*ws, C)``, models/transformer.py:225).
+    ``window_partition(...).view(-1, ws*ws, C)``, models/transformer.py:225)
+    in ``out_dtype`` (default: x's dtype; bf16 for fp32 x rounds each value
+    once, as a cast of the fp32 result would).  ``column_sums``: an fp32 [C]
+    tensor the per-channel sums of the bf16 windows written are ADDED into
+    (bf16 output from fp32 x only).
     """
     dev = _require_device(x)
     code = _dtype_code(x, tuple(_DTYPES))
@@ -174,18 +179,33 @@ def swin_partition(x: torch.Tensor, geom: WindowGeometry, pad_value: float = 0.0
                          f"{(geom.batch, geom.height, geom.width, geom.channels)}")
     if not x.is_contiguous():
         raise ValueError("x must be contiguous [B, H, W, C]")
+    odt = x.dtype if out_dtype is None else out_dtype
+    mixed = odt != x.dtype
+    if mixed and not (x.dtype == torch.float32 and odt == torch.bfloat16):
+        raise ValueError(f"out_dtype {odt} is not available for {x.dtype} x (fp32 x may give bf16 windows)")
+    if column_sums is not None:
+        if not mixed:
+            raise ValueError("column_sums are summed by the fp32 -> bf16 partition only")
+        if column_sums.dtype != torch.float32 or tuple(column_sums.shape) != (geom.channels,) \
+                or not column_sums.is_contiguous() or column_sums.device != dev:
+            raise ValueError(f"column_sums must be a contiguous fp32 [{geom.channels}] tensor on {dev}")
     shape = (geom.num_windows, geom.window * geom.window, geom.channels)
     if out is None:
-        out = torch.empty(shape, dtype=x.dtype, device=dev)
-    elif tuple(out.shape) != shape or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
-        raise ValueError(f"out must be a contiguous {x.dtype} tensor of shape {shape} on {dev}")
+        out = torch.empty(shape, dtype=odt, device=dev)
+    elif tuple(out.shape) != shape or out.dtype != odt or not out.is_contiguous() or out.device != dev:
+        raise ValueError(f"out must be a contiguous {odt} tensor of shape {shape} on {dev}")
     if geom.batch == 0:  # an empty batch: nothing to launch (torch returns the empty result)
         return out
     c_geom = geom.to_c()
     with torch.cuda.device(dev):
-        st = _lib.load().terra_swin_partition(_ptr(x), _ptr(out), code, ctypes.byref(c_geom),
-                                              float(pad_value), _stream(dev))
-    _lib.check(st, "terra_swin_partition")
+        if mixed:
+            st = _lib.load().terra_swin_partition_mixed(_ptr(x), code, _ptr(out), _lib.DTYPE_BF16,
+                                                        ctypes.byref(c_geom), float(pad_value), _ptr(column_sums),
+                                                        _stream(dev))
+        else:
+            st = _lib.load().terra_swin_partition(_ptr(x), _ptr(out), code, ctypes.byref(c_geom),
+                                                  float(pad_value), _stream(dev))
+    _lib.check(st, "terra_swin_partition_mixed" if mixed else "terra_swin_partition")
     return out
 
 
@@ -303,10 +323,17 @@ def rows_geometry(tokens: int, channels: int) -> WindowGeometry:
 
 
 def swin_reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional[torch.Tensor] = None,
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Fused window_reverse + roll(+shift) + crop (+ residual) to [B, H, W, C]."""
+                 out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Fused window_reverse + roll(+shift) + crop (+ residual) to [B, H, W, C]
+    in ``out_dtype`` (default: the windows' dtype; fp32 for bf16 windows
+    widens them exactly and adds an fp32 residual in fp32, as torch's type
+    promotion does for ``shortcut + x``)."""
     dev = _require_device(windows) if residual is None else _require_device(windows, residual)
     code = _dtype_code(windows, tuple(_DTYPES))
+    odt = windows.dtype if out_dtype is None else out_dtype
+    mixed = odt != windows.dtype
+    if mixed and not (windows.dtype == torch.bfloat16 and odt == torch.float32):
+        raise ValueError(f"out_dtype {odt} is not available for {windows.dtype} windows (bf16 windows may give fp32)")
     n = geom.window * geom.window
     if windows.numel() != geom.num_windows * n * geom.channels:
         raise ValueError(f"windows has {windows.numel()} elements, geometry needs "
@@ -315,22 +342,26 @@ def swin_reverse(windows: torch.Tensor, geom: WindowGeometry, residual: Optional
         raise ValueError("windows must be contiguous")
     shape = (geom.batch, geom.height, geom.width, geom.channels)
     if residual is not None:
-        if residual.dtype != windows.dtype or residual.numel() != geom.batch * geom.height * geom.width * geom.channels:
+        if residual.dtype != odt or residual.numel() != geom.batch * geom.height * geom.width * geom.channels:
             raise ValueError("residual must match the output grid in dtype and size")
         if not residual.is_contiguous():
             raise ValueError("residual must be contiguous")
     if out is None:
-        out = torch.empty(shape, dtype=windows.dtype, device=dev)
-    elif out.numel() != geom.batch * geom.height * geom.width * geom.channels or out.dtype != windows.dtype \
+        out = torch.empty(shape, dtype=odt, device=dev)
+    elif out.numel() != geom.batch * geom.height * geom.width * geom.channels or out.dtype != odt \
             or not out.is_contiguous() or out.device != dev:
-        raise ValueError(f"out must be a contiguous {windows.dtype} tensor with {shape} elements on {dev}")
+        raise ValueError(f"out must be a contiguous {odt} tensor with {shape} elements on {dev}")
     if geom.batch == 0:
         return out.view(shape)
     c_geom = geom.to_c()
     with torch.cuda.device(dev):
-        st = _lib.load().terra_swin_reverse(_ptr(windows), _ptr(out), _ptr(residual), code,
-                                            ctypes.byref(c_geom), _stream(dev))
-    _lib.check(st, "terra_swin_reverse")
+        if mixed:
+            st = _lib.load().terra_swin_reverse_mixed(_ptr(windows), code, _ptr(out), _ptr(residual),
+                                                      _lib.DTYPE_F32, ctypes.byref(c_geom), _stream(dev))
+        else:
+            st = _lib.load().terra_swin_reverse(_ptr(windows), _ptr(out), _ptr(residual), code,
+                                                ctypes.byref(c_geom), _stream(dev))
+    _lib.check(st, "terra_swin_reverse_mixed" if mixed else "terra_swin_reverse")
     return out.view(shape)
 
 
@@ -471,12 +502,17 @@ def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                               n_real: Optional[int] = None, mask_value: float = MASK_VALUE,
                               pad_key_value: float = PAD_KEY_VALUE,
                               dq: Optional[torch.Tensor] = None, dk: Optional[torch.Tensor] = None,
-                              dv: Optional[torch.Tensor] = None, dbias: Optional[torch.Tensor] = None):
+                              dv: Optional[torch.Tensor] = None, dbias: Optional[torch.Tensor] = None,
+                              column_sums: Optional[torch.Tensor] = None):
     """Gradients of :func:`window_attention` (terra_swin_attn_bwd).
 
     Returns (dq, dk, dv); each may be given as an output view (e.g. a column
     block of one [B_, N, 3C] buffer).  ``dbias``: an fp32 tensor shaped like
     the bias table that the kernel ADDS the bias gradient into, or None.
+    ``column_sums``: an fp32 [3C] tensor the column sums of dq | dk | dv (the
+    q / k / v Linear's bias gradient) are ADDED into, or None
+    (terra_swin_attn_bwd_sums; bf16 windows of at most 64 tokens only, see
+    :func:`attention_backward_sums_supported`).
     """
     dev = _require_device(q, k, v, dout)
     for t in (k, v, dout):
@@ -508,13 +544,33 @@ def window_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         if dbias.dtype != torch.float32 or tuple(dbias.shape) != tuple(table.shape) or not dbias.is_contiguous() \
                 or dbias.device != dev:
             raise ValueError(f"dbias must be a contiguous fp32 tensor of shape {tuple(table.shape)} on {dev}")
+    if column_sums is not None and (column_sums.dtype != torch.float32 or tuple(column_sums.shape) != (3 * channels,)
+                                    or not column_sums.is_contiguous() or column_sums.device != dev):
+        raise ValueError(f"column_sums must be a contiguous fp32 [{3 * channels}] tensor on {dev}")
     emask, land = _attn_masks(bd.fwd, num_windows, mask)
     with torch.cuda.device(dev):
-        st = _lib.load().terra_swin_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(outs[0]), _ptr(outs[1]),
-                                             _ptr(outs[2]), code, ctypes.byref(bd),
-                                             _ptr(table), _ptr(dbias), _ptr(emask), _ptr(land), _stream(dev))
-    _lib.check(st, "terra_swin_attn_bwd")
+        if column_sums is not None:
+            base = _ptr(column_sums)
+            step = channels * 4
+            st = _lib.load().terra_swin_attn_bwd_sums(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(outs[0]),
+                                                      _ptr(outs[1]), _ptr(outs[2]), code, ctypes.byref(bd),
+                                                      _ptr(table), _ptr(dbias), _ptr(emask), _ptr(land), base,
+                                                      base + step, base + 2 * step, _stream(dev))
+        else:
+            st = _lib.load().terra_swin_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(outs[0]),
+                                                 _ptr(outs[1]), _ptr(outs[2]), code, ctypes.byref(bd),
+                                                 _ptr(table), _ptr(dbias), _ptr(emask), _ptr(land), _stream(dev))
+    _lib.check(st, "terra_swin_attn_bwd_sums" if column_sums is not None else "terra_swin_attn_bwd")
     return tuple(outs)
+
+
+def attention_backward_sums_supported(q: torch.Tensor, num_heads: int, window_size: Tuple[int, int],
+                                      n_real: Optional[int] = None) -> bool:
+    """Whether :func:`window_attention_backward` also sums dq | dk | dv
+    (``column_sums``): bf16 windows of at most 64 tokens (the MFMA tile
+    kernel)."""
+    return (q.dtype == torch.bfloat16 and q.shape[-2] <= 64
+            and attention_backward_supported(q, num_heads, window_size, n_real))
 
 
 # (window, heads, channels) the fused half-block serves: 8x8 windows with 6
@@ -808,6 +864,48 @@ def linear_residual(x: torch.Tensor, weight_packed: torch.Tensor, out_features: 
                                                     None if c_geom is None else ctypes.byref(c_geom), _stream(dev))
     _lib.check(st, "terra_swin_linear_residual")
     return out.view(shape)
+
+
+def gelu_backward_supported(h: torch.Tensor) -> bool:
+    """Whether :func:`gelu_backward` serves a pre-activation like ``h``
+    (a bf16 or fp32 device tensor whose rows are whole 16-byte chunks of at
+    most 8192 bytes)."""
+    if h.device.type != "cuda" or h.dtype not in (torch.bfloat16, torch.float32) or h.dim() == 0:
+        return False
+    row_bytes = h.shape[-1] * h.element_size()
+    return row_bytes % 16 == 0 and 0 < row_bytes <= 8192
+
+
+def gelu_backward(dout: torch.Tensor, h: torch.Tensor, column_sums: Optional[torch.Tensor] = None,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The gradient of nn.GELU() (erf form, models/mlp.py:165) at ``h`` for
+    the output gradient ``dout`` (same shape and dtype, bf16 or fp32):
+    ``dout * (Phi(h) + h phi(h))`` in fp32, rounded once; what
+    ``torch.ops.aten.gelu_backward(dout, h)`` computes.  ``column_sums``: an
+    fp32 [features] tensor the per-feature sums of the result are ADDED into
+    (the bias gradient of the Linear that produced ``h``)."""
+    dev = _require_device(dout, h)
+    code = _dtype_code(h, (torch.float32, torch.bfloat16))
+    if dout.shape != h.shape or dout.dtype != h.dtype:
+        raise ValueError(f"dout {tuple(dout.shape)} {dout.dtype} must match h {tuple(h.shape)} {h.dtype}")
+    if not (dout.is_contiguous() and h.is_contiguous()):
+        raise ValueError("dout and h must be contiguous")
+    features = h.shape[-1] if h.dim() > 0 else 1
+    rows = h.numel() // features if features else 0
+    if column_sums is not None and (column_sums.dtype != torch.float32 or tuple(column_sums.shape) != (features,)
+                                    or not column_sums.is_contiguous() or column_sums.device != dev):
+        raise ValueError(f"column_sums must be a contiguous fp32 [{features}] tensor on {dev}")
+    if out is None:
+        out = torch.empty_like(h)
+    elif out.shape != h.shape or out.dtype != h.dtype or not out.is_contiguous() or out.device != dev:
+        raise ValueError(f"out must be a contiguous {h.dtype} tensor like h on {dev}")
+    if rows == 0:
+        return out
+    with torch.cuda.device(dev):
+        st = _lib.load().terra_swin_gelu_bwd(_ptr(dout), _ptr(h), _ptr(out), code, int(rows), int(features),
+                                             _ptr(column_sums), _stream(dev))
+    _lib.check(st, "terra_swin_gelu_bwd")
+    return out
 
 
 def swin_mlp_supported(x: torch.Tensor, channels: int, hidden: int) -> bool:

@@ -235,6 +235,7 @@ class SequentialSwinTransformer(torch.nn.Module):
             if config.use_layernorm:  # a norm layer the gather does not fuse runs on its own
                 grid = self.norm1(grid.view(B, L, C)).contiguous().view(B, H, W, C)
             x_windows = autograd.partition(grid, geom)
+        bias_sums = None
         if not training and self._proj_scatter(x_windows, shortcut, geom):
             # proj + window reverse + inverse roll + residual in one kernel.
             o = self.attn.attend(x_windows, mask=self.window_mask(geom))
@@ -244,12 +245,23 @@ class SequentialSwinTransformer(torch.nn.Module):
                 return y.view(B, H * W, C)
             attn_windows = autograd.linear(o, self.attn.proj.weight, self.attn.proj.bias)
         else:
-            attn_windows = self.attn(x_windows, mask=self.window_mask(geom))
+            proj = self.attn.proj
+            if training and type(proj) is torch.nn.Linear and proj.bias is not None:
+                # proj's bias gradient is summed by the scatter's backward
+                # kernel while it writes proj's output gradient.
+                bias_sums = autograd.ColumnSumLink()
+                o = self.attn.attend(x_windows, mask=self.window_mask(geom))
+                attn_windows = autograd.linear(o, proj.weight, proj.bias, bias_sums=bias_sums)
+            else:
+                attn_windows = self.attn(x_windows, mask=self.window_mask(geom))
         out_dtype = torch.promote_types(attn_windows.dtype, shortcut.dtype)
         residual = shortcut.to(out_dtype).contiguous().view(B, H, W, C)
         # The link carries the residual's gradient only when the residual is
         # the LayerNorm's input itself (same dtype, no copy in between).
         link = link if (config.use_layernorm and residual.data_ptr() == grid.data_ptr()
                         and residual.dtype == grid.dtype) else None
-        y = autograd.reverse(attn_windows.to(out_dtype).contiguous(), geom, residual=residual, link=link)
+        # bf16 windows into an fp32 result (autocast's proj output plus the
+        # fp32 shortcut) are widened by the scatter kernel itself.
+        y = autograd.reverse(attn_windows.contiguous(), geom, residual=residual, link=link, out_dtype=out_dtype,
+                             bias_sums=bias_sums)
         return y.view(B, H * W, C)

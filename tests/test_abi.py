@@ -246,6 +246,55 @@ def test_partition_ln_mixed_rejects_bad_arguments():
                None) == -3
 
 
+def test_mixed_copies_reject_bad_arguments():
+    lib = L.load()
+    g = _geom(channels=8)
+    part = lib.terra_swin_partition_mixed
+    # only fp32 x into bf16 windows
+    assert part(FAKE, L.DTYPE_BF16, FAKE, L.DTYPE_F32, ctypes.byref(g), 0.0, None, None) == -2
+    assert "mixed partition" in L.last_error()
+    assert part(FAKE, L.DTYPE_F32, FAKE, L.DTYPE_F32, ctypes.byref(g), 0.0, None, None) == -2
+    assert part(None, L.DTYPE_F32, FAKE, L.DTYPE_BF16, ctypes.byref(g), 0.0, None, None) == -1
+    assert part(FAKE, L.DTYPE_F32, FAKE, L.DTYPE_BF16, None, 0.0, None, None) == -1
+    assert part(FAKE, L.DTYPE_F32, FAKE, L.DTYPE_BF16, ctypes.byref(_geom(channels=6)), 0.0, None, None) == -4
+    assert part(FAKE, L.DTYPE_F32, ctypes.c_void_p((1 << 20) + 4), L.DTYPE_BF16, ctypes.byref(g), 0.0, None,
+                None) == -4
+    assert part(FAKE, L.DTYPE_F32, FAKE, L.DTYPE_BF16, ctypes.byref(g), 0.0, ctypes.c_void_p((1 << 20) + 2),
+                None) == -4
+    assert part(FAKE, L.DTYPE_F32, FAKE, L.DTYPE_BF16, ctypes.byref(_geom(channels=1028)), 0.0, None, None) == -5
+    assert part(FAKE, L.DTYPE_F32, FAKE, L.DTYPE_BF16, ctypes.byref(_geom(height=15)), 0.0, None, None) == -3
+    rev = lib.terra_swin_reverse_mixed
+    assert rev(FAKE, L.DTYPE_F32, FAKE, None, L.DTYPE_BF16, ctypes.byref(g), None) == -2
+    assert "mixed reverse" in L.last_error()
+    assert rev(FAKE, L.DTYPE_BF16, FAKE, None, L.DTYPE_F16, ctypes.byref(g), None) == -2
+    assert rev(None, L.DTYPE_BF16, FAKE, None, L.DTYPE_F32, ctypes.byref(g), None) == -1
+    assert rev(FAKE, L.DTYPE_BF16, None, None, L.DTYPE_F32, ctypes.byref(g), None) == -1
+    assert rev(ctypes.c_void_p((1 << 20) + 4), L.DTYPE_BF16, FAKE, None, L.DTYPE_F32, ctypes.byref(g), None) == -4
+    assert rev(FAKE, L.DTYPE_BF16, FAKE, ctypes.c_void_p((1 << 20) + 8), L.DTYPE_F32, ctypes.byref(g), None) == -4
+    assert rev(FAKE, L.DTYPE_BF16, FAKE, None, L.DTYPE_F32, ctypes.byref(_geom(window=0)), None) == -3
+
+
+def test_gelu_bwd_rejects_bad_arguments():
+    gelu = L.load().terra_swin_gelu_bwd
+    other = ctypes.c_void_p(1 << 30)
+    dh = ctypes.c_void_p(1 << 31)
+    assert gelu(None, other, dh, L.DTYPE_BF16, 4, 64, None, None) == -1
+    assert gelu(FAKE, other, None, L.DTYPE_BF16, 4, 64, None, None) == -1
+    assert gelu(FAKE, other, dh, L.DTYPE_F16, 4, 64, None, None) == -2
+    assert gelu(FAKE, other, dh, L.DTYPE_BF16, -1, 64, None, None) == -3
+    assert gelu(FAKE, other, dh, L.DTYPE_BF16, 4, 0, None, None) == -3
+    assert gelu(FAKE, other, dh, L.DTYPE_BF16, 4, 12, None, None) == -4     # 24-byte rows
+    assert "16-byte" in L.last_error()
+    assert gelu(FAKE, other, dh, L.DTYPE_BF16, 4, 4104, None, None) == -5   # rows over 8192 bytes
+    assert gelu(FAKE, other, dh, L.DTYPE_F32, 4, 2056, None, None) == -5
+    assert gelu(ctypes.c_void_p((1 << 20) + 8), other, dh, L.DTYPE_BF16, 4, 64, None, None) == -4
+    assert gelu(FAKE, other, dh, L.DTYPE_BF16, 4, 64, ctypes.c_void_p((1 << 20) + 2), None) == -4
+    assert gelu(FAKE, other, FAKE, L.DTYPE_BF16, 4, 64, None, None) == -3   # dh is dout
+    assert "overlap" in L.last_error()
+    assert gelu(FAKE, other, ctypes.c_void_p((1 << 30) + 64), L.DTYPE_BF16, 4, 64, None, None) == -3
+    assert gelu(FAKE, other, dh, L.DTYPE_BF16, 0, 64, None, None) == 0      # no rows: nothing launched
+
+
 def _block_desc(geom_kw=None, **kw):
     d = L.SwinBlockDesc()
     gk = dict(channels=192, window=8)

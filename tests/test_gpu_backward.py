@@ -13,6 +13,8 @@ fp32 activations (the generic kernel, all fp32; reference in float64):
   module (LayerNorm + Linears + attention + residual, all bf16 in torch's
   and the kernel's rounding): normwise |got - ref| / |ref| <= 3e-2 per tensor.
 Partition / reverse gradients are permutations: bit-exact.
+Column sums of dq | dk | dv (the q / k / v bias gradient): within the fp32
+summation bound n u sum |x| of the float64 sums of the stored values.
 """
 import pytest
 import torch
@@ -531,3 +533,66 @@ def test_block_backward_window_32(dev, layer_idx):
             assert p.grad.double().norm().item() <= 3e-2 * params["attn.q_linear.bias"].grad.norm().item()
             continue
         assert _normwise(p.grad, params[name].grad) <= 3e-2, name
+
+
+def _sum_bound(vals: torch.Tensor) -> torch.Tensor:
+    """Worst-case error of an fp32 sum of the column's n terms in any order:
+    n u sum |x| (u = 2^-24)."""
+    flat = vals.reshape(-1, vals.shape[-1]).double().cpu()
+    return flat.shape[0] * 2.0 ** -24 * flat.abs().sum(0) + 1e-30
+
+
+@pytest.mark.parametrize("case", ["c3", "odd_heads", "hd64", "hd128", "w7_padded", "explicit"])
+def test_attention_backward_column_sums(dev, case):
+    """terra_swin_attn_bwd_sums: dq | dk | dv bit for bit those of
+    terra_swin_attn_bwd, and the column sums (the q / k / v bias gradient,
+    added into a [3C] buffer) within the fp32 summation bound of the float64
+    sums of the stored values; with a dense mask, padded keys, one head per
+    workgroup and head dims 64 / 128."""
+    ws, n_real, mask, N = (8, 8), None, None, 64
+    if case == "c3":
+        C, heads, B_ = 192, 6, 40
+    elif case == "odd_heads":
+        C, heads, B_ = 96, 3, 24
+    elif case == "hd64":
+        C, heads, B_ = 256, 4, 16
+    elif case == "hd128":
+        C, heads, B_ = 256, 2, 16
+    elif case == "w7_padded":
+        C, heads, B_, ws, n_real = 128, 4, 8, (7, 7), 49
+    else:
+        C, heads, B_ = 192, 6, 16
+        mask = so.shift_mask(16, 32, 8, 4).to(dev)
+    q, k, v, dout, table = _inputs(B_, C, heads, 600)
+    tsize = (2 * ws[0] - 1) * (2 * ws[1] - 1)
+    table = table[:tsize].contiguous()
+    args = (q.to(dev), k.to(dev), v.to(dev), dout.to(dev), heads, ws, (C // heads) ** -0.5)
+    kw = dict(bias_table=table.to(dev), mask=mask, n_real=n_real)
+    assert kernels.attention_backward_sums_supported(args[0], heads, ws, n_real)
+    want = kernels.window_attention_backward(*args, **kw)
+    sums = torch.zeros(3 * C, device=dev)
+    got = kernels.window_attention_backward(*args, column_sums=sums, **kw)
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
+    cat = torch.cat(got, -1)
+    ref = cat.double().sum((0, 1)).cpu()
+    assert ((sums.double().cpu() - ref).abs() <= _sum_bound(cat)).all()
+    # accumulates, and the bias-table gradient is unchanged by the sums
+    d0, d1 = torch.zeros(table.shape, device=dev), torch.zeros(table.shape, device=dev)
+    kernels.window_attention_backward(*args, dbias=d0, **kw)
+    kernels.window_attention_backward(*args, dbias=d1, column_sums=sums, **kw)
+    assert ((sums.double().cpu() - 2 * ref).abs() <= 2 * _sum_bound(cat)).all()
+    assert (d1 - d0).abs().max().item() <= 1e-5 * d0.abs().max().item()
+
+
+def test_attention_backward_column_sums_unsupported(dev):
+    """fp32 activations (the generic kernel) and windows of more than 64
+    tokens (the flash path) do not sum: the request is refused."""
+    q = workloads.activations((2, 64, 64), 610).to(dev)
+    assert not kernels.attention_backward_sums_supported(q, 2, (8, 8))
+    with pytest.raises(ValueError, match="column sums"):
+        kernels.window_attention_backward(q, q, q, q, 2, (8, 8), 0.2, column_sums=torch.zeros(192, device=dev))
+    qb = workloads.activations((1, 256, 128), 611).to(torch.bfloat16).to(dev)
+    assert not kernels.attention_backward_sums_supported(qb, 2, (16, 16))
+    with pytest.raises(ValueError, match="column sums"):
+        kernels.window_attention_backward(qb, qb, qb, qb, 2, (16, 16), 0.125, column_sums=torch.zeros(384, device=dev))

@@ -1,7 +1,9 @@
-"""The training path's LayerNorm kernels: the backward of the fused
-LayerNorm + partition (terra_swin_partition_ln_bwd), alone and inside the
-block, and the MLP half's backward (autograd.mlp), against torch autograd of
-the oracle's restatement.
+"""The training path's kernels: the backward of the fused LayerNorm +
+partition (terra_swin_partition_ln_bwd), alone and inside the block, and the
+MLP half's backward (autograd.mlp), against torch autograd of the oracle's
+restatement; the mixed-dtype gather / scatter of bf16 autocast and the GELU
+backward (terra_swin_gelu_bwd), each with its bias-gradient column sums,
+against the separate ops they replace and float64 arithmetic.
 
 Tolerances: fp32 activations, every gradient within 1e-5 of the float64
 reference (max-abs relative, per tensor); bf16, within one bf16 rounding of
@@ -247,3 +249,219 @@ def test_partition_ln_mixed_rejects_other_pairs(dev):
     with pytest.raises(ValueError):
         kernels.swin_partition_ln_backward(torch.zeros((1, 64, 64), dtype=torch.float16, device=dev), x.float(), g,
                                            None, 1e-5)
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("residual", [False, True])
+def test_reverse_mixed_equals_widen_and_reverse(dev, case, residual):
+    """bf16 windows into an fp32 grid (plus an fp32 residual): bit for bit
+    the fp32 reverse of the windows cast to fp32 (the widening is exact and
+    the add is the fp32 add either way)."""
+    B, H, W, C, ws, s, pad, r0, rows, valid = case
+    g = _geom(*case)
+    win = workloads.activations((g.num_windows, ws * ws, C), 520).to(torch.bfloat16).to(dev)
+    res = (workloads.activations((B, H, W, C), 521) * 3).to(dev) if residual else None
+    want = kernels.swin_reverse(win.float(), g, residual=res)
+    got = kernels.swin_reverse(win, g, residual=res, out_dtype=torch.float32)
+    assert got.dtype == torch.float32
+    assert torch.equal(got, want)
+    if residual:  # in place on the residual
+        res2 = res.clone()
+        kernels.swin_reverse(win, g, residual=res2, out=res2, out_dtype=torch.float32)
+        assert torch.equal(res2, want)
+
+
+def _sum_bound(vals: torch.Tensor, dims) -> torch.Tensor:
+    """Worst-case error of fp32 summation in any order: n u sum |x| (n terms,
+    u = 2^-24), per column."""
+    n = 1
+    for d in dims:
+        n *= vals.shape[d]
+    return n * 2.0 ** -24 * vals.double().abs().sum(dims).cpu() + 1e-30
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_partition_mixed_equals_partition_and_cast(dev, case):
+    """fp32 grid into bf16 windows: bit for bit the fp32 partition followed
+    by a cast (pad slots included), and the column sums of the values written
+    within the fp32 summation bound of their float64 sums; the sums
+    accumulate over calls."""
+    B, H, W, C, ws, s, pad, r0, rows, valid = case
+    g = _geom(*case)
+    x = (workloads.activations((B, H, W, C), 522) * 3).to(dev)
+    want = kernels.swin_partition(x, g, pad_value=0.5).to(torch.bfloat16)
+    sums = torch.zeros(C, device=dev)
+    got = kernels.swin_partition(x, g, pad_value=0.5, out_dtype=torch.bfloat16, column_sums=sums)
+    assert got.dtype == torch.bfloat16
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    ref = want.double().sum((0, 1)).cpu()
+    bound = _sum_bound(want, (0, 1))
+    assert ((sums.double().cpu() - ref).abs() <= bound).all()
+    got2 = kernels.swin_partition(x, g, pad_value=0.5, out_dtype=torch.bfloat16, column_sums=sums)
+    assert torch.equal(got2.view(torch.int16), want.view(torch.int16))
+    assert ((sums.double().cpu() - 2 * ref).abs() <= 2 * bound).all()
+    # without sums; and the identity frame over token rows (the MLP half's cast)
+    assert torch.equal(kernels.swin_partition(x, g, pad_value=0.5, out_dtype=torch.bfloat16).view(torch.int16),
+                       want.view(torch.int16))
+    T = B * H * W
+    rows_sums = torch.zeros(C, device=dev)
+    flat = kernels.swin_partition(x.view(1, T, 1, C), kernels.rows_geometry(T, C), out_dtype=torch.bfloat16,
+                                  column_sums=rows_sums).view(T, C)
+    assert torch.equal(flat.view(torch.int16), x.view(T, C).to(torch.bfloat16).view(torch.int16))
+    assert ((rows_sums.double().cpu() - flat.double().sum(0).cpu()).abs() <= _sum_bound(flat, (0,))).all()
+
+
+def _gelu_grad64(g: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
+    """d/dh of 0.5 h (1 + erf(h / sqrt 2)) times g, in float64."""
+    g, h = g.double().cpu(), h.double().cpu()
+    cdf = 0.5 * (1 + torch.erf(h / 2 ** 0.5))
+    pdf = torch.exp(-0.5 * h * h) / (2 * torch.pi) ** 0.5
+    return g * (cdf + h * pdf)
+
+
+@pytest.mark.parametrize("dtype,features", [(torch.bfloat16, 512), (torch.bfloat16, 768), (torch.bfloat16, 1536),
+                                            (torch.bfloat16, 3072), (torch.bfloat16, 4096), (torch.float32, 768),
+                                            (torch.float32, 2048)])
+@pytest.mark.parametrize("rows", [1, 37, 2053])
+def test_gelu_backward(dev, dtype, features, rows):
+    """terra_swin_gelu_bwd against the float64 derivative (one rounding to
+    the dtype plus fp32 arithmetic: 2^-8 relative for bf16, 1e-6 for fp32,
+    with an absolute floor of 1e-6 of the tensor's scale for values that
+    cancel to near zero) and against torch's gelu_backward (at most one bf16
+    unit in the last place, and equal for at least 99.9 % of the values);
+    fc1's bias gradient (the column sums of the values written) within the
+    fp32 summation bound."""
+    h = (workloads.activations((rows, features), 530) * 2.5).to(dtype).to(dev)
+    gy = workloads.activations((rows, features), 531).to(dtype).to(dev)
+    sums = torch.zeros(features, device=dev)
+    got = kernels.gelu_backward(gy, h, column_sums=sums)
+    assert got.dtype == dtype and got.shape == h.shape
+    ref = _gelu_grad64(gy, h)
+    rel = 2.0 ** -8 if dtype == torch.bfloat16 else 1e-6
+    err = (got.double().cpu() - ref).abs()
+    assert (err <= rel * ref.abs() + 1e-6 * ref.abs().max()).all(), err.max().item()
+    want = torch.ops.aten.gelu_backward(gy, h)
+    if dtype == torch.bfloat16:
+        gi, wi = got.view(torch.int16).int().cpu(), want.view(torch.int16).int().cpu()
+        assert (gi - wi).abs().max().item() <= 1
+        assert (gi == wi).float().mean().item() >= 0.999
+    else:
+        assert ((got - want).abs() <= 1e-6 * want.abs() + 1e-30).float().mean().item() >= 0.999
+    assert ((sums.double().cpu() - got.double().sum(0).cpu()).abs() <= _sum_bound(got, (0,))).all()
+    # without sums: the same values
+    assert torch.equal(kernels.gelu_backward(gy, h), got)
+
+
+def test_gelu_backward_special_values(dev):
+    """Zeros, tiny and huge inputs, infinities and NaN give torch's values."""
+    vals = [0.0, -0.0, 1e-30, -1e-30, 2.0 ** -26, -(2.0 ** -20), 0.5, -0.5, 3.0, -3.0, 6.0, -6.0, 32.0, -32.0,
+            1e4, -1e4, float("inf"), float("-inf"), float("nan")]
+    h = torch.tensor(vals * 8, dtype=torch.float32)[:152].view(1, 152)
+    h = torch.cat([h, torch.zeros(1, 8)], 1).to(torch.bfloat16).to(dev)  # 160 features: 20 chunks
+    gy = torch.full(h.shape, -1.5, dtype=torch.bfloat16, device=dev)
+    got = kernels.gelu_backward(gy, h)
+    want = torch.ops.aten.gelu_backward(gy, h)
+    assert torch.equal(torch.isnan(got), torch.isnan(want))
+    fin = ~torch.isnan(want)
+    assert torch.equal(got[fin], want[fin])
+
+
+def test_gelu_backward_rejects_bad_arguments(dev):
+    h = torch.zeros((4, 12), dtype=torch.bfloat16, device=dev)  # 24-byte rows
+    with pytest.raises(ValueError, match="16-byte"):
+        kernels.gelu_backward(h, h)
+    h = torch.zeros((4, 16), dtype=torch.float16, device=dev)
+    with pytest.raises(TypeError):
+        kernels.gelu_backward(h, h)
+    h = torch.zeros((4, 16), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        kernels.gelu_backward(h, h, column_sums=torch.zeros(8, device=dev))
+    with pytest.raises(ValueError, match="overlap"):  # dh overlapping dout
+        kernels.gelu_backward(h, h.clone(), out=h)
+
+
+def test_mlp_backward_autocast_routes_through_fused_kernels(dev):
+    """Under autocast the MLP half's backward casts the output gradient with
+    terra_swin_partition_mixed (fc2's bias gradient summed there) and runs
+    the GELU derivative on terra_swin_gelu_bwd (fc1's bias gradient summed
+    there): one call each."""
+    m = _mlp_case(192, 560)
+    md = copy.deepcopy(m).to(dev)
+    calls = {"part": 0, "gelu": 0}
+    p0, g0 = kernels.swin_partition, kernels.gelu_backward
+
+    def cp(*a, **k):
+        if k.get("column_sums") is not None:
+            calls["part"] += 1
+        return p0(*a, **k)
+
+    def cg(*a, **k):
+        calls["gelu"] += 1
+        return g0(*a, **k)
+
+    kernels.swin_partition, kernels.gelu_backward = cp, cg
+    try:
+        x = workloads.activations((2, 96, 192), 561).to(dev).requires_grad_(True)
+        with torch.amp.autocast(device_type="cuda", dtype=torch.bfloat16):
+            y = md(x)
+        y.backward(workloads.activations(tuple(y.shape), 562).to(dev))
+    finally:
+        kernels.swin_partition, kernels.gelu_backward = p0, g0
+    assert calls["part"] == 1 and calls["gelu"] == 1
+    assert md.fc1.bias.grad is not None and md.fc2.bias.grad is not None
+
+
+def test_block_autocast_training_sums_biases_in_kernels(dev):
+    """A block's training step under autocast: the scatter's backward writes
+    proj's bf16 output gradient with its column sums (terra_swin_partition_mixed)
+    and the attention core's backward sums the q | k | v gradient
+    (terra_swin_attn_bwd_sums); the forward's scatter widens the bf16 proj
+    output itself (terra_swin_reverse_mixed).  The bias gradients equal the
+    column sums torch takes of the same gradients, within the fp32 summation
+    bound."""
+    cfg = workloads.CONFIGS["c3"].scaled(16, 32)
+    blk = gain_block(workloads.block_for(cfg, 1)).to(dev)
+    calls = {"part": 0, "attn": 0, "rev": 0}
+    p0, a0, r0 = kernels.swin_partition, kernels.window_attention_backward, kernels.swin_reverse
+    seen = {}
+
+    def cp(*a, **k):
+        if k.get("column_sums") is not None:
+            calls["part"] += 1
+            out = p0(*a, **k)
+            seen["dproj"] = out.detach().clone()
+            return out
+        return p0(*a, **k)
+
+    def ca(*a, **k):
+        if k.get("column_sums") is not None:
+            calls["attn"] += 1
+            outs = a0(*a, **k)
+            seen["dqkv"] = torch.cat([t.detach() for t in outs], -1).clone()
+            return outs
+        return a0(*a, **k)
+
+    def cr(*a, **k):
+        if k.get("out_dtype") == torch.float32 and a[0].dtype == torch.bfloat16:
+            calls["rev"] += 1
+        return r0(*a, **k)
+
+    kernels.swin_partition, kernels.window_attention_backward, kernels.swin_reverse = cp, ca, cr
+    try:
+        x = workloads.activations((1, 16 * 32, cfg.channels), 570).to(dev).requires_grad_(True)
+        with torch.amp.autocast(device_type="cuda", dtype=torch.bfloat16):
+            y = blk(x)
+        y.backward(workloads.activations(tuple(y.shape), 571).to(dev))
+    finally:
+        kernels.swin_partition, kernels.window_attention_backward, kernels.swin_reverse = p0, a0, r0
+    assert calls == {"part": 1, "attn": 1, "rev": 1}
+    C = cfg.channels
+    dproj = seen["dproj"].reshape(-1, C)
+    want = dproj.double().sum(0).cpu()
+    got = blk.attn.proj.bias.grad.double().cpu()
+    assert ((got - want).abs() <= dproj.shape[0] * 2.0 ** -24 * dproj.double().abs().sum(0).cpu() + 1e-30).all()
+    dqkv = seen["dqkv"].reshape(-1, 3 * C)
+    want = dqkv.double().sum(0).cpu()
+    bound = dqkv.shape[0] * 2.0 ** -24 * dqkv.double().abs().sum(0).cpu() + 1e-30
+    got = torch.cat([blk.attn.q_linear.bias.grad, blk.attn.k_linear.bias.grad, blk.attn.v_linear.bias.grad])
+    assert ((got.double().cpu() - want).abs() <= bound).all()
