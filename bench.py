@@ -60,9 +60,10 @@ def parse():
                     help="seconds of untimed steps before the counted warm-up (clock settling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
-    ap.add_argument("--mode", choices=("step", "kernels"), default="step",
+    ap.add_argument("--mode", choices=("step", "kernels", "training"), default="step",
                     help="step: the timed benchmark; kernels: run the step's HIP kernels --steps times "
-                         "(for rocprofv3 counter passes) and a 192 MiB copy of known size")
+                         "(for rocprofv3 counter passes) and a 192 MiB copy of known size; training: only the "
+                         "training step (2 warm-up steps, then --steps timed ones; for rocprofv3 traces)")
     return ap.parse_args()
 
 
@@ -289,6 +290,10 @@ def main():
     x = workloads.activations((cfg.batch, cfg.height * cfg.width, cfg.channels), 1003, dtype).to(dev)
     if args.mode == "kernels":
         run_kernels(cfg, blk, x, args.steps)
+        return
+    if args.mode == "training":
+        us = training_step_us(cfg, dev, warmup=2, reps=max(1, args.steps))
+        print(json.dumps({"training_step_us": us, "config": args.config, "steps": max(1, args.steps)}), flush=True)
         return
 
     # Events around the fused kernel on its launch stream (torch's current

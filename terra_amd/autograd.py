@@ -236,7 +236,14 @@ class _Mlp(torch.autograd.Function):
         h1 = torch.nn.functional.linear(xn, w1, b1)
         a = torch.nn.functional.gelu(h1)
         h2 = torch.nn.functional.linear(a, w2, b2)
-        y = rows + h2
+        if h2.dtype == torch.bfloat16 and rows.dtype == torch.float32 and C % 4 == 0 and h2.shape[-1] == C:
+            # x + fc2(...) under autocast: the bf16 h2 widened and added to the
+            # fp32 rows in one pass (the mixed scatter over an identity frame;
+            # bit for bit torch's promoted add).
+            y = kernels.swin_reverse(h2.contiguous(), geom, residual=rows.view(1, -1, 1, C),
+                                     out_dtype=torch.float32).view(rows.shape)
+        else:
+            y = rows + h2
         ctx.eps, ctx.geom, ctx.shape = eps, geom, x.shape
         ctx.autocast = torch.is_autocast_enabled(x.device.type)
         ctx.save_for_backward(rows, ln_w, ln_b, xn, h1, a, w1, w2)
