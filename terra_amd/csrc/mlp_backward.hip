@@ -70,12 +70,14 @@ template <int DT> struct GeluElt;
 template <> struct GeluElt<TERRA_DTYPE_F32> { static constexpr int kPerChunk = 4; };
 template <> struct GeluElt<TERRA_DTYPE_BF16> { static constexpr int kPerChunk = 8; };
 
-// One wave per row (kGeluRows rows per pass), lane l holding the 16-byte
-// chunks l, l + 64, ... of each row, so its columns stay fixed and their sums
-// stay in registers.  Workgroups loop over the rows grid-stride (the resident
-// count, capped); at the end each workgroup reduces its lanes' sums in LDS and
-// adds them to colsum with one float atomic per column.
-template <int DT, int CPL, bool kSum>
+// kL lanes per row (64: one wave; 32: two rows side by side, for rows of
+// 32 * odd chunks that would leave half a wave idle on their last chunk),
+// kGeluRows rows per lane group and pass, lane l of a group holding the
+// 16-byte chunks l, l + kL, ... of its rows, so its columns stay fixed and
+// their sums stay in registers.  Workgroups loop over the rows grid-stride
+// (the resident count, capped); at the end each workgroup reduces its lanes'
+// sums in LDS and adds them to colsum with one float atomic per column.
+template <int DT, int CPL, bool kSum, int kL = 64>
 __global__ __launch_bounds__(kGeluThreads) void gelu_bwd_kernel(const uint8_t* __restrict__ dout,
                                                                 const uint8_t* __restrict__ h,
                                                                 uint8_t* __restrict__ dh, float* colsum,
@@ -83,6 +85,9 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_bwd_kernel(const uint8_t* _
   constexpr int E = GeluElt<DT>::kPerChunk;
   constexpr int kMaxCols = CPL * 64 * E;
   constexpr int kGeluRows = gelu_rows<CPL>();
+  constexpr int kSub = 64 / kL;                 // rows side by side in a wave
+  constexpr int kWaveRows = kGeluRows * kSub;   // rows per wave and pass
+  static_assert(kL == 64 || kL == 32, "lanes per row");
   constexpr bool kTable = DT == TERRA_DTYPE_BF16;
   __shared__ float s_sum[kSum ? kMaxCols : 1];
   __shared__ float s_slope[kTable ? kSlopeEntries : 1];
@@ -90,7 +95,8 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_bwd_kernel(const uint8_t* _
     for (int c = threadIdx.x; c < kMaxCols; c += kGeluThreads) s_sum[c] = 0.f;
   if constexpr (kTable) slope_table_fill(s_slope);
   if constexpr (kSum || kTable) __syncthreads();
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & (kL - 1);      // lane within its row group
+  const int sub = kSub == 1 ? 0 : (int)((threadIdx.x & 63) / kL);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row_bytes = (int64_t)chunks * 16;
   float acc[CPL][E];
@@ -99,29 +105,34 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_bwd_kernel(const uint8_t* _
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[k][e] = 0.f;
 
-  const int64_t stride = (int64_t)gridDim.x * kGeluWaves * kGeluRows;
-  for (int64_t r0 = ((int64_t)blockIdx.x * kGeluWaves + wave) * kGeluRows; r0 < rows; r0 += stride) {
+  const int64_t stride = (int64_t)gridDim.x * kGeluWaves * kWaveRows;
+  for (int64_t r0 = ((int64_t)blockIdx.x * kGeluWaves + wave) * kWaveRows; r0 < rows; r0 += stride) {
     u32x4 gv[kGeluRows][CPL], hv[kGeluRows][CPL];
 #pragma unroll
     for (int i = 0; i < kGeluRows; ++i) {
-      const int64_t r = r0 + i < rows ? r0 + i : r0;  // a missing row re-reads row r0 and stores nothing
+      const int64_t ri = r0 + kSub * i + sub;
+      const int64_t r = ri < rows ? ri : r0;  // a missing row re-reads row r0 and stores nothing
       const u32x4* gs = reinterpret_cast<const u32x4*>(dout + r * row_bytes);
       const u32x4* hs = reinterpret_cast<const u32x4*>(h + r * row_bytes);
 #pragma unroll
       for (int k = 0; k < CPL; ++k) {
-        const int c = lane + 64 * k < chunks ? lane + 64 * k : 0;
+        const int c = lane + kL * k < chunks ? lane + kL * k : 0;
         gv[i][k] = __builtin_nontemporal_load(gs + c);
         hv[i][k] = __builtin_nontemporal_load(hs + c);
       }
     }
 #pragma unroll
     for (int i = 0; i < kGeluRows; ++i) {
-      if (r0 + i >= rows) break;  // uniform per wave
-      const __amdgpu_buffer_rsrc_t out = buffer_rsrc(dh + (r0 + i) * row_bytes, (uint32_t)row_bytes);
+      if (r0 + kSub * i >= rows) break;  // uniform per wave
+      // One descriptor over the wave's kSub rows of this step (uniform).
+      const int64_t left = rows - (r0 + kSub * i);
+      const __amdgpu_buffer_rsrc_t out =
+          buffer_rsrc(dh + (r0 + kSub * i) * row_bytes, (uint32_t)((left < kSub ? left : kSub) * row_bytes));
+      const bool live = r0 + kSub * i + sub < rows;
 #pragma unroll
       for (int k = 0; k < CPL; ++k) {
-        const int c = lane + 64 * k;
-        if (c >= chunks) continue;
+        const int c = lane + kL * k;
+        if (c >= chunks || !live) continue;
         u32x4 res;
         if constexpr (DT == TERRA_DTYPE_BF16) {
 #pragma unroll
@@ -144,14 +155,14 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_bwd_kernel(const uint8_t* _
             if constexpr (kSum) acc[k][q] += v;
           }
         }
-        stream_store_sc1(res, out, (uint32_t)c * 16);
+        stream_store_sc1(res, out, (uint32_t)(sub * row_bytes) + (uint32_t)c * 16);
       }
     }
   }
   if constexpr (kSum) {
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
-      const int c = lane + 64 * k;
+      const int c = lane + kL * k;
       if (c >= chunks) continue;
 #pragma unroll
       for (int e = 0; e < E; ++e) atomicAdd(&s_sum[c * E + e], acc[k][e]);
@@ -166,10 +177,10 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_bwd_kernel(const uint8_t* _
 // those to 2 * CUs * F per launch.
 constexpr int kGeluMaxBlocksPerCu = 2;
 
-template <int DT, int CPL, bool kSum>
+template <int DT, int CPL, bool kSum, int kL = 64>
 int launch_gelu_bwd(const void* dout, const void* h, void* dh, float* colsum, int64_t rows, int chunks,
                     hipStream_t s) {
-  auto kern = gelu_bwd_kernel<DT, CPL, kSum>;
+  auto kern = gelu_bwd_kernel<DT, CPL, kSum, kL>;
   constexpr int kMaxDevices = 64;
   static int cache[kMaxDevices] = {0};
   int dev = 0;
@@ -183,7 +194,7 @@ int launch_gelu_bwd(const void* dout, const void* h, void* dh, float* colsum, in
     per_cu = per_cu < 1 ? 1 : (per_cu > kGeluMaxBlocksPerCu ? kGeluMaxBlocksPerCu : per_cu);
     cache[dev] = cus * per_cu;
   }
-  const int64_t per_block = (int64_t)kGeluWaves * gelu_rows<CPL>();
+  const int64_t per_block = (int64_t)kGeluWaves * gelu_rows<CPL>() * (64 / kL);
   const int64_t need = (rows + per_block - 1) / per_block;
   const int blocks = need < cache[dev] ? (int)need : cache[dev];
   kern<<<blocks, kGeluThreads, 0, s>>>((const uint8_t*)dout, (const uint8_t*)h, (uint8_t*)dh, colsum, rows, chunks);
@@ -193,7 +204,9 @@ int launch_gelu_bwd(const void* dout, const void* h, void* dh, float* colsum, in
 template <int DT, bool kSum>
 int dispatch_gelu_bwd(const void* dout, const void* h, void* dh, float* colsum, int64_t rows, int chunks,
                       hipStream_t s) {
+  if (chunks <= 32) return launch_gelu_bwd<DT, 1, kSum, 32>(dout, h, dh, colsum, rows, chunks, s);
   if (chunks <= 64) return launch_gelu_bwd<DT, 1, kSum>(dout, h, dh, colsum, rows, chunks, s);
+  if (chunks <= 96) return launch_gelu_bwd<DT, 3, kSum, 32>(dout, h, dh, colsum, rows, chunks, s);  // c3: 768 bf16
   if (chunks <= 128) return launch_gelu_bwd<DT, 2, kSum>(dout, h, dh, colsum, rows, chunks, s);
   if (chunks <= 192) return launch_gelu_bwd<DT, 3, kSum>(dout, h, dh, colsum, rows, chunks, s);
   if (chunks <= 256) return launch_gelu_bwd<DT, 4, kSum>(dout, h, dh, colsum, rows, chunks, s);

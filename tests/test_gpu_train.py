@@ -319,7 +319,8 @@ def _gelu_grad64(g: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
     return g * (cdf + h * pdf)
 
 
-@pytest.mark.parametrize("dtype,features", [(torch.bfloat16, 512), (torch.bfloat16, 768), (torch.bfloat16, 1536),
+@pytest.mark.parametrize("dtype,features", [(torch.bfloat16, 256), (torch.bfloat16, 512), (torch.bfloat16, 768),
+                                            (torch.bfloat16, 1536),
                                             (torch.bfloat16, 3072), (torch.bfloat16, 4096), (torch.float32, 768),
                                             (torch.float32, 2048)])
 @pytest.mark.parametrize("rows", [1, 37, 2053])
