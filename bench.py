@@ -474,9 +474,11 @@ def main():
         # and parameters under bf16 autocast, forward then backward of a
         # synthetic output gradient (no optimizer update).  The LayerNorms and
         # their backward, partition / reverse and the attention core with its
-        # backward run on the HIP kernels; the projection, fc1 and fc2 GEMMs
-        # and their backward on hipBLASLt through torch.
-        train = training_step_us(cfg, dev) if has_bwd else None
+        # backward run on the HIP kernels (the Linear bias gradients summed
+        # inside the kernels that write the gradients); the projection, fc1 and
+        # fc2 GEMMs and their backward on hipBLASLt through torch.  Median of
+        # 10 steps after 3 warm-up steps (a step is 5-6 ms at c3).
+        train = training_step_us(cfg, dev, warmup=3, reps=10) if has_bwd else None
     finally:
         for n in names:
             setattr(kernels, n, orig[n])
@@ -714,7 +716,7 @@ def main():
         "us": train, "tokens_per_s": tokens / (train * 1e-6),
         "what": ("forward + backward of the attention half and the MLP half, fp32 input and parameters under bf16 "
                  "autocast (the reference's training mode), synthetic output gradient, no optimizer update; "
-                 "median of 5 after 2 warm-up steps"),
+                 "median of 10 after 3 warm-up steps"),
     } if train is not None else {"us": None, "note": "no backward for windows of more than 64 tokens"}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg, blk, land if land is not None else
