@@ -29,6 +29,8 @@ serves the shape.
     python bench.py --mode kernels --steps 3     # the step's kernels only,
                                                  # plus a 192 MiB device copy
                                                  # (rocprofv3 counter calibration)
+    python bench.py --mode training --steps 5    # the training step only
+                                                 # (rocprofv3 kernel traces)
 """
 from __future__ import annotations
 
